@@ -1,0 +1,257 @@
+"""Host API over libaegist_mixer for torch device tensors.
+
+Names and argument meanings follow the reference's torch model
+(/root/reference/aegist-fast-35b/aegist/hybrid.py): ``delta_rule_step`` (:318-324),
+``delta_rule_chunked`` (:327-361), the GatedDeltaNet decode path (:388-421) and
+GatedAttention (:265-311); the ``engine_*`` functions wrap the engine-ABI mirrors of
+aegist_rs/kernels/hybrid.cu one to one. Every function launches HIP kernels on the current
+torch stream and returns without synchronising. torch is only the allocator and stream
+provider here: no op computes anything in torch.
+"""
+from __future__ import annotations
+
+import torch
+
+from ._lib import BF16, F32, AegistError, call, lib
+
+_DT = {torch.float32: F32, torch.bfloat16: BF16}
+
+
+def _dt(t: torch.Tensor) -> int:
+    try:
+        return _DT[t.dtype]
+    except KeyError:
+        raise AegistError("dtype", -3, f"tensor dtype {t.dtype} not supported (fp32 or bf16)") from None
+
+
+def _p(t: torch.Tensor | None) -> int | None:
+    if t is None:
+        return None
+    if not t.is_cuda:
+        raise AegistError("device", -1, "tensor is not on a GPU device")
+    return t.data_ptr()
+
+
+def _need_contig(*ts):
+    for t in ts:
+        if t is not None and not t.is_contiguous():
+            raise AegistError("layout", -1, "tensor must be contiguous")
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+_ws_cache: dict[tuple, torch.Tensor] = {}
+
+
+def _workspace(nbytes: int, device) -> torch.Tensor:
+    """Workspace tensor of at least nbytes (kept per device, grown on demand)."""
+    key = (str(device),)
+    ws = _ws_cache.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        _ws_cache[key] = ws
+    return ws
+
+
+# --- synthetic inputs ------------------------------------------------------------------------
+
+def fill_normal(t: torch.Tensor, seed: int, mean: float = 0.0, std: float = 1.0) -> torch.Tensor:
+    """Fill t (fp32 or bf16, contiguous) from the counter-based N(mean, std) generator."""
+    _need_contig(t)
+    call("aegist_fill_normal", _p(t), t.numel(), _dt(t), seed & ((1 << 64) - 1), mean, std, _stream())
+    return t
+
+
+def rope_inv_freq(rotary_dim: int, theta: float) -> torch.Tensor:
+    """The library's RoPE table (CPU fp32), 1 / theta^(2j/rd) rounded once from double."""
+    out = torch.empty(rotary_dim // 2, dtype=torch.float32)
+    call("aegist_rope_inv_freq", out.data_ptr(), rotary_dim, theta)
+    return out
+
+
+# --- gated DeltaNet -----------------------------------------------------------------------------
+
+def delta_decode_step(qkv, conv_w, conv_state, g, beta, state, hk: int, hv: int,
+                      out_dtype=torch.float32, eps: float = 1e-6):
+    """One decode token per sequence (hybrid.py:390-413 at T == 1 with history): conv-state
+    update + conv + SiLU + split + L2-norm + q/sqrt(128) + gated delta step, fused.
+
+    qkv [B, C] (fp32/bf16, pre-conv); conv_w [C, 4] bf16; conv_state [B, C, 3] fp32 and
+    state [B, HV, 128, 128] fp32 are updated in place; g, beta [B, HV] fp32.
+    Returns o [B, HV, 128] in out_dtype."""
+    B = qkv.shape[0]
+    _need_contig(qkv, conv_w, conv_state, g, beta, state)
+    out = torch.empty(B, hv, 128, dtype=out_dtype, device=qkv.device)
+    call("aegist_delta_decode_step", _p(qkv), _dt(qkv), _p(conv_w), _p(conv_state), _p(g), _p(beta), _p(state),
+         _p(out), _dt(out), B, hk, hv, 128 ** -0.5, eps, _stream())
+    return out
+
+
+def _seq_strides(t: torch.Tensor):
+    """(batch, token, head) element strides of a heads-first [B, H, T, d] tensor."""
+    if t.stride(-1) != 1:
+        raise AegistError("layout", -1, "the head dim must be contiguous")
+    return t.stride(0), t.stride(2), t.stride(1)
+
+
+def delta_rule_recurrent(q, k, v, g, beta, state=None, normalize: bool = False, qscale: float = 1.0,
+                         eps: float = 1e-6, out_dtype=torch.float32):
+    """The gated delta rule token by token (hybrid.py:318-324 looped).
+
+    q, k [B, HK, T, d]; v [B, HV, T, d] (heads-first, fp32 or bf16, any strides with the
+    head dim contiguous); g, beta [B, HV, T] fp32; state [B, HV, d, d] fp32 updated in place,
+    or None for a zero initial state. With normalize the kernel applies hybrid.py:408-410
+    (L2-norm of q and k, q * qscale). Returns o [B, HV, T, d]."""
+    B, HK, T, d = q.shape
+    HV = v.shape[1]
+    if d != 128 or v.shape[-1] != 128:
+        raise AegistError("delta_rule_recurrent", -1, "dk = dv = 128 required")
+    if k.dtype != q.dtype or v.dtype != q.dtype:
+        raise AegistError("delta_rule_recurrent", -3, "q, k, v must share a dtype")
+    if k.stride() != q.stride():
+        raise AegistError("delta_rule_recurrent", -1, "q and k must have the same strides")
+    gt = g.transpose(1, 2).contiguous()   # [B, T, HV]
+    bt = beta.transpose(1, 2).contiguous()
+    out = torch.empty(B, HV, T, d, dtype=out_dtype, device=q.device)
+    sq, sv, so = _seq_strides(q), _seq_strides(v), _seq_strides(out)
+    if state is not None:
+        _need_contig(state)
+    call("aegist_delta_recurrent", _p(q), _p(k), _p(v), _dt(q), *sq, *sv, _p(gt), _p(bt), _p(state), _p(out),
+         _dt(out), *so, B, T, HK, HV, int(normalize), qscale, eps, _stream())
+    return out
+
+
+def delta_rule_step(q, k, v, g, beta, state):
+    """One token (hybrid.py:318-324). q, k [B, H, dk]; v [B, H, dv]; g, beta [B, H];
+    state [B, H, dk, dv] fp32 updated in place. Returns o [B, H, dv] fp32."""
+    o = delta_rule_recurrent(q.unsqueeze(2), k.unsqueeze(2), v.unsqueeze(2), g.unsqueeze(2), beta.unsqueeze(2),
+                             state)
+    return o[:, :, 0]
+
+
+def delta_rule_chunked(q, k, v, g, beta, state=None, chunk: int = 64, normalize: bool = False,
+                       qscale: float = 1.0, eps: float = 1e-6, out_dtype=torch.float32):
+    """Chunked WY form (hybrid.py:327-361), on MFMA. Same tensors as delta_rule_recurrent;
+    returns (o [B, HV, T, d], final state [B, HV, d, d] fp32). A given state is updated in
+    place and also returned."""
+    if chunk != 64:
+        raise AegistError("delta_rule_chunked", -1, "chunk size 64 only")
+    B, HK, T, d = q.shape
+    HV = v.shape[1]
+    if d != 128 or v.shape[-1] != 128:
+        raise AegistError("delta_rule_chunked", -1, "dk = dv = 128 required")
+    if k.stride() != q.stride() or k.dtype != q.dtype or v.dtype != q.dtype:
+        raise AegistError("delta_rule_chunked", -1, "q and k must share strides; q, k, v a dtype")
+    gt = g.transpose(1, 2).contiguous()
+    bt = beta.transpose(1, 2).contiguous()
+    out = torch.empty(B, HV, T, d, dtype=out_dtype, device=q.device)
+    S = torch.zeros(B, HV, d, d, dtype=torch.float32, device=q.device) if state is None else state
+    _need_contig(S)
+    nbytes = lib().aegist_delta_chunked_workspace_bytes(B, T, HV)
+    ws = _workspace(nbytes, q.device)
+    sq, sv, so = _seq_strides(q), _seq_strides(v), _seq_strides(out)
+    call("aegist_delta_chunked", _p(q), _p(k), _p(v), _dt(q), *sq, *sv, _p(gt), _p(bt), _p(S), _p(out), _dt(out),
+         *so, B, T, HK, HV, int(normalize), qscale, eps, _p(ws), ws.numel(), _stream())
+    return out, S
+
+
+# --- gated attention --------------------------------------------------------------------------
+
+def attention_decode(qg, k_new, v_new, q_norm_w, k_norm_w, kc, vc, pos: int, rotary_dim: int = 64,
+                     theta: float = 1e7, eps: float = 1e-6, out_dtype=torch.float32):
+    """One query token per sequence at position ``pos`` (hybrid.py:280-310 at T == 1):
+    ZNorm + partial RoPE of q and the new k, cache append, split-K attention over rows
+    [0, pos], sigmoid gate. qg [B, H, 2*HD]; k_new, v_new [B, KV, HD]; caches
+    [B, KV, cap, HD] bf16. Returns [B, H, HD] in out_dtype."""
+    B, H, HD2 = qg.shape
+    KV, HD, cap = kc.shape[1], kc.shape[3], kc.shape[2]
+    _need_contig(qg, k_new, v_new, kc, vc, q_norm_w, k_norm_w)
+    if k_new.dtype != qg.dtype or v_new.dtype != qg.dtype:
+        raise AegistError("attention_decode", -3, "qg, k_new, v_new must share a dtype")
+    out = torch.empty(B, H, HD, dtype=out_dtype, device=qg.device)
+    nbytes = lib().aegist_attention_decode_workspace_bytes(B, H, KV, pos + 1)
+    ws = _workspace(nbytes, qg.device)
+    call("aegist_attention_decode", _p(qg), _p(k_new), _p(v_new), _dt(qg), _p(q_norm_w), _p(k_norm_w), _p(kc),
+         _p(vc), _p(out), _dt(out), B, H, KV, HD, rotary_dim, pos, cap, eps, theta, _p(ws), ws.numel(), _stream())
+    return out
+
+
+def attention_core(q, kc, vc, gate, pos: int, scale: float | None = None):
+    """Causal GQA attention core (hybrid.py:297-310). q [B, H, T, HD] fp32 (normed and roped);
+    caches [B, KV, cap, HD] bf16 holding rows [0, pos + T); gate [B, T, H*HD] fp32 or None.
+    Returns [B, T, H, HD] fp32 (gated when gate is given)."""
+    B, H, T, HD = q.shape
+    KV, cap = kc.shape[1], kc.shape[2]
+    _need_contig(q, kc, vc, gate)
+    out = torch.empty(B, T, H, HD, dtype=torch.float32, device=q.device)
+    nbytes = lib().aegist_attention_decode_workspace_bytes(B, H, KV, pos + 1)
+    ws = _workspace(nbytes, q.device)
+    sc = HD ** -0.5 if scale is None else scale
+    call("aegist_attention_core", _p(q), _p(kc), _p(vc), _p(gate), _p(out), B, H, KV, T, pos, cap, sc, _p(ws),
+         ws.numel(), _stream())
+    return out
+
+
+# --- engine-ABI mirrors (batch 1, fp32 activations; aegist_rs/kernels/hybrid.cu) ---------------
+
+def engine_znorm(x, w, eps=1e-6):
+    rows, D = x.shape
+    out = torch.empty_like(x)
+    call("aegist_znorm", _p(x), _p(w), _p(out), rows, D, eps, _stream())
+    return out
+
+
+def engine_attn_prep(qg, k, v, qw, kw, kc, vc, pos0, rotary_dim=64, theta=1e7, eps=1e-6):
+    """qg [T, H, 2HD]; k, v [T, KV, HD]; kc, vc [KV, cap, HD] bf16. Returns qn [T, H, HD]."""
+    T, H, HD2 = qg.shape
+    KV, cap, HD = kc.shape
+    qn = torch.empty(T, H, HD, dtype=torch.float32, device=qg.device)
+    call("aegist_attn_prep", _p(qg), _p(k), _p(v), _p(qw), _p(kw), _p(qn), _p(kc), _p(vc), T, H, KV, HD, rotary_dim,
+         pos0, cap, eps, theta, _stream())
+    return qn
+
+
+def engine_attention_gated(qn, kc, vc, qg, pos0):
+    T, H, HD = qn.shape
+    KV, cap, _ = kc.shape
+    out = torch.empty(T, H, HD, dtype=torch.float32, device=qn.device)
+    call("aegist_attention_gated", _p(qn), _p(kc), _p(vc), _p(qg), _p(out), T, H, KV, pos0, cap, HD ** -0.5,
+         _stream())
+    return out
+
+
+def engine_delta_gates(h, wb, wa, a_log, dt_bias):
+    T, D = h.shape
+    HV = wb.shape[0]
+    gb = torch.empty(T, 2 * HV, dtype=torch.float32, device=h.device)
+    call("aegist_delta_gates", _p(h), _p(wb), _p(wa), _p(a_log), _p(dt_bias), _p(gb), T, D, HV, _stream())
+    return gb
+
+
+def engine_conv_silu(x, w, state):
+    T, Cc = x.shape
+    y = torch.empty_like(x)
+    call("aegist_conv_silu", _p(x), _p(y), _p(w), _p(state), T, Cc, _stream())
+    return y
+
+
+def engine_l2norm_heads(y, nq, dk=128, qscale=128 ** -0.5, eps=1e-6):
+    T, Cc = y.shape
+    call("aegist_l2norm_heads", _p(y), T, Cc, nq, dk, qscale, eps, _stream())
+    return y
+
+
+def engine_delta_scan(y, gb, state, hk, hv):
+    T, Cc = y.shape
+    o = torch.empty(T, hv, 128, dtype=torch.float32, device=y.device)
+    call("aegist_delta_scan", _p(y), _p(gb), _p(state), _p(o), T, Cc, hk, hv, _stream())
+    return o
+
+
+def engine_gated_norm(o, z, w, eps=1e-6):
+    T, HV, DV = o.shape
+    out = torch.empty_like(o)
+    call("aegist_gated_norm", _p(o), _p(z), _p(w), _p(out), T, HV, DV, eps, _stream())
+    return out

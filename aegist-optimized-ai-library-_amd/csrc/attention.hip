@@ -1,0 +1,481 @@
+// Gated GQA attention for gfx950: split-K MFMA decode and a causal prefill kernel.
+//
+// Decode (one query per sequence). One workgroup of 4 waves per (sequence, KV head, split of
+// the context). The G <= 8 query heads of a KV head share every K/V byte the workgroup
+// reads, so the cache is streamed from HBM once (the reference kernel reads it once per
+// query head). Scores and P.V run on v_mfma_f32_16x16x32_bf16: the 16 MFMA rows hold the G
+// query heads twice, as a bf16 hi part (rows 0-7) and the bf16 residual (rows 8-15), so
+// q (fp32) and P (fp32) enter the products with ~16 significant bits while K and V are the
+// exact bf16 cache values; row h + row h+8 recovers the fp32-accurate result.
+//   - K operand: lane (key n, group g) loads K[key n][32 ks + 8 g .. +8] straight from HBM.
+//   - V operand: the wave stages its 32-key V tile row-major in LDS and reads 4 dims x 8
+//     keys per lane with 64-bit LDS reads, repacking pairs of keys into the bf16x8 operand;
+//     output column block 4p+j, lane column n is dim 64p + 4n + j.
+//   - P is transposed from the score layout to the A-operand layout through 1 KiB of LDS.
+// Each wave runs its own online softmax over its tiles; the 4 waves merge in LDS and the
+// workgroup writes (m, l, O) for its split. A merge kernel combines the splits with
+// log-sum-exp weights and applies the sigmoid output gate.
+//
+// Semantics: hybrid.py:280-310 (grouped SDPA at T == 1, causal SDPA otherwise, sigmoid gate);
+// engine kernels attn_prep / attention_gated (hybrid.cu:86-173).
+#include "common.h"
+
+#include <algorithm>
+
+using namespace aegist;
+
+namespace aegist {
+struct RopeTable;
+int launch_attn_prep(const void* qg, const void* k, const void* v, int in_dtype, const uint16_t* qw,
+                     const uint16_t* kw, float* qn, uint16_t* kc, uint16_t* vc, int B, int T, int H, int KV, int HD,
+                     int RD, int pos0, int cap, float eps, float theta, hipStream_t stream);
+void* mirror_workspace(size_t bytes, int* rc);
+}  // namespace aegist
+
+namespace {
+
+constexpr int HD = 256;
+constexpr int TILE = 32;             // keys per wave iteration
+constexpr int VROW = HD * 2 + 16;    // bytes per staged V row (16 B pad against bank conflicts)
+
+struct DecodeSplit {
+    int nsplit, per_split;
+};
+
+// Splits sized so a launch has about 2048 workgroups, each split a multiple of 128 keys
+// (one 32-key tile per wave per step).
+DecodeSplit choose_split(int B, int KV, int L) {
+    int units = std::max(1, B * KV);
+    int max_split = std::max(1, (L + 127) / 128);
+    int ns = std::min(max_split, std::max(1, (2048 + units - 1) / units));
+    int per = (L + ns - 1) / ns;
+    per = (per + 127) / 128 * 128;
+    ns = (L + per - 1) / per;
+    return {ns, per};
+}
+
+__device__ __forceinline__ uint16_t bf_bits(float f) { return f2bf(f); }
+
+// Split fp32 x into bf16 hi + bf16 lo with hi + lo ~= x to ~16 significant bits.
+__device__ __forceinline__ void split_bf16(float x, uint16_t& hi, uint16_t& lo) {
+    hi = f2bf(x);
+    lo = f2bf(x - bf2f(hi));
+}
+
+template <typename TG>
+struct GateLd {
+    static __device__ __forceinline__ float ld(const TG* p, size_t i) { return Act<TG>::ld(p, i); }
+};
+
+// q:   [B, H, HD] fp32 (normed, roped), head h of KV head kvh is kvh*G + r
+// kc, vc: [B, KV, cap, HD] bf16
+// part: [B, KV, nsplit, G, HD] fp32 partial outputs (unnormalised), ml: [B, KV, nsplit, G, 2]
+__global__ void __launch_bounds__(256) attn_decode_split_kernel(const float* __restrict__ q,
+                                                                const uint16_t* __restrict__ kc,
+                                                                const uint16_t* __restrict__ vc,
+                                                                float* __restrict__ part, float* __restrict__ ml,
+                                                                int H, int KV, int L, int cap, int per_split,
+                                                                float scale) {
+    __shared__ __attribute__((aligned(16))) unsigned char vbuf[4][TILE * VROW];
+    __shared__ __attribute__((aligned(16))) uint16_t pbuf[4][16][TILE];
+    __shared__ float wm[4][8], wl[4][8];
+    __shared__ float wo[4][8][HD];
+
+    const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z, nsplit = gridDim.x;
+    const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+    const int n = lane % 16, g = lane / 16;
+    const int G = H / KV;
+    const int k0 = split * per_split, k1 = min(L, k0 + per_split);
+
+    // ---- Q operand: rows 0..7 = hi(q*scale), rows 8..15 = lo; lane row n, k elems 8g..8g+7
+    bf16x8 qa[8];
+    {
+        const int r = n & 7;
+        const bool lo = n >= 8;
+        const bool valid = r < G;
+        const float* qrow = q + ((size_t)b * H + kvh * G + (valid ? r : 0)) * HD;
+#pragma unroll
+        for (int ks = 0; ks < 8; ks++) {
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                float x = valid ? qrow[ks * 32 + 8 * g + i] * scale : 0.f;
+                uint16_t h, l;
+                split_bf16(x, h, l);
+                qa[ks][i] = (short)(lo ? l : h);
+            }
+        }
+    }
+
+    const uint16_t* kbase = kc + ((size_t)b * KV + kvh) * (size_t)cap * HD;
+    const uint16_t* vbase = vc + ((size_t)b * KV + kvh) * (size_t)cap * HD;
+
+    // running softmax state for heads 4*(g%2)+j, j < 4 (duplicated in lanes g and g+2)
+    float m_run[4], l_run[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        m_run[j] = -INFINITY;
+        l_run[j] = 0.f;
+    }
+    f32x4 oacc[16];
+#pragma unroll
+    for (int i = 0; i < 16; i++) oacc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    unsigned char* vb = vbuf[wave];
+    for (int t0 = k0 + wave * TILE; t0 < k1; t0 += 4 * TILE) {
+        // ---- stage V tile rows t0..t0+31 into LDS (rows past the end are zero)
+#pragma unroll
+        for (int it = 0; it < (TILE * HD * 2) / (16 * WAVE); it++) {  // 16 iterations
+            int idx = it * WAVE + lane;       // 16-byte chunk index
+            int row = idx / (HD * 2 / 16);    // 32 chunks per row
+            int cc = idx % (HD * 2 / 16);
+            int key = t0 + row;
+            uint4 val = {0u, 0u, 0u, 0u};
+            if (key < k1) val = *(const uint4*)(vbase + (size_t)key * HD + cc * 8);
+            uint2* dst = (uint2*)(vb + row * VROW + cc * 16);
+            dst[0] = uint2{val.x, val.y};
+            dst[1] = uint2{val.z, val.w};
+        }
+        wave_sync();
+        // ---- scores: two 16-key blocks
+        f32x4 sc[2];
+#pragma unroll
+        for (int nb = 0; nb < 2; nb++) {
+            int key = t0 + nb * 16 + n;
+            int kr = key < k1 ? key : k1 - 1;
+            const uint16_t* krow = kbase + (size_t)kr * HD + 8 * g;
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < 8; ks++) {
+                bf16x8 kb = *(const bf16x8*)(krow + ks * 32);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[ks], kb, acc, 0, 0, 0);
+            }
+            // rows 4g+j; combine hi (g<2) and lo (g>=2) parts: lane g and g^2 hold h and h+8
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                float other = __shfl_xor(acc[j], 32, WAVE);
+                float s = acc[j] + other;
+                sc[nb][j] = key < k1 ? s : -INFINITY;
+            }
+        }
+        // ---- online softmax per head (over 16 lanes n and 2 blocks)
+        float p0[4], p1[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            float mt = fmaxf(sc[0][j], sc[1][j]);
+            mt = fmaxf(mt, __shfl_xor(mt, 1, WAVE));
+            mt = fmaxf(mt, __shfl_xor(mt, 2, WAVE));
+            mt = fmaxf(mt, __shfl_xor(mt, 4, WAVE));
+            mt = fmaxf(mt, __shfl_xor(mt, 8, WAVE));
+            float mn = fmaxf(m_run[j], mt);  // finite: every tile has at least one valid key
+            float corr = __expf(m_run[j] - mn);
+            p0[j] = __expf(sc[0][j] - mn);
+            p1[j] = __expf(sc[1][j] - mn);
+            l_run[j] = l_run[j] * corr + p0[j] + p1[j];
+            m_run[j] = mn;
+            // rescale O rows held by this lane: rows 4g+j are heads 4(g%2)+j
+#pragma unroll
+            for (int i = 0; i < 16; i++) oacc[i][j] *= corr;
+        }
+        // ---- P -> LDS as A operand [16 rows][32 keys]: rows 0-7 hi, 8-15 lo
+        {
+            const int hb = 4 * (g & 1);
+            const bool lo = g >= 2;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                uint16_t h0, l0, h1, l1;
+                split_bf16(p0[j], h0, l0);
+                split_bf16(p1[j], h1, l1);
+                int row = (lo ? 8 : 0) + hb + j;
+                pbuf[wave][row][n] = lo ? l0 : h0;
+                pbuf[wave][row][16 + n] = lo ? l1 : h1;
+            }
+        }
+        wave_sync();
+        bf16x8 pa = *(const bf16x8*)&pbuf[wave][n][8 * g];
+        // ---- O += P V
+#pragma unroll
+        for (int p = 0; p < 4; p++) {
+            uint2 vq[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) vq[i] = *(const uint2*)(vb + (8 * g + i) * VROW + (64 * p + 4 * n) * 2);
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                bf16x8 vop;
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    uint32_t w = (j < 2) ? vq[i].x : vq[i].y;
+                    vop[i] = (short)((j & 1) ? (w >> 16) : (w & 0xffffu));
+                }
+                oacc[4 * p + j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, vop, oacc[4 * p + j], 0, 0, 0);
+            }
+        }
+        wave_sync();  // this tile's LDS reads complete before the next tile overwrites
+    }
+
+    // ---- combine hi/lo rows and reduce l over the 16 key lanes
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        float l = l_run[j];
+        l += __shfl_xor(l, 1, WAVE);
+        l += __shfl_xor(l, 2, WAVE);
+        l += __shfl_xor(l, 4, WAVE);
+        l += __shfl_xor(l, 8, WAVE);
+        l_run[j] = l;
+    }
+#pragma unroll
+    for (int i = 0; i < 16; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) oacc[i][j] += __shfl_xor(oacc[i][j], 32, WAVE);
+    if (g < 2) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            int h = 4 * g + j;
+            if (n == 0) {
+                wm[wave][h] = m_run[j];
+                wl[wave][h] = l_run[j];
+            }
+#pragma unroll
+            for (int p = 0; p < 4; p++)
+#pragma unroll
+                for (int jj = 0; jj < 4; jj++) wo[wave][h][64 * p + 4 * n + jj] = oacc[4 * p + jj][j];
+        }
+    }
+    __syncthreads();
+    // ---- merge the 4 waves; thread = (head r, 32-dim slice)
+    const int tid = threadIdx.x;
+    const int r = tid / 32, d0 = (tid % 32) * 8;
+    if (r < G) {
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < 4; w++) M = fmaxf(M, wm[w][r]);
+        float Lsum = 0.f, f[4];
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            f[w] = wm[w][r] == -INFINITY ? 0.f : __expf(wm[w][r] - M);
+            Lsum += wl[w][r] * f[w];
+        }
+        size_t pidx = (((size_t)b * KV + kvh) * nsplit + split) * G + r;
+        float* po = part + pidx * HD + d0;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            float a = 0.f;
+#pragma unroll
+            for (int w = 0; w < 4; w++) a += wo[w][r][d0 + i] * f[w];
+            po[i] = a;
+        }
+        if (d0 == 0) {
+            ml[pidx * 2] = M;
+            ml[pidx * 2 + 1] = Lsum;
+        }
+    }
+}
+
+// out[b, h, :] = (sum_s e^{m_s - M} O_s) / (sum_s e^{m_s - M} l_s) * sigmoid(gate)
+template <typename TG, typename Tout>
+__global__ void __launch_bounds__(256) attn_decode_merge_kernel(const float* __restrict__ part,
+                                                                const float* __restrict__ ml, const TG* __restrict__ gate,
+                                                                long long gate_row_stride, Tout* __restrict__ out,
+                                                                long long out_row_stride, int H, int KV, int nsplit) {
+    const int bh = blockIdx.x, b = bh / H, h = bh % H, G = H / KV, kvh = h / G, r = h % G;
+    const int d = threadIdx.x;
+    const size_t base = ((size_t)b * KV + kvh) * nsplit;
+    float M = -INFINITY;
+    for (int s = 0; s < nsplit; s++) M = fmaxf(M, ml[((base + s) * G + r) * 2]);
+    float Lsum = 0.f, acc = 0.f;
+    for (int s = 0; s < nsplit; s++) {
+        size_t pidx = (base + s) * G + r;
+        float m = ml[pidx * 2];
+        float f = m == -INFINITY ? 0.f : __expf(m - M);
+        Lsum += ml[pidx * 2 + 1] * f;
+        acc += part[pidx * HD + d] * f;
+    }
+    float y = acc / Lsum;
+    if (gate) y *= sigmoid_f(Act<TG>::ld(gate, (size_t)bh * gate_row_stride + d));
+    Act<Tout>::st(out, (size_t)bh * out_row_stride + d, y);
+}
+
+// ---------------------------------------------------------------------------------------------
+// Causal prefill, one workgroup of 4 waves per (sequence, query head, 4 queries): each wave
+// owns one query, lanes own 4 dims, keys are walked with an online softmax. Correct for any
+// T; used for short prefills.
+struct Strides3 {
+    long long b, t, h;  // element strides of a [.., HD] row by sequence, token, head
+};
+
+__global__ void __launch_bounds__(256) attn_prefill_simple_kernel(const float* __restrict__ q, Strides3 qs,
+                                                                  const uint16_t* __restrict__ kc,
+                                                                  const uint16_t* __restrict__ vc,
+                                                                  const float* __restrict__ gate, Strides3 gs,
+                                                                  float* __restrict__ out, Strides3 os, int H, int KV,
+                                                                  int T, int pos, int cap, float scale) {
+    const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+    const int t = blockIdx.x * 4 + wave, h = blockIdx.y, b = blockIdx.z;
+    if (t >= T) return;
+    const int G = H / KV, kvh = h / G;
+    const float* qr = q + b * qs.b + t * qs.t + h * qs.h;
+    float qv[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) qv[i] = qr[lane * 4 + i];
+    const uint16_t* kb = kc + ((size_t)b * KV + kvh) * (size_t)cap * HD;
+    const uint16_t* vb = vc + ((size_t)b * KV + kvh) * (size_t)cap * HD;
+    float m = -INFINITY, l = 0.f, a[4] = {0.f, 0.f, 0.f, 0.f};
+    const int L = pos + t + 1;
+    for (int key = 0; key < L; key++) {
+        uint2 kp = *(const uint2*)(kb + (size_t)key * HD + lane * 4);
+        float s = qv[0] * bf_lo(kp.x) + qv[1] * bf_hi(kp.x) + qv[2] * bf_lo(kp.y) + qv[3] * bf_hi(kp.y);
+        s = wave_sum(s) * scale;
+        float mn = fmaxf(m, s);
+        float corr = __expf(m - mn), p = __expf(s - mn);
+        uint2 vp = *(const uint2*)(vb + (size_t)key * HD + lane * 4);
+        l = l * corr + p;
+        a[0] = a[0] * corr + p * bf_lo(vp.x);
+        a[1] = a[1] * corr + p * bf_hi(vp.x);
+        a[2] = a[2] * corr + p * bf_lo(vp.y);
+        a[3] = a[3] * corr + p * bf_hi(vp.y);
+        m = mn;
+    }
+    float* orow = out + b * os.b + t * os.t + h * os.h;
+    const float* grow = gate ? gate + b * gs.b + t * gs.t + h * gs.h : nullptr;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        float y = a[i] / l;
+        if (grow) y *= sigmoid_f(grow[lane * 4 + i]);
+        orow[lane * 4 + i] = y;
+    }
+}
+
+}  // namespace
+
+namespace aegist {
+
+size_t decode_workspace_bytes(int B, int H, int KV, int L, bool with_q) {
+    DecodeSplit sp = choose_split(B, KV, L);
+    int G = H / std::max(1, KV);
+    size_t part = (size_t)B * KV * sp.nsplit * G * HD * 4;
+    size_t ml = (size_t)B * KV * sp.nsplit * G * 2 * 4;
+    size_t qb = with_q ? (size_t)B * H * HD * 4 : 0;
+    auto al = [](size_t x) { return (x + 255) / 256 * 256; };
+    return al(part) + al(ml) + al(qb);
+}
+
+// q [B, H, HD] fp32 -> out rows (b*H + h) * out_row_stride, gate rows (b*H + h) * gate_row_stride
+template <typename TG, typename Tout>
+int launch_decode_core(const float* q, const uint16_t* kc, const uint16_t* vc, const TG* gate, long long gate_stride,
+                       Tout* out, long long out_stride, int B, int H, int KV, int L, int cap, float scale,
+                       void* ws, size_t ws_bytes, hipStream_t st) {
+    if (KV <= 0 || H % KV || H / KV > 8) return fail(AEGIST_ERR_SHAPE, "attention decode: need H % KV == 0 and H/KV <= 8");
+    if (L <= 0 || L > cap) return fail(AEGIST_ERR_SHAPE, "attention decode: need 0 < L <= cap");
+    DecodeSplit sp = choose_split(B, KV, L);
+    size_t need = decode_workspace_bytes(B, H, KV, L, false);
+    if (!ws || ws_bytes < need) return fail(AEGIST_ERR_WORKSPACE, "attention decode: workspace too small");
+    int G = H / KV;
+    float* part = (float*)ws;
+    size_t part_bytes = ((size_t)B * KV * sp.nsplit * G * HD * 4 + 255) / 256 * 256;
+    float* ml = (float*)((char*)ws + part_bytes);
+    attn_decode_split_kernel<<<dim3(sp.nsplit, KV, B), 256, 0, st>>>(q, kc, vc, part, ml, H, KV, L, cap, sp.per_split,
+                                                                      scale);
+    int rc = after_launch("attention_decode_split");
+    if (rc) return rc;
+    attn_decode_merge_kernel<TG, Tout><<<B * H, HD, 0, st>>>(part, ml, gate, gate_stride, out, out_stride, H, KV,
+                                                             sp.nsplit);
+    return after_launch("attention_decode_merge");
+}
+
+int launch_prefill_core(const float* q, Strides3 qs, const uint16_t* kc, const uint16_t* vc, const float* gate,
+                        Strides3 gs, float* out, Strides3 os, int B, int H, int KV, int T, int pos, int cap,
+                        float scale, hipStream_t st) {
+    if (KV <= 0 || H % KV) return fail(AEGIST_ERR_SHAPE, "attention prefill: need H % KV == 0");
+    if (pos < 0 || pos + T > cap) return fail(AEGIST_ERR_SHAPE, "attention prefill: rows exceed the cache capacity");
+    attn_prefill_simple_kernel<<<dim3((T + 3) / 4, H, B), 256, 0, st>>>(q, qs, kc, vc, gate, gs, out, os, H, KV, T,
+                                                                        pos, cap, scale);
+    return after_launch("attention_prefill");
+}
+
+}  // namespace aegist
+
+extern "C" {
+
+size_t aegist_attention_decode_workspace_bytes(int B, int H, int KV, int L) {
+    return decode_workspace_bytes(B, H, KV, L, true);
+}
+
+int aegist_attention_decode(const void* qg, const void* k_new, const void* v_new, int in_dtype,
+                            const uint16_t* q_norm_w, const uint16_t* k_norm_w, uint16_t* kc, uint16_t* vc, void* out,
+                            int out_dtype, int B, int H, int KV, int HDv, int RD, int pos, int cap, float eps,
+                            float theta, void* workspace, size_t workspace_bytes, void* stream) {
+    AEG_REQUIRE(HDv == HD, "attention_decode: head_dim must be 256");
+    AEG_REQUIRE(B >= 0 && H > 0 && KV > 0 && H % KV == 0 && H / KV <= 8, "attention_decode: need H % KV == 0, H/KV <= 8");
+    AEG_REQUIRE(pos >= 0 && pos < cap, "attention_decode: need 0 <= pos < cap");
+    if (B == 0) return 0;
+    size_t need = decode_workspace_bytes(B, H, KV, pos + 1, true);
+    if (!workspace || workspace_bytes < need)
+        return fail(AEGIST_ERR_WORKSPACE, "attention_decode: workspace smaller than aegist_attention_decode_workspace_bytes()");
+    hipStream_t st = AEG_STREAM(stream);
+    size_t core = decode_workspace_bytes(B, H, KV, pos + 1, false);
+    float* qn = (float*)((char*)workspace + core);
+    int rc = launch_attn_prep(qg, k_new, v_new, in_dtype, q_norm_w, k_norm_w, qn, kc, vc, B, 1, H, KV, HD, RD, pos, cap,
+                              eps, theta, st);
+    if (rc) return rc;
+    const float scale = 1.0f / sqrtf((float)HD);
+    // gate = second half of each head's 2*HD row of qg
+    if (in_dtype == AEGIST_F32) {
+        const float* gate = (const float*)qg + HD;
+        if (out_dtype == AEGIST_F32)
+            return launch_decode_core<float, float>(qn, kc, vc, gate, 2 * HD, (float*)out, HD, B, H, KV, pos + 1, cap,
+                                                    scale, workspace, core, st);
+        if (out_dtype == AEGIST_BF16)
+            return launch_decode_core<float, uint16_t>(qn, kc, vc, gate, 2 * HD, (uint16_t*)out, HD, B, H, KV, pos + 1,
+                                                       cap, scale, workspace, core, st);
+    } else if (in_dtype == AEGIST_BF16) {
+        const uint16_t* gate = (const uint16_t*)qg + HD;
+        if (out_dtype == AEGIST_F32)
+            return launch_decode_core<uint16_t, float>(qn, kc, vc, gate, 2 * HD, (float*)out, HD, B, H, KV, pos + 1,
+                                                       cap, scale, workspace, core, st);
+        if (out_dtype == AEGIST_BF16)
+            return launch_decode_core<uint16_t, uint16_t>(qn, kc, vc, gate, 2 * HD, (uint16_t*)out, HD, B, H, KV,
+                                                          pos + 1, cap, scale, workspace, core, st);
+    }
+    return fail(AEGIST_ERR_DTYPE, "attention_decode: dtypes must be AEGIST_F32 or AEGIST_BF16");
+}
+
+int aegist_attention_core(const float* q, const uint16_t* kc, const uint16_t* vc, const float* gate, float* out, int B,
+                          int H, int KV, int T, int pos, int cap, float scale, void* workspace, size_t workspace_bytes,
+                          void* stream) {
+    AEG_REQUIRE(B >= 0 && T >= 0 && H > 0 && KV > 0 && H % KV == 0, "attention_core: need H % KV == 0");
+    if (B == 0 || T == 0) return 0;
+    hipStream_t st = AEG_STREAM(stream);
+    if (T == 1) {
+        // q [B, H, 1, HD] == [B, H, HD]; gate [B, 1, H*HD]; out [B, 1, H, HD]
+        return launch_decode_core<float, float>(q, kc, vc, gate, HD, out, HD, B, H, KV, pos + 1, cap, scale, workspace,
+                                                workspace_bytes, st);
+    }
+    // q [B, H, T, HD]; gate [B, T, H*HD]; out [B, T, H, HD]
+    Strides3 qs{(long long)H * T * HD, HD, (long long)T * HD};
+    Strides3 gs{(long long)T * H * HD, (long long)H * HD, HD};
+    Strides3 os = gs;
+    return launch_prefill_core(q, qs, kc, vc, gate, gs, out, os, B, H, KV, T, pos, cap, scale, st);
+}
+
+// Engine mirror: q = qn [T, H, HD] fp32 (from attn_prep), gate inside qg [T, H, 2*HD],
+// out [T, H, HD]; batch 1, caches [KV, cap, HD].
+int aegist_attention_gated(const float* q, const uint16_t* kc, const uint16_t* vc, const float* qg, float* out, int T,
+                           int H, int KV, int pos0, int cap, float scale, void* stream) {
+    AEG_REQUIRE(T >= 0 && H > 0 && KV > 0 && H % KV == 0, "attention_gated: need H % KV == 0");
+    if (T == 0) return 0;
+    hipStream_t st = AEG_STREAM(stream);
+    if (T == 1) {
+        AEG_REQUIRE(H / KV <= 8, "attention_gated: H/KV must be <= 8");
+        size_t need = decode_workspace_bytes(1, H, KV, pos0 + 1, false);
+        int rc = 0;
+        void* ws = mirror_workspace(need, &rc);
+        if (rc) return rc;
+        return launch_decode_core<float, float>(q, kc, vc, qg + HD, 2 * HD, out, HD, 1, H, KV, pos0 + 1, cap, scale, ws,
+                                                need, st);
+    }
+    // engine layouts: q, out [T, H, HD]; gate rows inside qg [T, H, 2*HD]
+    Strides3 qs{0, (long long)H * HD, HD};
+    Strides3 gs{0, (long long)H * 2 * HD, 2 * HD};
+    return launch_prefill_core(q, qs, kc, vc, qg + HD, gs, out, qs, 1, H, KV, T, pos0, cap, scale, st);
+}
+
+}  // extern "C"

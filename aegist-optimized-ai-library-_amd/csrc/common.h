@@ -1,0 +1,102 @@
+// Shared device helpers for the gfx950 token-mixer kernels: bf16/fp16 conversion, wave64
+// reductions, MFMA vector types, and the host-side error/launch plumbing of the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+#include <string>
+
+#include "../../include/aegist_mixer.h"
+
+// ---------------------------------------------------------------------------------------------
+// Vector types used as MFMA operands / accumulators.
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef short bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+#define WAVE 64
+
+// ---------------------------------------------------------------------------------------------
+// bf16 <-> fp32. bf16 is the top half of an fp32; narrowing rounds to nearest even and maps
+// NaN to a quiet NaN.
+__device__ __forceinline__ float bf2f(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
+__device__ __forceinline__ float bf_lo(uint32_t p) { return __uint_as_float(p << 16); }
+__device__ __forceinline__ float bf_hi(uint32_t p) { return __uint_as_float(p & 0xffff0000u); }
+__device__ __forceinline__ uint16_t f2bf(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return (uint16_t)((u >> 16) | 0x40);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+// Element load/store for the activation dtypes the ABI accepts (fp32 or bf16).
+template <typename T> struct Act;
+template <> struct Act<float> {
+    static __device__ __forceinline__ float ld(const float* p, size_t i) { return p[i]; }
+    static __device__ __forceinline__ void st(float* p, size_t i, float v) { p[i] = v; }
+};
+template <> struct Act<uint16_t> {
+    static __device__ __forceinline__ float ld(const uint16_t* p, size_t i) { return bf2f(p[i]); }
+    static __device__ __forceinline__ void st(uint16_t* p, size_t i, float v) { p[i] = f2bf(v); }
+};
+
+__device__ __forceinline__ float silu_f(float x) { return x / (1.f + __expf(-x)); }
+__device__ __forceinline__ float sigmoid_f(float x) { return 1.f / (1.f + __expf(-x)); }
+
+// ---------------------------------------------------------------------------------------------
+// wave64 reductions (butterfly; every lane ends with the result).
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, WAVE));
+    return v;
+}
+
+// Orders LDS traffic between the lanes of one wave (no workgroup barrier needed for
+// wave-private buffers): stops compiler code motion and waits for outstanding LDS ops.
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Sum over the block; `red` holds one float per wave. Every thread gets the total.
+__device__ __forceinline__ float block_sum(float v, float* red) {
+    int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE, nw = (blockDim.x + WAVE - 1) / WAVE;
+    v = wave_sum(v);
+    __syncthreads();
+    if (lane == 0) red[w] = v;
+    __syncthreads();
+    float t = 0.f;
+    for (int i = 0; i < nw; i++) t += red[i];
+    return t;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Host side: thread-local error text and return-code helpers.
+namespace aegist {
+void set_error(const std::string& msg);
+int fail(int code, const std::string& msg);
+int check_hip(hipError_t e, const char* what);
+int after_launch(const char* what);  // launch error check; honours AEGIST_SYNC_LAUNCH
+}  // namespace aegist
+
+#define AEG_REQUIRE(cond, msg)                                              \
+    do {                                                                    \
+        if (!(cond)) return aegist::fail(AEGIST_ERR_SHAPE, std::string(msg)); \
+    } while (0)
+
+#define AEG_HIP(call)                                                  \
+    do {                                                               \
+        int _rc = aegist::check_hip((call), #call);                    \
+        if (_rc) return _rc;                                           \
+    } while (0)
+
+#define AEG_STREAM(s) ((hipStream_t)(s))

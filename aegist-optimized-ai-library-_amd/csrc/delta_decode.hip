@@ -1,0 +1,188 @@
+// Gated DeltaNet decode step, batched and fused, for gfx950.
+//
+// One workgroup per (sequence b, QK head kh) serves the R = HV/HK value heads that share that
+// QK head, with 256 threads per value head. The workgroup
+//   1. runs the causal conv (kernel 4) + SiLU for its 256 + 128R channels and writes the new
+//      conv state (each channel is owned by exactly one workgroup, so the in-place update is
+//      race-free),
+//   2. L2-normalises q and k (q also times qscale) in fp32 through LDS,
+//   3. streams each value head's 128x128 fp32 state HBM -> VGPRs -> HBM exactly once:
+//      every thread holds 16 rows x 4 columns (float4 loads; one wave instruction moves two
+//      full 512-byte rows), computes the column dot products S^T k and S^T q, reduces them
+//      across the 8 threads sharing a column (one xor-32 shuffle + LDS across 4 waves), then
+//      writes S' = e^g S + k delta^T with delta = (v - e^g S^T k) beta and emits
+//      o = e^g S^T q + (k.q) delta.
+// The o formula is S'^T q expanded, so the state is read once and written once: the kernel
+// is HBM-bound at 2 x 64 KiB of state per (b, value head) plus ~2 KiB of conv traffic.
+//
+// Semantics: hybrid.py:390-413 (conv, split, l2norm, q scale, delta_rule_step :318-324);
+// the engine's T == 1 path conv_silu -> l2norm_heads -> delta_scan (hybrid.cu:205-300).
+#include "common.h"
+
+using namespace aegist;
+
+namespace {
+
+constexpr int D = 128;  // dk = dv
+
+template <int R, typename Tin, typename Tout>
+__global__ void __launch_bounds__(256 * R) delta_decode_kernel(
+    const Tin* __restrict__ qkv, const uint16_t* __restrict__ conv_w, float* __restrict__ conv_state,
+    const float* __restrict__ g, const float* __restrict__ beta, float* __restrict__ state, Tout* __restrict__ out,
+    int HK, int HV, float qscale, float eps) {
+    constexpr int NT = 256 * R;
+    constexpr int NCH = 2 * D + R * D;
+    __shared__ float sq[D], sk[D], sv[R][D];
+    __shared__ float red[8];
+    __shared__ float4 part[R][4][2][D / 4];
+
+    const int kh = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
+    const int C = 2 * HK * D + HV * D;
+
+    // ---- 1. conv + SiLU + conv-state update for this workgroup's channels
+    float ymine = 0.f;
+    for (int ch = tid; ch < NCH; ch += NT) {
+        int c;
+        if (ch < D) c = kh * D + ch;
+        else if (ch < 2 * D) c = HK * D + kh * D + (ch - D);
+        else c = 2 * HK * D + kh * R * D + (ch - 2 * D);
+        const float xv = Act<Tin>::ld(qkv, (size_t)b * C + c);
+        float* st = conv_state + ((size_t)b * C + c) * 3;
+        const float s0 = st[0], s1 = st[1], s2 = st[2];
+        const uint2 wp = *(const uint2*)(conv_w + (size_t)c * 4);
+        const float acc = bf_lo(wp.x) * s0 + bf_hi(wp.x) * s1 + bf_lo(wp.y) * s2 + bf_hi(wp.y) * xv;
+        const float y = silu_f(acc);
+        st[0] = s1;
+        st[1] = s2;
+        st[2] = xv;
+        if (ch < 2 * D) ymine = y;  // threads 0..255 keep their q/k channel for the norms
+        else sv[(ch - 2 * D) / D][(ch - 2 * D) % D] = y;
+    }
+
+    // ---- 2. L2 norms: q lives in waves 0-1, k in waves 2-3
+    const int wave = tid / WAVE, lane = tid % WAVE;
+    if (tid < 2 * D) {
+        float ss = wave_sum(ymine * ymine);
+        if (lane == 0) red[wave] = ss;
+    }
+    __syncthreads();
+    if (tid < D) {
+        sq[tid] = (ymine * rsqrtf(red[0] + red[1] + eps)) * qscale;
+    } else if (tid < 2 * D) {
+        sk[tid - D] = ymine * rsqrtf(red[2] + red[3] + eps);
+    }
+    __syncthreads();
+    if (tid < D) {
+        float p = wave_sum(sq[tid] * sk[tid]);
+        if (lane == 0) red[4 + wave] = p;
+    }
+    __syncthreads();
+    const float kq = red[4] + red[5];
+
+    // ---- 3. state stream for value head hv
+    const int hl = tid / 256, lt = tid % 256, w4 = lt / WAVE, cg = lane % 32, rs = lane / 32;
+    const int hv = kh * R + hl;
+    float* S = state + ((size_t)b * HV + hv) * D * D;
+    const int row0 = w4 * 2 + rs;  // rows row0 + 8 i
+
+    float4 s[16];
+#pragma unroll
+    for (int i = 0; i < 16; i++) s[i] = *(const float4*)(S + (size_t)(row0 + 8 * i) * D + cg * 4);
+
+    float4 pk = {0.f, 0.f, 0.f, 0.f}, pq = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const float kr = sk[row0 + 8 * i], qr = sq[row0 + 8 * i];
+        pk.x += s[i].x * kr; pk.y += s[i].y * kr; pk.z += s[i].z * kr; pk.w += s[i].w * kr;
+        pq.x += s[i].x * qr; pq.y += s[i].y * qr; pq.z += s[i].z * qr; pq.w += s[i].w * qr;
+    }
+    pk.x += __shfl_xor(pk.x, 32, WAVE); pk.y += __shfl_xor(pk.y, 32, WAVE);
+    pk.z += __shfl_xor(pk.z, 32, WAVE); pk.w += __shfl_xor(pk.w, 32, WAVE);
+    pq.x += __shfl_xor(pq.x, 32, WAVE); pq.y += __shfl_xor(pq.y, 32, WAVE);
+    pq.z += __shfl_xor(pq.z, 32, WAVE); pq.w += __shfl_xor(pq.w, 32, WAVE);
+    if (rs == 0) {
+        part[hl][w4][0][cg] = pk;
+        part[hl][w4][1][cg] = pq;
+    }
+    __syncthreads();
+    float4 SK = part[hl][0][0][cg], SQ = part[hl][0][1][cg];
+#pragma unroll
+    for (int w = 1; w < 4; w++) {
+        const float4 a = part[hl][w][0][cg], c = part[hl][w][1][cg];
+        SK.x += a.x; SK.y += a.y; SK.z += a.z; SK.w += a.w;
+        SQ.x += c.x; SQ.y += c.y; SQ.z += c.z; SQ.w += c.w;
+    }
+    const float decay = expf(g[(size_t)b * HV + hv]), bt = beta[(size_t)b * HV + hv];
+    const float* vv = sv[hl] + cg * 4;
+    float4 dl;
+    dl.x = (vv[0] - decay * SK.x) * bt;
+    dl.y = (vv[1] - decay * SK.y) * bt;
+    dl.z = (vv[2] - decay * SK.z) * bt;
+    dl.w = (vv[3] - decay * SK.w) * bt;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const float kr = sk[row0 + 8 * i];
+        float4 n;
+        n.x = decay * s[i].x + kr * dl.x;
+        n.y = decay * s[i].y + kr * dl.y;
+        n.z = decay * s[i].z + kr * dl.z;
+        n.w = decay * s[i].w + kr * dl.w;
+        *(float4*)(S + (size_t)(row0 + 8 * i) * D + cg * 4) = n;
+    }
+    if (w4 == 0 && rs == 0) {
+        Tout* o = out + ((size_t)b * HV + hv) * D + cg * 4;
+        Act<Tout>::st(o, 0, decay * SQ.x + kq * dl.x);
+        Act<Tout>::st(o, 1, decay * SQ.y + kq * dl.y);
+        Act<Tout>::st(o, 2, decay * SQ.z + kq * dl.z);
+        Act<Tout>::st(o, 3, decay * SQ.w + kq * dl.w);
+    }
+}
+
+template <int R, typename Tin>
+int launch_out(const void* qkv, const uint16_t* w, float* cs, const float* g, const float* beta, float* state,
+               void* out, int out_dtype, int B, int HK, int HV, float qscale, float eps, hipStream_t st) {
+    dim3 grid(HK, B);
+    if (out_dtype == AEGIST_F32)
+        delta_decode_kernel<R, Tin, float><<<grid, 256 * R, 0, st>>>((const Tin*)qkv, w, cs, g, beta, state,
+                                                                    (float*)out, HK, HV, qscale, eps);
+    else if (out_dtype == AEGIST_BF16)
+        delta_decode_kernel<R, Tin, uint16_t><<<grid, 256 * R, 0, st>>>((const Tin*)qkv, w, cs, g, beta, state,
+                                                                       (uint16_t*)out, HK, HV, qscale, eps);
+    else
+        return fail(AEGIST_ERR_DTYPE, "delta_decode_step: out dtype must be AEGIST_F32 or AEGIST_BF16");
+    return after_launch("delta_decode_step");
+}
+
+template <int R>
+int launch_in(const void* qkv, int in_dtype, const uint16_t* w, float* cs, const float* g, const float* beta,
+              float* state, void* out, int out_dtype, int B, int HK, int HV, float qscale, float eps, hipStream_t st) {
+    if (in_dtype == AEGIST_F32)
+        return launch_out<R, float>(qkv, w, cs, g, beta, state, out, out_dtype, B, HK, HV, qscale, eps, st);
+    if (in_dtype == AEGIST_BF16)
+        return launch_out<R, uint16_t>(qkv, w, cs, g, beta, state, out, out_dtype, B, HK, HV, qscale, eps, st);
+    return fail(AEGIST_ERR_DTYPE, "delta_decode_step: qkv dtype must be AEGIST_F32 or AEGIST_BF16");
+}
+
+}  // namespace
+
+namespace aegist {
+int launch_delta_decode(const void* qkv, int in_dtype, const uint16_t* conv_w, float* conv_state, const float* g,
+                        const float* beta, float* state, void* out, int out_dtype, int B, int HK, int HV,
+                        float qscale, float eps, hipStream_t st) {
+    if (B < 0 || HK <= 0 || HV <= 0 || HV % HK) return fail(AEGIST_ERR_SHAPE, "delta_decode_step: need HV % HK == 0");
+    if (B == 0) return 0;
+    switch (HV / HK) {
+        case 1: return launch_in<1>(qkv, in_dtype, conv_w, conv_state, g, beta, state, out, out_dtype, B, HK, HV, qscale, eps, st);
+        case 2: return launch_in<2>(qkv, in_dtype, conv_w, conv_state, g, beta, state, out, out_dtype, B, HK, HV, qscale, eps, st);
+        case 4: return launch_in<4>(qkv, in_dtype, conv_w, conv_state, g, beta, state, out, out_dtype, B, HK, HV, qscale, eps, st);
+        default: return fail(AEGIST_ERR_SHAPE, "delta_decode_step: HV / HK must be 1, 2 or 4");
+    }
+}
+}  // namespace aegist
+
+extern "C" int aegist_delta_decode_step(const void* qkv, int qkv_dtype, const uint16_t* conv_w, float* conv_state,
+                                        const float* g, const float* beta, float* state, void* out, int out_dtype,
+                                        int B, int HK, int HV, float qscale, float eps, void* stream) {
+    return launch_delta_decode(qkv, qkv_dtype, conv_w, conv_state, g, beta, state, out, out_dtype, B, HK, HV, qscale,
+                               eps, AEG_STREAM(stream));
+}

@@ -1,0 +1,285 @@
+// Bandwidth-light ops around the mixer: norms, gates, conv + SiLU, L2-norm, gated norm and
+// the attention prep (ZNorm + partial RoPE + bf16 cache append). One wave64 per head or row
+// segment, reductions by wave butterflies, no block-wide barriers where a wave suffices.
+// Engine-ABI mirrors of aegist_rs/kernels/hybrid.cu (cited per entry point).
+#include "common.h"
+
+#include <algorithm>
+
+using namespace aegist;
+
+// ---------------------------------------------------------------------------------------------
+// ZNorm: out = (1 + w) * x * rsqrt(mean(x^2) + eps). One block of 256 per row.
+// Semantics: hybrid.py:119-130 / hybrid.cu:69-78.
+__global__ void __launch_bounds__(256) znorm_kernel(const float* __restrict__ x, const uint16_t* __restrict__ w,
+                                                    float* __restrict__ out, int D, float eps) {
+    __shared__ float red[4];
+    const float* xr = x + (size_t)blockIdx.x * D;
+    float* orow = out + (size_t)blockIdx.x * D;
+    float ss = 0.f;
+    for (int i = threadIdx.x; i < D; i += 256) ss += xr[i] * xr[i];
+    ss = block_sum(ss, red);
+    float inv = rsqrtf(ss / (float)D + eps);
+    for (int i = threadIdx.x; i < D; i += 256) orow[i] = (xr[i] * inv) * (1.f + bf2f(w[i]));
+}
+
+extern "C" int aegist_znorm(const float* x, const uint16_t* w, float* out, int rows, int D, float eps, void* stream) {
+    AEG_REQUIRE(rows >= 0 && D > 0, "znorm: rows >= 0 and D > 0 required");
+    if (rows == 0) return 0;
+    znorm_kernel<<<rows, 256, 0, AEG_STREAM(stream)>>>(x, w, out, D, eps);
+    return after_launch("znorm");
+}
+
+// ---------------------------------------------------------------------------------------------
+// Attention prep. One wave per (token, head): heads [0, H) are queries (read from the first HD
+// of each head's 2*HD row of qg), heads [H, H+KV) are keys (k rows) whose values (v rows) are
+// copied alongside. HD <= 256 (4 elements per lane); RoPE partners are exchanged through LDS.
+struct RopeTable {
+    float inv[128];
+};
+
+template <typename Tin>
+__global__ void __launch_bounds__(256) attn_prep_kernel(
+    const Tin* __restrict__ qg, const Tin* __restrict__ k, const Tin* __restrict__ v, const uint16_t* __restrict__ qw,
+    const uint16_t* __restrict__ kw, float* __restrict__ qn, uint16_t* __restrict__ kc, uint16_t* __restrict__ vc,
+    int B, int T, int H, int KV, int HD, int RD, int pos0, int cap, float eps, RopeTable rope) {
+    __shared__ float buf[4][256];
+    const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+    const int item = blockIdx.x * 4 + wave;  // (b, t, head) flattened
+    const int heads = H + KV;
+    const bool valid = item < B * T * heads;
+    const int it = valid ? item : 0;
+    const int hh = it % heads, t = (it / heads) % T, b = it / (heads * T);
+    const bool isq = hh < H;
+    const int h = isq ? hh : hh - H;
+    const Tin* src = isq ? qg + (((size_t)b * T + t) * H + h) * 2 * HD : k + (((size_t)b * T + t) * KV + h) * HD;
+    const uint16_t* nw = isq ? qw : kw;
+    float x[4], ss = 0.f;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        int i = lane + r * WAVE;
+        x[r] = i < HD ? Act<Tin>::ld(src, i) : 0.f;
+        ss += x[r] * x[r];
+    }
+    ss = wave_sum(ss);
+    const float inv = rsqrtf(ss / (float)HD + eps);
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        int i = lane + r * WAVE;
+        x[r] = i < HD ? (x[r] * inv) * (1.f + bf2f(nw[i])) : 0.f;
+        buf[wave][i] = x[r];
+    }
+    __syncthreads();
+    if (!valid) return;
+    const int half = RD / 2, pos = pos0 + t;
+    float outv[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        int i = lane + r * WAVE;
+        outv[r] = x[r];
+        if (i < RD) {
+            int j = i < half ? i : i - half;
+            float ang = (float)pos * rope.inv[j];
+            float s, c;
+            sincosf(ang, &s, &c);
+            float rot = i < half ? -buf[wave][i + half] : buf[wave][i - half];
+            outv[r] = x[r] * c + rot * s;
+        }
+    }
+    if (isq) {
+        float* dst = qn + (((size_t)b * T + t) * H + h) * HD;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            int i = lane + r * WAVE;
+            if (i < HD) dst[i] = outv[r];
+        }
+    } else {
+        size_t o = (((size_t)b * KV + h) * cap + pos) * HD;
+        const Tin* vs = v + (((size_t)b * T + t) * KV + h) * HD;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            int i = lane + r * WAVE;
+            if (i < HD) {
+                kc[o + i] = f2bf(outv[r]);
+                vc[o + i] = f2bf(Act<Tin>::ld(vs, i));
+            }
+        }
+    }
+}
+
+namespace aegist {
+int make_rope_table(RopeTable* tab, int RD, float theta) {
+    if (RD <= 0 || (RD & 1) || RD > 256) return fail(AEGIST_ERR_SHAPE, "rope: rotary dim must be even and in [2, 256]");
+    return aegist_rope_inv_freq(tab->inv, RD, theta);
+}
+
+// Batched prep used by the engine mirror and by the batched decode entry point.
+// qn [B, T, H, HD] fp32 (the engine layout); caches [B, KV, cap, HD].
+int launch_attn_prep(const void* qg, const void* k, const void* v, int in_dtype, const uint16_t* qw,
+                     const uint16_t* kw, float* qn, uint16_t* kc, uint16_t* vc, int B, int T, int H, int KV, int HD,
+                     int RD, int pos0, int cap, float eps, float theta, hipStream_t stream) {
+    if (HD <= 0 || HD > 256 || RD > HD) return fail(AEGIST_ERR_SHAPE, "attn_prep: need 0 < HD <= 256 and RD <= HD");
+    if (pos0 < 0 || pos0 + T > cap) return fail(AEGIST_ERR_SHAPE, "attn_prep: positions exceed the cache capacity");
+    RopeTable tab;
+    int rc = make_rope_table(&tab, RD, theta);
+    if (rc) return rc;
+    int items = B * T * (H + KV);
+    if (items == 0) return 0;
+    dim3 grid((items + 3) / 4);
+    if (in_dtype == AEGIST_F32)
+        attn_prep_kernel<float><<<grid, 256, 0, stream>>>((const float*)qg, (const float*)k, (const float*)v, qw, kw, qn,
+                                                          kc, vc, B, T, H, KV, HD, RD, pos0, cap, eps, tab);
+    else if (in_dtype == AEGIST_BF16)
+        attn_prep_kernel<uint16_t><<<grid, 256, 0, stream>>>((const uint16_t*)qg, (const uint16_t*)k,
+                                                             (const uint16_t*)v, qw, kw, qn, kc, vc, B, T, H, KV, HD,
+                                                             RD, pos0, cap, eps, tab);
+    else
+        return fail(AEGIST_ERR_DTYPE, "attn_prep: dtype must be AEGIST_F32 or AEGIST_BF16");
+    return after_launch("attn_prep");
+}
+}  // namespace aegist
+
+extern "C" int aegist_attn_prep(const float* qg, const float* k, const float* v, const uint16_t* qw, const uint16_t* kw,
+                                float* qn, uint16_t* kc, uint16_t* vc, int T, int H, int KV, int HD, int RD, int pos0,
+                                int cap, float eps, float theta, void* stream) {
+    return launch_attn_prep(qg, k, v, AEGIST_F32, qw, kw, qn, kc, vc, 1, T, H, KV, HD, RD, pos0, cap, eps, theta,
+                            AEG_STREAM(stream));
+}
+
+// ---------------------------------------------------------------------------------------------
+// DeltaNet gates: one wave per (token, output j); j < HV -> beta_j, else g_{j-HV}.
+// gb [T, 2HV]: g first, then beta (hybrid.cu:179-200; hybrid.py:403-404, softplus threshold 20).
+__global__ void __launch_bounds__(256) delta_gates_kernel(const float* __restrict__ h, const uint16_t* __restrict__ wb,
+                                                          const uint16_t* __restrict__ wa,
+                                                          const uint16_t* __restrict__ a_log,
+                                                          const uint16_t* __restrict__ dt_bias, float* __restrict__ gb,
+                                                          int T, int D, int HV) {
+    const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+    const int item = blockIdx.x * 4 + wave;
+    if (item >= T * 2 * HV) return;
+    const int t = item / (2 * HV), j = item % (2 * HV);
+    const float* hr = h + (size_t)t * D;
+    const uint16_t* wr = j < HV ? wb + (size_t)j * D : wa + (size_t)(j - HV) * D;
+    float acc = 0.f;
+    for (int i = lane; i < D; i += WAVE) acc += hr[i] * bf2f(wr[i]);
+    acc = wave_sum(acc);
+    if (lane == 0) {
+        if (j < HV) {
+            gb[(size_t)t * 2 * HV + HV + j] = 1.f / (1.f + expf(-acc));
+        } else {
+            int jj = j - HV;
+            float xx = acc + bf2f(dt_bias[jj]);
+            float sp = xx > 20.f ? xx : log1pf(expf(xx));
+            gb[(size_t)t * 2 * HV + jj] = -expf(bf2f(a_log[jj])) * sp;
+        }
+    }
+}
+
+extern "C" int aegist_delta_gates(const float* h, const uint16_t* wb, const uint16_t* wa, const uint16_t* a_log,
+                                  const uint16_t* dt_bias, float* gb, int T, int D, int HV, void* stream) {
+    AEG_REQUIRE(T >= 0 && D > 0 && HV > 0, "delta_gates: bad shape");
+    if (T == 0) return 0;
+    int items = T * 2 * HV;
+    delta_gates_kernel<<<(items + 3) / 4, 256, 0, AEG_STREAM(stream)>>>(h, wb, wa, a_log, dt_bias, gb, T, D, HV);
+    return after_launch("delta_gates");
+}
+
+// ---------------------------------------------------------------------------------------------
+// Depthwise causal conv (kernel 4) + SiLU over T rows, continuing from state [C,3] (oldest
+// first). One block owns 64 channels for the whole sequence, so the in-place state update is
+// ordered after every read of the old state by the block barrier. Threads: 64 channels x 4
+// token lanes. (hybrid.cu:205-221; hybrid.py:390-398.)
+__global__ void __launch_bounds__(256) conv_silu_kernel(const float* __restrict__ x, float* __restrict__ y,
+                                                        const uint16_t* __restrict__ w, float* __restrict__ state,
+                                                        int T, int C) {
+    const int c = blockIdx.x * 64 + (threadIdx.x % 64), tl = threadIdx.x / 64;
+    const bool ok = c < C;
+    float s0 = 0.f, s1 = 0.f, s2 = 0.f, w0 = 0.f, w1 = 0.f, w2 = 0.f, w3 = 0.f;
+    if (ok) {
+        s0 = state[(size_t)c * 3];
+        s1 = state[(size_t)c * 3 + 1];
+        s2 = state[(size_t)c * 3 + 2];
+        w0 = bf2f(w[(size_t)c * 4]);
+        w1 = bf2f(w[(size_t)c * 4 + 1]);
+        w2 = bf2f(w[(size_t)c * 4 + 2]);
+        w3 = bf2f(w[(size_t)c * 4 + 3]);
+        for (int t = tl; t < T; t += 4) {
+            float xm3 = t >= 3 ? x[(size_t)(t - 3) * C + c] : (t == 0 ? s0 : (t == 1 ? s1 : s2));
+            float xm2 = t >= 2 ? x[(size_t)(t - 2) * C + c] : (t == 0 ? s1 : s2);
+            float xm1 = t >= 1 ? x[(size_t)(t - 1) * C + c] : s2;
+            float x0 = x[(size_t)t * C + c];
+            y[(size_t)t * C + c] = silu_f(w0 * xm3 + w1 * xm2 + w2 * xm1 + w3 * x0);
+        }
+    }
+    __syncthreads();
+    if (ok && tl == 0) {
+        // new state = last three of [s0, s1, s2, x_0 .. x_{T-1}]
+        float h0 = T >= 3 ? x[(size_t)(T - 3) * C + c] : (T == 2 ? s2 : (T == 1 ? s1 : s0));
+        float h1 = T >= 2 ? x[(size_t)(T - 2) * C + c] : (T == 1 ? s2 : s1);
+        float h2 = T >= 1 ? x[(size_t)(T - 1) * C + c] : s2;
+        state[(size_t)c * 3] = h0;
+        state[(size_t)c * 3 + 1] = h1;
+        state[(size_t)c * 3 + 2] = h2;
+    }
+}
+
+extern "C" int aegist_conv_silu(const float* x, float* y, const uint16_t* w, float* state, int T, int C, void* stream) {
+    AEG_REQUIRE(T >= 0 && C > 0, "conv_silu: bad shape");
+    if (T == 0) return 0;
+    conv_silu_kernel<<<(C + 63) / 64, 256, 0, AEG_STREAM(stream)>>>(x, y, w, state, T, C);
+    return after_launch("conv_silu");
+}
+
+// ---------------------------------------------------------------------------------------------
+// L2-norm of the first 2*nq heads of each row (queries scaled by qscale). One wave per
+// (row, head). (hybrid.cu:225-232; hybrid.py:314-315, 408-410.)
+__global__ void __launch_bounds__(256) l2norm_heads_kernel(float* __restrict__ y, int T, int C, int nq, int dk,
+                                                           float qscale, float eps) {
+    const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+    const int item = blockIdx.x * 4 + wave;
+    if (item >= T * 2 * nq) return;
+    const int t = item / (2 * nq), hh = item % (2 * nq);
+    float* p = y + (size_t)t * C + (size_t)hh * dk;
+    float ss = 0.f;
+    for (int i = lane; i < dk; i += WAVE) ss += p[i] * p[i];
+    ss = wave_sum(ss);
+    const float r = rsqrtf(ss + eps), s = hh < nq ? qscale : 1.f;
+    for (int i = lane; i < dk; i += WAVE) p[i] = (p[i] * r) * s;
+}
+
+extern "C" int aegist_l2norm_heads(float* y, int T, int C, int nq, int dk, float qscale, float eps, void* stream) {
+    AEG_REQUIRE(T >= 0 && nq > 0 && dk > 0 && 2 * nq * dk <= C, "l2norm_heads: bad shape");
+    if (T == 0) return 0;
+    int items = T * 2 * nq;
+    l2norm_heads_kernel<<<(items + 3) / 4, 256, 0, AEG_STREAM(stream)>>>(y, T, C, nq, dk, qscale, eps);
+    return after_launch("l2norm_heads");
+}
+
+// ---------------------------------------------------------------------------------------------
+// Gated norm: out = w * rmsnorm(o) * silu(z) per value head; one wave per (row, head).
+// (hybrid.cu:303-311; hybrid.py:133-147 with act = silu.)
+__global__ void __launch_bounds__(256) gated_norm_kernel(const float* __restrict__ o, const float* __restrict__ z,
+                                                         const uint16_t* __restrict__ w, float* __restrict__ out,
+                                                         int rows, int DV, float eps) {
+    const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+    const int item = blockIdx.x * 4 + wave;
+    if (item >= rows) return;
+    const size_t base = (size_t)item * DV;
+    float ss = 0.f;
+    for (int i = lane; i < DV; i += WAVE) ss += o[base + i] * o[base + i];
+    ss = wave_sum(ss);
+    const float r = rsqrtf(ss / (float)DV + eps);
+    for (int i = lane; i < DV; i += WAVE) {
+        float zz = z[base + i];
+        out[base + i] = bf2f(w[i]) * (o[base + i] * r) * (zz / (1.f + expf(-zz)));
+    }
+}
+
+extern "C" int aegist_gated_norm(const float* o, const float* z, const uint16_t* w, float* out, int T, int HV, int DV,
+                                 float eps, void* stream) {
+    AEG_REQUIRE(T >= 0 && HV > 0 && DV > 0, "gated_norm: bad shape");
+    int rows = T * HV;
+    if (rows == 0) return 0;
+    gated_norm_kernel<<<(rows + 3) / 4, 256, 0, AEG_STREAM(stream)>>>(o, z, w, out, rows, DV, eps);
+    return after_launch("gated_norm");
+}

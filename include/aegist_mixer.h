@@ -1,0 +1,202 @@
+/*
+ * aegist_mixer.h — C ABI of the MI355X (gfx950) token-mixer library libaegist_mixer.so.
+ *
+ * Drop-in for the mixer kernels the Aegist Rust engine launches by name from its PTX module
+ * (/root/reference/aegist-fast-35b/aegist_rs/src/hybrid.rs:515-537, launched in
+ * HybridEngine::mixer hybrid.rs:787-861 and the identical arms of next.rs:1840-1972 and
+ * max.rs:654-728), plus batched entry points for the gated DeltaNet decode step, chunked
+ * DeltaNet prefill and split-K GQA decode.
+ *
+ * Conventions (replacing aegist_rs/src/cuda.rs):
+ *  - Every function returns 0 on success, a positive hipError_t value on a runtime error, or
+ *    a negative AEGIST_ERR_* code on a rejected argument. aegist_last_error() gives the text
+ *    (thread-local). Nothing throws across the ABI.
+ *  - All device pointers are caller-owned; kernels never allocate. Entry points that need
+ *    scratch take a caller-provided workspace sized by the matching *_workspace_bytes query.
+ *    The engine-ABI mirrors whose reference signature has no workspace argument
+ *    (aegist_attention_gated, aegist_delta_scan) use a per-device workspace the library grows
+ *    on demand; that is the only allocation the library makes on its own.
+ *  - `stream` is a hipStream_t (NULL = the device's null stream). Every launch is
+ *    asynchronous on that stream; no entry point synchronises unless named *_sync. Setting
+ *    AEGIST_SYNC_LAUNCH=1 synchronises after each launch and reports errors at the launch.
+ *  - Not re-entrant on one stream from several threads (same as the reference).
+ *  - Activation dtypes: AEGIST_F32 or AEGIST_BF16 where an argument says so; state and conv
+ *    state are always fp32; weights of the engine mirrors are bf16 (uint16_t bits).
+ */
+#ifndef AEGIST_MIXER_H
+#define AEGIST_MIXER_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { AEGIST_F32 = 0, AEGIST_BF16 = 1 };
+
+enum {
+    AEGIST_OK = 0,
+    AEGIST_ERR_SHAPE = -1,     /* unsupported shape or argument (message names it) */
+    AEGIST_ERR_WORKSPACE = -2, /* workspace missing or too small */
+    AEGIST_ERR_DTYPE = -3,     /* dtype code not supported by this entry point */
+};
+
+/* ---------------------------------------------------------------------------------------
+ * Runtime: device selection, errors, memory (replaces aegist_rs/src/cuda.rs:19-42, 62-86,
+ * 194-316: cuInit/context-per-thread, cuMemAlloc/Free, HtoD/DtoH/DtoD copies, memset,
+ * cuMemGetInfo).
+ * ------------------------------------------------------------------------------------- */
+const char* aegist_last_error(void);
+const char* aegist_version(void);
+int aegist_set_device(int device);
+int aegist_malloc(void** ptr, size_t bytes);
+int aegist_free(void* ptr);
+int aegist_memcpy_htod(void* dst, const void* src, size_t bytes, void* stream);
+int aegist_memcpy_dtoh(void* dst, const void* src, size_t bytes, void* stream);
+int aegist_memcpy_dtod(void* dst, const void* src, size_t bytes, void* stream);
+int aegist_memset(void* dst, int value, size_t bytes, void* stream);
+int aegist_mem_info(size_t* free_bytes, size_t* total_bytes);
+int aegist_stream_sync(void* stream);
+
+/* Synthetic inputs: n values ~ N(mean, std) from a counter-based generator
+ * (splitmix64 -> Box-Muller; element i depends only on (seed, i)), written as fp32 or bf16.
+ * No reference counterpart: the bench and tests use it to build inputs on the device. */
+int aegist_fill_normal(void* dst, size_t n, int dtype, uint64_t seed, float mean, float std, void* stream);
+
+/* ---------------------------------------------------------------------------------------
+ * Engine-ABI mirrors: same argument lists as the reference kernels (fp32 activations, bf16
+ * weights, batch 1, layouts of hybrid.rs), plus `stream`.
+ * ------------------------------------------------------------------------------------- */
+
+/* Zero-centred RMSNorm out = (1 + w) * x / rms(x), `rows` rows of D.
+ * Replaces znorm, aegist_rs/kernels/hybrid.cu:69-78 (launched hybrid.rs:737-740). */
+int aegist_znorm(const float* x, const uint16_t* w, float* out, int rows, int D, float eps, void* stream);
+
+/* Per (token, head): ZNorm of the query (first HD of each head's 2*HD in qg) and of k,
+ * rotate-half RoPE on the first RD dims at position pos0 + t; q -> qn [T,H,HD] fp32;
+ * k, v -> bf16 caches [KV,cap,HD] at pos0 + t.
+ * Replaces attn_prep, hybrid.cu:86-116 (launched hybrid.rs:800-809). */
+int aegist_attn_prep(const float* qg, const float* k, const float* v, const uint16_t* qw, const uint16_t* kw,
+                     float* qn, uint16_t* kc, uint16_t* vc, int T, int H, int KV, int HD, int RD, int pos0, int cap,
+                     float eps, float theta, void* stream);
+
+/* Causal GQA attention of T queries at positions pos0.. over cache rows [0, pos0+t], then
+ * out = attention * sigmoid(gate) with gate = the second HD of each head in qg.
+ * HD must be 256. T == 1 runs the split-K decode kernel, T > 1 the MFMA flash kernel.
+ * Replaces attention_gated, hybrid.cu:121-173 (launched hybrid.rs:810-818). */
+int aegist_attention_gated(const float* q, const uint16_t* kc, const uint16_t* vc, const float* qg, float* out, int T,
+                           int H, int KV, int pos0, int cap, float scale, void* stream);
+
+/* beta = sigmoid(h . Wb[j]); g = -exp(A_log[j]) * softplus(h . Wa[j] + dt_bias[j]).
+ * gb [T, 2*HV]: g in [0, HV), beta in [HV, 2*HV).
+ * Replaces delta_gates, hybrid.cu:179-200 (launched hybrid.rs:827-834). */
+int aegist_delta_gates(const float* h, const uint16_t* wb, const uint16_t* wa, const uint16_t* a_log,
+                       const uint16_t* dt_bias, float* gb, int T, int D, int HV, void* stream);
+
+/* Depthwise causal conv (kernel 4) over T new rows continuing from state [C,3] (oldest
+ * first, updated), then SiLU. x, y [T,C] fp32; w [C,4] bf16 (w[3] hits the newest input).
+ * Replaces conv_silu, hybrid.cu:205-221 (launched hybrid.rs:835-839). */
+int aegist_conv_silu(const float* x, float* y, const uint16_t* w, float* state, int T, int C, void* stream);
+
+/* In place on y [T,C]: L2-normalise the first 2*nq heads of dk (queries then keys), eps
+ * inside the rsqrt of the sum; queries also times qscale.
+ * Replaces l2norm_heads, hybrid.cu:225-232 (launched hybrid.rs:840-844). */
+int aegist_l2norm_heads(float* y, int T, int C, int nq, int dk, float qscale, float eps, void* stream);
+
+/* Gated delta rule over T tokens: y [T,C] rows q (HK heads) | k (HK heads) | v (HV heads),
+ * already L2-normalised; gb [T,2HV] from delta_gates; state [HV,128,128] fp32 (row = key
+ * dim), updated; o [T,HV,128] fp32. dk = dv = 128.
+ * T == 1: fused decode step; T < 64: recurrent scan; T >= 64: chunked WY prefill (MFMA).
+ * Replaces delta_scan, hybrid.cu:240-300 (launched hybrid.rs:845-852). */
+int aegist_delta_scan(const float* y, const float* gb, float* state, float* o, int T, int C, int HK, int HV,
+                      void* stream);
+
+/* out = w * rmsnorm(o) * silu(z) per value head. o, z, out [T,HV,DV] fp32; w [DV] bf16.
+ * Replaces gated_norm, hybrid.cu:303-311 (launched hybrid.rs:853-857). */
+int aegist_gated_norm(const float* o, const float* z, const uint16_t* w, float* out, int T, int HV, int DV, float eps,
+                      void* stream);
+
+/* ---------------------------------------------------------------------------------------
+ * Batched gated DeltaNet (the reference is batch 1 only; these add B and strides).
+ * Semantics: aegist/hybrid.py:314-421 (l2norm :314, delta_rule_step :318-324,
+ * delta_rule_chunked :327-361, GatedDeltaNet.forward :388-421). dk = dv = 128; HV % HK == 0
+ * and HV / HK in {1, 2, 4}.
+ * ------------------------------------------------------------------------------------- */
+
+/* One decode token per sequence, fused: conv-state update + depthwise conv (kernel 4) +
+ * SiLU + split + L2-norm + q * qscale + gated delta step.
+ *   qkv        [B, C] pre-conv projection (qkv_dtype), C = 2*HK*128 + HV*128, rows q|k|v
+ *   conv_w     [C, 4] bf16
+ *   conv_state [B, C, 3] fp32, oldest first, updated
+ *   g, beta    [B, HV] fp32 (log decay, write strength)
+ *   state      [B, HV, 128, 128] fp32, updated in place
+ *   out        [B, HV, 128] (out_dtype)
+ * Replaces the T == 1 path conv_silu -> l2norm_heads -> delta_scan
+ * (hybrid.rs:835-852; hybrid.py:393-413). */
+int aegist_delta_decode_step(const void* qkv, int qkv_dtype, const uint16_t* conv_w, float* conv_state,
+                             const float* g, const float* beta, float* state, void* out, int out_dtype, int B, int HK,
+                             int HV, float qscale, float eps, void* stream);
+
+/* Sequence layout shared by the recurrent and chunked entry points. Element strides (not
+ * bytes) for batch, token and head; the head dim is contiguous. For the engine's y [T,C]
+ * rows: q = y, k = y + HK*128, v = y + 2*HK*128, token stride C, head stride 128.
+ * q, k are indexed by QK head (HK of them); v, out by value head; value head h reads QK head
+ * h / (HV/HK). g, beta [B, T, HV] fp32 contiguous. If `normalize` is non-zero the kernels
+ * L2-normalise q and k (eps) and scale q by qscale (hybrid.py:408-410); otherwise they use
+ * q, k as given. */
+int aegist_delta_recurrent(const void* q, const void* k, const void* v, int in_dtype, long long sb_qk,
+                           long long st_qk, long long sh_qk, long long sb_v, long long st_v, long long sh_v,
+                           const float* g, const float* beta, float* state, void* out, int out_dtype,
+                           long long sb_o, long long st_o, long long sh_o, int B, int T, int HK, int HV,
+                           int normalize, float qscale, float eps, void* stream);
+
+/* Chunked (C = 64) WY-form prefill of the same recurrence, MFMA (fp16 operands after fp32
+ * per-row normalisation, fp32 accumulation and state). state may be NULL (zero initial state,
+ * final state not returned) or [B,HV,128,128] fp32 in/out. Needs workspace of
+ * aegist_delta_chunked_workspace_bytes(B, T, HV) bytes (256-byte aligned). */
+size_t aegist_delta_chunked_workspace_bytes(int B, int T, int HV);
+int aegist_delta_chunked(const void* q, const void* k, const void* v, int in_dtype, long long sb_qk,
+                         long long st_qk, long long sh_qk, long long sb_v, long long st_v, long long sh_v,
+                         const float* g, const float* beta, float* state, void* out, int out_dtype, long long sb_o,
+                         long long st_o, long long sh_o, int B, int T, int HK, int HV, int normalize, float qscale,
+                         float eps, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------------------
+ * Batched gated GQA attention (hybrid.py:265-311). HD = 256, H / KV <= 8, RD even <= HD.
+ * ------------------------------------------------------------------------------------- */
+
+/* RoPE inverse-frequency table inv[j] = 1 / theta^(2j/RD), j < RD/2, evaluated in double
+ * and rounded once to fp32 (hybrid.py:154 uses an fp32 pow). Every attention entry point
+ * uses this table; exported so a CPU checker can use the identical values. */
+int aegist_rope_inv_freq(float* inv_out, int RD, float theta);
+
+/* Decode: one query token per sequence at position `pos` (all sequences share the length).
+ *   qg     [B, H, 2*HD] (in_dtype): query | gate per head (hybrid.py:285-286)
+ *   k_new, v_new [B, KV, HD] (in_dtype): projections of the new token
+ *   q_norm_w, k_norm_w [HD] bf16: ZNorm weights (hybrid.py:276-277)
+ *   kc, vc [B, KV, cap, HD] bf16 caches; row `pos` is written here
+ *   out    [B, H, HD] (out_dtype) = softmax(q K^T / sqrt(HD)) V * sigmoid(gate) over rows
+ *          [0, pos]
+ * Split-K over the context with a log-sum-exp merge; needs
+ * aegist_attention_decode_workspace_bytes(B, H, KV, pos + 1) bytes of workspace. */
+size_t aegist_attention_decode_workspace_bytes(int B, int H, int KV, int L);
+int aegist_attention_decode(const void* qg, const void* k_new, const void* v_new, int in_dtype,
+                            const uint16_t* q_norm_w, const uint16_t* k_norm_w, uint16_t* kc, uint16_t* vc,
+                            void* out, int out_dtype, int B, int H, int KV, int HD, int RD, int pos, int cap,
+                            float eps, float theta, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Attention core only (no prep): q [B, H, T, HD] fp32 already normed and roped, caches
+ * [B, KV, cap, HD] bf16 holding rows [0, pos + T), gate [B, T, H*HD] fp32 or NULL (no gate).
+ * out [B, T, H, HD] fp32. Causal with offset: query t sees rows [0, pos + t].
+ * T == 1 uses split-K (workspace as above with L = pos + 1); T > 1 the flash kernel
+ * (no workspace). */
+int aegist_attention_core(const float* q, const uint16_t* kc, const uint16_t* vc, const float* gate, float* out,
+                          int B, int H, int KV, int T, int pos, int cap, float scale, void* workspace,
+                          size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* AEGIST_MIXER_H */

@@ -1,0 +1,251 @@
+"""CPU restatement of the Aegist token-mixer ops (torch-CPU, fp32 unless stated).
+
+TEST INFRASTRUCTURE ONLY. This module is the checker that the HIP kernels are compared
+against; only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import
+it. The product path (the HIP library and its bindings) never calls into it.
+
+Every function restates one op of the reference's torch model, written from the equations
+in /root/reference/aegist-fast-35b/aegist/hybrid.py (cited per function as
+``hybrid.py:<lines>``) and the engine conventions of aegist_rs/kernels/hybrid.cu. Layouts
+follow the reference: DeltaNet tensors heads-first ``[B, H, T, d]``; attention caches
+``[B, KV, cap, HD]``.
+
+Pinning (how each function is checked independently of its own formula) lives in
+tests/test_oracle_pins.py: fp64 brute force, closed-form special cases, chunked-vs-recurrent
+equivalence, one-at-a-time-vs-all-at-once conv, RoPE identities and norm preservation.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+import torch.nn.functional as F
+
+
+# --- norms (hybrid.py:119-147) --------------------------------------------------------------
+
+def znorm(x: torch.Tensor, w: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+    """Zero-centred RMSNorm ``(1 + w) * x / rms(x)`` in fp32 (hybrid.py:119-130)."""
+    xf = x.float()
+    xf = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)
+    return (xf * (1.0 + w.float())).to(x.dtype)
+
+
+def gated_norm(x: torch.Tensor, z: torch.Tensor, w: torch.Tensor, eps: float = 1e-6,
+               act: str = "silu") -> torch.Tensor:
+    """``w * rmsnorm(x) * act(z)`` per value head (hybrid.py:133-147).
+
+    The normalised x is cast back to x.dtype before the weight multiply (hybrid.py:145) and
+    the gate is computed in fp32 (hybrid.py:146)."""
+    xf = x.float()
+    xf = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)
+    y = w * xf.to(x.dtype)
+    g = torch.sigmoid(z.float()) if act == "sigmoid" else F.silu(z.float())
+    return (y * g).to(x.dtype)
+
+
+# --- position (hybrid.py:152-166) ------------------------------------------------------------
+
+def rope_inv_freq(rotary_dim: int, theta: float) -> torch.Tensor:
+    """``1 / theta^(2j / rd)`` for j < rd/2, as fp32.
+
+    hybrid.py:154 evaluates this with torch's fp32 ``pow``. This build evaluates it in fp64
+    and rounds once to fp32, and the HIP library is handed the identical table (computed the
+    same way on the host), so CPU and GPU angles agree to the last bit of ``pos * inv``."""
+    j = torch.arange(0, rotary_dim, 2, dtype=torch.float64)
+    return (1.0 / (theta ** (j / rotary_dim))).to(torch.float32)
+
+
+def rope_tables(rotary_dim: int, theta: float, positions: torch.Tensor):
+    """cos/sin tables ``[len(positions), rd]`` with ``emb = cat(f, f)`` (hybrid.py:152-157)."""
+    inv = rope_inv_freq(rotary_dim, theta)
+    f = torch.outer(positions.to(torch.float32), inv)  # fp32 product, as hybrid.py:155
+    emb = torch.cat([f, f], -1)
+    return emb.cos(), emb.sin()
+
+
+def apply_partial_rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """Rotate-half RoPE on the first ``cos.shape[-1]`` dims; pass the rest (hybrid.py:160-166)."""
+    rd = cos.shape[-1]
+    xr, xp = x[..., :rd], x[..., rd:]
+    h = rd // 2
+    rot = torch.cat([-xr[..., h:], xr[..., :h]], -1)
+    return torch.cat([xr * cos.to(x.dtype) + rot * sin.to(x.dtype), xp], -1)
+
+
+# --- gated DeltaNet (hybrid.py:314-421) ------------------------------------------------------
+
+def l2norm(x: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+    """``x * rsqrt(sum(x^2) + eps)`` over the last dim (hybrid.py:314-315)."""
+    return x * torch.rsqrt((x * x).sum(-1, keepdim=True) + eps)
+
+
+def delta_rule_step(q, k, v, g, beta, state):
+    """One token of the gated delta rule (hybrid.py:318-324).
+
+    q, k ``[B,H,dk]``; v ``[B,H,dv]``; g, beta ``[B,H]``; state ``[B,H,dk,dv]`` fp32, updated
+    in place. Returns o ``[B,H,dv]``."""
+    state.mul_(g.exp()[..., None, None])
+    kv_mem = (state * k.unsqueeze(-1)).sum(-2)
+    delta = (v - kv_mem) * beta.unsqueeze(-1)
+    state.add_(k.unsqueeze(-1) * delta.unsqueeze(-2))
+    return (state * q.unsqueeze(-1)).sum(-2)
+
+
+def delta_rule_recurrent(q, k, v, g, beta, state=None):
+    """``delta_rule_step`` looped over T (the form hybrid.py:411-413 takes one token at a time).
+
+    q, k ``[B,H,T,dk]``; v ``[B,H,T,dv]``; g, beta ``[B,H,T]``. Returns (o, final state)."""
+    B, H, T, dk = k.shape
+    dv = v.shape[-1]
+    S = torch.zeros(B, H, dk, dv, dtype=q.dtype) if state is None else state.clone().to(q.dtype)
+    outs = [delta_rule_step(q[:, :, t], k[:, :, t], v[:, :, t], g[:, :, t], beta[:, :, t], S) for t in range(T)]
+    o = torch.stack(outs, 2) if outs else torch.zeros(B, H, 0, dv, dtype=q.dtype)
+    return o, S
+
+
+def delta_rule_chunked(q, k, v, g, beta, state=None, chunk: int = 64):
+    """Chunked WY/UT form of the gated delta rule (hybrid.py:327-361).
+
+    Pads T to a multiple of ``chunk`` (hybrid.py:336-339); per chunk with ``cum = cumsum(g)``:
+    ``A = (kb k^T) o decay`` solved as a unit lower-triangular system (diagonal ignored) for
+    ``u = A^-1 vb`` and ``w = A^-1 (kb e^cum)``; ``intra = (q k^T) o decay`` (diagonal kept);
+    then sequentially ``v_new = u - w S; o = (q e^cum) S + intra v_new;
+    S = S e^{cum_last} + (k e^{cum_last - cum})^T v_new``."""
+    B, H, T, dk = k.shape
+    dv = v.shape[-1]
+    pad = (chunk - T % chunk) % chunk
+    if pad:
+        q, k, v = (F.pad(t, (0, 0, 0, pad)) for t in (q, k, v))
+        g, beta = (F.pad(t, (0, pad)) for t in (g, beta))
+    n = (T + pad) // chunk
+    kb = (k * beta.unsqueeze(-1)).view(B, H, n, chunk, dk)
+    vb = (v * beta.unsqueeze(-1)).view(B, H, n, chunk, dv)
+    q, k = q.reshape(B, H, n, chunk, dk), k.reshape(B, H, n, chunk, dk)
+    cum = g.reshape(B, H, n, chunk).cumsum(-1)
+    upper = torch.ones(chunk, chunk, dtype=torch.bool).triu(1)
+    decay = (cum.unsqueeze(-1) - cum.unsqueeze(-2)).masked_fill(upper, float("-inf")).exp()
+    system = (kb @ k.transpose(-1, -2)) * decay
+    u = torch.linalg.solve_triangular(system, vb, upper=False, unitriangular=True)
+    w = torch.linalg.solve_triangular(system, kb * cum.exp().unsqueeze(-1), upper=False, unitriangular=True)
+    intra = (q @ k.transpose(-1, -2)) * decay
+    q_dec = q * cum.exp().unsqueeze(-1)
+    k_dec = k * (cum[..., -1:] - cum).exp().unsqueeze(-1)
+    chunk_decay = cum[..., -1].exp()[..., None, None]
+    S = torch.zeros(B, H, dk, dv, dtype=q.dtype) if state is None else state.to(q.dtype).clone()
+    outs = []
+    for i in range(n):
+        v_new = u[:, :, i] - w[:, :, i] @ S
+        outs.append(q_dec[:, :, i] @ S + intra[:, :, i] @ v_new)
+        S = S * chunk_decay[:, :, i] + k_dec[:, :, i].transpose(-1, -2) @ v_new
+    out = torch.stack(outs, 2).reshape(B, H, n * chunk, dv)[:, :, :T]
+    return out, S
+
+
+def conv_silu(x: torch.Tensor, w: torch.Tensor, state: torch.Tensor | None):
+    """Depthwise causal conv (kernel K) continuing from the K-1 previous inputs, then SiLU.
+
+    x ``[B,T,C]``; w ``[C,K]`` (w[:, K-1] multiplies the newest input); state ``[B,C,K-1]``
+    oldest first, or None for zeros. Returns (y ``[B,T,C]``, new state ``[B,C,K-1]``) — the
+    new state is the last K-1 inputs of ``cat(state, x)`` (hybrid.py:393-398; the engine's
+    conv_silu in hybrid.cu:205-221 has the same contract)."""
+    B, T, C = x.shape
+    K = w.shape[1]
+    prev = torch.zeros(B, C, K - 1, dtype=x.dtype) if state is None else state.to(x.dtype)
+    xp = torch.cat([prev, x.transpose(1, 2)], -1)
+    new_state = xp[..., -(K - 1):].clone()
+    y = F.silu(F.conv1d(xp, w.to(x.dtype).unsqueeze(1), groups=C)).transpose(1, 2)
+    return y, new_state
+
+
+def delta_gates(h, wb, wa, a_log, dt_bias):
+    """``beta = sigmoid(h Wb^T)``, ``g = -exp(A_log) softplus(h Wa^T + dt_bias)`` (hybrid.py:403-404;
+    F.softplus has threshold 20, as hybrid.cu:195). h ``[..., D]``; wb, wa ``[HV, D]``."""
+    beta = (h.float() @ wb.float().t()).sigmoid()
+    g = -a_log.float().exp() * F.softplus(h.float() @ wa.float().t() + dt_bias.float())
+    return g, beta
+
+
+def delta_prep(y: torch.Tensor, hk: int, hv: int, dk: int, dv: int, eps: float = 1e-6):
+    """Split post-conv rows ``y [B,T,2*hk*dk + hv*dv]`` into heads-first q, k, v
+    ``[B,HV,T,d]`` with the QK heads repeated ``hv/hk`` times, q and k L2-normalised and q
+    scaled by ``dk^-1/2`` (hybrid.py:399-410)."""
+    B, T, _ = y.shape
+    q, k, v = y.split([hk * dk, hk * dk, hv * dv], -1)
+    q, k, v = q.reshape(B, T, hk, dk), k.reshape(B, T, hk, dk), v.reshape(B, T, hv, dv)
+    r = hv // hk
+    if r > 1:
+        q, k = q.repeat_interleave(r, 2), k.repeat_interleave(r, 2)
+    q, k, v = (t.transpose(1, 2).float() for t in (q, k, v))
+    q, k = l2norm(q, eps), l2norm(k, eps)
+    return q * dk ** -0.5, k, v
+
+
+def delta_decode_fused(qkv, conv_w, conv_state, g, beta, state, hk: int, hv: int, d: int = 128):
+    """One decode token of a gated DeltaNet layer from the pre-conv projection onwards:
+    conv state update + depthwise conv + SiLU + split + L2-norm + q-scale + delta step
+    (hybrid.py:390-413 with T == 1 and history).
+
+    qkv ``[B,C]``; conv_w ``[C,4]``; conv_state ``[B,C,3]`` (returned updated, new tensor);
+    g, beta ``[B,HV]``; state ``[B,HV,d,d]`` (updated in place). Returns (o ``[B,HV,d]``,
+    new conv state)."""
+    y, new_conv = conv_silu(qkv.float().unsqueeze(1), conv_w.float(), conv_state.float())
+    q, k, v = delta_prep(y, hk, hv, d, d)
+    o = delta_rule_step(q[:, :, 0], k[:, :, 0], v[:, :, 0], g.float(), beta.float(), state)
+    return o, new_conv
+
+
+# --- gated attention (hybrid.py:265-311) ----------------------------------------------------
+
+def attn_prep(qg, k, v, q_norm_w, k_norm_w, kc, vc, pos: int, rotary_dim: int, theta: float,
+              eps: float = 1e-6):
+    """ZNorm of q (first HD of each head's ``[query | gate]``) and of k, partial RoPE at
+    positions ``pos..pos+T-1``, and the k/v append into the cache (hybrid.py:284-296).
+
+    qg ``[B,T,H,2HD]``; k, v ``[B,T,KV,HD]``; kc, vc ``[B,KV,cap,HD]`` (written in their own
+    dtype, e.g. bf16, at ``pos:pos+T``). Returns (q ``[B,H,T,HD]`` fp32, gate ``[B,T,H*HD]``)."""
+    B, T, H, HD2 = qg.shape
+    HD = HD2 // 2
+    KV = k.shape[2]
+    q, gate = qg.float().chunk(2, -1)
+    gate = gate.reshape(B, T, H * HD)
+    q = znorm(q, q_norm_w, eps).transpose(1, 2)
+    kk = znorm(k.float(), k_norm_w, eps).transpose(1, 2)
+    vv = v.float().transpose(1, 2)
+    cos, sin = rope_tables(rotary_dim, theta, torch.arange(pos, pos + T))
+    q, kk = apply_partial_rope(q, cos, sin), apply_partial_rope(kk, cos, sin)
+    kc[:, :, pos:pos + T] = kk.to(kc.dtype)
+    vc[:, :, pos:pos + T] = vv.to(vc.dtype)
+    return q, gate
+
+
+def attention_core(q, kc, vc, pos: int, n_kv: int):
+    """Causal GQA softmax attention of T queries at positions ``pos..pos+T-1`` over cache
+    rows ``[0, pos+T)`` (hybrid.py:297-309: grouped SDPA at T == 1, causal / ``tril(pos)``
+    mask otherwise). q ``[B,H,T,HD]``; kc, vc ``[B,KV,cap,HD]``. Query head h reads KV head
+    ``h // (H/KV)``. Returns ``[B,H,T,HD]`` fp32."""
+    B, H, T, HD = q.shape
+    g = H // n_kv
+    k = kc[:, :, :pos + T].float().repeat_interleave(g, 1)
+    v = vc[:, :, :pos + T].float().repeat_interleave(g, 1)
+    mask = torch.ones(T, pos + T, dtype=torch.bool).tril(pos)
+    return F.scaled_dot_product_attention(q.float(), k, v, attn_mask=mask)
+
+
+def gated_attention_out(y, gate):
+    """``y * sigmoid(gate)`` with y ``[B,H,T,HD]`` -> ``[B,T,H*HD]`` (hybrid.py:310)."""
+    B, H, T, HD = y.shape
+    return y.transpose(1, 2).reshape(B, T, H * HD) * torch.sigmoid(gate.float())
+
+
+def attention_decode(qg, k_new, v_new, q_norm_w, k_norm_w, kc, vc, pos: int, rotary_dim: int,
+                     theta: float, eps: float = 1e-6):
+    """One query token per sequence: attn_prep at ``pos`` then attention over ``pos+1`` keys
+    and the sigmoid gate (hybrid.py:280-310 with T == 1). qg ``[B,H,2HD]``; k_new, v_new
+    ``[B,KV,HD]``. Returns ``[B,H,HD]`` fp32; writes the new k/v into the caches."""
+    B, H, HD2 = qg.shape
+    KV = k_new.shape[1]
+    q, gate = attn_prep(qg.unsqueeze(1), k_new.unsqueeze(1), v_new.unsqueeze(1), q_norm_w, k_norm_w,
+                        kc, vc, pos, rotary_dim, theta, eps)
+    y = attention_core(q, kc, vc, pos, KV)
+    return gated_attention_out(y, gate).reshape(B, H, HD2 // 2)

@@ -1,0 +1,39 @@
+"""Shared test setup: the `gpu` marker, import paths and the tolerance metric.
+
+Tolerance metric (norm-wise max relative error on fp32 outputs): max|x - ref| / max|ref|.
+Bars: 1e-3 for DeltaNet outputs and state, 2e-3 for attention."""
+import os
+import sys
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parent.parent
+PKG = ROOT / "aegist-optimized-ai-library-_amd"
+for p in (str(ROOT), str(PKG)):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+DELTA_TOL = 1e-3
+ATTN_TOL = 2e-3
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an MI355X (runs the HIP kernels)")
+    config.addinivalue_line("markers", "slow: large shapes (still under a minute)")
+
+
+def rel_err(x, ref) -> float:
+    import torch
+    x = x.detach().double().cpu()
+    ref = ref.detach().double().cpu()
+    den = ref.abs().max().item()
+    return (x - ref).abs().max().item() / (den if den > 0 else 1.0)
+
+
+@pytest.fixture(scope="session")
+def dev():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    return torch.device("cuda:0")

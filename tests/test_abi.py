@@ -1,0 +1,89 @@
+"""CPU checks of the C ABI: the library loads, exports every symbol include/aegist_mixer.h
+declares, rejects bad shapes with an error code and message before touching the device, and
+hands out the same RoPE table the oracle uses. No kernel is launched here."""
+import ctypes as C
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+from conftest import ROOT
+from oracle import mixer_ref as R
+
+import aegist_mixer
+from aegist_mixer import _lib
+
+HEADER = ROOT / "include" / "aegist_mixer.h"
+
+
+def declared_symbols():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[\w]+\s*\*?\s*(aegist_\w+)\s*\(", text, re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    L = _lib.lib()
+    names = declared_symbols()
+    assert len(names) >= 25
+    missing = [n for n in names if not hasattr(L, n)]
+    assert not missing, f"not exported: {missing}"
+    # and the ctypes table covers the header exactly
+    assert sorted(_lib.SIGNATURES) == names
+
+
+def test_version_and_no_error_initially():
+    assert b"gfx950" in _lib.lib().aegist_version()
+
+
+def test_rope_table_matches_oracle_bitwise():
+    for rd, theta in [(64, 1e7), (32, 1e4), (256, 5e5)]:
+        ours = aegist_mixer.ops.rope_inv_freq(rd, theta)
+        assert torch.equal(ours, R.rope_inv_freq(rd, theta))
+
+
+def test_rope_rejects_odd_dim():
+    buf = (C.c_float * 8)()
+    rc = _lib.lib().aegist_rope_inv_freq(buf, 7, 1e4)
+    assert rc == -1 and "even" in _lib.last_error()
+
+
+@pytest.mark.parametrize("hk,hv", [(16, 24), (16, 48), (3, 5)])
+def test_decode_step_rejects_head_ratio(hk, hv):
+    rc = _lib.lib().aegist_delta_decode_step(None, 1, None, None, None, None, None, None, 0, 4, hk, hv,
+                                             0.088, 1e-6, None)
+    assert rc == -1 and "HV" in _lib.last_error()
+
+
+def test_decode_step_rejects_bad_dtype():
+    rc = _lib.lib().aegist_delta_decode_step(None, 7, None, None, None, None, None, None, 0, 4, 16, 32,
+                                             0.088, 1e-6, None)
+    assert rc == -3
+
+
+def test_attention_decode_rejects_shapes():
+    L = _lib.lib()
+    args = [None, None, None, 1, None, None, None, None, None, 0]
+    rc = L.aegist_attention_decode(*args, 1, 16, 2, 128, 64, 10, 100, 1e-6, 1e7, None, 0, None)
+    assert rc == -1 and "256" in _lib.last_error()
+    rc = L.aegist_attention_decode(*args, 1, 16, 3, 256, 64, 10, 100, 1e-6, 1e7, None, 0, None)
+    assert rc == -1
+    rc = L.aegist_attention_decode(*args, 1, 16, 2, 256, 64, 100, 100, 1e-6, 1e7, None, 0, None)
+    assert rc == -1 and "cap" in _lib.last_error()
+    rc = L.aegist_attention_decode(*args, 1, 16, 2, 256, 64, 10, 100, 1e-6, 1e7, None, 0, None)
+    assert rc == -2  # workspace missing
+
+
+def test_workspace_queries_are_host_only():
+    L = _lib.lib()
+    a = L.aegist_attention_decode_workspace_bytes(32, 16, 2, 131073)
+    b = L.aegist_attention_decode_workspace_bytes(1, 16, 2, 4097)
+    assert a > 0 and b > 0 and a % 256 == 0
+    if hasattr(L, "aegist_delta_chunked_workspace_bytes"):
+        assert L.aegist_delta_chunked_workspace_bytes(1, 8192, 32) > 0
+
+
+def test_engine_mirrors_reject_shapes():
+    L = _lib.lib()
+    assert L.aegist_delta_scan(None, None, None, None, 4, 8191, 16, 32, None) == -1
+    assert L.aegist_l2norm_heads(None, 4, 100, 16, 128, 1.0, 1e-6, None) == -1

@@ -1,0 +1,111 @@
+"""GPU parity of the gated GQA attention kernels against the CPU oracle (bar: 2e-3 norm-wise
+max relative error on fp32 outputs; the cache rows written must equal the oracle's bf16)."""
+import pytest
+import torch
+
+from conftest import ATTN_TOL, rel_err
+from oracle import mixer_ref as R
+
+from aegist_mixer import ops
+
+pytestmark = pytest.mark.gpu
+
+HD, RD, THETA = 256, 64, 1e7
+
+
+def _gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+def decode_case(B, H, KV, L, cap, seed, dtype=torch.bfloat16):
+    g_ = _gen(seed)
+    qg = torch.randn(B, H, 2 * HD, generator=g_).to(dtype)
+    kn = torch.randn(B, KV, HD, generator=g_).to(dtype)
+    vn = torch.randn(B, KV, HD, generator=g_).to(dtype)
+    qw = (torch.randn(HD, generator=g_) * 0.1).to(torch.bfloat16)
+    kw = (torch.randn(HD, generator=g_) * 0.1).to(torch.bfloat16)
+    kc = torch.randn(B, KV, cap, HD, generator=g_).to(torch.bfloat16)
+    vc = torch.randn(B, KV, cap, HD, generator=g_).to(torch.bfloat16)
+    return qg, kn, vn, qw, kw, kc, vc
+
+
+@pytest.mark.parametrize("B,H,KV,L", [(1, 16, 2, 0), (1, 16, 2, 1), (2, 16, 2, 100), (1, 16, 2, 4096),
+                                      (3, 8, 2, 777), (2, 4, 4, 300), (8, 16, 2, 4096), (1, 16, 2, 32768)])
+def test_attention_decode_matches_oracle(dev, B, H, KV, L):
+    print(f"attention_decode B={B} H={H} KV={KV} L={L}", flush=True)
+    cap = L + 5
+    qg, kn, vn, qw, kw, kc, vc = decode_case(B, H, KV, L, cap, seed=L + B)
+    kc_r, vc_r = kc.clone(), vc.clone()
+    ref = R.attention_decode(qg.float(), kn.float(), vn.float(), qw.float(), kw.float(), kc_r, vc_r, L, RD, THETA)
+    kc_d, vc_d = kc.to(dev), vc.to(dev)
+    out = ops.attention_decode(qg.to(dev), kn.to(dev), vn.to(dev), qw.to(dev), kw.to(dev), kc_d, vc_d, L, RD, THETA)
+    torch.cuda.synchronize()
+    assert rel_err(out, ref) < ATTN_TOL
+    # the appended row: k roped then rounded to bf16, v copied; allow 1 bf16 ulp on k
+    assert torch.equal(vc_d[:, :, L].cpu(), vc_r[:, :, L])
+    dk = (kc_d[:, :, L].float().cpu() - kc_r[:, :, L].float()).abs()
+    assert (dk <= kc_r[:, :, L].float().abs() * 2 ** -7 + 1e-6).all()
+
+
+@pytest.mark.slow
+@pytest.mark.parametrize("B,L", [(1, 131072), (32, 4096)])
+def test_attention_decode_long(dev, B, L):
+    print(f"attention_decode long B={B} L={L}", flush=True)
+    qg, kn, vn, qw, kw, kc, vc = decode_case(B, 16, 2, L, L + 1, seed=3)
+    kc_r, vc_r = kc.clone(), vc.clone()
+    ref = R.attention_decode(qg.float(), kn.float(), vn.float(), qw.float(), kw.float(), kc_r, vc_r, L, RD, THETA)
+    out = ops.attention_decode(qg.to(dev), kn.to(dev), vn.to(dev), qw.to(dev), kw.to(dev), kc.to(dev), vc.to(dev), L,
+                               RD, THETA)
+    torch.cuda.synchronize()
+    assert rel_err(out, ref) < ATTN_TOL
+
+
+def test_attention_decode_bf16_out(dev):
+    qg, kn, vn, qw, kw, kc, vc = decode_case(2, 16, 2, 500, 505, seed=9)
+    ref = R.attention_decode(qg.float(), kn.float(), vn.float(), qw.float(), kw.float(), kc.clone(), vc.clone(),
+                             500, RD, THETA)
+    out = ops.attention_decode(qg.to(dev), kn.to(dev), vn.to(dev), qw.to(dev), kw.to(dev), kc.to(dev), vc.to(dev), 500,
+                               RD, THETA, out_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    assert (out.float().cpu() - ref).abs().max() <= ref.abs().max() * 2 ** -8 + 1e-3 * ref.abs().max()
+
+
+@pytest.mark.parametrize("B,H,KV,T,pos", [(1, 16, 2, 2, 0), (1, 16, 2, 17, 30), (2, 8, 2, 64, 0), (1, 16, 2, 130, 5)])
+def test_attention_core_prefill(dev, B, H, KV, T, pos):
+    g_ = _gen(T)
+    q = torch.randn(B, H, T, HD, generator=g_) * 0.5
+    kc = torch.randn(B, KV, pos + T + 3, HD, generator=g_).to(torch.bfloat16)
+    vc = torch.randn(B, KV, pos + T + 3, HD, generator=g_).to(torch.bfloat16)
+    gate = torch.randn(B, T, H * HD, generator=g_)
+    ref = R.gated_attention_out(R.attention_core(q, kc, vc, pos, KV), gate).reshape(B, T, H, HD)
+    out = ops.attention_core(q.to(dev), kc.to(dev), vc.to(dev), gate.to(dev), pos)
+    torch.cuda.synchronize()
+    assert rel_err(out, ref) < ATTN_TOL
+
+
+def test_engine_attention_pipeline(dev):
+    """attn_prep -> attention_gated with engine layouts, prefill of 9 tokens then 1 decode."""
+    H, KV, cap = 16, 2, 64
+    g_ = _gen(4)
+    T = 10
+    qg = torch.randn(T, H, 2 * HD, generator=g_)
+    k = torch.randn(T, KV, HD, generator=g_)
+    v = torch.randn(T, KV, HD, generator=g_)
+    qw = (torch.randn(HD, generator=g_) * 0.1).to(torch.bfloat16)
+    kw = (torch.randn(HD, generator=g_) * 0.1).to(torch.bfloat16)
+    kc_r = torch.zeros(1, KV, cap, HD, dtype=torch.bfloat16)
+    vc_r = torch.zeros(1, KV, cap, HD, dtype=torch.bfloat16)
+    q_r, gate_r = R.attn_prep(qg.unsqueeze(0), k.unsqueeze(0), v.unsqueeze(0), qw.float(), kw.float(), kc_r, vc_r, 0,
+                              RD, THETA)
+    ref = R.gated_attention_out(R.attention_core(q_r, kc_r, vc_r, 0, KV), gate_r).reshape(T, H, HD)
+    kc = torch.zeros(KV, cap, HD, dtype=torch.bfloat16, device=dev)
+    vc = torch.zeros(KV, cap, HD, dtype=torch.bfloat16, device=dev)
+    outs = []
+    for a, b_ in [(0, 9), (9, 10)]:
+        qgd = qg[a:b_].contiguous().to(dev)
+        qn = ops.engine_attn_prep(qgd, k[a:b_].contiguous().to(dev), v[a:b_].contiguous().to(dev), qw.to(dev),
+                                  kw.to(dev), kc, vc, a, RD, THETA)
+        assert rel_err(qn, q_r[0, :, a:b_].transpose(0, 1)) < 1e-5
+        outs.append(ops.engine_attention_gated(qn, kc, vc, qgd, a))
+    torch.cuda.synchronize()
+    assert rel_err(torch.cat(outs, 0), ref) < ATTN_TOL

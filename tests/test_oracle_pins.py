@@ -1,0 +1,247 @@
+"""Pins for the CPU oracle (oracle/mixer_ref.py), independent of its own formulas.
+
+The reference ships no golden vectors for the mixer ops (its only parity test is the
+end-to-end logits test tests/test_hybrid_rust.py, which needs the 21 GB brain and CUDA), so
+each oracle function is pinned here by fp64 brute force, closed-form special cases,
+equivalences between the recurrent and chunked forms, and algebraic identities, chosen so a
+dropped term, a wrong sign or index, or a transposed operand fails at least one of them."""
+import math
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from conftest import rel_err
+from oracle import mixer_ref as R
+
+torch.manual_seed(0)
+
+
+def _unit(x):
+    return x / x.norm(dim=-1, keepdim=True)
+
+
+def _delta_inputs(B=2, H=3, T=7, d=8, dtype=torch.float64, seed=0):
+    g_ = torch.Generator().manual_seed(seed)
+    q = _unit(torch.randn(B, H, T, d, generator=g_, dtype=dtype)) * d ** -0.5
+    k = _unit(torch.randn(B, H, T, d, generator=g_, dtype=dtype))
+    v = torch.randn(B, H, T, d, generator=g_, dtype=dtype)
+    beta = torch.sigmoid(torch.randn(B, H, T, generator=g_, dtype=dtype))
+    g = -F.softplus(torch.randn(B, H, T, generator=g_, dtype=dtype))
+    return q, k, v, g, beta
+
+
+def _brute_delta(q, k, v, g, beta, S0=None):
+    """Scalar loops in fp64: the gated delta rule written element by element."""
+    B, H, T, dk = q.shape
+    dv = v.shape[-1]
+    S = torch.zeros(B, H, dk, dv, dtype=torch.float64) if S0 is None else S0.double().clone()
+    o = torch.zeros(B, H, T, dv, dtype=torch.float64)
+    for b in range(B):
+        for h in range(H):
+            for t in range(T):
+                a = math.exp(g[b, h, t].item())
+                for i in range(dk):
+                    for j in range(dv):
+                        S[b, h, i, j] *= a
+                for j in range(dv):
+                    kv = sum(S[b, h, i, j].item() * k[b, h, t, i].item() for i in range(dk))
+                    dl = (v[b, h, t, j].item() - kv) * beta[b, h, t].item()
+                    for i in range(dk):
+                        S[b, h, i, j] += k[b, h, t, i].item() * dl
+                for j in range(dv):
+                    o[b, h, t, j] = sum(S[b, h, i, j].item() * q[b, h, t, i].item() for i in range(dk))
+    return o, S
+
+
+def test_delta_step_matches_brute_force():
+    q, k, v, g, beta = _delta_inputs(B=1, H=2, T=5, d=6)
+    S0 = torch.randn(1, 2, 6, 6, dtype=torch.float64) * 0.1
+    o, S = R.delta_rule_recurrent(q, k, v, g, beta, S0)
+    ob, Sb = _brute_delta(q, k, v, g, beta, S0)
+    assert rel_err(o, ob) < 1e-12 and rel_err(S, Sb) < 1e-12
+
+
+def test_delta_step_special_cases():
+    d = 8
+    S0 = torch.randn(1, 1, d, d, dtype=torch.float64)
+    q = torch.randn(1, 1, d, dtype=torch.float64)
+    k = _unit(torch.randn(1, 1, d, dtype=torch.float64))
+    v = torch.randn(1, 1, d, dtype=torch.float64)
+    # beta = 0: the state only decays, o = (e^g S)^T q
+    g = torch.tensor([[-0.7]], dtype=torch.float64)
+    S = S0.clone()
+    o = R.delta_rule_step(q, k, v, g, torch.zeros(1, 1, dtype=torch.float64), S)
+    assert torch.allclose(S, S0 * math.exp(-0.7))
+    assert torch.allclose(o[0, 0], (S0[0, 0] * math.exp(-0.7)).t() @ q[0, 0])
+    # g = 0, beta = 1, k = e_i: row i of S becomes v, other rows unchanged
+    i = 3
+    e = torch.zeros(1, 1, d, dtype=torch.float64)
+    e[0, 0, i] = 1
+    S = S0.clone()
+    R.delta_rule_step(q, e, v, torch.zeros(1, 1, dtype=torch.float64), torch.ones(1, 1, dtype=torch.float64), S)
+    expect = S0.clone()
+    expect[0, 0, i] = v[0, 0]
+    assert torch.allclose(S, expect)
+    # S0 = 0, one token: o = (q . k) beta v
+    S = torch.zeros(1, 1, d, d, dtype=torch.float64)
+    bt = torch.tensor([[0.37]], dtype=torch.float64)
+    o = R.delta_rule_step(q, k, v, g, bt, S)
+    assert torch.allclose(o[0, 0], (q[0, 0] @ k[0, 0]) * 0.37 * v[0, 0])
+
+
+@pytest.mark.parametrize("T", [1, 5, 63, 64, 100, 130])
+@pytest.mark.parametrize("with_state", [False, True])
+def test_chunked_equals_recurrent(T, with_state):
+    q, k, v, g, beta = _delta_inputs(B=2, H=2, T=T, d=16, seed=T)
+    S0 = torch.randn(2, 2, 16, 16, dtype=torch.float64) * 0.05 if with_state else None
+    o1, S1 = R.delta_rule_recurrent(q, k, v, g, beta, S0)
+    o2, S2 = R.delta_rule_chunked(q, k, v, g, beta, S0, chunk=64)
+    assert rel_err(o2, o1) < 1e-10 and rel_err(S2, S1) < 1e-10
+
+
+def test_chunked_chunk_size_invariance():
+    q, k, v, g, beta = _delta_inputs(B=1, H=2, T=96, d=16, seed=3)
+    o1, S1 = R.delta_rule_chunked(q, k, v, g, beta, None, chunk=16)
+    o2, S2 = R.delta_rule_chunked(q, k, v, g, beta, None, chunk=64)
+    assert rel_err(o1, o2) < 1e-10 and rel_err(S1, S2) < 1e-10
+
+
+def test_chunked_fp32_vs_fp64_at_scale():
+    """The fp32 oracle itself stays far inside the 1e-3 bar at d = 128, T = 512."""
+    q, k, v, g, beta = _delta_inputs(B=1, H=2, T=512, d=128, seed=5)
+    o64, S64 = R.delta_rule_chunked(q, k, v, g, beta)
+    o32, S32 = R.delta_rule_chunked(*(t.float() for t in (q, k, v, g, beta)))
+    assert rel_err(o32, o64) < 1e-5 and rel_err(S32, S64) < 1e-5
+
+
+def test_conv_silu_brute_force_and_streaming():
+    B, T, C, K = 2, 9, 5, 4
+    x = torch.randn(B, T, C, dtype=torch.float64)
+    w = torch.randn(C, K, dtype=torch.float64)
+    st = torch.randn(B, C, K - 1, dtype=torch.float64)
+    y, ns = R.conv_silu(x, w, st)
+    full = torch.cat([st.transpose(1, 2), x], 1)  # [B, K-1+T, C], oldest first
+    yb = torch.zeros_like(x)
+    for b in range(B):
+        for t in range(T):
+            for c in range(C):
+                acc = sum(w[c, j].item() * full[b, t + j, c].item() for j in range(K))
+                yb[b, t, c] = acc / (1 + math.exp(-acc))
+    assert rel_err(y, yb) < 1e-12
+    assert torch.equal(ns, full[:, -(K - 1):].transpose(1, 2))
+    # feeding one token at a time gives the same outputs and state
+    s = st.clone()
+    ys = []
+    for t in range(T):
+        yt, s = R.conv_silu(x[:, t:t + 1], w, s)
+        ys.append(yt)
+    assert rel_err(torch.cat(ys, 1), y) < 1e-12 and torch.equal(s, ns)
+
+
+def test_norms_closed_form():
+    x = torch.randn(3, 16, dtype=torch.float64)
+    w = torch.randn(16, dtype=torch.float64) * 0.1
+    rms = (x.pow(2).mean(-1, keepdim=True) + 1e-6).sqrt()
+    # znorm / gated_norm compute in fp32 by definition (hybrid.py:127, 143): fp32-level bar
+    assert rel_err(R.znorm(x, w), x / rms * (1 + w)) < 1e-6
+    z = torch.randn(3, 16, dtype=torch.float64)
+    wg = torch.randn(16, dtype=torch.float64)
+    assert rel_err(R.gated_norm(x, z, wg), wg * x / rms * z * torch.sigmoid(z)) < 1e-6
+    assert rel_err(R.gated_norm(x, z, wg, act="sigmoid"), wg * x / rms * torch.sigmoid(z)) < 1e-6
+    l2 = R.l2norm(x)
+    assert rel_err(l2.norm(dim=-1), torch.ones(3, dtype=torch.float64)) < 1e-6
+
+
+def test_delta_gates_closed_form():
+    h = torch.randn(4, 32, dtype=torch.float64)
+    wb, wa = torch.randn(3, 32, dtype=torch.float64), torch.randn(3, 32, dtype=torch.float64)
+    a_log, dt = torch.randn(3, dtype=torch.float64), torch.randn(3, dtype=torch.float64)
+    g, beta = R.delta_gates(h, wb, wa, a_log, dt)
+    for t in range(4):
+        for j in range(3):
+            b_ = 1 / (1 + math.exp(-(h[t] @ wb[j]).item()))
+            xx = (h[t] @ wa[j]).item() + dt[j].item()
+            sp = xx if xx > 20 else math.log1p(math.exp(xx))
+            # computed in fp32 by definition (hybrid.py:403-404 take .float())
+            assert abs(beta[t, j].item() - b_) < 1e-6
+            assert abs(g[t, j].item() + math.exp(a_log[j].item()) * sp) < 1e-5 * (1 + abs(sp))
+
+
+def test_delta_prep_head_mapping():
+    hk, hv, d = 2, 4, 8
+    y = torch.randn(1, 1, 2 * hk * d + hv * d, dtype=torch.float64)
+    q, k, v = R.delta_prep(y, hk, hv, d, d)
+    for h in range(hv):
+        kh = h // (hv // hk)
+        qraw = y[0, 0, kh * d:(kh + 1) * d]
+        kraw = y[0, 0, hk * d + kh * d: hk * d + (kh + 1) * d]
+        # heads are cast to fp32 before the norm (hybrid.py:408): fp32-level bar
+        assert rel_err(q[0, h, 0], qraw / (qraw.pow(2).sum() + 1e-6).sqrt() / math.sqrt(d)) < 1e-6
+        assert rel_err(k[0, h, 0], kraw / (kraw.pow(2).sum() + 1e-6).sqrt()) < 1e-6
+        assert torch.equal(v[0, h, 0], y[0, 0, 2 * hk * d + h * d: 2 * hk * d + (h + 1) * d].float())
+
+
+def test_rope_identities():
+    rd, theta = 64, 1e7
+    inv = R.rope_inv_freq(rd, theta)
+    assert inv[0].item() == 1.0
+    # against the closed form evaluated in fp64
+    for j in range(rd // 2):
+        assert abs(inv[j].item() - theta ** (-2 * j / rd)) <= 1e-7 * theta ** (-2 * j / rd)
+    x = torch.randn(5, 256, dtype=torch.float64)
+    c0, s0 = R.rope_tables(rd, theta, torch.tensor([0]))
+    assert torch.equal(R.apply_partial_rope(x, c0.double(), s0.double()), x)  # position 0 = identity
+    pos = torch.tensor([7, 1000, 131072])
+    c, s = R.rope_tables(rd, theta, pos)
+    for p_i in range(3):
+        y = R.apply_partial_rope(x[:1], c[p_i:p_i + 1].double(), s[p_i:p_i + 1].double())
+        # pairs (j, j + rd/2) rotate by angle pos * inv_j; the rest pass through
+        for j in (0, 5, 31):
+            ang = float(pos[p_i]) * float(inv[j])
+            a, b = x[0, j].item(), x[0, j + rd // 2].item()
+            assert abs(y[0, j].item() - (a * math.cos(ang) - b * math.sin(ang))) < 1e-4
+            assert abs(y[0, j + rd // 2].item() - (b * math.cos(ang) + a * math.sin(ang))) < 1e-4
+        assert torch.equal(y[0, rd:], x[0, rd:])
+        assert abs(y[0, :rd].norm().item() - x[0, :rd].norm().item()) < 1e-5
+
+
+def _brute_attention(q, k, v, pos, G):
+    """fp64 loops: softmax(q k^T / sqrt(HD)) v with causal offset and GQA h // G."""
+    B, H, T, HD = q.shape
+    out = torch.zeros(B, H, T, HD, dtype=torch.float64)
+    for b in range(B):
+        for h in range(H):
+            for t in range(T):
+                L = pos + t + 1
+                s = [(q[b, h, t] @ k[b, h // G, l]).item() / math.sqrt(HD) for l in range(L)]
+                m = max(s)
+                p = [math.exp(x - m) for x in s]
+                Z = sum(p)
+                out[b, h, t] = sum(p[l] / Z * v[b, h // G, l] for l in range(L))
+    return out
+
+
+@pytest.mark.parametrize("T,pos", [(1, 0), (1, 9), (3, 0), (4, 5)])
+def test_attention_core_brute_force(T, pos):
+    B, H, KV, HD = 2, 4, 2, 16
+    q = torch.randn(B, H, T, HD, dtype=torch.float64)
+    kc = torch.randn(B, KV, pos + T + 3, HD, dtype=torch.float64)
+    vc = torch.randn(B, KV, pos + T + 3, HD, dtype=torch.float64)
+    y = R.attention_core(q, kc, vc, pos, KV)
+    yb = _brute_attention(q, kc, vc, pos, H // KV)
+    assert rel_err(y, yb) < 1e-6  # the oracle runs SDPA in fp32, as hybrid.py:300-309
+
+
+def test_attention_single_key_is_gated_value():
+    B, H, KV, HD = 1, 4, 2, 8
+    qg = torch.randn(B, 1, H, 2 * HD, dtype=torch.float64)
+    k = torch.randn(B, 1, KV, HD, dtype=torch.float64)
+    v = torch.randn(B, 1, KV, HD, dtype=torch.float64)
+    kc = torch.zeros(B, KV, 4, HD, dtype=torch.float64)
+    vc = torch.zeros(B, KV, 4, HD, dtype=torch.float64)
+    w = torch.zeros(HD, dtype=torch.float64)
+    y = R.attention_decode(qg[:, 0], k[:, 0], v[:, 0], w, w, kc, vc, 0, 4, 1e7)
+    gate = qg[:, 0, :, HD:]
+    for h in range(H):
+        assert rel_err(y[0, h], v[0, 0, h // 2] * torch.sigmoid(gate[0, h])) < 1e-6
