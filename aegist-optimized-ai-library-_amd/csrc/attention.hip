@@ -29,7 +29,6 @@ struct RopeTable;
 int launch_attn_prep(const void* qg, const void* k, const void* v, int in_dtype, const uint16_t* qw,
                      const uint16_t* kw, float* qn, uint16_t* kc, uint16_t* vc, int B, int T, int H, int KV, int HD,
                      int RD, int pos0, int cap, float eps, float theta, hipStream_t stream);
-void* mirror_workspace(size_t bytes, int* rc);
 }  // namespace aegist
 
 namespace {

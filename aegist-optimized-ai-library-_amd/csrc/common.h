@@ -86,6 +86,8 @@ void set_error(const std::string& msg);
 int fail(int code, const std::string& msg);
 int check_hip(hipError_t e, const char* what);
 int after_launch(const char* what);  // launch error check; honours AEGIST_SYNC_LAUNCH
+// Library-owned per-device workspace for the engine-ABI mirrors (grown on demand).
+void* mirror_workspace(size_t bytes, int* rc);
 }  // namespace aegist
 
 #define AEG_REQUIRE(cond, msg)                                              \

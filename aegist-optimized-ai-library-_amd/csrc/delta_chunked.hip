@@ -1,0 +1,455 @@
+// Chunked (C = 64) WY-form prefill of the gated delta rule on gfx950 MFMA.
+//
+// Per chunk with cum = cumsum(g) and the L2-normalised rows q_n, k_n (hybrid.py:327-361):
+//   A     = strict_lower( beta_i e^{cum_i - cum_j} k_n,i . k_n,j )
+//   u     = (I + A)^-1 (beta v),   w = (I + A)^-1 (beta e^{cum} k_n)
+//   intra = lower_incl( e^{cum_i - cum_j} q_n,i . k_n,j )
+//   v_new = u - w S;  o = e^{cum} (q_n S) + intra v_new;  S = e^{cum_last} S + k_n^T (e^{cum_last - cum} v_new)
+//
+// Two kernels per segment of up to SEG tokens (the workspace holds one segment, so it stays
+// resident in L2 / MALL between the two launches):
+//  K1 delta_chunk_intra: one workgroup per (sequence, value head, chunk), fully parallel.
+//     Normalises q, k in fp32 and keeps them as fp16 in LDS; k_n k_n^T and q_n k_n^T on
+//     v_mfma_f32_16x16x32_f16 (lower-triangular blocks only); decay and beta applied in fp32 on
+//     the accumulators; the unit-lower-triangular solve runs in fp32 with one thread per
+//     right-hand-side column (256 columns = beta v | beta e^cum k_n), the matrix broadcast
+//     from LDS. Writes u (fp32), w (fp16), intra (fp16), cum, and - once per QK head - q_n
+//     and k_n^T (fp16).
+//  K2 delta_chunk_state: one workgroup per (sequence, value head, 32-column slice of S); the
+//     columns of S are independent, so 4 slices per head run in parallel. S lives in MFMA
+//     accumulator registers (fp32) for the whole segment; each chunk it is copied to LDS as
+//     fp16 (transposed, so the B operand is a 16-byte read), then w S and q_n S, intra v_new,
+//     and the rank-64 state update k_n^T v' run on MFMA.
+// Operands are fp16 (11-bit mantissa) rather than bf16: the per-row normalisation and every
+// decay / beta factor are applied in fp32 outside the products, and fp16 keeps the chunked
+// result within 5e-4 of fp64 at T = 8192, where bf16 operands give 4e-3 (over the 1e-3 bar).
+#include "common.h"
+
+#include <algorithm>
+
+using namespace aegist;
+
+namespace {
+
+constexpr int D = 128;
+constexpr int CH = 64;       // chunk length
+constexpr int SEG = 2048;    // tokens per segment (workspace granularity)
+constexpr int NSL = 4;       // 32-column slices of S per value head in K2
+constexpr int QK_LD = D + 8; // fp16 row stride (elements) of the q/k tiles in LDS
+constexpr int A_LD = 68;     // fp32 row stride of the A matrix in LDS (16-byte aligned rows)
+
+typedef _Float16 half_t;
+
+struct SeqLayout {
+    long long sb_qk, st_qk, sh_qk, sb_v, st_v, sh_v, sb_o, st_o, sh_o;
+    long long sb_g, st_g;  // g / beta strides by sequence and token; value head contiguous
+};
+
+// Workspace of one segment. Per (b, hv, chunk): u fp32 [64][128], w fp16 [64][128],
+// intra fp16 [64][64], cum fp32 [64]. Per (b, kh, chunk): qn fp16 [64][128], knT fp16 [128][64].
+// Plus the carried state [B, HV, 128, 128] fp32 when the caller passes none.
+struct WsLayout {
+    size_t u, w, intra, cum, qn, knt, state, total;
+};
+
+__host__ __device__ inline size_t al256(size_t x) { return (x + 255) / 256 * 256; }
+
+__host__ __device__ inline WsLayout ws_layout(int B, int HK, int HV, int nch) {
+    WsLayout L;
+    size_t units_v = (size_t)B * HV * nch, units_k = (size_t)B * HK * nch;
+    size_t off = 0;
+    L.u = off; off += al256(units_v * CH * D * 4);
+    L.w = off; off += al256(units_v * CH * D * 2);
+    L.intra = off; off += al256(units_v * CH * CH * 2);
+    L.cum = off; off += al256(units_v * CH * 4);
+    L.qn = off; off += al256(units_k * CH * D * 2);
+    L.knt = off; off += al256(units_k * CH * D * 2);
+    L.state = off; off += al256((size_t)B * HV * D * D * 4);
+    L.total = off;
+    return L;
+}
+
+__device__ __forceinline__ half8 ld_h8(const half_t* p) { return *(const half8*)p; }
+
+__device__ __forceinline__ f32x4 mfma16(half8 a, half8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// ---------------------------------------------------------------------------------------------
+// K1: intra-chunk work. grid (nch, HV, B), 256 threads.
+template <typename Tin>
+__global__ void __launch_bounds__(256) delta_chunk_intra(const Tin* __restrict__ q, const Tin* __restrict__ k,
+                                                         const Tin* __restrict__ v, const float* __restrict__ g,
+                                                         const float* __restrict__ beta, SeqLayout a, int t0, int T,
+                                                         int HK, int HV, int normalize, float qscale, float eps,
+                                                         unsigned char* __restrict__ ws, WsLayout L) {
+    __shared__ __attribute__((aligned(16))) half_t Qs[CH][QK_LD];
+    __shared__ __attribute__((aligned(16))) half_t Ks[CH][QK_LD];
+    __shared__ __attribute__((aligned(16))) float As[CH][A_LD];
+    __shared__ float cum_s[CH], beta_s[CH], rk_s[CH], g_s[CH];
+
+    const int c = blockIdx.x, hv = blockIdx.y, b = blockIdx.z, nch = gridDim.x;
+    const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
+    const int R = HV / HK, kh = hv / R;
+    const bool writes_qk = (hv % R) == 0;
+    const int tok0 = t0 + c * CH;
+
+    // ---- 1. load q, k rows; row norms; fp16 normalised tiles
+    {
+        const int row = tid / 4, qq = tid % 4, tok = tok0 + row;
+        const bool valid = tok < T;
+        const Tin* qp = q + b * a.sb_qk + (long long)tok * a.st_qk + kh * a.sh_qk + qq * 32;
+        const Tin* kp = k + b * a.sb_qk + (long long)tok * a.st_qk + kh * a.sh_qk + qq * 32;
+        float xq[32], xk[32], ssq = 0.f, ssk = 0.f;
+#pragma unroll
+        for (int e = 0; e < 32; e++) {
+            xq[e] = valid ? Act<Tin>::ld(qp, e) : 0.f;
+            xk[e] = valid ? Act<Tin>::ld(kp, e) : 0.f;
+            ssq += xq[e] * xq[e];
+            ssk += xk[e] * xk[e];
+        }
+        ssq += __shfl_xor(ssq, 1, WAVE);
+        ssq += __shfl_xor(ssq, 2, WAVE);
+        ssk += __shfl_xor(ssk, 1, WAVE);
+        ssk += __shfl_xor(ssk, 2, WAVE);
+        const float rq = normalize ? rsqrtf(ssq + eps) : 1.f, sc = normalize ? qscale : 1.f;
+        const float rk = normalize ? rsqrtf(ssk + eps) : 1.f;
+#pragma unroll
+        for (int e = 0; e < 32; e++) {
+            Qs[row][qq * 32 + e] = (half_t)((xq[e] * rq) * sc);
+            Ks[row][qq * 32 + e] = (half_t)(xk[e] * rk);
+        }
+        if (qq == 0) {
+            rk_s[row] = rk;
+            beta_s[row] = valid ? beta[b * a.sb_g + (long long)tok * a.st_g + hv] : 0.f;
+            g_s[row] = valid ? g[b * a.sb_g + (long long)tok * a.st_g + hv] : 0.f;
+        }
+    }
+    __syncthreads();
+    // ---- 2. cum = inclusive prefix sum of g (wave 0); q_n / k_n^T copies for K2
+    if (wave == 0) {
+        float x = g_s[lane];
+#pragma unroll
+        for (int d = 1; d < WAVE; d <<= 1) {
+            float y = __shfl_up(x, d, WAVE);
+            if (lane >= d) x += y;
+        }
+        cum_s[lane] = x;
+        ((float*)(ws + L.cum))[((size_t)(b * HV + hv) * nch + c) * CH + lane] = x;
+    }
+    if (writes_qk) {
+        const size_t ku = ((size_t)(b * HK + kh) * nch + c);
+        half_t* qn = (half_t*)(ws + L.qn) + ku * CH * D;
+        half_t* knt = (half_t*)(ws + L.knt) + ku * CH * D;
+        {   // q_n rows: thread = (row, 32-element quarter)
+            const int row = tid / 4, qq = tid % 4;
+            const half8* src = (const half8*)&Qs[row][qq * 32];
+            half8* dst = (half8*)(qn + row * D + qq * 32);
+#pragma unroll
+            for (int e = 0; e < 4; e++) dst[e] = src[e];
+        }
+        {   // k_n^T: thread = (dk, 32-row half)
+            const int dk = tid / 2, hh = tid % 2;
+            half8 buf[4];
+#pragma unroll
+            for (int e = 0; e < 32; e++) buf[e / 8][e % 8] = Ks[hh * 32 + e][dk];
+            half8* dst = (half8*)(knt + dk * CH + hh * 32);
+#pragma unroll
+            for (int e = 0; e < 4; e++) dst[e] = buf[e];
+        }
+    }
+    __syncthreads();
+
+    // ---- 3. k_n k_n^T and q_n k_n^T on MFMA: wave = 16-row block rb, column blocks cb <= rb
+    {
+        const int rb = wave, n = lane % 16, gq = lane / 16;
+        half_t* intra = (half_t*)(ws + L.intra) + ((size_t)(b * HV + hv) * nch + c) * CH * CH;
+        half8 ak[4], aq[4];
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) {
+            ak[ks] = ld_h8(&Ks[16 * rb + n][32 * ks + 8 * gq]);
+            aq[ks] = ld_h8(&Qs[16 * rb + n][32 * ks + 8 * gq]);
+        }
+        for (int cb = 0; cb < 4; cb++) {
+            const int jj = 16 * cb + n;
+            if (cb > rb) {
+#pragma unroll
+                for (int j = 0; j < 4; j++) intra[(16 * rb + 4 * gq + j) * CH + jj] = (half_t)0.f;
+                continue;
+            }
+            f32x4 accA = {0.f, 0.f, 0.f, 0.f}, accQ = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < 4; ks++) {
+                half8 bk = ld_h8(&Ks[jj][32 * ks + 8 * gq]);
+                accA = mfma16(ak[ks], bk, accA);
+                accQ = mfma16(aq[ks], bk, accQ);
+            }
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int i = 16 * rb + 4 * gq + j;
+                const float dec = __expf(cum_s[i] - cum_s[jj]);
+                As[i][jj] = jj < i ? beta_s[i] * (dec * accA[j]) : 0.f;
+                intra[i * CH + jj] = (half_t)(jj <= i ? dec * accQ[j] : 0.f);
+            }
+        }
+    }
+    __syncthreads();
+
+    // ---- 4. forward substitution, one thread per right-hand-side column
+    {
+        const int col = tid;
+        const bool isv = col < D;
+        const int cc = isv ? col : col - D;
+        float x[CH];
+#pragma unroll
+        for (int i = 0; i < CH; i++) {
+            const int tok = tok0 + i;
+            float r = 0.f;
+            if (tok < T) {
+                if (isv) r = beta_s[i] * Act<Tin>::ld(v, b * a.sb_v + (long long)tok * a.st_v + hv * a.sh_v + cc);
+                else
+                    r = beta_s[i] * __expf(cum_s[i]) *
+                        (Act<Tin>::ld(k, b * a.sb_qk + (long long)tok * a.st_qk + kh * a.sh_qk + cc) * rk_s[i]);
+            }
+            x[i] = r;
+        }
+#pragma unroll
+        for (int i = 1; i < CH; i++) {
+            float s = x[i];
+#pragma unroll
+            for (int kk = 0; kk < (i & ~3); kk += 4) {
+                const float4 a4 = *(const float4*)&As[i][kk];
+                s -= a4.x * x[kk] + a4.y * x[kk + 1] + a4.z * x[kk + 2] + a4.w * x[kk + 3];
+            }
+#pragma unroll
+            for (int kk = (i & ~3); kk < i; kk++) s -= As[i][kk] * x[kk];
+            x[i] = s;
+        }
+        const size_t vu = (size_t)(b * HV + hv) * nch + c;
+        if (isv) {
+            float* u = (float*)(ws + L.u) + vu * CH * D;
+#pragma unroll
+            for (int i = 0; i < CH; i++) u[i * D + cc] = x[i];
+        } else {
+            half_t* w = (half_t*)(ws + L.w) + vu * CH * D;
+#pragma unroll
+            for (int i = 0; i < CH; i++) w[i * D + cc] = (half_t)x[i];
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
+// K2: sequential recurrence over the chunks of a segment. grid (NSL, HV, B), 256 threads.
+// Wave w holds S rows [32w, 32w+32) x the slice's 32 columns as 2x2 MFMA tiles.
+template <typename Tout>
+__global__ void __launch_bounds__(256) delta_chunk_state(const unsigned char* __restrict__ ws, WsLayout L,
+                                                         float* __restrict__ state, int load_state, Tout* __restrict__ out,
+                                                         SeqLayout a, int t0, int T, int nch, int HK, int HV) {
+    __shared__ __attribute__((aligned(16))) half_t SsT[32][D + 8];   // S^T (fp16): [column][dk]
+    __shared__ __attribute__((aligned(16))) half_t VnT[32][CH + 8];  // v_new^T (fp16)
+    __shared__ __attribute__((aligned(16))) half_t VdT[32][CH + 8];  // (e^{cum_last-cum} v_new)^T
+
+    const int sl = blockIdx.x, hv = blockIdx.y, b = blockIdx.z;
+    const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE, n = lane % 16, gq = lane / 16;
+    const int R = HV / HK, kh = hv / R;
+    const int col0 = sl * 32;
+    float* Sg = state + (size_t)(b * HV + hv) * D * D;
+
+    f32x4 S[2][2];
+#pragma unroll
+    for (int rt = 0; rt < 2; rt++)
+#pragma unroll
+        for (int ct = 0; ct < 2; ct++)
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                S[rt][ct][j] = load_state ? Sg[(size_t)(32 * wave + 16 * rt + 4 * gq + j) * D + col0 + 16 * ct + n] : 0.f;
+
+    const size_t vbase = (size_t)(b * HV + hv) * nch, kbase = (size_t)(b * HK + kh) * nch;
+    for (int c = 0; c < nch; c++) {
+        const size_t vu = vbase + c, ku = kbase + c;
+        const half_t* Wc = (const half_t*)(ws + L.w) + vu * CH * D;
+        const half_t* Qc = (const half_t*)(ws + L.qn) + ku * CH * D;
+        const float* Uc = (const float*)(ws + L.u) + vu * CH * D;
+        const half_t* Ic = (const half_t*)(ws + L.intra) + vu * CH * CH;
+        const half_t* KTc = (const half_t*)(ws + L.knt) + ku * CH * D;
+        const float* cumc = (const float*)(ws + L.cum) + vu * CH;
+
+        // operands that do not depend on S: issue their loads first
+        half8 wa[4], qa[4], ia[2], ka[2][2];
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) {
+            wa[ks] = ld_h8(Wc + (16 * wave + n) * D + 32 * ks + 8 * gq);
+            qa[ks] = ld_h8(Qc + (16 * wave + n) * D + 32 * ks + 8 * gq);
+        }
+#pragma unroll
+        for (int ks = 0; ks < 2; ks++) ia[ks] = ld_h8(Ic + (16 * wave + n) * CH + 32 * ks + 8 * gq);
+#pragma unroll
+        for (int rt = 0; rt < 2; rt++)
+#pragma unroll
+            for (int ks = 0; ks < 2; ks++) ka[rt][ks] = ld_h8(KTc + (32 * wave + 16 * rt + n) * CH + 32 * ks + 8 * gq);
+        f32x4 uu[2];
+        float cum_i[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int i = 16 * wave + 4 * gq + j;
+            cum_i[j] = cumc[i];
+#pragma unroll
+            for (int ct = 0; ct < 2; ct++) uu[ct][j] = Uc[i * D + col0 + 16 * ct + n];
+        }
+        const float cum_last = cumc[CH - 1];
+
+        // (1) S -> LDS as fp16, transposed
+#pragma unroll
+        for (int rt = 0; rt < 2; rt++)
+#pragma unroll
+            for (int ct = 0; ct < 2; ct++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) SsT[16 * ct + n][32 * wave + 16 * rt + 4 * gq + j] = (half_t)S[rt][ct][j];
+        __syncthreads();
+
+        // (2) w S and q_n S for chunk rows [16 wave, 16 wave + 16)
+        f32x4 WS[2], QS[2];
+#pragma unroll
+        for (int ct = 0; ct < 2; ct++) {
+            WS[ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+            QS[ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < 4; ks++) {
+                half8 sb = ld_h8(&SsT[16 * ct + n][32 * ks + 8 * gq]);
+                WS[ct] = mfma16(wa[ks], sb, WS[ct]);
+                QS[ct] = mfma16(qa[ks], sb, QS[ct]);
+            }
+        }
+        // (3) v_new = u - w S; decayed copy for the state update
+#pragma unroll
+        for (int ct = 0; ct < 2; ct++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int i = 16 * wave + 4 * gq + j;
+                const float vn = uu[ct][j] - WS[ct][j];
+                VnT[16 * ct + n][i] = (half_t)vn;
+                VdT[16 * ct + n][i] = (half_t)(__expf(cum_last - cum_i[j]) * vn);
+            }
+        __syncthreads();
+
+        // (4) o = e^{cum} q_n S + intra v_new
+#pragma unroll
+        for (int ct = 0; ct < 2; ct++) {
+            f32x4 o = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < 2; ks++) o = mfma16(ia[ks], ld_h8(&VnT[16 * ct + n][32 * ks + 8 * gq]), o);
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int i = 16 * wave + 4 * gq + j, tok = t0 + c * CH + i;
+                if (tok < T) {
+                    const float y = __expf(cum_i[j]) * QS[ct][j] + o[j];
+                    Act<Tout>::st(out, b * a.sb_o + (long long)tok * a.st_o + hv * a.sh_o + col0 + 16 * ct + n, y);
+                }
+            }
+        }
+        // (5) S = e^{cum_last} S + k_n^T v'
+        const float gamma = __expf(cum_last);
+#pragma unroll
+        for (int rt = 0; rt < 2; rt++)
+#pragma unroll
+            for (int ct = 0; ct < 2; ct++) {
+                f32x4 acc = S[rt][ct] * gamma;
+#pragma unroll
+                for (int ks = 0; ks < 2; ks++) acc = mfma16(ka[rt][ks], ld_h8(&VdT[16 * ct + n][32 * ks + 8 * gq]), acc);
+                S[rt][ct] = acc;
+            }
+        __syncthreads();  // SsT / VnT / VdT are rewritten by the next chunk
+    }
+#pragma unroll
+    for (int rt = 0; rt < 2; rt++)
+#pragma unroll
+        for (int ct = 0; ct < 2; ct++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) Sg[(size_t)(32 * wave + 16 * rt + 4 * gq + j) * D + col0 + 16 * ct + n] = S[rt][ct][j];
+}
+
+int seg_chunks(int T) { return (std::min(T, SEG) + CH - 1) / CH; }
+
+}  // namespace
+
+namespace aegist {
+
+size_t delta_chunked_ws_bytes(int B, int T, int HK, int HV) {
+    if (B <= 0 || T <= 0 || HK <= 0 || HV <= 0) return 256;
+    return ws_layout(B, HK, HV, seg_chunks(T)).total;
+}
+
+template <typename Tin, typename Tout>
+int run_chunked(const Tin* q, const Tin* k, const Tin* v, const float* g, const float* beta, float* state, Tout* out,
+                const SeqLayout& a, int B, int T, int HK, int HV, int normalize, float qscale, float eps, void* ws,
+                size_t ws_bytes, hipStream_t st) {
+    const int nch_seg = seg_chunks(T);
+    WsLayout L = ws_layout(B, HK, HV, nch_seg);
+    if (!ws || ws_bytes < L.total) return fail(AEGIST_ERR_WORKSPACE, "delta_chunked: workspace too small");
+    unsigned char* w = (unsigned char*)ws;
+    // the carried state: the caller's, or the workspace copy (starts at zero: K2 does not load it)
+    float* S = state ? state : (float*)(w + L.state);
+    int load = state ? 1 : 0;
+    for (int t0 = 0; t0 < T; t0 += SEG) {
+        const int len = std::min(SEG, T - t0);
+        const int nch = (len + CH - 1) / CH;
+        WsLayout Ls = ws_layout(B, HK, HV, nch);
+        Ls.state = L.state;
+        delta_chunk_intra<Tin><<<dim3(nch, HV, B), 256, 0, st>>>(q, k, v, g, beta, a, t0, T, HK, HV, normalize, qscale,
+                                                               eps, w, Ls);
+        int rc = after_launch("delta_chunk_intra");
+        if (rc) return rc;
+        delta_chunk_state<Tout><<<dim3(NSL, HV, B), 256, 0, st>>>(w, Ls, S, load, out, a, t0, T, nch, HK, HV);
+        rc = after_launch("delta_chunk_state");
+        if (rc) return rc;
+        load = 1;
+    }
+    return 0;
+}
+
+int launch_delta_chunked(const void* q, const void* k, const void* v, int in_dtype, const SeqLayout& a,
+                         const float* g, const float* beta, float* state, void* out, int out_dtype, int B, int T,
+                         int HK, int HV, int normalize, float qscale, float eps, void* ws, size_t ws_bytes,
+                         hipStream_t st) {
+    if (B < 0 || T < 0 || HK <= 0 || HV <= 0 || HV % HK) return fail(AEGIST_ERR_SHAPE, "delta_chunked: need HV % HK == 0");
+    if (B == 0 || T == 0) return 0;
+#define AEG_CHUNKED(TI, TO)                                                                                          \
+    return run_chunked<TI, TO>((const TI*)q, (const TI*)k, (const TI*)v, g, beta, state, (TO*)out, a, B, T, HK, HV, \
+                               normalize, qscale, eps, ws, ws_bytes, st)
+    if (in_dtype == AEGIST_F32 && out_dtype == AEGIST_F32) AEG_CHUNKED(float, float);
+    if (in_dtype == AEGIST_F32 && out_dtype == AEGIST_BF16) AEG_CHUNKED(float, uint16_t);
+    if (in_dtype == AEGIST_BF16 && out_dtype == AEGIST_F32) AEG_CHUNKED(uint16_t, float);
+    if (in_dtype == AEGIST_BF16 && out_dtype == AEGIST_BF16) AEG_CHUNKED(uint16_t, uint16_t);
+#undef AEG_CHUNKED
+    return fail(AEGIST_ERR_DTYPE, "delta_chunked: dtypes must be AEGIST_F32 or AEGIST_BF16");
+}
+
+// Engine mirror for T >= 64: y [T, C] rows q | k | v (already normalised), gb [T, 2HV].
+int delta_scan_chunked(const float* y, const float* gb, float* state, float* o, int T, int C, int HK, int HV,
+                       hipStream_t st) {
+    SeqLayout a{0, C, D, 0, C, D, 0, (long long)HV * D, D, 0, 2 * HV};
+    size_t need = delta_chunked_ws_bytes(1, T, HK, HV);
+    int rc = 0;
+    void* ws = mirror_workspace(need, &rc);
+    if (rc) return rc;
+    return launch_delta_chunked(y, y + (size_t)HK * D, y + (size_t)2 * HK * D, AEGIST_F32, a, gb, gb + HV, state, o,
+                                AEGIST_F32, 1, T, HK, HV, 0, 1.f, 0.f, ws, need, st);
+}
+
+}  // namespace aegist
+
+extern "C" size_t aegist_delta_chunked_workspace_bytes(int B, int T, int HV) {
+    // HK only changes the q_n / k_n^T share; size for HK = HV (the largest)
+    return delta_chunked_ws_bytes(B, T, HV, HV);
+}
+
+extern "C" int aegist_delta_chunked(const void* q, const void* k, const void* v, int in_dtype, long long sb_qk,
+                                    long long st_qk, long long sh_qk, long long sb_v, long long st_v, long long sh_v,
+                                    const float* g, const float* beta, float* state, void* out, int out_dtype,
+                                    long long sb_o, long long st_o, long long sh_o, int B, int T, int HK, int HV,
+                                    int normalize, float qscale, float eps, void* workspace, size_t workspace_bytes,
+                                    void* stream) {
+    SeqLayout a{sb_qk, st_qk, sh_qk, sb_v, st_v, sh_v, sb_o, st_o, sh_o, (long long)T * HV, HV};
+    return launch_delta_chunked(q, k, v, in_dtype, a, g, beta, state, out, out_dtype, B, T, HK, HV, normalize, qscale,
+                                eps, workspace, workspace_bytes, AEG_STREAM(stream));
+}

@@ -6,12 +6,13 @@
 //      conv state (each channel is owned by exactly one workgroup, so the in-place update is
 //      race-free),
 //   2. L2-normalises q and k (q also times qscale) in fp32 through LDS,
-//   3. streams each value head's 128x128 fp32 state HBM -> VGPRs -> HBM exactly once:
-//      every thread holds 16 rows x 4 columns (float4 loads; one wave instruction moves two
-//      full 512-byte rows), computes the column dot products S^T k and S^T q, reduces them
-//      across the 8 threads sharing a column (one xor-32 shuffle + LDS across 4 waves), then
-//      writes S' = e^g S + k delta^T with delta = (v - e^g S^T k) beta and emits
-//      o = e^g S^T q + (k.q) delta.
+//   3. streams each value head's 128x128 fp32 state HBM -> VGPRs -> HBM exactly once, in
+//      four 32-column slices with two slices in flight (columns of S are independent): the
+//      first two slices are requested before the conv even starts; per slice every thread
+//      holds 4 rows x 4 columns, the column dot products S^T k and S^T q are reduced over
+//      rows (three xor shuffles + LDS across 4 waves), then S' = e^g S + k delta^T is
+//      written with delta = (v - e^g S^T k) beta, o = e^g S^T q + (k.q) delta is emitted,
+//      and slice j+2 is requested. Loads and stores are nontemporal (streamed once).
 // The o formula is S'^T q expanded, so the state is read once and written once: the kernel
 // is HBM-bound at 2 x 64 KiB of state per (b, value head) plus ~2 KiB of conv traffic.
 //
@@ -25,6 +26,23 @@ namespace {
 
 constexpr int D = 128;  // dk = dv
 
+// State traffic is streamed: nontemporal loads and stores keep the 128 MiB-per-layer state
+// from displacing reusable lines in L2 / MALL.
+__device__ __forceinline__ float4 ld_stream(const float* p) {
+    float4 r;
+    r.x = __builtin_nontemporal_load(p);
+    r.y = __builtin_nontemporal_load(p + 1);
+    r.z = __builtin_nontemporal_load(p + 2);
+    r.w = __builtin_nontemporal_load(p + 3);
+    return r;
+}
+__device__ __forceinline__ void st_stream(float* p, float4 v) {
+    __builtin_nontemporal_store(v.x, p);
+    __builtin_nontemporal_store(v.y, p + 1);
+    __builtin_nontemporal_store(v.z, p + 2);
+    __builtin_nontemporal_store(v.w, p + 3);
+}
+
 template <int R, typename Tin, typename Tout>
 __global__ void __launch_bounds__(256 * R) delta_decode_kernel(
     const Tin* __restrict__ qkv, const uint16_t* __restrict__ conv_w, float* __restrict__ conv_state,
@@ -34,10 +52,24 @@ __global__ void __launch_bounds__(256 * R) delta_decode_kernel(
     constexpr int NCH = 2 * D + R * D;
     __shared__ float sq[D], sk[D], sv[R][D];
     __shared__ float red[8];
-    __shared__ float4 part[R][4][2][D / 4];
+    __shared__ float4 part[2][R][4][2][8];
 
     const int kh = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
     const int C = 2 * HK * D + HV * D;
+    const int wave = tid / WAVE, lane = tid % WAVE;
+    // state mapping: per value head 256 threads; lane = (column group cg of 4 columns within a
+    // 32-column slice, row group rr); thread rows rbase + 32 i, i < 4
+    const int hl = tid / 256, lt = tid % 256, w4 = lt / WAVE, cg = lane % 8, rr = lane / 8;
+    const int hv = kh * R + hl;
+    float* S = state + ((size_t)b * HV + hv) * D * D;
+    const int rbase = w4 * 8 + rr;
+
+    // ---- 0. start streaming column slices 0 and 1 before the conv (independent of it)
+    float4 s[2][4];
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) s[j][i] = ld_stream(S + (size_t)(rbase + 32 * i) * D + 32 * j + cg * 4);
 
     // ---- 1. conv + SiLU + conv-state update for this workgroup's channels
     float ymine = 0.f;
@@ -60,7 +92,6 @@ __global__ void __launch_bounds__(256 * R) delta_decode_kernel(
     }
 
     // ---- 2. L2 norms: q lives in waves 0-1, k in waves 2-3
-    const int wave = tid / WAVE, lane = tid % WAVE;
     if (tid < 2 * D) {
         float ss = wave_sum(ymine * ymine);
         if (lane == 0) red[wave] = ss;
@@ -78,63 +109,70 @@ __global__ void __launch_bounds__(256 * R) delta_decode_kernel(
     }
     __syncthreads();
     const float kq = red[4] + red[5];
-
-    // ---- 3. state stream for value head hv
-    const int hl = tid / 256, lt = tid % 256, w4 = lt / WAVE, cg = lane % 32, rs = lane / 32;
-    const int hv = kh * R + hl;
-    float* S = state + ((size_t)b * HV + hv) * D * D;
-    const int row0 = w4 * 2 + rs;  // rows row0 + 8 i
-
-    float4 s[16];
-#pragma unroll
-    for (int i = 0; i < 16; i++) s[i] = *(const float4*)(S + (size_t)(row0 + 8 * i) * D + cg * 4);
-
-    float4 pk = {0.f, 0.f, 0.f, 0.f}, pq = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int i = 0; i < 16; i++) {
-        const float kr = sk[row0 + 8 * i], qr = sq[row0 + 8 * i];
-        pk.x += s[i].x * kr; pk.y += s[i].y * kr; pk.z += s[i].z * kr; pk.w += s[i].w * kr;
-        pq.x += s[i].x * qr; pq.y += s[i].y * qr; pq.z += s[i].z * qr; pq.w += s[i].w * qr;
-    }
-    pk.x += __shfl_xor(pk.x, 32, WAVE); pk.y += __shfl_xor(pk.y, 32, WAVE);
-    pk.z += __shfl_xor(pk.z, 32, WAVE); pk.w += __shfl_xor(pk.w, 32, WAVE);
-    pq.x += __shfl_xor(pq.x, 32, WAVE); pq.y += __shfl_xor(pq.y, 32, WAVE);
-    pq.z += __shfl_xor(pq.z, 32, WAVE); pq.w += __shfl_xor(pq.w, 32, WAVE);
-    if (rs == 0) {
-        part[hl][w4][0][cg] = pk;
-        part[hl][w4][1][cg] = pq;
-    }
-    __syncthreads();
-    float4 SK = part[hl][0][0][cg], SQ = part[hl][0][1][cg];
-#pragma unroll
-    for (int w = 1; w < 4; w++) {
-        const float4 a = part[hl][w][0][cg], c = part[hl][w][1][cg];
-        SK.x += a.x; SK.y += a.y; SK.z += a.z; SK.w += a.w;
-        SQ.x += c.x; SQ.y += c.y; SQ.z += c.z; SQ.w += c.w;
-    }
     const float decay = expf(g[(size_t)b * HV + hv]), bt = beta[(size_t)b * HV + hv];
-    const float* vv = sv[hl] + cg * 4;
-    float4 dl;
-    dl.x = (vv[0] - decay * SK.x) * bt;
-    dl.y = (vv[1] - decay * SK.y) * bt;
-    dl.z = (vv[2] - decay * SK.z) * bt;
-    dl.w = (vv[3] - decay * SK.w) * bt;
+    float kr[4], qr[4];
 #pragma unroll
-    for (int i = 0; i < 16; i++) {
-        const float kr = sk[row0 + 8 * i];
-        float4 n;
-        n.x = decay * s[i].x + kr * dl.x;
-        n.y = decay * s[i].y + kr * dl.y;
-        n.z = decay * s[i].z + kr * dl.z;
-        n.w = decay * s[i].w + kr * dl.w;
-        *(float4*)(S + (size_t)(row0 + 8 * i) * D + cg * 4) = n;
+    for (int i = 0; i < 4; i++) {
+        kr[i] = sk[rbase + 32 * i];
+        qr[i] = sq[rbase + 32 * i];
     }
-    if (w4 == 0 && rs == 0) {
-        Tout* o = out + ((size_t)b * HV + hv) * D + cg * 4;
-        Act<Tout>::st(o, 0, decay * SQ.x + kq * dl.x);
-        Act<Tout>::st(o, 1, decay * SQ.y + kq * dl.y);
-        Act<Tout>::st(o, 2, decay * SQ.z + kq * dl.z);
-        Act<Tout>::st(o, 3, decay * SQ.w + kq * dl.w);
+
+    // ---- 3. four 32-column slices, two in flight: reduce, update, store, prefetch
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        float4 pk = {0.f, 0.f, 0.f, 0.f}, pq = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float4 x = s[j & 1][i];
+            pk.x += x.x * kr[i]; pk.y += x.y * kr[i]; pk.z += x.z * kr[i]; pk.w += x.w * kr[i];
+            pq.x += x.x * qr[i]; pq.y += x.y * qr[i]; pq.z += x.z * qr[i]; pq.w += x.w * qr[i];
+        }
+#pragma unroll
+        for (int o = 8; o < WAVE; o <<= 1) {
+            pk.x += __shfl_xor(pk.x, o, WAVE); pk.y += __shfl_xor(pk.y, o, WAVE);
+            pk.z += __shfl_xor(pk.z, o, WAVE); pk.w += __shfl_xor(pk.w, o, WAVE);
+            pq.x += __shfl_xor(pq.x, o, WAVE); pq.y += __shfl_xor(pq.y, o, WAVE);
+            pq.z += __shfl_xor(pq.z, o, WAVE); pq.w += __shfl_xor(pq.w, o, WAVE);
+        }
+        if (rr == 0) {
+            part[j & 1][hl][w4][0][cg] = pk;
+            part[j & 1][hl][w4][1][cg] = pq;
+        }
+        __syncthreads();
+        float4 SK = part[j & 1][hl][0][0][cg], SQ = part[j & 1][hl][0][1][cg];
+#pragma unroll
+        for (int w = 1; w < 4; w++) {
+            const float4 a = part[j & 1][hl][w][0][cg], c = part[j & 1][hl][w][1][cg];
+            SK.x += a.x; SK.y += a.y; SK.z += a.z; SK.w += a.w;
+            SQ.x += c.x; SQ.y += c.y; SQ.z += c.z; SQ.w += c.w;
+        }
+        const float* vv = sv[hl] + 32 * j + cg * 4;
+        float4 dl;
+        dl.x = (vv[0] - decay * SK.x) * bt;
+        dl.y = (vv[1] - decay * SK.y) * bt;
+        dl.z = (vv[2] - decay * SK.z) * bt;
+        dl.w = (vv[3] - decay * SK.w) * bt;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float4 x = s[j & 1][i];
+            float4 n;
+            n.x = decay * x.x + kr[i] * dl.x;
+            n.y = decay * x.y + kr[i] * dl.y;
+            n.z = decay * x.z + kr[i] * dl.z;
+            n.w = decay * x.w + kr[i] * dl.w;
+            st_stream(S + (size_t)(rbase + 32 * i) * D + 32 * j + cg * 4, n);
+        }
+        if (j < 2) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) s[j & 1][i] = ld_stream(S + (size_t)(rbase + 32 * i) * D + 32 * (j + 2) + cg * 4);
+        }
+        if (w4 == 0 && rr == 0) {
+            Tout* o = out + ((size_t)b * HV + hv) * D + 32 * j + cg * 4;
+            Act<Tout>::st(o, 0, decay * SQ.x + kq * dl.x);
+            Act<Tout>::st(o, 1, decay * SQ.y + kq * dl.y);
+            Act<Tout>::st(o, 2, decay * SQ.z + kq * dl.z);
+            Act<Tout>::st(o, 3, decay * SQ.w + kq * dl.w);
+        }
     }
 }
 

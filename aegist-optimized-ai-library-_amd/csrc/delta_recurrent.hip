@@ -144,7 +144,11 @@ extern "C" int aegist_delta_recurrent(const void* q, const void* k, const void* 
 }
 
 // Engine mirror: y [T, C] fp32 rows q | k | v (already L2-normalised), gb [T, 2HV] (g, then
-// beta), state [HV, 128, 128], o [T, HV, 128].
+// beta), state [HV, 128, 128], o [T, HV, 128]. Sequences of 64+ tokens take the chunked path.
+namespace aegist {
+int delta_scan_chunked(const float* y, const float* gb, float* state, float* o, int T, int C, int HK, int HV,
+                       hipStream_t st);
+}
 
 extern "C" int aegist_delta_scan(const float* y, const float* gb, float* state, float* o, int T, int C, int HK, int HV,
                                  void* stream) {
@@ -152,6 +156,7 @@ extern "C" int aegist_delta_scan(const float* y, const float* gb, float* state, 
         return fail(AEGIST_ERR_SHAPE, "delta_scan: need C == 2*HK*128 + HV*128 and HV % HK == 0");
     if (T == 0) return 0;
     hipStream_t st = AEG_STREAM(stream);
+    if (T >= 64) return delta_scan_chunked(y, gb, state, o, T, C, HK, HV, st);
     // g and beta are interleaved per token in gb: present them through the strided kernel
     // by pointing g at gb and beta at gb + HV with a token stride of 2*HV.
     SeqArgs a{0, C, D, 0, C, D, 0, (long long)HV * D, D, 0, 2 * HV};

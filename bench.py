@@ -69,6 +69,41 @@ def cpu_baseline_decode(torch):
                       f"median of 5 after 2 warm-ups, scaled x{LAYERS}; {per_layer * 1e3:.1f} ms per layer"}
 
 
+PREFILL_T = 8192
+# algorithmic FLOPs per (value head, 64-token chunk): kb k^T, two unit-triangular solves,
+# q k^T, w S, q S, k^T v_new, intra v_new (C = 64, d = 128)
+FLOP_PER_HEAD_CHUNK = 2 * 64 * 64 * 128 + 2 * (64 * 63 // 2) * 128 * 2 + 2 * 64 * 64 * 128 + 3 * 2 * 64 * 128 * 128 \
+    + 2 * 64 * 64 * 128
+
+
+def bench_prefill(torch, ops, dev, reps=10):
+    """Config 2: chunked DeltaNet prefill, B=1, T=8192, 16 QK / 32 V heads, bf16 q/k/v
+    (normalised in-kernel), fp32 state; one layer per call."""
+    bf = torch.bfloat16
+    q = ops.fill_normal(torch.empty(1, PREFILL_T, HK, D, device=dev, dtype=bf), 7001).transpose(1, 2)
+    k = ops.fill_normal(torch.empty(1, PREFILL_T, HK, D, device=dev, dtype=bf), 7002).transpose(1, 2)
+    v = ops.fill_normal(torch.empty(1, PREFILL_T, HV, D, device=dev, dtype=bf), 7003).transpose(1, 2)
+    g = -torch.nn.functional.softplus(ops.fill_normal(torch.empty(1, HV, PREFILL_T, device=dev), 7004))
+    beta = torch.sigmoid(ops.fill_normal(torch.empty(1, HV, PREFILL_T, device=dev), 7005))
+    S = torch.zeros(1, HV, D, D, device=dev)
+    run = lambda: ops.delta_rule_chunked(q, k, v, g, beta, S, normalize=True, qscale=D ** -0.5, out_dtype=bf)
+    for _ in range(2):
+        run()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        run()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    flops = FLOP_PER_HEAD_CHUNK * HV * (PREFILL_T // 64)
+    tflops = flops / (ms * 1e-3) / 1e12
+    return {"workload": "config2: chunked WY prefill, B=1, T=8192, 32 V heads, one layer", "ms": round(ms, 4),
+            "tok_s": round(PREFILL_T / (ms * 1e-3), 1), "tflops": round(tflops, 2),
+            "mfma_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), "flop_per_call": flops}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -148,6 +183,7 @@ def main():
                      "launch_us": round(launch_ms * 1e3, 2)},
         "wall_s": round(wall, 3),
     }
+    res["prefill"] = bench_prefill(torch, ops, dev)
     if not args.no_cpu:
         res["cpu_baseline"] = cpu_baseline_decode(torch)
     print(json.dumps(res), flush=True)

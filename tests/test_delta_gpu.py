@@ -196,3 +196,79 @@ def test_engine_znorm(dev):
     got = ops.engine_znorm(x.to(dev), w.to(dev))
     torch.cuda.synchronize()
     assert rel_err(got, R.znorm(x, w.float())) < 1e-5
+
+
+# --- chunked WY prefill (MFMA) ----------------------------------------------------------------
+
+@pytest.mark.parametrize("T,with_state", [(1, False), (37, True), (64, False), (100, True), (130, False),
+                                          (512, True), (2100, True)])
+def test_chunked_matches_recurrent_oracle(dev, T, with_state):
+    print(f"chunked T={T} state={with_state}", flush=True)
+    q, k, v, g, beta = seq_inputs(1, 4, 8, T, seed=T)
+    S0 = torch.randn(1, 8, D, D, generator=_gen(T)) * 0.02 if with_state else None
+    o_ref, S_ref = oracle_seq(q, k, v, g, beta, None if S0 is None else S0.clone(), chunked=False)
+    S = S0.to(dev) if with_state else None
+    o, S_out = ops.delta_rule_chunked(q.to(dev), k.to(dev), v.to(dev), g.to(dev), beta.to(dev), S, normalize=True,
+                                      qscale=D ** -0.5)
+    torch.cuda.synchronize()
+    assert rel_err(o, o_ref) < DELTA_TOL
+    assert rel_err(S_out, S_ref) < DELTA_TOL
+
+
+def test_chunked_batch_and_layout(dev):
+    """B = 3, HV/HK = 2, engine-style row layout (q | k | v packed per token), fp32 inputs."""
+    B, HK, HV, T = 3, 2, 4, 150
+    g_ = _gen(8)
+    y = torch.randn(B, T, 2 * HK * D + HV * D, generator=g_)
+    qv = y[..., :HK * D].reshape(B, T, HK, D).transpose(1, 2)
+    kv = y[..., HK * D:2 * HK * D].reshape(B, T, HK, D).transpose(1, 2)
+    vv = y[..., 2 * HK * D:].reshape(B, T, HV, D).transpose(1, 2)
+    beta = torch.sigmoid(torch.randn(B, HV, T, generator=g_))
+    g = -F.softplus(torch.randn(B, HV, T, generator=g_))
+    o_ref, S_ref = oracle_seq(qv, kv, vv, g, beta, None)
+    yd = y.to(dev)
+    qd = yd[..., :HK * D].reshape(B, T, HK, D).transpose(1, 2)
+    kd = yd[..., HK * D:2 * HK * D].reshape(B, T, HK, D).transpose(1, 2)
+    vd = yd[..., 2 * HK * D:].reshape(B, T, HV, D).transpose(1, 2)
+    o, S = ops.delta_rule_chunked(qd, kd, vd, g.to(dev), beta.to(dev), None, normalize=True, qscale=D ** -0.5)
+    torch.cuda.synchronize()
+    assert rel_err(o, o_ref) < DELTA_TOL and rel_err(S, S_ref) < DELTA_TOL
+
+
+def test_config2_prefill_8k(dev):
+    """Config 2: B=1, T=8192, 16 QK / 32 V heads, zero initial state; against the CPU chunked
+    oracle on the full sequence and the recurrent form on the first 512 tokens."""
+    T = 8192
+    q, k, v, g, beta = seq_inputs(1, 16, 32, T, seed=2)
+    qd, kd, vd, gd, bd = (t.to(dev) for t in (q, k, v, g, beta))
+    o, S = ops.delta_rule_chunked(qd, kd, vd, gd, bd, None, normalize=True, qscale=D ** -0.5)
+    o512, S512 = ops.delta_rule_chunked(qd[:, :, :512], kd[:, :, :512], vd[:, :, :512], gd[:, :, :512],
+                                        bd[:, :, :512], None, normalize=True, qscale=D ** -0.5)
+    torch.cuda.synchronize()
+    o_ref, S_ref = oracle_seq(q, k, v, g, beta, None, chunked=True)
+    assert rel_err(o, o_ref) < DELTA_TOL, rel_err(o, o_ref)
+    assert rel_err(S, S_ref) < DELTA_TOL, rel_err(S, S_ref)
+    r_ref, rS_ref = oracle_seq(q[:, :, :512], k[:, :, :512], v[:, :, :512], g[:, :, :512], beta[:, :, :512], None,
+                               chunked=False)
+    assert rel_err(o512, r_ref) < DELTA_TOL and rel_err(S512, rS_ref) < DELTA_TOL
+    assert torch.equal(o[:, :, :512].cpu(), o512.cpu()) or rel_err(o[:, :, :512], o512) < 1e-6
+
+
+def test_engine_delta_scan_long_prompt(dev):
+    """delta_scan mirror at T = 200 takes the chunked path; equals the recurrent oracle."""
+    HK, HV, T = 16, 32, 200
+    C = 2 * HK * D + HV * D
+    g_ = _gen(31)
+    y = torch.randn(T, C, generator=g_)
+    gg = -F.softplus(torch.randn(T, HV, generator=g_))
+    bb = torch.sigmoid(torch.randn(T, HV, generator=g_))
+    S0 = torch.randn(1, HV, D, D, generator=g_) * 0.02
+    qr, kr, vr = R.delta_prep(y.unsqueeze(0), HK, HV, D, D)
+    yn = torch.cat([qr[0, ::2].transpose(0, 1).reshape(T, -1), kr[0, ::2].transpose(0, 1).reshape(T, -1),
+                    vr[0].transpose(0, 1).reshape(T, -1)], -1).contiguous()
+    o_ref, S_ref = R.delta_rule_recurrent(qr, kr, vr, gg.t().unsqueeze(0), bb.t().unsqueeze(0), S0.clone())
+    S = S0[0].clone().to(dev)
+    o = ops.engine_delta_scan(yn.to(dev), torch.cat([gg, bb], -1).to(dev), S, HK, HV)
+    torch.cuda.synchronize()
+    assert rel_err(o, o_ref[0].transpose(0, 1)) < DELTA_TOL
+    assert rel_err(S, S_ref[0]) < DELTA_TOL
