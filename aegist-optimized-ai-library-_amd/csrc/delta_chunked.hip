@@ -45,8 +45,10 @@ struct SeqLayout {
     long long sb_g, st_g;  // g / beta strides by sequence and token; value head contiguous
 };
 
-// Workspace of one segment. Per (b, hv, chunk): u fp32 [64][128], w fp16 [64][128],
-// intra fp16 [64][64], cum fp32 [64]. Per (b, kh, chunk): qn fp16 [64][128], knT fp16 [128][64].
+// Workspace of one segment. Per (b, hv, chunk): u fp32 [64][128] stored in K2's accumulator
+// fragment order (see u_frag), w fp16 [64][128], intra fp16 [64][64], and the decay factors
+// dec fp32 [3][64] = (e^{cum_i}, e^{cum_last - cum_i}, e^{cum_last}). Per (b, kh, chunk):
+// qn fp16 [64][128], knT fp16 [128][64].
 // Plus the carried state [B, HV, 128, 128] fp32 when the caller passes none.
 struct WsLayout {
     size_t u, w, intra, cum, qn, knt, state, total;
@@ -61,7 +63,7 @@ __host__ __device__ inline WsLayout ws_layout(int B, int HK, int HV, int nch) {
     L.u = off; off += al256(units_v * CH * D * 4);
     L.w = off; off += al256(units_v * CH * D * 2);
     L.intra = off; off += al256(units_v * CH * CH * 2);
-    L.cum = off; off += al256(units_v * CH * 4);
+    L.cum = off; off += al256(units_v * 3 * CH * 4);
     L.qn = off; off += al256(units_k * CH * D * 2);
     L.knt = off; off += al256(units_k * CH * D * 2);
     L.state = off; off += al256((size_t)B * HV * D * D * 4);
@@ -71,40 +73,80 @@ __host__ __device__ inline WsLayout ws_layout(int B, int HK, int HV, int nch) {
 
 __device__ __forceinline__ half8 ld_h8(const half_t* p) { return *(const half8*)p; }
 
+// 8 consecutive activations as fp32 (two 16-byte loads for fp32, one for bf16)
+template <typename T> __device__ __forceinline__ void ld8(const T* p, float* o);
+template <> __device__ __forceinline__ void ld8<float>(const float* p, float* o) {
+    const float4 a = ((const float4*)p)[0], b = ((const float4*)p)[1];
+    o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w; o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w;
+}
+template <> __device__ __forceinline__ void ld8<uint16_t>(const uint16_t* p, float* o) {
+    const uint4 a = *(const uint4*)p;
+    o[0] = bf_lo(a.x); o[1] = bf_hi(a.x); o[2] = bf_lo(a.y); o[3] = bf_hi(a.y);
+    o[4] = bf_lo(a.z); o[5] = bf_hi(a.z); o[6] = bf_lo(a.w); o[7] = bf_hi(a.w);
+}
+
+// Offset (in floats) of u[i][col] inside one chunk's u block, laid out as K2 reads it: slice
+// sl = col / 32, wave wv = i / 16, column tile ct, then the 64 lanes (gq = (i % 16) / 4,
+// n = col % 16) of a 16x16 accumulator, each holding rows 4gq .. 4gq+3 contiguously.
+__device__ __forceinline__ int u_frag(int i, int col) {
+    const int sl = col / 32, ct = (col % 32) / 16, n = col % 16, wv = i / 16, gq = (i % 16) / 4, j = i % 4;
+    return ((((sl * 4 + wv) * 2 + ct) * 64) + gq * 16 + n) * 4 + j;
+}
+
 __device__ __forceinline__ f32x4 mfma16(half8 a, half8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
 // ---------------------------------------------------------------------------------------------
-// K1: intra-chunk work. grid (nch, HV, B), 256 threads.
+// K1: intra-chunk work. grid (nch, HV, B), 256 threads (4 waves).
 template <typename Tin>
 __global__ void __launch_bounds__(256) delta_chunk_intra(const Tin* __restrict__ q, const Tin* __restrict__ k,
                                                          const Tin* __restrict__ v, const float* __restrict__ g,
                                                          const float* __restrict__ beta, SeqLayout a, int t0, int T,
                                                          int HK, int HV, int normalize, float qscale, float eps,
-                                                         unsigned char* __restrict__ ws, WsLayout L) {
-    __shared__ __attribute__((aligned(16))) half_t Qs[CH][QK_LD];
+                                                         unsigned char* __restrict__ ws, WsLayout L, int vec_in) {
+    constexpr bool kSplitV = sizeof(Tin) == 4;  // fp32 v needs a low fp16 part; bf16 v is exact in fp16
+    __shared__ __attribute__((aligned(16))) half_t QV[CH][QK_LD];  // q_n tile, then v (fp16 hi)
+    __shared__ __attribute__((aligned(16))) half_t Vl[kSplitV ? CH : 1][QK_LD];
     __shared__ __attribute__((aligned(16))) half_t Ks[CH][QK_LD];
-    __shared__ __attribute__((aligned(16))) float As[CH][A_LD];
-    __shared__ float cum_s[CH], beta_s[CH], rk_s[CH], g_s[CH];
+    __shared__ __attribute__((aligned(16))) float As[CH][A_LD];    // A, then X = (I + A)^-1 in place
+    __shared__ float Pt[3][16][17];
+    __shared__ float cum_s[CH], beta_s[CH], g_s[CH];
 
     const int c = blockIdx.x, hv = blockIdx.y, b = blockIdx.z, nch = gridDim.x;
-    const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
+    const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE, n = lane % 16, gq = lane / 16;
     const int R = HV / HK, kh = hv / R;
     const bool writes_qk = (hv % R) == 0;
     const int tok0 = t0 + c * CH;
+    const size_t vu = (size_t)(b * HV + hv) * nch + c;
 
-    // ---- 1. load q, k rows; row norms; fp16 normalised tiles
+    // ---- 1. q, k, v rows (thread = row, 32-element quarter); fp32 row norms; fp16 q_n, k_n
+    const int row = tid / 4, qq = tid % 4, tok = tok0 + row;
+    const bool valid = tok < T;
+    float xv[32];
     {
-        const int row = tid / 4, qq = tid % 4, tok = tok0 + row;
-        const bool valid = tok < T;
         const Tin* qp = q + b * a.sb_qk + (long long)tok * a.st_qk + kh * a.sh_qk + qq * 32;
         const Tin* kp = k + b * a.sb_qk + (long long)tok * a.st_qk + kh * a.sh_qk + qq * 32;
-        float xq[32], xk[32], ssq = 0.f, ssk = 0.f;
+        const Tin* vp = v + b * a.sb_v + (long long)tok * a.st_v + hv * a.sh_v + qq * 32;
+        float xq[32], xk[32];
+        if (valid && vec_in) {
+#pragma unroll
+            for (int e = 0; e < 32; e += 8) {
+                ld8<Tin>(qp + e, xq + e);
+                ld8<Tin>(kp + e, xk + e);
+                ld8<Tin>(vp + e, xv + e);
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 32; e++) {
+                xq[e] = valid ? Act<Tin>::ld(qp, e) : 0.f;
+                xk[e] = valid ? Act<Tin>::ld(kp, e) : 0.f;
+                xv[e] = valid ? Act<Tin>::ld(vp, e) : 0.f;
+            }
+        }
+        float ssq = 0.f, ssk = 0.f;
 #pragma unroll
         for (int e = 0; e < 32; e++) {
-            xq[e] = valid ? Act<Tin>::ld(qp, e) : 0.f;
-            xk[e] = valid ? Act<Tin>::ld(kp, e) : 0.f;
             ssq += xq[e] * xq[e];
             ssk += xk[e] * xk[e];
         }
@@ -115,18 +157,25 @@ __global__ void __launch_bounds__(256) delta_chunk_intra(const Tin* __restrict__
         const float rq = normalize ? rsqrtf(ssq + eps) : 1.f, sc = normalize ? qscale : 1.f;
         const float rk = normalize ? rsqrtf(ssk + eps) : 1.f;
 #pragma unroll
-        for (int e = 0; e < 32; e++) {
-            Qs[row][qq * 32 + e] = (half_t)((xq[e] * rq) * sc);
-            Ks[row][qq * 32 + e] = (half_t)(xk[e] * rk);
+        for (int e = 0; e < 32; e += 8) {
+            half8 hq, hk;
+#pragma unroll
+            for (int f = 0; f < 8; f++) {
+                hq[f] = (half_t)((xq[e + f] * rq) * sc);
+                hk[f] = (half_t)(xk[e + f] * rk);
+            }
+            *(half8*)&QV[row][qq * 32 + e] = hq;
+            *(half8*)&Ks[row][qq * 32 + e] = hk;
         }
         if (qq == 0) {
-            rk_s[row] = rk;
             beta_s[row] = valid ? beta[b * a.sb_g + (long long)tok * a.st_g + hv] : 0.f;
             g_s[row] = valid ? g[b * a.sb_g + (long long)tok * a.st_g + hv] : 0.f;
         }
     }
     __syncthreads();
-    // ---- 2. cum = inclusive prefix sum of g (wave 0); q_n / k_n^T copies for K2
+
+    // ---- 2. cum = inclusive prefix sum of g (wave 0) and the decay factors K2 needs;
+    // q_n rows and k_n^T for K2 (once per QK head)
     if (wave == 0) {
         float x = g_s[lane];
 #pragma unroll
@@ -135,20 +184,23 @@ __global__ void __launch_bounds__(256) delta_chunk_intra(const Tin* __restrict__
             if (lane >= d) x += y;
         }
         cum_s[lane] = x;
-        ((float*)(ws + L.cum))[((size_t)(b * HV + hv) * nch + c) * CH + lane] = x;
+        const float last = __shfl(x, CH - 1, WAVE);
+        float* dec = (float*)(ws + L.cum) + vu * 3 * CH;
+        dec[lane] = __expf(x);
+        dec[CH + lane] = __expf(last - x);
+        dec[2 * CH + lane] = __expf(last);
     }
     if (writes_qk) {
         const size_t ku = ((size_t)(b * HK + kh) * nch + c);
         half_t* qn = (half_t*)(ws + L.qn) + ku * CH * D;
         half_t* knt = (half_t*)(ws + L.knt) + ku * CH * D;
-        {   // q_n rows: thread = (row, 32-element quarter)
-            const int row = tid / 4, qq = tid % 4;
-            const half8* src = (const half8*)&Qs[row][qq * 32];
+        {
+            const half8* src = (const half8*)&QV[row][qq * 32];
             half8* dst = (half8*)(qn + row * D + qq * 32);
 #pragma unroll
             for (int e = 0; e < 4; e++) dst[e] = src[e];
         }
-        {   // k_n^T: thread = (dk, 32-row half)
+        {   // thread = (dk, 32-row half)
             const int dk = tid / 2, hh = tid % 2;
             half8 buf[4];
 #pragma unroll
@@ -162,19 +214,22 @@ __global__ void __launch_bounds__(256) delta_chunk_intra(const Tin* __restrict__
 
     // ---- 3. k_n k_n^T and q_n k_n^T on MFMA: wave = 16-row block rb, column blocks cb <= rb
     {
-        const int rb = wave, n = lane % 16, gq = lane / 16;
-        half_t* intra = (half_t*)(ws + L.intra) + ((size_t)(b * HV + hv) * nch + c) * CH * CH;
+        const int rb = wave;
+        half_t* intra = (half_t*)(ws + L.intra) + vu * CH * CH;
         half8 ak[4], aq[4];
 #pragma unroll
         for (int ks = 0; ks < 4; ks++) {
             ak[ks] = ld_h8(&Ks[16 * rb + n][32 * ks + 8 * gq]);
-            aq[ks] = ld_h8(&Qs[16 * rb + n][32 * ks + 8 * gq]);
+            aq[ks] = ld_h8(&QV[16 * rb + n][32 * ks + 8 * gq]);
         }
         for (int cb = 0; cb < 4; cb++) {
             const int jj = 16 * cb + n;
-            if (cb > rb) {
+            if (cb > rb) {  // upper blocks: zero in intra and in A (X = (I + A)^-1 stays lower there)
 #pragma unroll
-                for (int j = 0; j < 4; j++) intra[(16 * rb + 4 * gq + j) * CH + jj] = (half_t)0.f;
+                for (int j = 0; j < 4; j++) {
+                    intra[(16 * rb + 4 * gq + j) * CH + jj] = (half_t)0.f;
+                    As[16 * rb + 4 * gq + j][jj] = 0.f;
+                }
                 continue;
             }
             f32x4 accA = {0.f, 0.f, 0.f, 0.f}, accQ = {0.f, 0.f, 0.f, 0.f};
@@ -195,45 +250,132 @@ __global__ void __launch_bounds__(256) delta_chunk_intra(const Tin* __restrict__
     }
     __syncthreads();
 
-    // ---- 4. forward substitution, one thread per right-hand-side column
-    {
-        const int col = tid;
-        const bool isv = col < D;
-        const int cc = isv ? col : col - D;
-        float x[CH];
+    // ---- 4. v (fp16 hi / lo) into the q tile's space; X = (I + A)^-1, blocked by 16
 #pragma unroll
-        for (int i = 0; i < CH; i++) {
-            const int tok = tok0 + i;
-            float r = 0.f;
-            if (tok < T) {
-                if (isv) r = beta_s[i] * Act<Tin>::ld(v, b * a.sb_v + (long long)tok * a.st_v + hv * a.sh_v + cc);
-                else
-                    r = beta_s[i] * __expf(cum_s[i]) *
-                        (Act<Tin>::ld(k, b * a.sb_qk + (long long)tok * a.st_qk + kh * a.sh_qk + cc) * rk_s[i]);
-            }
-            x[i] = r;
+    for (int e = 0; e < 32; e += 8) {
+        half8 hv8, lv8;
+#pragma unroll
+        for (int f = 0; f < 8; f++) {
+            const half_t h = (half_t)xv[e + f];
+            hv8[f] = h;
+            lv8[f] = (half_t)(xv[e + f] - (float)h);
         }
+        *(half8*)&QV[row][qq * 32 + e] = hv8;
+        if constexpr (kSplitV) *(half8*)&Vl[row][qq * 32 + e] = lv8;
+    }
+    {   // 4a. diagonal block wave: lane j < 16 solves column j of (I + A_ww)^-1; A[i][k] of the
+        // block is broadcast from lane k with readlane
+        const int j = lane & 15, o = 16 * wave;
+        float acol[16], x[16];
 #pragma unroll
-        for (int i = 1; i < CH; i++) {
-            float s = x[i];
+        for (int i = 0; i < 16; i++) acol[i] = As[o + i][o + j];
 #pragma unroll
-            for (int kk = 0; kk < (i & ~3); kk += 4) {
-                const float4 a4 = *(const float4*)&As[i][kk];
-                s -= a4.x * x[kk] + a4.y * x[kk + 1] + a4.z * x[kk + 2] + a4.w * x[kk + 3];
-            }
+        for (int i = 0; i < 16; i++) {
+            float s = i == j ? 1.f : 0.f;
 #pragma unroll
-            for (int kk = (i & ~3); kk < i; kk++) s -= As[i][kk] * x[kk];
+            for (int kk = 0; kk < i; kk++)
+                s -= __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acol[i]), kk)) * x[kk];
             x[i] = s;
         }
-        const size_t vu = (size_t)(b * HV + hv) * nch + c;
-        if (isv) {
-            float* u = (float*)(ws + L.u) + vu * CH * D;
+        __syncthreads();  // every wave has read its A block column before X overwrites it
+        if (lane < 16) {
 #pragma unroll
-            for (int i = 0; i < CH; i++) u[i * D + cc] = x[i];
-        } else {
-            half_t* w = (half_t*)(ws + L.w) + vu * CH * D;
+            for (int i = 0; i < 16; i++) As[o + i][o + j] = x[i];
+        }
+    }
+    __syncthreads();
+    // 4b. block row r: wave c < r forms P = sum_{k=c}^{r-1} A_rk X_kc (fp32 MFMA 16x16x4), then
+    // X_rc = -X_rr P
+    for (int r = 1; r < 4; r++) {
+        f32x4 P = {0.f, 0.f, 0.f, 0.f};
+        const int cb = wave;
+        if (cb < r) {
+            for (int kb = cb; kb < r; kb++) {
 #pragma unroll
-            for (int i = 0; i < CH; i++) w[i * D + cc] = (half_t)x[i];
+                for (int s4 = 0; s4 < 4; s4++) {
+                    const float av = As[16 * r + n][16 * kb + 4 * s4 + gq];
+                    const float bv = As[16 * kb + 4 * s4 + gq][16 * cb + n];
+                    P = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, P, 0, 0, 0);
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < 4; j++) Pt[cb][4 * gq + j][n] = P[j];
+        }
+        __syncthreads();  // all reads of A_r* done; P visible
+        if (cb < r) {
+            f32x4 X = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int s4 = 0; s4 < 4; s4++) {
+                const float av = As[16 * r + n][16 * r + 4 * s4 + gq];
+                const float bv = Pt[cb][4 * s4 + gq][n];
+                X = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, X, 0, 0, 0);
+            }
+#pragma unroll
+            for (int j = 0; j < 4; j++) As[16 * r + 4 * gq + j][16 * cb + n] = -X[j];
+        }
+        __syncthreads();
+    }
+
+    // ---- 5. u = X diag(beta) v and w = X diag(beta e^cum) k_n on MFMA, X as fp16 hi + lo.
+    // Wave = column tiles {2 wave, 2 wave + 1} of both, all four 16-row blocks.
+    {
+        float* u = (float*)(ws + L.u) + vu * CH * D;
+        half_t* wout = (half_t*)(ws + L.w) + vu * CH * D;
+        half8 vbh[2][2], vbl[2][2], kb[2][2];
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            const int col = 16 * (2 * wave + t) + n;
+#pragma unroll
+            for (int ks = 0; ks < 2; ks++)
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    const int rr = 32 * ks + 8 * gq + i;
+                    vbh[t][ks][i] = QV[rr][col];
+                    if constexpr (kSplitV) vbl[t][ks][i] = Vl[rr][col];
+                    kb[t][ks][i] = Ks[rr][col];
+                }
+        }
+        float su[2][8], sw[2][8];
+#pragma unroll
+        for (int ks = 0; ks < 2; ks++)
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const int rr = 32 * ks + 8 * gq + i;
+                su[ks][i] = beta_s[rr];
+                sw[ks][i] = beta_s[rr] * __expf(cum_s[rr]);
+            }
+#pragma unroll
+        for (int rb = 0; rb < 4; rb++) {
+            half8 xuh[2], xul[2], xwh[2], xwl[2];
+#pragma unroll
+            for (int ks = 0; ks < 2; ks++)
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    const float x = As[16 * rb + n][32 * ks + 8 * gq + i];
+                    const float xu = x * su[ks][i], xw = x * sw[ks][i];
+                    half_t h = (half_t)xu;
+                    xuh[ks][i] = h;
+                    xul[ks][i] = (half_t)(xu - (float)h);
+                    h = (half_t)xw;
+                    xwh[ks][i] = h;
+                    xwl[ks][i] = (half_t)(xw - (float)h);
+                }
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+                f32x4 au = {0.f, 0.f, 0.f, 0.f}, aw = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int ks = 0; ks < 2; ks++) {
+                    au = mfma16(xuh[ks], vbh[t][ks], au);
+                    au = mfma16(xul[ks], vbh[t][ks], au);
+                    if constexpr (kSplitV) au = mfma16(xuh[ks], vbl[t][ks], au);
+                    aw = mfma16(xwh[ks], kb[t][ks], aw);
+                    aw = mfma16(xwl[ks], kb[t][ks], aw);
+                }
+                const int col = 16 * (2 * wave + t) + n;
+                *(f32x4*)(u + u_frag(16 * rb + 4 * gq, col)) = au;
+#pragma unroll
+                for (int j = 0; j < 4; j++) wout[(16 * rb + 4 * gq + j) * D + col] = (half_t)aw[j];
+            }
         }
     }
 }
@@ -244,10 +386,12 @@ __global__ void __launch_bounds__(256) delta_chunk_intra(const Tin* __restrict__
 template <typename Tout>
 __global__ void __launch_bounds__(256) delta_chunk_state(const unsigned char* __restrict__ ws, WsLayout L,
                                                          float* __restrict__ state, int load_state, Tout* __restrict__ out,
-                                                         SeqLayout a, int t0, int T, int nch, int HK, int HV) {
+                                                         SeqLayout a, int t0, int T, int nch, int HK, int HV,
+                                                         int vec_out) {
     __shared__ __attribute__((aligned(16))) half_t SsT[32][D + 8];   // S^T (fp16): [column][dk]
     __shared__ __attribute__((aligned(16))) half_t VnT[32][CH + 8];  // v_new^T (fp16)
     __shared__ __attribute__((aligned(16))) half_t VdT[32][CH + 8];  // (e^{cum_last-cum} v_new)^T
+    __shared__ float Ot[4][16][36];                                     // output staging per wave
 
     const int sl = blockIdx.x, hv = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE, n = lane % 16, gq = lane / 16;
@@ -265,38 +409,44 @@ __global__ void __launch_bounds__(256) delta_chunk_state(const unsigned char* __
                 S[rt][ct][j] = load_state ? Sg[(size_t)(32 * wave + 16 * rt + 4 * gq + j) * D + col0 + 16 * ct + n] : 0.f;
 
     const size_t vbase = (size_t)(b * HV + hv) * nch, kbase = (size_t)(b * HK + kh) * nch;
-    for (int c = 0; c < nch; c++) {
+    // operands of one chunk that do not depend on S; the next chunk's are requested while the
+    // current chunk computes (register double buffer), hiding the L2 / HBM latency
+    struct Ops {
+        half8 wa[4], qa[4], ia[2], ka[2][2];
+        f32x4 uu[2], ecum, edec;  // u fragment; e^{cum_i}, e^{cum_last - cum_i} for this lane's rows
+        float gamma;              // e^{cum_last}
+    };
+    auto fetch = [&](int c, Ops& o) {
         const size_t vu = vbase + c, ku = kbase + c;
         const half_t* Wc = (const half_t*)(ws + L.w) + vu * CH * D;
         const half_t* Qc = (const half_t*)(ws + L.qn) + ku * CH * D;
         const float* Uc = (const float*)(ws + L.u) + vu * CH * D;
         const half_t* Ic = (const half_t*)(ws + L.intra) + vu * CH * CH;
         const half_t* KTc = (const half_t*)(ws + L.knt) + ku * CH * D;
-        const float* cumc = (const float*)(ws + L.cum) + vu * CH;
-
-        // operands that do not depend on S: issue their loads first
-        half8 wa[4], qa[4], ia[2], ka[2][2];
+        const float* dec = (const float*)(ws + L.cum) + vu * 3 * CH;
 #pragma unroll
         for (int ks = 0; ks < 4; ks++) {
-            wa[ks] = ld_h8(Wc + (16 * wave + n) * D + 32 * ks + 8 * gq);
-            qa[ks] = ld_h8(Qc + (16 * wave + n) * D + 32 * ks + 8 * gq);
+            o.wa[ks] = ld_h8(Wc + (16 * wave + n) * D + 32 * ks + 8 * gq);
+            o.qa[ks] = ld_h8(Qc + (16 * wave + n) * D + 32 * ks + 8 * gq);
         }
 #pragma unroll
-        for (int ks = 0; ks < 2; ks++) ia[ks] = ld_h8(Ic + (16 * wave + n) * CH + 32 * ks + 8 * gq);
+        for (int ks = 0; ks < 2; ks++) o.ia[ks] = ld_h8(Ic + (16 * wave + n) * CH + 32 * ks + 8 * gq);
 #pragma unroll
         for (int rt = 0; rt < 2; rt++)
 #pragma unroll
-            for (int ks = 0; ks < 2; ks++) ka[rt][ks] = ld_h8(KTc + (32 * wave + 16 * rt + n) * CH + 32 * ks + 8 * gq);
-        f32x4 uu[2];
-        float cum_i[4];
+            for (int ks = 0; ks < 2; ks++) o.ka[rt][ks] = ld_h8(KTc + (32 * wave + 16 * rt + n) * CH + 32 * ks + 8 * gq);
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int i = 16 * wave + 4 * gq + j;
-            cum_i[j] = cumc[i];
-#pragma unroll
-            for (int ct = 0; ct < 2; ct++) uu[ct][j] = Uc[i * D + col0 + 16 * ct + n];
-        }
-        const float cum_last = cumc[CH - 1];
+        for (int ct = 0; ct < 2; ct++) o.uu[ct] = *(const f32x4*)(Uc + u_frag(16 * wave + 4 * gq, col0 + 16 * ct + n));
+        o.ecum = *(const f32x4*)(dec + 16 * wave + 4 * gq);
+        o.edec = *(const f32x4*)(dec + CH + 16 * wave + 4 * gq);
+        o.gamma = dec[2 * CH];
+    };
+    // per-chunk compute on operands `cur` (S-dependent part)
+    auto step = [&](int c, const Ops& cur) {
+        const half8* wa = cur.wa;
+        const half8* qa = cur.qa;
+        const half8* ia = cur.ia;
+        const f32x4* uu = cur.uu;
 
         // (1) S -> LDS as fp16, transposed
 #pragma unroll
@@ -328,7 +478,7 @@ __global__ void __launch_bounds__(256) delta_chunk_state(const unsigned char* __
                 const int i = 16 * wave + 4 * gq + j;
                 const float vn = uu[ct][j] - WS[ct][j];
                 VnT[16 * ct + n][i] = (half_t)vn;
-                VdT[16 * ct + n][i] = (half_t)(__expf(cum_last - cum_i[j]) * vn);
+                VdT[16 * ct + n][i] = (half_t)(cur.edec[j] * vn);
             }
         __syncthreads();
 
@@ -339,27 +489,57 @@ __global__ void __launch_bounds__(256) delta_chunk_state(const unsigned char* __
 #pragma unroll
             for (int ks = 0; ks < 2; ks++) o = mfma16(ia[ks], ld_h8(&VnT[16 * ct + n][32 * ks + 8 * gq]), o);
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const int i = 16 * wave + 4 * gq + j, tok = t0 + c * CH + i;
-                if (tok < T) {
-                    const float y = __expf(cum_i[j]) * QS[ct][j] + o[j];
-                    Act<Tout>::st(out, b * a.sb_o + (long long)tok * a.st_o + hv * a.sh_o + col0 + 16 * ct + n, y);
+            for (int j = 0; j < 4; j++) Ot[wave][4 * gq + j][16 * ct + n] = cur.ecum[j] * QS[ct][j] + o[j];
+        }
+        wave_sync();
+        {   // this wave's 16 rows x 32 columns: lane = (row, 8-column part)
+            const int r = lane / 4, p8 = (lane % 4) * 8, tok = t0 + c * CH + 16 * wave + r;
+            if (tok < T) {
+                Tout* dst = out + b * a.sb_o + (long long)tok * a.st_o + hv * a.sh_o + col0 + p8;
+                const float* src = &Ot[wave][r][p8];
+                if (vec_out) {
+                    if constexpr (sizeof(Tout) == 2) {
+                        uint4 pk;
+                        pk.x = (uint32_t)f2bf(src[0]) | ((uint32_t)f2bf(src[1]) << 16);
+                        pk.y = (uint32_t)f2bf(src[2]) | ((uint32_t)f2bf(src[3]) << 16);
+                        pk.z = (uint32_t)f2bf(src[4]) | ((uint32_t)f2bf(src[5]) << 16);
+                        pk.w = (uint32_t)f2bf(src[6]) | ((uint32_t)f2bf(src[7]) << 16);
+                        *(uint4*)dst = pk;
+                    } else {
+                        ((float4*)dst)[0] = float4{src[0], src[1], src[2], src[3]};
+                        ((float4*)dst)[1] = float4{src[4], src[5], src[6], src[7]};
+                    }
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 8; e++) Act<Tout>::st(dst, e, src[e]);
                 }
             }
         }
         // (5) S = e^{cum_last} S + k_n^T v'
-        const float gamma = __expf(cum_last);
+        const float gamma = cur.gamma;
 #pragma unroll
         for (int rt = 0; rt < 2; rt++)
 #pragma unroll
             for (int ct = 0; ct < 2; ct++) {
                 f32x4 acc = S[rt][ct] * gamma;
 #pragma unroll
-                for (int ks = 0; ks < 2; ks++) acc = mfma16(ka[rt][ks], ld_h8(&VdT[16 * ct + n][32 * ks + 8 * gq]), acc);
+                for (int ks = 0; ks < 2; ks++) acc = mfma16(cur.ka[rt][ks], ld_h8(&VdT[16 * ct + n][32 * ks + 8 * gq]), acc);
                 S[rt][ct] = acc;
             }
         __syncthreads();  // SsT / VnT / VdT are rewritten by the next chunk
+    };
+    // ping-pong between two operand sets (no register copies, so the wait for a prefetch only
+    // covers the loads issued before it)
+    Ops A, Bo;
+    fetch(0, A);
+    int c = 0;
+    for (; c + 1 < nch; c += 2) {
+        fetch(c + 1, Bo);
+        step(c, A);
+        fetch(min(c + 2, nch - 1), A);  // unconditional: keeps the wait counts static
+        step(c + 1, Bo);
     }
+    if (c < nch) step(c, A);
 #pragma unroll
     for (int rt = 0; rt < 2; rt++)
 #pragma unroll
@@ -389,6 +569,14 @@ int run_chunked(const Tin* q, const Tin* k, const Tin* v, const float* g, const 
     unsigned char* w = (unsigned char*)ws;
     // the carried state: the caller's, or the workspace copy (starts at zero: K2 does not load it)
     float* S = state ? state : (float*)(w + L.state);
+    // 16-byte input loads need 16-byte aligned rows (and 8-element runs)
+    const long long ei = 16 / (long long)sizeof(Tin);
+    const int vec_in = ((uintptr_t)q % 16 == 0) && ((uintptr_t)k % 16 == 0) && ((uintptr_t)v % 16 == 0) &&
+                       a.sb_qk % ei == 0 && a.st_qk % ei == 0 && a.sh_qk % ei == 0 && a.sb_v % ei == 0 &&
+                       a.st_v % ei == 0 && a.sh_v % ei == 0;
+    // 16-byte output stores need 16-byte aligned rows
+    const long long ev = 16 / (long long)sizeof(Tout);
+    const int vec_out = ((uintptr_t)out % 16 == 0) && a.sb_o % ev == 0 && a.st_o % ev == 0 && a.sh_o % ev == 0;
     int load = state ? 1 : 0;
     for (int t0 = 0; t0 < T; t0 += SEG) {
         const int len = std::min(SEG, T - t0);
@@ -396,10 +584,10 @@ int run_chunked(const Tin* q, const Tin* k, const Tin* v, const float* g, const 
         WsLayout Ls = ws_layout(B, HK, HV, nch);
         Ls.state = L.state;
         delta_chunk_intra<Tin><<<dim3(nch, HV, B), 256, 0, st>>>(q, k, v, g, beta, a, t0, T, HK, HV, normalize, qscale,
-                                                               eps, w, Ls);
+                                                               eps, w, Ls, vec_in);
         int rc = after_launch("delta_chunk_intra");
         if (rc) return rc;
-        delta_chunk_state<Tout><<<dim3(NSL, HV, B), 256, 0, st>>>(w, Ls, S, load, out, a, t0, T, nch, HK, HV);
+        delta_chunk_state<Tout><<<dim3(NSL, HV, B), 256, 0, st>>>(w, Ls, S, load, out, a, t0, T, nch, HK, HV, vec_out);
         rc = after_launch("delta_chunk_state");
         if (rc) return rc;
         load = 1;
