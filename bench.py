@@ -110,6 +110,10 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="also run a 1 GiB device copy (calibrates rocprof FETCH_SIZE / WRITE_SIZE)")
+    ap.add_argument("--traffic", type=str, default=str(ROOT / "profiles" / "delta_decode_traffic.json"),
+                    help="JSON file with measured HBM bytes per decode launch (from rocprof --pmc)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the mixer path is not "
@@ -183,7 +187,15 @@ def main():
                      "launch_us": round(launch_ms * 1e3, 2)},
         "wall_s": round(wall, 3),
     }
+    if args.traffic and os.path.exists(args.traffic):
+        with open(args.traffic) as f:
+            res["roofline"]["traffic"] = json.load(f).get("bytes_per_launch")
     res["prefill"] = bench_prefill(torch, ops, dev)
+    if args.calib_copy:
+        src = torch.empty(1 << 28, device=dev)  # 1 GiB fp32
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
     if not args.no_cpu:
         res["cpu_baseline"] = cpu_baseline_decode(torch)
     print(json.dumps(res), flush=True)
