@@ -34,7 +34,9 @@ namespace {
 constexpr int D = 128;
 constexpr int CH = 64;       // chunk length
 constexpr int SEG = 2048;    // tokens per segment (workspace granularity)
-constexpr int NSL = 4;       // 32-column slices of S per value head in K2
+#ifndef K2_NCT
+#define K2_NCT 1              // 16-column tiles per K2 workgroup (1: 8 workgroups per value head)
+#endif
 constexpr int QK_LD = D + 8; // fp16 row stride (elements) of the q/k tiles in LDS
 constexpr int A_LD = 68;     // fp32 row stride of the A matrix in LDS (16-byte aligned rows)
 
@@ -381,29 +383,37 @@ __global__ void __launch_bounds__(256) delta_chunk_intra(const Tin* __restrict__
 }
 
 // ---------------------------------------------------------------------------------------------
-// K2: sequential recurrence over the chunks of a segment. grid (NSL, HV, B), 256 threads.
-// Wave w holds S rows [32w, 32w+32) x the slice's 32 columns as 2x2 MFMA tiles.
-template <typename Tout>
+// K2: sequential recurrence over the chunks of a segment. 1-D grid of (B HV rounded up to 8) x
+// 128 / (16 NCT) blocks, 256 threads.
+// Wave w holds S rows [32w, 32w+32) x the slice's 16 NCT columns as 2 x NCT MFMA tiles.
+template <typename Tout, int NCT>
 __global__ void __launch_bounds__(256) delta_chunk_state(const unsigned char* __restrict__ ws, WsLayout L,
                                                          float* __restrict__ state, int load_state, Tout* __restrict__ out,
-                                                         SeqLayout a, int t0, int T, int nch, int HK, int HV,
-                                                         int vec_out) {
-    __shared__ __attribute__((aligned(16))) half_t SsT[32][D + 8];   // S^T (fp16): [column][dk]
-    __shared__ __attribute__((aligned(16))) half_t VnT[32][CH + 8];  // v_new^T (fp16)
-    __shared__ __attribute__((aligned(16))) half_t VdT[32][CH + 8];  // (e^{cum_last-cum} v_new)^T
-    __shared__ float Ot[4][16][36];                                     // output staging per wave
+                                                         SeqLayout a, int t0, int T, int nch, int B, int HK,
+                                                         int HV, int vec_out) {
+    __shared__ __attribute__((aligned(16))) half_t SsT[16 * NCT][D + 8];   // S^T (fp16): [column][dk]
+    __shared__ __attribute__((aligned(16))) half_t VnT[16 * NCT][CH + 8];  // v_new^T (fp16)
+    __shared__ __attribute__((aligned(16))) half_t VdT[16 * NCT][CH + 8];  // (e^{cum_last-cum} v_new)^T
+    __shared__ float Ot[4][16][16 * NCT + 4];                                     // output staging per wave
 
-    const int sl = blockIdx.x, hv = blockIdx.y, b = blockIdx.z;
+    // XCD-aware block mapping (1-D grid): blocks are dealt to the 8 XCDs round-robin, so unit
+    // u = (m / NS) * 8 + xcd keeps all NS column slices of one (sequence, head) on one XCD,
+    // where they share the chunk operands in that XCD's L2.
+    constexpr int NS = D / (16 * NCT);
+    const int Lb = blockIdx.x, xcd = Lb % 8, m = Lb / 8;
+    const int unit = (m / NS) * 8 + xcd, sl = m % NS;
+    if (unit >= B * HV) return;  // grid padded to a multiple of 8 units
+    const int hv = unit % HV, b = unit / HV;
     const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE, n = lane % 16, gq = lane / 16;
     const int R = HV / HK, kh = hv / R;
-    const int col0 = sl * 32;
+    const int col0 = sl * 16 * NCT;
     float* Sg = state + (size_t)(b * HV + hv) * D * D;
 
-    f32x4 S[2][2];
+    f32x4 S[2][NCT];
 #pragma unroll
     for (int rt = 0; rt < 2; rt++)
 #pragma unroll
-        for (int ct = 0; ct < 2; ct++)
+        for (int ct = 0; ct < NCT; ct++)
 #pragma unroll
             for (int j = 0; j < 4; j++)
                 S[rt][ct][j] = load_state ? Sg[(size_t)(32 * wave + 16 * rt + 4 * gq + j) * D + col0 + 16 * ct + n] : 0.f;
@@ -413,7 +423,7 @@ __global__ void __launch_bounds__(256) delta_chunk_state(const unsigned char* __
     // current chunk computes (register double buffer), hiding the L2 / HBM latency
     struct Ops {
         half8 wa[4], qa[4], ia[2], ka[2][2];
-        f32x4 uu[2], ecum, edec;  // u fragment; e^{cum_i}, e^{cum_last - cum_i} for this lane's rows
+        f32x4 uu[NCT], ecum, edec;  // u fragment; e^{cum_i}, e^{cum_last - cum_i} for this lane's rows
         float gamma;              // e^{cum_last}
     };
     auto fetch = [&](int c, Ops& o) {
@@ -436,7 +446,7 @@ __global__ void __launch_bounds__(256) delta_chunk_state(const unsigned char* __
 #pragma unroll
             for (int ks = 0; ks < 2; ks++) o.ka[rt][ks] = ld_h8(KTc + (32 * wave + 16 * rt + n) * CH + 32 * ks + 8 * gq);
 #pragma unroll
-        for (int ct = 0; ct < 2; ct++) o.uu[ct] = *(const f32x4*)(Uc + u_frag(16 * wave + 4 * gq, col0 + 16 * ct + n));
+        for (int ct = 0; ct < NCT; ct++) o.uu[ct] = *(const f32x4*)(Uc + u_frag(16 * wave + 4 * gq, col0 + 16 * ct + n));
         o.ecum = *(const f32x4*)(dec + 16 * wave + 4 * gq);
         o.edec = *(const f32x4*)(dec + CH + 16 * wave + 4 * gq);
         o.gamma = dec[2 * CH];
@@ -452,15 +462,15 @@ __global__ void __launch_bounds__(256) delta_chunk_state(const unsigned char* __
 #pragma unroll
         for (int rt = 0; rt < 2; rt++)
 #pragma unroll
-            for (int ct = 0; ct < 2; ct++)
+            for (int ct = 0; ct < NCT; ct++)
 #pragma unroll
                 for (int j = 0; j < 4; j++) SsT[16 * ct + n][32 * wave + 16 * rt + 4 * gq + j] = (half_t)S[rt][ct][j];
         __syncthreads();
 
         // (2) w S and q_n S for chunk rows [16 wave, 16 wave + 16)
-        f32x4 WS[2], QS[2];
+        f32x4 WS[NCT], QS[NCT];
 #pragma unroll
-        for (int ct = 0; ct < 2; ct++) {
+        for (int ct = 0; ct < NCT; ct++) {
             WS[ct] = f32x4{0.f, 0.f, 0.f, 0.f};
             QS[ct] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -472,7 +482,7 @@ __global__ void __launch_bounds__(256) delta_chunk_state(const unsigned char* __
         }
         // (3) v_new = u - w S; decayed copy for the state update
 #pragma unroll
-        for (int ct = 0; ct < 2; ct++)
+        for (int ct = 0; ct < NCT; ct++)
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 const int i = 16 * wave + 4 * gq + j;
@@ -484,7 +494,7 @@ __global__ void __launch_bounds__(256) delta_chunk_state(const unsigned char* __
 
         // (4) o = e^{cum} q_n S + intra v_new
 #pragma unroll
-        for (int ct = 0; ct < 2; ct++) {
+        for (int ct = 0; ct < NCT; ct++) {
             f32x4 o = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int ks = 0; ks < 2; ks++) o = mfma16(ia[ks], ld_h8(&VnT[16 * ct + n][32 * ks + 8 * gq]), o);
@@ -492,9 +502,10 @@ __global__ void __launch_bounds__(256) delta_chunk_state(const unsigned char* __
             for (int j = 0; j < 4; j++) Ot[wave][4 * gq + j][16 * ct + n] = cur.ecum[j] * QS[ct][j] + o[j];
         }
         wave_sync();
-        {   // this wave's 16 rows x 32 columns: lane = (row, 8-column part)
-            const int r = lane / 4, p8 = (lane % 4) * 8, tok = t0 + c * CH + 16 * wave + r;
-            if (tok < T) {
+        {   // this wave's 16 rows x 16 NCT columns: lane = (row, 8-column part)
+            constexpr int LPR = 2 * NCT;  // lanes per row
+            const int r = lane / LPR, p8 = (lane % LPR) * 8, tok = t0 + c * CH + 16 * wave + r;
+            if (r < 16 && tok < T) {
                 Tout* dst = out + b * a.sb_o + (long long)tok * a.st_o + hv * a.sh_o + col0 + p8;
                 const float* src = &Ot[wave][r][p8];
                 if (vec_out) {
@@ -520,7 +531,7 @@ __global__ void __launch_bounds__(256) delta_chunk_state(const unsigned char* __
 #pragma unroll
         for (int rt = 0; rt < 2; rt++)
 #pragma unroll
-            for (int ct = 0; ct < 2; ct++) {
+            for (int ct = 0; ct < NCT; ct++) {
                 f32x4 acc = S[rt][ct] * gamma;
 #pragma unroll
                 for (int ks = 0; ks < 2; ks++) acc = mfma16(cur.ka[rt][ks], ld_h8(&VdT[16 * ct + n][32 * ks + 8 * gq]), acc);
@@ -543,7 +554,7 @@ __global__ void __launch_bounds__(256) delta_chunk_state(const unsigned char* __
 #pragma unroll
     for (int rt = 0; rt < 2; rt++)
 #pragma unroll
-        for (int ct = 0; ct < 2; ct++)
+        for (int ct = 0; ct < NCT; ct++)
 #pragma unroll
             for (int j = 0; j < 4; j++) Sg[(size_t)(32 * wave + 16 * rt + 4 * gq + j) * D + col0 + 16 * ct + n] = S[rt][ct][j];
 }
@@ -587,7 +598,9 @@ int run_chunked(const Tin* q, const Tin* k, const Tin* v, const float* g, const 
                                                                eps, w, Ls, vec_in);
         int rc = after_launch("delta_chunk_intra");
         if (rc) return rc;
-        delta_chunk_state<Tout><<<dim3(NSL, HV, B), 256, 0, st>>>(w, Ls, S, load, out, a, t0, T, nch, HK, HV, vec_out);
+        const int units8 = (B * HV + 7) / 8 * 8;
+        delta_chunk_state<Tout, K2_NCT><<<units8 * (D / (16 * K2_NCT)), 256, 0, st>>>(w, Ls, S, load, out, a, t0, T,
+                                                                                  nch, B, HK, HV, vec_out);
         rc = after_launch("delta_chunk_state");
         if (rc) return rc;
         load = 1;
