@@ -28,7 +28,8 @@ namespace aegist {
 struct RopeTable;
 int launch_attn_prep(const void* qg, const void* k, const void* v, int in_dtype, const uint16_t* qw,
                      const uint16_t* kw, float* qn, uint16_t* kc, uint16_t* vc, int B, int T, int H, int KV, int HD,
-                     int RD, int pos0, int cap, float eps, float theta, hipStream_t stream);
+                     int RD, int pos0, int cap, float eps, float theta, hipStream_t stream, int* zero_ctr,
+                     int n_ctr);
 }  // namespace aegist
 
 namespace {
@@ -41,12 +42,13 @@ struct DecodeSplit {
     int nsplit, per_split;
 };
 
-// Splits sized so a launch has about 2048 workgroups, each split a multiple of 128 keys
-// (one 32-key tile per wave per step).
+// Splits sized so a launch has about 256 workgroups (one round of one workgroup per CU: the
+// kernel runs one wave per SIMD), each split a multiple of 128 keys (one 32-key tile per wave
+// per step), at most 256 splits per (sequence, KV head).
 DecodeSplit choose_split(int B, int KV, int L) {
     int units = std::max(1, B * KV);
-    int max_split = std::max(1, (L + 127) / 128);
-    int ns = std::min(max_split, std::max(1, (2048 + units - 1) / units));
+    int max_split = std::min(256, std::max(1, (L + 127) / 128));
+    int ns = std::min(max_split, std::max(1, (256 + units - 1) / units));
     int per = (L + ns - 1) / ns;
     per = (per + 127) / 128 * 128;
     ns = (L + per - 1) / per;
@@ -66,19 +68,71 @@ struct GateLd {
     static __device__ __forceinline__ float ld(const TG* p, size_t i) { return Act<TG>::ld(p, i); }
 };
 
+// Combine the nsplit (<= 256) partial results of one (sequence, KV head) for its G query heads:
+// y = (sum_s e^{m_s - M} O_s) / (sum_s e^{m_s - M} l_s) * sigmoid(gate). 256 threads: one
+// thread per split for the max / weights (in LDS), one thread per output dim for the sum.
+template <typename TG, typename Tout>
+__device__ void merge_splits(const float* __restrict__ part, const float* __restrict__ ml, size_t base, int nsplit,
+                             int G, const TG* __restrict__ gate, long long gate_stride, Tout* __restrict__ out,
+                             long long out_stride, size_t row0) {
+    __shared__ float fw[256];
+    __shared__ float red[2][4];
+    const int tid = threadIdx.x, lane = tid % WAVE, w = tid / WAVE;
+    for (int rr = 0; rr < G; rr++) {
+        const size_t pi = (base + tid) * G + rr;
+        const float m = tid < nsplit ? ml[pi * 2] : -INFINITY;
+        const float l = tid < nsplit ? ml[pi * 2 + 1] : 0.f;
+        float mx = wave_max(m);
+        if (lane == 0) red[0][w] = mx;
+        __syncthreads();
+        mx = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
+        const float f = m == -INFINITY ? 0.f : __expf(m - mx);
+        fw[tid] = f;
+        float ls = wave_sum(f * l);
+        if (lane == 0) red[1][w] = ls;
+        __syncthreads();
+        ls = red[1][0] + red[1][1] + red[1][2] + red[1][3];
+        float acc = 0.f;
+        int s = 0;
+        for (; s + 8 <= nsplit; s += 8) {
+            float v[8];
+#pragma unroll
+            for (int e = 0; e < 8; e++) v[e] = part[((base + s + e) * G + rr) * HD + tid];
+#pragma unroll
+            for (int e = 0; e < 8; e++) acc += v[e] * fw[s + e];
+        }
+        for (; s < nsplit; s++) acc += part[((base + s) * G + rr) * HD + tid] * fw[s];
+        const size_t row = row0 + rr;
+        float y = acc / ls;
+        if (gate) y *= sigmoid_f(Act<TG>::ld(gate, row * gate_stride + tid));
+        Act<Tout>::st(out, row * out_stride + tid, y);
+        __syncthreads();  // fw / red reused by the next head
+    }
+}
+
 // q:   [B, H, HD] fp32 (normed, roped), head h of KV head kvh is kvh*G + r
 // kc, vc: [B, KV, cap, HD] bf16
 // part: [B, KV, nsplit, G, HD] fp32 partial outputs (unnormalised), ml: [B, KV, nsplit, G, 2]
+// With `counters` set, the last workgroup of each (sequence, KV head) to finish merges all
+// splits and writes the gated output (the counter is zeroed by the prep kernel that runs
+// first and reset by that last workgroup); otherwise attn_decode_merge_kernel does it.
+template <typename TG, typename Tout>
 __global__ void __launch_bounds__(256) attn_decode_split_kernel(const float* __restrict__ q,
                                                                 const uint16_t* __restrict__ kc,
                                                                 const uint16_t* __restrict__ vc,
                                                                 float* __restrict__ part, float* __restrict__ ml,
                                                                 int H, int KV, int L, int cap, int per_split,
-                                                                float scale) {
-    __shared__ __attribute__((aligned(16))) unsigned char vbuf[4][TILE * VROW];
+                                                                float scale, int* __restrict__ counters,
+                                                                const TG* __restrict__ gate, long long gate_stride,
+                                                                Tout* __restrict__ out, long long out_stride) {
+    // V staging per wave during the loop; the 4-wave merge buffer reuses the same bytes after it
+    __shared__ __attribute__((aligned(16))) unsigned char vbuf_raw[4 * TILE * VROW];
+    __shared__ __attribute__((aligned(16))) unsigned char kbuf[4][TILE * VROW];
     __shared__ __attribute__((aligned(16))) uint16_t pbuf[4][16][TILE];
     __shared__ float wm[4][8], wl[4][8];
-    __shared__ float wo[4][8][HD];
+    unsigned char (*vbuf)[TILE * VROW] = (unsigned char (*)[TILE * VROW])vbuf_raw;
+    float (*wo)[8][HD] = (float (*)[8][HD])vbuf_raw;
+    static_assert(4 * 8 * HD * 4 <= 4 * TILE * VROW, "merge buffer fits in the V staging area");
 
     const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z, nsplit = gridDim.x;
     const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
@@ -120,32 +174,46 @@ __global__ void __launch_bounds__(256) attn_decode_split_kernel(const float* __r
     for (int i = 0; i < 16; i++) oacc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     unsigned char* vb = vbuf[wave];
-    for (int t0 = k0 + wave * TILE; t0 < k1; t0 += 4 * TILE) {
-        // ---- stage V tile rows t0..t0+31 into LDS (rows past the end are zero)
+    unsigned char* kb_l = kbuf[wave];
+    // The next tile's K and V rows (16 bytes per lane per step, 32 steps) are held in registers,
+    // requested a full tile ahead, and written to the wave's LDS staging at the top of the next
+    // iteration. Rows past the split are clamped to its last row (finite data, probability 0).
+    constexpr int NST = (TILE * HD * 2) / (16 * WAVE);  // 16 steps per tensor
+    uint4 kreg[NST], vreg[NST];
+    auto fetch = [&](int t0) {
 #pragma unroll
-        for (int it = 0; it < (TILE * HD * 2) / (16 * WAVE); it++) {  // 16 iterations
-            int idx = it * WAVE + lane;       // 16-byte chunk index
-            int row = idx / (HD * 2 / 16);    // 32 chunks per row
-            int cc = idx % (HD * 2 / 16);
-            int key = t0 + row;
-            uint4 val = {0u, 0u, 0u, 0u};
-            if (key < k1) val = *(const uint4*)(vbase + (size_t)key * HD + cc * 8);
-            uint2* dst = (uint2*)(vb + row * VROW + cc * 16);
-            dst[0] = uint2{val.x, val.y};
-            dst[1] = uint2{val.z, val.w};
+        for (int it = 0; it < NST; it++) {
+            const int idx = it * WAVE + lane, row = idx / (HD * 2 / 16), cc = idx % (HD * 2 / 16);
+            const int key = min(t0 + row, k1 - 1);
+            kreg[it] = *(const uint4*)(kbase + (size_t)key * HD + cc * 8);
+            vreg[it] = *(const uint4*)(vbase + (size_t)key * HD + cc * 8);
         }
+    };
+    const int first = k0 + wave * TILE, stride = 4 * TILE;
+    if (first < k1) fetch(first);
+    for (int t0 = first; t0 < k1; t0 += stride) {
+#pragma unroll
+        for (int it = 0; it < NST; it++) {
+            const int idx = it * WAVE + lane, row = idx / (HD * 2 / 16), cc = idx % (HD * 2 / 16);
+            uint2* dv = (uint2*)(vb + row * VROW + cc * 16);
+            dv[0] = uint2{vreg[it].x, vreg[it].y};
+            dv[1] = uint2{vreg[it].z, vreg[it].w};
+            uint2* dk = (uint2*)(kb_l + row * VROW + cc * 16);
+            dk[0] = uint2{kreg[it].x, kreg[it].y};
+            dk[1] = uint2{kreg[it].z, kreg[it].w};
+        }
+        fetch(min(t0 + stride, k1 - 1));  // next tile (unconditional: static wait counts)
         wave_sync();
         // ---- scores: two 16-key blocks
         f32x4 sc[2];
 #pragma unroll
         for (int nb = 0; nb < 2; nb++) {
             int key = t0 + nb * 16 + n;
-            int kr = key < k1 ? key : k1 - 1;
-            const uint16_t* krow = kbase + (size_t)kr * HD + 8 * g;
+            const unsigned char* krow = kb_l + (nb * 16 + n) * VROW + 16 * g;
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int ks = 0; ks < 8; ks++) {
-                bf16x8 kb = *(const bf16x8*)(krow + ks * 32);
+                bf16x8 kb = *(const bf16x8*)(krow + ks * 64);
                 acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[ks], kb, acc, 0, 0, 0);
             }
             // rows 4g+j; combine hi (g<2) and lo (g>=2) parts: lane g and g^2 hold h and h+8
@@ -210,6 +278,7 @@ __global__ void __launch_bounds__(256) attn_decode_split_kernel(const float* __r
         }
         wave_sync();  // this tile's LDS reads complete before the next tile overwrites
     }
+    __syncthreads();  // all waves done with their V staging before the merge reuses it
 
     // ---- combine hi/lo rows and reduce l over the 16 key lanes
 #pragma unroll
@@ -267,30 +336,29 @@ __global__ void __launch_bounds__(256) attn_decode_split_kernel(const float* __r
             ml[pidx * 2 + 1] = Lsum;
         }
     }
+    if (counters == nullptr) return;
+    // ---- fused split merge: the last workgroup of this (b, kvh) combines every split
+    __shared__ int last;
+    __threadfence();
+    __syncthreads();
+    if (tid == 0) last = atomicAdd(&counters[b * KV + kvh], 1) == nsplit - 1;
+    __syncthreads();
+    if (!last) return;
+    __threadfence();
+    merge_splits<TG, Tout>(part, ml, ((size_t)b * KV + kvh) * nsplit, nsplit, G, gate, gate_stride, out, out_stride,
+                           (size_t)b * H + kvh * G);
+    if (tid == 0) counters[b * KV + kvh] = 0;
 }
 
-// out[b, h, :] = (sum_s e^{m_s - M} O_s) / (sum_s e^{m_s - M} l_s) * sigmoid(gate)
+// Standalone split merge (used when no counters are available): one block per (b, kvh).
 template <typename TG, typename Tout>
 __global__ void __launch_bounds__(256) attn_decode_merge_kernel(const float* __restrict__ part,
                                                                 const float* __restrict__ ml, const TG* __restrict__ gate,
                                                                 long long gate_row_stride, Tout* __restrict__ out,
                                                                 long long out_row_stride, int H, int KV, int nsplit) {
-    const int bh = blockIdx.x, b = bh / H, h = bh % H, G = H / KV, kvh = h / G, r = h % G;
-    const int d = threadIdx.x;
-    const size_t base = ((size_t)b * KV + kvh) * nsplit;
-    float M = -INFINITY;
-    for (int s = 0; s < nsplit; s++) M = fmaxf(M, ml[((base + s) * G + r) * 2]);
-    float Lsum = 0.f, acc = 0.f;
-    for (int s = 0; s < nsplit; s++) {
-        size_t pidx = (base + s) * G + r;
-        float m = ml[pidx * 2];
-        float f = m == -INFINITY ? 0.f : __expf(m - M);
-        Lsum += ml[pidx * 2 + 1] * f;
-        acc += part[pidx * HD + d] * f;
-    }
-    float y = acc / Lsum;
-    if (gate) y *= sigmoid_f(Act<TG>::ld(gate, (size_t)bh * gate_row_stride + d));
-    Act<Tout>::st(out, (size_t)bh * out_row_stride + d, y);
+    const int u = blockIdx.x, b = u / KV, kvh = u % KV, G = H / KV;
+    merge_splits<TG, Tout>(part, ml, (size_t)u * nsplit, nsplit, G, gate, gate_row_stride, out, out_row_stride,
+                           (size_t)b * H + kvh * G);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -353,15 +421,16 @@ size_t decode_workspace_bytes(int B, int H, int KV, int L, bool with_q) {
     size_t part = (size_t)B * KV * sp.nsplit * G * HD * 4;
     size_t ml = (size_t)B * KV * sp.nsplit * G * 2 * 4;
     size_t qb = with_q ? (size_t)B * H * HD * 4 : 0;
+    size_t cnt = with_q ? (size_t)B * KV * 4 : 0;
     auto al = [](size_t x) { return (x + 255) / 256 * 256; };
-    return al(part) + al(ml) + al(qb);
+    return al(part) + al(ml) + al(qb) + al(cnt);
 }
 
 // q [B, H, HD] fp32 -> out rows (b*H + h) * out_row_stride, gate rows (b*H + h) * gate_row_stride
 template <typename TG, typename Tout>
 int launch_decode_core(const float* q, const uint16_t* kc, const uint16_t* vc, const TG* gate, long long gate_stride,
                        Tout* out, long long out_stride, int B, int H, int KV, int L, int cap, float scale,
-                       void* ws, size_t ws_bytes, hipStream_t st) {
+                       void* ws, size_t ws_bytes, hipStream_t st, int* counters = nullptr) {
     if (KV <= 0 || H % KV || H / KV > 8) return fail(AEGIST_ERR_SHAPE, "attention decode: need H % KV == 0 and H/KV <= 8");
     if (L <= 0 || L > cap) return fail(AEGIST_ERR_SHAPE, "attention decode: need 0 < L <= cap");
     DecodeSplit sp = choose_split(B, KV, L);
@@ -371,12 +440,12 @@ int launch_decode_core(const float* q, const uint16_t* kc, const uint16_t* vc, c
     float* part = (float*)ws;
     size_t part_bytes = ((size_t)B * KV * sp.nsplit * G * HD * 4 + 255) / 256 * 256;
     float* ml = (float*)((char*)ws + part_bytes);
-    attn_decode_split_kernel<<<dim3(sp.nsplit, KV, B), 256, 0, st>>>(q, kc, vc, part, ml, H, KV, L, cap, sp.per_split,
-                                                                      scale);
+    attn_decode_split_kernel<TG, Tout><<<dim3(sp.nsplit, KV, B), 256, 0, st>>>(
+        q, kc, vc, part, ml, H, KV, L, cap, sp.per_split, scale, counters, gate, gate_stride, out, out_stride);
     int rc = after_launch("attention_decode_split");
-    if (rc) return rc;
-    attn_decode_merge_kernel<TG, Tout><<<B * H, HD, 0, st>>>(part, ml, gate, gate_stride, out, out_stride, H, KV,
-                                                             sp.nsplit);
+    if (rc || counters) return rc;
+    attn_decode_merge_kernel<TG, Tout><<<B * KV, 256, 0, st>>>(part, ml, gate, gate_stride, out, out_stride, H, KV,
+                                                               sp.nsplit);
     return after_launch("attention_decode_merge");
 }
 
@@ -412,8 +481,9 @@ int aegist_attention_decode(const void* qg, const void* k_new, const void* v_new
     hipStream_t st = AEG_STREAM(stream);
     size_t core = decode_workspace_bytes(B, H, KV, pos + 1, false);
     float* qn = (float*)((char*)workspace + core);
+    int* ctr = (int*)((char*)qn + ((size_t)B * H * HD * 4 + 255) / 256 * 256);
     int rc = launch_attn_prep(qg, k_new, v_new, in_dtype, q_norm_w, k_norm_w, qn, kc, vc, B, 1, H, KV, HD, RD, pos, cap,
-                              eps, theta, st);
+                              eps, theta, st, ctr, B * KV);
     if (rc) return rc;
     const float scale = 1.0f / sqrtf((float)HD);
     // gate = second half of each head's 2*HD row of qg
@@ -421,18 +491,18 @@ int aegist_attention_decode(const void* qg, const void* k_new, const void* v_new
         const float* gate = (const float*)qg + HD;
         if (out_dtype == AEGIST_F32)
             return launch_decode_core<float, float>(qn, kc, vc, gate, 2 * HD, (float*)out, HD, B, H, KV, pos + 1, cap,
-                                                    scale, workspace, core, st);
+                                                    scale, workspace, core, st, ctr);
         if (out_dtype == AEGIST_BF16)
             return launch_decode_core<float, uint16_t>(qn, kc, vc, gate, 2 * HD, (uint16_t*)out, HD, B, H, KV, pos + 1,
-                                                       cap, scale, workspace, core, st);
+                                                       cap, scale, workspace, core, st, ctr);
     } else if (in_dtype == AEGIST_BF16) {
         const uint16_t* gate = (const uint16_t*)qg + HD;
         if (out_dtype == AEGIST_F32)
             return launch_decode_core<uint16_t, float>(qn, kc, vc, gate, 2 * HD, (float*)out, HD, B, H, KV, pos + 1,
-                                                       cap, scale, workspace, core, st);
+                                                       cap, scale, workspace, core, st, ctr);
         if (out_dtype == AEGIST_BF16)
             return launch_decode_core<uint16_t, uint16_t>(qn, kc, vc, gate, 2 * HD, (uint16_t*)out, HD, B, H, KV,
-                                                          pos + 1, cap, scale, workspace, core, st);
+                                                          pos + 1, cap, scale, workspace, core, st, ctr);
     }
     return fail(AEGIST_ERR_DTYPE, "attention_decode: dtypes must be AEGIST_F32 or AEGIST_BF16");
 }

@@ -104,6 +104,55 @@ def bench_prefill(torch, ops, dev, reps=10):
             "mfma_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), "flop_per_call": flops}
 
 
+ATTN_H, ATTN_KV, ATTN_HD, ATTN_RD, ATTN_THETA = 16, 2, 256, 64, 1e7
+
+
+def bench_attention_decode(torch, ops, dev, reps=20):
+    """Config 3: gated GQA decode (ZNorm + RoPE of q and the new k, cache append, split-K
+    attention over L+1 rows, sigmoid gate) at L in {4k, 32k, 128k} x B in {1, 8, 32}.
+    Bytes per call = 2048 B L (bf16 K and V) + q/gate/new k, v/out."""
+    from aegist_mixer._lib import BF16, call, lib
+    out = []
+    bf = torch.bfloat16
+    stream = torch.cuda.current_stream().cuda_stream
+    for L in (4096, 32768, 131072):
+        for Bt in (1, 8, 32):
+            cap = L + 1
+            kc = ops.fill_normal(torch.empty(Bt, ATTN_KV, cap, ATTN_HD, device=dev, dtype=bf), 8001)
+            vc = ops.fill_normal(torch.empty(Bt, ATTN_KV, cap, ATTN_HD, device=dev, dtype=bf), 8002)
+            qg = ops.fill_normal(torch.empty(Bt, ATTN_H, 2 * ATTN_HD, device=dev, dtype=bf), 8003)
+            kn = ops.fill_normal(torch.empty(Bt, ATTN_KV, ATTN_HD, device=dev, dtype=bf), 8004)
+            vn = ops.fill_normal(torch.empty(Bt, ATTN_KV, ATTN_HD, device=dev, dtype=bf), 8005)
+            qw = torch.zeros(ATTN_HD, device=dev, dtype=bf)
+            kw = torch.zeros(ATTN_HD, device=dev, dtype=bf)
+            o = torch.empty(Bt, ATTN_H, ATTN_HD, device=dev, dtype=bf)
+            nbytes = lib().aegist_attention_decode_workspace_bytes(Bt, ATTN_H, ATTN_KV, L + 1)
+            ws = torch.empty(nbytes, device=dev, dtype=torch.uint8)
+
+            def run():
+                call("aegist_attention_decode", qg.data_ptr(), kn.data_ptr(), vn.data_ptr(), BF16, qw.data_ptr(),
+                     kw.data_ptr(), kc.data_ptr(), vc.data_ptr(), o.data_ptr(), BF16, Bt, ATTN_H, ATTN_KV, ATTN_HD,
+                     ATTN_RD, L, cap, 1e-6, ATTN_THETA, ws.data_ptr(), nbytes, stream)
+            for _ in range(3):
+                run()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(reps):
+                run()
+            e1.record()
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) * 1e3 / reps
+            byt = 2048 * Bt * (L + 1) + Bt * ATTN_H * ATTN_HD * 2 * 3 + Bt * ATTN_KV * ATTN_HD * 2 * 2
+            gbs = byt / (us * 1e-6) / 1e9
+            out.append({"L": L, "B": Bt, "us": round(us, 2), "tok_s": round(Bt / (us * 1e-6), 1),
+                        "GB_s": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)})
+            del kc, vc, ws
+            torch.cuda.empty_cache()
+    return {"workload": "config3: gated GQA decode, 16 q heads / 2 KV heads, HD 256, bf16 cache", "points": out,
+            "note": "L=4096 at B=1 (8 MB) is MALL-resident and launch-bound"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -191,6 +240,7 @@ def main():
         with open(args.traffic) as f:
             res["roofline"]["traffic"] = json.load(f).get("bytes_per_launch")
     res["prefill"] = bench_prefill(torch, ops, dev)
+    res["attention_decode"] = bench_attention_decode(torch, ops, dev)
     if args.calib_copy:
         src = torch.empty(1 << 28, device=dev)  # 1 GiB fp32
         dst = torch.empty_like(src)
