@@ -68,45 +68,66 @@ struct GateLd {
     static __device__ __forceinline__ float ld(const TG* p, size_t i) { return Act<TG>::ld(p, i); }
 };
 
-// Combine the nsplit (<= 256) partial results of one (sequence, KV head) for its G query heads:
-// y = (sum_s e^{m_s - M} O_s) / (sum_s e^{m_s - M} l_s) * sigmoid(gate). 256 threads: one
-// thread per split for the max / weights (in LDS), one thread per output dim for the sum.
+// Combine the nsplit (<= 256) partial results of one (sequence, KV head) for its G <= 8 query
+// heads: y = (sum_s e^{m_s - M} O_s) / (sum_s e^{m_s - M} l_s) * sigmoid(gate). 256 threads =
+// 8 heads x 32 threads; every head is merged at once (thread = 8 output dims), weights in LDS.
 template <typename TG, typename Tout>
 __device__ void merge_splits(const float* __restrict__ part, const float* __restrict__ ml, size_t base, int nsplit,
                              int G, const TG* __restrict__ gate, long long gate_stride, Tout* __restrict__ out,
                              long long out_stride, size_t row0) {
-    __shared__ float fw[256];
-    __shared__ float red[2][4];
-    const int tid = threadIdx.x, lane = tid % WAVE, w = tid / WAVE;
-    for (int rr = 0; rr < G; rr++) {
-        const size_t pi = (base + tid) * G + rr;
-        const float m = tid < nsplit ? ml[pi * 2] : -INFINITY;
-        const float l = tid < nsplit ? ml[pi * 2 + 1] : 0.f;
-        float mx = wave_max(m);
-        if (lane == 0) red[0][w] = mx;
-        __syncthreads();
-        mx = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
-        const float f = m == -INFINITY ? 0.f : __expf(m - mx);
-        fw[tid] = f;
-        float ls = wave_sum(f * l);
-        if (lane == 0) red[1][w] = ls;
-        __syncthreads();
-        ls = red[1][0] + red[1][1] + red[1][2] + red[1][3];
-        float acc = 0.f;
-        int s = 0;
-        for (; s + 8 <= nsplit; s += 8) {
-            float v[8];
+    __shared__ float fw[8][256];
+    const int tid = threadIdx.x, rr = tid / 32, t32 = tid % 32;
+    const bool active = rr < G;
+    float mx = -INFINITY;
+    if (active)
+        for (int s = t32; s < nsplit; s += 32) mx = fmaxf(mx, ml[((base + s) * G + rr) * 2]);
 #pragma unroll
-            for (int e = 0; e < 8; e++) v[e] = part[((base + s + e) * G + rr) * HD + tid];
-#pragma unroll
-            for (int e = 0; e < 8; e++) acc += v[e] * fw[s + e];
+    for (int o = 16; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, WAVE));
+    float ls = 0.f;
+    if (active)
+        for (int s = t32; s < nsplit; s += 32) {
+            const size_t pi = (base + s) * G + rr;
+            const float m = ml[pi * 2];
+            const float f = m == -INFINITY ? 0.f : __expf(m - mx);
+            fw[rr][s] = f;
+            ls += ml[pi * 2 + 1] * f;
         }
-        for (; s < nsplit; s++) acc += part[((base + s) * G + rr) * HD + tid] * fw[s];
-        const size_t row = row0 + rr;
-        float y = acc / ls;
-        if (gate) y *= sigmoid_f(Act<TG>::ld(gate, row * gate_stride + tid));
-        Act<Tout>::st(out, row * out_stride + tid, y);
-        __syncthreads();  // fw / red reused by the next head
+#pragma unroll
+    for (int o = 16; o > 0; o >>= 1) ls += __shfl_xor(ls, o, WAVE);
+    __syncthreads();
+    if (!active) return;
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    const int d0 = t32 * 8;
+    int s = 0;
+    for (; s + 4 <= nsplit; s += 4) {
+        float4 v[4][2];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const float4* p = (const float4*)(part + ((base + s + e) * G + rr) * HD + d0);
+            v[e][0] = p[0];
+            v[e][1] = p[1];
+        }
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const float f = fw[rr][s + e];
+            acc[0] += v[e][0].x * f; acc[1] += v[e][0].y * f; acc[2] += v[e][0].z * f; acc[3] += v[e][0].w * f;
+            acc[4] += v[e][1].x * f; acc[5] += v[e][1].y * f; acc[6] += v[e][1].z * f; acc[7] += v[e][1].w * f;
+        }
+    }
+    for (; s < nsplit; s++) {
+        const float4* p = (const float4*)(part + ((base + s) * G + rr) * HD + d0);
+        const float4 v0 = p[0], v1 = p[1];
+        const float f = fw[rr][s];
+        acc[0] += v0.x * f; acc[1] += v0.y * f; acc[2] += v0.z * f; acc[3] += v0.w * f;
+        acc[4] += v1.x * f; acc[5] += v1.y * f; acc[6] += v1.z * f; acc[7] += v1.w * f;
+    }
+    const size_t row = row0 + rr;
+    const float inv = 1.f / ls;
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        float y = acc[e] * inv;
+        if (gate) y *= sigmoid_f(Act<TG>::ld(gate, row * gate_stride + d0 + e));
+        Act<Tout>::st(out, row * out_stride + d0 + e, y);
     }
 }
 
