@@ -70,7 +70,8 @@ def test_attention_decode_bf16_out(dev):
     assert (out.float().cpu() - ref).abs().max() <= ref.abs().max() * 2 ** -8 + 1e-3 * ref.abs().max()
 
 
-@pytest.mark.parametrize("B,H,KV,T,pos", [(1, 16, 2, 2, 0), (1, 16, 2, 17, 30), (2, 8, 2, 64, 0), (1, 16, 2, 130, 5)])
+@pytest.mark.parametrize("B,H,KV,T,pos", [(1, 16, 2, 2, 0), (1, 16, 2, 17, 30), (2, 8, 2, 64, 0), (1, 16, 2, 130, 5),
+                                          (1, 16, 2, 1000, 0), (2, 16, 2, 300, 500), (1, 4, 4, 77, 3)])
 def test_attention_core_prefill(dev, B, H, KV, T, pos):
     g_ = _gen(T)
     q = torch.randn(B, H, T, HD, generator=g_) * 0.5
