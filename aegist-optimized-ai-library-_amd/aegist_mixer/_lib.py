@@ -50,7 +50,30 @@ SIGNATURES: dict[str, tuple] = {
     "aegist_attention_decode_workspace_bytes": (SZ, [I, I, I, I]),
     "aegist_attention_decode": (I, [P, P, P, I, P, P, P, P, P, I, I, I, I, I, I, I, I, F, F, P, SZ, P]),
     "aegist_attention_core": (I, [P, P, P, P, P, I, I, I, I, I, I, F, P, SZ, P]),
+    "aegist_stack_create": (I, [P, C.POINTER(C.c_void_p)]),
+    "aegist_stack_destroy": (I, [P]),
+    "aegist_stack_set_layer": (I, [P, I, P]),
+    "aegist_stack_reset": (I, [P, P]),
+    "aegist_stack_length": (I, [P]),
+    "aegist_stack_forward": (I, [P, P, I, I, P]),
+    "aegist_embed_bf16": (I, [P, P, P, I, I, P]),
 }
+
+
+MAX_LAYERS = 64
+
+
+class StackConfig(C.Structure):
+    """AegistStackConfig of include/aegist_mixer.h."""
+    _fields_ = [("n_layers", I), ("d_model", I), ("hk", I), ("hv", I), ("n_heads", I), ("n_kv", I),
+                ("head_dim", I), ("rotary_dim", I), ("rope_theta", F), ("eps", F), ("max_batch", I),
+                ("max_tokens", I), ("max_context", I), ("layer_is_attn", C.c_ubyte * MAX_LAYERS)]
+
+
+class LayerWeights(C.Structure):
+    """AegistLayerWeights of include/aegist_mixer.h (device pointers)."""
+    _fields_ = [(name, P) for name in ("norm1", "w_qkv", "w_z", "w_b", "w_a", "conv_w", "a_log", "dt_bias",
+                                       "gnorm_w", "w_out", "w_q", "w_k", "w_v", "w_o", "q_norm", "k_norm")]
 
 
 class AegistError(RuntimeError):

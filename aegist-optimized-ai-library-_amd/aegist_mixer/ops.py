@@ -255,3 +255,70 @@ def engine_gated_norm(o, z, w, eps=1e-6):
     out = torch.empty_like(o)
     call("aegist_gated_norm", _p(o), _p(z), _p(w), _p(out), T, HV, DV, eps, _stream())
     return out
+
+
+# --- the hybrid mixer stack (config 4) ----------------------------------------------------------
+
+class HybridStack:
+    """Batched mixer stack on the device (aegist_stack_* of the C ABI): per layer
+    x = x + mixer(znorm(x)), DeltaNet or gated attention, MoE FFN as identity
+    (hybrid.py:812-843; hybrid.rs:760-861). `layers` is a list of dicts of bf16 device tensors
+    named as AegistLayerWeights; the stack keeps pointers to them (they must stay alive)."""
+
+    _DELTA = ("norm1", "w_qkv", "w_z", "w_b", "w_a", "conv_w", "a_log", "dt_bias", "gnorm_w", "w_out")
+    _ATTN = ("norm1", "w_q", "w_k", "w_v", "w_o", "q_norm", "k_norm")
+
+    def __init__(self, cfg: dict, kinds: list, layers: list, max_batch: int, max_tokens: int, max_context: int):
+        import ctypes as C
+        from ._lib import LayerWeights, StackConfig
+        c = StackConfig()
+        c.n_layers, c.d_model, c.hk, c.hv = len(kinds), cfg["d_model"], cfg["hk"], cfg["hv"]
+        c.n_heads, c.n_kv, c.head_dim, c.rotary_dim = cfg["n_heads"], cfg["n_kv"], cfg["head_dim"], cfg["rotary_dim"]
+        c.rope_theta, c.eps = cfg["rope_theta"], cfg["eps"]
+        c.max_batch, c.max_tokens, c.max_context = max_batch, max_tokens, max_context
+        for i, k in enumerate(kinds):
+            c.layer_is_attn[i] = 1 if k == "attn" else 0
+        self._h = C.c_void_p()
+        call("aegist_stack_create", C.byref(c), C.byref(self._h))
+        self.layers = layers  # keep the weights alive
+        for i, (W, kind) in enumerate(zip(layers, kinds)):
+            lw = LayerWeights()
+            for name in (self._ATTN if kind == "attn" else self._DELTA):
+                t = W[name]
+                if t.dtype != torch.bfloat16 or not t.is_contiguous():
+                    raise AegistError("HybridStack", -3, f"layer {i} {name}: contiguous bf16 expected")
+                setattr(lw, name, _p(t))
+            call("aegist_stack_set_layer", self._h, i, C.byref(lw))
+
+    def forward(self, x):
+        """x [B, T, d] fp32 contiguous device tensor, updated in place and returned."""
+        _need_contig(x)
+        B, T, _ = x.shape
+        call("aegist_stack_forward", self._h, _p(x), B, T, _stream())
+        return x
+
+    def reset(self):
+        call("aegist_stack_reset", self._h, _stream())
+
+    @property
+    def length(self) -> int:
+        return lib().aegist_stack_length(self._h)
+
+    def close(self):
+        if getattr(self, "_h", None) is not None and self._h.value:
+            lib().aegist_stack_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def embed(table, ids):
+    """fp32 rows of a bf16 embedding table [V, d] for int32 ids [n] (device tensors)."""
+    n, D = ids.numel(), table.shape[1]
+    out = torch.empty(n, D, dtype=torch.float32, device=table.device)
+    call("aegist_embed_bf16", _p(table), _p(ids), _p(out), n, D, _stream())
+    return out

@@ -485,28 +485,45 @@ __global__ void __launch_bounds__(256) attn_prefill_mfma_kernel(const float* __r
 
     const int last_key = pos + min(q0 + PQ, T) - 1;   // keys [0, last_key] are visible to this block
     const int ntiles = last_key / PK + 1;
+    // Tile staging: step `it` moves the 16-byte chunk c8 = 8 it .. of key (row) tid % 64 for
+    // tid / 64 = it % 4 ... lanes run over consecutive keys, so the V^T writes are contiguous
+    // 2-byte runs (conflict-free) and the K writes land in distinct rows. The next tile is held
+    // in registers (requested a full tile ahead).
+    constexpr int NSTEP = (PK * HD) / (8 * 256);  // 8
+    uint4 kreg[NSTEP], vreg[NSTEP];
+    auto fetch = [&](int kt) {
+        const int row = tid % PK, key = min(kt * PK + row, last_key);
+#pragma unroll
+        for (int it = 0; it < NSTEP; it++) {
+            const int c8 = ((tid / PK) + 4 * it) * 8;
+            kreg[it] = *(const uint4*)(kbase + (size_t)key * HD + c8);
+            vreg[it] = *(const uint4*)(vbase + (size_t)key * HD + c8);
+        }
+    };
+    fetch(0);
     for (int kt = 0; kt < ntiles; kt++) {
         const int key0 = kt * PK;
-        // ---- stage K (row-major) and V^T as fp16; rows past last_key are clamped (masked below)
-        __syncthreads();
+        __syncthreads();  // previous tile's LDS reads done
+        {
+            const int row = tid % PK;
 #pragma unroll
-        for (int it = 0; it < (PK * HD) / (8 * 256); it++) {  // 8 steps of 8 elements
-            const int idx = it * 256 + tid, row = idx / (HD / 8), c8 = (idx % (HD / 8)) * 8;
-            const int key = min(key0 + row, last_key);
-            const uint4 kr = *(const uint4*)(kbase + (size_t)key * HD + c8);
-            const uint4 vr = *(const uint4*)(vbase + (size_t)key * HD + c8);
-            const uint32_t kw[4] = {kr.x, kr.y, kr.z, kr.w}, vw[4] = {vr.x, vr.y, vr.z, vr.w};
-            half8 kh;
+            for (int it = 0; it < NSTEP; it++) {
+                const int c8 = ((tid / PK) + 4 * it) * 8;
+                const uint32_t kw[4] = {kreg[it].x, kreg[it].y, kreg[it].z, kreg[it].w};
+                const uint32_t vw[4] = {vreg[it].x, vreg[it].y, vreg[it].z, vreg[it].w};
+                half8 kh;
 #pragma unroll
-            for (int e = 0; e < 4; e++) {
-                kh[2 * e] = (_Float16)bf_lo(kw[e]);
-                kh[2 * e + 1] = (_Float16)bf_hi(kw[e]);
-                Vt[c8 + 2 * e][row] = (_Float16)bf_lo(vw[e]);
-                Vt[c8 + 2 * e + 1][row] = (_Float16)bf_hi(vw[e]);
+                for (int e = 0; e < 4; e++) {
+                    kh[2 * e] = (_Float16)bf_lo(kw[e]);
+                    kh[2 * e + 1] = (_Float16)bf_hi(kw[e]);
+                    Vt[c8 + 2 * e][row] = (_Float16)bf_lo(vw[e]);
+                    Vt[c8 + 2 * e + 1][row] = (_Float16)bf_hi(vw[e]);
+                }
+                *(half8*)&Kt[row][c8] = kh;
             }
-            *(half8*)&Kt[row][c8] = kh;
         }
         __syncthreads();
+        fetch(min(kt + 1, ntiles - 1));  // unconditional: static wait counts
         // ---- scores for 4 blocks of 16 keys
         f32x4 sc[4];
 #pragma unroll
@@ -632,6 +649,20 @@ int launch_prefill_core(const float* q, Strides3 qs, const uint16_t* kc, const u
                                                                             pos, cap, scale);
     }
     return after_launch("attention_prefill");
+}
+
+// Wrappers for the layer stack: qn [B, T, H, HD], gate inside qg [B, T, H, 2 HD] (+HD),
+// out [B, T, H, HD] fp32.
+int stack_attn_decode(const float* qn, const uint16_t* kc, const uint16_t* vc, const float* qg, float* out, int B,
+                      int H, int KV, int L, int cap, float scale, void* ws, size_t ws_bytes, hipStream_t st) {
+    return launch_decode_core<float, float>(qn, kc, vc, qg + HD, 2 * HD, out, HD, B, H, KV, L, cap, scale, ws,
+                                            ws_bytes, st);
+}
+int stack_attn_prefill(const float* qn, const uint16_t* kc, const uint16_t* vc, const float* qg, float* out, int B,
+                       int H, int KV, int T, int pos, int cap, float scale, hipStream_t st) {
+    Strides3 qs{(long long)T * H * HD, (long long)H * HD, HD};
+    Strides3 gs{(long long)T * H * 2 * HD, (long long)H * 2 * HD, 2 * HD};
+    return launch_prefill_core(qn, qs, kc, vc, qg + HD, gs, out, qs, B, H, KV, T, pos, cap, scale, st);
 }
 
 }  // namespace aegist

@@ -287,3 +287,140 @@ extern "C" int aegist_gated_norm(const float* o, const float* z, const uint16_t*
     gated_norm_kernel<<<(rows + 3) / 4, 256, 0, AEG_STREAM(stream)>>>(o, z, w, out, rows, DV, eps);
     return after_launch("gated_norm");
 }
+
+// ---------------------------------------------------------------------------------------------
+// Helpers for the layer stack (batched rows, bf16 outputs feeding the projection GEMMs).
+namespace {
+
+// ZNorm of `rows` rows of D into bf16 (the GEMM input of the mixer projections).
+__global__ void __launch_bounds__(256) znorm_bf16_kernel(const float* __restrict__ x, const uint16_t* __restrict__ w,
+                                                         uint16_t* __restrict__ out, int D, float eps) {
+    __shared__ float red[4];
+    const float* xr = x + (size_t)blockIdx.x * D;
+    float ss = 0.f;
+    for (int i = threadIdx.x; i < D; i += 256) ss += xr[i] * xr[i];
+    ss = block_sum(ss, red);
+    const float inv = rsqrtf(ss / (float)D + eps);
+    for (int i = threadIdx.x; i < D; i += 256) out[(size_t)blockIdx.x * D + i] = f2bf((xr[i] * inv) * (1.f + bf2f(w[i])));
+}
+
+__global__ void cast_bf16_kernel(const float* __restrict__ x, uint16_t* __restrict__ y, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        y[i] = f2bf(x[i]);
+}
+
+// beta = sigmoid(b), g = -exp(A_log) softplus(a + dt_bias) from projected rows ba [rows, 2HV]
+// (b in columns [0, HV), a in [HV, 2HV)). g, beta [rows, HV].
+__global__ void gates_from_proj_kernel(const float* __restrict__ ba, const uint16_t* __restrict__ a_log,
+                                       const uint16_t* __restrict__ dt_bias, float* __restrict__ g,
+                                       float* __restrict__ beta, int rows, int HV) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= rows * HV) return;
+    const int r = i / HV, j = i % HV;
+    const float bb = ba[(size_t)r * 2 * HV + j], aa = ba[(size_t)r * 2 * HV + HV + j];
+    beta[i] = 1.f / (1.f + expf(-bb));
+    const float xx = aa + bf2f(dt_bias[j]);
+    const float sp = xx > 20.f ? xx : log1pf(expf(xx));
+    g[i] = -expf(bf2f(a_log[j])) * sp;
+}
+
+// Gated norm into bf16: out = w * rmsnorm(o) * silu(z), one wave per (row, head).
+__global__ void __launch_bounds__(256) gated_norm_bf16_kernel(const float* __restrict__ o, const float* __restrict__ z,
+                                                              const uint16_t* __restrict__ w, uint16_t* __restrict__ out,
+                                                              int rows, int DV, float eps) {
+    const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+    const int item = blockIdx.x * 4 + wave;
+    if (item >= rows) return;
+    const size_t base = (size_t)item * DV;
+    float ss = 0.f;
+    for (int i = lane; i < DV; i += WAVE) ss += o[base + i] * o[base + i];
+    ss = wave_sum(ss);
+    const float r = rsqrtf(ss / (float)DV + eps);
+    for (int i = lane; i < DV; i += WAVE) {
+        const float zz = z[base + i];
+        out[base + i] = f2bf(bf2f(w[i]) * (o[base + i] * r) * (zz / (1.f + expf(-zz))));
+    }
+}
+
+// Batched conv + SiLU: x, y [B, T, C]; state [B, C, 3]; grid (ceil(C/64), B).
+__global__ void __launch_bounds__(256) conv_silu_batched_kernel(const float* __restrict__ x, float* __restrict__ y,
+                                                                const uint16_t* __restrict__ w,
+                                                                float* __restrict__ state, int T, int C) {
+    const int b = blockIdx.y;
+    x += (size_t)b * T * C;
+    y += (size_t)b * T * C;
+    state += (size_t)b * C * 3;
+    const int c = blockIdx.x * 64 + (threadIdx.x % 64), tl = threadIdx.x / 64;
+    const bool ok = c < C;
+    float s0 = 0.f, s1 = 0.f, s2 = 0.f;
+    if (ok) {
+        s0 = state[(size_t)c * 3];
+        s1 = state[(size_t)c * 3 + 1];
+        s2 = state[(size_t)c * 3 + 2];
+        const float w0 = bf2f(w[(size_t)c * 4]), w1 = bf2f(w[(size_t)c * 4 + 1]), w2 = bf2f(w[(size_t)c * 4 + 2]),
+                    w3 = bf2f(w[(size_t)c * 4 + 3]);
+        for (int t = tl; t < T; t += 4) {
+            const float xm3 = t >= 3 ? x[(size_t)(t - 3) * C + c] : (t == 0 ? s0 : (t == 1 ? s1 : s2));
+            const float xm2 = t >= 2 ? x[(size_t)(t - 2) * C + c] : (t == 0 ? s1 : s2);
+            const float xm1 = t >= 1 ? x[(size_t)(t - 1) * C + c] : s2;
+            y[(size_t)t * C + c] = silu_f(w0 * xm3 + w1 * xm2 + w2 * xm1 + w3 * x[(size_t)t * C + c]);
+        }
+    }
+    __syncthreads();
+    if (ok && tl == 0) {
+        const float h0 = T >= 3 ? x[(size_t)(T - 3) * C + c] : (T == 2 ? s2 : (T == 1 ? s1 : s0));
+        const float h1 = T >= 2 ? x[(size_t)(T - 2) * C + c] : (T == 1 ? s2 : s1);
+        const float h2 = T >= 1 ? x[(size_t)(T - 1) * C + c] : s2;
+        state[(size_t)c * 3] = h0;
+        state[(size_t)c * 3 + 1] = h1;
+        state[(size_t)c * 3 + 2] = h2;
+    }
+}
+
+// Embedding rows: out[i] = fp32(table[ids[i]]), D per row.
+__global__ void embed_bf16_kernel(const uint16_t* __restrict__ table, const int* __restrict__ ids,
+                                  float* __restrict__ out, int n, int D) {
+    const int r = blockIdx.x;
+    if (r >= n) return;
+    const uint16_t* src = table + (size_t)ids[r] * D;
+    for (int i = threadIdx.x; i < D; i += blockDim.x) out[(size_t)r * D + i] = bf2f(src[i]);
+}
+
+}  // namespace
+
+namespace aegist {
+int launch_znorm_bf16(const float* x, const uint16_t* w, uint16_t* out, int rows, int D, float eps, hipStream_t st) {
+    if (rows <= 0) return 0;
+    znorm_bf16_kernel<<<rows, 256, 0, st>>>(x, w, out, D, eps);
+    return after_launch("znorm_bf16");
+}
+int launch_cast_bf16(const float* x, uint16_t* y, size_t n, hipStream_t st) {
+    if (n == 0) return 0;
+    unsigned blocks = (unsigned)std::min<size_t>((n + 255) / 256, 16384);
+    cast_bf16_kernel<<<blocks, 256, 0, st>>>(x, y, n);
+    return after_launch("cast_bf16");
+}
+int launch_gates_from_proj(const float* ba, const uint16_t* a_log, const uint16_t* dt_bias, float* g, float* beta,
+                           int rows, int HV, hipStream_t st) {
+    if (rows <= 0) return 0;
+    gates_from_proj_kernel<<<(rows * HV + 255) / 256, 256, 0, st>>>(ba, a_log, dt_bias, g, beta, rows, HV);
+    return after_launch("gates_from_proj");
+}
+int launch_gated_norm_bf16(const float* o, const float* z, const uint16_t* w, uint16_t* out, int rows, int DV,
+                           float eps, hipStream_t st) {
+    if (rows <= 0) return 0;
+    gated_norm_bf16_kernel<<<(rows + 3) / 4, 256, 0, st>>>(o, z, w, out, rows, DV, eps);
+    return after_launch("gated_norm_bf16");
+}
+int launch_conv_silu_batched(const float* x, float* y, const uint16_t* w, float* state, int B, int T, int C,
+                             hipStream_t st) {
+    if (B <= 0 || T <= 0) return 0;
+    conv_silu_batched_kernel<<<dim3((C + 63) / 64, B), 256, 0, st>>>(x, y, w, state, T, C);
+    return after_launch("conv_silu_batched");
+}
+int launch_embed_bf16(const uint16_t* table, const int* ids, float* out, int n, int D, hipStream_t st) {
+    if (n <= 0) return 0;
+    embed_bf16_kernel<<<n, 256, 0, st>>>(table, ids, out, n, D);
+    return after_launch("embed_bf16");
+}
+}  // namespace aegist

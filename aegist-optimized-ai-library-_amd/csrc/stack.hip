@@ -1,0 +1,268 @@
+// The hybrid mixer stack: a batched, native counterpart of HybridEngine::forward_chunk /
+// HybridEngine::mixer (aegist_rs/src/hybrid.rs:760-861) and HybridBlock.forward with the MoE
+// FFN replaced by the identity (aegist/hybrid.py:812-843): for every layer
+//     x = x + mixer(znorm(x))
+// where the mixer is the gated DeltaNet (hybrid.py:388-421) or the gated GQA attention
+// (hybrid.py:280-311). The stack owns the recurrent state, conv state and bf16 KV cache of every
+// layer (HybridCache, hybrid.py:171-260; the engine buffers of hybrid.rs:607-629).
+//
+// Projections are plain GEMMs and go to rocBLAS (bf16 operands, fp32 accumulation and output,
+// the out-projections accumulate straight into the fp32 residual with beta = 1); every other op
+// is one of this library's kernels.
+#include "common.h"
+
+#include <rocblas/rocblas.h>
+
+#include <algorithm>
+#include <vector>
+
+namespace aegist {
+int launch_znorm_bf16(const float* x, const uint16_t* w, uint16_t* out, int rows, int D, float eps, hipStream_t st);
+int launch_cast_bf16(const float* x, uint16_t* y, size_t n, hipStream_t st);
+int launch_gates_from_proj(const float* ba, const uint16_t* a_log, const uint16_t* dt_bias, float* g, float* beta,
+                           int rows, int HV, hipStream_t st);
+int launch_gated_norm_bf16(const float* o, const float* z, const uint16_t* w, uint16_t* out, int rows, int DV,
+                           float eps, hipStream_t st);
+int launch_conv_silu_batched(const float* x, float* y, const uint16_t* w, float* state, int B, int T, int C,
+                             hipStream_t st);
+int launch_embed_bf16(const uint16_t* table, const int* ids, float* out, int n, int D, hipStream_t st);
+int launch_attn_prep(const void* qg, const void* k, const void* v, int in_dtype, const uint16_t* qw,
+                     const uint16_t* kw, float* qn, uint16_t* kc, uint16_t* vc, int B, int T, int H, int KV, int HD,
+                     int RD, int pos0, int cap, float eps, float theta, hipStream_t stream, int* zero_ctr, int n_ctr);
+int stack_attn_decode(const float* qn, const uint16_t* kc, const uint16_t* vc, const float* qg, float* out, int B,
+                      int H, int KV, int L, int cap, float scale, void* ws, size_t ws_bytes, hipStream_t st);
+int stack_attn_prefill(const float* qn, const uint16_t* kc, const uint16_t* vc, const float* qg, float* out, int B,
+                       int H, int KV, int T, int pos, int cap, float scale, hipStream_t st);
+size_t decode_workspace_bytes(int B, int H, int KV, int L, bool with_q);
+}  // namespace aegist
+
+using namespace aegist;
+
+namespace {
+
+constexpr int D = 128;  // dk = dv
+
+struct Buf {
+    void* p = nullptr;
+    size_t n = 0;
+};
+
+struct Stack {
+    AegistStackConfig cfg;
+    std::vector<AegistLayerWeights> w;
+    std::vector<int> slot;  // per layer: index among its kind
+    int n_delta = 0, n_attn = 0, length = 0, device = 0;
+    rocblas_handle blas = nullptr;
+    // states
+    float* conv = nullptr;     // [n_delta, maxB, C, 3]
+    float* rec = nullptr;      // [n_delta, maxB, HV, 128, 128]
+    uint16_t* kc = nullptr;    // [n_attn, maxB, KV, cap, HD]
+    uint16_t* vc = nullptr;
+    // per-call scratch (max_tokens rows)
+    uint16_t* hb = nullptr;    // znorm out, bf16 [rows, d]
+    float* proj = nullptr;     // qkv or q|gate [rows, max(C, 2 H HD)]
+    float* z = nullptr;        // [rows, HV 128]
+    float* kv2 = nullptr;      // k then v projections [2, rows, KV HD]
+    float* ba = nullptr;       // [rows, 2 HV]
+    float* g = nullptr;        // [rows, HV]
+    float* beta = nullptr;     // [rows, HV]
+    float* y = nullptr;        // conv out [rows, C], or attention q_n [rows, H, HD]
+    float* o = nullptr;        // mixer core out [rows, max(HV 128, H HD)]
+    uint16_t* ob = nullptr;    // bf16 copy of o (GEMM input)
+    void* ws = nullptr;        // chunked prefill / attention decode workspace
+    size_t ws_bytes = 0;
+    std::vector<void*> allocs;
+
+    int C() const { return 2 * cfg.hk * D + cfg.hv * D; }
+};
+
+int alloc(Stack* s, void** p, size_t bytes) {
+    int rc = check_hip(hipMalloc(p, std::max<size_t>(bytes, 256)), "hipMalloc(stack)");
+    if (!rc) s->allocs.push_back(*p);
+    return rc;
+}
+
+// Y[M, N] (row-major, leading dim ldy) = A[M, K] (bf16 row-major) . W[N, K]^T (bf16 row-major)
+//                                          + beta * Y
+int gemm(Stack* s, const uint16_t* A, const uint16_t* W, float* Y, int M, int N, int K, int ldy, float beta) {
+    const float alpha = 1.f;
+    rocblas_status st = rocblas_gemm_ex(s->blas, rocblas_operation_transpose, rocblas_operation_none, N, M, K, &alpha, W,
+                                        rocblas_datatype_bf16_r, K, A, rocblas_datatype_bf16_r, K, &beta, Y,
+                                        rocblas_datatype_f32_r, ldy, Y, rocblas_datatype_f32_r, ldy,
+                                        rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0);
+    if (st != rocblas_status_success)
+        return fail(AEGIST_ERR_SHAPE, std::string("rocblas_gemm_ex: ") + rocblas_status_to_string(st));
+    return after_launch("projection gemm");
+}
+
+#define RC(x)                  \
+    do {                       \
+        int _r = (x);          \
+        if (_r) return _r;     \
+    } while (0)
+
+int delta_layer(Stack* s, const AegistLayerWeights& w, int sl, float* x, int B, int T, hipStream_t st) {
+    const AegistStackConfig& c = s->cfg;
+    const int rows = B * T, C = s->C(), HV = c.hv, HK = c.hk, dm = c.d_model;
+    const size_t mb = (size_t)c.max_batch;
+    float* conv = s->conv + (size_t)sl * mb * C * 3;
+    float* rec = s->rec + (size_t)sl * mb * HV * D * D;
+    RC(gemm(s, s->hb, w.w_qkv, s->proj, rows, C, dm, C, 0.f));
+    RC(gemm(s, s->hb, w.w_z, s->z, rows, HV * D, dm, HV * D, 0.f));
+    RC(gemm(s, s->hb, w.w_b, s->ba, rows, HV, dm, 2 * HV, 0.f));
+    RC(gemm(s, s->hb, w.w_a, s->ba + HV, rows, HV, dm, 2 * HV, 0.f));
+    RC(launch_gates_from_proj(s->ba, w.a_log, w.dt_bias, s->g, s->beta, rows, HV, st));
+    const float qscale = 1.f / sqrtf((float)D);
+    if (T == 1) {
+        // decode: conv-state update + conv + SiLU + L2-norm + delta step, fused (hybrid.py:411-413)
+        RC(aegist_delta_decode_step(s->proj, AEGIST_F32, w.conv_w, conv, s->g, s->beta, rec, s->o, AEGIST_F32, B, HK,
+                                    HV, qscale, 1e-6f, st));
+    } else {
+        // prefill: conv over the chunk, then the chunked WY form from the carried state
+        RC(launch_conv_silu_batched(s->proj, s->y, w.conv_w, conv, B, T, C, st));
+        const long long sb = (long long)T * C, so_b = (long long)T * HV * D;
+        RC(aegist_delta_chunked(s->y, s->y + (size_t)HK * D, s->y + (size_t)2 * HK * D, AEGIST_F32, sb, C, D, sb, C, D,
+                                s->g, s->beta, rec, s->o, AEGIST_F32, so_b, (long long)HV * D, D, B, T, HK, HV, 1,
+                                qscale, 1e-6f, s->ws, s->ws_bytes, st));
+    }
+    RC(launch_gated_norm_bf16(s->o, s->z, w.gnorm_w, s->ob, rows * HV, D, c.eps, st));
+    return gemm(s, s->ob, w.w_out, x, rows, dm, HV * D, dm, 1.f);
+}
+
+int attn_layer(Stack* s, const AegistLayerWeights& w, int sl, float* x, int B, int T, hipStream_t st) {
+    const AegistStackConfig& c = s->cfg;
+    const int rows = B * T, H = c.n_heads, KV = c.n_kv, HD = c.head_dim, dm = c.d_model;
+    const size_t mb = (size_t)c.max_batch, cap = (size_t)c.max_context;
+    uint16_t* kc = s->kc + (size_t)sl * mb * KV * cap * HD;
+    uint16_t* vc = s->vc + (size_t)sl * mb * KV * cap * HD;
+    float* kp = s->kv2;
+    float* vp = s->kv2 + (size_t)c.max_tokens * KV * HD;
+    RC(gemm(s, s->hb, w.w_q, s->proj, rows, 2 * H * HD, dm, 2 * H * HD, 0.f));
+    RC(gemm(s, s->hb, w.w_k, kp, rows, KV * HD, dm, KV * HD, 0.f));
+    RC(gemm(s, s->hb, w.w_v, vp, rows, KV * HD, dm, KV * HD, 0.f));
+    RC(launch_attn_prep(s->proj, kp, vp, AEGIST_F32, w.q_norm, w.k_norm, s->y, kc, vc, B, T, H, KV, HD, c.rotary_dim,
+                        s->length, (int)cap, c.eps, c.rope_theta, st, nullptr, 0));
+    const float scale = 1.f / sqrtf((float)HD);
+    if (T == 1)
+        RC(stack_attn_decode(s->y, kc, vc, s->proj, s->o, B, H, KV, s->length + 1, (int)cap, scale, s->ws, s->ws_bytes,
+                             st));
+    else
+        RC(stack_attn_prefill(s->y, kc, vc, s->proj, s->o, B, H, KV, T, s->length, (int)cap, scale, st));
+    RC(launch_cast_bf16(s->o, s->ob, (size_t)rows * H * HD, st));
+    return gemm(s, s->ob, w.w_o, x, rows, dm, H * HD, dm, 1.f);
+}
+
+}  // namespace
+
+extern "C" {
+
+int aegist_stack_create(const AegistStackConfig* cfg, void** handle) {
+    if (!cfg || !handle) return fail(AEGIST_ERR_SHAPE, "stack_create: null argument");
+    const AegistStackConfig& c = *cfg;
+    if (c.n_layers <= 0 || c.n_layers > AEGIST_MAX_LAYERS) return fail(AEGIST_ERR_SHAPE, "stack_create: bad n_layers");
+    if (c.hk <= 0 || c.hv % c.hk || (c.hv / c.hk != 1 && c.hv / c.hk != 2 && c.hv / c.hk != 4))
+        return fail(AEGIST_ERR_SHAPE, "stack_create: need HV / HK in {1, 2, 4}");
+    if (c.head_dim != 256 || c.n_kv <= 0 || c.n_heads % c.n_kv || c.n_heads / c.n_kv > 8)
+        return fail(AEGIST_ERR_SHAPE, "stack_create: need head_dim 256 and H / KV <= 8");
+    if (c.max_batch <= 0 || c.max_tokens < c.max_batch || c.max_context <= 0 || c.d_model <= 0)
+        return fail(AEGIST_ERR_SHAPE, "stack_create: bad capacities");
+    Stack* s = new Stack();
+    s->cfg = c;
+    s->w.resize(c.n_layers);
+    s->slot.resize(c.n_layers);
+    for (int l = 0; l < c.n_layers; l++) s->slot[l] = c.layer_is_attn[l] ? s->n_attn++ : s->n_delta++;
+    int rc = check_hip(hipGetDevice(&s->device), "hipGetDevice");
+    if (!rc && rocblas_create_handle(&s->blas) != rocblas_status_success)
+        rc = fail(AEGIST_ERR_SHAPE, "rocblas_create_handle failed");
+    const size_t rows = c.max_tokens, C = s->C(), mb = c.max_batch;
+    const int H = c.n_heads, KV = c.n_kv, HD = c.head_dim, HV = c.hv;
+    const size_t wide = std::max<size_t>((size_t)HV * D, (size_t)H * HD);
+    auto A = [&](void** p, size_t bytes) {
+        if (!rc) rc = alloc(s, p, bytes);
+    };
+    A((void**)&s->conv, (size_t)std::max(1, s->n_delta) * mb * C * 3 * 4);
+    A((void**)&s->rec, (size_t)std::max(1, s->n_delta) * mb * HV * D * D * 4);
+    A((void**)&s->kc, (size_t)std::max(1, s->n_attn) * mb * KV * c.max_context * HD * 2);
+    A((void**)&s->vc, (size_t)std::max(1, s->n_attn) * mb * KV * c.max_context * HD * 2);
+    A((void**)&s->hb, rows * c.d_model * 2);
+    A((void**)&s->proj, rows * std::max<size_t>(C, (size_t)2 * H * HD) * 4);
+    A((void**)&s->z, rows * HV * D * 4);
+    A((void**)&s->kv2, 2 * rows * KV * HD * 4);
+    A((void**)&s->ba, rows * 2 * HV * 4);
+    A((void**)&s->g, rows * HV * 4);
+    A((void**)&s->beta, rows * HV * 4);
+    A((void**)&s->y, rows * std::max<size_t>(C, (size_t)H * HD) * 4);
+    A((void**)&s->o, rows * wide * 4);
+    A((void**)&s->ob, rows * wide * 2);
+    s->ws_bytes = std::max(aegist_delta_chunked_workspace_bytes(c.max_batch, (int)std::min<size_t>(rows, 1 << 30), HV),
+                           decode_workspace_bytes(c.max_batch, H, KV, c.max_context, false));
+    A(&s->ws, s->ws_bytes);
+    if (rc) {
+        aegist_stack_destroy(s);
+        return rc;
+    }
+    *handle = s;
+    return aegist_stack_reset(s, nullptr);
+}
+
+int aegist_stack_destroy(void* handle) {
+    Stack* s = (Stack*)handle;
+    if (!s) return 0;
+    (void)hipDeviceSynchronize();
+    for (void* p : s->allocs) (void)hipFree(p);
+    if (s->blas) rocblas_destroy_handle(s->blas);
+    delete s;
+    return 0;
+}
+
+int aegist_stack_set_layer(void* handle, int layer, const AegistLayerWeights* w) {
+    Stack* s = (Stack*)handle;
+    if (!s || !w || layer < 0 || layer >= s->cfg.n_layers) return fail(AEGIST_ERR_SHAPE, "stack_set_layer: bad layer");
+    s->w[layer] = *w;
+    return 0;
+}
+
+int aegist_stack_reset(void* handle, void* stream) {
+    Stack* s = (Stack*)handle;
+    if (!s) return fail(AEGIST_ERR_SHAPE, "stack_reset: null handle");
+    const AegistStackConfig& c = s->cfg;
+    const size_t mb = c.max_batch;
+    hipStream_t st = AEG_STREAM(stream);
+    AEG_HIP(hipMemsetAsync(s->conv, 0, (size_t)std::max(1, s->n_delta) * mb * s->C() * 3 * 4, st));
+    AEG_HIP(hipMemsetAsync(s->rec, 0, (size_t)std::max(1, s->n_delta) * mb * c.hv * D * D * 4, st));
+    s->length = 0;
+    return 0;
+}
+
+int aegist_stack_length(void* handle) { return handle ? ((Stack*)handle)->length : -1; }
+
+int aegist_stack_forward(void* handle, float* x, int B, int T, void* stream) {
+    Stack* s = (Stack*)handle;
+    if (!s) return fail(AEGIST_ERR_SHAPE, "stack_forward: null handle");
+    const AegistStackConfig& c = s->cfg;
+    if (B <= 0 || T <= 0 || B > c.max_batch || (size_t)B * T > (size_t)c.max_tokens)
+        return fail(AEGIST_ERR_SHAPE, "stack_forward: B * T exceeds the stack's max_tokens / max_batch");
+    if (s->length + T > c.max_context)
+        return fail(AEGIST_ERR_SHAPE, "stack_forward: context of " + std::to_string(s->length + T) +
+                                          " tokens exceeds the stack's max_context");
+    for (int l = 0; l < c.n_layers; l++)
+        if (!s->w[l].norm1) return fail(AEGIST_ERR_SHAPE, "stack_forward: layer " + std::to_string(l) + " has no weights");
+    hipStream_t st = AEG_STREAM(stream);
+    if (rocblas_set_stream(s->blas, st) != rocblas_status_success) return fail(AEGIST_ERR_SHAPE, "rocblas_set_stream");
+    const int rows = B * T;
+    for (int l = 0; l < c.n_layers; l++) {
+        const AegistLayerWeights& w = s->w[l];
+        RC(launch_znorm_bf16(x, w.norm1, s->hb, rows, c.d_model, c.eps, st));
+        if (c.layer_is_attn[l]) RC(attn_layer(s, w, s->slot[l], x, B, T, st));
+        else RC(delta_layer(s, w, s->slot[l], x, B, T, st));
+    }
+    s->length += T;
+    return 0;
+}
+
+int aegist_embed_bf16(const uint16_t* table, const int* ids, float* out, int n, int D_, void* stream) {
+    if (n < 0 || D_ <= 0) return fail(AEGIST_ERR_SHAPE, "embed: bad shape");
+    return launch_embed_bf16(table, ids, out, n, D_, AEG_STREAM(stream));
+}
+
+}  // extern "C"

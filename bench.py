@@ -153,6 +153,37 @@ def bench_attention_decode(torch, ops, dev, reps=20):
             "note": "L=4096 at B=1 (8 MB) is MALL-resident and launch-bound"}
 
 
+def bench_attention_prefill(torch, ops, dev, T=2048, reps=10):
+    """Causal gated GQA prefill (config 4's attention layers): B=1, T=2048, 16 q heads, 2 KV
+    heads, HD 256, cache rows [0, T). FLOPs = 4 * H * HD * T (T + 1) / 2 (QK^T and PV)."""
+    from aegist_mixer._lib import call, lib
+    bf = torch.bfloat16
+    q = ops.fill_normal(torch.empty(1, ATTN_H, T, ATTN_HD, device=dev), 9001)
+    kc = ops.fill_normal(torch.empty(1, ATTN_KV, T, ATTN_HD, device=dev, dtype=bf), 9002)
+    vc = ops.fill_normal(torch.empty(1, ATTN_KV, T, ATTN_HD, device=dev, dtype=bf), 9003)
+    gate = ops.fill_normal(torch.empty(1, T, ATTN_H * ATTN_HD, device=dev), 9004)
+    out = torch.empty(1, T, ATTN_H, ATTN_HD, device=dev)
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def run():
+        call("aegist_attention_core", q.data_ptr(), kc.data_ptr(), vc.data_ptr(), gate.data_ptr(), out.data_ptr(), 1,
+             ATTN_H, ATTN_KV, T, 0, T, ATTN_HD ** -0.5, None, 0, stream)
+    for _ in range(2):
+        run()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        run()
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / reps
+    flops = 4 * ATTN_H * ATTN_HD * T * (T + 1) / 2
+    tf = flops / (us * 1e-6) / 1e12
+    return {"workload": f"causal gated GQA prefill, B=1, T={T}, 16/2 heads, HD 256", "us": round(us, 2),
+            "tflops": round(tf, 2), "mfma_frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4)}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -241,6 +272,7 @@ def main():
             res["roofline"]["traffic"] = json.load(f).get("bytes_per_launch")
     res["prefill"] = bench_prefill(torch, ops, dev)
     res["attention_decode"] = bench_attention_decode(torch, ops, dev)
+    res["attention_prefill"] = bench_attention_prefill(torch, ops, dev)
     if args.calib_copy:
         src = torch.empty(1 << 28, device=dev)  # 1 GiB fp32
         dst = torch.empty_like(src)

@@ -15,7 +15,8 @@
  *    scratch take a caller-provided workspace sized by the matching *_workspace_bytes query.
  *    The engine-ABI mirrors whose reference signature has no workspace argument
  *    (aegist_attention_gated, aegist_delta_scan) use a per-device workspace the library grows
- *    on demand; that is the only allocation the library makes on its own.
+ *    on demand; aegist_stack_create allocates the stack's states and scratch once. Nothing
+ *    else allocates.
  *  - `stream` is a hipStream_t (NULL = the device's null stream). Every launch is
  *    asynchronous on that stream; no entry point synchronises unless named *_sync. Setting
  *    AEGIST_SYNC_LAUNCH=1 synchronises after each launch and reports errors at the launch.
@@ -194,6 +195,54 @@ int aegist_attention_decode(const void* qg, const void* k_new, const void* v_new
 int aegist_attention_core(const float* q, const uint16_t* kc, const uint16_t* vc, const float* gate, float* out,
                           int B, int H, int KV, int T, int pos, int cap, float scale, void* workspace,
                           size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------------------
+ * Hybrid mixer stack: per layer x = x + mixer(znorm(x)) with the MoE FFN as identity
+ * (HybridBlock.forward, aegist/hybrid.py:812-843; HybridEngine::forward_chunk / mixer,
+ * aegist_rs/src/hybrid.rs:760-861). The stack owns every layer's recurrent state, conv state
+ * and bf16 KV cache (HybridCache, hybrid.py:171-260; engine buffers hybrid.rs:607-629); all
+ * sequences of a batch share one length. Projections run on rocBLAS (bf16 operands, fp32
+ * accumulation), everything else on this library's kernels. Weights are caller-owned bf16,
+ * row-major [out, in] as torch nn.Linear stores them.
+ * ------------------------------------------------------------------------------------- */
+#define AEGIST_MAX_LAYERS 64
+
+typedef struct AegistStackConfig {
+    int n_layers;
+    int d_model;
+    int hk, hv;                   /* DeltaNet QK / V heads (dk = dv = 128) */
+    int n_heads, n_kv, head_dim;  /* attention (head_dim 256) */
+    int rotary_dim;
+    float rope_theta, eps;        /* eps: ZNorm and GatedNorm */
+    int max_batch;                /* sequences per forward call */
+    int max_tokens;               /* B * T per forward call */
+    int max_context;              /* KV-cache capacity per sequence */
+    unsigned char layer_is_attn[AEGIST_MAX_LAYERS];
+} AegistStackConfig;
+
+typedef struct AegistLayerWeights {
+    const uint16_t* norm1;                        /* [d] ZNorm weight */
+    /* gated DeltaNet (hybrid.py:372-384) */
+    const uint16_t *w_qkv, *w_z, *w_b, *w_a;      /* [C, d], [HV*128, d], [HV, d], [HV, d] */
+    const uint16_t *conv_w, *a_log, *dt_bias;     /* [C, 4], [HV], [HV] */
+    const uint16_t *gnorm_w, *w_out;              /* [128], [d, HV*128] */
+    /* gated attention (hybrid.py:270-278) */
+    const uint16_t *w_q, *w_k, *w_v, *w_o;        /* [2*H*HD, d], [KV*HD, d] x2, [d, H*HD] */
+    const uint16_t *q_norm, *k_norm;              /* [HD] ZNorm weights */
+} AegistLayerWeights;
+
+int aegist_stack_create(const AegistStackConfig* cfg, void** handle);
+int aegist_stack_destroy(void* handle);
+int aegist_stack_set_layer(void* handle, int layer, const AegistLayerWeights* weights);
+/* length = 0, recurrent and conv states zeroed (HybridCache.reset, hybrid.py:258-263) */
+int aegist_stack_reset(void* handle, void* stream);
+int aegist_stack_length(void* handle);
+/* x [B, T, d] fp32 residual stream, updated in place; T == 1 takes the decode kernels,
+ * T > 1 the prefill kernels. Positions continue from aegist_stack_length(). */
+int aegist_stack_forward(void* handle, float* x, int B, int T, void* stream);
+/* out[i, :] = fp32(table[ids[i], :]) for n ids; the engine's embedding lookup
+ * (hybrid.rs:743-758) done on the device. */
+int aegist_embed_bf16(const uint16_t* table, const int* ids, float* out, int n, int D, void* stream);
 
 #ifdef __cplusplus
 }

@@ -249,3 +249,71 @@ def attention_decode(qg, k_new, v_new, q_norm_w, k_norm_w, kc, vc, pos: int, rot
                         kc, vc, pos, rotary_dim, theta, eps)
     y = attention_core(q, kc, vc, pos, KV)
     return gated_attention_out(y, gate).reshape(B, H, HD2 // 2)
+
+
+# --- composites: the mixers and the layer stack (config 4) ---------------------------------
+
+def _lin(x, w, round_in: bool):
+    """x @ w^T with w a bf16 nn.Linear weight [out, in]; with round_in the activation is
+    rounded to bf16 first, as a bf16 model feeds its projections (the HIP stack does the same)."""
+    xin = x.to(torch.bfloat16).float() if round_in else x.float()
+    return xin @ w.float().t()
+
+
+def gated_deltanet_mixer(h, W: dict, conv_state, state, length: int, hk: int, hv: int, eps: float = 1e-6,
+                         round_in: bool = True):
+    """GatedDeltaNet.forward (hybrid.py:388-421). h [B,T,d]; conv_state [B,C,3] (returned
+    updated as a new tensor); state [B,HV,128,128] updated in place. Returns (out [B,T,d],
+    new conv state)."""
+    B, T, _ = h.shape
+    d = 128
+    qkv = _lin(h, W["w_qkv"], round_in)
+    z = _lin(h, W["w_z"], round_in).view(B, T, hv, d)
+    b = _lin(h, W["w_b"], round_in)
+    a = _lin(h, W["w_a"], round_in)
+    y, new_conv = conv_silu(qkv, W["conv_w"].float(), conv_state)
+    q, k, v = delta_prep(y, hk, hv, d, d)
+    beta = b.sigmoid().transpose(1, 2)
+    g = (-W["a_log"].float().exp() * F.softplus(a + W["dt_bias"].float())).transpose(1, 2)
+    if T == 1 and length > 0:
+        out = delta_rule_step(q[:, :, 0], k[:, :, 0], v[:, :, 0], g[:, :, 0], beta[:, :, 0], state).unsqueeze(2)
+    else:
+        out, S = delta_rule_chunked(q, k, v, g, beta, state if length > 0 else None)
+        state.copy_(S)
+    out = out.transpose(1, 2)
+    o = gated_norm(out, z, W["gnorm_w"].float(), eps)
+    return _lin(o.reshape(B, T, hv * d), W["w_out"], round_in), new_conv
+
+
+def gated_attention_mixer(h, W: dict, kc, vc, pos: int, H: int, KV: int, HD: int = 256, rotary_dim: int = 64,
+                          theta: float = 1e7, eps: float = 1e-6, round_in: bool = True):
+    """GatedAttention.forward (hybrid.py:280-311) with the cache rows written at pos..pos+T-1."""
+    B, T, _ = h.shape
+    qg = _lin(h, W["w_q"], round_in).view(B, T, H, 2 * HD)
+    k = _lin(h, W["w_k"], round_in).view(B, T, KV, HD)
+    v = _lin(h, W["w_v"], round_in).view(B, T, KV, HD)
+    q, gate = attn_prep(qg, k, v, W["q_norm"].float(), W["k_norm"].float(), kc, vc, pos, rotary_dim, theta, eps)
+    y = gated_attention_out(attention_core(q, kc, vc, pos, KV), gate)
+    return _lin(y, W["w_o"], round_in)
+
+
+def hybrid_stack_forward(x, layers: list, kinds: list, cache: dict, cfg: dict, round_in: bool = True):
+    """HybridBlock.forward with the MoE FFN as identity (hybrid.py:812-843): per layer
+    x = x + mixer(znorm(x)). cache: {'length', 'conv': [..], 'state': [..], 'k': [..], 'v': [..]}
+    per-kind lists, updated. Returns the new x."""
+    delta_i = attn_i = 0
+    for W, kind in zip(layers, kinds):
+        h = znorm(x, W["norm1"].float(), cfg["eps"])
+        if kind == "attn":
+            y = gated_attention_mixer(h, W, cache["k"][attn_i], cache["v"][attn_i], cache["length"], cfg["n_heads"],
+                                      cfg["n_kv"], cfg["head_dim"], cfg["rotary_dim"], cfg["rope_theta"], cfg["eps"],
+                                      round_in)
+            attn_i += 1
+        else:
+            y, cache["conv"][delta_i] = gated_deltanet_mixer(h, W, cache["conv"][delta_i], cache["state"][delta_i],
+                                                             cache["length"], cfg["hk"], cfg["hv"], cfg["eps"],
+                                                             round_in)
+            delta_i += 1
+        x = x + y
+    cache["length"] += x.shape[1]
+    return x
