@@ -184,6 +184,58 @@ def bench_attention_prefill(torch, ops, dev, T=2048, reps=10):
             "tflops": round(tf, 2), "mfma_frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4)}
 
 
+def bench_stack(torch, ops, dev, B=16, T=2048, steps=256):
+    """Config 4: 40-layer hybrid mixer stack (3 DeltaNet + 1 attention, x10; d 2048), bf16
+    projection weights ~N(0, 0.02) (random init), MoE FFN as identity, bf16 embedding table
+    ~N(0, 0.02) with random token ids. Prefill B x T tokens, then `steps` decode steps at B."""
+    bf = torch.bfloat16
+    cfg = dict(d_model=2048, hk=16, hv=32, n_heads=16, n_kv=2, head_dim=256, rotary_dim=64, rope_theta=1e7, eps=1e-6)
+    kinds = (["delta"] * 3 + ["attn"]) * 10
+    C = 2 * 16 * 128 + 32 * 128
+    seed = [100]
+
+    def w(*shape, std=0.02):
+        seed[0] += 1
+        return ops.fill_normal(torch.empty(*shape, device=dev, dtype=bf), seed[0], 0.0, std)
+    layers = []
+    for kind in kinds:
+        W = {"norm1": w(2048, std=0.0)}
+        if kind == "delta":
+            W.update(w_qkv=w(C, 2048), w_z=w(4096, 2048), w_b=w(32, 2048), w_a=w(32, 2048), conv_w=w(C, 4, std=0.05),
+                     a_log=w(32, std=0.0), dt_bias=w(32, std=0.0), gnorm_w=w(128, std=0.0), w_out=w(2048, 4096))
+            W["dt_bias"].fill_(1.0)
+            W["gnorm_w"].fill_(1.0)
+        else:
+            W.update(w_q=w(8192, 2048), w_k=w(512, 2048), w_v=w(512, 2048), w_o=w(2048, 4096), q_norm=w(256, std=0.0),
+                     k_norm=w(256, std=0.0))
+        layers.append(W)
+    table = w(4096, 2048)
+    stack = ops.HybridStack(cfg, kinds, layers, max_batch=B, max_tokens=B * T, max_context=T + steps)
+    ids = torch.randint(0, 4096, (B, T + steps), generator=torch.Generator().manual_seed(5), dtype=torch.int32).to(dev)
+    e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+    # warm-up pass (also builds rocBLAS kernels), then the timed run from a reset state
+    x = ops.embed(table, ids[:, :T].reshape(-1)).view(B, T, 2048)
+    stack.forward(x)
+    stack.reset()
+    torch.cuda.synchronize()
+    e[0].record()
+    x = ops.embed(table, ids[:, :T].reshape(-1)).view(B, T, 2048)
+    stack.forward(x)
+    e[1].record()
+    for s in range(steps):
+        xt = ops.embed(table, ids[:, T + s].contiguous()).view(B, 1, 2048)
+        stack.forward(xt)
+    e[2].record()
+    torch.cuda.synchronize()
+    pre_ms, dec_ms = e[0].elapsed_time(e[1]), e[1].elapsed_time(e[2])
+    stack.close()
+    return {"workload": f"config4: 40-layer mixer stack, d 2048, prefill {B}x{T} then {steps} decode steps at B={B}",
+            "prefill_ms": round(pre_ms, 3), "prefill_tok_s": round(B * T / (pre_ms * 1e-3), 1),
+            "decode_ms_per_step": round(dec_ms / steps, 4), "decode_tok_s": round(B * steps / (dec_ms * 1e-3), 1),
+            "total_tok_s": round(B * (T + steps) / ((pre_ms + dec_ms) * 1e-3), 1),
+            "finite": bool(torch.isfinite(xt).all().item())}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -273,6 +325,7 @@ def main():
     res["prefill"] = bench_prefill(torch, ops, dev)
     res["attention_decode"] = bench_attention_decode(torch, ops, dev)
     res["attention_prefill"] = bench_attention_prefill(torch, ops, dev)
+    res["stack"] = bench_stack(torch, ops, dev)
     if args.calib_copy:
         src = torch.empty(1 << 28, device=dev)  # 1 GiB fp32
         dst = torch.empty_like(src)
