@@ -10,7 +10,7 @@ from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libaegist_mixer.so"
 
-F32, BF16 = 0, 1
+F32, BF16, I8 = 0, 1, 2
 
 P = C.c_void_p
 I = C.c_int
@@ -57,6 +57,10 @@ SIGNATURES: dict[str, tuple] = {
     "aegist_stack_length": (I, [P]),
     "aegist_stack_forward": (I, [P, P, I, I, P]),
     "aegist_embed_bf16": (I, [P, P, P, I, I, P]),
+    "aegist_gemv_i8": (I, [P, P, P, P, I, I, I, P]),
+    "aegist_gemv_bf16": (I, [P, P, P, I, I, P]),
+    "aegist_gemm_i8": (I, [P, P, P, P, I, I, I, I, P]),
+    "aegist_linear": (I, [P, I, LL, P, I, P, P, LL, I, I, I, I, P]),
 }
 
 

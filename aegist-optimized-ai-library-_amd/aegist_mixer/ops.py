@@ -12,7 +12,7 @@ from __future__ import annotations
 
 import torch
 
-from ._lib import BF16, F32, AegistError, call, lib
+from ._lib import BF16, F32, I8, AegistError, call, lib
 
 _DT = {torch.float32: F32, torch.bfloat16: BF16}
 
@@ -258,6 +258,74 @@ def engine_gated_norm(o, z, w, eps=1e-6):
 
 
 # --- the hybrid mixer stack (config 4) ----------------------------------------------------------
+
+# --- projections (QLinear, aegist/model.py:78-93; engine gemv_i8 / gemm_i8 / gemv_bf16) -------
+
+def linear(x, weight, scale=None, out=None, accumulate: bool = False):
+    """out[..., n] (+)= scale[n] * sum_k x[..., k] weight[n, k] in fp32.
+
+    x: [..., K] fp32 or bf16 (rows contiguous); weight: [N, K] int8 (QLinear.qweight) or bf16;
+    scale: [N] bf16 (QLinear.scale) or None; out: fp32 [..., N] (allocated if None; with
+    accumulate=True the product is added into it, the engine's fused residual add)."""
+    K = x.shape[-1]
+    N = weight.shape[0]
+    if weight.dim() != 2 or weight.shape[1] != K:
+        raise AegistError("shape", -1, f"weight {tuple(weight.shape)} does not match x [..., {K}]")
+    x2 = x.reshape(-1, K)
+    if x2.stride(1) != 1:
+        raise AegistError("layout", -1, "x rows must be contiguous")
+    _need_contig(weight, scale)
+    M = x2.shape[0]
+    if out is None:
+        if accumulate:
+            raise AegistError("shape", -1, "accumulate needs out")
+        out = torch.empty(*x.shape[:-1], N, dtype=torch.float32, device=x.device)
+    _need_contig(out)
+    if out.dtype != torch.float32 or out.numel() != M * N:
+        raise AegistError("shape", -1, "out must be fp32 [..., N]")
+    if weight.dtype == torch.int8:
+        wdt = I8
+    elif weight.dtype == torch.bfloat16:
+        wdt = BF16
+    else:
+        raise AegistError("dtype", -3, "weight must be int8 or bf16")
+    if scale is not None and (scale.dtype != torch.bfloat16 or scale.numel() != N):
+        raise AegistError("shape", -1, "scale must be bf16 [N]")
+    call("aegist_linear", _p(x2), _dt(x2), x2.stride(0), _p(weight), wdt, _p(scale), _p(out), N, M, N, K,
+         int(accumulate), _stream())
+    return out
+
+
+def gemv_i8(x, qweight, scale, y=None, accumulate: bool = False):
+    """Engine gemv_i8 (aegist.cu:85-91): y[n] (+)= scale[n] * (qweight[n] . x), x fp32 [K]."""
+    _need_contig(x, qweight, scale)
+    N, K = qweight.shape
+    if y is None:
+        y = torch.empty(N, dtype=torch.float32, device=x.device)
+    call("aegist_gemv_i8", _p(x), _p(qweight), _p(scale), _p(y), N, K, int(accumulate), _stream())
+    return y
+
+
+def gemm_i8(x, qweight, scale, y=None, accumulate: bool = False):
+    """Engine gemm_i8 (aegist.cu:126-172): Y[m, n] (+)= scale[n] * (qweight[n] . X[m]), X fp32 [M, K]."""
+    _need_contig(x, qweight, scale)
+    M, K = x.shape
+    N = qweight.shape[0]
+    if y is None:
+        y = torch.empty(M, N, dtype=torch.float32, device=x.device)
+    call("aegist_gemm_i8", _p(x), _p(qweight), _p(scale), _p(y), M, N, K, int(accumulate), _stream())
+    return y
+
+
+def gemv_bf16(x, weight, y=None):
+    """Engine gemv_bf16 (aegist.cu:108-124): y[n] = weight[n] . x, x fp32 [K], weight bf16 [N, K]."""
+    _need_contig(x, weight)
+    N, K = weight.shape
+    if y is None:
+        y = torch.empty(N, dtype=torch.float32, device=x.device)
+    call("aegist_gemv_bf16", _p(x), _p(weight), _p(y), N, K, _stream())
+    return y
+
 
 class HybridStack:
     """Batched mixer stack on the device (aegist_stack_* of the C ABI): per layer

@@ -1,0 +1,325 @@
+// Projections around the mixer: the weight-streaming matmuls of QLinear
+// (aegist/model.py:78-93: int8 weight, per-output-row absmax scale in bf16) and of plain bf16
+// weights, as the engine runs them (aegist_rs/kernels/aegist.cu:84-172: gemv_i8, gemv_bf16,
+// gemm_i8; called through HybridEngine::mm, aegist_rs/src/hybrid.rs:717-735):
+//     Y[m, n] (+)= scale[n] * sum_k X[m, k] W[n, k]
+// with fp32 accumulation. accumulate = 1 adds into Y (the residual add of the out-projections).
+//
+// At decode sizes (M = batch <= 64) the op streams the weight matrix once from HBM, so the
+// kernel is built around that stream: each wave owns RT 16-row tiles of W and a contiguous run
+// of 64-wide k steps, loads 16 bytes of int8 weights (or 32 of bf16) per lane per step, and
+// feeds v_mfma_f32_16x16x32_bf16 with W as the A operand and X^T as the B operand, so every
+// weight byte is used by MT 16-row tiles of X at once. Four waves of a workgroup interleave
+// their k steps (neighbouring waves read neighbouring 64-byte runs of the same rows) and add
+// their partial tiles through LDS at the end, where the row scale and the accumulate are fused
+// into the store.
+//
+// int8 and bf16 weights are exact in bf16. An fp32 X is split into bf16 hi + lo
+// (x = hi + lo + O(2^-17 |x|)) and both halves go through the MFMA, so the result matches an
+// fp32 dot product to ~1e-5 relative; a bf16 X needs only the hi half.
+#include "common.h"
+
+using namespace aegist;
+
+namespace {
+
+constexpr int KSTEP = 64;  // k per wave step: 16 bytes of int8 (two MFMA k-blocks of 32) per lane
+
+typedef int int4v __attribute__((ext_vector_type(4)));
+
+// 16 consecutive weights of one row starting at k (zero outside the row), as two bf16x8
+// operands: lo = k .. k+7, hi = k+8 .. k+15.
+template <typename TW> struct WLoad;
+template <> struct WLoad<int8_t> {
+    int4v raw;
+    __device__ __forceinline__ void load(const int8_t* row, int k, int K, bool ok) {
+        raw = (ok && k < K) ? *(const int4v*)(row + k) : int4v{0, 0, 0, 0};
+    }
+    __device__ __forceinline__ void cvt(bf16x8& a, bf16x8& b) const {
+        // int8 -> fp32 is exact (one sign-extending byte conversion each) and |q| <= 128 keeps
+        // 8 significant bits, so the top half of the fp32 pattern is the exact bf16; one byte
+        // permute packs two of them
+        uint32_t pa[4], pb[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t d = (uint32_t)raw[i];
+            const float f0 = (float)(int8_t)d, f1 = (float)(int8_t)(d >> 8);
+            const float f2 = (float)(int8_t)(d >> 16), f3 = (float)(int8_t)(d >> 24);
+            const uint32_t p01 = __builtin_amdgcn_perm(__float_as_uint(f1), __float_as_uint(f0), 0x07060302u);
+            const uint32_t p23 = __builtin_amdgcn_perm(__float_as_uint(f3), __float_as_uint(f2), 0x07060302u);
+            if (i < 2) {
+                pa[2 * i] = p01;
+                pa[2 * i + 1] = p23;
+            } else {
+                pb[2 * (i - 2)] = p01;
+                pb[2 * (i - 2) + 1] = p23;
+            }
+        }
+        a = __builtin_bit_cast(bf16x8, pa);
+        b = __builtin_bit_cast(bf16x8, pb);
+    }
+};
+template <> struct WLoad<uint16_t> {
+    bf16x8 r0, r1;
+    __device__ __forceinline__ void load(const uint16_t* row, int k, int K, bool ok) {
+        if (ok && k < K) {
+            r0 = *(const bf16x8*)(row + k);
+            r1 = *(const bf16x8*)(row + k + 8);
+        } else {
+            r0 = bf16x8{0, 0, 0, 0, 0, 0, 0, 0};
+            r1 = r0;
+        }
+    }
+    __device__ __forceinline__ void cvt(bf16x8& a, bf16x8& b) const {
+        a = r0;
+        b = r1;
+    }
+};
+
+// 16 consecutive activations of one row of X starting at k, as bf16 hi (and lo for fp32 X).
+template <typename TX> struct XLoad;
+template <> struct XLoad<float> {
+    static constexpr bool kLo = true;
+    f32x4 r[4];
+    __device__ __forceinline__ void load(const float* row, int k, int K, bool ok) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) r[i] = (ok && k < K) ? *(const f32x4*)(row + k + 4 * i) : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    // x = hi + lo with hi = x truncated to bf16 (exact difference) and lo rounded to bf16:
+    // |x - hi - lo| <= 2^-16 |x|
+    __device__ __forceinline__ void cvt(bf16x8& ha, bf16x8& hb, bf16x8& la, bf16x8& lb) const {
+        uint32_t h[8], l[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const float x0 = r[i / 2][2 * (i % 2)], x1 = r[i / 2][2 * (i % 2) + 1];
+            h[i] = __builtin_amdgcn_perm(__float_as_uint(x1), __float_as_uint(x0), 0x07060302u);
+            typedef float f2 __attribute__((ext_vector_type(2)));
+            typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+            const f2 lo = {x0 - __uint_as_float(__float_as_uint(x0) & 0xffff0000u),
+                           x1 - __uint_as_float(__float_as_uint(x1) & 0xffff0000u)};
+            l[i] = __builtin_bit_cast(uint32_t, __builtin_convertvector(lo, b2));
+        }
+        ha = __builtin_bit_cast(bf16x8, *(uint32_t(*)[4])h);
+        hb = __builtin_bit_cast(bf16x8, *(uint32_t(*)[4])(h + 4));
+        la = __builtin_bit_cast(bf16x8, *(uint32_t(*)[4])l);
+        lb = __builtin_bit_cast(bf16x8, *(uint32_t(*)[4])(l + 4));
+    }
+};
+template <> struct XLoad<uint16_t> {
+    static constexpr bool kLo = false;
+    bf16x8 r0, r1;
+    __device__ __forceinline__ void load(const uint16_t* row, int k, int K, bool ok) {
+        if (ok && k < K) {
+            r0 = *(const bf16x8*)(row + k);
+            r1 = *(const bf16x8*)(row + k + 8);
+        } else {
+            r0 = bf16x8{0, 0, 0, 0, 0, 0, 0, 0};
+            r1 = r0;
+        }
+    }
+    __device__ __forceinline__ void cvt(bf16x8& ha, bf16x8& hb, bf16x8&, bf16x8&) const {
+        ha = r0;
+        hb = r1;
+    }
+};
+
+// One workgroup: rows [n0, n0 + 16 RT) of W against rows [m0, m0 + 16 MT) of X, all of K.
+// grid = (ceil(N / 16RT), ceil(M / 16MT)); NWAVE waves split the k steps.
+template <typename TW, typename TX, int MT, int RT, int NWAVE>
+__global__ __launch_bounds__(64 * NWAVE) void proj_skinny_kernel(const TX* __restrict__ X, long long ldx,
+                                                          const TW* __restrict__ W, const uint16_t* __restrict__ scale,
+                                                          float* __restrict__ Y, long long ldy, int M, int N, int K,
+                                                          int accumulate) {
+    __shared__ f32x4 red[NWAVE][RT * MT][WAVE];
+    const int lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
+    const int r16 = lane % 16, g = lane / 16;
+    const int n0 = blockIdx.x * 16 * RT, m0 = blockIdx.y * 16 * MT;
+
+    const TW* wrow[RT];
+    bool wok[RT];
+#pragma unroll
+    for (int rt = 0; rt < RT; rt++) {
+        const int n = n0 + 16 * rt + r16;
+        wok[rt] = n < N;
+        wrow[rt] = W + (size_t)(wok[rt] ? n : 0) * K;
+    }
+    const TX* xrow[MT];
+    bool xok[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++) {
+        const int m = m0 + 16 * mt + r16;
+        xok[mt] = m < M;
+        xrow[mt] = X + (size_t)(xok[mt] ? m : 0) * ldx;
+    }
+
+    f32x4 acc[RT][MT];
+#pragma unroll
+    for (int rt = 0; rt < RT; rt++)
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) acc[rt][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    // loads of DEPTH steps are issued together, then consumed: with ~4 steps per wave that is
+    // every load of the wave in flight at once
+    constexpr int DEPTH = (XLoad<TX>::kLo ? MT * 16 : MT * 8) + RT * 8 <= 32 ? 4 : 2;
+    WLoad<TW> wl[DEPTH][RT];
+    XLoad<TX> xl[DEPTH][MT];
+    auto fetch = [&](int buf, int step) {
+        const int k = step * KSTEP + 16 * g;
+#pragma unroll
+        for (int rt = 0; rt < RT; rt++) wl[buf][rt].load(wrow[rt], k, K, wok[rt]);
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) xl[buf][mt].load(xrow[mt], k, K, xok[mt]);
+    };
+    auto compute = [&](int buf) {
+        bf16x8 xa[MT], xb[MT], la[MT], lb[MT];
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) xl[buf][mt].cvt(xa[mt], xb[mt], la[mt], lb[mt]);
+#pragma unroll
+        for (int rt = 0; rt < RT; rt++) {
+            bf16x8 wa, wb;
+            wl[buf][rt].cvt(wa, wb);
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++) {
+                acc[rt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa, xa[mt], acc[rt][mt], 0, 0, 0);
+                acc[rt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wb, xb[mt], acc[rt][mt], 0, 0, 0);
+                if (XLoad<TX>::kLo) {
+                    acc[rt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa, la[mt], acc[rt][mt], 0, 0, 0);
+                    acc[rt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wb, lb[mt], acc[rt][mt], 0, 0, 0);
+                }
+            }
+        }
+    };
+
+    // wave w takes steps w, w + NWAVE, ... (neighbouring waves read neighbouring runs of a row);
+    // steps past the end load zeros and are skipped
+    const int nsteps = (K + KSTEP - 1) / KSTEP;
+    for (int s0 = wave; s0 < nsteps; s0 += DEPTH * NWAVE) {
+#pragma unroll
+        for (int d = 0; d < DEPTH; d++) fetch(d, s0 + d * NWAVE);
+#pragma unroll
+        for (int d = 0; d < DEPTH; d++)
+            if (s0 + d * NWAVE < nsteps) compute(d);
+    }
+
+#pragma unroll
+    for (int rt = 0; rt < RT; rt++)
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) red[wave][rt * MT + mt][lane] = acc[rt][mt];
+    __syncthreads();
+    // tile t is finished by wave t % 4: lane holds column m = m0 + 16 mt + r16, rows n 4g .. 4g+3
+    for (int t = wave; t < RT * MT; t += NWAVE) {
+        f32x4 v = red[0][t][lane];
+#pragma unroll
+        for (int w = 1; w < NWAVE; w++) v += red[w][t][lane];
+        const int rt = t / MT, mt = t % MT;
+        const int m = m0 + 16 * mt + r16;
+        if (m >= M) continue;
+        float* yrow = Y + (size_t)m * ldy;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int n = n0 + 16 * rt + 4 * g + j;
+            if (n >= N) continue;
+            float y = v[j] * (scale ? bf2f(scale[n]) : 1.f);
+            yrow[n] = accumulate ? yrow[n] + y : y;
+        }
+    }
+}
+
+template <typename TW, typename TX, int MT, int RT, int NW>
+void launch_k(const TX* X, long long ldx, const TW* W, const uint16_t* scale, float* Y, long long ldy, int M, int N,
+              int K, int accumulate, hipStream_t st) {
+    const dim3 grid((N + 16 * RT - 1) / (16 * RT), (M + 16 * MT - 1) / (16 * MT));
+    proj_skinny_kernel<TW, TX, MT, RT, NW><<<grid, 64 * NW, 0, st>>>(X, ldx, W, scale, Y, ldy, M, N, K, accumulate);
+}
+
+// Shape of the launch: about 2048 waves in all (8 per CU, enough loads in flight to cover HBM
+// latency) with at least two k steps per wave; two row tiles per wave where that is reachable
+// (each activation load then feeds twice the weights), else one.
+template <typename TW, typename TX, int MT>
+void launch_mt(const TX* X, long long ldx, const TW* W, const uint16_t* scale, float* Y, long long ldy, int M, int N,
+               int K, int accumulate, hipStream_t st) {
+    const long long gy = (M + 16 * MT - 1) / (16 * MT);
+    const int nsteps = (K + KSTEP - 1) / KSTEP;
+    const long long t2 = (N + 31) / 32 * gy, t1 = (N + 15) / 16 * gy;
+    constexpr int kTarget = 2048;
+#define AEG_PROJ(RT, NW) return launch_k<TW, TX, MT, RT, NW>(X, ldx, W, scale, Y, ldy, M, N, K, accumulate, st)
+    if (t2 * 4 >= kTarget) AEG_PROJ(2, 4);
+    if (t2 * 8 >= kTarget && nsteps >= 16) AEG_PROJ(2, 8);
+    if (t1 * 4 >= kTarget) AEG_PROJ(1, 4);
+    if (t1 * 8 >= kTarget || nsteps < 32) {
+        if (nsteps >= 16) AEG_PROJ(1, 8);
+        AEG_PROJ(1, 4);
+    }
+    // sixteen waves per workgroup leave 128 registers per lane: one m tile only
+    if constexpr (MT == 1) AEG_PROJ(1, 16);
+    else AEG_PROJ(1, 8);
+#undef AEG_PROJ
+}
+
+template <typename TW, typename TX>
+int run_proj(const TX* X, long long ldx, const TW* W, const uint16_t* scale, float* Y, long long ldy, int M, int N,
+             int K, int accumulate, hipStream_t st) {
+    // m tiles per workgroup: the whole batch up to 64 rows of bf16 X (32 of fp32 X, whose hi/lo
+    // operands take twice the registers), so the weights are read once; larger M is covered by
+    // a grid of row groups
+    if (M <= 16) {
+        launch_mt<TW, TX, 1>(X, ldx, W, scale, Y, ldy, M, N, K, accumulate, st);
+    } else if constexpr (XLoad<TX>::kLo) {
+        launch_mt<TW, TX, 2>(X, ldx, W, scale, Y, ldy, M, N, K, accumulate, st);
+    } else {
+        if (M <= 32) launch_mt<TW, TX, 2>(X, ldx, W, scale, Y, ldy, M, N, K, accumulate, st);
+        else if (M <= 48) launch_mt<TW, TX, 3>(X, ldx, W, scale, Y, ldy, M, N, K, accumulate, st);
+        else launch_mt<TW, TX, 4>(X, ldx, W, scale, Y, ldy, M, N, K, accumulate, st);
+    }
+    return after_launch("proj_skinny");
+}
+
+}  // namespace
+
+namespace aegist {
+
+// Shared checks: 16-byte rows for the vector loads.
+int launch_proj(const void* X, int x_dtype, long long ldx, const void* W, int w_dtype, const uint16_t* scale, float* Y,
+                long long ldy, int M, int N, int K, int accumulate, hipStream_t st) {
+    if (M < 0 || N < 0 || K < 0) return fail(AEGIST_ERR_SHAPE, "proj: negative size");
+    if (M == 0 || N == 0) return 0;
+    if (K % 16) return fail(AEGIST_ERR_SHAPE, "proj: K must be a multiple of 16");
+    if (ldy < N) return fail(AEGIST_ERR_SHAPE, "proj: ldy < N");
+    const int xs = x_dtype == AEGIST_F32 ? 4 : 2;
+    if (ldx < K || (ldx * xs) % 16 || (uintptr_t)X % 16 || (uintptr_t)W % 16)
+        return fail(AEGIST_ERR_SHAPE, "proj: X and W need 16-byte aligned rows (ldx >= K)");
+    if (w_dtype == AEGIST_I8 && x_dtype == AEGIST_F32)
+        return run_proj<int8_t, float>((const float*)X, ldx, (const int8_t*)W, scale, Y, ldy, M, N, K, accumulate, st);
+    if (w_dtype == AEGIST_I8 && x_dtype == AEGIST_BF16)
+        return run_proj<int8_t, uint16_t>((const uint16_t*)X, ldx, (const int8_t*)W, scale, Y, ldy, M, N, K,
+                                          accumulate, st);
+    if (w_dtype == AEGIST_BF16 && x_dtype == AEGIST_F32)
+        return run_proj<uint16_t, float>((const float*)X, ldx, (const uint16_t*)W, scale, Y, ldy, M, N, K, accumulate,
+                                         st);
+    if (w_dtype == AEGIST_BF16 && x_dtype == AEGIST_BF16)
+        return run_proj<uint16_t, uint16_t>((const uint16_t*)X, ldx, (const uint16_t*)W, scale, Y, ldy, M, N, K,
+                                            accumulate, st);
+    return fail(AEGIST_ERR_DTYPE, "proj: W must be AEGIST_I8 or AEGIST_BF16, X AEGIST_F32 or AEGIST_BF16");
+}
+
+}  // namespace aegist
+
+extern "C" int aegist_gemv_i8(const float* x, const int8_t* W, const uint16_t* scale, float* y, int N, int K,
+                              int accumulate, void* stream) {
+    return launch_proj(x, AEGIST_F32, K, W, AEGIST_I8, scale, y, N, 1, N, K, accumulate, AEG_STREAM(stream));
+}
+
+extern "C" int aegist_gemv_bf16(const float* x, const uint16_t* W, float* y, int N, int K, void* stream) {
+    return launch_proj(x, AEGIST_F32, K, W, AEGIST_BF16, nullptr, y, N, 1, N, K, 0, AEG_STREAM(stream));
+}
+
+extern "C" int aegist_gemm_i8(const float* X, const int8_t* W, const uint16_t* scale, float* Y, int M, int N, int K,
+                              int accumulate, void* stream) {
+    return launch_proj(X, AEGIST_F32, K, W, AEGIST_I8, scale, Y, N, M, N, K, accumulate, AEG_STREAM(stream));
+}
+
+extern "C" int aegist_linear(const void* X, int x_dtype, long long ldx, const void* W, int w_dtype,
+                             const uint16_t* scale, float* Y, long long ldy, int M, int N, int K, int accumulate,
+                             void* stream) {
+    return launch_proj(X, x_dtype, ldx, W, w_dtype, scale, Y, ldy, M, N, K, accumulate, AEG_STREAM(stream));
+}

@@ -6,9 +6,10 @@
 // (hybrid.py:280-311). The stack owns the recurrent state, conv state and bf16 KV cache of every
 // layer (HybridCache, hybrid.py:171-260; the engine buffers of hybrid.rs:607-629).
 //
-// Projections are plain GEMMs and go to rocBLAS (bf16 operands, fp32 accumulation and output,
-// the out-projections accumulate straight into the fp32 residual with beta = 1); every other op
-// is one of this library's kernels.
+// Projections are plain GEMMs (bf16 operands, fp32 accumulation and output; the out-projections
+// accumulate straight into the fp32 residual): decode-sized ones on this library's
+// weight-streaming MFMA kernel, prefill-sized ones on rocBLAS; every other op is one of this
+// library's kernels.
 #include "common.h"
 
 #include <rocblas/rocblas.h>
@@ -34,6 +35,8 @@ int stack_attn_decode(const float* qn, const uint16_t* kc, const uint16_t* vc, c
 int stack_attn_prefill(const float* qn, const uint16_t* kc, const uint16_t* vc, const float* qg, float* out, int B,
                        int H, int KV, int T, int pos, int cap, float scale, hipStream_t st);
 size_t decode_workspace_bytes(int B, int H, int KV, int L, bool with_q);
+int launch_proj(const void* X, int x_dtype, long long ldx, const void* W, int w_dtype, const uint16_t* scale, float* Y,
+                long long ldy, int M, int N, int K, int accumulate, hipStream_t st);
 }  // namespace aegist
 
 using namespace aegist;
@@ -83,8 +86,15 @@ int alloc(Stack* s, void** p, size_t bytes) {
 }
 
 // Y[M, N] (row-major, leading dim ldy) = A[M, K] (bf16 row-major) . W[N, K]^T (bf16 row-major)
-//                                          + beta * Y
-int gemm(Stack* s, const uint16_t* A, const uint16_t* W, float* Y, int M, int N, int K, int ldy, float beta) {
+//                                          + beta * Y,   beta in {0, 1}
+// Decode-sized M (<= 64 rows) goes to this library's weight-streaming kernel (one pass over W,
+// no host-side algorithm lookup); larger M to rocBLAS on the caller's stream.
+int gemm(Stack* s, const uint16_t* A, const uint16_t* W, float* Y, int M, int N, int K, int ldy, float beta,
+         hipStream_t stream) {
+    if (M <= 64 && K % 16 == 0)
+        return launch_proj(A, AEGIST_BF16, K, W, AEGIST_BF16, nullptr, Y, ldy, M, N, K, beta != 0.f, stream);
+    if (rocblas_set_stream(s->blas, stream) != rocblas_status_success)
+        return fail(AEGIST_ERR_SHAPE, "rocblas_set_stream failed");
     const float alpha = 1.f;
     rocblas_status st = rocblas_gemm_ex(s->blas, rocblas_operation_transpose, rocblas_operation_none, N, M, K, &alpha, W,
                                         rocblas_datatype_bf16_r, K, A, rocblas_datatype_bf16_r, K, &beta, Y,
@@ -107,10 +117,10 @@ int delta_layer(Stack* s, const AegistLayerWeights& w, int sl, float* x, int B, 
     const size_t mb = (size_t)c.max_batch;
     float* conv = s->conv + (size_t)sl * mb * C * 3;
     float* rec = s->rec + (size_t)sl * mb * HV * D * D;
-    RC(gemm(s, s->hb, w.w_qkv, s->proj, rows, C, dm, C, 0.f));
-    RC(gemm(s, s->hb, w.w_z, s->z, rows, HV * D, dm, HV * D, 0.f));
-    RC(gemm(s, s->hb, w.w_b, s->ba, rows, HV, dm, 2 * HV, 0.f));
-    RC(gemm(s, s->hb, w.w_a, s->ba + HV, rows, HV, dm, 2 * HV, 0.f));
+    RC(gemm(s, s->hb, w.w_qkv, s->proj, rows, C, dm, C, 0.f, st));
+    RC(gemm(s, s->hb, w.w_z, s->z, rows, HV * D, dm, HV * D, 0.f, st));
+    RC(gemm(s, s->hb, w.w_b, s->ba, rows, HV, dm, 2 * HV, 0.f, st));
+    RC(gemm(s, s->hb, w.w_a, s->ba + HV, rows, HV, dm, 2 * HV, 0.f, st));
     RC(launch_gates_from_proj(s->ba, w.a_log, w.dt_bias, s->g, s->beta, rows, HV, st));
     const float qscale = 1.f / sqrtf((float)D);
     if (T == 1) {
@@ -126,7 +136,7 @@ int delta_layer(Stack* s, const AegistLayerWeights& w, int sl, float* x, int B, 
                                 qscale, 1e-6f, s->ws, s->ws_bytes, st));
     }
     RC(launch_gated_norm_bf16(s->o, s->z, w.gnorm_w, s->ob, rows * HV, D, c.eps, st));
-    return gemm(s, s->ob, w.w_out, x, rows, dm, HV * D, dm, 1.f);
+    return gemm(s, s->ob, w.w_out, x, rows, dm, HV * D, dm, 1.f, st);
 }
 
 int attn_layer(Stack* s, const AegistLayerWeights& w, int sl, float* x, int B, int T, hipStream_t st) {
@@ -137,9 +147,9 @@ int attn_layer(Stack* s, const AegistLayerWeights& w, int sl, float* x, int B, i
     uint16_t* vc = s->vc + (size_t)sl * mb * KV * cap * HD;
     float* kp = s->kv2;
     float* vp = s->kv2 + (size_t)c.max_tokens * KV * HD;
-    RC(gemm(s, s->hb, w.w_q, s->proj, rows, 2 * H * HD, dm, 2 * H * HD, 0.f));
-    RC(gemm(s, s->hb, w.w_k, kp, rows, KV * HD, dm, KV * HD, 0.f));
-    RC(gemm(s, s->hb, w.w_v, vp, rows, KV * HD, dm, KV * HD, 0.f));
+    RC(gemm(s, s->hb, w.w_q, s->proj, rows, 2 * H * HD, dm, 2 * H * HD, 0.f, st));
+    RC(gemm(s, s->hb, w.w_k, kp, rows, KV * HD, dm, KV * HD, 0.f, st));
+    RC(gemm(s, s->hb, w.w_v, vp, rows, KV * HD, dm, KV * HD, 0.f, st));
     RC(launch_attn_prep(s->proj, kp, vp, AEGIST_F32, w.q_norm, w.k_norm, s->y, kc, vc, B, T, H, KV, HD, c.rotary_dim,
                         s->length, (int)cap, c.eps, c.rope_theta, st, nullptr, 0));
     const float scale = 1.f / sqrtf((float)HD);
@@ -149,7 +159,7 @@ int attn_layer(Stack* s, const AegistLayerWeights& w, int sl, float* x, int B, i
     else
         RC(stack_attn_prefill(s->y, kc, vc, s->proj, s->o, B, H, KV, T, s->length, (int)cap, scale, st));
     RC(launch_cast_bf16(s->o, s->ob, (size_t)rows * H * HD, st));
-    return gemm(s, s->ob, w.w_o, x, rows, dm, H * HD, dm, 1.f);
+    return gemm(s, s->ob, w.w_o, x, rows, dm, H * HD, dm, 1.f, st);
 }
 
 }  // namespace

@@ -184,6 +184,53 @@ def bench_attention_prefill(torch, ops, dev, T=2048, reps=10):
             "tflops": round(tf, 2), "mfma_frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4)}
 
 
+def bench_proj(torch, ops, dev, reps=3):
+    """Decode-sized projections (QLinear int8 + bf16 scale with fp32 activations, as the engine
+    ships them; bf16 weights with bf16 activations, as config 4 runs them). The timed loop walks
+    a ring of distinct weight matrices totalling > 1 GB so that every launch streams its weights
+    from HBM, as a 40-layer decode step does (a single 17-67 MB matrix would sit in the MALL).
+    Bytes per launch = W + X + Y."""
+    from aegist_mixer._lib import BF16, F32, I8, call
+    stream = torch.cuda.current_stream().cuda_stream
+    out = []
+    for wdt, xdt, N, K in [(I8, F32, 8192, 2048), (BF16, BF16, 8192, 2048), (BF16, BF16, 2048, 4096)]:
+        wbytes = N * K * (1 if wdt == I8 else 2)
+        ncopy = max(2, (1 << 30) // wbytes + 1)
+        if wdt == I8:
+            Ws = [torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev) for _ in range(ncopy)]
+            sc = ops.fill_normal(torch.empty(N, device=dev, dtype=torch.bfloat16), 77, 1e-3, 0.0)
+        else:
+            Ws = [ops.fill_normal(torch.empty(N, K, device=dev, dtype=torch.bfloat16), 80 + i, 0.0, 0.02)
+                  for i in range(ncopy)]
+            sc = None
+        for M in (1, 16, 64):
+            X = ops.fill_normal(torch.empty(M, K, device=dev, dtype=torch.float32 if xdt == F32 else torch.bfloat16), 5)
+            Y = torch.empty(M, N, device=dev)
+
+            def run(Wm):
+                call("aegist_linear", X.data_ptr(), xdt, K, Wm.data_ptr(), wdt, None if sc is None else sc.data_ptr(),
+                     Y.data_ptr(), N, M, N, K, 0, stream)
+            for Wm in Ws[:2]:
+                run(Wm)
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(reps):
+                for Wm in Ws:
+                    run(Wm)
+            e1.record()
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) * 1e3 / (reps * ncopy)
+            nbytes = wbytes + M * K * X.element_size() + M * N * 4
+            gbs = nbytes / (us * 1e-6) / 1e9
+            out.append({"w": "int8" if wdt == I8 else "bf16", "x": "fp32" if xdt == F32 else "bf16", "M": M, "N": N,
+                        "K": K, "us": round(us, 2), "GB_s": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)})
+        del Ws
+        torch.cuda.empty_cache()
+    return {"workload": "decode projections Y[M,N] = X[M,K] W[N,K]^T (x scale), weights streamed from HBM",
+            "points": out}
+
+
 def bench_stack(torch, ops, dev, B=16, T=2048, steps=256):
     """Config 4: 40-layer hybrid mixer stack (3 DeltaNet + 1 attention, x10; d 2048), bf16
     projection weights ~N(0, 0.02) (random init), MoE FFN as identity, bf16 embedding table
@@ -325,6 +372,7 @@ def main():
     res["prefill"] = bench_prefill(torch, ops, dev)
     res["attention_decode"] = bench_attention_decode(torch, ops, dev)
     res["attention_prefill"] = bench_attention_prefill(torch, ops, dev)
+    res["proj"] = bench_proj(torch, ops, dev)
     res["stack"] = bench_stack(torch, ops, dev)
     if args.calib_copy:
         src = torch.empty(1 << 28, device=dev)  # 1 GiB fp32

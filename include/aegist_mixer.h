@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-enum { AEGIST_F32 = 0, AEGIST_BF16 = 1 };
+enum { AEGIST_F32 = 0, AEGIST_BF16 = 1, AEGIST_I8 = 2 /* weights only */ };
 
 enum {
     AEGIST_OK = 0,
@@ -201,8 +201,9 @@ int aegist_attention_core(const float* q, const uint16_t* kc, const uint16_t* vc
  * (HybridBlock.forward, aegist/hybrid.py:812-843; HybridEngine::forward_chunk / mixer,
  * aegist_rs/src/hybrid.rs:760-861). The stack owns every layer's recurrent state, conv state
  * and bf16 KV cache (HybridCache, hybrid.py:171-260; engine buffers hybrid.rs:607-629); all
- * sequences of a batch share one length. Projections run on rocBLAS (bf16 operands, fp32
- * accumulation), everything else on this library's kernels. Weights are caller-owned bf16,
+ * sequences of a batch share one length. Projections: bf16 operands, fp32 accumulation; up to
+ * 64 rows on this library's weight-streaming kernel (aegist_linear), more on rocBLAS; everything
+ * else on this library's kernels. Weights are caller-owned bf16,
  * row-major [out, in] as torch nn.Linear stores them.
  * ------------------------------------------------------------------------------------- */
 #define AEGIST_MAX_LAYERS 64
@@ -243,6 +244,25 @@ int aegist_stack_forward(void* handle, float* x, int B, int T, void* stream);
 /* out[i, :] = fp32(table[ids[i], :]) for n ids; the engine's embedding lookup
  * (hybrid.rs:743-758) done on the device. */
 int aegist_embed_bf16(const uint16_t* table, const int* ids, float* out, int n, int D, void* stream);
+
+/* -------------------------------------------------------------------------------------
+ * Projections (QLinear, aegist/model.py:78-93: int8 weight W [N, K] with a per-output-row bf16
+ * absmax scale; and plain bf16 weights):  Y[m, n] (+)= scale[n] * sum_k X[m, k] W[n, k],
+ * fp32 accumulation; accumulate != 0 adds into Y (the fused residual add). K % 16 == 0 and
+ * 16-byte aligned X / W rows. Weight-streaming MFMA kernel: one pass over W for M <= 64.
+ * ------------------------------------------------------------------------------------- */
+/* gemv_i8, aegist_rs/kernels/aegist.cu:85-91 (launched by HybridEngine::mm, hybrid.rs:717-724) */
+int aegist_gemv_i8(const float* x, const int8_t* W, const uint16_t* scale, float* y, int N, int K, int accumulate,
+                   void* stream);
+/* gemv_bf16, aegist_rs/kernels/aegist.cu:108-124 (the tied output head) */
+int aegist_gemv_bf16(const float* x, const uint16_t* W, float* y, int N, int K, void* stream);
+/* gemm_i8, aegist_rs/kernels/aegist.cu:126-172 (HybridEngine::mm for t > 1, hybrid.rs:725-734) */
+int aegist_gemm_i8(const float* X, const int8_t* W, const uint16_t* scale, float* Y, int M, int N, int K,
+                   int accumulate, void* stream);
+/* Strided form of the three above: X dtype AEGIST_F32 | AEGIST_BF16 (row stride ldx elements),
+ * W dtype AEGIST_I8 | AEGIST_BF16, scale NULL = 1, Y fp32 with row stride ldy. */
+int aegist_linear(const void* X, int x_dtype, long long ldx, const void* W, int w_dtype, const uint16_t* scale,
+                  float* Y, long long ldy, int M, int N, int K, int accumulate, void* stream);
 
 #ifdef __cplusplus
 }

@@ -251,6 +251,40 @@ def attention_decode(qg, k_new, v_new, q_norm_w, k_norm_w, kc, vc, pos: int, rot
     return gated_attention_out(y, gate).reshape(B, H, HD2 // 2)
 
 
+# --- projections: QLinear (model.py:78-93) and the engine matvecs (aegist.cu:52-172) --------
+
+def qlinear_quantize(weight: torch.Tensor):
+    """QLinear.__init__ (model.py:84-90): per-output-row absmax scale
+    s = max|w_row| (clamped at 1e-8) / 127; q = round(w / s) as int8 (round half to even);
+    the scale is kept in bf16 (after q was computed with the fp32 scale)."""
+    w = weight.float()
+    s = w.abs().amax(1, keepdim=True).clamp(min=1e-8) / 127.0
+    q = torch.round(w / s).to(torch.int8)
+    return q, s.to(torch.bfloat16).reshape(-1)
+
+
+def qlinear_engine(x: torch.Tensor, q: torch.Tensor, scale: torch.Tensor | None, y: torch.Tensor | None = None,
+                   accumulate: bool = False) -> torch.Tensor:
+    """The engine's int8 / bf16 matvec and matmul (aegist.cu:52-63 row_dot_i8, :85-91 gemv_i8,
+    :108-124 gemv_bf16, :126-172 gemm_i8): fp32 dot of the fp32 activation row with the weight
+    row (int8 or bf16 values taken exactly), times the row scale, optionally added into y.
+    Summed in fp64 here so the restatement carries no rounding of its own."""
+    acc = x.double() @ q.double().t()
+    if scale is not None:
+        acc = acc * scale.double()
+    acc = acc.float()
+    if accumulate:
+        return y.float() + acc
+    return acc
+
+
+def qlinear_torch(x: torch.Tensor, q: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
+    """QLinear.forward (model.py:92-93): F.linear(x, q.to(x.dtype) * scale.to(x.dtype)) - the
+    weight is dequantised in the activation dtype (bf16 rounding of q*s in a bf16 model)."""
+    w = q.to(x.dtype) * scale.to(x.dtype).reshape(-1, 1)
+    return F.linear(x, w)
+
+
 # --- composites: the mixers and the layer stack (config 4) ---------------------------------
 
 def _lin(x, w, round_in: bool):

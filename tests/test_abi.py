@@ -87,3 +87,19 @@ def test_engine_mirrors_reject_shapes():
     L = _lib.lib()
     assert L.aegist_delta_scan(None, None, None, None, 4, 8191, 16, 32, None) == -1
     assert L.aegist_l2norm_heads(None, 4, 100, 16, 128, 1.0, 1e-6, None) == -1
+
+
+def test_linear_rejects_shapes_and_dtypes():
+    L = _lib.lib()
+    # K % 16 != 0
+    assert L.aegist_linear(None, 0, 24, None, 2, None, None, 8, 2, 8, 24, 0, None) == -1
+    assert b"multiple of 16" in L.aegist_last_error()
+    # ldy < N
+    assert L.aegist_linear(None, 0, 32, None, 2, None, None, 4, 2, 8, 32, 0, None) == -1
+    # unsupported weight dtype (fp32 weights are not a QLinear form)
+    assert L.aegist_linear(None, 0, 32, None, 0, None, None, 8, 2, 8, 32, 0, None) == -3
+    # the engine argument lists validate the same way
+    assert L.aegist_gemv_i8(None, None, None, None, 8, 24, 0, None) == -1
+    assert L.aegist_gemm_i8(None, None, None, None, 3, 8, 40, 0, None) == -1
+    # empty outputs are a no-op
+    assert L.aegist_gemm_i8(None, None, None, None, 0, 8, 32, 0, None) == 0

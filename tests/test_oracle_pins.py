@@ -245,3 +245,64 @@ def test_attention_single_key_is_gated_value():
     gate = qg[:, 0, :, HD:]
     for h in range(H):
         assert rel_err(y[0, h], v[0, 0, h // 2] * torch.sigmoid(gate[0, h])) < 1e-6
+
+
+# --- QLinear (model.py:78-93) and the engine matvec (aegist.cu:52-172) -------------------------
+
+def test_qlinear_quantize_known_answer():
+    """Rows chosen so the fp32 scale is exact: s = 1 and s = 2; q rounds half to even."""
+    w = torch.tensor([[127.0, -63.5, 31.5, 0.49, -0.5],
+                      [-254.0, 1.0, 3.0, 5.0, 253.0],
+                      [0.0, 0.0, 0.0, 0.0, 0.0]])
+    q, s = R.qlinear_quantize(w)
+    assert q.dtype == torch.int8 and s.dtype == torch.bfloat16
+    assert q[0].tolist() == [127, -64, 32, 0, 0]
+    assert q[1].tolist() == [-127, 0, 2, 2, 126]  # 0.5 -> 0, 1.5 -> 2, 2.5 -> 2, 126.5 -> 126
+    assert q[2].tolist() == [0, 0, 0, 0, 0]
+    assert s[0].item() == 1.0 and s[1].item() == 2.0
+    assert s[2].item() == torch.tensor(1e-8 / 127.0).to(torch.bfloat16).item()
+
+
+def test_qlinear_quantize_round_trip_bound():
+    g = torch.Generator().manual_seed(0)
+    w = torch.randn(64, 300, generator=g) * 0.02
+    q, s = R.qlinear_quantize(w)
+    s32 = w.abs().amax(1, keepdim=True) / 127.0
+    assert (q.abs() <= 127).all() and (q.abs().amax(1) == 127).all()
+    # with the fp32 scale the error is at most half a step
+    assert ((q.float() * s32 - w).abs() <= s32 / 2 * (1 + 1e-5)).all()
+
+
+def test_qlinear_engine_brute_force_and_identity():
+    g = torch.Generator().manual_seed(1)
+    x = torch.randn(2, 5, generator=g)
+    q = torch.randint(-127, 128, (3, 5), generator=g, dtype=torch.int8)
+    s = torch.rand(3, generator=g).to(torch.bfloat16)
+    y = R.qlinear_engine(x, q, s)
+    for m in range(2):
+        for n in range(3):
+            ref = sum(float(x[m, k]) * int(q[n, k]) for k in range(5)) * float(s[n])
+            assert abs(float(y[m, n]) - ref) <= 1e-6 * (1 + abs(ref))
+    # identity weight: q = 127 I, s = bf16(1/127) -> y = x * 127 * bf16(1/127)
+    qi, si = R.qlinear_quantize(torch.eye(5))
+    assert (qi == 127 * torch.eye(5, dtype=torch.int8)).all()
+    yi = R.qlinear_engine(x, qi, si)
+    assert torch.allclose(yi, x * (127 * float(si[0])), rtol=1e-6, atol=0)
+    # accumulate adds; no scale means 1; linearity in x
+    y0 = torch.randn(2, 3, generator=g)
+    assert torch.allclose(R.qlinear_engine(x, q, s, y0, accumulate=True), y0 + y, atol=1e-6)
+    assert torch.allclose(R.qlinear_engine(x, q, None), x @ q.float().t(), rtol=1e-6, atol=1e-5)
+    x2 = torch.randn(2, 5, generator=g)
+    assert torch.allclose(R.qlinear_engine(x + x2, q, s), y + R.qlinear_engine(x2, q, s), rtol=1e-5, atol=1e-4)
+
+
+def test_qlinear_torch_module_form_matches_engine_form():
+    """QLinear.forward dequantises first; in fp32 that differs from the engine's scale-after-dot
+    form by rounding only."""
+    g = torch.Generator().manual_seed(2)
+    w = torch.randn(40, 256, generator=g) * 0.02
+    x = torch.randn(7, 256, generator=g)
+    q, s = R.qlinear_quantize(w)
+    assert rel_err(R.qlinear_torch(x, q, s), R.qlinear_engine(x, q, s)) < 1e-5
+    # and both approximate the unquantised linear to the int8 step size
+    assert rel_err(R.qlinear_engine(x, q, s), x @ w.t()) < 2e-2

@@ -1,0 +1,93 @@
+"""GPU parity of the projection kernels (QLinear int8 / bf16 weights) against the CPU oracle's
+engine formula (aegist.cu gemv_i8 / gemm_i8 / gemv_bf16). The kernel splits an fp32 activation
+into bf16 hi + lo, so the bar is fp32-level: 2e-5 norm-wise max relative error (1e-5 for
+bf16 activations, whose products are exact)."""
+import pytest
+import torch
+
+from conftest import rel_err
+from oracle import mixer_ref as R
+
+from aegist_mixer import ops
+from aegist_mixer._lib import AegistError
+
+pytestmark = pytest.mark.gpu
+
+TOL_F32X = 2e-5
+TOL_BF16X = 1e-5
+
+
+def _case(M, N, K, seed, xdtype=torch.float32):
+    g = torch.Generator().manual_seed(seed)
+    w = torch.randn(N, K, generator=g) * 0.02
+    q, s = R.qlinear_quantize(w)
+    x = torch.randn(M, K, generator=g).to(xdtype)
+    return x, q, s, w
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 32, 16), (1, 2048, 4096), (1, 8192, 2048), (5, 100, 48), (16, 4096, 2048),
+                                   (17, 300, 2048), (33, 2048, 4096), (64, 8192, 2048), (100, 520, 1024),
+                                   (300, 64, 256)])
+def test_linear_int8_fp32x(dev, M, N, K):
+    print(f"linear int8 fp32x M={M} N={N} K={K}", flush=True)
+    x, q, s, _ = _case(M, N, K, seed=M + N + K)
+    ref = R.qlinear_engine(x, q, s)
+    out = ops.linear(x.to(dev), q.to(dev), s.to(dev))
+    torch.cuda.synchronize()
+    assert rel_err(out, ref) < TOL_F32X
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 4096, 2048), (16, 8192, 2048), (48, 2048, 4096), (64, 32, 2048),
+                                   (130, 256, 512)])
+def test_linear_bf16_weight_bf16x(dev, M, N, K):
+    print(f"linear bf16 bf16x M={M} N={N} K={K}", flush=True)
+    g = torch.Generator().manual_seed(M * 7 + N)
+    w = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16)
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    ref = R.qlinear_engine(x.float(), w.float(), None)
+    out = ops.linear(x.to(dev), w.to(dev))
+    torch.cuda.synchronize()
+    assert rel_err(out, ref) < TOL_BF16X
+
+
+def test_linear_accumulate_and_strides(dev):
+    """Residual add into a strided Y (ldy > N) from a strided X (ldx > K), bf16 weights, fp32 X."""
+    M, N, K = 9, 96, 640
+    g = torch.Generator().manual_seed(5)
+    w = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16)
+    xbig = torch.randn(M, K + 64, generator=g)
+    ybig = torch.randn(M, N + 32, generator=g)
+    ref = ybig.clone()
+    ref[:, :N] = R.qlinear_engine(xbig[:, :K], w.float(), None, ybig[:, :N], accumulate=True)
+    xd, yd = xbig.to(dev), ybig.to(dev)
+    from aegist_mixer._lib import BF16, F32, call
+    call("aegist_linear", xd.data_ptr(), F32, K + 64, w.to(dev).data_ptr(), BF16, None, yd.data_ptr(), N + 32, M, N, K,
+         1, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert rel_err(yd, ref) < TOL_F32X
+    assert torch.equal(yd[:, N:].cpu(), ybig[:, N:])  # the columns past N are untouched
+
+
+def test_engine_entry_points(dev):
+    """gemv_i8 (with and without accumulate), gemm_i8 and gemv_bf16 with the engine argument lists."""
+    x, q, s, w = _case(1, 2048, 4096, seed=11)
+    y0 = torch.randn(2048)
+    yd = y0.to(dev)
+    ops.gemv_i8(x[0].to(dev), q.to(dev), s.to(dev), yd, accumulate=True)
+    out1 = ops.gemv_i8(x[0].to(dev), q.to(dev), s.to(dev))
+    X, q2, s2, _ = _case(40, 1024, 2048, seed=12)
+    out2 = ops.gemm_i8(X.to(dev), q2.to(dev), s2.to(dev))
+    wb = w.to(torch.bfloat16)
+    out3 = ops.gemv_bf16(x[0].to(dev), wb.to(dev))
+    torch.cuda.synchronize()
+    assert rel_err(yd, R.qlinear_engine(x, q, s, y0.unsqueeze(0), accumulate=True)[0]) < TOL_F32X
+    assert rel_err(out1, R.qlinear_engine(x, q, s)[0]) < TOL_F32X
+    assert rel_err(out2, R.qlinear_engine(X, q2, s2)) < TOL_F32X
+    assert rel_err(out3, R.qlinear_engine(x, wb.float(), None)[0]) < TOL_F32X
+
+
+def test_linear_shape_errors(dev):
+    x = torch.randn(2, 24, device=dev)
+    w = torch.zeros(8, 24, dtype=torch.int8, device=dev)
+    with pytest.raises(AegistError):
+        ops.linear(x, w)  # K % 16 != 0
