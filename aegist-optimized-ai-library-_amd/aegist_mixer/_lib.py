@@ -61,6 +61,7 @@ SIGNATURES: dict[str, tuple] = {
     "aegist_gemv_bf16": (I, [P, P, P, I, I, P]),
     "aegist_gemm_i8": (I, [P, P, P, P, I, I, I, I, P]),
     "aegist_linear": (I, [P, I, LL, P, I, P, P, LL, I, I, I, I, P]),
+    "aegist_linear_multi": (I, [P, I, LL, I, I, P, P, P, P, P, I, I, I, P]),
 }
 
 

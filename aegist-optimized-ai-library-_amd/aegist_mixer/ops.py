@@ -296,6 +296,37 @@ def linear(x, weight, scale=None, out=None, accumulate: bool = False):
     return out
 
 
+def linear_multi(x, weights, scales=None, outs=None):
+    """One launch for up to four weight matrices sharing the input x [M, K]: returns
+    [x @ (w_i * s_i)^T] as fp32 [M, N_i] (a layer's input projections, e.g. in_qkv | in_z |
+    in_b | in_a). All weights share one dtype (int8 or bf16); scales: list of bf16 [N_i] or None."""
+    import ctypes as C
+    n = len(weights)
+    if not 1 <= n <= 4:
+        raise AegistError("shape", -1, "1 to 4 weight matrices")
+    K = x.shape[-1]
+    x2 = x.reshape(-1, K)
+    M = x2.shape[0]
+    wdt = {torch.int8: I8, torch.bfloat16: BF16}.get(weights[0].dtype)
+    if wdt is None or any(w.dtype != weights[0].dtype for w in weights):
+        raise AegistError("dtype", -3, "weights must all be int8 or all bf16")
+    for w in weights:
+        _need_contig(w)
+        if w.dim() != 2 or w.shape[1] != K:
+            raise AegistError("shape", -1, "weight shape does not match x")
+    if outs is None:
+        outs = [torch.empty(M, w.shape[0], dtype=torch.float32, device=x.device) for w in weights]
+    Wa = (C.c_void_p * n)(*[w.data_ptr() for w in weights])
+    Sa = None if scales is None else (C.c_void_p * n)(*[None if sc is None else sc.data_ptr() for sc in scales])
+    Ya = (C.c_void_p * n)(*[o.data_ptr() for o in outs])
+    La = (C.c_longlong * n)(*[o.stride(0) for o in outs])
+    Na = (C.c_int * n)(*[w.shape[0] for w in weights])
+    call("aegist_linear_multi", _p(x2), _dt(x2), x2.stride(0), wdt, n, C.cast(Wa, C.c_void_p),
+         None if Sa is None else C.cast(Sa, C.c_void_p), C.cast(Ya, C.c_void_p), C.cast(La, C.c_void_p),
+         C.cast(Na, C.c_void_p), M, K, 0, _stream())
+    return outs
+
+
 def gemv_i8(x, qweight, scale, y=None, accumulate: bool = False):
     """Engine gemv_i8 (aegist.cu:85-91): y[n] (+)= scale[n] * (qweight[n] . x), x fp32 [K]."""
     _need_contig(x, qweight, scale)

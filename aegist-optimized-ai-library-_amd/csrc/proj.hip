@@ -123,17 +123,41 @@ template <> struct XLoad<uint16_t> {
     }
 };
 
-// One workgroup: rows [n0, n0 + 16 RT) of W against rows [m0, m0 + 16 MT) of X, all of K.
-// grid = (ceil(N / 16RT), ceil(M / 16MT)); NWAVE waves split the k steps.
+// Up to four weight matrices that share X (a layer's input projections) go in one launch;
+// segment i owns workgroups [tile0[i], tile0[i+1]) along grid x.
+constexpr int MAX_SEG = 4;
+struct ProjSeg {
+    const void* W;
+    const uint16_t* scale;  // per-row scale or null
+    float* Y;
+    long long ldy;
+    int N;
+};
+struct ProjSegs {
+    ProjSeg s[MAX_SEG];
+    int tile0[MAX_SEG + 1];
+    int n;
+};
+
+// One workgroup: rows [n0, n0 + 16 RT) of one segment's W against rows [m0, m0 + 16 MT) of X,
+// all of K. grid = (total row tiles of all segments, ceil(M / 16MT)); NWAVE waves split the k
+// steps.
 template <typename TW, typename TX, int MT, int RT, int NWAVE>
 __global__ __launch_bounds__(64 * NWAVE) void proj_skinny_kernel(const TX* __restrict__ X, long long ldx,
-                                                          const TW* __restrict__ W, const uint16_t* __restrict__ scale,
-                                                          float* __restrict__ Y, long long ldy, int M, int N, int K,
-                                                          int accumulate) {
+                                                                 const ProjSegs segs, int M, int K, int accumulate) {
     __shared__ f32x4 red[NWAVE][RT * MT][WAVE];
     const int lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
     const int r16 = lane % 16, g = lane / 16;
-    const int n0 = blockIdx.x * 16 * RT, m0 = blockIdx.y * 16 * MT;
+    int si = 0;
+#pragma unroll
+    for (int i = 1; i < MAX_SEG; i++)
+        if (i < segs.n && (int)blockIdx.x >= segs.tile0[i]) si = i;
+    const TW* __restrict__ W = (const TW*)segs.s[si].W;
+    const uint16_t* __restrict__ scale = segs.s[si].scale;
+    float* __restrict__ Y = segs.s[si].Y;
+    const long long ldy = segs.s[si].ldy;
+    const int N = segs.s[si].N;
+    const int n0 = ((int)blockIdx.x - segs.tile0[si]) * 16 * RT, m0 = blockIdx.y * 16 * MT;
 
     const TW* wrow[RT];
     bool wok[RT];
@@ -226,23 +250,31 @@ __global__ __launch_bounds__(64 * NWAVE) void proj_skinny_kernel(const TX* __res
 }
 
 template <typename TW, typename TX, int MT, int RT, int NW>
-void launch_k(const TX* X, long long ldx, const TW* W, const uint16_t* scale, float* Y, long long ldy, int M, int N,
-              int K, int accumulate, hipStream_t st) {
-    const dim3 grid((N + 16 * RT - 1) / (16 * RT), (M + 16 * MT - 1) / (16 * MT));
-    proj_skinny_kernel<TW, TX, MT, RT, NW><<<grid, 64 * NW, 0, st>>>(X, ldx, W, scale, Y, ldy, M, N, K, accumulate);
+void launch_k(const TX* X, long long ldx, ProjSegs segs, int M, int K, int accumulate, hipStream_t st) {
+    int t = 0;
+    for (int i = 0; i < segs.n; i++) {
+        segs.tile0[i] = t;
+        t += (segs.s[i].N + 16 * RT - 1) / (16 * RT);
+    }
+    segs.tile0[segs.n] = t;
+    const dim3 grid(t, (M + 16 * MT - 1) / (16 * MT));
+    proj_skinny_kernel<TW, TX, MT, RT, NW><<<grid, 64 * NW, 0, st>>>(X, ldx, segs, M, K, accumulate);
 }
 
 // Shape of the launch: about 2048 waves in all (8 per CU, enough loads in flight to cover HBM
 // latency) with at least two k steps per wave; two row tiles per wave where that is reachable
 // (each activation load then feeds twice the weights), else one.
 template <typename TW, typename TX, int MT>
-void launch_mt(const TX* X, long long ldx, const TW* W, const uint16_t* scale, float* Y, long long ldy, int M, int N,
-               int K, int accumulate, hipStream_t st) {
+void launch_mt(const TX* X, long long ldx, const ProjSegs& segs, int M, int K, int accumulate, hipStream_t st) {
     const long long gy = (M + 16 * MT - 1) / (16 * MT);
     const int nsteps = (K + KSTEP - 1) / KSTEP;
-    const long long t2 = (N + 31) / 32 * gy, t1 = (N + 15) / 16 * gy;
+    long long t2 = 0, t1 = 0;
+    for (int i = 0; i < segs.n; i++) {
+        t2 += (segs.s[i].N + 31) / 32 * gy;
+        t1 += (segs.s[i].N + 15) / 16 * gy;
+    }
     constexpr int kTarget = 2048;
-#define AEG_PROJ(RT, NW) return launch_k<TW, TX, MT, RT, NW>(X, ldx, W, scale, Y, ldy, M, N, K, accumulate, st)
+#define AEG_PROJ(RT, NW) return launch_k<TW, TX, MT, RT, NW>(X, ldx, segs, M, K, accumulate, st)
     if (t2 * 4 >= kTarget) AEG_PROJ(2, 4);
     if (t2 * 8 >= kTarget && nsteps >= 16) AEG_PROJ(2, 8);
     if (t1 * 4 >= kTarget) AEG_PROJ(1, 4);
@@ -257,19 +289,18 @@ void launch_mt(const TX* X, long long ldx, const TW* W, const uint16_t* scale, f
 }
 
 template <typename TW, typename TX>
-int run_proj(const TX* X, long long ldx, const TW* W, const uint16_t* scale, float* Y, long long ldy, int M, int N,
-             int K, int accumulate, hipStream_t st) {
+int run_proj(const TX* X, long long ldx, const ProjSegs& segs, int M, int K, int accumulate, hipStream_t st) {
     // m tiles per workgroup: the whole batch up to 64 rows of bf16 X (32 of fp32 X, whose hi/lo
     // operands take twice the registers), so the weights are read once; larger M is covered by
     // a grid of row groups
     if (M <= 16) {
-        launch_mt<TW, TX, 1>(X, ldx, W, scale, Y, ldy, M, N, K, accumulate, st);
+        launch_mt<TW, TX, 1>(X, ldx, segs, M, K, accumulate, st);
     } else if constexpr (XLoad<TX>::kLo) {
-        launch_mt<TW, TX, 2>(X, ldx, W, scale, Y, ldy, M, N, K, accumulate, st);
+        launch_mt<TW, TX, 2>(X, ldx, segs, M, K, accumulate, st);
     } else {
-        if (M <= 32) launch_mt<TW, TX, 2>(X, ldx, W, scale, Y, ldy, M, N, K, accumulate, st);
-        else if (M <= 48) launch_mt<TW, TX, 3>(X, ldx, W, scale, Y, ldy, M, N, K, accumulate, st);
-        else launch_mt<TW, TX, 4>(X, ldx, W, scale, Y, ldy, M, N, K, accumulate, st);
+        if (M <= 32) launch_mt<TW, TX, 2>(X, ldx, segs, M, K, accumulate, st);
+        else if (M <= 48) launch_mt<TW, TX, 3>(X, ldx, segs, M, K, accumulate, st);
+        else launch_mt<TW, TX, 4>(X, ldx, segs, M, K, accumulate, st);
     }
     return after_launch("proj_skinny");
 }
@@ -278,28 +309,38 @@ int run_proj(const TX* X, long long ldx, const TW* W, const uint16_t* scale, flo
 
 namespace aegist {
 
-// Shared checks: 16-byte rows for the vector loads.
+// Y_i[m, n] (+)= scale_i[n] * sum_k X[m, k] W_i[n, k] for nseg (<= 4) weight matrices sharing X.
+int launch_proj_multi(const void* X, int x_dtype, long long ldx, int w_dtype, int nseg, const void* const* W,
+                      const uint16_t* const* scale, float* const* Y, const long long* ldy, const int* N, int M, int K,
+                      int accumulate, hipStream_t st) {
+    if (nseg < 1 || nseg > MAX_SEG) return fail(AEGIST_ERR_SHAPE, "proj: 1 to 4 weight matrices per launch");
+    if (M < 0 || K < 0) return fail(AEGIST_ERR_SHAPE, "proj: negative size");
+    if (K % 16) return fail(AEGIST_ERR_SHAPE, "proj: K must be a multiple of 16");
+    const int xs = x_dtype == AEGIST_F32 ? 4 : 2;
+    if (ldx < K || (ldx * xs) % 16 || (uintptr_t)X % 16)
+        return fail(AEGIST_ERR_SHAPE, "proj: X needs 16-byte aligned rows (ldx >= K)");
+    ProjSegs segs{};
+    for (int i = 0; i < nseg; i++) {
+        if (N[i] < 0) return fail(AEGIST_ERR_SHAPE, "proj: negative size");
+        if (N[i] == 0) continue;
+        if (ldy[i] < N[i]) return fail(AEGIST_ERR_SHAPE, "proj: ldy < N");
+        if ((uintptr_t)W[i] % 16) return fail(AEGIST_ERR_SHAPE, "proj: W needs 16-byte aligned rows");
+        segs.s[segs.n++] = ProjSeg{W[i], scale ? scale[i] : nullptr, Y[i], ldy[i], N[i]};
+    }
+    if (M == 0 || segs.n == 0) return 0;
+    if (w_dtype == AEGIST_I8 && x_dtype == AEGIST_F32) return run_proj<int8_t, float>((const float*)X, ldx, segs, M, K, accumulate, st);
+    if (w_dtype == AEGIST_I8 && x_dtype == AEGIST_BF16)
+        return run_proj<int8_t, uint16_t>((const uint16_t*)X, ldx, segs, M, K, accumulate, st);
+    if (w_dtype == AEGIST_BF16 && x_dtype == AEGIST_F32)
+        return run_proj<uint16_t, float>((const float*)X, ldx, segs, M, K, accumulate, st);
+    if (w_dtype == AEGIST_BF16 && x_dtype == AEGIST_BF16)
+        return run_proj<uint16_t, uint16_t>((const uint16_t*)X, ldx, segs, M, K, accumulate, st);
+    return fail(AEGIST_ERR_DTYPE, "proj: W must be AEGIST_I8 or AEGIST_BF16, X AEGIST_F32 or AEGIST_BF16");
+}
+
 int launch_proj(const void* X, int x_dtype, long long ldx, const void* W, int w_dtype, const uint16_t* scale, float* Y,
                 long long ldy, int M, int N, int K, int accumulate, hipStream_t st) {
-    if (M < 0 || N < 0 || K < 0) return fail(AEGIST_ERR_SHAPE, "proj: negative size");
-    if (M == 0 || N == 0) return 0;
-    if (K % 16) return fail(AEGIST_ERR_SHAPE, "proj: K must be a multiple of 16");
-    if (ldy < N) return fail(AEGIST_ERR_SHAPE, "proj: ldy < N");
-    const int xs = x_dtype == AEGIST_F32 ? 4 : 2;
-    if (ldx < K || (ldx * xs) % 16 || (uintptr_t)X % 16 || (uintptr_t)W % 16)
-        return fail(AEGIST_ERR_SHAPE, "proj: X and W need 16-byte aligned rows (ldx >= K)");
-    if (w_dtype == AEGIST_I8 && x_dtype == AEGIST_F32)
-        return run_proj<int8_t, float>((const float*)X, ldx, (const int8_t*)W, scale, Y, ldy, M, N, K, accumulate, st);
-    if (w_dtype == AEGIST_I8 && x_dtype == AEGIST_BF16)
-        return run_proj<int8_t, uint16_t>((const uint16_t*)X, ldx, (const int8_t*)W, scale, Y, ldy, M, N, K,
-                                          accumulate, st);
-    if (w_dtype == AEGIST_BF16 && x_dtype == AEGIST_F32)
-        return run_proj<uint16_t, float>((const float*)X, ldx, (const uint16_t*)W, scale, Y, ldy, M, N, K, accumulate,
-                                         st);
-    if (w_dtype == AEGIST_BF16 && x_dtype == AEGIST_BF16)
-        return run_proj<uint16_t, uint16_t>((const uint16_t*)X, ldx, (const uint16_t*)W, scale, Y, ldy, M, N, K,
-                                            accumulate, st);
-    return fail(AEGIST_ERR_DTYPE, "proj: W must be AEGIST_I8 or AEGIST_BF16, X AEGIST_F32 or AEGIST_BF16");
+    return launch_proj_multi(X, x_dtype, ldx, w_dtype, 1, &W, &scale, &Y, &ldy, &N, M, K, accumulate, st);
 }
 
 }  // namespace aegist
@@ -322,4 +363,11 @@ extern "C" int aegist_linear(const void* X, int x_dtype, long long ldx, const vo
                              const uint16_t* scale, float* Y, long long ldy, int M, int N, int K, int accumulate,
                              void* stream) {
     return launch_proj(X, x_dtype, ldx, W, w_dtype, scale, Y, ldy, M, N, K, accumulate, AEG_STREAM(stream));
+}
+
+extern "C" int aegist_linear_multi(const void* X, int x_dtype, long long ldx, int w_dtype, int n, const void* const* W,
+                                   const uint16_t* const* scale, float* const* Y, const long long* ldy, const int* N,
+                                   int M, int K, int accumulate, void* stream) {
+    if (!W || !Y || !ldy || !N) return fail(AEGIST_ERR_SHAPE, "linear_multi: null argument array");
+    return launch_proj_multi(X, x_dtype, ldx, w_dtype, n, W, scale, Y, ldy, N, M, K, accumulate, AEG_STREAM(stream));
 }

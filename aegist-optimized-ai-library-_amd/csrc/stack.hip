@@ -37,6 +37,9 @@ int stack_attn_prefill(const float* qn, const uint16_t* kc, const uint16_t* vc, 
 size_t decode_workspace_bytes(int B, int H, int KV, int L, bool with_q);
 int launch_proj(const void* X, int x_dtype, long long ldx, const void* W, int w_dtype, const uint16_t* scale, float* Y,
                 long long ldy, int M, int N, int K, int accumulate, hipStream_t st);
+int launch_proj_multi(const void* X, int x_dtype, long long ldx, int w_dtype, int nseg, const void* const* W,
+                      const uint16_t* const* scale, float* const* Y, const long long* ldy, const int* N, int M, int K,
+                      int accumulate, hipStream_t st);
 }  // namespace aegist
 
 using namespace aegist;
@@ -105,6 +108,20 @@ int gemm(Stack* s, const uint16_t* A, const uint16_t* W, float* Y, int M, int N,
     return after_launch("projection gemm");
 }
 
+// The input projections of one layer (up to four weights sharing A): one grouped launch at
+// decode sizes, one GEMM each otherwise.
+int gemm_group(Stack* s, const uint16_t* A, int n, const uint16_t* const* W, float* const* Y, const int* N,
+               const long long* ldy, int M, int K, hipStream_t stream) {
+    if (M <= 64 && K % 16 == 0)
+        return launch_proj_multi(A, AEGIST_BF16, K, AEGIST_BF16, n, (const void* const*)W, nullptr, Y, ldy, N, M, K, 0,
+                                 stream);
+    for (int i = 0; i < n; i++) {
+        int rc = gemm(s, A, W[i], Y[i], M, N[i], K, (int)ldy[i], 0.f, stream);
+        if (rc) return rc;
+    }
+    return 0;
+}
+
 #define RC(x)                  \
     do {                       \
         int _r = (x);          \
@@ -117,10 +134,13 @@ int delta_layer(Stack* s, const AegistLayerWeights& w, int sl, float* x, int B, 
     const size_t mb = (size_t)c.max_batch;
     float* conv = s->conv + (size_t)sl * mb * C * 3;
     float* rec = s->rec + (size_t)sl * mb * HV * D * D;
-    RC(gemm(s, s->hb, w.w_qkv, s->proj, rows, C, dm, C, 0.f, st));
-    RC(gemm(s, s->hb, w.w_z, s->z, rows, HV * D, dm, HV * D, 0.f, st));
-    RC(gemm(s, s->hb, w.w_b, s->ba, rows, HV, dm, 2 * HV, 0.f, st));
-    RC(gemm(s, s->hb, w.w_a, s->ba + HV, rows, HV, dm, 2 * HV, 0.f, st));
+    {
+        const uint16_t* W[4] = {w.w_qkv, w.w_z, w.w_b, w.w_a};
+        float* Y[4] = {s->proj, s->z, s->ba, s->ba + HV};
+        const int N[4] = {C, HV * D, HV, HV};
+        const long long ldy[4] = {C, HV * D, 2 * HV, 2 * HV};
+        RC(gemm_group(s, s->hb, 4, W, Y, N, ldy, rows, dm, st));
+    }
     RC(launch_gates_from_proj(s->ba, w.a_log, w.dt_bias, s->g, s->beta, rows, HV, st));
     const float qscale = 1.f / sqrtf((float)D);
     if (T == 1) {
@@ -147,9 +167,13 @@ int attn_layer(Stack* s, const AegistLayerWeights& w, int sl, float* x, int B, i
     uint16_t* vc = s->vc + (size_t)sl * mb * KV * cap * HD;
     float* kp = s->kv2;
     float* vp = s->kv2 + (size_t)c.max_tokens * KV * HD;
-    RC(gemm(s, s->hb, w.w_q, s->proj, rows, 2 * H * HD, dm, 2 * H * HD, 0.f, st));
-    RC(gemm(s, s->hb, w.w_k, kp, rows, KV * HD, dm, KV * HD, 0.f, st));
-    RC(gemm(s, s->hb, w.w_v, vp, rows, KV * HD, dm, KV * HD, 0.f, st));
+    {
+        const uint16_t* W[3] = {w.w_q, w.w_k, w.w_v};
+        float* Y[3] = {s->proj, kp, vp};
+        const int N[3] = {2 * H * HD, KV * HD, KV * HD};
+        const long long ldy[3] = {2 * H * HD, KV * HD, KV * HD};
+        RC(gemm_group(s, s->hb, 3, W, Y, N, ldy, rows, dm, st));
+    }
     RC(launch_attn_prep(s->proj, kp, vp, AEGIST_F32, w.q_norm, w.k_norm, s->y, kc, vc, B, T, H, KV, HD, c.rotary_dim,
                         s->length, (int)cap, c.eps, c.rope_theta, st, nullptr, 0));
     const float scale = 1.f / sqrtf((float)HD);

@@ -263,6 +263,14 @@ int aegist_gemm_i8(const float* X, const int8_t* W, const uint16_t* scale, float
  * W dtype AEGIST_I8 | AEGIST_BF16, scale NULL = 1, Y fp32 with row stride ldy. */
 int aegist_linear(const void* X, int x_dtype, long long ldx, const void* W, int w_dtype, const uint16_t* scale,
                   float* Y, long long ldy, int M, int N, int K, int accumulate, void* stream);
+/* Grouped form: n (1..4) weight matrices W[i] [N[i], K] of one dtype that share the input X
+ * (a layer's input projections, e.g. in_qkv | in_z | in_b | in_a of GatedDeltaNet,
+ * hybrid.py:372-384, or q | k | v of GatedAttention, hybrid.py:270-275) in one launch:
+ * Y[i][m, n] (+)= scale[i][n] * sum_k X[m, k] W[i][n, k]. W, scale (may be NULL, or hold NULLs),
+ * Y, ldy and N are host arrays of n entries. */
+int aegist_linear_multi(const void* X, int x_dtype, long long ldx, int w_dtype, int n, const void* const* W,
+                        const uint16_t* const* scale, float* const* Y, const long long* ldy, const int* N, int M,
+                        int K, int accumulate, void* stream);
 
 #ifdef __cplusplus
 }

@@ -103,3 +103,13 @@ def test_linear_rejects_shapes_and_dtypes():
     assert L.aegist_gemm_i8(None, None, None, None, 3, 8, 40, 0, None) == -1
     # empty outputs are a no-op
     assert L.aegist_gemm_i8(None, None, None, None, 0, 8, 32, 0, None) == 0
+
+
+def test_linear_multi_rejects_counts():
+    L = _lib.lib()
+    arr = (C.c_void_p * 5)()
+    lds = (C.c_longlong * 5)(*([8] * 5))
+    ns = (C.c_int * 5)(*([8] * 5))
+    for n in (0, 5):
+        assert L.aegist_linear_multi(None, 0, 32, 2, n, arr, None, arr, lds, ns, 2, 32, 0, None) == -1
+    assert L.aegist_linear_multi(None, 0, 32, 2, 1, None, None, arr, lds, ns, 2, 32, 0, None) == -1

@@ -91,3 +91,26 @@ def test_linear_shape_errors(dev):
     w = torch.zeros(8, 24, dtype=torch.int8, device=dev)
     with pytest.raises(AegistError):
         ops.linear(x, w)  # K % 16 != 0
+
+
+@pytest.mark.parametrize("M", [1, 16, 40])
+def test_linear_multi_matches_separate(dev, M):
+    """One grouped launch over a layer's input projections (sizes of in_qkv, in_z, in_b, in_a
+    scaled down, plus an empty one) equals the oracle per weight."""
+    print(f"linear_multi M={M}", flush=True)
+    g = torch.Generator().manual_seed(M)
+    K = 512
+    Ns = [1024, 512, 32, 0]
+    ws = [torch.randn(n, K, generator=g) * 0.02 for n in Ns]
+    qs = [R.qlinear_quantize(w) for w in ws]
+    x = torch.randn(M, K, generator=g)
+    outs = ops.linear_multi(x.to(dev), [q.to(dev) for q, _ in qs], [s.to(dev) for _, s in qs])
+    wb = [w.to(torch.bfloat16) for w in ws[:3]]
+    xb = x.to(torch.bfloat16)
+    outs_b = ops.linear_multi(xb.to(dev), [w.to(dev) for w in wb])
+    torch.cuda.synchronize()
+    for (q, s), o in zip(qs[:3], outs[:3]):
+        assert rel_err(o, R.qlinear_engine(x, q, s)) < TOL_F32X
+    assert outs[3].numel() == 0
+    for w, o in zip(wb, outs_b):
+        assert rel_err(o, R.qlinear_engine(xb.float(), w.float(), None)) < TOL_BF16X
