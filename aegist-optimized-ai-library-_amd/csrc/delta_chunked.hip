@@ -6,8 +6,10 @@
 //   intra = lower_incl( e^{cum_i - cum_j} q_n,i . k_n,j )
 //   v_new = u - w S;  o = e^{cum} (q_n S) + intra v_new;  S = e^{cum_last} S + k_n^T (e^{cum_last - cum} v_new)
 //
-// Two kernels per segment of up to SEG tokens (the workspace holds one segment, so it stays
-// resident in L2 / MALL between the two launches):
+// Two kernels per segment of up to SEG tokens (a segment's workspace stays resident in the
+// MALL between the two launches). With more than one segment the workspace holds two segment
+// buffers and K1 of segment s+1 runs on a second stream while K2 of segment s runs on the
+// caller's (K2 keeps one workgroup per CU busy, K1 fills the rest of the CU):
 //  K1 delta_chunk_intra: one workgroup per (sequence, value head, chunk), fully parallel.
 //     Normalises q, k in fp32 and keeps them as fp16 in LDS; k_n k_n^T and q_n k_n^T on
 //     v_mfma_f32_16x16x32_f16 (lower-triangular blocks only); decay and beta applied in fp32 on
@@ -15,8 +17,9 @@
 //     right-hand-side column (256 columns = beta v | beta e^cum k_n), the matrix broadcast
 //     from LDS. Writes u (fp32), w (fp16), intra (fp16), cum, and - once per QK head - q_n
 //     and k_n^T (fp16).
-//  K2 delta_chunk_state: one workgroup per (sequence, value head, 32-column slice of S); the
-//     columns of S are independent, so 4 slices per head run in parallel. S lives in MFMA
+//  K2 delta_chunk_state: one workgroup per (sequence, value head, 16-column slice of S); the
+//     columns of S are independent, so 8 slices per head run in parallel, the slices of one
+//     head on one XCD (they share its L2 for the chunk operands). S lives in MFMA
 //     accumulator registers (fp32) for the whole segment; each chunk it is copied to LDS as
 //     fp16 (transposed, so the B operand is a 16-byte read), then w S and q_n S, intra v_new,
 //     and the rank-64 state update k_n^T v' run on MFMA.
@@ -24,6 +27,8 @@
 // decay / beta factor are applied in fp32 outside the products, and fp16 keeps the chunked
 // result within 5e-4 of fp64 at T = 8192, where bf16 operands give 4e-3 (over the 1e-3 bar).
 #include "common.h"
+
+#include <mutex>
 
 #include <algorithm>
 
@@ -50,7 +55,8 @@ struct SeqLayout {
 // Workspace of one segment. Per (b, hv, chunk): u fp32 [64][128] stored in K2's accumulator
 // fragment order (see u_frag), w fp16 [64][128], intra fp16 [64][64], and the decay factors
 // dec fp32 [3][64] = (e^{cum_i}, e^{cum_last - cum_i}, e^{cum_last}). Per (b, kh, chunk):
-// qn fp16 [64][128], knT fp16 [128][64].
+// qn fp16 [64][128], knT fp16 [128][64]. w, intra, qn and knT are stored in MFMA A-operand
+// fragment order (afrag_coords).
 // Plus the carried state [B, HV, 128, 128] fp32 when the caller passes none.
 struct WsLayout {
     size_t u, w, intra, cum, qn, knt, state, total;
@@ -74,6 +80,18 @@ __host__ __device__ inline WsLayout ws_layout(int B, int HK, int HV, int nch) {
 }
 
 __device__ __forceinline__ half8 ld_h8(const half_t* p) { return *(const half8*)p; }
+
+// MFMA A-operand fragment order. For A [M][K] (M % 16 == 0, K % 32 == 0), fragment (mb, ks)
+// holds for lane l the 8 halves A[16 mb + l % 16][32 ks + 8 (l / 16) + i], i < 8 - exactly what
+// lane l passes to v_mfma_f32_16x16x32_f16 for row block mb and k block ks. Fragments are
+// stored contiguously, offset ((mb * K / 32 + ks) * 64 + l) * 8 halves, so a wave loads one
+// operand with a single 1 KB contiguous access. Returns the (row, first column) of fragment
+// slot f.
+__device__ __forceinline__ void afrag_coords(int f, int KS, int& r, int& c0) {
+    const int l = f % 64, ks = (f / 64) % KS, mb = f / (64 * KS);
+    r = 16 * mb + l % 16;
+    c0 = 32 * ks + 8 * (l / 16);
+}
 
 // 8 consecutive activations as fp32 (two 16-byte loads for fp32, one for bf16)
 template <typename T> __device__ __forceinline__ void ld8(const T* p, float* o);
@@ -114,6 +132,7 @@ __global__ void __launch_bounds__(256) delta_chunk_intra(const Tin* __restrict__
     __shared__ __attribute__((aligned(16))) float As[CH][A_LD];    // A, then X = (I + A)^-1 in place
     __shared__ float Pt[3][16][17];
     __shared__ float cum_s[CH], beta_s[CH], g_s[CH];
+    __shared__ __attribute__((aligned(16))) half_t It[CH][CH + 8];  // intra, staged for fragment order
 
     const int c = blockIdx.x, hv = blockIdx.y, b = blockIdx.z, nch = gridDim.x;
     const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE, n = lane % 16, gq = lane / 16;
@@ -193,23 +212,22 @@ __global__ void __launch_bounds__(256) delta_chunk_intra(const Tin* __restrict__
         dec[2 * CH + lane] = __expf(last);
     }
     if (writes_qk) {
+        // q_n (A of q_n S: 64 x 128) and k_n^T (A of the state update: 128 dk x 64 rows) in
+        // fragment order
         const size_t ku = ((size_t)(b * HK + kh) * nch + c);
-        half_t* qn = (half_t*)(ws + L.qn) + ku * CH * D;
-        half_t* knt = (half_t*)(ws + L.knt) + ku * CH * D;
-        {
-            const half8* src = (const half8*)&QV[row][qq * 32];
-            half8* dst = (half8*)(qn + row * D + qq * 32);
+        half8* qn = (half8*)((half_t*)(ws + L.qn) + ku * CH * D);
+        half8* knt = (half8*)((half_t*)(ws + L.knt) + ku * CH * D);
 #pragma unroll
-            for (int e = 0; e < 4; e++) dst[e] = src[e];
-        }
-        {   // thread = (dk, 32-row half)
-            const int dk = tid / 2, hh = tid % 2;
-            half8 buf[4];
+        for (int it = 0; it < 4; it++) {
+            const int f = tid + 256 * it;
+            int r, c0;
+            afrag_coords(f, 4, r, c0);
+            qn[f] = ld_h8(&QV[r][c0]);
+            afrag_coords(f, 2, r, c0);  // r = dk, c0 = first chunk row
+            half8 v;
 #pragma unroll
-            for (int e = 0; e < 32; e++) buf[e / 8][e % 8] = Ks[hh * 32 + e][dk];
-            half8* dst = (half8*)(knt + dk * CH + hh * 32);
-#pragma unroll
-            for (int e = 0; e < 4; e++) dst[e] = buf[e];
+            for (int i = 0; i < 8; i++) v[i] = Ks[c0 + i][r];
+            knt[f] = v;
         }
     }
     __syncthreads();
@@ -217,7 +235,6 @@ __global__ void __launch_bounds__(256) delta_chunk_intra(const Tin* __restrict__
     // ---- 3. k_n k_n^T and q_n k_n^T on MFMA: wave = 16-row block rb, column blocks cb <= rb
     {
         const int rb = wave;
-        half_t* intra = (half_t*)(ws + L.intra) + vu * CH * CH;
         half8 ak[4], aq[4];
 #pragma unroll
         for (int ks = 0; ks < 4; ks++) {
@@ -229,7 +246,7 @@ __global__ void __launch_bounds__(256) delta_chunk_intra(const Tin* __restrict__
             if (cb > rb) {  // upper blocks: zero in intra and in A (X = (I + A)^-1 stays lower there)
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
-                    intra[(16 * rb + 4 * gq + j) * CH + jj] = (half_t)0.f;
+                    It[16 * rb + 4 * gq + j][jj] = (half_t)0.f;
                     As[16 * rb + 4 * gq + j][jj] = 0.f;
                 }
                 continue;
@@ -246,11 +263,21 @@ __global__ void __launch_bounds__(256) delta_chunk_intra(const Tin* __restrict__
                 const int i = 16 * rb + 4 * gq + j;
                 const float dec = __expf(cum_s[i] - cum_s[jj]);
                 As[i][jj] = jj < i ? beta_s[i] * (dec * accA[j]) : 0.f;
-                intra[i * CH + jj] = (half_t)(jj <= i ? dec * accQ[j] : 0.f);
+                It[i][jj] = (half_t)(jj <= i ? dec * accQ[j] : 0.f);
             }
         }
     }
     __syncthreads();
+    {   // intra (A of intra v_new: 64 x 64) in fragment order
+        half8* intra = (half8*)((half_t*)(ws + L.intra) + vu * CH * CH);
+#pragma unroll
+        for (int it = 0; it < 2; it++) {
+            const int f = tid + 256 * it;
+            int r, c0;
+            afrag_coords(f, 2, r, c0);
+            intra[f] = ld_h8(&It[r][c0]);
+        }
+    }
 
     // ---- 4. v (fp16 hi / lo) into the q tile's space; X = (I + A)^-1, blocked by 16
 #pragma unroll
@@ -337,6 +364,7 @@ __global__ void __launch_bounds__(256) delta_chunk_intra(const Tin* __restrict__
                     kb[t][ks][i] = Ks[rr][col];
                 }
         }
+        __syncthreads();  // every wave holds its v / k_n operands: Ks becomes the w staging tile
         float su[2][8], sw[2][8];
 #pragma unroll
         for (int ks = 0; ks < 2; ks++)
@@ -376,8 +404,18 @@ __global__ void __launch_bounds__(256) delta_chunk_intra(const Tin* __restrict__
                 const int col = 16 * (2 * wave + t) + n;
                 *(f32x4*)(u + u_frag(16 * rb + 4 * gq, col)) = au;
 #pragma unroll
-                for (int j = 0; j < 4; j++) wout[(16 * rb + 4 * gq + j) * D + col] = (half_t)aw[j];
+                for (int j = 0; j < 4; j++) Ks[16 * rb + 4 * gq + j][col] = (half_t)aw[j];
             }
+        }
+        __syncthreads();
+        // w (A of w S: 64 x 128) in fragment order
+        half8* wf = (half8*)wout;
+#pragma unroll
+        for (int it = 0; it < 4; it++) {
+            const int f = tid + 256 * it;
+            int r, c0;
+            afrag_coords(f, 4, r, c0);
+            wf[f] = ld_h8(&Ks[r][c0]);
         }
     }
 }
@@ -434,17 +472,18 @@ __global__ void __launch_bounds__(256) delta_chunk_state(const unsigned char* __
         const half_t* Ic = (const half_t*)(ws + L.intra) + vu * CH * CH;
         const half_t* KTc = (const half_t*)(ws + L.knt) + ku * CH * D;
         const float* dec = (const float*)(ws + L.cum) + vu * 3 * CH;
+        // fragment-order operands (written so by K1): one contiguous 1 KB load per fragment
 #pragma unroll
         for (int ks = 0; ks < 4; ks++) {
-            o.wa[ks] = ld_h8(Wc + (16 * wave + n) * D + 32 * ks + 8 * gq);
-            o.qa[ks] = ld_h8(Qc + (16 * wave + n) * D + 32 * ks + 8 * gq);
+            o.wa[ks] = ld_h8(Wc + ((4 * wave + ks) * 64 + lane) * 8);
+            o.qa[ks] = ld_h8(Qc + ((4 * wave + ks) * 64 + lane) * 8);
         }
 #pragma unroll
-        for (int ks = 0; ks < 2; ks++) o.ia[ks] = ld_h8(Ic + (16 * wave + n) * CH + 32 * ks + 8 * gq);
+        for (int ks = 0; ks < 2; ks++) o.ia[ks] = ld_h8(Ic + ((2 * wave + ks) * 64 + lane) * 8);
 #pragma unroll
         for (int rt = 0; rt < 2; rt++)
 #pragma unroll
-            for (int ks = 0; ks < 2; ks++) o.ka[rt][ks] = ld_h8(KTc + (32 * wave + 16 * rt + n) * CH + 32 * ks + 8 * gq);
+            for (int ks = 0; ks < 2; ks++) o.ka[rt][ks] = ld_h8(KTc + ((2 * (2 * wave + rt) + ks) * 64 + lane) * 8);
 #pragma unroll
         for (int ct = 0; ct < NCT; ct++) o.uu[ct] = *(const f32x4*)(Uc + u_frag(16 * wave + 4 * gq, col0 + 16 * ct + n));
         o.ecum = *(const f32x4*)(dec + 16 * wave + 4 * gq);
@@ -559,27 +598,75 @@ __global__ void __launch_bounds__(256) delta_chunk_state(const unsigned char* __
             for (int j = 0; j < 4; j++) Sg[(size_t)(32 * wave + 16 * rt + 4 * gq + j) * D + col0 + 16 * ct + n] = S[rt][ct][j];
 }
 
-int seg_chunks(int T) { return (std::min(T, SEG) + CH - 1) / CH; }
+// Chunks per segment: SEG tokens (the workspace of one segment, ~72 MB at B = 1 with 32 value
+// heads, stays resident in the MALL between the two kernels that touch it).
+int seg_chunks(int B, int T, int HV) {
+    (void)B;
+    (void)HV;
+    return (std::min(T, SEG) + CH - 1) / CH;
+}
 
 }  // namespace
 
 namespace aegist {
 
+// Workspace: [carried state (when the caller passes none)][segment buffer 0][segment buffer 1]
+// (the second buffer only when there is more than one segment: the intra-chunk kernel of the
+// next segment then runs on a second stream while the state kernel reads this one).
+struct WsPlan {
+    size_t state_off, seg_bytes, total;
+    int nch_seg, nbuf;
+};
+static WsPlan ws_plan(int B, int T, int HK, int HV) {
+    WsPlan p;
+    p.nch_seg = seg_chunks(B, T, HV);
+    p.seg_bytes = ws_layout(B, HK, HV, p.nch_seg).state;  // the per-segment part, 256-aligned
+    p.nbuf = (T + CH - 1) / CH > p.nch_seg ? 2 : 1;
+    p.state_off = 0;
+    p.total = al256((size_t)B * HV * D * D * 4) + p.nbuf * p.seg_bytes;
+    return p;
+}
+
 size_t delta_chunked_ws_bytes(int B, int T, int HK, int HV) {
     if (B <= 0 || T <= 0 || HK <= 0 || HV <= 0) return 256;
-    return ws_layout(B, HK, HV, seg_chunks(T)).total;
+    return ws_plan(B, T, HK, HV).total;
+}
+
+// Second stream and events per device for the overlapped schedule; created on first use (default
+// priority, non-blocking) and kept for the life of the process. The enqueue of one chunked call
+// holds the device's lock, so calls from several host threads do not interleave their events.
+struct AuxStream {
+    std::mutex mu;
+    hipStream_t stream = nullptr;
+    hipEvent_t ev_main = nullptr, ev_aux = nullptr;
+};
+static AuxStream g_aux[64];
+
+static int aux_for_device(AuxStream** out) {
+    int dev = 0;
+    AEG_HIP(hipGetDevice(&dev));
+    if (dev < 0 || dev >= 64) return fail(AEGIST_ERR_SHAPE, "delta_chunked: device index out of range");
+    AuxStream& a = g_aux[dev];
+    if (!a.stream) {
+        AEG_HIP(hipStreamCreateWithFlags(&a.stream, hipStreamNonBlocking));
+        AEG_HIP(hipEventCreateWithFlags(&a.ev_main, hipEventDisableTiming));
+        AEG_HIP(hipEventCreateWithFlags(&a.ev_aux, hipEventDisableTiming));
+    }
+    *out = &a;
+    return 0;
 }
 
 template <typename Tin, typename Tout>
 int run_chunked(const Tin* q, const Tin* k, const Tin* v, const float* g, const float* beta, float* state, Tout* out,
                 const SeqLayout& a, int B, int T, int HK, int HV, int normalize, float qscale, float eps, void* ws,
                 size_t ws_bytes, hipStream_t st) {
-    const int nch_seg = seg_chunks(T);
-    WsLayout L = ws_layout(B, HK, HV, nch_seg);
-    if (!ws || ws_bytes < L.total) return fail(AEGIST_ERR_WORKSPACE, "delta_chunked: workspace too small");
+    const WsPlan plan = ws_plan(B, T, HK, HV);
+    if (!ws || ws_bytes < plan.total) return fail(AEGIST_ERR_WORKSPACE, "delta_chunked: workspace too small");
     unsigned char* w = (unsigned char*)ws;
     // the carried state: the caller's, or the workspace copy (starts at zero: K2 does not load it)
-    float* S = state ? state : (float*)(w + L.state);
+    float* S = state ? state : (float*)(w + plan.state_off);
+    unsigned char* segbuf[2] = {w + al256((size_t)B * HV * D * D * 4), nullptr};
+    segbuf[1] = segbuf[0] + plan.seg_bytes;
     // 16-byte input loads need 16-byte aligned rows (and 8-element runs)
     const long long ei = 16 / (long long)sizeof(Tin);
     const int vec_in = ((uintptr_t)q % 16 == 0) && ((uintptr_t)k % 16 == 0) && ((uintptr_t)v % 16 == 0) &&
@@ -588,22 +675,43 @@ int run_chunked(const Tin* q, const Tin* k, const Tin* v, const float* g, const 
     // 16-byte output stores need 16-byte aligned rows
     const long long ev = 16 / (long long)sizeof(Tout);
     const int vec_out = ((uintptr_t)out % 16 == 0) && a.sb_o % ev == 0 && a.st_o % ev == 0 && a.sh_o % ev == 0;
-    int load = state ? 1 : 0;
-    for (int t0 = 0; t0 < T; t0 += SEG) {
-        const int len = std::min(SEG, T - t0);
-        const int nch = (len + CH - 1) / CH;
-        WsLayout Ls = ws_layout(B, HK, HV, nch);
-        Ls.state = L.state;
-        delta_chunk_intra<Tin><<<dim3(nch, HV, B), 256, 0, st>>>(q, k, v, g, beta, a, t0, T, HK, HV, normalize, qscale,
-                                                               eps, w, Ls, vec_in);
-        int rc = after_launch("delta_chunk_intra");
-        if (rc) return rc;
-        const int units8 = (B * HV + 7) / 8 * 8;
-        delta_chunk_state<Tout, K2_NCT><<<units8 * (D / (16 * K2_NCT)), 256, 0, st>>>(w, Ls, S, load, out, a, t0, T,
-                                                                                  nch, B, HK, HV, vec_out);
-        rc = after_launch("delta_chunk_state");
-        if (rc) return rc;
-        load = 1;
+    const int seg = plan.nch_seg * CH;
+    const int nseg = (T + seg - 1) / seg;
+    const int units8 = (B * HV + 7) / 8 * 8;
+
+    auto intra = [&](int s, hipStream_t on) {
+        const int t0 = s * seg, nch = (std::min(seg, T - t0) + CH - 1) / CH;
+        const WsLayout Ls = ws_layout(B, HK, HV, nch);
+        delta_chunk_intra<Tin><<<dim3(nch, HV, B), 256, 0, on>>>(q, k, v, g, beta, a, t0, T, HK, HV, normalize, qscale,
+                                                                eps, segbuf[s & 1], Ls, vec_in);
+        return after_launch("delta_chunk_intra");
+    };
+    auto state_pass = [&](int s) {
+        const int t0 = s * seg, nch = (std::min(seg, T - t0) + CH - 1) / CH;
+        const WsLayout Ls = ws_layout(B, HK, HV, nch);
+        delta_chunk_state<Tout, K2_NCT><<<units8 * (D / (16 * K2_NCT)), 256, 0, st>>>(
+            segbuf[s & 1], Ls, S, (state || s > 0) ? 1 : 0, out, a, t0, T, nch, B, HK, HV, vec_out);
+        return after_launch("delta_chunk_state");
+    };
+
+    int rc = intra(0, st);
+    if (rc) return rc;
+    if (nseg == 1) return state_pass(0);
+    // K1 of segment s+1 (second stream) overlaps K2 of segment s (caller's stream). K1(s+1)
+    // overwrites the buffer K2(s-1) read, so it waits for the caller's stream up to K2(s-1);
+    // K2(s) waits for K1(s). Every second-stream launch is joined back before the call returns.
+    AuxStream* ax = nullptr;
+    if ((rc = aux_for_device(&ax))) return rc;
+    std::lock_guard<std::mutex> lock(ax->mu);
+    for (int s = 0; s < nseg; s++) {
+        if (s > 0) AEG_HIP(hipStreamWaitEvent(st, ax->ev_aux, 0));
+        if (s + 1 < nseg) {
+            AEG_HIP(hipEventRecord(ax->ev_main, st));
+            AEG_HIP(hipStreamWaitEvent(ax->stream, ax->ev_main, 0));
+            if ((rc = intra(s + 1, ax->stream))) return rc;
+            AEG_HIP(hipEventRecord(ax->ev_aux, ax->stream));
+        }
+        if ((rc = state_pass(s))) return rc;
     }
     return 0;
 }
@@ -640,8 +748,12 @@ int delta_scan_chunked(const float* y, const float* gb, float* state, float* o, 
 }  // namespace aegist
 
 extern "C" size_t aegist_delta_chunked_workspace_bytes(int B, int T, int HV) {
-    // HK only changes the q_n / k_n^T share; size for HK = HV (the largest)
-    return delta_chunked_ws_bytes(B, T, HV, HV);
+    // HK only changes the q_n / k_n^T share; size for HK = HV (the largest). The segment length
+    // depends on B, so take the largest need over batches 1..B: a workspace sized for (B, T)
+    // then serves every call with B' <= B sequences of T' <= T tokens.
+    size_t need = 256;
+    for (int b = 1; b <= B; b++) need = std::max(need, delta_chunked_ws_bytes(b, T, HV, HV));
+    return need;
 }
 
 extern "C" int aegist_delta_chunked(const void* q, const void* k, const void* v, int in_dtype, long long sb_qk,

@@ -272,3 +272,24 @@ def test_engine_delta_scan_long_prompt(dev):
     torch.cuda.synchronize()
     assert rel_err(o, o_ref[0].transpose(0, 1)) < DELTA_TOL
     assert rel_err(S, S_ref[0]) < DELTA_TOL
+
+
+def test_chunked_multi_segment_on_side_stream(dev):
+    """Two 5000-token calls (3 segments each, so the overlapped two-stream schedule runs) on a
+    non-default stream, the second continuing from the first's state: equals the oracle over
+    the 10000-token sequence. Small heads keep the CPU oracle quick."""
+    HK, HV, T = 2, 4, 5000
+    q, k, v, g, beta = seq_inputs(1, HK, HV, 2 * T, seed=77)
+    o_ref, S_ref = oracle_seq(q, k, v, g, beta, None, chunked=True)
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        qd, kd, vd, gd, bd = (t.to(dev) for t in (q, k, v, g, beta))
+        S = torch.zeros(1, HV, D, D, device=dev)
+        o1, _ = ops.delta_rule_chunked(qd[:, :, :T], kd[:, :, :T], vd[:, :, :T], gd[:, :, :T], bd[:, :, :T], S,
+                                       normalize=True, qscale=D ** -0.5)
+        o2, _ = ops.delta_rule_chunked(qd[:, :, T:], kd[:, :, T:], vd[:, :, T:], gd[:, :, T:], bd[:, :, T:], S,
+                                       normalize=True, qscale=D ** -0.5)
+        o = torch.cat([o1, o2], 2)
+    side.synchronize()
+    assert rel_err(o, o_ref) < DELTA_TOL
+    assert rel_err(S, S_ref) < DELTA_TOL
