@@ -429,9 +429,11 @@ __global__ void __launch_bounds__(256) delta_chunk_state(const unsigned char* __
                                                          float* __restrict__ state, int load_state, Tout* __restrict__ out,
                                                          SeqLayout a, int t0, int T, int nch, int B, int HK,
                                                          int HV, int vec_out) {
-    __shared__ __attribute__((aligned(16))) half_t SsT[16 * NCT][D + 8];   // S^T (fp16): [column][dk]
-    __shared__ __attribute__((aligned(16))) half_t VnT[16 * NCT][CH + 8];  // v_new^T (fp16)
-    __shared__ __attribute__((aligned(16))) half_t VdT[16 * NCT][CH + 8];  // (e^{cum_last-cum} v_new)^T
+    // double-buffered by chunk parity: a wave cannot pass the next chunk's first barrier before
+    // every wave has finished reading this chunk's tiles, so no end-of-chunk barrier is needed
+    __shared__ __attribute__((aligned(16))) half_t SsT[2][16 * NCT][D + 8];   // S^T (fp16): [column][dk]
+    __shared__ __attribute__((aligned(16))) half_t VnT[2][16 * NCT][CH + 8];  // v_new^T (fp16)
+    __shared__ __attribute__((aligned(16))) half_t VdT[2][16 * NCT][CH + 8];  // (e^{cum_last-cum} v_new)^T
     __shared__ float Ot[4][16][16 * NCT + 4];                                     // output staging per wave
 
     // XCD-aware block mapping (1-D grid): blocks are dealt to the 8 XCDs round-robin, so unit
@@ -497,13 +499,15 @@ __global__ void __launch_bounds__(256) delta_chunk_state(const unsigned char* __
         const half8* ia = cur.ia;
         const f32x4* uu = cur.uu;
 
-        // (1) S -> LDS as fp16, transposed
+        const int pb = c & 1;
+        // (1) S -> LDS as fp16, transposed (a lane's 4 rows are adjacent in S^T: one 8-byte write)
 #pragma unroll
         for (int rt = 0; rt < 2; rt++)
 #pragma unroll
-            for (int ct = 0; ct < NCT; ct++)
-#pragma unroll
-                for (int j = 0; j < 4; j++) SsT[16 * ct + n][32 * wave + 16 * rt + 4 * gq + j] = (half_t)S[rt][ct][j];
+            for (int ct = 0; ct < NCT; ct++) {
+                const half4 h = {(half_t)S[rt][ct][0], (half_t)S[rt][ct][1], (half_t)S[rt][ct][2], (half_t)S[rt][ct][3]};
+                *(half4*)&SsT[pb][16 * ct + n][32 * wave + 16 * rt + 4 * gq] = h;
+            }
         __syncthreads();
 
         // (2) w S and q_n S for chunk rows [16 wave, 16 wave + 16)
@@ -514,21 +518,24 @@ __global__ void __launch_bounds__(256) delta_chunk_state(const unsigned char* __
             QS[ct] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int ks = 0; ks < 4; ks++) {
-                half8 sb = ld_h8(&SsT[16 * ct + n][32 * ks + 8 * gq]);
+                half8 sb = ld_h8(&SsT[pb][16 * ct + n][32 * ks + 8 * gq]);
                 WS[ct] = mfma16(wa[ks], sb, WS[ct]);
                 QS[ct] = mfma16(qa[ks], sb, QS[ct]);
             }
         }
         // (3) v_new = u - w S; decayed copy for the state update
 #pragma unroll
-        for (int ct = 0; ct < NCT; ct++)
+        for (int ct = 0; ct < NCT; ct++) {
+            half4 hn, hd;
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                const int i = 16 * wave + 4 * gq + j;
                 const float vn = uu[ct][j] - WS[ct][j];
-                VnT[16 * ct + n][i] = (half_t)vn;
-                VdT[16 * ct + n][i] = (half_t)(cur.edec[j] * vn);
+                hn[j] = (half_t)vn;
+                hd[j] = (half_t)(cur.edec[j] * vn);
             }
+            *(half4*)&VnT[pb][16 * ct + n][16 * wave + 4 * gq] = hn;
+            *(half4*)&VdT[pb][16 * ct + n][16 * wave + 4 * gq] = hd;
+        }
         __syncthreads();
 
         // (4) o = e^{cum} q_n S + intra v_new
@@ -536,7 +543,7 @@ __global__ void __launch_bounds__(256) delta_chunk_state(const unsigned char* __
         for (int ct = 0; ct < NCT; ct++) {
             f32x4 o = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int ks = 0; ks < 2; ks++) o = mfma16(ia[ks], ld_h8(&VnT[16 * ct + n][32 * ks + 8 * gq]), o);
+            for (int ks = 0; ks < 2; ks++) o = mfma16(ia[ks], ld_h8(&VnT[pb][16 * ct + n][32 * ks + 8 * gq]), o);
 #pragma unroll
             for (int j = 0; j < 4; j++) Ot[wave][4 * gq + j][16 * ct + n] = cur.ecum[j] * QS[ct][j] + o[j];
         }
@@ -573,10 +580,9 @@ __global__ void __launch_bounds__(256) delta_chunk_state(const unsigned char* __
             for (int ct = 0; ct < NCT; ct++) {
                 f32x4 acc = S[rt][ct] * gamma;
 #pragma unroll
-                for (int ks = 0; ks < 2; ks++) acc = mfma16(cur.ka[rt][ks], ld_h8(&VdT[16 * ct + n][32 * ks + 8 * gq]), acc);
+                for (int ks = 0; ks < 2; ks++) acc = mfma16(cur.ka[rt][ks], ld_h8(&VdT[pb][16 * ct + n][32 * ks + 8 * gq]), acc);
                 S[rt][ct] = acc;
             }
-        __syncthreads();  // SsT / VnT / VdT are rewritten by the next chunk
     };
     // ping-pong between two operand sets (no register copies, so the wait for a prefetch only
     // covers the loads issued before it)
