@@ -57,6 +57,11 @@ SIGNATURES: dict[str, tuple] = {
     "aegist_stack_length": (I, [P]),
     "aegist_stack_forward": (I, [P, P, I, I, P]),
     "aegist_embed_bf16": (I, [P, P, P, I, I, P]),
+    "aegist_stack_snapshot": (I, [P, P]),
+    "aegist_stack_crop": (I, [P, I, P]),
+    "aegist_stack_state_bytes": (SZ, [P, I]),
+    "aegist_stack_save_state": (I, [P, I, P, SZ, P]),
+    "aegist_stack_load_state": (I, [P, I, I, P, SZ, P]),
     "aegist_gemv_i8": (I, [P, P, P, P, I, I, I, P]),
     "aegist_gemv_bf16": (I, [P, P, P, I, I, P]),
     "aegist_gemm_i8": (I, [P, P, P, P, I, I, I, I, P]),

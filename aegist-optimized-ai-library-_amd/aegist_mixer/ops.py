@@ -399,6 +399,45 @@ class HybridStack:
     def reset(self):
         call("aegist_stack_reset", self._h, _stream())
 
+    def snapshot(self):
+        """Remember the recurrent state at the current length (Lm::snapshot)."""
+        call("aegist_stack_snapshot", self._h, _stream())
+
+    def crop(self, n: int) -> int:
+        """Go back to at most n tokens (Lm::crop); returns the length kept: the latest snapshot
+        at or before n, 0 if there is none (the stack is reset), the length if n >= length."""
+        r = lib().aegist_stack_crop(self._h, int(n), _stream())
+        if r < 0:
+            raise AegistError("aegist_stack_crop", r, lib().aegist_last_error().decode(errors="replace"))
+        return r
+
+    def state_bytes(self, n: int | None = None) -> int:
+        return lib().aegist_stack_state_bytes(self._h, self.length if n is None else int(n))
+
+    def save_state(self, path, toks, key: str | None = None, b: int = 0):
+        """Write sequence b's state after len(toks) == length tokens to `path` in the engine's
+        saved-state format (Lm::save_state)."""
+        import ctypes as C
+        from . import state_file
+        n = self.length
+        if len(toks) != n:
+            raise AegistError("save_state", -1, f"{len(toks)} token ids for a length of {n}")
+        buf = C.create_string_buffer(max(1, self.state_bytes(n)))
+        call("aegist_stack_save_state", self._h, b, buf, len(buf), _stream())
+        state_file.write(path, key, list(toks), buf.raw[:self.state_bytes(n)])
+
+    def load_state(self, path, key: str | None = None, b: int = 0) -> list:
+        """Read a state written by save_state (same key) into sequence b; returns its token ids
+        (Lm::load_state). On an error the stack is left empty and the error is raised."""
+        from . import state_file
+        try:
+            toks, payload = state_file.read(path, key)
+        except state_file.StateFileError:
+            self.reset()
+            raise
+        call("aegist_stack_load_state", self._h, b, len(toks), payload, len(payload), _stream())
+        return toks
+
     @property
     def length(self) -> int:
         return lib().aegist_stack_length(self._h)

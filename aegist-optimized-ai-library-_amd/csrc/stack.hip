@@ -77,9 +77,16 @@ struct Stack {
     uint16_t* ob = nullptr;    // bf16 copy of o (GEMM input)
     void* ws = nullptr;        // chunked prefill / attention decode workspace
     size_t ws_bytes = 0;
+    // snapshots of the recurrent layers' conv and recurrent states (the KV cache is append-only,
+    // so rewinding the length is enough for it); position -1 = empty slot
+    float* snap_conv[AEGIST_STACK_SNAPSHOTS] = {};
+    float* snap_rec[AEGIST_STACK_SNAPSHOTS] = {};
+    int snap_pos[AEGIST_STACK_SNAPSHOTS] = {};
     std::vector<void*> allocs;
 
     int C() const { return 2 * cfg.hk * D + cfg.hv * D; }
+    size_t conv_bytes() const { return (size_t)std::max(1, n_delta) * cfg.max_batch * C() * 3 * 4; }
+    size_t rec_bytes() const { return (size_t)std::max(1, n_delta) * cfg.max_batch * cfg.hv * D * D * 4; }
 };
 
 int alloc(Stack* s, void** p, size_t bytes) {
@@ -231,6 +238,10 @@ int aegist_stack_create(const AegistStackConfig* cfg, void** handle) {
     s->ws_bytes = std::max(aegist_delta_chunked_workspace_bytes(c.max_batch, (int)std::min<size_t>(rows, 1 << 30), HV),
                            decode_workspace_bytes(c.max_batch, H, KV, c.max_context, false));
     A(&s->ws, s->ws_bytes);
+    for (int i = 0; i < AEGIST_STACK_SNAPSHOTS; i++) {
+        A((void**)&s->snap_conv[i], s->conv_bytes());
+        A((void**)&s->snap_rec[i], s->rec_bytes());
+    }
     if (rc) {
         aegist_stack_destroy(s);
         return rc;
@@ -262,10 +273,138 @@ int aegist_stack_reset(void* handle, void* stream) {
     const AegistStackConfig& c = s->cfg;
     const size_t mb = c.max_batch;
     hipStream_t st = AEG_STREAM(stream);
-    AEG_HIP(hipMemsetAsync(s->conv, 0, (size_t)std::max(1, s->n_delta) * mb * s->C() * 3 * 4, st));
-    AEG_HIP(hipMemsetAsync(s->rec, 0, (size_t)std::max(1, s->n_delta) * mb * c.hv * D * D * 4, st));
+    (void)c;
+    (void)mb;
+    AEG_HIP(hipMemsetAsync(s->conv, 0, s->conv_bytes(), st));
+    AEG_HIP(hipMemsetAsync(s->rec, 0, s->rec_bytes(), st));
     s->length = 0;
+    for (int i = 0; i < AEGIST_STACK_SNAPSHOTS; i++) s->snap_pos[i] = -1;
     return 0;
+}
+
+// Lm::snapshot of the engine (hybrid.rs:1060-1070): nothing to do if a snapshot at this length
+// exists; else an empty slot, or the oldest snapshot's, takes the conv and recurrent states.
+int aegist_stack_snapshot(void* handle, void* stream) {
+    Stack* s = (Stack*)handle;
+    if (!s) return fail(AEGIST_ERR_SHAPE, "stack_snapshot: null handle");
+    int slot = 0;
+    for (int i = 0; i < AEGIST_STACK_SNAPSHOTS; i++) {
+        if (s->snap_pos[i] == s->length) return 0;
+        if (s->snap_pos[i] < s->snap_pos[slot]) slot = i;  // empty (-1) sorts first, then oldest
+    }
+    hipStream_t st = AEG_STREAM(stream);
+    AEG_HIP(hipMemcpyAsync(s->snap_conv[slot], s->conv, s->conv_bytes(), hipMemcpyDeviceToDevice, st));
+    AEG_HIP(hipMemcpyAsync(s->snap_rec[slot], s->rec, s->rec_bytes(), hipMemcpyDeviceToDevice, st));
+    s->snap_pos[slot] = s->length;
+    return 0;
+}
+
+// Lm::crop (hybrid.rs:1029-1058): back to the latest snapshot at or before n; later snapshots are
+// dropped. Without one the stack starts over from zero. Returns the length kept.
+int aegist_stack_crop(void* handle, int n, void* stream) {
+    Stack* s = (Stack*)handle;
+    if (!s) return fail(AEGIST_ERR_SHAPE, "stack_crop: null handle");
+    if (n < 0) return fail(AEGIST_ERR_SHAPE, "stack_crop: negative length");
+    if (n >= s->length) return s->length;
+    int best = -1;
+    for (int i = 0; i < AEGIST_STACK_SNAPSHOTS; i++)
+        if (s->snap_pos[i] >= 0 && s->snap_pos[i] <= n && (best < 0 || s->snap_pos[i] > s->snap_pos[best])) best = i;
+    if (best < 0) {
+        const int rc = aegist_stack_reset(s, stream);
+        return rc ? rc : 0;
+    }
+    hipStream_t st = AEG_STREAM(stream);
+    AEG_HIP(hipMemcpyAsync(s->conv, s->snap_conv[best], s->conv_bytes(), hipMemcpyDeviceToDevice, st));
+    AEG_HIP(hipMemcpyAsync(s->rec, s->snap_rec[best], s->rec_bytes(), hipMemcpyDeviceToDevice, st));
+    s->length = s->snap_pos[best];
+    for (int i = 0; i < AEGIST_STACK_SNAPSHOTS; i++)
+        if (s->snap_pos[i] > s->length) s->snap_pos[i] = -1;
+    return s->length;
+}
+
+extern "C++" {
+namespace {
+// The pieces one sequence's state is made of, layer by layer, in the engine's saved-state order
+// (NextEngine::state_pieces, next.rs:2471-2500): an attention layer's first n rows of K then of
+// V for each KV head; a recurrent layer's conv state [C][3] then recurrent state [HV][dk][dv].
+template <typename F>
+void for_each_piece(const Stack* s, int b, int n, F&& f) {
+    const AegistStackConfig& c = s->cfg;
+    const size_t mb = c.max_batch, cap = c.max_context, HD = c.head_dim, KV = c.n_kv;
+    for (int l = 0; l < c.n_layers; l++) {
+        const size_t sl = s->slot[l];
+        if (c.layer_is_attn[l]) {
+            for (size_t h = 0; h < KV; h++) {
+                const size_t at = ((sl * mb + b) * KV + h) * cap * HD;
+                f((void*)(s->kc + at), (size_t)n * HD * 2);
+                f((void*)(s->vc + at), (size_t)n * HD * 2);
+            }
+        } else {
+            f((void*)(s->conv + (sl * mb + b) * s->C() * 3), (size_t)s->C() * 3 * 4);
+            f((void*)(s->rec + (sl * mb + b) * c.hv * D * D), (size_t)c.hv * D * D * 4);
+        }
+    }
+}
+}  // namespace
+}  // extern "C++"
+
+size_t aegist_stack_state_bytes(void* handle, int n) {
+    const Stack* s = (const Stack*)handle;
+    if (!s || n < 0) return 0;
+    size_t total = 0;
+    for_each_piece(s, 0, n, [&](void*, size_t bytes) { total += bytes; });
+    return total;
+}
+
+// Lm::save_state's payload (next.rs:2548-2563) for sequence b at the current length, into a host
+// buffer; returns once the copy is complete.
+int aegist_stack_save_state(void* handle, int b, void* host, size_t bytes, void* stream) {
+    Stack* s = (Stack*)handle;
+    if (!s) return fail(AEGIST_ERR_SHAPE, "stack_save_state: null handle");
+    if (b < 0 || b >= s->cfg.max_batch) return fail(AEGIST_ERR_SHAPE, "stack_save_state: sequence index out of range");
+    if (!host || bytes < aegist_stack_state_bytes(s, s->length))
+        return fail(AEGIST_ERR_WORKSPACE, "stack_save_state: host buffer smaller than aegist_stack_state_bytes");
+    hipStream_t st = AEG_STREAM(stream);
+    unsigned char* dst = (unsigned char*)host;
+    int rc = 0;
+    for_each_piece(s, b, s->length, [&](void* src, size_t nb) {
+        if (!rc && nb) rc = check_hip(hipMemcpyAsync(dst, src, nb, hipMemcpyDeviceToHost, st), "hipMemcpyAsync(save_state)");
+        dst += nb;
+    });
+    if (rc) return rc;
+    AEG_HIP(hipStreamSynchronize(st));
+    return 0;
+}
+
+// Lm::load_state (next.rs:2565-2578, read_state :2502-2538) for sequence b: n tokens' state from a
+// host buffer written by aegist_stack_save_state. The stack's length becomes n (all sequences
+// share one length), the snapshots are cleared and one is taken at n. On an error the stack is
+// left empty (reset). Returns once the copy is complete.
+int aegist_stack_load_state(void* handle, int b, int n, const void* host, size_t bytes, void* stream) {
+    Stack* s = (Stack*)handle;
+    if (!s) return fail(AEGIST_ERR_SHAPE, "stack_load_state: null handle");
+    hipStream_t st = AEG_STREAM(stream);
+    auto bail = [&](int code, const std::string& msg) {
+        (void)aegist_stack_reset(s, stream);
+        return fail(code, msg);
+    };
+    if (b < 0 || b >= s->cfg.max_batch) return bail(AEGIST_ERR_SHAPE, "stack_load_state: sequence index out of range");
+    if (n <= 0 || n >= s->cfg.max_context)
+        return bail(AEGIST_ERR_SHAPE, "stack_load_state: " + std::to_string(n) + " tokens do not fit a context of " +
+                                          std::to_string(s->cfg.max_context));
+    if (!host || bytes < aegist_stack_state_bytes(s, n))
+        return bail(AEGIST_ERR_WORKSPACE, "stack_load_state: host buffer smaller than aegist_stack_state_bytes");
+    const unsigned char* src = (const unsigned char*)host;
+    int rc = 0;
+    for_each_piece(s, b, n, [&](void* dst, size_t nb) {
+        if (!rc && nb) rc = check_hip(hipMemcpyAsync(dst, src, nb, hipMemcpyHostToDevice, st), "hipMemcpyAsync(load_state)");
+        src += nb;
+    });
+    if (rc) return bail(rc, std::string("stack_load_state: ") + aegist_last_error());
+    if ((rc = check_hip(hipStreamSynchronize(st), "hipStreamSynchronize"))) return bail(rc, aegist_last_error());
+    s->length = n;
+    for (int i = 0; i < AEGIST_STACK_SNAPSHOTS; i++) s->snap_pos[i] = -1;
+    return aegist_stack_snapshot(s, stream);
 }
 
 int aegist_stack_length(void* handle) { return handle ? ((Stack*)handle)->length : -1; }

@@ -241,6 +241,25 @@ int aegist_stack_length(void* handle);
 /* x [B, T, d] fp32 residual stream, updated in place; T == 1 takes the decode kernels,
  * T > 1 the prefill kernels. Positions continue from aegist_stack_length(). */
 int aegist_stack_forward(void* handle, float* x, int B, int T, void* stream);
+/* Snapshots (Lm::snapshot / crop, aegist_rs/src/model.rs:368-372; engine hybrid.rs:1029-1070):
+ * AEGIST_STACK_SNAPSHOTS slots hold the recurrent layers' conv and recurrent states at a length
+ * (the KV cache is append-only, so the length alone rewinds it). snapshot is a no-op when one
+ * exists at the current length, else it fills an empty slot or replaces the oldest. crop(n)
+ * returns to the latest snapshot at or before n (dropping later ones) and returns the length
+ * kept; with none it resets the stack and returns 0; n >= length keeps everything. */
+#define AEGIST_STACK_SNAPSHOTS 2
+int aegist_stack_snapshot(void* handle, void* stream);
+int aegist_stack_crop(void* handle, int n, void* stream);
+/* Saved state of one sequence (Lm::save_state / load_state payload, next.rs:2471-2578): per
+ * layer in order, an attention layer's first n rows of K then V per KV head (bf16), a recurrent
+ * layer's conv state [C][3] then state [HV][128][128] (fp32). state_bytes(n) sizes the buffer
+ * for n tokens. save copies sequence b at the current length into host memory; load copies n
+ * tokens' state of sequence b back, sets the length to n (shared by all sequences), clears the
+ * snapshots and takes one at n; on an error the stack is reset. Both return when done. The file
+ * framing (magic, JSON header with the token ids) is the host's (aegist_mixer.state_file). */
+size_t aegist_stack_state_bytes(void* handle, int n);
+int aegist_stack_save_state(void* handle, int b, void* host, size_t bytes, void* stream);
+int aegist_stack_load_state(void* handle, int b, int n, const void* host, size_t bytes, void* stream);
 /* out[i, :] = fp32(table[ids[i], :]) for n ids; the engine's embedding lookup
  * (hybrid.rs:743-758) done on the device. */
 int aegist_embed_bf16(const uint16_t* table, const int* ids, float* out, int n, int D, void* stream);

@@ -113,3 +113,12 @@ def test_linear_multi_rejects_counts():
     for n in (0, 5):
         assert L.aegist_linear_multi(None, 0, 32, 2, n, arr, None, arr, lds, ns, 2, 32, 0, None) == -1
     assert L.aegist_linear_multi(None, 0, 32, 2, 1, None, None, arr, lds, ns, 2, 32, 0, None) == -1
+
+
+def test_stack_state_entry_points_reject_null_handle():
+    L = _lib.lib()
+    assert L.aegist_stack_snapshot(None, None) == -1
+    assert L.aegist_stack_crop(None, 3, None) == -1
+    assert L.aegist_stack_state_bytes(None, 3) == 0
+    assert L.aegist_stack_save_state(None, 0, None, 0, None) == -1
+    assert L.aegist_stack_load_state(None, 0, 1, None, 0, None) == -1
