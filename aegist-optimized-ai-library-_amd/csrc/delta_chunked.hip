@@ -132,7 +132,10 @@ __global__ void __launch_bounds__(256) delta_chunk_intra(const Tin* __restrict__
     __shared__ __attribute__((aligned(16))) float As[CH][A_LD];    // A, then X = (I + A)^-1 in place
     __shared__ float Pt[3][16][17];
     __shared__ float cum_s[CH], beta_s[CH], g_s[CH];
-    __shared__ __attribute__((aligned(16))) half_t It[CH][CH + 8];  // intra, staged for fragment order
+    // intra, staged for fragment order; with fp32 inputs it borrows Vl, which is first written
+    // after the intra fragments have gone out (keeps the fp32 variant at two workgroups per CU)
+    __shared__ __attribute__((aligned(16))) half_t ItBuf[kSplitV ? 1 : CH][CH + 8];
+    half_t (*It)[CH + 8] = kSplitV ? (half_t (*)[CH + 8])&Vl[0][0] : ItBuf;
 
     const int c = blockIdx.x, hv = blockIdx.y, b = blockIdx.z, nch = gridDim.x;
     const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE, n = lane % 16, gq = lane / 16;
@@ -278,6 +281,7 @@ __global__ void __launch_bounds__(256) delta_chunk_intra(const Tin* __restrict__
             intra[f] = ld_h8(&It[r][c0]);
         }
     }
+    if constexpr (kSplitV) __syncthreads();  // It aliases Vl, written next
 
     // ---- 4. v (fp16 hi / lo) into the q tile's space; X = (I + A)^-1, blocked by 16
 #pragma unroll

@@ -291,6 +291,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run a 1 GiB device copy (calibrates rocprof FETCH_SIZE / WRITE_SIZE)")
+    ap.add_argument("--legs", type=str, default="prefill,attention_decode,attention_prefill,proj,stack",
+                    help="comma list of the extra legs to run after the decode headline (default: all); "
+                         "'none' for the headline only")
     ap.add_argument("--traffic", type=str, default=str(ROOT / "profiles" / "delta_decode_traffic.json"),
                     help="JSON file with measured HBM bytes per decode launch (from rocprof --pmc)")
     args = ap.parse_args()
@@ -369,11 +372,15 @@ def main():
     if args.traffic and os.path.exists(args.traffic):
         with open(args.traffic) as f:
             res["roofline"]["traffic"] = json.load(f).get("bytes_per_launch")
-    res["prefill"] = bench_prefill(torch, ops, dev)
-    res["attention_decode"] = bench_attention_decode(torch, ops, dev)
-    res["attention_prefill"] = bench_attention_prefill(torch, ops, dev)
-    res["proj"] = bench_proj(torch, ops, dev)
-    res["stack"] = bench_stack(torch, ops, dev)
+    legs = {"prefill": bench_prefill, "attention_decode": bench_attention_decode,
+            "attention_prefill": bench_attention_prefill, "proj": bench_proj, "stack": bench_stack}
+    want = [] if args.legs.strip() == "none" else [x.strip() for x in args.legs.split(",") if x.strip()]
+    unknown = [x for x in want if x not in legs]
+    if unknown:
+        print(f"unknown --legs {unknown}; choose from {sorted(legs)}", file=sys.stderr)
+        sys.exit(2)
+    for name in want:
+        res[name] = legs[name](torch, ops, dev)
     if args.calib_copy:
         src = torch.empty(1 << 28, device=dev)  # 1 GiB fp32
         dst = torch.empty_like(src)
