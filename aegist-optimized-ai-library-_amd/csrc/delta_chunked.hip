@@ -40,7 +40,7 @@ constexpr int D = 128;
 constexpr int CH = 64;       // chunk length
 constexpr int SEG = 2048;    // tokens per segment (workspace granularity)
 #ifndef K2_NCT
-#define K2_NCT 1              // 16-column tiles per K2 workgroup (1: 8 workgroups per value head)
+#define K2_NCT 2              // 16-column tiles per K2 workgroup (4 workgroups per value head)
 #endif
 constexpr int QK_LD = D + 8; // fp16 row stride (elements) of the q/k tiles in LDS
 constexpr int A_LD = 68;     // fp32 row stride of the A matrix in LDS (16-byte aligned rows)
@@ -552,27 +552,32 @@ __global__ void __launch_bounds__(256) delta_chunk_state(const unsigned char* __
             for (int j = 0; j < 4; j++) Ot[wave][4 * gq + j][16 * ct + n] = cur.ecum[j] * QS[ct][j] + o[j];
         }
         wave_sync();
-        {   // this wave's 16 rows x 16 NCT columns: lane = (row, 8-column part)
+        {   // this wave's 16 rows x 16 NCT columns: lane = (row, 8-column part), 64 / LPR rows
+            // per pass
             constexpr int LPR = 2 * NCT;  // lanes per row
-            const int r = lane / LPR, p8 = (lane % LPR) * 8, tok = t0 + c * CH + 16 * wave + r;
-            if (r < 16 && tok < T) {
-                Tout* dst = out + b * a.sb_o + (long long)tok * a.st_o + hv * a.sh_o + col0 + p8;
-                const float* src = &Ot[wave][r][p8];
-                if (vec_out) {
-                    if constexpr (sizeof(Tout) == 2) {
-                        uint4 pk;
-                        pk.x = (uint32_t)f2bf(src[0]) | ((uint32_t)f2bf(src[1]) << 16);
-                        pk.y = (uint32_t)f2bf(src[2]) | ((uint32_t)f2bf(src[3]) << 16);
-                        pk.z = (uint32_t)f2bf(src[4]) | ((uint32_t)f2bf(src[5]) << 16);
-                        pk.w = (uint32_t)f2bf(src[6]) | ((uint32_t)f2bf(src[7]) << 16);
-                        *(uint4*)dst = pk;
-                    } else {
-                        ((float4*)dst)[0] = float4{src[0], src[1], src[2], src[3]};
-                        ((float4*)dst)[1] = float4{src[4], src[5], src[6], src[7]};
-                    }
-                } else {
+            constexpr int RPP = WAVE / LPR;
 #pragma unroll
-                    for (int e = 0; e < 8; e++) Act<Tout>::st(dst, e, src[e]);
+            for (int r0 = 0; r0 < 16; r0 += RPP) {
+                const int r = r0 + lane / LPR, p8 = (lane % LPR) * 8, tok = t0 + c * CH + 16 * wave + r;
+                if (r < 16 && tok < T) {
+                    Tout* dst = out + b * a.sb_o + (long long)tok * a.st_o + hv * a.sh_o + col0 + p8;
+                    const float* src = &Ot[wave][r][p8];
+                    if (vec_out) {
+                        if constexpr (sizeof(Tout) == 2) {
+                            uint4 pk;
+                            pk.x = (uint32_t)f2bf(src[0]) | ((uint32_t)f2bf(src[1]) << 16);
+                            pk.y = (uint32_t)f2bf(src[2]) | ((uint32_t)f2bf(src[3]) << 16);
+                            pk.z = (uint32_t)f2bf(src[4]) | ((uint32_t)f2bf(src[5]) << 16);
+                            pk.w = (uint32_t)f2bf(src[6]) | ((uint32_t)f2bf(src[7]) << 16);
+                            *(uint4*)dst = pk;
+                        } else {
+                            ((float4*)dst)[0] = float4{src[0], src[1], src[2], src[3]};
+                            ((float4*)dst)[1] = float4{src[4], src[5], src[6], src[7]};
+                        }
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 8; e++) Act<Tout>::st(dst, e, src[e]);
+                    }
                 }
             }
         }
