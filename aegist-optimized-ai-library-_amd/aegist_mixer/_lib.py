@@ -62,6 +62,12 @@ SIGNATURES: dict[str, tuple] = {
     "aegist_stack_state_bytes": (SZ, [P, I]),
     "aegist_stack_save_state": (I, [P, I, P, SZ, P]),
     "aegist_stack_load_state": (I, [P, I, I, P, SZ, P]),
+    "aegist_idx_prep": (I, [P, P, P, P, I, I, I, I, I, F, F, P]),
+    "aegist_idx_blocks": (I, [P, P, P, I, I, I, I, I, F, F, P]),
+    "aegist_idx_scores": (I, [P, P, P, I, I, I, I, I, I, P]),
+    "aegist_idx_select": (I, [P, P, P, I, I, I, I, I, P]),
+    "aegist_attention_gated_list": (I, [P, P, P, P, P, I, I, I, I, I, F, P, P, I, I, P]),
+    "aegist_gated_norm2": (I, [P, P, P, P, I, I, I, F, I, P]),
     "aegist_gemv_i8": (I, [P, P, P, P, I, I, I, P]),
     "aegist_gemv_bf16": (I, [P, P, P, I, I, P]),
     "aegist_gemm_i8": (I, [P, P, P, P, I, I, I, I, P]),

@@ -259,6 +259,55 @@ def engine_gated_norm(o, z, w, eps=1e-6):
 
 # --- the hybrid mixer stack (config 4) ----------------------------------------------------------
 
+# --- second core: QSA indexer and gated norm with a choice of gate (engine ABI, batch 1) -----
+
+def engine_idx_prep(qk, qw, qi, kraw, pos0: int, rotary_dim: int = 64, theta: float = 1e7, eps: float = 1e-6):
+    """qk [T, H+1, 128] -> qi [T, H, 128] (normed, roped) and kraw[pos0:pos0+T] (raw keys)."""
+    _need_contig(qk, qw, qi, kraw)
+    T, H1, HD = qk.shape
+    call("aegist_idx_prep", _p(qk), _p(qw), _p(qi), _p(kraw), T, H1 - 1, HD, rotary_dim, pos0, eps, theta, _stream())
+    return qi
+
+
+def engine_idx_blocks(kraw, kw, bk, b0: int, n: int, R: int, rotary_dim: int = 64, theta: float = 1e7,
+                      eps: float = 1e-6):
+    _need_contig(kraw, kw, bk)
+    call("aegist_idx_blocks", _p(kraw), _p(kw), _p(bk), b0, n, R, kraw.shape[-1], rotary_dim, eps, theta, _stream())
+    return bk
+
+
+def engine_idx_scores(qi, bk, sc, pos0: int, R: int):
+    _need_contig(qi, bk, sc)
+    T, H, HD = qi.shape
+    call("aegist_idx_scores", _p(qi), _p(bk), _p(sc), T, H, HD, pos0, R, sc.shape[1], _stream())
+    return sc
+
+
+def engine_idx_select(sc, blist, nsel, top: int, R: int, pos0: int):
+    _need_contig(sc, blist, nsel)
+    call("aegist_idx_select", _p(sc), _p(blist), _p(nsel), sc.shape[0], top, R, pos0, sc.shape[1], _stream())
+    return blist, nsel
+
+
+def engine_attention_gated_list(q, kc, vc, qg, pos0: int, blist, nsel, top: int, R: int, scale: float | None = None):
+    """q [T, H, 256] normed + roped; kc, vc [KV, cap, 256] bf16; qg [T, H, 512]; -> out [T, H, 256]."""
+    _need_contig(q, kc, vc, qg, blist, nsel)
+    T, H, HD = q.shape
+    KV, cap = kc.shape[0], kc.shape[1]
+    out = torch.empty(T, H, HD, dtype=torch.float32, device=q.device)
+    call("aegist_attention_gated_list", _p(q), _p(kc), _p(vc), _p(qg), _p(out), T, H, KV, pos0, cap,
+         HD ** -0.5 if scale is None else scale, _p(blist), _p(nsel), top, R, _stream())
+    return out
+
+
+def engine_gated_norm2(o, z, w, sig: bool, eps: float = 1e-6):
+    _need_contig(o, z, w)
+    T, HV, DV = o.shape
+    out = torch.empty_like(o)
+    call("aegist_gated_norm2", _p(o), _p(z), _p(w), _p(out), T, HV, DV, eps, int(sig), _stream())
+    return out
+
+
 # --- projections (QLinear, aegist/model.py:78-93; engine gemv_i8 / gemm_i8 / gemv_bf16) -------
 
 def linear(x, weight, scale=None, out=None, accumulate: bool = False):

@@ -137,6 +137,16 @@ __device__ void merge_splits(const float* __restrict__ part, const float* __rest
 // With `counters` set, the last workgroup of each (sequence, KV head) to finish merges all
 // splits and writes the gated output (the counter is zeroed by the prep kernel that runs
 // first and reset by that last workgroup); otherwise attn_decode_merge_kernel does it.
+// Keys of a sparse (listed-block) query, attention_gated_list (next.cu:648-705): the query at
+// position p = pos0 + b sees the R keys of each of its nsel[b] listed blocks, in list order, then
+// the keys of its own incomplete block, positions complete R .. p (complete = (p + 1) / R).
+// blist == nullptr: the plain range [0, L) of sequence b's cache.
+struct KeyList {
+    const int* blist;
+    const int* nsel;
+    int top, R, pos0;
+};
+
 template <typename TG, typename Tout>
 __global__ void __launch_bounds__(256) attn_decode_split_kernel(const float* __restrict__ q,
                                                                 const uint16_t* __restrict__ kc,
@@ -145,7 +155,8 @@ __global__ void __launch_bounds__(256) attn_decode_split_kernel(const float* __r
                                                                 int H, int KV, int L, int cap, int per_split,
                                                                 float scale, int* __restrict__ counters,
                                                                 const TG* __restrict__ gate, long long gate_stride,
-                                                                Tout* __restrict__ out, long long out_stride) {
+                                                                Tout* __restrict__ out, long long out_stride,
+                                                                KeyList kl) {
     // V staging per wave during the loop; the 4-wave merge buffer reuses the same bytes after it
     __shared__ __attribute__((aligned(16))) unsigned char vbuf_raw[4 * TILE * VROW];
     __shared__ __attribute__((aligned(16))) unsigned char kbuf[4][TILE * VROW];
@@ -159,7 +170,18 @@ __global__ void __launch_bounds__(256) attn_decode_split_kernel(const float* __r
     const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
     const int n = lane % 16, g = lane / 16;
     const int G = H / KV;
-    const int k0 = split * per_split, k1 = min(L, k0 + per_split);
+    // listed keys: this query's key count and the list -> cache position map (batch-1 cache)
+    const bool listed = kl.blist != nullptr;
+    int Lb = L, nsR = 0, tail0 = 0;
+    const int* bl = nullptr;
+    if (listed) {
+        const int p = kl.pos0 + b, complete = (p + 1) / kl.R;
+        nsR = kl.nsel[b] * kl.R;
+        tail0 = complete * kl.R;
+        Lb = nsR + (p + 1 - tail0);
+        bl = kl.blist + (size_t)b * kl.top;
+    }
+    const int k0 = split * per_split, k1 = min(Lb, k0 + per_split);
 
     // ---- Q operand: rows 0..7 = hi(q*scale), rows 8..15 = lo; lane row n, k elems 8g..8g+7
     bf16x8 qa[8];
@@ -180,8 +202,10 @@ __global__ void __launch_bounds__(256) attn_decode_split_kernel(const float* __r
         }
     }
 
-    const uint16_t* kbase = kc + ((size_t)b * KV + kvh) * (size_t)cap * HD;
-    const uint16_t* vbase = vc + ((size_t)b * KV + kvh) * (size_t)cap * HD;
+    const size_t cache_row = listed ? (size_t)kvh : (size_t)b * KV + kvh;
+    const uint16_t* kbase = kc + cache_row * (size_t)cap * HD;
+    const uint16_t* vbase = vc + cache_row * (size_t)cap * HD;
+    auto key_pos = [&](int j) { return !listed ? j : j < nsR ? bl[j / kl.R] * kl.R + j % kl.R : tail0 + (j - nsR); };
 
     // running softmax state for heads 4*(g%2)+j, j < 4 (duplicated in lanes g and g+2)
     float m_run[4], l_run[4];
@@ -205,7 +229,7 @@ __global__ void __launch_bounds__(256) attn_decode_split_kernel(const float* __r
 #pragma unroll
         for (int it = 0; it < NST; it++) {
             const int idx = it * WAVE + lane, row = idx / (HD * 2 / 16), cc = idx % (HD * 2 / 16);
-            const int key = min(t0 + row, k1 - 1);
+            const int key = key_pos(min(t0 + row, k1 - 1));
             kreg[it] = *(const uint4*)(kbase + (size_t)key * HD + cc * 8);
             vreg[it] = *(const uint4*)(vbase + (size_t)key * HD + cc * 8);
         }
@@ -616,7 +640,8 @@ size_t decode_workspace_bytes(int B, int H, int KV, int L, bool with_q) {
 template <typename TG, typename Tout>
 int launch_decode_core(const float* q, const uint16_t* kc, const uint16_t* vc, const TG* gate, long long gate_stride,
                        Tout* out, long long out_stride, int B, int H, int KV, int L, int cap, float scale,
-                       void* ws, size_t ws_bytes, hipStream_t st, int* counters = nullptr) {
+                       void* ws, size_t ws_bytes, hipStream_t st, int* counters = nullptr,
+                       KeyList kl = KeyList{nullptr, nullptr, 0, 0, 0}) {
     if (KV <= 0 || H % KV || H / KV > 8) return fail(AEGIST_ERR_SHAPE, "attention decode: need H % KV == 0 and H/KV <= 8");
     if (L <= 0 || L > cap) return fail(AEGIST_ERR_SHAPE, "attention decode: need 0 < L <= cap");
     DecodeSplit sp = choose_split(B, KV, L);
@@ -627,7 +652,7 @@ int launch_decode_core(const float* q, const uint16_t* kc, const uint16_t* vc, c
     size_t part_bytes = ((size_t)B * KV * sp.nsplit * G * HD * 4 + 255) / 256 * 256;
     float* ml = (float*)((char*)ws + part_bytes);
     attn_decode_split_kernel<TG, Tout><<<dim3(sp.nsplit, KV, B), 256, 0, st>>>(
-        q, kc, vc, part, ml, H, KV, L, cap, sp.per_split, scale, counters, gate, gate_stride, out, out_stride);
+        q, kc, vc, part, ml, H, KV, L, cap, sp.per_split, scale, counters, gate, gate_stride, out, out_stride, kl);
     int rc = after_launch("attention_decode_split");
     if (rc || counters) return rc;
     attn_decode_merge_kernel<TG, Tout><<<B * KV, 256, 0, st>>>(part, ml, gate, gate_stride, out, out_stride, H, KV,
@@ -751,6 +776,26 @@ int aegist_attention_gated(const float* q, const uint16_t* kc, const uint16_t* v
     Strides3 qs{0, (long long)H * HD, HD};
     Strides3 gs{0, (long long)H * 2 * HD, 2 * HD};
     return launch_prefill_core(q, qs, kc, vc, qg + HD, gs, out, qs, 1, H, KV, T, pos0, cap, scale, st);
+}
+
+// attention_gated over listed blocks (next.cu:648-705): the split-K decode kernel with one query
+// token per "sequence" and its keys taken from the block list. Engine layouts as attention_gated.
+int aegist_attention_gated_list(const float* q, const uint16_t* kc, const uint16_t* vc, const float* qg, float* out,
+                                int T, int H, int KV, int pos0, int cap, float scale, const int* blist,
+                                const int* nsel, int top, int R, void* stream) {
+    AEG_REQUIRE(T >= 0 && H > 0 && KV > 0 && H % KV == 0 && H / KV <= 8,
+                "attention_gated_list: need H % KV == 0 and H/KV <= 8");
+    AEG_REQUIRE(top > 0 && R > 0 && pos0 >= 0 && pos0 + T <= cap, "attention_gated_list: bad list or positions");
+    if (T == 0) return 0;
+    // longest key list: top blocks plus the keys of an incomplete block, and never more than the
+    // last query's position + 1
+    const int Lmax = std::min(top * R + R - 1, pos0 + T);
+    const size_t need = decode_workspace_bytes(T, H, KV, Lmax, false);
+    int rc = 0;
+    void* ws = mirror_workspace(need, &rc);
+    if (rc) return rc;
+    return launch_decode_core<float, float>(q, kc, vc, qg + HD, 2 * HD, out, HD, T, H, KV, Lmax, cap, scale, ws, need,
+                                            AEG_STREAM(stream), nullptr, KeyList{blist, nsel, top, R, pos0});
 }
 
 }  // extern "C"

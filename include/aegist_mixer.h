@@ -265,6 +265,37 @@ int aegist_stack_load_state(void* handle, int b, int n, const void* host, size_t
 int aegist_embed_bf16(const uint16_t* table, const int* ids, float* out, int n, int D, void* stream);
 
 /* -------------------------------------------------------------------------------------
+ * Second language core: QSA sparse-attention indexer and the gated norm with a choice of gate
+ * (QSAIndexer, aegist/hc.py:237-283; NextEngine::mixer, aegist_rs/src/next.rs:1866-1925).
+ * Engine layouts, batch 1: qk [T, (H+1)*128] fp32 (H index query heads then one index key);
+ * qi [T, H, 128]; kraw [cap, 128] fp32 raw index keys; bk [cap/R, 128] fp32 block keys;
+ * sc [T, nbmax]; blist [T, top] int32; nsel [T] int32. The indexer head dim must be 128.
+ * ------------------------------------------------------------------------------------- */
+/* idx_prep, next.cu:488-503: qi = rope(znorm(q)) at pos0 + t; kraw[pos0 + t] = raw key */
+int aegist_idx_prep(const float* qk, const uint16_t* qw, float* qi, float* kraw, int T, int H, int HD, int RD,
+                    int pos0, float eps, float theta, void* stream);
+/* idx_blocks, next.cu:505-520: bk[b] = rope(znorm(mean of kraw[b R .. b R + R - 1]), b R) for
+ * b in [b0, b0 + n) */
+int aegist_idx_blocks(const float* kraw, const uint16_t* kw, float* bk, int b0, int n, int R, int HD, int RD,
+                      float eps, float theta, void* stream);
+/* idx_scores, next.cu:522-541: sc[t, b] = sum_h relu(qi[t, h] . bk[b]) / sqrt(128) for the
+ * blocks complete at the query's position (b < (pos0 + t + 1) / R) */
+int aegist_idx_scores(const float* qi, const float* bk, float* sc, int T, int H, int HD, int pos0, int R, int nbmax,
+                      void* stream);
+/* idx_select, next.cu:543-625: per query, all n complete blocks when n <= top (nsel = n), else
+ * the top highest scores (ties to the lower block), listed in block order (nsel = top) */
+int aegist_idx_select(const float* sc, int* blist, int* nsel, int T, int top, int R, int pos0, int nbmax,
+                      void* stream);
+/* attention_gated_list, next.cu:627-705: attention_gated for query t over the R keys of each
+ * listed block plus its own incomplete block (positions (pos0 + t + 1) / R * R .. pos0 + t) */
+int aegist_attention_gated_list(const float* q, const uint16_t* kc, const uint16_t* vc, const float* qg, float* out,
+                                int T, int H, int KV, int pos0, int cap, float scale, const int* blist,
+                                const int* nsel, int top, int R, void* stream);
+/* gated_norm2, next.cu:129-142: out = w * rmsnorm(o) * (sig ? sigmoid(z) : silu(z)) */
+int aegist_gated_norm2(const float* o, const float* z, const uint16_t* w, float* out, int T, int HV, int DV, float eps,
+                       int sig, void* stream);
+
+/* -------------------------------------------------------------------------------------
  * Projections (QLinear, aegist/model.py:78-93: int8 weight W [N, K] with a per-output-row bf16
  * absmax scale; and plain bf16 weights):  Y[m, n] (+)= scale[n] * sum_k X[m, k] W[n, k],
  * fp32 accumulation; accumulate != 0 adds into Y (the fused residual add). K % 16 == 0 and

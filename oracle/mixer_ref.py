@@ -251,6 +251,98 @@ def attention_decode(qg, k_new, v_new, q_norm_w, k_norm_w, kc, vc, pos: int, rot
     return gated_attention_out(y, gate).reshape(B, H, HD2 // 2)
 
 
+# --- QSA sparse-attention indexer of the second core (hc.py:237-283; next.cu:488-705) ------
+
+def idx_prep(qk, qw, pos0: int, rotary_dim: int, theta: float, eps: float = 1e-6):
+    """qk ``[T, (H+1), HD]`` (H index query heads, then the index key). Returns
+    (qi ``[T, H, HD]`` = rope(znorm_qw(q)) at positions pos0.., kraw ``[T, HD]`` the raw keys)
+    (hc.py:255, 264; next.cu:488-503)."""
+    T = qk.shape[0]
+    q, k = qk[:, :-1].float(), qk[:, -1].float()
+    cos, sin = rope_tables(rotary_dim, theta, torch.arange(pos0, pos0 + T))
+    qi = apply_partial_rope(znorm(q, qw.float(), eps), cos.unsqueeze(1), sin.unsqueeze(1))
+    return qi, k
+
+
+def idx_blocks(kraw, kw, R: int, b0: int, n: int, rotary_dim: int, theta: float, eps: float = 1e-6):
+    """Block keys b0 .. b0+n-1: the mean of R raw keys, znorm_kw, rope at the block's first
+    position b R (hc.py:265-268 with fp32 keys, as the engine keeps them; next.cu:505-520).
+    kraw ``[>= (b0+n) R, HD]`` fp32. Returns ``[n, HD]``."""
+    HD = kraw.shape[-1]
+    blocks = kraw[b0 * R:(b0 + n) * R].float().view(n, R, HD)
+    m = blocks[:, 0].clone()
+    for j in range(1, R):  # summed in order, then divided, as the engine does
+        m = m + blocks[:, j]
+    m = m / R
+    cos, sin = rope_tables(rotary_dim, theta, torch.arange(b0, b0 + n) * R)
+    return apply_partial_rope(znorm(m, kw.float(), eps), cos, sin)
+
+
+def idx_scores(qi, bk, pos0: int, R: int):
+    """``sc[t, b] = sum_h relu(qi[t, h] . bk[b]) / sqrt(HD)`` for the blocks complete at the
+    query's position, -inf elsewhere (hc.py:269-273; next.cu:522-541). Returns ``[T, nb]``."""
+    T, H, HD = qi.shape
+    nb = bk.shape[0]
+    d = torch.einsum("thd,nd->thn", qi.double(), bk.double())
+    sc = (torch.relu(d).sum(1) / math.sqrt(HD)).float()
+    vis = (torch.arange(pos0, pos0 + T) + 1) // R
+    return sc.masked_fill(torch.arange(nb).view(1, -1) >= vis.view(-1, 1), float("-inf"))
+
+
+def idx_select(sc, top: int, R: int, pos0: int):
+    """Per query: every complete block when there are at most ``top`` of them, else the ``top``
+    highest scores with ties going to the lower block, listed in block order (next.cu:543-625;
+    hc.py:274-278 leaves the tie order to torch.topk). Returns a list of block-index lists."""
+    out = []
+    for t in range(sc.shape[0]):
+        n = (pos0 + t + 1) // R
+        if n <= top:
+            out.append(list(range(n)))
+            continue
+        s = sc[t, :n].tolist()
+        order = sorted(range(n), key=lambda b: (-s[b], b))
+        out.append(sorted(order[:top]))
+    return out
+
+
+def attention_list(q, kc, vc, qg, pos0: int, lists, R: int):
+    """attention_gated over each query's listed blocks plus its own incomplete block
+    (next.cu:627-705; hc.py:279-283 as a mask). q ``[T, H, HD]`` (normed, roped), kc / vc
+    ``[KV, cap, HD]``, qg ``[T, H, 2 HD]`` (gate = second half). Returns ``[T, H, HD]`` fp32."""
+    T, H, HD = q.shape
+    KV = kc.shape[0]
+    g = H // KV
+    out = torch.empty(T, H, HD)
+    for t in range(T):
+        p = pos0 + t
+        complete = (p + 1) // R
+        keys = [b * R + j for b in lists[t] for j in range(R)] + list(range(complete * R, p + 1))
+        idx = torch.tensor(keys, dtype=torch.long)
+        for h in range(H):
+            k = kc[h // g, idx].double()
+            v = vc[h // g, idx].double()
+            a = torch.softmax(k @ q[t, h].double() / math.sqrt(HD), 0)
+            out[t, h] = ((a @ v) * torch.sigmoid(qg[t, h, HD:].double())).float()
+    return out
+
+
+def qsa_mask(sc, top: int, R: int, pos0: int, L: int):
+    """The indexer's output in hc.py's form (hc.py:270-283): a bool mask ``[T, L]`` of the keys
+    each query attends to (chosen blocks' tokens, its own incomplete block, causal). Picks with
+    torch.topk, so ties are resolved however torch resolves them."""
+    T, nb = sc.shape
+    p = torch.arange(pos0, pos0 + T)
+    complete = (p + 1) // R
+    k_top = min(top, nb)
+    chosen = torch.zeros(T, nb, dtype=torch.bool)
+    chosen.scatter_(-1, sc.topk(k_top, -1).indices, True)
+    chosen &= torch.isfinite(sc)
+    tok = chosen.repeat_interleave(R, -1)
+    tail = torch.arange(L).view(1, -1) >= (complete * R).view(-1, 1)
+    causal = torch.arange(L).view(1, -1) <= p.view(-1, 1)
+    return (F.pad(tok, (0, L - nb * R)) | tail) & causal
+
+
 # --- projections: QLinear (model.py:78-93) and the engine matvecs (aegist.cu:52-172) --------
 
 def qlinear_quantize(weight: torch.Tensor):

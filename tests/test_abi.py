@@ -122,3 +122,24 @@ def test_stack_state_entry_points_reject_null_handle():
     assert L.aegist_stack_state_bytes(None, 3) == 0
     assert L.aegist_stack_save_state(None, 0, None, 0, None) == -1
     assert L.aegist_stack_load_state(None, 0, 1, None, 0, None) == -1
+
+
+def test_indexer_entry_points_reject_shapes():
+    L = _lib.lib()
+    # the indexer head dim must be 128
+    assert L.aegist_idx_prep(None, None, None, None, 1, 4, 64, 64, 0, 1e-6, 1e7, None) == -1
+    assert L.aegist_idx_blocks(None, None, None, 0, 1, 4, 64, 64, 1e-6, 1e7, None) == -1
+    assert L.aegist_idx_scores(None, None, None, 1, 4, 64, 0, 4, 8, None) == -1
+    # odd rotary dim
+    assert L.aegist_idx_prep(None, None, None, None, 1, 4, 128, 63, 0, 1e-6, 1e7, None) == -1
+    # nbmax below the number of complete blocks
+    assert L.aegist_idx_select(None, None, None, 1, 16, 4, 100, 10, None) == -1
+    # top / R must be positive; list attention needs H % KV == 0 and positions inside the cache
+    assert L.aegist_idx_select(None, None, None, 1, 0, 4, 0, 8, None) == -1
+    assert L.aegist_attention_gated_list(None, None, None, None, None, 1, 6, 4, 0, 8, 1.0, None, None, 4, 4,
+                                         None) == -1
+    assert L.aegist_attention_gated_list(None, None, None, None, None, 2, 16, 2, 7, 8, 1.0, None, None, 4, 4,
+                                         None) == -1
+    assert L.aegist_gated_norm2(None, None, None, None, 1, 0, 128, 1e-6, 1, None) == -1
+    # empty inputs are a no-op
+    assert L.aegist_idx_select(None, None, None, 0, 16, 4, 0, 8, None) == 0

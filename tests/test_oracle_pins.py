@@ -306,3 +306,78 @@ def test_qlinear_torch_module_form_matches_engine_form():
     assert rel_err(R.qlinear_torch(x, q, s), R.qlinear_engine(x, q, s)) < 1e-5
     # and both approximate the unquantised linear to the int8 step size
     assert rel_err(R.qlinear_engine(x, q, s), x @ w.t()) < 2e-2
+
+
+# --- QSA indexer (hc.py:237-283; next.cu:488-705) -------------------------------------------
+
+def test_idx_select_known_answers():
+    sc = torch.tensor([[1.0, 3.0, 3.0, 2.0, 3.0, 0.0, 0.0, 0.0]])
+    # position 7 with R = 1: 8 complete blocks; top 2 of {3, 3, 3} go to the lower blocks
+    assert R.idx_select(sc, top=2, R=1, pos0=7) == [[1, 2]]
+    assert R.idx_select(sc, top=4, R=1, pos0=7) == [[1, 2, 3, 4]]
+    # at most `top` complete blocks: all of them, whatever the scores
+    assert R.idx_select(sc, top=8, R=1, pos0=7) == [[0, 1, 2, 3, 4, 5, 6, 7]]
+    # R = 2, position 4: (4 + 1) // 2 = 2 complete blocks <= top 3
+    assert R.idx_select(sc, top=3, R=2, pos0=4) == [[0, 1]]
+    # all-zero scores (every head's dot product negative): the lowest blocks
+    assert R.idx_select(torch.zeros(1, 10), top=3, R=1, pos0=9) == [[0, 1, 2]]
+
+
+def test_idx_scores_and_blocks_brute_force():
+    g = torch.Generator().manual_seed(3)
+    T, H, HD, RB, pos0 = 2, 3, 8, 2, 5
+    qi = torch.randn(T, H, HD, generator=g)
+    bk = torch.randn(4, HD, generator=g)
+    sc = R.idx_scores(qi, bk, pos0, RB)
+    for t in range(T):
+        for b in range(4):
+            if b >= (pos0 + t + 1) // RB:
+                assert sc[t, b] == float("-inf")
+                continue
+            want = sum(max(0.0, sum(float(qi[t, h, i]) * float(bk[b, i]) for i in range(HD))) for h in range(H))
+            assert abs(float(sc[t, b]) - want / math.sqrt(HD)) < 1e-5 * (1 + abs(want))
+    # block keys: R = 1 is rope(znorm(key)) at the key's own position; R = 2 averages pairs
+    kraw = torch.randn(8, 128, generator=g)
+    kw = torch.randn(128, generator=g) * 0.1
+    one = R.idx_blocks(kraw, kw, 1, 0, 8, 64, 1e7)
+    cos, sin = R.rope_tables(64, 1e7, torch.arange(8))
+    assert torch.allclose(one, R.apply_partial_rope(R.znorm(kraw, kw), cos, sin), atol=1e-6)
+    two = R.idx_blocks(kraw, kw, 2, 1, 3, 64, 1e7)
+    mean = (kraw[2:8:2] + kraw[3:8:2]) / 2
+    cos, sin = R.rope_tables(64, 1e7, torch.tensor([2, 4, 6]))
+    assert torch.allclose(two, R.apply_partial_rope(R.znorm(mean, kw), cos, sin), atol=1e-6)
+
+
+def test_engine_list_form_equals_hc_mask_form():
+    """The engine's block lists + tail select exactly the keys of hc.py's mask, and attention
+    over them equals SDPA with that mask (hc.py:298-299)."""
+    g = torch.Generator().manual_seed(4)
+    T, H, KV, HD, RB, top, pos0 = 6, 4, 2, 32, 4, 5, 60
+    L = pos0 + T
+    nb = L // RB
+    sc = torch.rand(T, nb, generator=g)  # continuous: no ties
+    vis = (torch.arange(pos0, L) + 1) // RB
+    sc = sc.masked_fill(torch.arange(nb).view(1, -1) >= vis.view(-1, 1), float("-inf"))
+    lists = R.idx_select(sc, top, RB, pos0)
+    mask = R.qsa_mask(sc, top, RB, pos0, L)
+    for t in range(T):
+        p = pos0 + t
+        keys = {b * RB + j for b in lists[t] for j in range(RB)} | set(range((p + 1) // RB * RB, p + 1))
+        assert set(torch.nonzero(mask[t]).flatten().tolist()) == keys
+    q = torch.randn(T, H, HD, generator=g)
+    kc = torch.randn(KV, L, HD, generator=g)
+    vc = torch.randn(KV, L, HD, generator=g)
+    qg = torch.randn(T, H, 2 * HD, generator=g)
+    got = R.attention_list(q, kc, vc, qg, pos0, lists, RB)
+    k = kc.repeat_interleave(H // KV, 0).unsqueeze(0)
+    v = vc.repeat_interleave(H // KV, 0).unsqueeze(0)
+    y = F.scaled_dot_product_attention(q.transpose(0, 1).unsqueeze(0), k, v, attn_mask=mask)[0].transpose(0, 1)
+    assert torch.allclose(got, y * torch.sigmoid(qg[..., HD:]), atol=1e-5)
+
+
+def test_gated_norm_sigmoid_gate_closed_form():
+    g = torch.Generator().manual_seed(5)
+    o, z, w = torch.randn(3, 16, generator=g), torch.randn(3, 16, generator=g), torch.randn(16, generator=g)
+    rms = torch.sqrt((o.double() ** 2).mean(-1, keepdim=True) + 1e-6)
+    want = w.double() * (o.double() / rms) / (1 + torch.exp(-z.double()))
+    assert torch.allclose(R.gated_norm(o, z, w, act="sigmoid").double(), want, atol=1e-6)
