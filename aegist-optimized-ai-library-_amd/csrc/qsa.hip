@@ -12,8 +12,8 @@
 // The attention over the listed blocks is attention_gated_list (attention.hip).
 //
 // Scores use fp32 MFMA (v_mfma_f32_16x16x4f32) so the selection sees fp32 products like the
-// engine's; the selection is a four-pass 8-bit radix select on the (non-negative) score bits in
-// LDS, then an order-preserving compaction with wave ballots.
+// engine's; the selection builds the top-th largest score bit by bit from register-resident
+// scores (counting with ballots), then compacts in block order with wave ballots.
 #include "common.h"
 
 using namespace aegist;
@@ -150,102 +150,133 @@ __global__ void __launch_bounds__(256) idx_scores_kernel(const float* __restrict
     if (g == 0 && blk < nvis) sc[(size_t)t * nbmax + blk] = tot / sqrtf((float)IHD);
 }
 
-// Inclusive scan of one value per lane across the wave.
-__device__ __forceinline__ unsigned wave_incl_scan(unsigned v, int lane) {
-#pragma unroll
-    for (int off = 1; off < WAVE; off <<= 1) {
-        const unsigned u = __shfl_up(v, off, WAVE);
-        if (lane >= off) v += u;
-    }
-    return v;
-}
+// One workgroup of 16 waves per query; thread tid holds the PER consecutive scores of blocks
+// [tid PER, tid PER + PER) in registers. The top-th largest score bit pattern T is built from
+// the most significant bit down, two bits per step: of the three candidates T | k << b (k = 1..3)
+// the largest with at least `top` scores >= it is kept (scores are non-negative, so bit patterns
+// order like values). A count is a compare-and-add over the thread's registers, wave totals from
+// ballots of the count's bits, and one barrier for the three sums over waves. The listing is an
+// exclusive prefix over threads of (above T, equal to T) counts, so each thread writes its own
+// blocks in order: every block above T and the lowest-numbered blocks equal to T.
+// PER = 0 (more than 32768 blocks): the thread's scores are re-read from global memory
+// (L2-resident), chunk by chunk, instead of registers.
+constexpr int SEL_THREADS = 1024, SEL_WAVES = SEL_THREADS / WAVE;
 
-// One workgroup (4 waves) per query. Finds the top-th largest score bit pattern digit by digit
-// (8 bits per pass, histogram in LDS), then lists, in block order, every block above it and the
-// lowest-numbered blocks equal to it until `top` are listed.
-__global__ void __launch_bounds__(256) idx_select_kernel(const float* __restrict__ sc, int* __restrict__ blist,
-                                                         int* __restrict__ nsel, int top, int R, int pos0, int nbmax) {
-    __shared__ unsigned hist[256];
-    __shared__ unsigned s_prefix, s_need;
-    __shared__ unsigned wcnt[2][4];
+template <int PER>
+__global__ void __launch_bounds__(SEL_THREADS) idx_select_kernel(const float* __restrict__ sc, int* __restrict__ blist,
+                                                                 int* __restrict__ nsel, int top, int R, int pos0,
+                                                                 int nbmax, int vec) {
+    __shared__ unsigned wc[2][4][SEL_WAVES];
     const int t = blockIdx.x, tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
     const int n = (pos0 + t + 1) / R;
-    const unsigned* s = (const unsigned*)(sc + (size_t)t * nbmax);
+    const unsigned* sg = (const unsigned*)(sc + (size_t)t * nbmax);
     int* out = blist + (size_t)t * top;
     if (n <= top) {  // every complete block
-        for (int b = tid; b < n; b += blockDim.x) out[b] = b;
+        for (int b = tid; b < n; b += SEL_THREADS) out[b] = b;
         if (tid == 0) nsel[t] = n;
         return;
     }
-    if (tid == 0) {
-        s_prefix = 0;
-        s_need = (unsigned)top;
-    }
-    unsigned mask = 0;
-    for (int shift = 24; shift >= 0; shift -= 8) {
-        hist[tid] = 0;
-        __syncthreads();
-        const unsigned pf = s_prefix;
-        for (int b = tid; b < n; b += blockDim.x) {
-            const unsigned u = s[b];
-            if ((u & mask) == pf) atomicAdd(&hist[(u >> shift) & 255u], 1u);
-        }
-        __syncthreads();
-        if (wave == 0) {
-            // lane l owns bins 4l .. 4l+3; count of elements in bins above lane l's = suffix sum
-            unsigned c4[4], c = 0;
+    // this thread's blocks: [lo, lo + per), per = PER or ceil(n / 1024)
+    const int per = PER > 0 ? PER : (n + SEL_THREADS - 1) / SEL_THREADS;
+    const int lo = tid * per;
+    constexpr int NREG = PER > 0 ? PER : 1;
+    unsigned u[NREG];
+    if constexpr (PER > 0) {
 #pragma unroll
-            for (int q = 0; q < 4; q++) {
-                c4[q] = hist[4 * lane + q];
-                c += c4[q];
-            }
-            // suffix (from the top lane down): reverse the lane order for an inclusive scan
-            const unsigned rev = wave_incl_scan(__shfl(c, WAVE - 1 - lane, WAVE), lane);
-            const unsigned incl = __shfl(rev, WAVE - 1 - lane, WAVE);  // sum over lanes >= lane
-            const unsigned above = incl - c;
-            const unsigned need = s_need;
-            if (above < need && need <= incl) {
-                unsigned rem = need - above;
-                int bin = 4 * lane;
+        for (int i = 0; i < PER; i += 4) {
+            if (vec && lo + i + 3 < n) {
+                const uint4 v = *(const uint4*)(sg + lo + i);  // 16-byte aligned rows
+                u[i] = v.x;
+                u[i + 1] = v.y;
+                u[i + 2] = v.z;
+                u[i + 3] = v.w;
+            } else {
 #pragma unroll
-                for (int q = 3; q >= 0; q--) {
-                    if (c4[q] >= rem) {
-                        bin = 4 * lane + q;
-                        break;
-                    }
-                    rem -= c4[q];
-                }
-                s_prefix = pf | ((unsigned)bin << shift);
-                s_need = rem;
+                for (int k = 0; k < 4; k++) u[i + k] = lo + i + k < n ? sg[lo + i + k] : 0u;  // 0 never counts
             }
         }
-        mask |= 255u << shift;
-        __syncthreads();
     }
-    const unsigned thr = s_prefix, take_eq = s_need;  // top-th largest value; equal ones to take
-    // order-preserving compaction, 256 blocks per round
-    unsigned eq_before = 0, sel_before = 0;
-    for (int base = 0; base < n; base += blockDim.x) {
-        const int b = base + tid;
-        const unsigned u = b < n ? s[b] : 0u;
-        const bool gt = b < n && u > thr, eq = b < n && u == thr;
-        const unsigned long long beq = __ballot(eq);
-        if (lane == 0) wcnt[0][wave] = __popcll(beq);
-        __syncthreads();
-        unsigned eq_rank = eq_before + __popcll(beq & ((1ull << lane) - 1));
-        for (int w = 0; w < wave; w++) eq_rank += wcnt[0][w];
-        const bool sel = gt || (eq && eq_rank < take_eq);
-        const unsigned long long bsel = __ballot(sel);
-        if (lane == 0) wcnt[1][wave] = __popcll(bsel);
-        __syncthreads();
-        unsigned pos = sel_before + __popcll(bsel & ((1ull << lane) - 1));
-        for (int w = 0; w < wave; w++) pos += wcnt[1][w];
-        if (sel) out[pos] = b;
-        for (int w = 0; w < 4; w++) {
-            eq_before += wcnt[0][w];
-            sel_before += wcnt[1][w];
+    auto val = [&](int i) -> unsigned {
+        if constexpr (PER > 0) return u[i];
+        return lo + i < n ? sg[lo + i] : 0u;
+    };
+    const unsigned long long below = (1ull << lane) - 1;
+    const int cbits = 32 - __builtin_clz((unsigned)per);  // per-thread counts are <= per
+    // wave total (and exclusive prefix below this lane) of a per-thread count, from ballots
+    auto wave_count = [&](unsigned c, unsigned& pre) {
+        unsigned tot = 0;
+        pre = 0;
+        for (int bit = 0; bit < cbits; bit++) {
+            const unsigned long long m = __ballot((c >> bit) & 1u);
+            tot += (unsigned)__popcll(m) << bit;
+            pre += (unsigned)__popcll(m & below) << bit;
         }
-        __syncthreads();  // wcnt is rewritten next round
+        return tot;
+    };
+    int par = 0;
+    unsigned T = 0;
+    for (int bit = 29; bit >= -1; bit -= 2) {  // bits (30, 29), ..., (0, -); the sign bit is 0
+        const int sh = bit < 0 ? 0 : bit;
+        const int nk = bit < 0 ? 1 : 3;  // the last step decides bit 0 alone
+        unsigned c[3] = {0u, 0u, 0u};
+        for (int i = 0; i < per; i++) {
+            const unsigned v = val(i);
+#pragma unroll
+            for (int k = 0; k < 3; k++) c[k] += v >= (T | ((unsigned)(k + 1) << sh));
+        }
+#pragma unroll
+        for (int k = 0; k < 3; k++) {
+            unsigned pre;
+            const unsigned wt = wave_count(c[k], pre);
+            if (lane == 0) wc[par][k][wave] = wt;
+        }
+        __syncthreads();
+        unsigned tot[3] = {0u, 0u, 0u};
+        for (int w = 0; w < SEL_WAVES; w++)
+#pragma unroll
+            for (int k = 0; k < 3; k++) tot[k] += wc[par][k][w];
+        par ^= 1;  // the next step writes the other buffer: no second barrier needed
+        for (int k = nk - 1; k >= 0; k--)
+            if (tot[k] >= (unsigned)top) {
+                T |= (unsigned)(k + 1) << sh;
+                break;
+            }
+    }
+    // listing: per-thread counts above / equal to T, exclusive prefix over threads
+    unsigned gtc = 0, eqc = 0;
+    for (int i = 0; i < per; i++) {
+        const unsigned v = val(i);
+        gtc += lo + i < n && v > T;
+        eqc += lo + i < n && v == T;
+    }
+    unsigned gpre, epre;
+    const unsigned gw = wave_count(gtc, gpre), ew = wave_count(eqc, epre);
+    if (lane == 0) {
+        wc[par][0][wave] = gw;
+        wc[par][1][wave] = ew;
+    }
+    __syncthreads();
+    unsigned gt_before = gpre, eq_before = epre, gt_total = 0;
+    for (int w = 0; w < SEL_WAVES; w++) {
+        const unsigned g = wc[par][0][w], e = wc[par][1][w];
+        gt_total += g;
+        if (w < wave) {
+            gt_before += g;
+            eq_before += e;
+        }
+    }
+    const unsigned take_eq = (unsigned)top - gt_total;  // equal-valued blocks that make the top
+    // this thread's output position: blocks above T before it plus the equal ones taken before it
+    unsigned pos = gt_before + min(eq_before, take_eq), eq_seen = eq_before;
+    for (int i = 0; i < per; i++) {
+        if (lo + i >= n) break;
+        const unsigned v = val(i);
+        if (v > T) {
+            out[pos++] = lo + i;
+        } else if (v == T) {
+            if (eq_seen < take_eq) out[pos++] = lo + i;
+            eq_seen++;
+        }
     }
     if (tid == 0) nsel[t] = top;
 }
@@ -322,7 +353,15 @@ int aegist_idx_select(const float* sc, int* blist, int* nsel, int T, int top, in
     AEG_REQUIRE(T >= 0 && top > 0 && R > 0 && pos0 >= 0, "idx_select: bad shape");
     AEG_REQUIRE((pos0 + T) / R <= nbmax, "idx_select: nbmax smaller than the number of complete blocks");
     if (T == 0) return 0;
-    idx_select_kernel<<<T, 256, 0, AEG_STREAM(stream)>>>(sc, blist, nsel, top, R, pos0, nbmax);
+    const int nmax = (pos0 + T) / R;  // the most complete blocks any of these queries sees
+    const int vec = nbmax % 4 == 0 && (uintptr_t)sc % 16 == 0;
+    hipStream_t st = AEG_STREAM(stream);
+    if (nmax <= 8 * SEL_THREADS)
+        idx_select_kernel<8><<<T, SEL_THREADS, 0, st>>>(sc, blist, nsel, top, R, pos0, nbmax, vec);
+    else if (nmax <= 32 * SEL_THREADS)
+        idx_select_kernel<32><<<T, SEL_THREADS, 0, st>>>(sc, blist, nsel, top, R, pos0, nbmax, vec);
+    else
+        idx_select_kernel<0><<<T, SEL_THREADS, 0, st>>>(sc, blist, nsel, top, R, pos0, nbmax, vec);
     return after_launch("idx_select");
 }
 

@@ -231,6 +231,55 @@ def bench_proj(torch, ops, dev, reps=3):
             "points": out}
 
 
+def bench_qsa(torch, ops, dev, reps=20):
+    """Second core's sparse decode step at long context: one query at position L - 1 with
+    L = 131072, R = 4 (32768 blocks), top = 512 (budget 2048), 16 index heads of 128 (an assumed
+    head count: the released config is not in the reference tree), then attention over the 512
+    listed blocks + tail with 16 / 2 heads of 256. Times each kernel of the decode-time path
+    (block scores, top-k select, listed attention) with HIP events."""
+    from aegist_mixer._lib import call
+    stream = torch.cuda.current_stream().cuda_stream
+    L, RB, top, H, KV, HD, IH = 131072, 4, 512, 16, 2, 256, 16
+    nb = L // RB
+    pos0 = L - 1
+    qi = ops.fill_normal(torch.empty(1, IH, 128, device=dev), 71)
+    bk = ops.fill_normal(torch.empty(nb, 128, device=dev), 72)
+    sc = torch.empty(1, nb, device=dev)
+    blist = torch.empty(1, top, dtype=torch.int32, device=dev)
+    nsel = torch.empty(1, dtype=torch.int32, device=dev)
+    q = ops.fill_normal(torch.empty(1, H, HD, device=dev), 73)
+    kc = ops.fill_normal(torch.empty(KV, L, HD, device=dev, dtype=torch.bfloat16), 74)
+    vc = ops.fill_normal(torch.empty(KV, L, HD, device=dev, dtype=torch.bfloat16), 75)
+    qg = ops.fill_normal(torch.empty(1, H, 2 * HD, device=dev), 76)
+    out = torch.empty(1, H, HD, device=dev)
+    steps = {
+        "scores": lambda: call("aegist_idx_scores", qi.data_ptr(), bk.data_ptr(), sc.data_ptr(), 1, IH, 128, pos0, RB,
+                               nb, stream),
+        "select": lambda: call("aegist_idx_select", sc.data_ptr(), blist.data_ptr(), nsel.data_ptr(), 1, top, RB, pos0,
+                               nb, stream),
+        "attention_list": lambda: call("aegist_attention_gated_list", q.data_ptr(), kc.data_ptr(), vc.data_ptr(),
+                                       qg.data_ptr(), out.data_ptr(), 1, H, KV, pos0, L, HD ** -0.5, blist.data_ptr(),
+                                       nsel.data_ptr(), top, RB, stream),
+    }
+    res = {"workload": f"QSA sparse decode, L={L}, R={RB}, top={top}, 16 index heads x 128, 16/2 heads x 256",
+           "note": "16 index heads is an assumption (the released head count is not in the reference tree)"}
+    for name, fn in steps.items():
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        res[name + "_us"] = round(e0.elapsed_time(e1) * 1e3 / reps, 2)
+    # bytes: block keys for the scores; 2 KV heads x (top R + tail) rows of K and V for the attention
+    res["scores_GB_s"] = round(nb * 128 * 4 / (res["scores_us"] * 1e-6) / 1e9, 1)
+    res["attention_list_GB_s"] = round(KV * (top * RB + RB) * HD * 2 * 2 / (res["attention_list_us"] * 1e-6) / 1e9, 1)
+    return res
+
+
 def bench_stack(torch, ops, dev, B=16, T=2048, steps=256):
     """Config 4: 40-layer hybrid mixer stack (3 DeltaNet + 1 attention, x10; d 2048), bf16
     projection weights ~N(0, 0.02) (random init), MoE FFN as identity, bf16 embedding table
@@ -291,7 +340,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run a 1 GiB device copy (calibrates rocprof FETCH_SIZE / WRITE_SIZE)")
-    ap.add_argument("--legs", type=str, default="prefill,attention_decode,attention_prefill,proj,stack",
+    ap.add_argument("--legs", type=str, default="prefill,attention_decode,attention_prefill,proj,qsa,stack",
                     help="comma list of the extra legs to run after the decode headline (default: all); "
                          "'none' for the headline only")
     ap.add_argument("--traffic", type=str, default=str(ROOT / "profiles" / "delta_decode_traffic.json"),
@@ -373,7 +422,8 @@ def main():
         with open(args.traffic) as f:
             res["roofline"]["traffic"] = json.load(f).get("bytes_per_launch")
     legs = {"prefill": bench_prefill, "attention_decode": bench_attention_decode,
-            "attention_prefill": bench_attention_prefill, "proj": bench_proj, "stack": bench_stack}
+            "attention_prefill": bench_attention_prefill, "proj": bench_proj, "qsa": bench_qsa,
+            "stack": bench_stack}
     want = [] if args.legs.strip() == "none" else [x.strip() for x in args.legs.split(",") if x.strip()]
     unknown = [x for x in want if x not in legs]
     if unknown:

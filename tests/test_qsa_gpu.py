@@ -82,7 +82,7 @@ def test_indexer_pipeline(dev, T, pos0):
     _check_lists(_lists(blist, nsel), lists_ref, sc_ref, top, RB, pos0)
 
 
-@pytest.mark.parametrize("T,pos0,nbits", [(37, 500, 0), (5, 131067, 0), (9, 4000, 3)])
+@pytest.mark.parametrize("T,pos0,nbits", [(37, 500, 0), (5, 131067, 0), (9, 4000, 3), (2, 160000, 0), (2, 160000, 2)])
 def test_select_exact_with_ties(dev, T, pos0, nbits):
     """Scores given directly (no arithmetic differences): lists equal the oracle's exactly,
     including ties (scores rounded to few distinct values) and n = 32768 blocks."""
