@@ -457,34 +457,62 @@ __global__ void __launch_bounds__(256) attn_prefill_simple_kernel(const float* _
 }
 
 // ---------------------------------------------------------------------------------------------
-// Causal flash prefill on v_mfma_f32_16x16x32_f16. One workgroup of 4 waves per (sequence,
-// query head, 64 queries); wave w owns query rows [16w, 16w + 16). Key tiles of 64: K row-major
-// and V transposed are staged in LDS as fp16 (bf16 cache values convert exactly), q * scale and
-// the probabilities enter as fp16 (11-bit mantissa; within 2e-4 of fp64 on N(0,1) inputs where
-// bf16 gives 1.5e-3). Online softmax per row in fp32; output * sigmoid(gate).
-constexpr int PQ = 64, PK = 64;       // queries per workgroup, keys per tile
-constexpr int PLD = HD + 8;           // K tile row stride (halves)
-constexpr int VLD = PK + 8;           // V^T tile row stride (halves)
+// Causal flash prefill on v_mfma_f32_16x16x32_bf16. One workgroup of 8 waves per (sequence,
+// query head, 128 queries); wave w owns query rows [16w, 16w + 16). Key tiles of 64 rows: K and
+// V are staged in LDS as the cache's own bf16 rows (a plain copy, no conversion). The scores
+// q K^T take K rows straight as the B operand; P V takes V through LDS transpose reads
+// (ds_read_b64_tr_b16: each lane of a 16-lane group receives 4 consecutive keys of one dim), so
+// V never needs a transposed copy. q * scale and the probabilities enter as bf16 hi + lo pairs
+// (two MFMAs each): ~16 significant bits against the exact bf16 K and V. Online softmax per row
+// in fp32 (base-2, log2 e folded into the q scale; the accumulators are rescaled only when a
+// row's running maximum moved); output * sigmoid(gate). A wave whose rows cannot see any key of
+// a tile skips it.
+constexpr int PQ = 128, PK = 64;      // queries per workgroup, keys per tile
+constexpr int PW = PQ / 16;           // waves per workgroup
+constexpr int KVLD = HD + 16;         // K / V tile row stride (bf16): 136 words = 8 mod 64 banks
 
-__global__ void __launch_bounds__(256) attn_prefill_mfma_kernel(const float* __restrict__ q, Strides3 qs,
-                                                                const uint16_t* __restrict__ kc,
-                                                                const uint16_t* __restrict__ vc,
-                                                                const float* __restrict__ gate, Strides3 gs,
-                                                                float* __restrict__ out, Strides3 os, int H, int KV,
-                                                                int T, int pos, int cap, float scale) {
-    __shared__ __attribute__((aligned(16))) _Float16 Kt[PK][PLD];
-    __shared__ __attribute__((aligned(16))) _Float16 Vt[HD][VLD];
-    __shared__ __attribute__((aligned(16))) _Float16 Pt[4][16][PK + 8];
+typedef short short4v __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ void split_bf16x8(const float* x, bf16x8& hi, bf16x8& lo) {
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        uint16_t h, l;
+        split_bf16(x[i], h, l);
+        hi[i] = (short)h;
+        lo[i] = (short)l;
+    }
+}
+
+// B operand of P V for keys [row0, row0 + 8) of dim block col0..col0+15 from row-major bf16 V
+// rows in LDS: lane (g, n) gets V[row0 + 8 g + e][col0 + n], e < 8, via two transpose reads.
+__device__ __forceinline__ bf16x8 v_operand(const uint16_t* vt, int row0, int col0, int lane) {
+    const int g = lane / 16, k = lane % 16;
+    const uint16_t* p = vt + (size_t)(row0 + 8 * g + (k >> 2)) * KVLD + col0 + 4 * (k & 3);
+    typedef __attribute__((address_space(3))) short4v lds_short4;
+    const short4v a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4*)(p));
+    const short4v b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4*)(p + 4 * KVLD));
+    return bf16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+}
+
+__global__ void __launch_bounds__(64 * PW) attn_prefill_mfma_kernel(const float* __restrict__ q, Strides3 qs,
+                                                                     const uint16_t* __restrict__ kc,
+                                                                     const uint16_t* __restrict__ vc,
+                                                                     const float* __restrict__ gate, Strides3 gs,
+                                                                     float* __restrict__ out, Strides3 os, int H,
+                                                                     int KV, int T, int pos, int cap, float scale) {
+    __shared__ __attribute__((aligned(16))) uint16_t Kt[PK * KVLD];
+    __shared__ __attribute__((aligned(16))) uint16_t Vt[PK * KVLD];
+    __shared__ __attribute__((aligned(16))) uint16_t Pt[PW][2][16][PK + 8];  // P hi, lo (bf16)
 
     const int qb = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE, n = lane % 16, g = lane / 16;
     const int G = H / KV, kvh = h / G;
-    const int q0 = qb * PQ;                    // first query (sequence-relative)
+    const int q0 = qb * PQ;  // first query (sequence-relative)
     const uint16_t* kbase = kc + ((size_t)b * KV + kvh) * (size_t)cap * HD;
     const uint16_t* vbase = vc + ((size_t)b * KV + kvh) * (size_t)cap * HD;
 
-    // Q operand: row n of this wave's 16 queries, k elements 32 ks + 8 g .. +8
-    half8 qa[8];
+    // Q operand: row n of this wave's 16 queries, k elements 32 ks + 8 g .. +8, as bf16 hi + lo
+    bf16x8 qh[8], ql[8];
     {
         const int t = min(q0 + 16 * wave + n, T - 1);
         const float* qr = q + b * qs.b + (long long)t * qs.t + h * qs.h;
@@ -492,9 +520,10 @@ __global__ void __launch_bounds__(256) attn_prefill_mfma_kernel(const float* __r
         for (int ks = 0; ks < 8; ks++) {
             const float4 a0 = *(const float4*)(qr + 32 * ks + 8 * g);
             const float4 a1 = *(const float4*)(qr + 32 * ks + 8 * g + 4);
-            qa[ks] = half8{(_Float16)(a0.x * scale), (_Float16)(a0.y * scale), (_Float16)(a0.z * scale),
-                           (_Float16)(a0.w * scale), (_Float16)(a1.x * scale), (_Float16)(a1.y * scale),
-                           (_Float16)(a1.z * scale), (_Float16)(a1.w * scale)};
+            // scores in the log2 domain: exp(s) = exp2(s log2 e)
+            const float sl = scale * 1.4426950408889634f;
+            const float x[8] = {a0.x * sl, a0.y * sl, a0.z * sl, a0.w * sl, a1.x * sl, a1.y * sl, a1.z * sl, a1.w * sl};
+            split_bf16x8(x, qh[ks], ql[ks]);
         }
     }
     float m_run[4], l_run[4];
@@ -507,19 +536,18 @@ __global__ void __launch_bounds__(256) attn_prefill_mfma_kernel(const float* __r
 #pragma unroll
     for (int i = 0; i < 16; i++) oacc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    const int last_key = pos + min(q0 + PQ, T) - 1;   // keys [0, last_key] are visible to this block
+    const int last_key = pos + min(q0 + PQ, T) - 1;  // keys [0, last_key] are visible to this block
     const int ntiles = last_key / PK + 1;
-    // Tile staging: step `it` moves the 16-byte chunk c8 = 8 it .. of key (row) tid % 64 for
-    // tid / 64 = it % 4 ... lanes run over consecutive keys, so the V^T writes are contiguous
-    // 2-byte runs (conflict-free) and the K writes land in distinct rows. The next tile is held
-    // in registers (requested a full tile ahead).
-    constexpr int NSTEP = (PK * HD) / (8 * 256);  // 8
+    const int wave_last = pos + min(q0 + 16 * wave + 15, T - 1);  // the last key this wave's rows see
+    // Tile staging: 16-byte chunk c8 of key row r; the next tile is held in registers, requested
+    // a full tile ahead.
+    constexpr int NSTEP = (PK * HD) / (8 * 64 * PW);  // 4
     uint4 kreg[NSTEP], vreg[NSTEP];
     auto fetch = [&](int kt) {
-        const int row = tid % PK, key = min(kt * PK + row, last_key);
 #pragma unroll
         for (int it = 0; it < NSTEP; it++) {
-            const int c8 = ((tid / PK) + 4 * it) * 8;
+            const int idx = it * 64 * PW + tid, r = idx / (HD / 8), c8 = (idx % (HD / 8)) * 8;
+            const int key = min(kt * PK + r, last_key);
             kreg[it] = *(const uint4*)(kbase + (size_t)key * HD + c8);
             vreg[it] = *(const uint4*)(vbase + (size_t)key * HD + c8);
         }
@@ -528,34 +556,26 @@ __global__ void __launch_bounds__(256) attn_prefill_mfma_kernel(const float* __r
     for (int kt = 0; kt < ntiles; kt++) {
         const int key0 = kt * PK;
         __syncthreads();  // previous tile's LDS reads done
-        {
-            const int row = tid % PK;
 #pragma unroll
-            for (int it = 0; it < NSTEP; it++) {
-                const int c8 = ((tid / PK) + 4 * it) * 8;
-                const uint32_t kw[4] = {kreg[it].x, kreg[it].y, kreg[it].z, kreg[it].w};
-                const uint32_t vw[4] = {vreg[it].x, vreg[it].y, vreg[it].z, vreg[it].w};
-                half8 kh;
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    kh[2 * e] = (_Float16)bf_lo(kw[e]);
-                    kh[2 * e + 1] = (_Float16)bf_hi(kw[e]);
-                    Vt[c8 + 2 * e][row] = (_Float16)bf_lo(vw[e]);
-                    Vt[c8 + 2 * e + 1][row] = (_Float16)bf_hi(vw[e]);
-                }
-                *(half8*)&Kt[row][c8] = kh;
-            }
+        for (int it = 0; it < NSTEP; it++) {
+            const int idx = it * 64 * PW + tid, r = idx / (HD / 8), c8 = (idx % (HD / 8)) * 8;
+            *(uint4*)&Kt[r * KVLD + c8] = kreg[it];
+            *(uint4*)&Vt[r * KVLD + c8] = vreg[it];
         }
         __syncthreads();
         fetch(min(kt + 1, ntiles - 1));  // unconditional: static wait counts
+        if (key0 > wave_last) continue;  // no row of this wave sees any key of this tile
         // ---- scores for 4 blocks of 16 keys
         f32x4 sc[4];
 #pragma unroll
         for (int nb = 0; nb < 4; nb++) {
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int ks = 0; ks < 8; ks++) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                                                qa[ks], *(const half8*)&Kt[16 * nb + n][32 * ks + 8 * g], acc, 0, 0, 0);
+            for (int ks = 0; ks < 8; ks++) {
+                const bf16x8 kb = *(const bf16x8*)&Kt[(16 * nb + n) * KVLD + 32 * ks + 8 * g];
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qh[ks], kb, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ql[ks], kb, acc, 0, 0, 0);
+            }
             // lane: key 16 nb + n, query rows 4 g + j of the wave; causal mask
 #pragma unroll
             for (int j = 0; j < 4; j++) {
@@ -563,7 +583,10 @@ __global__ void __launch_bounds__(256) attn_prefill_mfma_kernel(const float* __r
                 sc[nb][j] = key <= qpos ? acc[j] : -INFINITY;
             }
         }
-        // ---- online softmax per query row (row = 4 g + j; keys over the 16 lanes n and 4 blocks)
+        // ---- online softmax per query row (row = 4 g + j; keys over the 16 lanes n and 4 blocks),
+        // base-2 exponentials; the accumulators are rescaled only when some row's maximum moved
+        bool moved = false;
+        float corr[4];
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             float mt = fmaxf(fmaxf(sc[0][j], sc[1][j]), fmaxf(sc[2][j], sc[3][j]));
@@ -572,32 +595,51 @@ __global__ void __launch_bounds__(256) attn_prefill_mfma_kernel(const float* __r
             mt = fmaxf(mt, __shfl_xor(mt, 4, WAVE));
             mt = fmaxf(mt, __shfl_xor(mt, 8, WAVE));
             const float mn = fmaxf(m_run[j], mt);
-            // a row with no visible key yet keeps m = -inf: use 0 as the reference so exp() is 0
+            // a row with no visible key yet keeps m = -inf: use 0 as the reference so exp2() is 0
             const float ref = mn == -INFINITY ? 0.f : mn;
-            const float corr = __expf(m_run[j] - ref);
+            corr[j] = exp2f(m_run[j] - ref);
+            moved |= mn != m_run[j];
             float ps = 0.f;
 #pragma unroll
-            for (int nb = 0; nb < 4; nb++) {
-                const float p = __expf(sc[nb][j] - ref);
-                ps += p;
-                Pt[wave][4 * g + j][16 * nb + n] = (_Float16)p;
+            for (int nb = 0; nb < 4; nb += 2) {
+                const float p0 = exp2f(sc[nb][j] - ref), p1 = exp2f(sc[nb + 1][j] - ref);
+                ps += p0 + p1;
+                // hi = p truncated to bf16 (exact remainder), lo = the remainder rounded to bf16
+                typedef float f2 __attribute__((ext_vector_type(2)));
+                typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+                const uint32_t h0 = __float_as_uint(p0) & 0xffff0000u, h1 = __float_as_uint(p1) & 0xffff0000u;
+                const f2 lo = {p0 - __uint_as_float(h0), p1 - __uint_as_float(h1)};
+                const uint32_t lp = __builtin_bit_cast(uint32_t, __builtin_convertvector(lo, b2));
+                Pt[wave][0][4 * g + j][16 * nb + n] = (uint16_t)(h0 >> 16);
+                Pt[wave][0][4 * g + j][16 * (nb + 1) + n] = (uint16_t)(h1 >> 16);
+                Pt[wave][1][4 * g + j][16 * nb + n] = (uint16_t)(lp & 0xffffu);
+                Pt[wave][1][4 * g + j][16 * (nb + 1) + n] = (uint16_t)(lp >> 16);
             }
-            l_run[j] = l_run[j] * corr + ps;
+            l_run[j] = l_run[j] * corr[j] + ps;
             m_run[j] = mn;
+        }
+        if (__ballot(moved)) {
 #pragma unroll
-            for (int i = 0; i < 16; i++) oacc[i][j] *= corr;
+            for (int i = 0; i < 16; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) oacc[i][j] *= corr[j];
         }
         wave_sync();
         // ---- O += P V (k = 64 keys in 2 steps; 16 output blocks of 16 dims)
-        half8 pa[2];
+        bf16x8 ph[2], pl[2];
 #pragma unroll
-        for (int ks = 0; ks < 2; ks++) pa[ks] = *(const half8*)&Pt[wave][n][32 * ks + 8 * g];
+        for (int ks = 0; ks < 2; ks++) {
+            ph[ks] = *(const bf16x8*)&Pt[wave][0][n][32 * ks + 8 * g];
+            pl[ks] = *(const bf16x8*)&Pt[wave][1][n][32 * ks + 8 * g];
+        }
 #pragma unroll
         for (int db = 0; db < 16; db++)
 #pragma unroll
-            for (int ks = 0; ks < 2; ks++)
-                oacc[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[ks], *(const half8*)&Vt[16 * db + n][32 * ks + 8 * g],
-                                                                 oacc[db], 0, 0, 0);
+            for (int ks = 0; ks < 2; ks++) {
+                const bf16x8 vb = v_operand(Vt, 32 * ks, 16 * db, lane);
+                oacc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ph[ks], vb, oacc[db], 0, 0, 0);
+                oacc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pl[ks], vb, oacc[db], 0, 0, 0);
+            }
     }
     // ---- normalise, gate, store: lane holds rows 4 g + j, dims 16 db + n
 #pragma unroll
@@ -667,8 +709,8 @@ int launch_prefill_core(const float* q, Strides3 qs, const uint16_t* kc, const u
     if (pos < 0 || pos + T > cap) return fail(AEGIST_ERR_SHAPE, "attention prefill: rows exceed the cache capacity");
     const bool vec_q = ((uintptr_t)q % 16 == 0) && qs.b % 4 == 0 && qs.t % 4 == 0 && qs.h % 4 == 0;
     if (T >= 16 && vec_q) {
-        attn_prefill_mfma_kernel<<<dim3((T + PQ - 1) / PQ, H, B), 256, 0, st>>>(q, qs, kc, vc, gate, gs, out, os, H, KV,
-                                                                              T, pos, cap, scale);
+        attn_prefill_mfma_kernel<<<dim3((T + PQ - 1) / PQ, H, B), 64 * PW, 0, st>>>(q, qs, kc, vc, gate, gs, out, os, H,
+                                                                                  KV, T, pos, cap, scale);
     } else {
         attn_prefill_simple_kernel<<<dim3((T + 3) / 4, H, B), 256, 0, st>>>(q, qs, kc, vc, gate, gs, out, os, H, KV, T,
                                                                             pos, cap, scale);
