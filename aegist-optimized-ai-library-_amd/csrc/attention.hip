@@ -467,7 +467,14 @@ __global__ void __launch_bounds__(256) attn_prefill_simple_kernel(const float* _
 // in fp32 (base-2, log2 e folded into the q scale; the accumulators are rescaled only when a
 // row's running maximum moved); output * sigmoid(gate). A wave whose rows cannot see any key of
 // a tile skips it.
-constexpr int PQ = 128, PK = 64;      // queries per workgroup, keys per tile
+#ifndef PREFILL_PQ
+#define PREFILL_PQ 128
+#endif
+#ifndef PREFILL_PK
+#define PREFILL_PK 64
+#endif
+constexpr int PQ = PREFILL_PQ, PK = PREFILL_PK;  // queries per workgroup, keys per tile
+constexpr int PNB = PK / 16, PKS = PK / 32;      // 16-key score blocks, 32-key P V steps
 constexpr int PW = PQ / 16;           // waves per workgroup
 constexpr int KVLD = HD + 16;         // K / V tile row stride (bf16): 136 words = 8 mod 64 banks
 
@@ -566,9 +573,9 @@ __global__ void __launch_bounds__(64 * PW) attn_prefill_mfma_kernel(const float*
         fetch(min(kt + 1, ntiles - 1));  // unconditional: static wait counts
         if (key0 > wave_last) continue;  // no row of this wave sees any key of this tile
         // ---- scores for 4 blocks of 16 keys
-        f32x4 sc[4];
+        f32x4 sc[PNB];
 #pragma unroll
-        for (int nb = 0; nb < 4; nb++) {
+        for (int nb = 0; nb < PNB; nb++) {
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int ks = 0; ks < 8; ks++) {
@@ -589,7 +596,9 @@ __global__ void __launch_bounds__(64 * PW) attn_prefill_mfma_kernel(const float*
         float corr[4];
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            float mt = fmaxf(fmaxf(sc[0][j], sc[1][j]), fmaxf(sc[2][j], sc[3][j]));
+            float mt = sc[0][j];
+#pragma unroll
+            for (int nb = 1; nb < PNB; nb++) mt = fmaxf(mt, sc[nb][j]);
             mt = fmaxf(mt, __shfl_xor(mt, 1, WAVE));
             mt = fmaxf(mt, __shfl_xor(mt, 2, WAVE));
             mt = fmaxf(mt, __shfl_xor(mt, 4, WAVE));
@@ -601,7 +610,7 @@ __global__ void __launch_bounds__(64 * PW) attn_prefill_mfma_kernel(const float*
             moved |= mn != m_run[j];
             float ps = 0.f;
 #pragma unroll
-            for (int nb = 0; nb < 4; nb += 2) {
+            for (int nb = 0; nb < PNB; nb += 2) {
                 const float p0 = exp2f(sc[nb][j] - ref), p1 = exp2f(sc[nb + 1][j] - ref);
                 ps += p0 + p1;
                 // hi = p truncated to bf16 (exact remainder), lo = the remainder rounded to bf16
@@ -626,16 +635,16 @@ __global__ void __launch_bounds__(64 * PW) attn_prefill_mfma_kernel(const float*
         }
         wave_sync();
         // ---- O += P V (k = 64 keys in 2 steps; 16 output blocks of 16 dims)
-        bf16x8 ph[2], pl[2];
+        bf16x8 ph[PKS], pl[PKS];
 #pragma unroll
-        for (int ks = 0; ks < 2; ks++) {
+        for (int ks = 0; ks < PKS; ks++) {
             ph[ks] = *(const bf16x8*)&Pt[wave][0][n][32 * ks + 8 * g];
             pl[ks] = *(const bf16x8*)&Pt[wave][1][n][32 * ks + 8 * g];
         }
 #pragma unroll
         for (int db = 0; db < 16; db++)
 #pragma unroll
-            for (int ks = 0; ks < 2; ks++) {
+            for (int ks = 0; ks < PKS; ks++) {
                 const bf16x8 vb = v_operand(Vt, 32 * ks, 16 * db, lane);
                 oacc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ph[ks], vb, oacc[db], 0, 0, 0);
                 oacc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pl[ks], vb, oacc[db], 0, 0, 0);

@@ -28,7 +28,6 @@
 // result within 5e-4 of fp64 at T = 8192, where bf16 operands give 4e-3 (over the 1e-3 bar).
 #include "common.h"
 
-#include <mutex>
 
 #include <algorithm>
 
@@ -118,26 +117,40 @@ __device__ __forceinline__ f32x4 mfma16(half8 a, half8 b, f32x4 c) {
 }
 
 // ---------------------------------------------------------------------------------------------
-// K1: intra-chunk work. grid (nch, HV, B), 256 threads (4 waves).
-template <typename Tin>
-__global__ void __launch_bounds__(256) delta_chunk_intra(const Tin* __restrict__ q, const Tin* __restrict__ k,
-                                                         const Tin* __restrict__ v, const float* __restrict__ g,
-                                                         const float* __restrict__ beta, SeqLayout a, int t0, int T,
-                                                         int HK, int HV, int normalize, float qscale, float eps,
-                                                         unsigned char* __restrict__ ws, WsLayout L, int vec_in) {
-    constexpr bool kSplitV = sizeof(Tin) == 4;  // fp32 v needs a low fp16 part; bf16 v is exact in fp16
-    __shared__ __attribute__((aligned(16))) half_t QV[CH][QK_LD];  // q_n tile, then v (fp16 hi)
-    __shared__ __attribute__((aligned(16))) half_t Vl[kSplitV ? CH : 1][QK_LD];
-    __shared__ __attribute__((aligned(16))) half_t Ks[CH][QK_LD];
-    __shared__ __attribute__((aligned(16))) float As[CH][A_LD];    // A, then X = (I + A)^-1 in place
-    __shared__ float Pt[3][16][17];
-    __shared__ float cum_s[CH], beta_s[CH], g_s[CH];
+// K1: intra-chunk work, one workgroup of 256 threads (4 waves) per (chunk c, value head hv,
+// sequence b). The body is shared by the standalone kernel (grid (nch, HV, B)) and the fused
+// launch below; its LDS is one struct so the fused kernel can overlay it with K2's.
+template <bool kSplitV>
+struct K1Smem {
+    __attribute__((aligned(16))) half_t QV[CH][QK_LD];  // q_n tile, then v (fp16 hi)
+    __attribute__((aligned(16))) half_t Vl[kSplitV ? CH : 1][QK_LD];
+    __attribute__((aligned(16))) half_t Ks[CH][QK_LD];
+    __attribute__((aligned(16))) float As[CH][A_LD];    // A, then X = (I + A)^-1 in place
+    float Pt[3][16][17];
+    float cum_s[CH], beta_s[CH], g_s[CH];
     // intra, staged for fragment order; with fp32 inputs it borrows Vl, which is first written
     // after the intra fragments have gone out (keeps the fp32 variant at two workgroups per CU)
-    __shared__ __attribute__((aligned(16))) half_t ItBuf[kSplitV ? 1 : CH][CH + 8];
-    half_t (*It)[CH + 8] = kSplitV ? (half_t (*)[CH + 8])&Vl[0][0] : ItBuf;
+    __attribute__((aligned(16))) half_t ItBuf[kSplitV ? 1 : CH][CH + 8];
+};
 
-    const int c = blockIdx.x, hv = blockIdx.y, b = blockIdx.z, nch = gridDim.x;
+template <typename Tin>
+__device__ __forceinline__ void chunk_intra_body(const Tin* __restrict__ q, const Tin* __restrict__ k,
+                                                 const Tin* __restrict__ v, const float* __restrict__ g,
+                                                 const float* __restrict__ beta, const SeqLayout& a, int t0, int T,
+                                                 int HK, int HV, int normalize, float qscale, float eps,
+                                                 unsigned char* __restrict__ ws, const WsLayout& L, int vec_in,
+                                                 K1Smem<sizeof(Tin) == 4>& sm, int c, int hv, int b, int nch) {
+    constexpr bool kSplitV = sizeof(Tin) == 4;  // fp32 v needs a low fp16 part; bf16 v is exact in fp16
+    auto& QV = sm.QV;
+    auto& Vl = sm.Vl;
+    auto& Ks = sm.Ks;
+    auto& As = sm.As;
+    auto& Pt = sm.Pt;
+    auto& cum_s = sm.cum_s;
+    auto& beta_s = sm.beta_s;
+    auto& g_s = sm.g_s;
+    half_t (*It)[CH + 8] = kSplitV ? (half_t (*)[CH + 8])&Vl[0][0] : sm.ItBuf;
+
     const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE, n = lane % 16, gq = lane / 16;
     const int R = HV / HK, kh = hv / R;
     const bool writes_qk = (hv % R) == 0;
@@ -424,27 +437,46 @@ __global__ void __launch_bounds__(256) delta_chunk_intra(const Tin* __restrict__
     }
 }
 
+template <typename Tin>
+__global__ void __launch_bounds__(256) delta_chunk_intra(const Tin* __restrict__ q, const Tin* __restrict__ k,
+                                                         const Tin* __restrict__ v, const float* __restrict__ g,
+                                                         const float* __restrict__ beta, SeqLayout a, int t0, int T,
+                                                         int HK, int HV, int normalize, float qscale, float eps,
+                                                         unsigned char* __restrict__ ws, WsLayout L, int vec_in) {
+    __shared__ K1Smem<sizeof(Tin) == 4> sm;
+    chunk_intra_body<Tin>(q, k, v, g, beta, a, t0, T, HK, HV, normalize, qscale, eps, ws, L, vec_in, sm, blockIdx.x,
+                          blockIdx.y, blockIdx.z, gridDim.x);
+}
+
 // ---------------------------------------------------------------------------------------------
 // K2: sequential recurrence over the chunks of a segment. 1-D grid of (B HV rounded up to 8) x
-// 128 / (16 NCT) blocks, 256 threads.
+// 128 / (16 NCT) blocks, 256 threads; Lb is the block's index in that grid.
 // Wave w holds S rows [32w, 32w+32) x the slice's 16 NCT columns as 2 x NCT MFMA tiles.
-template <typename Tout, int NCT>
-__global__ void __launch_bounds__(256) delta_chunk_state(const unsigned char* __restrict__ ws, WsLayout L,
-                                                         float* __restrict__ state, int load_state, Tout* __restrict__ out,
-                                                         SeqLayout a, int t0, int T, int nch, int B, int HK,
-                                                         int HV, int vec_out) {
+template <int NCT>
+struct K2Smem {
     // double-buffered by chunk parity: a wave cannot pass the next chunk's first barrier before
     // every wave has finished reading this chunk's tiles, so no end-of-chunk barrier is needed
-    __shared__ __attribute__((aligned(16))) half_t SsT[2][16 * NCT][D + 8];   // S^T (fp16): [column][dk]
-    __shared__ __attribute__((aligned(16))) half_t VnT[2][16 * NCT][CH + 8];  // v_new^T (fp16)
-    __shared__ __attribute__((aligned(16))) half_t VdT[2][16 * NCT][CH + 8];  // (e^{cum_last-cum} v_new)^T
-    __shared__ float Ot[4][16][16 * NCT + 4];                                     // output staging per wave
+    __attribute__((aligned(16))) half_t SsT[2][16 * NCT][D + 8];   // S^T (fp16): [column][dk]
+    __attribute__((aligned(16))) half_t VnT[2][16 * NCT][CH + 8];  // v_new^T (fp16)
+    __attribute__((aligned(16))) half_t VdT[2][16 * NCT][CH + 8];  // (e^{cum_last-cum} v_new)^T
+    float Ot[4][16][16 * NCT + 4];                                 // output staging per wave
+};
+
+template <typename Tout, int NCT>
+__device__ __forceinline__ void chunk_state_body(const unsigned char* __restrict__ ws, const WsLayout& L,
+                                                 float* __restrict__ state, int load_state, Tout* __restrict__ out,
+                                                 const SeqLayout& a, int t0, int T, int nch, int B, int HK, int HV,
+                                                 int vec_out, K2Smem<NCT>& sm, int Lb) {
+    auto& SsT = sm.SsT;
+    auto& VnT = sm.VnT;
+    auto& VdT = sm.VdT;
+    auto& Ot = sm.Ot;
 
     // XCD-aware block mapping (1-D grid): blocks are dealt to the 8 XCDs round-robin, so unit
     // u = (m / NS) * 8 + xcd keeps all NS column slices of one (sequence, head) on one XCD,
     // where they share the chunk operands in that XCD's L2.
     constexpr int NS = D / (16 * NCT);
-    const int Lb = blockIdx.x, xcd = Lb % 8, m = Lb / 8;
+    const int xcd = Lb % 8, m = Lb / 8;
     const int unit = (m / NS) * 8 + xcd, sl = m % NS;
     if (unit >= B * HV) return;  // grid padded to a multiple of 8 units
     const int hv = unit % HV, b = unit / HV;
@@ -613,6 +645,44 @@ __global__ void __launch_bounds__(256) delta_chunk_state(const unsigned char* __
             for (int j = 0; j < 4; j++) Sg[(size_t)(32 * wave + 16 * rt + 4 * gq + j) * D + col0 + 16 * ct + n] = S[rt][ct][j];
 }
 
+template <typename Tout, int NCT>
+__global__ void __launch_bounds__(256) delta_chunk_state(const unsigned char* __restrict__ ws, WsLayout L,
+                                                         float* __restrict__ state, int load_state, Tout* __restrict__ out,
+                                                         SeqLayout a, int t0, int T, int nch, int B, int HK,
+                                                         int HV, int vec_out) {
+    __shared__ K2Smem<NCT> sm;
+    chunk_state_body<Tout, NCT>(ws, L, state, load_state, out, a, t0, T, nch, B, HK, HV, vec_out, sm, blockIdx.x);
+}
+
+// One launch holding K2 of one segment (blocks [0, nk2)) and K1 of the next segment (the
+// remaining blocks, chunk fastest): the two are independent (different workspace buffers), so
+// the K1 workgroups fill the CUs around K2's without a second stream or events. LDS is the
+// union of the two bodies' needs.
+template <typename Tin, typename Tout, int NCT>
+__global__ void __launch_bounds__(256, 2) delta_chunk_fused(
+    // K2 of segment s
+    const unsigned char* __restrict__ ws2, WsLayout L2, float* __restrict__ state, int load_state,
+    Tout* __restrict__ out, int t0s, int nch2, int nk2,
+    // K1 of segment s + 1
+    const Tin* __restrict__ q, const Tin* __restrict__ k, const Tin* __restrict__ v, const float* __restrict__ g,
+    const float* __restrict__ beta, int t0i, int nch1, unsigned char* __restrict__ ws1, WsLayout L1, int vec_in,
+    int normalize, float qscale, float eps,
+    // shared
+    SeqLayout a, int T, int B, int HK, int HV, int vec_out) {
+    __shared__ union {
+        K1Smem<sizeof(Tin) == 4> k1;
+        K2Smem<NCT> k2;
+    } sm;
+    if ((int)blockIdx.x < nk2) {
+        chunk_state_body<Tout, NCT>(ws2, L2, state, load_state, out, a, t0s, T, nch2, B, HK, HV, vec_out, sm.k2,
+                                    blockIdx.x);
+    } else {
+        const int r = blockIdx.x - nk2, c = r % nch1, hv = (r / nch1) % HV, b = r / (nch1 * HV);
+        chunk_intra_body<Tin>(q, k, v, g, beta, a, t0i, T, HK, HV, normalize, qscale, eps, ws1, L1, vec_in, sm.k1, c,
+                              hv, b, nch1);
+    }
+}
+
 // Chunks per segment: SEG tokens (the workspace of one segment, ~72 MB at B = 1 with 32 value
 // heads, stays resident in the MALL between the two kernels that touch it).
 int seg_chunks(int B, int T, int HV) {
@@ -647,30 +717,6 @@ size_t delta_chunked_ws_bytes(int B, int T, int HK, int HV) {
     return ws_plan(B, T, HK, HV).total;
 }
 
-// Second stream and events per device for the overlapped schedule; created on first use (default
-// priority, non-blocking) and kept for the life of the process. The enqueue of one chunked call
-// holds the device's lock, so calls from several host threads do not interleave their events.
-struct AuxStream {
-    std::mutex mu;
-    hipStream_t stream = nullptr;
-    hipEvent_t ev_main = nullptr, ev_aux = nullptr;
-};
-static AuxStream g_aux[64];
-
-static int aux_for_device(AuxStream** out) {
-    int dev = 0;
-    AEG_HIP(hipGetDevice(&dev));
-    if (dev < 0 || dev >= 64) return fail(AEGIST_ERR_SHAPE, "delta_chunked: device index out of range");
-    AuxStream& a = g_aux[dev];
-    if (!a.stream) {
-        AEG_HIP(hipStreamCreateWithFlags(&a.stream, hipStreamNonBlocking));
-        AEG_HIP(hipEventCreateWithFlags(&a.ev_main, hipEventDisableTiming));
-        AEG_HIP(hipEventCreateWithFlags(&a.ev_aux, hipEventDisableTiming));
-    }
-    *out = &a;
-    return 0;
-}
-
 template <typename Tin, typename Tout>
 int run_chunked(const Tin* q, const Tin* k, const Tin* v, const float* g, const float* beta, float* state, Tout* out,
                 const SeqLayout& a, int B, int T, int HK, int HV, int normalize, float qscale, float eps, void* ws,
@@ -694,39 +740,37 @@ int run_chunked(const Tin* q, const Tin* k, const Tin* v, const float* g, const 
     const int nseg = (T + seg - 1) / seg;
     const int units8 = (B * HV + 7) / 8 * 8;
 
-    auto intra = [&](int s, hipStream_t on) {
+    auto seg_layout = [&](int s) {
         const int t0 = s * seg, nch = (std::min(seg, T - t0) + CH - 1) / CH;
-        const WsLayout Ls = ws_layout(B, HK, HV, nch);
-        delta_chunk_intra<Tin><<<dim3(nch, HV, B), 256, 0, on>>>(q, k, v, g, beta, a, t0, T, HK, HV, normalize, qscale,
-                                                                eps, segbuf[s & 1], Ls, vec_in);
-        return after_launch("delta_chunk_intra");
+        return std::make_pair(nch, ws_layout(B, HK, HV, nch));
     };
-    auto state_pass = [&](int s) {
-        const int t0 = s * seg, nch = (std::min(seg, T - t0) + CH - 1) / CH;
-        const WsLayout Ls = ws_layout(B, HK, HV, nch);
-        delta_chunk_state<Tout, K2_NCT><<<units8 * (D / (16 * K2_NCT)), 256, 0, st>>>(
-            segbuf[s & 1], Ls, S, (state || s > 0) ? 1 : 0, out, a, t0, T, nch, B, HK, HV, vec_out);
-        return after_launch("delta_chunk_state");
-    };
-
-    int rc = intra(0, st);
-    if (rc) return rc;
-    if (nseg == 1) return state_pass(0);
-    // K1 of segment s+1 (second stream) overlaps K2 of segment s (caller's stream). K1(s+1)
-    // overwrites the buffer K2(s-1) read, so it waits for the caller's stream up to K2(s-1);
-    // K2(s) waits for K1(s). Every second-stream launch is joined back before the call returns.
-    AuxStream* ax = nullptr;
-    if ((rc = aux_for_device(&ax))) return rc;
-    std::lock_guard<std::mutex> lock(ax->mu);
+    const int nk2 = units8 * (D / (16 * K2_NCT));
+    // segment 0's K1 alone; then K2 of segment s with K1 of segment s + 1 in one launch; the last
+    // K2 alone. Stream order carries every dependency: K1(s + 1) rewrites the buffer K2(s - 1)
+    // read one launch earlier.
+    {
+        const auto [nch, Ls] = seg_layout(0);
+        delta_chunk_intra<Tin><<<dim3(nch, HV, B), 256, 0, st>>>(q, k, v, g, beta, a, 0, T, HK, HV, normalize, qscale,
+                                                                eps, segbuf[0], Ls, vec_in);
+        int rc = after_launch("delta_chunk_intra");
+        if (rc) return rc;
+    }
     for (int s = 0; s < nseg; s++) {
-        if (s > 0) AEG_HIP(hipStreamWaitEvent(st, ax->ev_aux, 0));
+        const auto [nch2, L2] = seg_layout(s);
+        const int load = (state || s > 0) ? 1 : 0;
         if (s + 1 < nseg) {
-            AEG_HIP(hipEventRecord(ax->ev_main, st));
-            AEG_HIP(hipStreamWaitEvent(ax->stream, ax->ev_main, 0));
-            if ((rc = intra(s + 1, ax->stream))) return rc;
-            AEG_HIP(hipEventRecord(ax->ev_aux, ax->stream));
+            const auto [nch1, L1] = seg_layout(s + 1);
+            delta_chunk_fused<Tin, Tout, K2_NCT><<<nk2 + nch1 * HV * B, 256, 0, st>>>(
+                segbuf[s & 1], L2, S, load, out, s * seg, nch2, nk2, q, k, v, g, beta, (s + 1) * seg, nch1,
+                segbuf[(s + 1) & 1], L1, vec_in, normalize, qscale, eps, a, T, B, HK, HV, vec_out);
+            int rc = after_launch("delta_chunk_fused");
+            if (rc) return rc;
+        } else {
+            delta_chunk_state<Tout, K2_NCT><<<nk2, 256, 0, st>>>(segbuf[s & 1], L2, S, load, out, a, s * seg, T, nch2,
+                                                                  B, HK, HV, vec_out);
+            int rc = after_launch("delta_chunk_state");
+            if (rc) return rc;
         }
-        if ((rc = state_pass(s))) return rc;
     }
     return 0;
 }
