@@ -45,6 +45,12 @@ constexpr int QK_LD = D + 8; // fp16 row stride (elements) of the q/k tiles in L
 constexpr int A_LD = 68;     // fp32 row stride of the A matrix in LDS (16-byte aligned rows)
 
 typedef _Float16 half_t;
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+// raw buffer resource for the output stores: range (bytes) and the gfx9 word 3 (32-bit data,
+// no swizzle); kOutDrop lies past the range, so a store at that offset is discarded
+constexpr int kOutRange = 0x40000000;
+constexpr int kOutDrop = 0x7ffffff0;
+constexpr int kBufWord3 = 0x00020000;
 
 struct SeqLayout {
     long long sb_qk, st_qk, sh_qk, sb_v, st_v, sh_v, sb_o, st_o, sh_o;
@@ -462,11 +468,11 @@ struct K2Smem {
     float Ot[4][16][16 * NCT + 4];                                 // output staging per wave
 };
 
-template <typename Tout, int NCT>
+template <typename Tout, int NCT, bool VEC>
 __device__ __forceinline__ void chunk_state_body(const unsigned char* __restrict__ ws, const WsLayout& L,
                                                  float* __restrict__ state, int load_state, Tout* __restrict__ out,
                                                  const SeqLayout& a, int t0, int T, int nch, int B, int HK, int HV,
-                                                 int vec_out, K2Smem<NCT>& sm, int Lb) {
+                                                 K2Smem<NCT>& sm, int Lb) {
     auto& SsT = sm.SsT;
     auto& VnT = sm.VnT;
     auto& VdT = sm.VdT;
@@ -588,25 +594,43 @@ __device__ __forceinline__ void chunk_state_body(const unsigned char* __restrict
             // per pass
             constexpr int LPR = 2 * NCT;  // lanes per row
             constexpr int RPP = WAVE / LPR;
+            const int tc = t0 + c * CH;  // first token of the chunk
+            if constexpr (VEC) {
+                // Raw buffer stores, issued on every lane: rows past T (or past the wave's 16)
+                // get an offset beyond num_records and the hardware drops them. A store count
+                // that does not depend on a branch lets the compiler's wait for the next chunk's
+                // operands (issued before these stores) leave the stores in flight.
+                const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+                    out + b * a.sb_o + (long long)tc * a.st_o + hv * a.sh_o + col0, (short)0, kOutRange, kBufWord3);
 #pragma unroll
-            for (int r0 = 0; r0 < 16; r0 += RPP) {
-                const int r = r0 + lane / LPR, p8 = (lane % LPR) * 8, tok = t0 + c * CH + 16 * wave + r;
-                if (r < 16 && tok < T) {
-                    Tout* dst = out + b * a.sb_o + (long long)tok * a.st_o + hv * a.sh_o + col0 + p8;
-                    const float* src = &Ot[wave][r][p8];
-                    if (vec_out) {
-                        if constexpr (sizeof(Tout) == 2) {
-                            uint4 pk;
-                            pk.x = (uint32_t)f2bf(src[0]) | ((uint32_t)f2bf(src[1]) << 16);
-                            pk.y = (uint32_t)f2bf(src[2]) | ((uint32_t)f2bf(src[3]) << 16);
-                            pk.z = (uint32_t)f2bf(src[4]) | ((uint32_t)f2bf(src[5]) << 16);
-                            pk.w = (uint32_t)f2bf(src[6]) | ((uint32_t)f2bf(src[7]) << 16);
-                            *(uint4*)dst = pk;
-                        } else {
-                            ((float4*)dst)[0] = float4{src[0], src[1], src[2], src[3]};
-                            ((float4*)dst)[1] = float4{src[4], src[5], src[6], src[7]};
-                        }
+                for (int r0 = 0; r0 < 16; r0 += RPP) {
+                    const int r = r0 + lane / LPR, p8 = (lane % LPR) * 8, row = 16 * wave + r;
+                    const bool ok = r < 16 && tc + row < T;
+                    const int off = ok ? (int)(((long long)row * a.st_o + p8) * (long long)sizeof(Tout)) : kOutDrop;
+                    const float* src = &Ot[wave][r & 15][p8];
+                    if constexpr (sizeof(Tout) == 2) {
+                        u32x4 pk;
+                        pk.x = (uint32_t)f2bf(src[0]) | ((uint32_t)f2bf(src[1]) << 16);
+                        pk.y = (uint32_t)f2bf(src[2]) | ((uint32_t)f2bf(src[3]) << 16);
+                        pk.z = (uint32_t)f2bf(src[4]) | ((uint32_t)f2bf(src[5]) << 16);
+                        pk.w = (uint32_t)f2bf(src[6]) | ((uint32_t)f2bf(src[7]) << 16);
+                        __builtin_amdgcn_raw_buffer_store_b128(pk, rs, off, 0, 0);
                     } else {
+                        const u32x4 lo = {__float_as_uint(src[0]), __float_as_uint(src[1]), __float_as_uint(src[2]),
+                                          __float_as_uint(src[3])};
+                        const u32x4 hi = {__float_as_uint(src[4]), __float_as_uint(src[5]), __float_as_uint(src[6]),
+                                          __float_as_uint(src[7])};
+                        __builtin_amdgcn_raw_buffer_store_b128(lo, rs, off, 0, 0);
+                        __builtin_amdgcn_raw_buffer_store_b128(hi, rs, ok ? off + 16 : kOutDrop, 0, 0);
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int r0 = 0; r0 < 16; r0 += RPP) {
+                    const int r = r0 + lane / LPR, p8 = (lane % LPR) * 8, tok = tc + 16 * wave + r;
+                    if (r < 16 && tok < T) {
+                        Tout* dst = out + b * a.sb_o + (long long)tok * a.st_o + hv * a.sh_o + col0 + p8;
+                        const float* src = &Ot[wave][r][p8];
 #pragma unroll
                         for (int e = 0; e < 8; e++) Act<Tout>::st(dst, e, src[e]);
                     }
@@ -629,6 +653,14 @@ __device__ __forceinline__ void chunk_state_body(const unsigned char* __restrict
     // covers the loads issued before it)
     Ops A, Bo;
     fetch(0, A);
+    if constexpr (VEC) {
+        // a discarded store in the place the loop body has one, so the loop entry and the back
+        // edge carry the same count of memory operations between A's and Bo's loads
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(out, (short)0, kOutRange, kBufWord3);
+        __builtin_amdgcn_raw_buffer_store_b128(u32x4{0u, 0u, 0u, 0u}, rs, kOutDrop, 0, 0);
+        if constexpr (sizeof(Tout) == 4)
+            __builtin_amdgcn_raw_buffer_store_b128(u32x4{0u, 0u, 0u, 0u}, rs, kOutDrop - 64, 0, 0);
+    }
     int c = 0;
     for (; c + 1 < nch; c += 2) {
         fetch(c + 1, Bo);
@@ -645,20 +677,20 @@ __device__ __forceinline__ void chunk_state_body(const unsigned char* __restrict
             for (int j = 0; j < 4; j++) Sg[(size_t)(32 * wave + 16 * rt + 4 * gq + j) * D + col0 + 16 * ct + n] = S[rt][ct][j];
 }
 
-template <typename Tout, int NCT>
+template <typename Tout, int NCT, bool VEC>
 __global__ void __launch_bounds__(256) delta_chunk_state(const unsigned char* __restrict__ ws, WsLayout L,
                                                          float* __restrict__ state, int load_state, Tout* __restrict__ out,
                                                          SeqLayout a, int t0, int T, int nch, int B, int HK,
-                                                         int HV, int vec_out) {
+                                                         int HV) {
     __shared__ K2Smem<NCT> sm;
-    chunk_state_body<Tout, NCT>(ws, L, state, load_state, out, a, t0, T, nch, B, HK, HV, vec_out, sm, blockIdx.x);
+    chunk_state_body<Tout, NCT, VEC>(ws, L, state, load_state, out, a, t0, T, nch, B, HK, HV, sm, blockIdx.x);
 }
 
 // One launch holding K2 of one segment (blocks [0, nk2)) and K1 of the next segment (the
 // remaining blocks, chunk fastest): the two are independent (different workspace buffers), so
 // the K1 workgroups fill the CUs around K2's without a second stream or events. LDS is the
 // union of the two bodies' needs.
-template <typename Tin, typename Tout, int NCT>
+template <typename Tin, typename Tout, int NCT, bool VEC>
 __global__ void __launch_bounds__(256, 2) delta_chunk_fused(
     // K2 of segment s
     const unsigned char* __restrict__ ws2, WsLayout L2, float* __restrict__ state, int load_state,
@@ -668,14 +700,14 @@ __global__ void __launch_bounds__(256, 2) delta_chunk_fused(
     const float* __restrict__ beta, int t0i, int nch1, unsigned char* __restrict__ ws1, WsLayout L1, int vec_in,
     int normalize, float qscale, float eps,
     // shared
-    SeqLayout a, int T, int B, int HK, int HV, int vec_out) {
+    SeqLayout a, int T, int B, int HK, int HV) {
     __shared__ union {
         K1Smem<sizeof(Tin) == 4> k1;
         K2Smem<NCT> k2;
     } sm;
     if ((int)blockIdx.x < nk2) {
-        chunk_state_body<Tout, NCT>(ws2, L2, state, load_state, out, a, t0s, T, nch2, B, HK, HV, vec_out, sm.k2,
-                                    blockIdx.x);
+        chunk_state_body<Tout, NCT, VEC>(ws2, L2, state, load_state, out, a, t0s, T, nch2, B, HK, HV, sm.k2,
+                                         blockIdx.x);
     } else {
         const int r = blockIdx.x - nk2, c = r % nch1, hv = (r / nch1) % HV, b = r / (nch1 * HV);
         chunk_intra_body<Tin>(q, k, v, g, beta, a, t0i, T, HK, HV, normalize, qscale, eps, ws1, L1, vec_in, sm.k1, c,
@@ -696,8 +728,8 @@ int seg_chunks(int B, int T, int HV) {
 namespace aegist {
 
 // Workspace: [carried state (when the caller passes none)][segment buffer 0][segment buffer 1]
-// (the second buffer only when there is more than one segment: the intra-chunk kernel of the
-// next segment then runs on a second stream while the state kernel reads this one).
+// (the second buffer only when there is more than one segment: the intra-chunk work of the
+// next segment then writes one buffer while the state work of this segment reads the other).
 struct WsPlan {
     size_t state_off, seg_bytes, total;
     int nch_seg, nbuf;
@@ -717,6 +749,12 @@ size_t delta_chunked_ws_bytes(int B, int T, int HK, int HV) {
     return ws_plan(B, T, HK, HV).total;
 }
 
+template <typename Tin, typename Tout, bool VEC>
+int run_segments(const Tin* q, const Tin* k, const Tin* v, const float* g, const float* beta, float* S,
+                 bool has_state, Tout* out, const SeqLayout& a, int B, int T, int HK, int HV, int normalize,
+                 float qscale, float eps, unsigned char* const segbuf[2], const WsPlan& plan, int vec_in,
+                 hipStream_t st);
+
 template <typename Tin, typename Tout>
 int run_chunked(const Tin* q, const Tin* k, const Tin* v, const float* g, const float* beta, float* state, Tout* out,
                 const SeqLayout& a, int B, int T, int HK, int HV, int normalize, float qscale, float eps, void* ws,
@@ -733,9 +771,22 @@ int run_chunked(const Tin* q, const Tin* k, const Tin* v, const float* g, const 
     const int vec_in = ((uintptr_t)q % 16 == 0) && ((uintptr_t)k % 16 == 0) && ((uintptr_t)v % 16 == 0) &&
                        a.sb_qk % ei == 0 && a.st_qk % ei == 0 && a.sh_qk % ei == 0 && a.sb_v % ei == 0 &&
                        a.st_v % ei == 0 && a.sh_v % ei == 0;
-    // 16-byte output stores need 16-byte aligned rows
+    // 16-byte buffer stores need 16-byte aligned rows, and the byte offsets of one chunk's rows
+    // from its first must stay below the buffer range
     const long long ev = 16 / (long long)sizeof(Tout);
-    const int vec_out = ((uintptr_t)out % 16 == 0) && a.sb_o % ev == 0 && a.st_o % ev == 0 && a.sh_o % ev == 0;
+    const bool vec_out = ((uintptr_t)out % 16 == 0) && a.sb_o % ev == 0 && a.st_o % ev == 0 && a.sh_o % ev == 0 &&
+                         a.st_o >= 0 && (long long)CH * a.st_o * (long long)sizeof(Tout) < kOutRange;
+    return vec_out ? run_segments<Tin, Tout, true>(q, k, v, g, beta, S, state != nullptr, out, a, B, T, HK, HV,
+                                                  normalize, qscale, eps, segbuf, plan, vec_in, st)
+                   : run_segments<Tin, Tout, false>(q, k, v, g, beta, S, state != nullptr, out, a, B, T, HK, HV,
+                                                   normalize, qscale, eps, segbuf, plan, vec_in, st);
+}
+
+template <typename Tin, typename Tout, bool VEC>
+int run_segments(const Tin* q, const Tin* k, const Tin* v, const float* g, const float* beta, float* S,
+                 bool has_state, Tout* out, const SeqLayout& a, int B, int T, int HK, int HV, int normalize,
+                 float qscale, float eps, unsigned char* const segbuf[2], const WsPlan& plan, int vec_in,
+                 hipStream_t st) {
     const int seg = plan.nch_seg * CH;
     const int nseg = (T + seg - 1) / seg;
     const int units8 = (B * HV + 7) / 8 * 8;
@@ -757,17 +808,17 @@ int run_chunked(const Tin* q, const Tin* k, const Tin* v, const float* g, const 
     }
     for (int s = 0; s < nseg; s++) {
         const auto [nch2, L2] = seg_layout(s);
-        const int load = (state || s > 0) ? 1 : 0;
+        const int load = (has_state || s > 0) ? 1 : 0;
         if (s + 1 < nseg) {
             const auto [nch1, L1] = seg_layout(s + 1);
-            delta_chunk_fused<Tin, Tout, K2_NCT><<<nk2 + nch1 * HV * B, 256, 0, st>>>(
+            delta_chunk_fused<Tin, Tout, K2_NCT, VEC><<<nk2 + nch1 * HV * B, 256, 0, st>>>(
                 segbuf[s & 1], L2, S, load, out, s * seg, nch2, nk2, q, k, v, g, beta, (s + 1) * seg, nch1,
-                segbuf[(s + 1) & 1], L1, vec_in, normalize, qscale, eps, a, T, B, HK, HV, vec_out);
+                segbuf[(s + 1) & 1], L1, vec_in, normalize, qscale, eps, a, T, B, HK, HV);
             int rc = after_launch("delta_chunk_fused");
             if (rc) return rc;
         } else {
-            delta_chunk_state<Tout, K2_NCT><<<nk2, 256, 0, st>>>(segbuf[s & 1], L2, S, load, out, a, s * seg, T, nch2,
-                                                                  B, HK, HV, vec_out);
+            delta_chunk_state<Tout, K2_NCT, VEC><<<nk2, 256, 0, st>>>(segbuf[s & 1], L2, S, load, out, a, s * seg, T,
+                                                                       nch2, B, HK, HV);
             int rc = after_launch("delta_chunk_state");
             if (rc) return rc;
         }
