@@ -458,46 +458,63 @@ __global__ void __launch_bounds__(256) attn_prefill_simple_kernel(const float* _
 
 // ---------------------------------------------------------------------------------------------
 // Causal flash prefill on v_mfma_f32_16x16x32_bf16. One workgroup of 8 waves per (sequence,
-// query head, 128 queries); wave w owns query rows [16w, 16w + 16). Key tiles of 64 rows: K and
-// V are staged in LDS as the cache's own bf16 rows (a plain copy, no conversion). The scores
-// q K^T take K rows straight as the B operand; P V takes V through LDS transpose reads
-// (ds_read_b64_tr_b16: each lane of a 16-lane group receives 4 consecutive keys of one dim), so
-// V never needs a transposed copy. q * scale and the probabilities enter as bf16 hi + lo pairs
-// (two MFMAs each): ~16 significant bits against the exact bf16 K and V. Online softmax per row
-// in fp32 (base-2, log2 e folded into the q scale; the accumulators are rescaled only when a
-// row's running maximum moved); output * sigmoid(gate). A wave whose rows cannot see any key of
-// a tile skips it.
+// query head, 128 queries); wave w owns queries [16w, 16w + 16). Key tiles of 64 rows: K and V
+// are staged in LDS as the cache's own bf16 rows (a plain copy, no conversion).
+//
+// Everything is computed transposed, so that a lane owns one query throughout:
+//   S^T = K q^T     (A = K rows from LDS, B = q): lane (n, g) holds query n's scores for keys
+//                   16 nb + 4 g + j (nb < 4, j < 4);
+//   O^T += V^T P^T  (A = V^T through LDS transpose reads, B = P^T straight from the score
+//                   registers): lane (n, g) accumulates query n's output dims 16 db + 4 g + j.
+// The k index of a P V step runs over the 32 keys of two score blocks in the order the score
+// registers hold them (lane group g: keys 4 g .. 4 g + 3 of block 2 ks, then of block 2 ks + 1);
+// the V operand reads the same keys (ds_read_b64_tr_b16 hands lane j four consecutive keys of
+// one dim), so P never goes through LDS and the online-softmax statistics of a query live in
+// the four lanes n, n + 16, n + 32, n + 48 (max: two cross-group shuffles; sum: kept per lane,
+// reduced once at the end).
+//
+// q * scale and the probabilities enter as bf16 hi + lo pairs (two MFMAs each): ~16
+// significant bits against the exact bf16 K and V. Base-2 softmax (log2 e folded into the q
+// scale); the accumulators are rescaled only when some query's running maximum moved;
+// output * sigmoid(gate). A wave whose queries cannot see any key of a tile skips it.
 #ifndef PREFILL_PQ
 #define PREFILL_PQ 128
 #endif
-#ifndef PREFILL_PK
-#define PREFILL_PK 64
-#endif
-constexpr int PQ = PREFILL_PQ, PK = PREFILL_PK;  // queries per workgroup, keys per tile
-constexpr int PNB = PK / 16, PKS = PK / 32;      // 16-key score blocks, 32-key P V steps
-constexpr int PW = PQ / 16;           // waves per workgroup
-constexpr int KVLD = HD + 16;         // K / V tile row stride (bf16): 136 words = 8 mod 64 banks
+constexpr int PQ = PREFILL_PQ, PK = 64;  // queries per workgroup, keys per tile
+constexpr int PW = PQ / 16;              // waves per workgroup
+// LDS row strides (bf16 elements). K: 132 words = 4 mod 64 banks, so the 16 rows a 16-lane
+// group reads with 16-byte loads cover all 64 banks. V: 136 words = 8 mod 64 banks: a transpose
+// read touches 4 consecutive rows x 32 bytes per 16 lanes, and the two lane groups served in
+// one cycle sit 4 rows (32 banks) apart.
+constexpr int KLD = HD + 8, VLD = HD + 16;
 
 typedef short short4v __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ void split_bf16x8(const float* x, bf16x8& hi, bf16x8& lo) {
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-        uint16_t h, l;
-        split_bf16(x[i], h, l);
-        hi[i] = (short)h;
-        lo[i] = (short)l;
-    }
+// x0, x1 -> elements e, e + 1 of hi and lo: hi = x truncated to bf16 (so x - hi is exact in
+// fp32), lo = that remainder rounded to bf16; hi + lo carries ~16 significant bits of x
+__device__ __forceinline__ void split_pairs(float x0, float x1, bf16x8& hi, bf16x8& lo, int e) {
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+    const uint32_t u0 = __float_as_uint(x0), u1 = __float_as_uint(x1);
+    const f2 r = {x0 - __uint_as_float(u0 & 0xffff0000u), x1 - __uint_as_float(u1 & 0xffff0000u)};
+    const uint32_t lp = __builtin_bit_cast(uint32_t, __builtin_convertvector(r, b2));
+    const uint32_t hp = __builtin_amdgcn_perm(u1, u0, 0x07060302u);
+    hi[e] = (short)(hp & 0xffffu);
+    hi[e + 1] = (short)(hp >> 16);
+    lo[e] = (short)(lp & 0xffffu);
+    lo[e + 1] = (short)(lp >> 16);
 }
 
-// B operand of P V for keys [row0, row0 + 8) of dim block col0..col0+15 from row-major bf16 V
-// rows in LDS: lane (g, n) gets V[row0 + 8 g + e][col0 + n], e < 8, via two transpose reads.
-__device__ __forceinline__ bf16x8 v_operand(const uint16_t* vt, int row0, int col0, int lane) {
+// A operand of O^T += V^T P^T for P V step ks and dim block db: lane (d, g) gets
+// V[32 ks + 4 g + e][16 db + d] (e < 4), then V[32 ks + 16 + 4 g + e][16 db + d]. In a transpose
+// read lane k addresses row R + k / 4, dims C + 4 (k % 4) .. +3; lane j receives rows R .. R + 3
+// of dim C + j.
+__device__ __forceinline__ bf16x8 vt_operand(const uint16_t* vt, int ks, int db, int lane) {
     const int g = lane / 16, k = lane % 16;
-    const uint16_t* p = vt + (size_t)(row0 + 8 * g + (k >> 2)) * KVLD + col0 + 4 * (k & 3);
+    const uint16_t* p = vt + (size_t)(32 * ks + 4 * g + (k >> 2)) * VLD + 16 * db + 4 * (k & 3);
     typedef __attribute__((address_space(3))) short4v lds_short4;
     const short4v a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4*)(p));
-    const short4v b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4*)(p + 4 * KVLD));
+    const short4v b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4*)(p + 16 * VLD));
     return bf16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
 }
 
@@ -506,39 +523,44 @@ __global__ void __launch_bounds__(64 * PW) attn_prefill_mfma_kernel(const float*
                                                                      const uint16_t* __restrict__ vc,
                                                                      const float* __restrict__ gate, Strides3 gs,
                                                                      float* __restrict__ out, Strides3 os, int H,
-                                                                     int KV, int T, int pos, int cap, float scale) {
-    __shared__ __attribute__((aligned(16))) uint16_t Kt[PK * KVLD];
-    __shared__ __attribute__((aligned(16))) uint16_t Vt[PK * KVLD];
-    __shared__ __attribute__((aligned(16))) uint16_t Pt[PW][2][16][PK + 8];  // P hi, lo (bf16)
+                                                                     int KV, int T, int pos, int cap, float scale,
+                                                                     int B, int per_xcd) {
+    __shared__ __attribute__((aligned(16))) uint16_t Kt[PK * KLD];
+    __shared__ __attribute__((aligned(16))) uint16_t Vt[PK * VLD];
 
-    const int qb = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    // XCD-aware order (1-D grid of 8 per_xcd blocks, dealt round-robin to the 8 XCDs): XCD x
+    // runs logical blocks [x per_xcd, (x + 1) per_xcd) in order, so the workgroups resident on
+    // one XCD at a time belong to one (sequence, KV head) and share its K / V rows in that
+    // XCD's L2. Within a (sequence, KV head): query head, then query blocks longest first.
+    const int nqb = (T + PQ - 1) / PQ, G = H / KV;
+    const int li = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+    if (li >= nqb * H * B) return;
+    const int qb = nqb - 1 - li % nqb, hh = (li / nqb) % G, kvh = (li / (nqb * G)) % KV, b = li / (nqb * H);
+    const int h = kvh * G + hh;
     const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE, n = lane % 16, g = lane / 16;
-    const int G = H / KV, kvh = h / G;
     const int q0 = qb * PQ;  // first query (sequence-relative)
     const uint16_t* kbase = kc + ((size_t)b * KV + kvh) * (size_t)cap * HD;
     const uint16_t* vbase = vc + ((size_t)b * KV + kvh) * (size_t)cap * HD;
 
-    // Q operand: row n of this wave's 16 queries, k elements 32 ks + 8 g .. +8, as bf16 hi + lo
+    // q operand (B of S^T): query n of this wave, dims 32 ks + 8 g .. +8, as bf16 hi + lo
     bf16x8 qh[8], ql[8];
     {
         const int t = min(q0 + 16 * wave + n, T - 1);
         const float* qr = q + b * qs.b + (long long)t * qs.t + h * qs.h;
+        // scores in the log2 domain: exp(s) = exp2(s log2 e)
+        const float sl = scale * 1.4426950408889634f;
 #pragma unroll
         for (int ks = 0; ks < 8; ks++) {
             const float4 a0 = *(const float4*)(qr + 32 * ks + 8 * g);
             const float4 a1 = *(const float4*)(qr + 32 * ks + 8 * g + 4);
-            // scores in the log2 domain: exp(s) = exp2(s log2 e)
-            const float sl = scale * 1.4426950408889634f;
-            const float x[8] = {a0.x * sl, a0.y * sl, a0.z * sl, a0.w * sl, a1.x * sl, a1.y * sl, a1.z * sl, a1.w * sl};
-            split_bf16x8(x, qh[ks], ql[ks]);
+            split_pairs(a0.x * sl, a0.y * sl, qh[ks], ql[ks], 0);
+            split_pairs(a0.z * sl, a0.w * sl, qh[ks], ql[ks], 2);
+            split_pairs(a1.x * sl, a1.y * sl, qh[ks], ql[ks], 4);
+            split_pairs(a1.z * sl, a1.w * sl, qh[ks], ql[ks], 6);
         }
     }
-    float m_run[4], l_run[4];
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-        m_run[j] = -INFINITY;
-        l_run[j] = 0.f;
-    }
+    const int qpos = pos + q0 + 16 * wave + n;  // this lane's query position in the cache
+    float m_run = -INFINITY, l_part = 0.f;     // l_part: this lane's share of the row sum
     f32x4 oacc[16];
 #pragma unroll
     for (int i = 0; i < 16; i++) oacc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -548,127 +570,119 @@ __global__ void __launch_bounds__(64 * PW) attn_prefill_mfma_kernel(const float*
     const int wave_last = pos + min(q0 + 16 * wave + 15, T - 1);  // the last key this wave's rows see
     // Tile staging: 16-byte chunk c8 of key row r; the next tile is held in registers, requested
     // a full tile ahead.
-    constexpr int NSTEP = (PK * HD) / (8 * 64 * PW);  // 4
-    uint4 kreg[NSTEP], vreg[NSTEP];
-    auto fetch = [&](int kt) {
+    constexpr int NSTEP = (PK * HD) / (8 * 64 * PW);
+    constexpr int RSTEP = 64 * PW / (HD / 8);  // key rows between a thread's chunks
+    const int r_own = tid / (HD / 8), c_own = (tid % (HD / 8)) * 8;
+    typedef unsigned u32x4 __attribute__((ext_vector_type(4)));  // (HIP's uint4 blocks register promotion)
+    u32x4 kreg[NSTEP], vreg[NSTEP];
 #pragma unroll
-        for (int it = 0; it < NSTEP; it++) {
-            const int idx = it * 64 * PW + tid, r = idx / (HD / 8), c8 = (idx % (HD / 8)) * 8;
-            const int key = min(kt * PK + r, last_key);
-            kreg[it] = *(const uint4*)(kbase + (size_t)key * HD + c8);
-            vreg[it] = *(const uint4*)(vbase + (size_t)key * HD + c8);
-        }
-    };
-    fetch(0);
+    for (int it = 0; it < NSTEP; it++) {
+        const size_t off = (size_t)min(r_own + it * RSTEP, last_key) * HD + c_own;
+        kreg[it] = *(const u32x4*)(kbase + off);
+        vreg[it] = *(const u32x4*)(vbase + off);
+    }
     for (int kt = 0; kt < ntiles; kt++) {
         const int key0 = kt * PK;
         __syncthreads();  // previous tile's LDS reads done
 #pragma unroll
         for (int it = 0; it < NSTEP; it++) {
-            const int idx = it * 64 * PW + tid, r = idx / (HD / 8), c8 = (idx % (HD / 8)) * 8;
-            *(uint4*)&Kt[r * KVLD + c8] = kreg[it];
-            *(uint4*)&Vt[r * KVLD + c8] = vreg[it];
+            const int r = r_own + it * RSTEP;
+            *(u32x4*)&Kt[r * KLD + c_own] = kreg[it];
+            *(u32x4*)&Vt[r * VLD + c_own] = vreg[it];
         }
         __syncthreads();
-        fetch(min(kt + 1, ntiles - 1));  // unconditional: static wait counts
-        if (key0 > wave_last) continue;  // no row of this wave sees any key of this tile
-        // ---- scores for 4 blocks of 16 keys
-        f32x4 sc[PNB];
+        {   // next tile (unconditional: static wait counts)
+            const int kn = min(kt + 1, ntiles - 1) * PK;
 #pragma unroll
-        for (int nb = 0; nb < PNB; nb++) {
+            for (int it = 0; it < NSTEP; it++) {
+                const size_t off = (size_t)min(kn + r_own + it * RSTEP, last_key) * HD + c_own;
+                kreg[it] = *(const u32x4*)(kbase + off);
+                vreg[it] = *(const u32x4*)(vbase + off);
+            }
+        }
+        if (key0 > wave_last) continue;  // no query of this wave sees any key of this tile
+        // ---- S^T for 4 blocks of 16 keys: sc[nb][j] = score of key key0 + 16 nb + 4 g + j
+        f32x4 sc[4];
+#pragma unroll
+        for (int nb = 0; nb < 4; nb++) {
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int ks = 0; ks < 8; ks++) {
-                const bf16x8 kb = *(const bf16x8*)&Kt[(16 * nb + n) * KVLD + 32 * ks + 8 * g];
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qh[ks], kb, acc, 0, 0, 0);
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ql[ks], kb, acc, 0, 0, 0);
+                const bf16x8 kb = *(const bf16x8*)&Kt[(16 * nb + n) * KLD + 32 * ks + 8 * g];
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kb, qh[ks], acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kb, ql[ks], acc, 0, 0, 0);
             }
-            // lane: key 16 nb + n, query rows 4 g + j of the wave; causal mask
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const int qpos = pos + q0 + 16 * wave + 4 * g + j, key = key0 + 16 * nb + n;
-                sc[nb][j] = key <= qpos ? acc[j] : -INFINITY;
-            }
+            for (int j = 0; j < 4; j++) sc[nb][j] = key0 + 16 * nb + 4 * g + j <= qpos ? acc[j] : -INFINITY;
         }
-        // ---- online softmax per query row (row = 4 g + j; keys over the 16 lanes n and 4 blocks),
-        // base-2 exponentials; the accumulators are rescaled only when some row's maximum moved
-        bool moved = false;
-        float corr[4];
+        // ---- online softmax for query n (its 64 keys over this lane's 16 and lanes n + 16 g)
+        float mt = sc[0][0];
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            float mt = sc[0][j];
+        for (int nb = 0; nb < 4; nb++)
 #pragma unroll
-            for (int nb = 1; nb < PNB; nb++) mt = fmaxf(mt, sc[nb][j]);
-            mt = fmaxf(mt, __shfl_xor(mt, 1, WAVE));
-            mt = fmaxf(mt, __shfl_xor(mt, 2, WAVE));
-            mt = fmaxf(mt, __shfl_xor(mt, 4, WAVE));
-            mt = fmaxf(mt, __shfl_xor(mt, 8, WAVE));
-            const float mn = fmaxf(m_run[j], mt);
-            // a row with no visible key yet keeps m = -inf: use 0 as the reference so exp2() is 0
-            const float ref = mn == -INFINITY ? 0.f : mn;
-            corr[j] = exp2f(m_run[j] - ref);
-            moved |= mn != m_run[j];
-            float ps = 0.f;
+            for (int j = 0; j < 4; j++) mt = fmaxf(mt, sc[nb][j]);
+        mt = fmaxf(mt, __shfl_xor(mt, 16, WAVE));
+        mt = fmaxf(mt, __shfl_xor(mt, 32, WAVE));
+        const float mn = fmaxf(m_run, mt);
+        // a query with no visible key yet keeps m = -inf: use 0 as the reference so exp2() is 0
+        const float ref = mn == -INFINITY ? 0.f : mn;
+        const float corr = exp2f(m_run - ref);
+        const bool moved = mn != m_run;
+        m_run = mn;
+        // P^T operand of step ks: keys 4 g + e of block 2 ks (e < 4), then of block 2 ks + 1;
+        // hi = p truncated to bf16 (exact remainder), lo = the remainder rounded to bf16
+        bf16x8 ph[2], pl[2];
+        float ps = 0.f;
 #pragma unroll
-            for (int nb = 0; nb < PNB; nb += 2) {
-                const float p0 = exp2f(sc[nb][j] - ref), p1 = exp2f(sc[nb + 1][j] - ref);
+        for (int ks = 0; ks < 2; ks++)
+#pragma unroll
+            for (int e = 0; e < 8; e += 2) {
+                const int nb = 2 * ks + (e >> 2), j = e & 3;
+                // arguments <= 0 (or -inf): the hardware exp2 needs no range fix-up here
+                const float p0 = __builtin_amdgcn_exp2f(sc[nb][j] - ref);
+                const float p1 = __builtin_amdgcn_exp2f(sc[nb][j + 1] - ref);
                 ps += p0 + p1;
-                // hi = p truncated to bf16 (exact remainder), lo = the remainder rounded to bf16
-                typedef float f2 __attribute__((ext_vector_type(2)));
-                typedef __bf16 b2 __attribute__((ext_vector_type(2)));
-                const uint32_t h0 = __float_as_uint(p0) & 0xffff0000u, h1 = __float_as_uint(p1) & 0xffff0000u;
-                const f2 lo = {p0 - __uint_as_float(h0), p1 - __uint_as_float(h1)};
-                const uint32_t lp = __builtin_bit_cast(uint32_t, __builtin_convertvector(lo, b2));
-                Pt[wave][0][4 * g + j][16 * nb + n] = (uint16_t)(h0 >> 16);
-                Pt[wave][0][4 * g + j][16 * (nb + 1) + n] = (uint16_t)(h1 >> 16);
-                Pt[wave][1][4 * g + j][16 * nb + n] = (uint16_t)(lp & 0xffffu);
-                Pt[wave][1][4 * g + j][16 * (nb + 1) + n] = (uint16_t)(lp >> 16);
+                split_pairs(p0, p1, ph[ks], pl[ks], e);
             }
-            l_run[j] = l_run[j] * corr[j] + ps;
-            m_run[j] = mn;
-        }
+        l_part = l_part * corr + ps;
         if (__ballot(moved)) {
 #pragma unroll
             for (int i = 0; i < 16; i++)
 #pragma unroll
-                for (int j = 0; j < 4; j++) oacc[i][j] *= corr[j];
+                for (int j = 0; j < 4; j++) oacc[i][j] *= corr;
         }
-        wave_sync();
-        // ---- O += P V (k = 64 keys in 2 steps; 16 output blocks of 16 dims)
-        bf16x8 ph[PKS], pl[PKS];
-#pragma unroll
-        for (int ks = 0; ks < PKS; ks++) {
-            ph[ks] = *(const bf16x8*)&Pt[wave][0][n][32 * ks + 8 * g];
-            pl[ks] = *(const bf16x8*)&Pt[wave][1][n][32 * ks + 8 * g];
-        }
+        // ---- O^T += V^T P^T (16 dim blocks, 64 keys in 2 steps)
 #pragma unroll
         for (int db = 0; db < 16; db++)
 #pragma unroll
-            for (int ks = 0; ks < PKS; ks++) {
-                const bf16x8 vb = v_operand(Vt, 32 * ks, 16 * db, lane);
-                oacc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ph[ks], vb, oacc[db], 0, 0, 0);
-                oacc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pl[ks], vb, oacc[db], 0, 0, 0);
+            for (int ks = 0; ks < 2; ks++) {
+                const bf16x8 va = vt_operand(Vt, ks, db, lane);
+                oacc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, ph[ks], oacc[db], 0, 0, 0);
+                oacc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pl[ks], oacc[db], 0, 0, 0);
             }
     }
-    // ---- normalise, gate, store: lane holds rows 4 g + j, dims 16 db + n
+    // ---- normalise, gate, store: lane holds query n, dims 16 db + 4 g .. +4
+    float l = l_part;
+    l += __shfl_xor(l, 16, WAVE);
+    l += __shfl_xor(l, 32, WAVE);
+    const int t = q0 + 16 * wave + n;
+    if (t >= T) return;
+    float* orow = out + b * os.b + (long long)t * os.t + h * os.h;
+    const float* grow = gate ? gate + b * gs.b + (long long)t * gs.t + h * gs.h : nullptr;
+    const float inv = 1.f / l;
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-        float l = l_run[j];
-        l += __shfl_xor(l, 1, WAVE);
-        l += __shfl_xor(l, 2, WAVE);
-        l += __shfl_xor(l, 4, WAVE);
-        l += __shfl_xor(l, 8, WAVE);
-        const int t = q0 + 16 * wave + 4 * g + j;
-        if (t >= T) continue;
-        float* orow = out + b * os.b + (long long)t * os.t + h * os.h;
-        const float* grow = gate ? gate + b * gs.b + (long long)t * gs.t + h * gs.h : nullptr;
-        const float inv = 1.f / l;
+    for (int db = 0; db < 16; db++) {
+        float y[4];
 #pragma unroll
-        for (int db = 0; db < 16; db++) {
-            float y = oacc[db][j] * inv;
-            if (grow) y *= sigmoid_f(grow[16 * db + n]);
-            orow[16 * db + n] = y;
+        for (int j = 0; j < 4; j++) y[j] = oacc[db][j] * inv;
+        if (grow) {
+            const float4 gv = *(const float4*)(grow + 16 * db + 4 * g);
+            y[0] *= sigmoid_f(gv.x);
+            y[1] *= sigmoid_f(gv.y);
+            y[2] *= sigmoid_f(gv.z);
+            y[3] *= sigmoid_f(gv.w);
         }
+        *(float4*)(orow + 16 * db + 4 * g) = float4{y[0], y[1], y[2], y[3]};
     }
 }
 
@@ -716,10 +730,15 @@ int launch_prefill_core(const float* q, Strides3 qs, const uint16_t* kc, const u
                         float scale, hipStream_t st) {
     if (KV <= 0 || H % KV) return fail(AEGIST_ERR_SHAPE, "attention prefill: need H % KV == 0");
     if (pos < 0 || pos + T > cap) return fail(AEGIST_ERR_SHAPE, "attention prefill: rows exceed the cache capacity");
-    const bool vec_q = ((uintptr_t)q % 16 == 0) && qs.b % 4 == 0 && qs.t % 4 == 0 && qs.h % 4 == 0;
-    if (T >= 16 && vec_q) {
-        attn_prefill_mfma_kernel<<<dim3((T + PQ - 1) / PQ, H, B), 64 * PW, 0, st>>>(q, qs, kc, vc, gate, gs, out, os, H,
-                                                                                  KV, T, pos, cap, scale);
+    // the MFMA kernel reads q and gate and writes out as 16-byte rows
+    auto rows16 = [](const void* p, const Strides3& s) {
+        return (uintptr_t)p % 16 == 0 && s.b % 4 == 0 && s.t % 4 == 0 && s.h % 4 == 0;
+    };
+    const bool vec = rows16(q, qs) && rows16(out, os) && (!gate || rows16(gate, gs));
+    if (T >= 16 && vec) {
+        const int nblk = (T + PQ - 1) / PQ * H * B, per_xcd = (nblk + 7) / 8;
+        attn_prefill_mfma_kernel<<<8 * per_xcd, 64 * PW, 0, st>>>(q, qs, kc, vc, gate, gs, out, os, H, KV, T, pos, cap,
+                                                                  scale, B, per_xcd);
     } else {
         attn_prefill_simple_kernel<<<dim3((T + 3) / 4, H, B), 256, 0, st>>>(q, qs, kc, vc, gate, gs, out, os, H, KV, T,
                                                                             pos, cap, scale);

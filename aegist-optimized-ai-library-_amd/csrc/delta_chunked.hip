@@ -678,7 +678,7 @@ __device__ __forceinline__ void chunk_state_body(const unsigned char* __restrict
 }
 
 template <typename Tout, int NCT, bool VEC>
-__global__ void __launch_bounds__(256) delta_chunk_state(const unsigned char* __restrict__ ws, WsLayout L,
+__global__ void __launch_bounds__(256, 2) delta_chunk_state(const unsigned char* __restrict__ ws, WsLayout L,
                                                          float* __restrict__ state, int load_state, Tout* __restrict__ out,
                                                          SeqLayout a, int t0, int T, int nch, int B, int HK,
                                                          int HV) {
