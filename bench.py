@@ -154,34 +154,40 @@ def bench_attention_decode(torch, ops, dev, reps=20):
 
 
 def bench_attention_prefill(torch, ops, dev, T=2048, reps=10):
-    """Causal gated GQA prefill (config 4's attention layers): B=1, T=2048, 16 q heads, 2 KV
-    heads, HD 256, cache rows [0, T). FLOPs = 4 * H * HD * T (T + 1) / 2 (QK^T and PV)."""
-    from aegist_mixer._lib import call, lib
+    """Causal gated GQA prefill (config 4's attention layers): T=2048, 16 q heads, 2 KV heads,
+    HD 256, cache rows [0, T), at B=1 (the headline fields) and at config 4's B=16 (`points`).
+    FLOPs = 4 * B * H * HD * T (T + 1) / 2 (QK^T and PV)."""
+    from aegist_mixer._lib import call
     bf = torch.bfloat16
-    q = ops.fill_normal(torch.empty(1, ATTN_H, T, ATTN_HD, device=dev), 9001)
-    kc = ops.fill_normal(torch.empty(1, ATTN_KV, T, ATTN_HD, device=dev, dtype=bf), 9002)
-    vc = ops.fill_normal(torch.empty(1, ATTN_KV, T, ATTN_HD, device=dev, dtype=bf), 9003)
-    gate = ops.fill_normal(torch.empty(1, T, ATTN_H * ATTN_HD, device=dev), 9004)
-    out = torch.empty(1, T, ATTN_H, ATTN_HD, device=dev)
     stream = torch.cuda.current_stream().cuda_stream
+    points = []
+    for B in (1, 16):
+        q = ops.fill_normal(torch.empty(B, ATTN_H, T, ATTN_HD, device=dev), 9001)
+        kc = ops.fill_normal(torch.empty(B, ATTN_KV, T, ATTN_HD, device=dev, dtype=bf), 9002)
+        vc = ops.fill_normal(torch.empty(B, ATTN_KV, T, ATTN_HD, device=dev, dtype=bf), 9003)
+        gate = ops.fill_normal(torch.empty(B, T, ATTN_H * ATTN_HD, device=dev), 9004)
+        out = torch.empty(B, T, ATTN_H, ATTN_HD, device=dev)
 
-    def run():
-        call("aegist_attention_core", q.data_ptr(), kc.data_ptr(), vc.data_ptr(), gate.data_ptr(), out.data_ptr(), 1,
-             ATTN_H, ATTN_KV, T, 0, T, ATTN_HD ** -0.5, None, 0, stream)
-    for _ in range(2):
-        run()
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(reps):
-        run()
-    e1.record()
-    torch.cuda.synchronize()
-    us = e0.elapsed_time(e1) * 1e3 / reps
-    flops = 4 * ATTN_H * ATTN_HD * T * (T + 1) / 2
-    tf = flops / (us * 1e-6) / 1e12
-    return {"workload": f"causal gated GQA prefill, B=1, T={T}, 16/2 heads, HD 256", "us": round(us, 2),
-            "tflops": round(tf, 2), "mfma_frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4)}
+        def run():
+            call("aegist_attention_core", q.data_ptr(), kc.data_ptr(), vc.data_ptr(), gate.data_ptr(), out.data_ptr(),
+                 B, ATTN_H, ATTN_KV, T, 0, T, ATTN_HD ** -0.5, None, 0, stream)
+        for _ in range(2):
+            run()
+        torch.cuda.synchronize()
+        n = reps if B == 1 else max(2, reps // 4)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(n):
+            run()
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / n
+        tf = 4 * B * ATTN_H * ATTN_HD * T * (T + 1) / 2 / (us * 1e-6) / 1e12
+        points.append({"B": B, "us": round(us, 2), "tflops": round(tf, 2), "mfma_frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4)})
+        del q, kc, vc, gate, out
+    p1 = points[0]
+    return {"workload": f"causal gated GQA prefill, T={T}, 16/2 heads, HD 256 (headline fields: B=1)",
+            "us": p1["us"], "tflops": p1["tflops"], "mfma_frac": p1["mfma_frac"], "points": points}
 
 
 def bench_proj(torch, ops, dev, reps=3):
