@@ -73,6 +73,11 @@ SIGNATURES: dict[str, tuple] = {
     "aegist_gemm_i8": (I, [P, P, P, P, I, I, I, I, P]),
     "aegist_linear": (I, [P, I, LL, P, I, P, P, LL, I, I, I, I, P]),
     "aegist_linear_multi": (I, [P, I, LL, I, I, P, P, P, P, P, I, I, I, P]),
+    "aegist_router_topk": (I, [P, P, P, P, I, I, I, I, P]),
+    "aegist_moe_workspace_bytes": (SZ, [I, I, I, I, I]),
+    "aegist_moe_experts": (I, [P, P, P, P, P, I, I, I, I, I, P, P, P, SZ, P]),
+    "aegist_shared_gate_add": (I, [P, P, P, P, I, I, P]),
+    "aegist_silu_mul": (I, [P, P, P, LL, P]),
 }
 
 

@@ -407,6 +407,81 @@ def gemv_bf16(x, weight, y=None):
     return y
 
 
+# --- mixture of experts (MoE, aegist/hybrid.py:631-652; HybridEngine::moe, hybrid.rs:863-955) -----
+
+def router_topk(h, W, K: int):
+    """router_topk (hybrid.cu:317-362): h fp32 [T, D], W bf16 [E, D] -> (idx int32 [T, K], wts fp32
+    [T, K]): the K most probable experts of softmax(h W^T) in descending order (ties to the lower
+    expert), weights renormalised over the picks."""
+    _need_contig(h, W)
+    T, D = h.shape
+    E = W.shape[0]
+    idx = torch.empty(T, K, dtype=torch.int32, device=h.device)
+    wts = torch.empty(T, K, dtype=torch.float32, device=h.device)
+    call("aegist_router_topk", _p(h), _p(W), _p(idx), _p(wts), T, D, E, K, _stream())
+    return idx, wts
+
+
+def expert_pointers(experts):
+    """Device array of expert-row addresses for a contiguous uint8 [E, row_bytes] expert tensor."""
+    E, rb = experts.shape
+    base = experts.data_ptr()
+    return torch.tensor([base + e * rb for e in range(E)], dtype=torch.int64, device=experts.device)
+
+
+def moe_experts(h, experts, idx, wts, x, I: int, ysh=None, wg=None, eptr=None):
+    """x[t] += sum_k wts[t, k] * expert_idx[t, k](h[t]) (+ sigmoid(h[t] . wg) * ysh[t]); in place.
+
+    h, x: fp32 [T, D]; experts: uint8 [E, row] in the expert_layout of hybrid.py:472-482 (or pass
+    eptr, an int64 device array of E row addresses, with experts=None and E = eptr.numel());
+    idx int32 / wts fp32 [T, K]; ysh fp32 [T, D] and wg bf16 [D] for the gated shared expert."""
+    _need_contig(h, idx, wts, x, ysh, wg)
+    T, D = h.shape
+    K = idx.shape[1]
+    if eptr is None:
+        eptr = expert_pointers(experts)
+    E = eptr.numel()
+    need = lib().aegist_moe_workspace_bytes(T, K, D, I, E)
+    ws = torch.empty(need, dtype=torch.uint8, device=h.device)
+    call("aegist_moe_experts", _p(h), _p(eptr), _p(idx), _p(wts), _p(x), T, D, I, E, K, _p(ysh), _p(wg), _p(ws),
+         need, _stream())
+    return x
+
+
+def shared_gate_add(x, y, h, wg):
+    """shared_gate_add (hybrid.cu:569-577): x[t] += sigmoid(h[t] . wg) * y[t], in place."""
+    _need_contig(x, y, h, wg)
+    T, D = x.shape
+    call("aegist_shared_gate_add", _p(x), _p(y), _p(h), _p(wg), T, D, _stream())
+    return x
+
+
+def silu_mul(g, u, out=None):
+    """silu_mul (aegist.cu:174-178): out = silu(g) * u."""
+    _need_contig(g, u)
+    if out is None:
+        out = torch.empty_like(g)
+    call("aegist_silu_mul", _p(g), _p(u), _p(out), g.numel(), _stream())
+    return out
+
+
+def moe_forward(h, x, router_w, experts, I: int, K: int, shared=None, shared_gate=None):
+    """The MoE block of one layer on the residual x (MoE.forward, hybrid.py:647-652; the engine's
+    moe(), hybrid.rs:863-955, without its expert paging): route, the routed experts, and the
+    shared SwiGLU expert gated by sigmoid(h . shared_gate). shared: ((w_gate, s_gate), (w_up,
+    s_up), (w_down, s_down)) QLinear int8 weights with bf16 scales (or bf16 weights with None).
+    Returns (idx, wts)."""
+    idx, wts = router_topk(h, router_w, K)
+    ysh = None
+    if shared is not None:
+        (wgt, sg), (wup, su), (wdn, sd) = shared
+        g = linear(h, wgt, sg)
+        u = linear(h, wup, su)
+        ysh = linear(silu_mul(g, u), wdn, sd)
+    moe_experts(h, experts, idx, wts, x, I, ysh=ysh, wg=shared_gate if shared is not None else None)
+    return idx, wts
+
+
 class HybridStack:
     """Batched mixer stack on the device (aegist_stack_* of the C ABI): per layer
     x = x + mixer(znorm(x)), DeltaNet or gated attention, MoE FFN as identity

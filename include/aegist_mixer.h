@@ -322,6 +322,38 @@ int aegist_linear_multi(const void* X, int x_dtype, long long ldx, int w_dtype, 
                         const uint16_t* const* scale, float* const* Y, const long long* ldy, const int* N, int M,
                         int K, int accumulate, void* stream);
 
+/* -------------------------------------------------------------------------------------
+ * Mixture of experts: the block after the mixer in every layer (MoE, aegist/hybrid.py:631-652;
+ * HybridEngine::moe, aegist_rs/src/hybrid.rs:863-955). h [T, D] fp32 (the norm2 output), x
+ * [T, D] fp32 residual. Experts are 4-bit SwiGLU experts of hidden size I in 64-value groups,
+ * each one packed row in the layout of expert_layout (aegist/hybrid.py:472-482):
+ * [gu_q 2I x D/2 u8 | gu_s 2I x D/64 f16 | gu_m | dn_q D x I/2 | dn_s D x I/64 f16 | dn_m],
+ * gate rows first in gu; w = code * scale + min, the even element in the low nibble
+ * (q4_dequantize, :463-469). D % 64 == 0, I % 64 == 0, E <= 1024, K <= 16.
+ * ------------------------------------------------------------------------------------- */
+/* router_topk, hybrid.cu:317-362 (MoE.route, hybrid.py:637-641): logits = h W^T with W bf16
+ * [E, D]; p = softmax(logits) in fp32; idx [T, K] = the K largest in descending order (ties to
+ * the lower expert); wts [T, K] = p / sum of the picked p. */
+int aegist_router_topk(const float* h, const uint16_t* W, int* idx, float* wts, int T, int D, int E, int K,
+                       void* stream);
+/* Workspace (device bytes) of aegist_moe_experts for up to T tokens. */
+size_t aegist_moe_workspace_bytes(int T, int K, int D, int I, int E);
+/* The routed experts (ExpertBank.forward, hybrid.py:608-628) added into the residual:
+ * x[t] += sum_k wts[t, k] * W_dn (silu(W_g h[t]) * (W_u h[t])) with the weights of expert
+ * idx[t, k], and, when ysh is not NULL, + sigmoid(h[t] . wg) * ysh[t] (the gated shared expert,
+ * ysh [T, D] its output, wg bf16 [D]). eptr: device array of E expert-row addresses (any
+ * placement: one contiguous [E, row] array, or pooled slots). Replaces the engine's host
+ * grouping (hybrid.rs:875-913, here on the device: no host sync) and moe_gu_gemv / gemm,
+ * moe_dn_gemv / gemm, moe_reduce (hybrid.cu:386-567). Picks with an expert id outside [0, E)
+ * add nothing. */
+int aegist_moe_experts(const float* h, const unsigned long long* eptr, const int* idx, const float* wts, float* x,
+                       int T, int D, int I, int E, int K, const float* ysh, const uint16_t* wg, void* ws,
+                       size_t ws_bytes, void* stream);
+/* shared_gate_add, hybrid.cu:569-577: x[t] += sigmoid(h[t] . wg) * y[t] */
+int aegist_shared_gate_add(float* x, const float* y, const float* h, const uint16_t* wg, int T, int D, void* stream);
+/* silu_mul, aegist.cu:174-178: out = silu(g) * u over n elements (the shared expert's SwiGLU) */
+int aegist_silu_mul(const float* g, const float* u, float* out, long long n, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -377,6 +377,106 @@ def qlinear_torch(x: torch.Tensor, q: torch.Tensor, scale: torch.Tensor) -> torc
     return F.linear(x, w)
 
 
+# --- mixture of experts (hybrid.py:424-652; engine hybrid.cu:313-577) ------------------------
+# Computed in fp64 from the exact stored values (fp32 activations, bf16 router, f16 scales).
+
+def q4_dequantize(packed: torch.Tensor, scale: torch.Tensor, mn: torch.Tensor, group: int = 64) -> torch.Tensor:
+    """hybrid.py:463-469: two 4-bit codes per byte, the even element in the low nibble;
+    w = code * scale + min per `group` consecutive inputs. Returns fp64 [..., 2 * packed.shape[-1]]."""
+    lo = (packed & 0xF).double()
+    hi = (packed >> 4).double()
+    code = torch.stack([lo, hi], -1).flatten(-2)
+    *lead, n = code.shape
+    code = code.view(*lead, n // group, group)
+    return (code * scale.double().unsqueeze(-1) + mn.double().unsqueeze(-1)).reshape(*lead, n)
+
+
+def expert_layout(D: int, I: int, group: int = 64):
+    """hybrid.py:472-482: the sections of one 4-bit expert row, in order: (name, shape, dtype)."""
+    return [("gu_q", (2 * I, D // 2), torch.uint8), ("gu_s", (2 * I, D // group), torch.float16),
+            ("gu_m", (2 * I, D // group), torch.float16), ("dn_q", (D, I // 2), torch.uint8),
+            ("dn_s", (D, I // group), torch.float16), ("dn_m", (D, I // group), torch.float16)]
+
+
+def expert_row_bytes(D: int, I: int, group: int = 64) -> int:
+    """hybrid.py:485-487: the section bytes, rounded up to 64."""
+    n = sum(math.prod(shape) * torch.tensor([], dtype=dt).element_size() for _, shape, dt in expert_layout(D, I, group))
+    return -(-n // 64) * 64
+
+
+def pack_codes(codes: torch.Tensor) -> torch.Tensor:
+    """uint8 codes [..., n] in 0..15 -> [..., n / 2], the even element in the low nibble (hybrid.py:460)."""
+    c = codes.to(torch.uint8)
+    return c[..., 0::2] | (c[..., 1::2] << 4)
+
+
+def pack_expert(gu_codes, gu_s, gu_m, dn_codes, dn_s, dn_m) -> torch.Tensor:
+    """One expert row (uint8 [expert_row_bytes]) from codes [2I, D] / [D, I] and f16 scales and mins."""
+    D = gu_codes.shape[1]
+    I = dn_codes.shape[1]
+    parts = [pack_codes(gu_codes), gu_s.half(), gu_m.half(), pack_codes(dn_codes), dn_s.half(), dn_m.half()]
+    row = torch.cat([p.contiguous().view(torch.uint8).reshape(-1) for p in parts])
+    return F.pad(row, (0, expert_row_bytes(D, I) - row.numel()))
+
+
+def unpack_expert(row: torch.Tensor, D: int, I: int, group: int = 64):
+    """hybrid.py:536-548 (4-bit branch): one row -> (gate_up [2I, D], down [D, I]) in fp64."""
+    out, off = {}, 0
+    for name, shape, dt in expert_layout(D, I, group):
+        nb = math.prod(shape) * torch.tensor([], dtype=dt).element_size()
+        out[name] = row[off:off + nb].view(dt).view(shape)
+        off += nb
+    return (q4_dequantize(out["gu_q"], out["gu_s"], out["gu_m"], group),
+            q4_dequantize(out["dn_q"], out["dn_s"], out["dn_m"], group))
+
+
+def route(h: torch.Tensor, W: torch.Tensor, K: int):
+    """MoE.route (hybrid.py:637-641) with the engine's tie rule (equal probabilities: the lower
+    expert first, hybrid.cu:30-39): p = softmax(h W^T), the K largest in descending order,
+    weights p / sum(top p). h fp32 [T, D], W bf16 [E, D]. Returns (idx int64 [T, K], wts fp64)."""
+    logits = h.double() @ W.double().t()
+    p = torch.softmax(logits, -1)
+    order = torch.sort(-p, dim=-1, stable=True).indices[:, :K]
+    top = torch.gather(p, 1, order)
+    return order, top / top.sum(-1, keepdim=True)
+
+
+def expert_ffn(x: torch.Tensor, gu: torch.Tensor, dn: torch.Tensor) -> torch.Tensor:
+    """One SwiGLU expert (hybrid.py:624-626): gate | up = x gu^T; down(silu(gate) * up). fp64."""
+    gate, up = (x.double() @ gu.t()).chunk(2, -1)
+    return (F.silu(gate) * up) @ dn.t()
+
+
+def moe_experts(h: torch.Tensor, rows: torch.Tensor, idx: torch.Tensor, wts: torch.Tensor, D: int, I: int):
+    """ExpertBank.forward (hybrid.py:608-628): out[t] = sum_k wts[t, k] * expert_idx[t,k](h[t]).
+    rows: uint8 [E, row_bytes]. Picks with an id outside [0, E) add nothing. fp64 [T, D]."""
+    out = torch.zeros(h.shape[0], D, dtype=torch.float64)
+    E = rows.shape[0]
+    for e in sorted(set(int(v) for v in idx.reshape(-1).tolist())):
+        if not 0 <= e < E:
+            continue
+        tok, kk = (idx == e).nonzero(as_tuple=True)
+        gu, dn = unpack_expert(rows[e], D, I)
+        out.index_add_(0, tok, expert_ffn(h[tok], gu, dn) * wts[tok, kk].double().unsqueeze(-1))
+    return out
+
+
+def swiglu(x: torch.Tensor, wg: torch.Tensor, wu: torch.Tensor, wd: torch.Tensor) -> torch.Tensor:
+    """SwiGLU (model.py:188-196): down(silu(gate x) * up x), fp64 from the given weights."""
+    x = x.double()
+    return (F.silu(x @ wg.double().t()) * (x @ wu.double().t())) @ wd.double().t()
+
+
+def moe_forward(h, router_w, rows, D: int, I: int, K: int, ysh=None, shared_gate=None):
+    """MoE.forward (hybrid.py:647-652): routed experts + sigmoid(h . shared_gate) * shared(h).
+    ysh: the shared expert's output [T, D] (or None). Returns (out fp64 [T, D], idx, wts)."""
+    idx, wts = route(h, router_w, K)
+    out = moe_experts(h, rows, idx, wts, D, I)
+    if ysh is not None:
+        out = out + torch.sigmoid(h.double() @ shared_gate.double()).unsqueeze(-1) * ysh.double()
+    return out, idx, wts
+
+
 # --- composites: the mixers and the layer stack (config 4) ---------------------------------
 
 def _lin(x, w, round_in: bool):

@@ -381,3 +381,110 @@ def test_gated_norm_sigmoid_gate_closed_form():
     rms = torch.sqrt((o.double() ** 2).mean(-1, keepdim=True) + 1e-6)
     want = w.double() * (o.double() / rms) / (1 + torch.exp(-z.double()))
     assert torch.allclose(R.gated_norm(o, z, w, act="sigmoid").double(), want, atol=1e-6)
+
+
+# --- mixture of experts -----------------------------------------------------------------------
+
+def test_q4_dequantize_known_answers():
+    # byte 0x21 holds codes (1, 2): the even element in the low nibble; 0xF0 holds (0, 15)
+    packed = torch.zeros(1, 32, dtype=torch.uint8)
+    packed[0, 0], packed[0, 1] = 0x21, 0xF0
+    scale = torch.tensor([[0.5]], dtype=torch.float16)
+    mn = torch.tensor([[-1.0]], dtype=torch.float16)
+    w = R.q4_dequantize(packed, scale, mn, 64)
+    assert w.shape == (1, 64)
+    assert w[0, :4].tolist() == [-0.5, 0.0, -1.0, 6.5]
+    assert torch.all(w[0, 4:] == -1.0)
+
+
+def test_expert_row_layout_by_hand():
+    # D = 128, I = 64, group 64: place single codes by hand-computed byte offsets and read them
+    # back through unpack_expert (gate rows first, then up rows, then the down matrix)
+    D, I = 128, 64
+    gu_q, gu_s = 2 * I * D // 2, 2 * I * (D // 64) * 2
+    dn_q, dn_s = D * I // 2, D * (I // 64) * 2
+    assert R.expert_row_bytes(D, I) == -(-(gu_q + 2 * gu_s + dn_q + 2 * dn_s) // 64) * 64
+    row = torch.zeros(R.expert_row_bytes(D, I), dtype=torch.uint8)
+    one = torch.tensor([1.0], dtype=torch.float16).view(torch.uint8)  # f16 1.0 = bytes 00 3c
+    row[gu_q:gu_q + gu_s].view(torch.float16)[:] = 1.0     # every gate/up scale 1, min 0
+    row[gu_q + 2 * gu_s + dn_q:gu_q + 2 * gu_s + dn_q + dn_s].view(torch.float16)[:] = 1.0
+    row[(I + 5) * (D // 2) + 7] = 0x30                     # up row 5, input 15 -> code 3
+    row[gu_q + 2 * gu_s + 9 * (I // 2) + 2] = 0x07         # down row 9, input 4 -> code 7
+    assert one.tolist() == [0, 60]
+    gu, dn = R.unpack_expert(row, D, I)
+    nz = gu.nonzero().tolist()
+    assert nz == [[I + 5, 15]] and gu[I + 5, 15] == 3.0
+    assert dn.nonzero().tolist() == [[9, 4]] and dn[9, 4] == 7.0
+
+
+def test_route_ties_and_brute_force():
+    # equal logits: the lower experts first, equal weights
+    h = torch.ones(2, 8)
+    W = torch.ones(6, 8, dtype=torch.bfloat16)
+    idx, wts = R.route(h, W, 3)
+    assert idx.tolist() == [[0, 1, 2], [0, 1, 2]]
+    assert torch.allclose(wts, torch.full((2, 3), 1 / 3, dtype=torch.float64))
+    g = torch.Generator().manual_seed(7)
+    h = torch.randn(5, 16, generator=g)
+    W = torch.randn(12, 16, generator=g).bfloat16()
+    idx, wts = R.route(h, W, 4)
+    for t in range(5):
+        lg = [sum(float(h[t, d]) * float(W[e, d]) for d in range(16)) for e in range(12)]
+        m = max(lg)
+        p = [math.exp(v - m) for v in lg]
+        p = [v / sum(p) for v in p]
+        best = sorted(range(12), key=lambda e: (-p[e], e))[:4]
+        assert idx[t].tolist() == best
+        s = sum(p[e] for e in best)
+        assert all(abs(float(wts[t, i]) - p[e] / s) < 1e-12 for i, e in enumerate(best))
+
+
+def test_expert_ffn_and_bank_brute_force():
+    g = torch.Generator().manual_seed(8)
+    D, I, E = 64, 64, 3
+    rows = []
+    for _ in range(E):
+        rows.append(R.pack_expert(torch.randint(0, 16, (2 * I, D), generator=g),
+                                  (torch.rand(2 * I, 1, generator=g) * 0.01).half(),
+                                  (-torch.rand(2 * I, 1, generator=g) * 0.05).half(),
+                                  torch.randint(0, 16, (D, I), generator=g),
+                                  (torch.rand(D, 1, generator=g) * 0.01).half(),
+                                  (-torch.rand(D, 1, generator=g) * 0.05).half()))
+    rows = torch.stack(rows)
+    h = torch.randn(4, D, generator=g)
+    idx = torch.tensor([[0, 2], [1, 1], [2, 0], [9, 1]])  # expert 9 is out of range: adds nothing
+    wts = torch.tensor([[0.75, 0.25], [0.5, 0.5], [0.9, 0.1], [0.3, 0.7]])
+    got = R.moe_experts(h, rows, idx, wts, D, I)
+    for t in range(4):
+        want = [0.0] * D
+        for k in range(2):
+            e = int(idx[t, k])
+            if e >= E:
+                continue
+            gu, dn = R.unpack_expert(rows[e], D, I)
+            a = []
+            for r in range(I):
+                gate = sum(float(gu[r, c]) * float(h[t, c]) for c in range(D))
+                up = sum(float(gu[I + r, c]) * float(h[t, c]) for c in range(D))
+                a.append(gate / (1 + math.exp(-gate)) * up)
+            for o in range(D):
+                want[o] += float(wts[t, k]) * sum(float(dn[o, r]) * a[r] for r in range(I))
+        assert torch.allclose(got[t], torch.tensor(want, dtype=torch.float64), rtol=1e-9, atol=1e-9)
+
+
+def test_moe_forward_shared_gate():
+    g = torch.Generator().manual_seed(9)
+    D, I, E = 64, 64, 4
+    rows = torch.stack([R.pack_expert(torch.randint(0, 16, (2 * I, D), generator=g), torch.full((2 * I, 1), 0.01),
+                                      torch.full((2 * I, 1), -0.05), torch.randint(0, 16, (D, I), generator=g),
+                                      torch.full((D, 1), 0.01), torch.full((D, 1), -0.05)) for _ in range(E)])
+    h = torch.randn(3, D, generator=g)
+    W = torch.randn(E, D, generator=g).bfloat16()
+    ysh = torch.randn(3, D, generator=g)
+    wg = torch.randn(D, generator=g).bfloat16()
+    out, idx, wts = R.moe_forward(h, W, rows, D, I, 2, ysh=ysh, shared_gate=wg)
+    routed = R.moe_experts(h, rows, idx, wts, D, I)
+    for t in range(3):
+        s = sum(float(h[t, d]) * float(wg[d]) for d in range(D))
+        gate = 1 / (1 + math.exp(-s))
+        assert torch.allclose(out[t], routed[t] + gate * ysh[t].double(), atol=1e-12)
