@@ -27,6 +27,11 @@
 
 #include <algorithm>
 
+namespace aegist {
+int launch_proj(const void* X, int x_dtype, long long ldx, const void* W, int w_dtype, const uint16_t* scale, float* Y,
+                long long ldy, int M, int N, int K, int accumulate, hipStream_t st);
+}  // namespace aegist
+
 using namespace aegist;
 
 namespace {
@@ -34,7 +39,6 @@ namespace {
 constexpr int PB = 32;            // picks per expert tile (two 16-column MFMA tiles)
 constexpr int RB = 64;            // output rows per workgroup (4 waves x 16)
 constexpr int MAX_E = 1024;       // experts per layer the grouping kernel handles
-constexpr int RT = 4;             // tokens per router workgroup
 
 struct ExpertOffsets {            // byte offsets inside one expert row (expert_layout)
     long long gu_s, gu_m, dn_q, dn_s, dn_m;
@@ -52,99 +56,75 @@ static ExpertOffsets expert_offsets(int D, int I) {
 __device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
 
 // ---------------------------------------------------------------------------------------------
-// Router: RT tokens per workgroup of E threads (lane = expert, E <= 256 by launch: 256 threads
-// cover up to 256 experts; more experts loop). x rows in LDS (broadcast reads); W rows bf16.
-__global__ void __launch_bounds__(256) router_topk_kernel(const float* __restrict__ h, const uint16_t* __restrict__ W,
-                                                          int* __restrict__ idx, float* __restrict__ wts, int T, int D,
-                                                          int E, int K) {
-    extern __shared__ float sm[];
-    float* xs = sm;                     // [RT][D]
-    float* lg = sm + RT * D;            // [RT][E]
-    const int t0 = blockIdx.x * RT, tid = threadIdx.x;
-    const int nt = min(RT, T - t0);
-    for (int i = tid; i < RT * D; i += blockDim.x) {
-        const int r = i / D;
-        xs[i] = r < nt ? h[(size_t)(t0 + r) * D + (i % D)] : 0.f;
+// Router top-K over precomputed logits [T, E] (the projection kernel computes h W^T): one wave
+// per token, lane holds the probabilities of experts lane + 64 i in registers; softmax in fp32;
+// K rounds of a wave argmax that prefers the lower expert on equal probabilities.
+template <int NPER>  // experts per lane held in registers (E <= 64 NPER)
+__global__ void __launch_bounds__(256) router_topk_kernel(const float* __restrict__ logits, int* __restrict__ idx,
+                                                          float* __restrict__ wts, int T, int E, int K) {
+    const int lane = threadIdx.x % WAVE, t = blockIdx.x * (blockDim.x / WAVE) + threadIdx.x / WAVE;
+    if (t >= T) return;
+    const float* l = logits + (size_t)t * E;
+    float p[NPER];
+    float m = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < NPER; i++) {
+        const int e = lane + WAVE * i;
+        p[i] = e < E ? l[e] : -INFINITY;
+        m = fmaxf(m, p[i]);
     }
-    __syncthreads();
-    for (int e = tid; e < E; e += blockDim.x) {
-        const uint4* row = (const uint4*)(W + (size_t)e * D);
-        float acc[RT];
+    m = wave_max(m);
+    float s = 0.f;
 #pragma unroll
-        for (int r = 0; r < RT; r++) acc[r] = 0.f;
-        for (int c = 0; c < D / 8; c++) {
-            const uint4 p = row[c];
-            const float w[8] = {bf_lo(p.x), bf_hi(p.x), bf_lo(p.y), bf_hi(p.y),
-                                bf_lo(p.z), bf_hi(p.z), bf_lo(p.w), bf_hi(p.w)};
-#pragma unroll
-            for (int r = 0; r < RT; r++) {
-                const float4 a = *(const float4*)&xs[r * D + 8 * c], b = *(const float4*)&xs[r * D + 8 * c + 4];
-                acc[r] += a.x * w[0] + a.y * w[1] + a.z * w[2] + a.w * w[3] + b.x * w[4] + b.y * w[5] + b.z * w[6] +
-                          b.w * w[7];
-            }
-        }
-#pragma unroll
-        for (int r = 0; r < RT; r++) lg[r * E + e] = acc[r];
+    for (int i = 0; i < NPER; i++) {
+        p[i] = lane + WAVE * i < E ? expf(p[i] - m) : 0.f;
+        s += p[i];
     }
-    __syncthreads();
-    // softmax + top-K: wave w takes tokens w, w + 4, ...; lane holds experts lane + 64 i
-    const int wave = tid / WAVE, lane = tid % WAVE, nw = blockDim.x / WAVE;
-    for (int r = wave; r < nt; r += nw) {
-        const float* l = lg + r * E;
-        float m = -INFINITY;
-        for (int e = lane; e < E; e += WAVE) m = fmaxf(m, l[e]);
-        m = wave_max(m);
-        float s = 0.f;
-        for (int e = lane; e < E; e += WAVE) s += expf(l[e] - m);
-        s = wave_sum(s);
-        float sel = 0.f;                 // sum of the picked probabilities
-        int taken_lo = 0, taken_hi = 0;  // picked slots among this lane's experts e = lane + 64 i
-        float myv = 0.f;                 // lane k keeps pick k
-        int mye = 0;
-        for (int k = 0; k < K; k++) {
-            // this lane's best remaining expert (lowest index on ties: experts visited in order)
-            float bv = -1.f;
-            int bi = 0x7fffffff;
-            for (int i = 0, e = lane; e < E; i++, e += WAVE) {
-                const bool taken = i < 32 ? (taken_lo >> i) & 1 : (taken_hi >> (i - 32)) & 1;
-                const float p = expf(l[e] - m) / s;
-                if (!taken && p > bv) {
-                    bv = p;
-                    bi = e;
-                }
+    s = wave_sum(s);
+#pragma unroll
+    for (int i = 0; i < NPER; i++) p[i] = lane + WAVE * i < E ? p[i] / s : -1.f;  // -1: not an expert
+    float sel = 0.f;  // sum of the picked probabilities
+    float myv = 0.f;  // lane k keeps pick k
+    int mye = 0;
+    for (int k = 0; k < K; k++) {
+        float bv = -1.f;
+        int bi = 0x7fffffff;
+#pragma unroll
+        for (int i = 0; i < NPER; i++)  // experts in increasing order: the first of equals wins
+            if (p[i] > bv) {
+                bv = p[i];
+                bi = lane + WAVE * i;
             }
 #pragma unroll
-            for (int o = 32; o > 0; o >>= 1) {
-                const float v2 = __shfl_xor(bv, o, WAVE);
-                const int i2 = __shfl_xor(bi, o, WAVE);
-                if (v2 > bv || (v2 == bv && i2 < bi)) {
-                    bv = v2;
-                    bi = i2;
-                }
+        for (int o = 32; o > 0; o >>= 1) {
+            const float v2 = __shfl_xor(bv, o, WAVE);
+            const int i2 = __shfl_xor(bi, o, WAVE);
+            if (v2 > bv || (v2 == bv && i2 < bi)) {
+                bv = v2;
+                bi = i2;
             }
-            if ((bi % WAVE) == lane) {
-                const int i = bi / WAVE;
-                if (i < 32) taken_lo |= 1 << i;
-                else taken_hi |= 1 << (i - 32);
-            }
-            if (lane == k) {
-                myv = bv;
-                mye = bi;
-            }
-            sel += bv;
         }
-        if (lane < K) {
-            idx[(size_t)(t0 + r) * K + lane] = mye;
-            wts[(size_t)(t0 + r) * K + lane] = myv / sel;
+#pragma unroll
+        for (int i = 0; i < NPER; i++)
+            if (bi == lane + WAVE * i) p[i] = -2.f;  // taken
+        if (lane == k) {
+            myv = bv;
+            mye = bi;
         }
+        sel += bv;
+    }
+    if (lane < K) {
+        idx[(size_t)t * K + lane] = mye;
+        wts[(size_t)t * K + lane] = myv / sel;
     }
 }
 
 // ---------------------------------------------------------------------------------------------
 // Grouping (one workgroup of 1024 threads): picks i = t K + k with expert idx[i]; out of range
 // experts are dropped and counted. eoff[E + 1]: exclusive prefix of the counts; ptok / psrc:
-// token and pick index of each grouped position; tiles: (expert, p0, p1) blocks of <= PB
-// positions; meta[0] = tile count, meta[1] = dropped picks. The order of positions inside an
+// token and pick index of each grouped position. An expert's positions are cut into blocks of
+// PB; blocks of <= 16 positions go to tiles1 (meta[0] of them), larger ones to tiles2
+// (meta[2]), as (expert, p0, p1). meta[1] = dropped picks. The order of positions inside an
 // expert is unspecified (atomics); no result depends on it.
 __device__ __forceinline__ int block_excl_scan(int v, int* wsum, int* total) {
     const int lane = threadIdx.x % WAVE, w = threadIdx.x / WAVE, nw = blockDim.x / WAVE;
@@ -168,8 +148,8 @@ __device__ __forceinline__ int block_excl_scan(int v, int* wsum, int* total) {
 
 __global__ void __launch_bounds__(1024) moe_group_kernel(const int* __restrict__ idx, int N, int K, int E,
                                                          int* __restrict__ eoff, int* __restrict__ ptok,
-                                                         int* __restrict__ psrc, int4* __restrict__ tiles,
-                                                         int* __restrict__ meta) {
+                                                         int* __restrict__ psrc, int4* __restrict__ tiles1,
+                                                         int4* __restrict__ tiles2, int* __restrict__ meta) {
     __shared__ int cnt[MAX_E], cur[MAX_E], wsum[16], bad;
     const int tid = threadIdx.x;
     for (int e = tid; e < MAX_E; e += blockDim.x) cnt[e] = 0;
@@ -181,19 +161,24 @@ __global__ void __launch_bounds__(1024) moe_group_kernel(const int* __restrict__
         else atomicAdd(&bad, 1);
     }
     __syncthreads();
-    const int c = tid < E ? cnt[tid] : 0, ntl = (c + PB - 1) / PB;
-    int tot_c, tot_t;
+    const int c = tid < E ? cnt[tid] : 0, rem = c % PB;
+    const int small = rem > 0 && rem <= 16 ? 1 : 0;      // the last block, if it is small
+    const int big = c / PB + (rem > 16 ? 1 : 0);         // full blocks and a large last block
+    int tot_c, tot_1, tot_2;
     const int off = block_excl_scan(c, wsum, &tot_c);
-    const int toff = block_excl_scan(ntl, wsum, &tot_t);
+    const int off1 = block_excl_scan(small, wsum, &tot_1);
+    const int off2 = block_excl_scan(big, wsum, &tot_2);
     if (tid < E) {
         eoff[tid] = off;
         cur[tid] = off;
-        for (int j = 0; j < ntl; j++) tiles[toff + j] = int4{tid, off + j * PB, off + min(c, (j + 1) * PB), 0};
+        for (int j = 0; j < big; j++) tiles2[off2 + j] = int4{tid, off + j * PB, off + min(c, (j + 1) * PB), 0};
+        if (small) tiles1[off1] = int4{tid, off + c - rem, off + c, 0};
     }
     if (tid == 0) {
         eoff[E] = tot_c;
-        meta[0] = tot_t;
+        meta[0] = tot_1;
         meta[1] = bad;
+        meta[2] = tot_2;
     }
     __syncthreads();
     for (int i = tid; i < N; i += blockDim.x) {
@@ -266,94 +251,201 @@ __device__ __forceinline__ f32x4 mfma_bf(bf16x8 a, bf16x8 b, f32x4 c) {
 }
 
 // ---------------------------------------------------------------------------------------------
-// One expert matrix block (NM = 1 or 2 matrices sharing the activations) times a tile of <= PB
-// picks: wave w owns rows rowA[m] + 16 w + (0..15) of matrix m; lane (n, g) accumulates rows
-// 4g + j (j < 4) for picks 16 t + n (t < 2). Scale / min (as s and m - 128 s) for the block's
-// rows are staged in LDS; the activation group sums per pick too.
-template <int NM>
+// One expert matrix block (NM = 1 or 2 matrices sharing the activations; RB = 64 rows each)
+// times a tile of <= 16 NT picks. The 64-groups are split over the 4 waves (wave w takes
+// groups w, w + 4, ...), so each activation fragment is read once per workgroup; every wave
+// covers all 64 rows as 4 row tiles and the waves' partial sums are added in LDS afterwards.
+// Lane (n, g) accumulates rows 16 rt + 4g + j (j < 4) for picks 16 t + n. Per 64-group a lane
+// holds the 16 codes [64 grp + 16 g, +16) of its row (one 8-byte load): dword ks feeds the
+// MFMA of step ks, so each MFMA's 32 codes (8 per lane group) lie in one group; the
+// activations are read at the same k. Codes stream through a register ring (the HBM stream),
+// activations through a 2-slot ring.
+constexpr int RTL = RB / 16;  // row tiles per wave
+
+template <int NM, int NT>
 struct BlockAcc {
-    f32x4 acc[NM][2];
+    f32x4 acc[NM][RTL][NT];
 };
 
-// sc: NM tables of [RB][ngroups] (s, m - 128 s); gs: [PB][ngroups] activation group sums.
-template <int NM>
+template <int NM, int NT>
 __device__ __forceinline__ void expert_block(const unsigned char* __restrict__ qbase, const long long* qrow0, int Kdim,
                                              const float2* sc, const uint16_t* __restrict__ xh,
                                              const uint16_t* __restrict__ xl, const long long* xrow, const float* gs,
-                                             BlockAcc<NM>& out, int ngroups) {
+                                             BlockAcc<NM, NT>& out, int ngroups) {
+    // groups of codes in flight per lane (per row tile and matrix): two for decode-sized tiles,
+    // where the weight stream is the whole cost; one for two pick tiles (register budget)
+    constexpr int PD = NT == 1 ? 2 : 1;
     const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE, n = lane % 16, g = lane / 16;
 #pragma unroll
     for (int m = 0; m < NM; m++)
 #pragma unroll
-        for (int t = 0; t < 2; t++) out.acc[m][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int rt = 0; rt < RTL; rt++)
+#pragma unroll
+            for (int t = 0; t < NT; t++) out.acc[m][rt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const int nmine = ngroups > wave ? (ngroups - wave + 3) / 4 : 0;  // this wave's groups
+    if (nmine == 0) return;
     const size_t rowbytes = Kdim / 2;
-    // A operand rows: matrix m, row qrow0[m] + 16 wave + n
     const unsigned char* arow[NM];
 #pragma unroll
-    for (int m = 0; m < NM; m++) arow[m] = qbase + (size_t)(qrow0[m] + 16 * wave + n) * rowbytes;
-    for (int grp = 0; grp < ngroups; grp++) {
-        f32x4 P[NM][2];
+    for (int m = 0; m < NM; m++) arow[m] = qbase + (size_t)(qrow0[m] + n) * rowbytes + 8 * g;
+    auto gaddr = [&](int i) { return 32 * (wave + 4 * min(i, nmine - 1)); };  // byte offset of my i-th group
+    typedef uint32_t u2v __attribute__((ext_vector_type(2)));
+    u2v ar[NM][RTL][PD];
+#pragma unroll
+    for (int u = 0; u < PD; u++)
 #pragma unroll
         for (int m = 0; m < NM; m++)
 #pragma unroll
-            for (int t = 0; t < 2; t++) P[m][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int ks = 0; ks < 2; ks++) {
-            const int k0 = 64 * grp + 32 * ks + 8 * g;
-            bf16x8 bh[2], bl[2];
-#pragma unroll
-            for (int t = 0; t < 2; t++) {
-                bh[t] = ld_bf8(xh + xrow[t] + k0);
-                bl[t] = ld_bf8(xl + xrow[t] + k0);
-            }
-#pragma unroll
-            for (int m = 0; m < NM; m++) {
-                const bf16x8 a = codes_bf16(*(const uint32_t*)(arow[m] + k0 / 2));
-#pragma unroll
-                for (int t = 0; t < 2; t++) {
-                    P[m][t] = mfma_bf(a, bh[t], P[m][t]);
-                    P[m][t] = mfma_bf(a, bl[t], P[m][t]);
-                }
-            }
+            for (int rt = 0; rt < RTL; rt++) ar[m][rt][u] = *(const u2v*)(arow[m] + 16 * rt * rowbytes + gaddr(u));
+    constexpr int NB = NT == 1 ? 2 : 1;  // activation slots (prefetched a group ahead for one tile)
+    bf16x8 bh[NB][NT][2], bl[NB][NT][2];  // [slot][tile][ks]
+#define AEG_LOAD_B(slot, grp)                                                  \
+    _Pragma("unroll") for (int t = 0; t < NT; t++)                             \
+        _Pragma("unroll") for (int ks = 0; ks < 2; ks++) {                     \
+            const long long k0 = xrow[t] + 64 * (grp) + 16 * g + 8 * ks;       \
+            bh[slot][t][ks] = ld_bf8(xh + k0);                                 \
+            bl[slot][t][ks] = ld_bf8(xl + k0);                                 \
         }
-        // y += s P + (m - 128 s) X per row (lane rows 4g + j) and pick (lane column n of tile t)
-        const float X0 = gs[n * ngroups + grp], X1 = gs[(16 + n) * ngroups + grp];
+    AEG_LOAD_B(0, wave)
+    for (int i0 = 0; i0 < nmine; i0 += PD) {
 #pragma unroll
-        for (int m = 0; m < NM; m++)
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const float2 sm = sc[(m * RB + 16 * wave + 4 * g + j) * ngroups + grp];
-                out.acc[m][0][j] = fmaf(sm.x, P[m][0][j], fmaf(sm.y, X0, out.acc[m][0][j]));
-                out.acc[m][1][j] = fmaf(sm.x, P[m][1][j], fmaf(sm.y, X1, out.acc[m][1][j]));
+        for (int u = 0; u < PD; u++) {
+            const int i = i0 + u;
+            if (i >= nmine) break;
+            const int grp = wave + 4 * i, slot = NB == 2 ? (u & 1) : 0;
+            if constexpr (NB == 2) {
+                if (i + 1 < nmine) {
+                    AEG_LOAD_B((slot ^ 1), grp + 4)
+                }
+            } else if (i > 0) {
+                AEG_LOAD_B(0, grp)
             }
+            float X[NT];
+#pragma unroll
+            for (int t = 0; t < NT; t++) X[t] = gs[(16 * t + n) * ngroups + grp];
+#pragma unroll
+            for (int m = 0; m < NM; m++)
+#pragma unroll
+                for (int rt = 0; rt < RTL; rt++) {
+                    const u2v a2 = ar[m][rt][u];
+                    // refill this ring slot with my group PD ahead (clamped: static wait counts)
+                    ar[m][rt][u] = *(const u2v*)(arow[m] + 16 * rt * rowbytes + gaddr(i + PD));
+                    f32x4 P[NT];
+#pragma unroll
+                    for (int t = 0; t < NT; t++) P[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int ks = 0; ks < 2; ks++) {
+                        const bf16x8 a = codes_bf16(ks ? a2.y : a2.x);
+#pragma unroll
+                        for (int t = 0; t < NT; t++) {
+                            P[t] = mfma_bf(a, bh[slot][t][ks], P[t]);
+                            P[t] = mfma_bf(a, bl[slot][t][ks], P[t]);
+                        }
+                    }
+                    // y += s P + (m - 128 s) X for this row tile's rows and every pick tile
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        const float2 sm = sc[(m * RB + 16 * rt + 4 * g + j) * ngroups + grp];
+#pragma unroll
+                        for (int t = 0; t < NT; t++)
+                            out.acc[m][rt][t][j] = fmaf(sm.x, P[t][j], fmaf(sm.y, X[t], out.acc[m][rt][t][j]));
+                    }
+                }
+        }
+    }
+#undef AEG_LOAD_B
+}
+
+// Sum the 4 waves' partials of matrix m into red[pick][row] (row < RB), in wave order (the
+// result does not depend on scheduling). red has PB rows of RB + 1 floats.
+template <int NM, int NT>
+__device__ __forceinline__ void reduce_waves(const BlockAcc<NM, NT>& a, int m, float (*red)[RB + 1]) {
+    const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE, n = lane % 16, g = lane / 16;
+    for (int w = 0; w < 4; w++) {
+        if (wave == w) {
+#pragma unroll
+            for (int rt = 0; rt < RTL; rt++)
+#pragma unroll
+                for (int t = 0; t < NT; t++)
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        float& r = red[16 * t + n][16 * rt + 4 * g + j];
+                        r = (w == 0 ? 0.f : r) + a.acc[m][rt][t][j];
+                    }
+        }
+        __syncthreads();
     }
 }
 
-// Stage (s, m - 128 s) of rows [row0, row0 + RB) x groups [0, G) of one matrix into sc[RB][G]
-// (the rows' scale and min entries are contiguous: one pass over RB G values).
+// Stage (s, m - 128 s) of rows [row0, row0 + RB) x groups [0, G) of one matrix into sc[RB][G]:
+// the block's scale and min entries are one contiguous run of RB G halves each, read as 16-byte
+// pieces (8 per load), all loads of a thread issued before any is used.
 __device__ __forceinline__ void stage_scales(float2* sc, const uint16_t* __restrict__ s,
                                              const uint16_t* __restrict__ mn, long long row0, int G) {
-    const size_t k0 = (size_t)row0 * G;
-    for (int i = threadIdx.x; i < RB * G; i += blockDim.x) {
-        const float sv = h2f(s[k0 + i]), mv = h2f(mn[k0 + i]);
-        sc[i] = float2{sv, mv - 128.f * sv};
+    const uint4* s4 = (const uint4*)(s + (size_t)row0 * G);
+    const uint4* m4 = (const uint4*)(mn + (size_t)row0 * G);
+    const int n8 = RB * G / 8;  // 16-byte pieces (RB G is a multiple of 8: G = K / 64, RB = 64)
+    constexpr int MAXP = RB * 64 / 8 / 256;  // pieces per thread at the largest G (64)
+    uint4 sv[MAXP], mv[MAXP];
+#pragma unroll
+    for (int u = 0; u < MAXP; u++) {
+        const int i = threadIdx.x + 256 * u;
+        if (i < n8) {
+            sv[u] = s4[i];
+            mv[u] = m4[i];
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < MAXP; u++) {
+        const int i = threadIdx.x + 256 * u;
+        if (i < n8) {
+            const uint32_t sw[4] = {sv[u].x, sv[u].y, sv[u].z, sv[u].w}, mw[4] = {mv[u].x, mv[u].y, mv[u].z, mv[u].w};
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const float a = h2f((uint16_t)(sw[e / 2] >> (16 * (e & 1)))), b = h2f((uint16_t)(mw[e / 2] >> (16 * (e & 1))));
+                sc[8 * i + e] = float2{a, b - 128.f * a};
+            }
+        }
+    }
+}
+
+// Stage the activation group sums of the tile's picks: gs[pr][c] = src[row(pr) G + c] for
+// pr < PB (rows past the tile repeat its last pick), all loads issued first.
+__device__ __forceinline__ void stage_gsums(float* gs, const float* __restrict__ src, const int* __restrict__ rowmap,
+                                            int p0, int np, int G) {
+    constexpr int MAXP = PB * 64 / 256;
+    float v[MAXP];
+#pragma unroll
+    for (int u = 0; u < MAXP; u++) {
+        const int i = threadIdx.x + 256 * u;
+        if (i < PB * G) {
+            const int pr = i / G, c = i % G, p = p0 + min(pr, np - 1);
+            v[u] = src[(size_t)(rowmap ? rowmap[p] : p) * G + c];
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < MAXP; u++) {
+        const int i = threadIdx.x + 256 * u;
+        if (i < PB * G) gs[i] = v[u];
     }
 }
 
 // Gate / up: block (unit block ub of RB units) x tile. act[p][r] = silu(gate_r . x) * (up_r . x)
 // for the tile's picks, stored as bf16 hi / lo in chunk order (ah, al [P][I]) with group sums
 // as [P][I / 64] (the unit block is one 64-group of the down projection's input).
-__global__ void __launch_bounds__(256) moe_gate_up_kernel(const unsigned long long* __restrict__ eptr,
-                                                          const int4* __restrict__ tiles, const int* __restrict__ meta,
+template <int NT>  // pick tiles of 16: 1 for tiles of <= 16 picks, 2 for larger ones
+__global__ void __launch_bounds__(256, 2) moe_gate_up_kernel(const unsigned long long* __restrict__ eptr,
+                                                          const int4* __restrict__ tiles, const int* __restrict__ ntiles,
                                                           const int* __restrict__ ptok, const uint16_t* __restrict__ xh,
                                                           const uint16_t* __restrict__ xl, const float* __restrict__ xs,
                                                           int D, int I, ExpertOffsets off, uint16_t* __restrict__ ah,
                                                           uint16_t* __restrict__ al, float* __restrict__ as) {
     // dynamic LDS: sc [2][RB][G] (s, m - 128 s) | gs [PB][G] activation group sums
     extern __shared__ float2 dyn[];
-    __shared__ float ob[PB][RB + 1];     // act staging
+    __shared__ float ob[PB][RB + 1];     // gate sums, then act
+    __shared__ float ub2[PB][RB + 1];    // up sums
     const int tile = blockIdx.y, ub = blockIdx.x;
-    if (tile >= meta[0]) return;
+    if (tile >= *ntiles) return;
     const int4 tl = tiles[tile];
     const int e = tl.x, p0 = tl.y, np = tl.z - tl.y;
     const unsigned char* base = (const unsigned char*)eptr[e];
@@ -362,28 +454,22 @@ __global__ void __launch_bounds__(256) moe_gate_up_kernel(const unsigned long lo
     float* gs = (float*)(dyn + 2 * RB * G);
     stage_scales(sc, (const uint16_t*)(base + off.gu_s), (const uint16_t*)(base + off.gu_m), r0, G);
     stage_scales(sc + RB * G, (const uint16_t*)(base + off.gu_s), (const uint16_t*)(base + off.gu_m), I + r0, G);
-    for (int i = threadIdx.x; i < PB * G; i += blockDim.x) {
-        const int pr = i / G, c = i % G;
-        gs[i] = xs[(size_t)ptok[p0 + min(pr, np - 1)] * G + c];
-    }
+    stage_gsums(gs, xs, ptok, p0, np, G);
     __syncthreads();
     const int lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE, n = lane % 16, g = lane / 16;
     long long xrow[2];
 #pragma unroll
     for (int t = 0; t < 2; t++) xrow[t] = (long long)ptok[p0 + min(16 * t + n, np - 1)] * D;
-    const long long qrow0[2] = {r0, I + r0};
-    BlockAcc<2> acc;
-    expert_block<2>(base, qrow0, D, sc, xh, xl, xrow, gs, acc, G);
-#pragma unroll
-    for (int t = 0; t < 2; t++)
-#pragma unroll
-        for (int j = 0; j < 4; j++) ob[16 * t + n][16 * wave + 4 * g + j] = silu_f(acc.acc[0][t][j]) * acc.acc[1][t][j];
-    __syncthreads();
+    const long long qrow0[2] = {r0, I + r0};  // gate rows, up rows of this unit block
+    BlockAcc<2, NT> acc;
+    expert_block<2, NT>(base, qrow0, D, sc, xh, xl, xrow, gs, acc, G);
+    reduce_waves<2, NT>(acc, 0, ob);   // gate sums
+    reduce_waves<2, NT>(acc, 1, ub2);  // up sums
     // 256 threads = 32 picks x 8 chunks of the 64 units
     const int pr = threadIdx.x / 8, q = threadIdx.x % 8;
     float v[8];
 #pragma unroll
-    for (int i = 0; i < 8; i++) v[i] = ob[pr][8 * q + i];
+    for (int i = 0; i < 8; i++) v[i] = silu_f(ob[pr][8 * q + i]) * ub2[pr][8 * q + i];
     uint4 hi, lo;
     float s;
     split8(v, hi, lo, s);
@@ -399,16 +485,18 @@ __global__ void __launch_bounds__(256) moe_gate_up_kernel(const unsigned long lo
 }
 
 // Down: block (output rows [RB ob, RB ob + RB)) x tile. ypick[src][o] = wts[src] * (dn_o . act).
-__global__ void __launch_bounds__(256) moe_down_kernel(const unsigned long long* __restrict__ eptr,
-                                                       const int4* __restrict__ tiles, const int* __restrict__ meta,
+template <int NT>
+__global__ void __launch_bounds__(256, 2) moe_down_kernel(const unsigned long long* __restrict__ eptr,
+                                                       const int4* __restrict__ tiles, const int* __restrict__ ntiles,
                                                        const int* __restrict__ psrc, const float* __restrict__ wts,
                                                        const uint16_t* __restrict__ ah, const uint16_t* __restrict__ al,
                                                        const float* __restrict__ as, int D, int I, ExpertOffsets off,
                                                        float* __restrict__ ypick) {
     // dynamic LDS: sc [RB][G] | gs [PB][G]
     extern __shared__ float2 dyn[];
+    __shared__ float red[PB][RB + 1];  // the waves' summed outputs
     const int tile = blockIdx.y, ob = blockIdx.x;
-    if (tile >= meta[0]) return;
+    if (tile >= *ntiles) return;
     const int4 tl = tiles[tile];
     const int e = tl.x, p0 = tl.y, np = tl.z - tl.y;
     const unsigned char* base = (const unsigned char*)eptr[e];
@@ -416,52 +504,58 @@ __global__ void __launch_bounds__(256) moe_down_kernel(const unsigned long long*
     float2* sc = dyn;
     float* gs = (float*)(dyn + RB * G);
     stage_scales(sc, (const uint16_t*)(base + off.dn_s), (const uint16_t*)(base + off.dn_m), o0, G);
-    for (int i = threadIdx.x; i < PB * G; i += blockDim.x) {
-        const int pr = i / G, c = i % G;
-        gs[i] = as[(size_t)(p0 + min(pr, np - 1)) * G + c];
-    }
+    stage_gsums(gs, as, nullptr, p0, np, G);
     __syncthreads();
     const int lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE, n = lane % 16, g = lane / 16;
     long long xrow[2];
 #pragma unroll
     for (int t = 0; t < 2; t++) xrow[t] = (long long)(p0 + min(16 * t + n, np - 1)) * I;
     const long long qrow0[1] = {o0};
-    BlockAcc<1> acc;
-    expert_block<1>(base + off.dn_q, qrow0, I, sc, ah, al, xrow, gs, acc, G);
-#pragma unroll
-    for (int t = 0; t < 2; t++) {
-        const int pr = 16 * t + n;
-        if (pr >= np) continue;
+    BlockAcc<1, NT> acc;
+    expert_block<1, NT>(base + off.dn_q, qrow0, I, sc, ah, al, xrow, gs, acc, G);
+    reduce_waves<1, NT>(acc, 0, red);
+    // 256 threads = 32 picks x 8 runs of 8 rows: ypick[src][o0 + 8 q ..] = w * y
+    const int pr = threadIdx.x / 8, q = threadIdx.x % 8;
+    if (pr < np) {
         const int src = psrc[p0 + pr];
         const float w = wts[src];
-        const f32x4 y = acc.acc[0][t];
-        *(float4*)(ypick + (size_t)src * D + o0 + 16 * wave + 4 * g) = float4{w * y[0], w * y[1], w * y[2], w * y[3]};
+        float* dst = ypick + (size_t)src * D + o0 + 8 * q;
+        const float* r = &red[pr][8 * q];
+        ((float4*)dst)[0] = float4{w * r[0], w * r[1], w * r[2], w * r[3]};
+        ((float4*)dst)[1] = float4{w * r[4], w * r[5], w * r[6], w * r[7]};
     }
 }
 
 // x[t] += sum_k ypick[t K + k] (k in order) and, with a shared expert, + sigmoid(h_t . wg) ysh[t].
+// Grid (T, D / 256): one thread per column; the K pick rows are loaded together.
 __global__ void __launch_bounds__(256) moe_combine_kernel(float* __restrict__ x, const float* __restrict__ ypick,
                                                           const int* __restrict__ idx, int E,
                                                           const float* __restrict__ ysh, const float* __restrict__ h,
                                                           const uint16_t* __restrict__ wg, int D, int K) {
     __shared__ float red[8];
-    const int t = blockIdx.x;
+    const int t = blockIdx.x, i = blockIdx.y * blockDim.x + threadIdx.x;
     float gate = 0.f;
     if (ysh) {
         float a = 0.f;
-        for (int i = threadIdx.x; i < D; i += blockDim.x) a += h[(size_t)t * D + i] * bf2f(wg[i]);
+        for (int c = threadIdx.x; c < D; c += blockDim.x) a += h[(size_t)t * D + c] * bf2f(wg[c]);
         gate = sigmoid_f(block_sum(a, red));
     }
-    for (int i = threadIdx.x; i < D; i += blockDim.x) {
-        float s = 0.f;
-        for (int k = 0; k < K; k++) {
+    if (i >= D) return;
+    float v[16];
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+        if (k < K) {
             const int e = idx[(size_t)t * K + k];
-            if (e >= 0 && e < E) s += ypick[((size_t)t * K + k) * D + i];
+            v[k] = (e >= 0 && e < E) ? ypick[((size_t)t * K + k) * D + i] : 0.f;
         }
-        float v = x[(size_t)t * D + i] + s;
-        if (ysh) v += gate * ysh[(size_t)t * D + i];
-        x[(size_t)t * D + i] = v;
     }
+    float s = 0.f;
+#pragma unroll
+    for (int k = 0; k < 16; k++)
+        if (k < K) s += v[k];
+    float r = x[(size_t)t * D + i] + s;
+    if (ysh) r += gate * ysh[(size_t)t * D + i];
+    x[(size_t)t * D + i] = r;
 }
 
 // x[t] += sigmoid(h_t . wg) y[t] (the engine's shared_gate_add)
@@ -484,14 +578,16 @@ __global__ void silu_mul_kernel(const float* __restrict__ g, const float* __rest
 
 // Workspace plan of aegist_moe_experts.
 struct MoePlan {
-    size_t xh, xl, xs, ah, al, as, yp, eoff, ptok, psrc, tiles, meta, total;
-    int max_tiles;
+    size_t xh, xl, xs, ah, al, as, yp, eoff, ptok, psrc, tiles1, tiles2, meta, total;
+    int max1, max2;  // tile-list capacities: <= 16 picks (one per expert), larger
 };
 static size_t al256(size_t x) { return (x + 255) / 256 * 256; }
 static MoePlan moe_plan(int T, int K, int D, int I, int E) {
     MoePlan p;
     const size_t N = (size_t)T * K;
-    p.max_tiles = (int)((N + PB - 1) / PB + std::min<size_t>(N, (size_t)E));
+    p.max1 = (int)std::min<size_t>(N, (size_t)E);
+    // an expert with c picks has floor(c / PB) + [c % PB > 16] <= c / 17 large blocks
+    p.max2 = (int)(N / 17);
     size_t o = 0;
     auto take = [&](size_t bytes) {
         const size_t at = o;
@@ -508,7 +604,8 @@ static MoePlan moe_plan(int T, int K, int D, int I, int E) {
     p.eoff = take((size_t)(E + 1) * 4);
     p.ptok = take(N * 4);
     p.psrc = take(N * 4);
-    p.tiles = take((size_t)p.max_tiles * 16);
+    p.tiles1 = take((size_t)p.max1 * 16);
+    p.tiles2 = take((size_t)std::max(p.max2, 1) * 16);
     p.meta = take(16);
     p.total = o;
     return p;
@@ -520,13 +617,23 @@ extern "C" {
 
 int aegist_router_topk(const float* h, const uint16_t* W, int* idx, float* wts, int T, int D, int E, int K,
                        void* stream) {
-    AEG_REQUIRE(T >= 0 && D > 0 && D % 8 == 0, "router_topk: need D % 8 == 0");
+    AEG_REQUIRE(T >= 0 && D > 0 && D % 16 == 0, "router_topk: need D % 16 == 0");
     AEG_REQUIRE(E > 0 && E <= 64 * 64, "router_topk: need 0 < E <= 4096");
     AEG_REQUIRE(K > 0 && K <= 16 && K <= E, "router_topk: need 0 < K <= min(16, E)");
     if (T == 0) return 0;
-    const size_t lds = (size_t)RT * (D + E) * 4;
-    AEG_REQUIRE(lds <= 64 * 1024, "router_topk: RT * (D + E) floats must fit in 64 KiB of LDS");
-    router_topk_kernel<<<(T + RT - 1) / RT, 256, lds, AEG_STREAM(stream)>>>(h, W, idx, wts, T, D, E, K);
+    // logits [T, E] = h W^T on the projection kernel (fp32 h as bf16 hi + lo against the exact
+    // bf16 W), in the library's per-device scratch (stream-ordered reuse)
+    int rc = 0;
+    float* logits = (float*)mirror_workspace((size_t)T * E * 4, &rc);
+    if (rc) return rc;
+    hipStream_t st = AEG_STREAM(stream);
+    rc = launch_proj(h, AEGIST_F32, D, W, AEGIST_BF16, nullptr, logits, E, T, E, D, 0, st);
+    if (rc) return rc;
+    const unsigned grid = (T + 3) / 4;
+    if (E <= 64) router_topk_kernel<1><<<grid, 256, 0, st>>>(logits, idx, wts, T, E, K);
+    else if (E <= 256) router_topk_kernel<4><<<grid, 256, 0, st>>>(logits, idx, wts, T, E, K);
+    else if (E <= 1024) router_topk_kernel<16><<<grid, 256, 0, st>>>(logits, idx, wts, T, E, K);
+    else router_topk_kernel<64><<<grid, 256, 0, st>>>(logits, idx, wts, T, E, K);
     return after_launch("router_topk");
 }
 
@@ -555,7 +662,8 @@ int aegist_moe_experts(const float* h, const unsigned long long* eptr, const int
     int* eoff = (int*)(w + p.eoff);
     int* ptok = (int*)(w + p.ptok);
     int* psrc = (int*)(w + p.psrc);
-    int4* tiles = (int4*)(w + p.tiles);
+    int4* tiles1 = (int4*)(w + p.tiles1);
+    int4* tiles2 = (int4*)(w + p.tiles2);
     int* meta = (int*)(w + p.meta);
     uint16_t* xh = (uint16_t*)(w + p.xh);
     uint16_t* xl = (uint16_t*)(w + p.xl);
@@ -565,7 +673,7 @@ int aegist_moe_experts(const float* h, const unsigned long long* eptr, const int
     float* as = (float*)(w + p.as);
     float* yp = (float*)(w + p.yp);
 
-    moe_group_kernel<<<1, 1024, 0, st>>>(idx, N, K, E, eoff, ptok, psrc, tiles, meta);
+    moe_group_kernel<<<1, 1024, 0, st>>>(idx, N, K, E, eoff, ptok, psrc, tiles1, tiles2, meta);
     int rc = after_launch("moe_group");
     if (rc) return rc;
     const long long nq = (long long)T * (D / 8);
@@ -574,13 +682,25 @@ int aegist_moe_experts(const float* h, const unsigned long long* eptr, const int
     // Picks with an out-of-range expert id are dropped: no tile covers them and the combine
     // skips their rows, so nothing has to be cleared.
     const size_t lds_gu = (size_t)(2 * RB + PB) * (D / 64) * 8, lds_dn = (size_t)(RB + PB) * (I / 64) * 8;
-    moe_gate_up_kernel<<<dim3(I / RB, p.max_tiles), 256, lds_gu, st>>>(eptr, tiles, meta, ptok, xh, xl, xs, D, I, off,
-                                                                       ah, al, as);
+    // two launches per projection: tiles of <= 16 picks (one MFMA column tile, the decode case)
+    // and larger tiles (two); a launch whose list is empty exits at once
+    moe_gate_up_kernel<1><<<dim3(I / RB, p.max1), 256, lds_gu, st>>>(eptr, tiles1, meta, ptok, xh, xl, xs, D, I, off,
+                                                                     ah, al, as);
     if ((rc = after_launch("moe_gate_up"))) return rc;
-    moe_down_kernel<<<dim3(D / RB, p.max_tiles), 256, lds_dn, st>>>(eptr, tiles, meta, psrc, wts, ah, al, as, D, I,
-                                                                    off, yp);
+    if (p.max2 > 0) {
+        moe_gate_up_kernel<2><<<dim3(I / RB, p.max2), 256, lds_gu, st>>>(eptr, tiles2, meta + 2, ptok, xh, xl, xs, D, I,
+                                                                         off, ah, al, as);
+        if ((rc = after_launch("moe_gate_up"))) return rc;
+    }
+    moe_down_kernel<1><<<dim3(D / RB, p.max1), 256, lds_dn, st>>>(eptr, tiles1, meta, psrc, wts, ah, al, as, D, I, off,
+                                                                  yp);
     if ((rc = after_launch("moe_down"))) return rc;
-    moe_combine_kernel<<<T, 256, 0, st>>>(x, yp, idx, E, ysh, h, wg, D, K);
+    if (p.max2 > 0) {
+        moe_down_kernel<2><<<dim3(D / RB, p.max2), 256, lds_dn, st>>>(eptr, tiles2, meta + 2, psrc, wts, ah, al, as, D,
+                                                                      I, off, yp);
+        if ((rc = after_launch("moe_down"))) return rc;
+    }
+    moe_combine_kernel<<<dim3(T, (D + 255) / 256), 256, 0, st>>>(x, yp, idx, E, ysh, h, wg, D, K);
     return after_launch("moe_combine");
 }
 

@@ -237,6 +237,69 @@ def bench_proj(torch, ops, dev, reps=3):
             "points": out}
 
 
+def bench_moe(torch, ops, dev, reps=3):
+    """MoE block after the mixer (hybrid.py:631-652): router top-8 of 256 experts, then the 4-bit
+    SwiGLU experts (D 2048, I 512, 64-groups: 1,769,472 bytes per expert) added into the residual.
+    Decode points stream a ring of 6 layers' experts (2.7 GB, beyond the MALL) and are priced
+    against HBM: bytes = unique experts touched x expert bytes + router weights + activations.
+    The prefill point (T = 2048, one layer) is priced in algorithmic FLOPs, 2 T K (2 I D + D I)."""
+    from aegist_mixer._lib import call, lib
+    E, K, D, I, NL = 256, 8, 2048, 512, 6
+    rb = 1769472
+    gu_q, gu_s = 2 * I * D // 2, 2 * I * (D // 64) * 2
+    dn_q, dn_s = D * I // 2, D * (I // 64) * 2
+    layers = []
+    for li in range(NL):
+        rows = torch.randint(0, 256, (E, rb), dtype=torch.uint8, device=dev)
+        for off, nb, v in ((gu_q, gu_s, 0.005), (gu_q + gu_s, gu_s, -0.03), (gu_q + 2 * gu_s + dn_q, dn_s, 0.005),
+                           (gu_q + 2 * gu_s + dn_q + dn_s, dn_s, -0.03)):
+            rows[:, off:off + nb].view(torch.float16).fill_(v)
+        eptr = torch.arange(E, dtype=torch.int64, device=dev) * rb + rows.data_ptr()
+        W = (torch.randn(E, D, device=dev) * 0.02).to(torch.bfloat16)
+        layers.append((rows, eptr, W))
+    stream = torch.cuda.current_stream().cuda_stream
+    points = []
+    for T in (1, 16, 64, 2048):
+        h = torch.randn(T, D, device=dev)
+        x = torch.zeros(T, D, device=dev)
+        idx = torch.empty(T, K, dtype=torch.int32, device=dev)
+        wts = torch.empty(T, K, device=dev)
+        need = lib().aegist_moe_workspace_bytes(T, K, D, I, E)
+        ws = torch.empty(need, dtype=torch.uint8, device=dev)
+        uniq = []
+
+        def run(li):
+            rows, eptr, W = layers[li]
+            call("aegist_router_topk", h.data_ptr(), W.data_ptr(), idx.data_ptr(), wts.data_ptr(), T, D, E, K, stream)
+            call("aegist_moe_experts", h.data_ptr(), eptr.data_ptr(), idx.data_ptr(), wts.data_ptr(), x.data_ptr(),
+                 T, D, I, E, K, None, None, ws.data_ptr(), need, stream)
+        for li in range(NL):
+            run(li)
+            uniq.append(int(torch.unique(idx).numel()))
+        torch.cuda.synchronize()
+        n = NL * (reps if T < 2048 else 1)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for i in range(n):
+            run(i % NL)
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / n
+        u = sum(uniq) / len(uniq)
+        pt = {"T": T, "us": round(us, 2), "unique_experts": round(u, 1)}
+        if T < 2048:
+            byts = u * rb + E * D * 2 + T * D * 4 * 3
+            pt.update({"GB_s": round(byts / us / 1e3, 1), "hbm_frac": round(byts / us / 1e3 / HBM_PEAK_GBS, 4)})
+        else:
+            tf = 2 * T * K * (2 * I * D + D * I) / (us * 1e-6) / 1e12
+            pt.update({"tflops": round(tf, 2), "mfma_frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4)})
+        points.append(pt)
+        del h, x, idx, wts, ws
+    del layers
+    return {"workload": "MoE block: router top-8 of 256, 4-bit SwiGLU experts D 2048 / I 512 (group 64), residual add",
+            "points": points}
+
+
 def bench_qsa(torch, ops, dev, reps=20):
     """Second core's sparse decode step at long context: one query at position L - 1 with
     L = 131072, R = 4 (32768 blocks), top = 512 (budget 2048), 16 index heads of 128 (an assumed
@@ -346,7 +409,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run a 1 GiB device copy (calibrates rocprof FETCH_SIZE / WRITE_SIZE)")
-    ap.add_argument("--legs", type=str, default="prefill,attention_decode,attention_prefill,proj,qsa,stack",
+    ap.add_argument("--legs", type=str, default="prefill,attention_decode,attention_prefill,proj,qsa,moe,stack",
                     help="comma list of the extra legs to run after the decode headline (default: all); "
                          "'none' for the headline only")
     ap.add_argument("--traffic", type=str, default=str(ROOT / "profiles" / "delta_decode_traffic.json"),
@@ -429,7 +492,7 @@ def main():
             res["roofline"]["traffic"] = json.load(f).get("bytes_per_launch")
     legs = {"prefill": bench_prefill, "attention_decode": bench_attention_decode,
             "attention_prefill": bench_attention_prefill, "proj": bench_proj, "qsa": bench_qsa,
-            "stack": bench_stack}
+            "moe": bench_moe, "stack": bench_stack}
     want = [] if args.legs.strip() == "none" else [x.strip() for x in args.legs.split(",") if x.strip()]
     unknown = [x for x in want if x not in legs]
     if unknown:
