@@ -40,6 +40,11 @@ constexpr int PB = 32;            // picks per expert tile (two 16-column MFMA t
 constexpr int RB = 64;            // output rows per workgroup (4 waves x 16)
 constexpr int MAX_E = 1024;       // experts per layer the grouping kernel handles
 
+struct MoeTile {                  // one block of <= PB grouped picks of one expert
+    unsigned long long base;      // the expert's row address (resolved from the pointer table)
+    int p0, p1;                   // grouped positions [p0, p1)
+};
+
 struct ExpertOffsets {            // byte offsets inside one expert row (expert_layout)
     long long gu_s, gu_m, dn_q, dn_s, dn_m;
 };
@@ -54,6 +59,14 @@ static ExpertOffsets expert_offsets(int D, int I) {
 }
 
 __device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+
+// Loads through expert-row addresses taken from the pointer table: the compiler cannot tell
+// those are global memory and would emit flat loads, which also count against the LDS wait
+// counter (every LDS wait would then drain the prefetched code stream). Global address space.
+template <typename T>
+__device__ __forceinline__ T ld_global(const void* p) {
+    return *(const __attribute__((address_space(1))) T*)p;
+}
 
 // ---------------------------------------------------------------------------------------------
 // Router top-K over precomputed logits [T, E] (the projection kernel computes h W^T): one wave
@@ -147,9 +160,10 @@ __device__ __forceinline__ int block_excl_scan(int v, int* wsum, int* total) {
 }
 
 __global__ void __launch_bounds__(1024) moe_group_kernel(const int* __restrict__ idx, int N, int K, int E,
+                                                         const unsigned long long* __restrict__ eptr,
                                                          int* __restrict__ eoff, int* __restrict__ ptok,
-                                                         int* __restrict__ psrc, int4* __restrict__ tiles1,
-                                                         int4* __restrict__ tiles2, int* __restrict__ meta) {
+                                                         int* __restrict__ psrc, MoeTile* __restrict__ tiles1,
+                                                         MoeTile* __restrict__ tiles2, int* __restrict__ meta) {
     __shared__ int cnt[MAX_E], cur[MAX_E], wsum[16], bad;
     const int tid = threadIdx.x;
     for (int e = tid; e < MAX_E; e += blockDim.x) cnt[e] = 0;
@@ -171,8 +185,9 @@ __global__ void __launch_bounds__(1024) moe_group_kernel(const int* __restrict__
     if (tid < E) {
         eoff[tid] = off;
         cur[tid] = off;
-        for (int j = 0; j < big; j++) tiles2[off2 + j] = int4{tid, off + j * PB, off + min(c, (j + 1) * PB), 0};
-        if (small) tiles1[off1] = int4{tid, off + c - rem, off + c, 0};
+        const unsigned long long base = c > 0 ? eptr[tid] : 0ull;
+        for (int j = 0; j < big; j++) tiles2[off2 + j] = MoeTile{base, off + j * PB, off + min(c, (j + 1) * PB)};
+        if (small) tiles1[off1] = MoeTile{base, off + c - rem, off + c};
     }
     if (tid == 0) {
         eoff[E] = tot_c;
@@ -267,11 +282,13 @@ struct BlockAcc {
     f32x4 acc[NM][RTL][NT];
 };
 
-template <int NM, int NT>
+// `stage` fills sc and gs (LDS); it runs after this wave's first code and activation loads are
+// issued, so its global round trip overlaps theirs, and is followed by the workgroup barrier.
+template <int NM, int NT, typename Stage>
 __device__ __forceinline__ void expert_block(const unsigned char* __restrict__ qbase, const long long* qrow0, int Kdim,
                                              const float2* sc, const uint16_t* __restrict__ xh,
                                              const uint16_t* __restrict__ xl, const long long* xrow, const float* gs,
-                                             BlockAcc<NM, NT>& out, int ngroups) {
+                                             BlockAcc<NM, NT>& out, int ngroups, Stage stage) {
     // groups of codes in flight per lane (per row tile and matrix): two for decode-sized tiles,
     // where the weight stream is the whole cost; one for two pick tiles (register budget)
     constexpr int PD = NT == 1 ? 2 : 1;
@@ -283,7 +300,11 @@ __device__ __forceinline__ void expert_block(const unsigned char* __restrict__ q
 #pragma unroll
             for (int t = 0; t < NT; t++) out.acc[m][rt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
     const int nmine = ngroups > wave ? (ngroups - wave + 3) / 4 : 0;  // this wave's groups
-    if (nmine == 0) return;
+    if (nmine == 0) {
+        stage();
+        __syncthreads();
+        return;
+    }
     const size_t rowbytes = Kdim / 2;
     const unsigned char* arow[NM];
 #pragma unroll
@@ -296,7 +317,7 @@ __device__ __forceinline__ void expert_block(const unsigned char* __restrict__ q
 #pragma unroll
         for (int m = 0; m < NM; m++)
 #pragma unroll
-            for (int rt = 0; rt < RTL; rt++) ar[m][rt][u] = *(const u2v*)(arow[m] + 16 * rt * rowbytes + gaddr(u));
+            for (int rt = 0; rt < RTL; rt++) ar[m][rt][u] = ld_global<u2v>(arow[m] + 16 * rt * rowbytes + gaddr(u));
     constexpr int NB = NT == 1 ? 2 : 1;  // activation slots (prefetched a group ahead for one tile)
     bf16x8 bh[NB][NT][2], bl[NB][NT][2];  // [slot][tile][ks]
 #define AEG_LOAD_B(slot, grp)                                                  \
@@ -307,6 +328,8 @@ __device__ __forceinline__ void expert_block(const unsigned char* __restrict__ q
             bl[slot][t][ks] = ld_bf8(xl + k0);                                 \
         }
     AEG_LOAD_B(0, wave)
+    stage();
+    __syncthreads();
     for (int i0 = 0; i0 < nmine; i0 += PD) {
 #pragma unroll
         for (int u = 0; u < PD; u++) {
@@ -329,7 +352,7 @@ __device__ __forceinline__ void expert_block(const unsigned char* __restrict__ q
                 for (int rt = 0; rt < RTL; rt++) {
                     const u2v a2 = ar[m][rt][u];
                     // refill this ring slot with my group PD ahead (clamped: static wait counts)
-                    ar[m][rt][u] = *(const u2v*)(arow[m] + 16 * rt * rowbytes + gaddr(i + PD));
+                    ar[m][rt][u] = ld_global<u2v>(arow[m] + 16 * rt * rowbytes + gaddr(i + PD));
                     f32x4 P[NT];
 #pragma unroll
                     for (int t = 0; t < NT; t++) P[t] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -382,17 +405,18 @@ __device__ __forceinline__ void reduce_waves(const BlockAcc<NM, NT>& a, int m, f
 // pieces (8 per load), all loads of a thread issued before any is used.
 __device__ __forceinline__ void stage_scales(float2* sc, const uint16_t* __restrict__ s,
                                              const uint16_t* __restrict__ mn, long long row0, int G) {
-    const uint4* s4 = (const uint4*)(s + (size_t)row0 * G);
-    const uint4* m4 = (const uint4*)(mn + (size_t)row0 * G);
+    const uint16_t* s0 = s + (size_t)row0 * G;
+    const uint16_t* m0 = mn + (size_t)row0 * G;
     const int n8 = RB * G / 8;  // 16-byte pieces (RB G is a multiple of 8: G = K / 64, RB = 64)
     constexpr int MAXP = RB * 64 / 8 / 256;  // pieces per thread at the largest G (64)
-    uint4 sv[MAXP], mv[MAXP];
+    typedef uint32_t u4v __attribute__((ext_vector_type(4)));
+    u4v sv[MAXP], mv[MAXP];
 #pragma unroll
     for (int u = 0; u < MAXP; u++) {
         const int i = threadIdx.x + 256 * u;
         if (i < n8) {
-            sv[u] = s4[i];
-            mv[u] = m4[i];
+            sv[u] = ld_global<u4v>(s0 + 8 * i);
+            mv[u] = ld_global<u4v>(m0 + 8 * i);
         }
     }
 #pragma unroll
@@ -433,9 +457,11 @@ __device__ __forceinline__ void stage_gsums(float* gs, const float* __restrict__
 // Gate / up: block (unit block ub of RB units) x tile. act[p][r] = silu(gate_r . x) * (up_r . x)
 // for the tile's picks, stored as bf16 hi / lo in chunk order (ah, al [P][I]) with group sums
 // as [P][I / 64] (the unit block is one 64-group of the down projection's input).
+// Grid (I / RB unit blocks, tile-list capacity); the tile count and the tile record are read
+// together, and the record carries the expert's row address (no pointer-table round trip).
 template <int NT>  // pick tiles of 16: 1 for tiles of <= 16 picks, 2 for larger ones
-__global__ void __launch_bounds__(256, 2) moe_gate_up_kernel(const unsigned long long* __restrict__ eptr,
-                                                          const int4* __restrict__ tiles, const int* __restrict__ ntiles,
+__global__ void __launch_bounds__(256, 2) moe_gate_up_kernel(const MoeTile* __restrict__ tiles,
+                                                          const int* __restrict__ ntiles,
                                                           const int* __restrict__ ptok, const uint16_t* __restrict__ xh,
                                                           const uint16_t* __restrict__ xl, const float* __restrict__ xs,
                                                           int D, int I, ExpertOffsets off, uint16_t* __restrict__ ah,
@@ -444,25 +470,26 @@ __global__ void __launch_bounds__(256, 2) moe_gate_up_kernel(const unsigned long
     extern __shared__ float2 dyn[];
     __shared__ float ob[PB][RB + 1];     // gate sums, then act
     __shared__ float ub2[PB][RB + 1];    // up sums
-    const int tile = blockIdx.y, ub = blockIdx.x;
+    const int ub = blockIdx.x, tile = blockIdx.y;
+    const MoeTile tl = tiles[tile];  // read before the count is known (capacity-sized list)
     if (tile >= *ntiles) return;
-    const int4 tl = tiles[tile];
-    const int e = tl.x, p0 = tl.y, np = tl.z - tl.y;
-    const unsigned char* base = (const unsigned char*)eptr[e];
     const int G = D / 64, r0 = ub * RB;
     float2* sc = dyn;
     float* gs = (float*)(dyn + 2 * RB * G);
-    stage_scales(sc, (const uint16_t*)(base + off.gu_s), (const uint16_t*)(base + off.gu_m), r0, G);
-    stage_scales(sc + RB * G, (const uint16_t*)(base + off.gu_s), (const uint16_t*)(base + off.gu_m), I + r0, G);
-    stage_gsums(gs, xs, ptok, p0, np, G);
-    __syncthreads();
+    const int p0 = tl.p0, np = tl.p1 - tl.p0;
+    const unsigned char* base = (const unsigned char*)tl.base;
+    auto stage = [&]() {
+        stage_scales(sc, (const uint16_t*)(base + off.gu_s), (const uint16_t*)(base + off.gu_m), r0, G);
+        stage_scales(sc + RB * G, (const uint16_t*)(base + off.gu_s), (const uint16_t*)(base + off.gu_m), I + r0, G);
+        stage_gsums(gs, xs, ptok, p0, np, G);
+    };
     const int lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE, n = lane % 16, g = lane / 16;
     long long xrow[2];
 #pragma unroll
     for (int t = 0; t < 2; t++) xrow[t] = (long long)ptok[p0 + min(16 * t + n, np - 1)] * D;
     const long long qrow0[2] = {r0, I + r0};  // gate rows, up rows of this unit block
     BlockAcc<2, NT> acc;
-    expert_block<2, NT>(base, qrow0, D, sc, xh, xl, xrow, gs, acc, G);
+    expert_block<2, NT>(base, qrow0, D, sc, xh, xl, xrow, gs, acc, G, stage);
     reduce_waves<2, NT>(acc, 0, ob);   // gate sums
     reduce_waves<2, NT>(acc, 1, ub2);  // up sums
     // 256 threads = 32 picks x 8 chunks of the 64 units
@@ -485,9 +512,10 @@ __global__ void __launch_bounds__(256, 2) moe_gate_up_kernel(const unsigned long
 }
 
 // Down: block (output rows [RB ob, RB ob + RB)) x tile. ypick[src][o] = wts[src] * (dn_o . act).
+// Grid (D / RB output blocks, tile-list capacity), tile records as for gate / up.
 template <int NT>
-__global__ void __launch_bounds__(256, 2) moe_down_kernel(const unsigned long long* __restrict__ eptr,
-                                                       const int4* __restrict__ tiles, const int* __restrict__ ntiles,
+__global__ void __launch_bounds__(256, 2) moe_down_kernel(const MoeTile* __restrict__ tiles,
+                                                       const int* __restrict__ ntiles,
                                                        const int* __restrict__ psrc, const float* __restrict__ wts,
                                                        const uint16_t* __restrict__ ah, const uint16_t* __restrict__ al,
                                                        const float* __restrict__ as, int D, int I, ExpertOffsets off,
@@ -495,24 +523,25 @@ __global__ void __launch_bounds__(256, 2) moe_down_kernel(const unsigned long lo
     // dynamic LDS: sc [RB][G] | gs [PB][G]
     extern __shared__ float2 dyn[];
     __shared__ float red[PB][RB + 1];  // the waves' summed outputs
-    const int tile = blockIdx.y, ob = blockIdx.x;
+    const int ob = blockIdx.x, tile = blockIdx.y;
+    const MoeTile tl = tiles[tile];
     if (tile >= *ntiles) return;
-    const int4 tl = tiles[tile];
-    const int e = tl.x, p0 = tl.y, np = tl.z - tl.y;
-    const unsigned char* base = (const unsigned char*)eptr[e];
     const int G = I / 64, o0 = ob * RB;
     float2* sc = dyn;
     float* gs = (float*)(dyn + RB * G);
-    stage_scales(sc, (const uint16_t*)(base + off.dn_s), (const uint16_t*)(base + off.dn_m), o0, G);
-    stage_gsums(gs, as, nullptr, p0, np, G);
-    __syncthreads();
+    const int p0 = tl.p0, np = tl.p1 - tl.p0;
+    const unsigned char* base = (const unsigned char*)tl.base;
+    auto stage = [&]() {
+        stage_scales(sc, (const uint16_t*)(base + off.dn_s), (const uint16_t*)(base + off.dn_m), o0, G);
+        stage_gsums(gs, as, nullptr, p0, np, G);
+    };
     const int lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE, n = lane % 16, g = lane / 16;
     long long xrow[2];
 #pragma unroll
     for (int t = 0; t < 2; t++) xrow[t] = (long long)(p0 + min(16 * t + n, np - 1)) * I;
     const long long qrow0[1] = {o0};
     BlockAcc<1, NT> acc;
-    expert_block<1, NT>(base + off.dn_q, qrow0, I, sc, ah, al, xrow, gs, acc, G);
+    expert_block<1, NT>(base + off.dn_q, qrow0, I, sc, ah, al, xrow, gs, acc, G, stage);
     reduce_waves<1, NT>(acc, 0, red);
     // 256 threads = 32 picks x 8 runs of 8 rows: ypick[src][o0 + 8 q ..] = w * y
     const int pr = threadIdx.x / 8, q = threadIdx.x % 8;
@@ -604,8 +633,8 @@ static MoePlan moe_plan(int T, int K, int D, int I, int E) {
     p.eoff = take((size_t)(E + 1) * 4);
     p.ptok = take(N * 4);
     p.psrc = take(N * 4);
-    p.tiles1 = take((size_t)p.max1 * 16);
-    p.tiles2 = take((size_t)std::max(p.max2, 1) * 16);
+    p.tiles1 = take((size_t)p.max1 * sizeof(MoeTile));
+    p.tiles2 = take((size_t)std::max(p.max2, 1) * sizeof(MoeTile));
     p.meta = take(16);
     p.total = o;
     return p;
@@ -662,8 +691,8 @@ int aegist_moe_experts(const float* h, const unsigned long long* eptr, const int
     int* eoff = (int*)(w + p.eoff);
     int* ptok = (int*)(w + p.ptok);
     int* psrc = (int*)(w + p.psrc);
-    int4* tiles1 = (int4*)(w + p.tiles1);
-    int4* tiles2 = (int4*)(w + p.tiles2);
+    MoeTile* tiles1 = (MoeTile*)(w + p.tiles1);
+    MoeTile* tiles2 = (MoeTile*)(w + p.tiles2);
     int* meta = (int*)(w + p.meta);
     uint16_t* xh = (uint16_t*)(w + p.xh);
     uint16_t* xl = (uint16_t*)(w + p.xl);
@@ -673,7 +702,7 @@ int aegist_moe_experts(const float* h, const unsigned long long* eptr, const int
     float* as = (float*)(w + p.as);
     float* yp = (float*)(w + p.yp);
 
-    moe_group_kernel<<<1, 1024, 0, st>>>(idx, N, K, E, eoff, ptok, psrc, tiles1, tiles2, meta);
+    moe_group_kernel<<<1, 1024, 0, st>>>(idx, N, K, E, eptr, eoff, ptok, psrc, tiles1, tiles2, meta);
     int rc = after_launch("moe_group");
     if (rc) return rc;
     const long long nq = (long long)T * (D / 8);
@@ -683,21 +712,20 @@ int aegist_moe_experts(const float* h, const unsigned long long* eptr, const int
     // skips their rows, so nothing has to be cleared.
     const size_t lds_gu = (size_t)(2 * RB + PB) * (D / 64) * 8, lds_dn = (size_t)(RB + PB) * (I / 64) * 8;
     // two launches per projection: tiles of <= 16 picks (one MFMA column tile, the decode case)
-    // and larger tiles (two); a launch whose list is empty exits at once
-    moe_gate_up_kernel<1><<<dim3(I / RB, p.max1), 256, lds_gu, st>>>(eptr, tiles1, meta, ptok, xh, xl, xs, D, I, off,
-                                                                     ah, al, as);
+    // and larger tiles (two); a workgroup past its list's count exits at once
+    moe_gate_up_kernel<1><<<dim3(I / RB, p.max1), 256, lds_gu, st>>>(tiles1, meta, ptok, xh, xl, xs, D, I, off, ah, al,
+                                                                     as);
     if ((rc = after_launch("moe_gate_up"))) return rc;
     if (p.max2 > 0) {
-        moe_gate_up_kernel<2><<<dim3(I / RB, p.max2), 256, lds_gu, st>>>(eptr, tiles2, meta + 2, ptok, xh, xl, xs, D, I,
-                                                                         off, ah, al, as);
+        moe_gate_up_kernel<2><<<dim3(I / RB, p.max2), 256, lds_gu, st>>>(tiles2, meta + 2, ptok, xh, xl, xs, D, I, off,
+                                                                         ah, al, as);
         if ((rc = after_launch("moe_gate_up"))) return rc;
     }
-    moe_down_kernel<1><<<dim3(D / RB, p.max1), 256, lds_dn, st>>>(eptr, tiles1, meta, psrc, wts, ah, al, as, D, I, off,
-                                                                  yp);
+    moe_down_kernel<1><<<dim3(D / RB, p.max1), 256, lds_dn, st>>>(tiles1, meta, psrc, wts, ah, al, as, D, I, off, yp);
     if ((rc = after_launch("moe_down"))) return rc;
     if (p.max2 > 0) {
-        moe_down_kernel<2><<<dim3(D / RB, p.max2), 256, lds_dn, st>>>(eptr, tiles2, meta + 2, psrc, wts, ah, al, as, D,
-                                                                      I, off, yp);
+        moe_down_kernel<2><<<dim3(D / RB, p.max2), 256, lds_dn, st>>>(tiles2, meta + 2, psrc, wts, ah, al, as, D, I,
+                                                                      off, yp);
         if ((rc = after_launch("moe_down"))) return rc;
     }
     moe_combine_kernel<<<dim3(T, (D + 255) / 256), 256, 0, st>>>(x, yp, idx, E, ysh, h, wg, D, K);
