@@ -24,6 +24,9 @@ using namespace aegist;
 namespace {
 
 constexpr int KSTEP = 64;  // k per wave step: 16 bytes of int8 (two MFMA k-blocks of 32) per lane
+#ifndef PROJ_TARGET_WAVES
+#define PROJ_TARGET_WAVES 2048  // waves per launch the shape heuristic aims for
+#endif
 
 typedef int int4v __attribute__((ext_vector_type(4)));
 
@@ -182,6 +185,24 @@ __global__ __launch_bounds__(64 * NWAVE) void proj_skinny_kernel(const TX* __res
 #pragma unroll
         for (int mt = 0; mt < MT; mt++) acc[rt][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+    // The epilogue's row scales (and, when accumulating, the old Y values) of the tiles this
+    // wave finishes (tile t by wave t % NWAVE) are requested now, so they arrive with the
+    // weights instead of costing a round trip at the end.
+    constexpr int NFIN = (RT * MT + NWAVE - 1) / NWAVE;  // tiles finished per wave, at most
+    float fscale[NFIN][4], fy[NFIN][4];
+#pragma unroll
+    for (int u = 0; u < NFIN; u++) {
+        const int t = wave + NWAVE * u, rt = t / MT, mt = t % MT;
+        const int m = m0 + 16 * mt + r16;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int n = n0 + 16 * rt + 4 * g + j;
+            const bool ok = t < RT * MT && n < N && m < M;
+            fscale[u][j] = (ok && scale) ? bf2f(scale[n]) : 1.f;
+            fy[u][j] = (ok && accumulate) ? Y[(size_t)m * ldy + n] : 0.f;
+        }
+    }
+
     // loads of DEPTH steps are issued together, then consumed: with ~4 steps per wave that is
     // every load of the wave in flight at once
     constexpr int DEPTH = (XLoad<TX>::kLo ? MT * 16 : MT * 8) + RT * 8 <= 32 ? 4 : 2;
@@ -216,13 +237,19 @@ __global__ __launch_bounds__(64 * NWAVE) void proj_skinny_kernel(const TX* __res
 
     // wave w takes steps w, w + NWAVE, ... (neighbouring waves read neighbouring runs of a row);
     // steps past the end load zeros and are skipped
+    // rolling prefetch: a buffer is refilled with the step DEPTH rounds ahead as soon as it has
+    // been consumed, so the next round's loads are in flight during this round's MFMAs
     const int nsteps = (K + KSTEP - 1) / KSTEP;
+#pragma unroll
+    for (int d = 0; d < DEPTH; d++) fetch(d, wave + d * NWAVE);
     for (int s0 = wave; s0 < nsteps; s0 += DEPTH * NWAVE) {
 #pragma unroll
-        for (int d = 0; d < DEPTH; d++) fetch(d, s0 + d * NWAVE);
-#pragma unroll
-        for (int d = 0; d < DEPTH; d++)
-            if (s0 + d * NWAVE < nsteps) compute(d);
+        for (int d = 0; d < DEPTH; d++) {
+            const int st = s0 + d * NWAVE;
+            if (st < nsteps) compute(d);
+            const int nx = st + DEPTH * NWAVE;
+            if (s0 + DEPTH * NWAVE < nsteps) fetch(d, nx);  // uniform: the next round exists
+        }
     }
 
 #pragma unroll
@@ -230,8 +257,12 @@ __global__ __launch_bounds__(64 * NWAVE) void proj_skinny_kernel(const TX* __res
 #pragma unroll
         for (int mt = 0; mt < MT; mt++) red[wave][rt * MT + mt][lane] = acc[rt][mt];
     __syncthreads();
-    // tile t is finished by wave t % 4: lane holds column m = m0 + 16 mt + r16, rows n 4g .. 4g+3
-    for (int t = wave; t < RT * MT; t += NWAVE) {
+    // tile t is finished by wave t % NWAVE: lane holds column m = m0 + 16 mt + r16, rows
+    // n 4g .. 4g+3
+#pragma unroll
+    for (int u = 0; u < NFIN; u++) {
+        const int t = wave + NWAVE * u;
+        if (t >= RT * MT) break;
         f32x4 v = red[0][t][lane];
 #pragma unroll
         for (int w = 1; w < NWAVE; w++) v += red[w][t][lane];
@@ -243,8 +274,7 @@ __global__ __launch_bounds__(64 * NWAVE) void proj_skinny_kernel(const TX* __res
         for (int j = 0; j < 4; j++) {
             const int n = n0 + 16 * rt + 4 * g + j;
             if (n >= N) continue;
-            float y = v[j] * (scale ? bf2f(scale[n]) : 1.f);
-            yrow[n] = accumulate ? yrow[n] + y : y;
+            yrow[n] = fy[u][j] + v[j] * fscale[u][j];
         }
     }
 }
@@ -273,7 +303,7 @@ void launch_mt(const TX* X, long long ldx, const ProjSegs& segs, int M, int K, i
         t2 += (segs.s[i].N + 31) / 32 * gy;
         t1 += (segs.s[i].N + 15) / 16 * gy;
     }
-    constexpr int kTarget = 2048;
+    constexpr int kTarget = PROJ_TARGET_WAVES;
 #define AEG_PROJ(RT, NW) return launch_k<TW, TX, MT, RT, NW>(X, ldx, segs, M, K, accumulate, st)
     if (t2 * 4 >= kTarget) AEG_PROJ(2, 4);
     if (t2 * 8 >= kTarget && nsteps >= 16) AEG_PROJ(2, 8);
