@@ -155,10 +155,16 @@ int delta_layer(Stack* s, const AegistLayerWeights& w, int sl, float* x, int B, 
         RC(aegist_delta_decode_step(s->proj, AEGIST_F32, w.conv_w, conv, s->g, s->beta, rec, s->o, AEGIST_F32, B, HK,
                                     HV, qscale, 1e-6f, st));
     } else {
-        // prefill: conv over the chunk, then the chunked WY form from the carried state
+        // prefill: conv over the chunk, then the fp32 token-by-token scan below 64 tokens (the
+        // engine scans every length, hybrid.rs:845-852), the chunked WY form from 64 tokens up
         RC(launch_conv_silu_batched(s->proj, s->y, w.conv_w, conv, B, T, C, st));
         const long long sb = (long long)T * C, so_b = (long long)T * HV * D;
-        RC(aegist_delta_chunked(s->y, s->y + (size_t)HK * D, s->y + (size_t)2 * HK * D, AEGIST_F32, sb, C, D, sb, C, D,
+        if (T < 64)
+            RC(aegist_delta_recurrent(s->y, s->y + (size_t)HK * D, s->y + (size_t)2 * HK * D, AEGIST_F32, sb, C, D, sb,
+                                      C, D, s->g, s->beta, rec, s->o, AEGIST_F32, so_b, (long long)HV * D, D, B, T, HK,
+                                      HV, 1, qscale, 1e-6f, st));
+        else
+            RC(aegist_delta_chunked(s->y, s->y + (size_t)HK * D, s->y + (size_t)2 * HK * D, AEGIST_F32, sb, C, D, sb, C, D,
                                 s->g, s->beta, rec, s->o, AEGIST_F32, so_b, (long long)HV * D, D, B, T, HK, HV, 1,
                                 qscale, 1e-6f, s->ws, s->ws_bytes, st));
     }
