@@ -21,15 +21,16 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 // ---------------------------------------------------------------------------------------------
 // bf16 <-> fp32. bf16 is the top half of an fp32; narrowing rounds to nearest even and maps
-// NaN to a quiet NaN.
+// NaN to a quiet NaN (one v_cvt_pk_bf16_f32 on gfx950, no branch).
 __device__ __forceinline__ float bf2f(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
 __device__ __forceinline__ float bf_lo(uint32_t p) { return __uint_as_float(p << 16); }
 __device__ __forceinline__ float bf_hi(uint32_t p) { return __uint_as_float(p & 0xffff0000u); }
-__device__ __forceinline__ uint16_t f2bf(float f) {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return (uint16_t)((u >> 16) | 0x40);
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return (uint16_t)(u >> 16);
+__device__ __forceinline__ uint16_t f2bf(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
+// two floats -> packed bf16 pair (a in the low half)
+__device__ __forceinline__ uint32_t f2bf2(float a, float b) {
+    typedef float f2v __attribute__((ext_vector_type(2)));
+    typedef __bf16 b2v __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2v{a, b}), b2v));
 }
 
 // Element load/store for the activation dtypes the ABI accepts (fp32 or bf16).

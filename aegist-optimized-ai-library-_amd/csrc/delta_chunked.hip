@@ -465,7 +465,7 @@ struct K2Smem {
     __attribute__((aligned(16))) half_t SsT[2][16 * NCT][D + 8];   // S^T (fp16): [column][dk]
     __attribute__((aligned(16))) half_t VnT[2][16 * NCT][CH + 8];  // v_new^T (fp16)
     __attribute__((aligned(16))) half_t VdT[2][16 * NCT][CH + 8];  // (e^{cum_last-cum} v_new)^T
-    float Ot[4][16][16 * NCT + 4];                                 // output staging per wave
+    __attribute__((aligned(16))) float Ot[4][16][16 * NCT + 4];  // output staging per wave
 };
 
 template <typename Tout, int NCT, bool VEC>
@@ -607,19 +607,16 @@ __device__ __forceinline__ void chunk_state_body(const unsigned char* __restrict
                     const int r = r0 + lane / LPR, p8 = (lane % LPR) * 8, row = 16 * wave + r;
                     const bool ok = r < 16 && tc + row < T;
                     const int off = ok ? (int)(((long long)row * a.st_o + p8) * (long long)sizeof(Tout)) : kOutDrop;
-                    const float* src = &Ot[wave][r & 15][p8];
+                    // two 16-byte LDS reads per lane (row pitch and p8 keep them aligned)
+                    const f32x4 s0 = *(const f32x4*)&Ot[wave][r & 15][p8];
+                    const f32x4 s1 = *(const f32x4*)&Ot[wave][r & 15][p8 + 4];
                     if constexpr (sizeof(Tout) == 2) {
-                        u32x4 pk;
-                        pk.x = (uint32_t)f2bf(src[0]) | ((uint32_t)f2bf(src[1]) << 16);
-                        pk.y = (uint32_t)f2bf(src[2]) | ((uint32_t)f2bf(src[3]) << 16);
-                        pk.z = (uint32_t)f2bf(src[4]) | ((uint32_t)f2bf(src[5]) << 16);
-                        pk.w = (uint32_t)f2bf(src[6]) | ((uint32_t)f2bf(src[7]) << 16);
+                        const u32x4 pk = {f2bf2(s0[0], s0[1]), f2bf2(s0[2], s0[3]), f2bf2(s1[0], s1[1]),
+                                          f2bf2(s1[2], s1[3])};
                         __builtin_amdgcn_raw_buffer_store_b128(pk, rs, off, 0, 0);
                     } else {
-                        const u32x4 lo = {__float_as_uint(src[0]), __float_as_uint(src[1]), __float_as_uint(src[2]),
-                                          __float_as_uint(src[3])};
-                        const u32x4 hi = {__float_as_uint(src[4]), __float_as_uint(src[5]), __float_as_uint(src[6]),
-                                          __float_as_uint(src[7])};
+                        const u32x4 lo = __builtin_bit_cast(u32x4, s0);
+                        const u32x4 hi = __builtin_bit_cast(u32x4, s1);
                         __builtin_amdgcn_raw_buffer_store_b128(lo, rs, off, 0, 0);
                         __builtin_amdgcn_raw_buffer_store_b128(hi, rs, ok ? off + 16 : kOutDrop, 0, 0);
                     }
