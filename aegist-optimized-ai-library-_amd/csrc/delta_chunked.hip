@@ -131,12 +131,13 @@ struct K1Smem {
     __attribute__((aligned(16))) half_t QV[CH][QK_LD];  // q_n tile, then v (fp16 hi)
     __attribute__((aligned(16))) half_t Vl[kSplitV ? CH : 1][QK_LD];
     __attribute__((aligned(16))) half_t Ks[CH][QK_LD];
-    __attribute__((aligned(16))) float As[CH][A_LD];    // A, then X = (I + A)^-1 in place
-    float Pt[3][16][17];
+    // A, then X = (I + A)^-1 in place. Its upper block column 3 (rows 0..47, columns 48..63: zero
+    // in A and X) carries the P tiles of the blocked inversion and is cleared afterwards.
+    __attribute__((aligned(16))) float As[CH][A_LD];
     float cum_s[CH], beta_s[CH], g_s[CH];
-    // intra, staged for fragment order; with fp32 inputs it borrows Vl, which is first written
-    // after the intra fragments have gone out (keeps the fp32 variant at two workgroups per CU)
-    __attribute__((aligned(16))) half_t ItBuf[kSplitV ? 1 : CH][CH + 8];
+    // intra is staged for fragment order in QV's space: q_n has been read into registers by then,
+    // and v is written there only after the intra fragments have gone out. 53 KB in all for bf16
+    // inputs: three workgroups per CU.
 };
 
 template <typename Tin>
@@ -151,11 +152,12 @@ __device__ __forceinline__ void chunk_intra_body(const Tin* __restrict__ q, cons
     auto& Vl = sm.Vl;
     auto& Ks = sm.Ks;
     auto& As = sm.As;
-    auto& Pt = sm.Pt;
     auto& cum_s = sm.cum_s;
     auto& beta_s = sm.beta_s;
     auto& g_s = sm.g_s;
-    half_t (*It)[CH + 8] = kSplitV ? (half_t (*)[CH + 8])&Vl[0][0] : sm.ItBuf;
+    half_t (*It)[CH + 8] = (half_t (*)[CH + 8])&QV[0][0];
+    // P tile of block column cb during the blocked inversion: As rows 16 cb.., columns 48..63
+    auto Pt = [&](int cb, int i, int j) -> float& { return As[16 * cb + i][48 + j]; };
 
     const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE, n = lane % 16, gq = lane / 16;
     const int R = HV / HK, kh = hv / R;
@@ -263,6 +265,7 @@ __device__ __forceinline__ void chunk_intra_body(const Tin* __restrict__ q, cons
             ak[ks] = ld_h8(&Ks[16 * rb + n][32 * ks + 8 * gq]);
             aq[ks] = ld_h8(&QV[16 * rb + n][32 * ks + 8 * gq]);
         }
+        __syncthreads();  // every wave holds its q_n rows: It (QV's space) is written next
         for (int cb = 0; cb < 4; cb++) {
             const int jj = 16 * cb + n;
             if (cb > rb) {  // upper blocks: zero in intra and in A (X = (I + A)^-1 stays lower there)
@@ -300,7 +303,7 @@ __device__ __forceinline__ void chunk_intra_body(const Tin* __restrict__ q, cons
             intra[f] = ld_h8(&It[r][c0]);
         }
     }
-    if constexpr (kSplitV) __syncthreads();  // It aliases Vl, written next
+    __syncthreads();  // It (QV's space) has gone out; v is written there next
 
     // ---- 4. v (fp16 hi / lo) into the q tile's space; X = (I + A)^-1, blocked by 16
 #pragma unroll
@@ -351,7 +354,7 @@ __device__ __forceinline__ void chunk_intra_body(const Tin* __restrict__ q, cons
                 }
             }
 #pragma unroll
-            for (int j = 0; j < 4; j++) Pt[cb][4 * gq + j][n] = P[j];
+            for (int j = 0; j < 4; j++) Pt(cb, 4 * gq + j, n) = P[j];
         }
         __syncthreads();  // all reads of A_r* done; P visible
         if (cb < r) {
@@ -359,13 +362,19 @@ __device__ __forceinline__ void chunk_intra_body(const Tin* __restrict__ q, cons
 #pragma unroll
             for (int s4 = 0; s4 < 4; s4++) {
                 const float av = As[16 * r + n][16 * r + 4 * s4 + gq];
-                const float bv = Pt[cb][4 * s4 + gq][n];
+                const float bv = Pt(cb, 4 * s4 + gq, n);
                 X = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, X, 0, 0, 0);
             }
 #pragma unroll
             for (int j = 0; j < 4; j++) As[16 * r + 4 * gq + j][16 * cb + n] = -X[j];
         }
         __syncthreads();
+    }
+    // clear the P tiles: X is zero above its diagonal blocks (read after step 5's barrier)
+#pragma unroll
+    for (int it = 0; it < 3; it++) {
+        const int e = tid + 256 * it;
+        As[e / 16][48 + e % 16] = 0.f;
     }
 
     // ---- 5. u = X diag(beta) v and w = X diag(beta e^cum) k_n on MFMA, X as fp16 hi + lo.
@@ -444,7 +453,7 @@ __device__ __forceinline__ void chunk_intra_body(const Tin* __restrict__ q, cons
 }
 
 template <typename Tin>
-__global__ void __launch_bounds__(256) delta_chunk_intra(const Tin* __restrict__ q, const Tin* __restrict__ k,
+__global__ void __launch_bounds__(256, 3) delta_chunk_intra(const Tin* __restrict__ q, const Tin* __restrict__ k,
                                                          const Tin* __restrict__ v, const float* __restrict__ g,
                                                          const float* __restrict__ beta, SeqLayout a, int t0, int T,
                                                          int HK, int HV, int normalize, float qscale, float eps,
@@ -508,7 +517,8 @@ __device__ __forceinline__ void chunk_state_body(const unsigned char* __restrict
         f32x4 uu[NCT], ecum, edec;  // u fragment; e^{cum_i}, e^{cum_last - cum_i} for this lane's rows
         float gamma;              // e^{cum_last}
     };
-    auto fetch = [&](int c, Ops& o) {
+    // part < 0: every operand; part 0..4: the slice of the fetch issued at that phase of step()
+    auto fetch = [&](int c, Ops& o, int part = -1) {
         const size_t vu = vbase + c, ku = kbase + c;
         const half_t* Wc = (const half_t*)(ws + L.w) + vu * CH * D;
         const half_t* Qc = (const half_t*)(ws + L.qn) + ku * CH * D;
@@ -516,26 +526,46 @@ __device__ __forceinline__ void chunk_state_body(const unsigned char* __restrict
         const half_t* Ic = (const half_t*)(ws + L.intra) + vu * CH * CH;
         const half_t* KTc = (const half_t*)(ws + L.knt) + ku * CH * D;
         const float* dec = (const float*)(ws + L.cum) + vu * 3 * CH;
-        // fragment-order operands (written so by K1): one contiguous 1 KB load per fragment
+        // fragment-order operands (written so by K1): one contiguous 1 KB load per fragment.
+        // Parts in the order step() consumes them: 0 = w, q_n (w S, q_n S); 1 = u, e^{cum_last -
+        // cum} (v_new); 2 = intra, e^{cum} (output); 3 = k_n^T, e^{cum_last} (state update)
+        if (part < 0 || part == 0)
 #pragma unroll
-        for (int ks = 0; ks < 4; ks++) {
-            o.wa[ks] = ld_h8(Wc + ((4 * wave + ks) * 64 + lane) * 8);
-            o.qa[ks] = ld_h8(Qc + ((4 * wave + ks) * 64 + lane) * 8);
+            for (int ks = 0; ks < 4; ks++) {
+                o.wa[ks] = ld_h8(Wc + ((4 * wave + ks) * 64 + lane) * 8);
+                o.qa[ks] = ld_h8(Qc + ((4 * wave + ks) * 64 + lane) * 8);
+            }
+        if (part < 0 || part == 1) {
+#pragma unroll
+            for (int ct = 0; ct < NCT; ct++)
+                o.uu[ct] = *(const f32x4*)(Uc + u_frag(16 * wave + 4 * gq, col0 + 16 * ct + n));
+            o.edec = *(const f32x4*)(dec + CH + 16 * wave + 4 * gq);
         }
+        if (part < 0 || part == 2) {
 #pragma unroll
-        for (int ks = 0; ks < 2; ks++) o.ia[ks] = ld_h8(Ic + ((2 * wave + ks) * 64 + lane) * 8);
+            for (int ks = 0; ks < 2; ks++) o.ia[ks] = ld_h8(Ic + ((2 * wave + ks) * 64 + lane) * 8);
+            o.ecum = *(const f32x4*)(dec + 16 * wave + 4 * gq);
+        }
+        if (part < 0 || part == 3) {
 #pragma unroll
-        for (int rt = 0; rt < 2; rt++)
+            for (int rt = 0; rt < 2; rt++)
 #pragma unroll
-            for (int ks = 0; ks < 2; ks++) o.ka[rt][ks] = ld_h8(KTc + ((2 * (2 * wave + rt) + ks) * 64 + lane) * 8);
-#pragma unroll
-        for (int ct = 0; ct < NCT; ct++) o.uu[ct] = *(const f32x4*)(Uc + u_frag(16 * wave + 4 * gq, col0 + 16 * ct + n));
-        o.ecum = *(const f32x4*)(dec + 16 * wave + 4 * gq);
-        o.edec = *(const f32x4*)(dec + CH + 16 * wave + 4 * gq);
-        o.gamma = dec[2 * CH];
+                for (int ks = 0; ks < 2; ks++)
+                    o.ka[rt][ks] = ld_h8(KTc + ((2 * (2 * wave + rt) + ks) * 64 + lane) * 8);
+            o.gamma = dec[2 * CH];
+        }
     };
-    // per-chunk compute on operands `cur` (S-dependent part)
-    auto step = [&](int c, const Ops& cur) {
+    // per-chunk compute on operands `op`. Each part of `op` is refilled with chunk cn's values
+    // right after its last use, so one register set suffices and the vector-memory path streams
+    // the next chunk's operands while this chunk computes (a load burst would stall the wave at
+    // issue; the operand volume per chunk is the bound of this loop)
+    auto step = [&](int c, Ops& op, int cn) {
+        const Ops& cur = op;
+        auto issue = [&](int part) {
+            __builtin_amdgcn_sched_barrier(0);
+            fetch(cn, op, part);
+            __builtin_amdgcn_sched_barrier(0);
+        };
         const half8* wa = cur.wa;
         const half8* qa = cur.qa;
         const half8* ia = cur.ia;
@@ -565,6 +595,7 @@ __device__ __forceinline__ void chunk_state_body(const unsigned char* __restrict
                 QS[ct] = mfma16(qa[ks], sb, QS[ct]);
             }
         }
+        issue(0);
         // (3) v_new = u - w S; decayed copy for the state update
 #pragma unroll
         for (int ct = 0; ct < NCT; ct++) {
@@ -578,6 +609,7 @@ __device__ __forceinline__ void chunk_state_body(const unsigned char* __restrict
             *(half4*)&VnT[pb][16 * ct + n][16 * wave + 4 * gq] = hn;
             *(half4*)&VdT[pb][16 * ct + n][16 * wave + 4 * gq] = hd;
         }
+        issue(1);
         __syncthreads();
 
         // (4) o = e^{cum} q_n S + intra v_new
@@ -634,6 +666,7 @@ __device__ __forceinline__ void chunk_state_body(const unsigned char* __restrict
                 }
             }
         }
+        issue(2);
         // (5) S = e^{cum_last} S + k_n^T v'
         const float gamma = cur.gamma;
 #pragma unroll
@@ -645,27 +678,24 @@ __device__ __forceinline__ void chunk_state_body(const unsigned char* __restrict
                 for (int ks = 0; ks < 2; ks++) acc = mfma16(cur.ka[rt][ks], ld_h8(&VdT[pb][16 * ct + n][32 * ks + 8 * gq]), acc);
                 S[rt][ct] = acc;
             }
+        issue(3);
     };
-    // ping-pong between two operand sets (no register copies, so the wait for a prefetch only
-    // covers the loads issued before it)
-    Ops A, Bo;
-    fetch(0, A);
+    // the first chunk's operands in the order the loop refills them, with a discarded store where
+    // the loop body has its output store, so the loop entry and the back edge carry the same
+    // sequence of memory operations (static wait counts)
+    Ops op;
+    fetch(0, op, 0);
+    fetch(0, op, 1);
     if constexpr (VEC) {
-        // a discarded store in the place the loop body has one, so the loop entry and the back
-        // edge carry the same count of memory operations between A's and Bo's loads
         const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(out, (short)0, kOutRange, kBufWord3);
         __builtin_amdgcn_raw_buffer_store_b128(u32x4{0u, 0u, 0u, 0u}, rs, kOutDrop, 0, 0);
         if constexpr (sizeof(Tout) == 4)
             __builtin_amdgcn_raw_buffer_store_b128(u32x4{0u, 0u, 0u, 0u}, rs, kOutDrop - 64, 0, 0);
     }
-    int c = 0;
-    for (; c + 1 < nch; c += 2) {
-        fetch(c + 1, Bo);
-        step(c, A);
-        fetch(min(c + 2, nch - 1), A);  // unconditional: keeps the wait counts static
-        step(c + 1, Bo);
-    }
-    if (c < nch) step(c, A);
+    fetch(0, op, 2);
+    fetch(0, op, 3);
+    // the next-chunk index is clamped, not skipped, so every step issues the same loads
+    for (int c = 0; c < nch; c++) step(c, op, min(c + 1, nch - 1));
 #pragma unroll
     for (int rt = 0; rt < 2; rt++)
 #pragma unroll
@@ -688,7 +718,7 @@ __global__ void __launch_bounds__(256, 2) delta_chunk_state(const unsigned char*
 // the K1 workgroups fill the CUs around K2's without a second stream or events. LDS is the
 // union of the two bodies' needs.
 template <typename Tin, typename Tout, int NCT, bool VEC>
-__global__ void __launch_bounds__(256, 2) delta_chunk_fused(
+__global__ void __launch_bounds__(256, 3) delta_chunk_fused(
     // K2 of segment s
     const unsigned char* __restrict__ ws2, WsLayout L2, float* __restrict__ state, int load_state,
     Tout* __restrict__ out, int t0s, int nch2, int nk2,
