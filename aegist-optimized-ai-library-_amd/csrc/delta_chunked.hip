@@ -140,6 +140,10 @@ struct K1Smem {
     // inputs: three workgroups per CU.
 };
 
+// step 5 reuses QV and Ks for the X fragments (hi + lo: 16 KB each) and As for the w staging tile
+static_assert(sizeof(half_t) * CH * QK_LD >= 2 * CH * CH * sizeof(half_t), "X fragments exceed the q / k tile");
+static_assert(sizeof(float) * CH * A_LD >= sizeof(half_t) * CH * QK_LD, "w staging exceeds As");
+
 template <typename Tin>
 __device__ __forceinline__ void chunk_intra_body(const Tin* __restrict__ q, const Tin* __restrict__ k,
                                                  const Tin* __restrict__ v, const float* __restrict__ g,
@@ -170,6 +174,12 @@ __device__ __forceinline__ void chunk_intra_body(const Tin* __restrict__ q, cons
     const bool valid = tok < T;
     float xv[32];
     {
+        // beta / g first: their latency overlaps the row loads
+        float beta_r = 0.f, g_r = 0.f;
+        if (qq == 0 && valid) {
+            beta_r = beta[b * a.sb_g + (long long)tok * a.st_g + hv];
+            g_r = g[b * a.sb_g + (long long)tok * a.st_g + hv];
+        }
         const Tin* qp = q + b * a.sb_qk + (long long)tok * a.st_qk + kh * a.sh_qk + qq * 32;
         const Tin* kp = k + b * a.sb_qk + (long long)tok * a.st_qk + kh * a.sh_qk + qq * 32;
         const Tin* vp = v + b * a.sb_v + (long long)tok * a.st_v + hv * a.sh_v + qq * 32;
@@ -213,8 +223,8 @@ __device__ __forceinline__ void chunk_intra_body(const Tin* __restrict__ q, cons
             *(half8*)&Ks[row][qq * 32 + e] = hk;
         }
         if (qq == 0) {
-            beta_s[row] = valid ? beta[b * a.sb_g + (long long)tok * a.st_g + hv] : 0.f;
-            g_s[row] = valid ? g[b * a.sb_g + (long long)tok * a.st_g + hv] : 0.f;
+            beta_s[row] = beta_r;
+            g_s[row] = g_r;
         }
     }
     __syncthreads();
@@ -256,39 +266,55 @@ __device__ __forceinline__ void chunk_intra_body(const Tin* __restrict__ q, cons
     }
     __syncthreads();
 
-    // ---- 3. k_n k_n^T and q_n k_n^T on MFMA: wave = 16-row block rb, column blocks cb <= rb
+    // ---- 3. k_n k_n^T and q_n k_n^T on MFMA, lower 16 x 16 blocks only: 10 blocks of each, as
+    // 20 jobs of 4 MFMAs, 5 per wave: wave w forms the A blocks of row block w (w + 1 of them) and
+    // the intra blocks of row block 3 - w (4 - w of them), and clears the upper blocks of both
     {
-        const int rb = wave;
+        const int wv = __builtin_amdgcn_readfirstlane(wave);
+        const int ra = wv, rq = 3 - wv;
         half8 ak[4], aq[4];
 #pragma unroll
         for (int ks = 0; ks < 4; ks++) {
-            ak[ks] = ld_h8(&Ks[16 * rb + n][32 * ks + 8 * gq]);
-            aq[ks] = ld_h8(&QV[16 * rb + n][32 * ks + 8 * gq]);
+            ak[ks] = ld_h8(&Ks[16 * ra + n][32 * ks + 8 * gq]);
+            aq[ks] = ld_h8(&QV[16 * rq + n][32 * ks + 8 * gq]);
+        }
+        float ca[4], ba[4], cq[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            ca[j] = cum_s[16 * ra + 4 * gq + j];
+            ba[j] = beta_s[16 * ra + 4 * gq + j];
+            cq[j] = cum_s[16 * rq + 4 * gq + j];
         }
         __syncthreads();  // every wave holds its q_n rows: It (QV's space) is written next
         for (int cb = 0; cb < 4; cb++) {
             const int jj = 16 * cb + n;
-            if (cb > rb) {  // upper blocks: zero in intra and in A (X = (I + A)^-1 stays lower there)
+            if (cb > ra) {
+#pragma unroll
+                for (int j = 0; j < 4; j++) As[16 * ra + 4 * gq + j][jj] = 0.f;
+            } else {
+                f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int ks = 0; ks < 4; ks++) acc = mfma16(ak[ks], ld_h8(&Ks[jj][32 * ks + 8 * gq]), acc);
+                const float cj = cum_s[jj];
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
-                    It[16 * rb + 4 * gq + j][jj] = (half_t)0.f;
-                    As[16 * rb + 4 * gq + j][jj] = 0.f;
+                    const int i = 16 * ra + 4 * gq + j;
+                    As[i][jj] = jj < i ? ba[j] * (__expf(ca[j] - cj) * acc[j]) : 0.f;
                 }
-                continue;
             }
-            f32x4 accA = {0.f, 0.f, 0.f, 0.f}, accQ = {0.f, 0.f, 0.f, 0.f};
+            if (cb > rq) {
 #pragma unroll
-            for (int ks = 0; ks < 4; ks++) {
-                half8 bk = ld_h8(&Ks[jj][32 * ks + 8 * gq]);
-                accA = mfma16(ak[ks], bk, accA);
-                accQ = mfma16(aq[ks], bk, accQ);
-            }
+                for (int j = 0; j < 4; j++) It[16 * rq + 4 * gq + j][jj] = (half_t)0.f;
+            } else {
+                f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const int i = 16 * rb + 4 * gq + j;
-                const float dec = __expf(cum_s[i] - cum_s[jj]);
-                As[i][jj] = jj < i ? beta_s[i] * (dec * accA[j]) : 0.f;
-                It[i][jj] = (half_t)(jj <= i ? dec * accQ[j] : 0.f);
+                for (int ks = 0; ks < 4; ks++) acc = mfma16(aq[ks], ld_h8(&Ks[jj][32 * ks + 8 * gq]), acc);
+                const float cj = cum_s[jj];
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const int i = 16 * rq + 4 * gq + j;
+                    It[i][jj] = (half_t)(jj <= i ? __expf(cq[j] - cj) * acc[j] : 0.f);
+                }
             }
         }
     }
@@ -396,32 +422,52 @@ __device__ __forceinline__ void chunk_intra_body(const Tin* __restrict__ q, cons
                     kb[t][ks][i] = Ks[rr][col];
                 }
         }
-        __syncthreads();  // every wave holds its v / k_n operands: Ks becomes the w staging tile
-        float su[2][8], sw[2][8];
+        __syncthreads();  // every wave holds its v / k_n operands: QV and Ks take the X fragments
+        // X diag(beta) and X diag(beta e^cum), each as fp16 hi + lo (hi + lo carries ~22 bits),
+        // converted once per workgroup into A-fragment order (afrag_coords, K = 64): thread =
+        // (row r, 16 consecutive k); QV holds the u factors, Ks the w factors
+        half8* XU = (half8*)&QV[0][0];  // [hi: 512 fragments][lo: 512]
+        half8* XW = (half8*)&Ks[0][0];
+        {
+            const int r = tid / 4, kq = tid % 4;
 #pragma unroll
-        for (int ks = 0; ks < 2; ks++)
+            for (int h = 0; h < 2; h++) {
+                const int k0 = 16 * kq + 8 * h;
+                const f32x4 x0 = *(const f32x4*)&As[r][k0], x1 = *(const f32x4*)&As[r][k0 + 4];
+                half8 uh, ul, wh, wl;
 #pragma unroll
-            for (int i = 0; i < 8; i++) {
-                const int rr = 32 * ks + 8 * gq + i;
-                su[ks][i] = beta_s[rr];
-                sw[ks][i] = beta_s[rr] * __expf(cum_s[rr]);
+                for (int i = 0; i < 8; i++) {
+                    const float x = i < 4 ? x0[i] : x1[i - 4];
+                    const float bu = beta_s[k0 + i], xu = x * bu, xw = x * (bu * __expf(cum_s[k0 + i]));
+                    half_t hh = (half_t)xu;
+                    uh[i] = hh;
+                    ul[i] = (half_t)(xu - (float)hh);
+                    hh = (half_t)xw;
+                    wh[i] = hh;
+                    wl[i] = (half_t)(xw - (float)hh);
+                }
+                // fragment (mb, ks) lane l = r % 16 + 16 gq' holds k = 32 ks + 8 gq' + i
+                const int f = ((r / 16) * 2 + k0 / 32) * 64 + (r % 16) + 16 * ((k0 % 32) / 8);
+                XU[f] = uh;
+                XU[512 + f] = ul;
+                XW[f] = wh;
+                XW[512 + f] = wl;
             }
+        }
+        __syncthreads();
+        // w staging for fragment order, in As's space (X has been read)
+        half_t (*Wst)[QK_LD] = (half_t (*)[QK_LD])&As[0][0];
 #pragma unroll
         for (int rb = 0; rb < 4; rb++) {
             half8 xuh[2], xul[2], xwh[2], xwl[2];
 #pragma unroll
-            for (int ks = 0; ks < 2; ks++)
-#pragma unroll
-                for (int i = 0; i < 8; i++) {
-                    const float x = As[16 * rb + n][32 * ks + 8 * gq + i];
-                    const float xu = x * su[ks][i], xw = x * sw[ks][i];
-                    half_t h = (half_t)xu;
-                    xuh[ks][i] = h;
-                    xul[ks][i] = (half_t)(xu - (float)h);
-                    h = (half_t)xw;
-                    xwh[ks][i] = h;
-                    xwl[ks][i] = (half_t)(xw - (float)h);
-                }
+            for (int ks = 0; ks < 2; ks++) {
+                const int f = (rb * 2 + ks) * 64 + lane;
+                xuh[ks] = XU[f];
+                xul[ks] = XU[512 + f];
+                xwh[ks] = XW[f];
+                xwl[ks] = XW[512 + f];
+            }
 #pragma unroll
             for (int t = 0; t < 2; t++) {
                 f32x4 au = {0.f, 0.f, 0.f, 0.f}, aw = {0.f, 0.f, 0.f, 0.f};
@@ -436,7 +482,7 @@ __device__ __forceinline__ void chunk_intra_body(const Tin* __restrict__ q, cons
                 const int col = 16 * (2 * wave + t) + n;
                 *(f32x4*)(u + u_frag(16 * rb + 4 * gq, col)) = au;
 #pragma unroll
-                for (int j = 0; j < 4; j++) Ks[16 * rb + 4 * gq + j][col] = (half_t)aw[j];
+                for (int j = 0; j < 4; j++) Wst[16 * rb + 4 * gq + j][col] = (half_t)aw[j];
             }
         }
         __syncthreads();
@@ -447,7 +493,7 @@ __device__ __forceinline__ void chunk_intra_body(const Tin* __restrict__ q, cons
             const int f = tid + 256 * it;
             int r, c0;
             afrag_coords(f, 4, r, c0);
-            wf[f] = ld_h8(&Ks[r][c0]);
+            wf[f] = ld_h8(&Wst[r][c0]);
         }
     }
 }
@@ -582,18 +628,25 @@ __device__ __forceinline__ void chunk_state_body(const unsigned char* __restrict
             }
         __syncthreads();
 
-        // (2) w S and q_n S for chunk rows [16 wave, 16 wave + 16)
+        // (2) w S, then q_n S, for chunk rows [16 wave, 16 wave + 16): v_new needs only w S, so
+        // its VALU work overlaps the q_n S products in the MFMA pipe
+        half8 sb[NCT][4];
+#pragma unroll
+        for (int ct = 0; ct < NCT; ct++)
+#pragma unroll
+            for (int ks = 0; ks < 4; ks++) sb[ct][ks] = ld_h8(&SsT[pb][16 * ct + n][32 * ks + 8 * gq]);
         f32x4 WS[NCT], QS[NCT];
 #pragma unroll
         for (int ct = 0; ct < NCT; ct++) {
             WS[ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < 4; ks++) WS[ct] = mfma16(wa[ks], sb[ct][ks], WS[ct]);
+        }
+#pragma unroll
+        for (int ct = 0; ct < NCT; ct++) {
             QS[ct] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int ks = 0; ks < 4; ks++) {
-                half8 sb = ld_h8(&SsT[pb][16 * ct + n][32 * ks + 8 * gq]);
-                WS[ct] = mfma16(wa[ks], sb, WS[ct]);
-                QS[ct] = mfma16(qa[ks], sb, QS[ct]);
-            }
+            for (int ks = 0; ks < 4; ks++) QS[ct] = mfma16(qa[ks], sb[ct][ks], QS[ct]);
         }
         issue(0);
         // (3) v_new = u - w S; decayed copy for the state update
@@ -612,15 +665,33 @@ __device__ __forceinline__ void chunk_state_body(const unsigned char* __restrict
         issue(1);
         __syncthreads();
 
-        // (4) o = e^{cum} q_n S + intra v_new
+        // (4) intra v_new, then (5) S = e^{cum_last} S + k_n^T v' in the MFMA pipe; the output
+        // staging and stores below overlap the state update
+        f32x4 ov[NCT];
 #pragma unroll
         for (int ct = 0; ct < NCT; ct++) {
-            f32x4 o = f32x4{0.f, 0.f, 0.f, 0.f};
+            ov[ct] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int ks = 0; ks < 2; ks++) o = mfma16(ia[ks], ld_h8(&VnT[pb][16 * ct + n][32 * ks + 8 * gq]), o);
-#pragma unroll
-            for (int j = 0; j < 4; j++) Ot[wave][4 * gq + j][16 * ct + n] = cur.ecum[j] * QS[ct][j] + o[j];
+            for (int ks = 0; ks < 2; ks++) ov[ct] = mfma16(ia[ks], ld_h8(&VnT[pb][16 * ct + n][32 * ks + 8 * gq]), ov[ct]);
         }
+        {
+            const float gamma = cur.gamma;
+#pragma unroll
+            for (int rt = 0; rt < 2; rt++)
+#pragma unroll
+                for (int ct = 0; ct < NCT; ct++) {
+                    f32x4 acc = S[rt][ct] * gamma;
+#pragma unroll
+                    for (int ks = 0; ks < 2; ks++)
+                        acc = mfma16(cur.ka[rt][ks], ld_h8(&VdT[pb][16 * ct + n][32 * ks + 8 * gq]), acc);
+                    S[rt][ct] = acc;
+                }
+        }
+        // o = e^{cum} q_n S + intra v_new
+#pragma unroll
+        for (int ct = 0; ct < NCT; ct++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) Ot[wave][4 * gq + j][16 * ct + n] = cur.ecum[j] * QS[ct][j] + ov[ct][j];
         wave_sync();
         {   // this wave's 16 rows x 16 NCT columns: lane = (row, 8-column part), 64 / LPR rows
             // per pass
@@ -667,17 +738,6 @@ __device__ __forceinline__ void chunk_state_body(const unsigned char* __restrict
             }
         }
         issue(2);
-        // (5) S = e^{cum_last} S + k_n^T v'
-        const float gamma = cur.gamma;
-#pragma unroll
-        for (int rt = 0; rt < 2; rt++)
-#pragma unroll
-            for (int ct = 0; ct < NCT; ct++) {
-                f32x4 acc = S[rt][ct] * gamma;
-#pragma unroll
-                for (int ks = 0; ks < 2; ks++) acc = mfma16(cur.ka[rt][ks], ld_h8(&VdT[pb][16 * ct + n][32 * ks + 8 * gq]), acc);
-                S[rt][ct] = acc;
-            }
         issue(3);
     };
     // the first chunk's operands in the order the loop refills them, with a discarded store where
