@@ -509,6 +509,20 @@ __device__ __forceinline__ void split_pairs(float x0, float x1, bf16x8& hi, bf16
 // V[32 ks + 4 g + e][16 db + d] (e < 4), then V[32 ks + 16 + 4 g + e][16 db + d]. In a transpose
 // read lane k addresses row R + k / 4, dims C + 4 (k % 4) .. +3; lane j receives rows R .. R + 3
 // of dim C + j.
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));  // (HIP's uint4 blocks register promotion)
+
+// 8 bf16 (one 16-byte chunk of a cache row) -> 8 fp16, exact for |x| in fp16's normal range
+// (bf16's 8-bit significand fits fp16's 11); the prefill kernel stages K and V tiles as fp16
+__device__ __forceinline__ u32x4 bf8_to_f16(u32x4 x) {
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    u32x4 r;
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+        r[i] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f2{bf_lo(x[i]), bf_hi(x[i])}), h2));
+    return r;
+}
+
 __device__ __forceinline__ bf16x8 vt_operand(const uint16_t* vt, int ks, int db, int lane) {
     const int g = lane / 16, k = lane % 16;
     const uint16_t* p = vt + (size_t)(32 * ks + 4 * g + (k >> 2)) * VLD + 16 * db + 4 * (k & 3);
@@ -542,8 +556,8 @@ __global__ void __launch_bounds__(64 * PW) attn_prefill_mfma_kernel(const float*
     const uint16_t* kbase = kc + ((size_t)b * KV + kvh) * (size_t)cap * HD;
     const uint16_t* vbase = vc + ((size_t)b * KV + kvh) * (size_t)cap * HD;
 
-    // q operand (B of S^T): query n of this wave, dims 32 ks + 8 g .. +8, as bf16 hi + lo
-    bf16x8 qh[8], ql[8];
+    // q operand (B of S^T): query n of this wave, dims 32 ks + 8 g .. +8, as fp16
+    half8 qf[8];
     {
         const int t = min(q0 + 16 * wave + n, T - 1);
         const float* qr = q + b * qs.b + (long long)t * qs.t + h * qs.h;
@@ -553,10 +567,8 @@ __global__ void __launch_bounds__(64 * PW) attn_prefill_mfma_kernel(const float*
         for (int ks = 0; ks < 8; ks++) {
             const float4 a0 = *(const float4*)(qr + 32 * ks + 8 * g);
             const float4 a1 = *(const float4*)(qr + 32 * ks + 8 * g + 4);
-            split_pairs(a0.x * sl, a0.y * sl, qh[ks], ql[ks], 0);
-            split_pairs(a0.z * sl, a0.w * sl, qh[ks], ql[ks], 2);
-            split_pairs(a1.x * sl, a1.y * sl, qh[ks], ql[ks], 4);
-            split_pairs(a1.z * sl, a1.w * sl, qh[ks], ql[ks], 6);
+            qf[ks] = half8{(_Float16)(a0.x * sl), (_Float16)(a0.y * sl), (_Float16)(a0.z * sl), (_Float16)(a0.w * sl),
+                           (_Float16)(a1.x * sl), (_Float16)(a1.y * sl), (_Float16)(a1.z * sl), (_Float16)(a1.w * sl)};
         }
     }
     const int qpos = pos + q0 + 16 * wave + n;  // this lane's query position in the cache
@@ -573,7 +585,6 @@ __global__ void __launch_bounds__(64 * PW) attn_prefill_mfma_kernel(const float*
     constexpr int NSTEP = (PK * HD) / (8 * 64 * PW);
     constexpr int RSTEP = 64 * PW / (HD / 8);  // key rows between a thread's chunks
     const int r_own = tid / (HD / 8), c_own = (tid % (HD / 8)) * 8;
-    typedef unsigned u32x4 __attribute__((ext_vector_type(4)));  // (HIP's uint4 blocks register promotion)
     u32x4 kreg[NSTEP], vreg[NSTEP];
 #pragma unroll
     for (int it = 0; it < NSTEP; it++) {
@@ -587,8 +598,8 @@ __global__ void __launch_bounds__(64 * PW) attn_prefill_mfma_kernel(const float*
 #pragma unroll
         for (int it = 0; it < NSTEP; it++) {
             const int r = r_own + it * RSTEP;
-            *(u32x4*)&Kt[r * KLD + c_own] = kreg[it];
-            *(u32x4*)&Vt[r * VLD + c_own] = vreg[it];
+            *(u32x4*)&Kt[r * KLD + c_own] = bf8_to_f16(kreg[it]);
+            *(u32x4*)&Vt[r * VLD + c_own] = bf8_to_f16(vreg[it]);
         }
         __syncthreads();
         {   // next tile (unconditional: static wait counts)
@@ -608,9 +619,8 @@ __global__ void __launch_bounds__(64 * PW) attn_prefill_mfma_kernel(const float*
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int ks = 0; ks < 8; ks++) {
-                const bf16x8 kb = *(const bf16x8*)&Kt[(16 * nb + n) * KLD + 32 * ks + 8 * g];
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kb, qh[ks], acc, 0, 0, 0);
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kb, ql[ks], acc, 0, 0, 0);
+                const half8 kb = *(const half8*)&Kt[(16 * nb + n) * KLD + 32 * ks + 8 * g];
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kb, qf[ks], acc, 0, 0, 0);
             }
 #pragma unroll
             for (int j = 0; j < 4; j++) sc[nb][j] = key0 + 16 * nb + 4 * g + j <= qpos ? acc[j] : -INFINITY;
@@ -629,20 +639,19 @@ __global__ void __launch_bounds__(64 * PW) attn_prefill_mfma_kernel(const float*
         const float corr = exp2f(m_run - ref);
         const bool moved = mn != m_run;
         m_run = mn;
-        // P^T operand of step ks: keys 4 g + e of block 2 ks (e < 4), then of block 2 ks + 1;
-        // hi = p truncated to bf16 (exact remainder), lo = the remainder rounded to bf16
-        bf16x8 ph[2], pl[2];
+        // P^T operand of step ks: keys 4 g + e of block 2 ks (e < 4), then of block 2 ks + 1, as
+        // fp16 (p in [0, 1]: 11 significant bits); the row sum takes the fp32 values
+        half8 pf[2];
         float ps = 0.f;
 #pragma unroll
         for (int ks = 0; ks < 2; ks++)
 #pragma unroll
-            for (int e = 0; e < 8; e += 2) {
+            for (int e = 0; e < 8; e++) {
                 const int nb = 2 * ks + (e >> 2), j = e & 3;
                 // arguments <= 0 (or -inf): the hardware exp2 needs no range fix-up here
-                const float p0 = __builtin_amdgcn_exp2f(sc[nb][j] - ref);
-                const float p1 = __builtin_amdgcn_exp2f(sc[nb][j + 1] - ref);
-                ps += p0 + p1;
-                split_pairs(p0, p1, ph[ks], pl[ks], e);
+                const float p = __builtin_amdgcn_exp2f(sc[nb][j] - ref);
+                ps += p;
+                pf[ks][e] = (_Float16)p;
             }
         l_part = l_part * corr + ps;
         if (__ballot(moved)) {
@@ -656,9 +665,8 @@ __global__ void __launch_bounds__(64 * PW) attn_prefill_mfma_kernel(const float*
         for (int db = 0; db < 16; db++)
 #pragma unroll
             for (int ks = 0; ks < 2; ks++) {
-                const bf16x8 va = vt_operand(Vt, ks, db, lane);
-                oacc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, ph[ks], oacc[db], 0, 0, 0);
-                oacc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pl[ks], oacc[db], 0, 0, 0);
+                const half8 va = __builtin_bit_cast(half8, vt_operand(Vt, ks, db, lane));
+                oacc[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pf[ks], oacc[db], 0, 0, 0);
             }
     }
     // ---- normalise, gate, store: lane holds query n, dims 16 db + 4 g .. +4
