@@ -580,6 +580,7 @@ __global__ void __launch_bounds__(64 * PW) attn_prefill_mfma_kernel(const float*
     const int last_key = pos + min(q0 + PQ, T) - 1;  // keys [0, last_key] are visible to this block
     const int ntiles = last_key / PK + 1;
     const int wave_last = pos + min(q0 + 16 * wave + 15, T - 1);  // the last key this wave's rows see
+    const int wave_first = pos + q0 + 16 * wave;                  // keys up to here need no mask
     // Tile staging: 16-byte chunk c8 of key row r; the next tile is held in registers, requested
     // a full tile ahead.
     constexpr int NSTEP = (PK * HD) / (8 * 64 * PW);
@@ -622,8 +623,15 @@ __global__ void __launch_bounds__(64 * PW) attn_prefill_mfma_kernel(const float*
                 const half8 kb = *(const half8*)&Kt[(16 * nb + n) * KLD + 32 * ks + 8 * g];
                 acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kb, qf[ks], acc, 0, 0, 0);
             }
+            sc[nb] = acc;
+        }
+        // causal mask, only on a tile that reaches past this wave's first query
+        if (key0 + PK - 1 > wave_first) {
 #pragma unroll
-            for (int j = 0; j < 4; j++) sc[nb][j] = key0 + 16 * nb + 4 * g + j <= qpos ? acc[j] : -INFINITY;
+            for (int nb = 0; nb < 4; nb++)
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+                    if (key0 + 16 * nb + 4 * g + j > qpos) sc[nb][j] = -INFINITY;
         }
         // ---- online softmax for query n (its 64 keys over this lane's 16 and lanes n + 16 g)
         float mt = sc[0][0];
