@@ -76,7 +76,7 @@ FLOP_PER_HEAD_CHUNK = 2 * 64 * 64 * 128 + 2 * (64 * 63 // 2) * 128 * 2 + 2 * 64 
     + 2 * 64 * 64 * 128
 
 
-def bench_prefill(torch, ops, dev, reps=10):
+def bench_prefill(torch, ops, dev, reps=40):
     """Config 2: chunked DeltaNet prefill, B=1, T=8192, 16 QK / 32 V heads, bf16 q/k/v
     (normalised in-kernel), fp32 state; one layer per call."""
     bf = torch.bfloat16
@@ -153,7 +153,7 @@ def bench_attention_decode(torch, ops, dev, reps=20):
             "note": "L=4096 at B=1 (8 MB) is MALL-resident and launch-bound"}
 
 
-def bench_attention_prefill(torch, ops, dev, T=2048, reps=10):
+def bench_attention_prefill(torch, ops, dev, T=2048, reps=40):
     """Causal gated GQA prefill (config 4's attention layers): T=2048, 16 q heads, 2 KV heads,
     HD 256, cache rows [0, T), at B=1 (the headline fields) and at config 4's B=16 (`points`).
     FLOPs = 4 * B * H * HD * T (T + 1) / 2 (QK^T and PV)."""
