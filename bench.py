@@ -45,9 +45,19 @@ def cpu_threads() -> int:
         return os.cpu_count() or 1
 
 
-def cpu_baseline_decode(torch):
+def _errs(torch, x, ref):
+    """Norm-wise max relative error max|x - ref| / max|ref| and the element-wise
+    max |x - ref| / (|ref| + 1e-3 max|ref|), on fp32 (pre-rounding) outputs."""
+    x, ref = x.detach().double().cpu(), ref.detach().double().cpu()
+    d, m = (x - ref).abs(), ref.abs().max().item()
+    return {"norm": float(d.max().item() / m), "elem": float((d / (ref.abs() + 1e-3 * m)).max().item())}
+
+
+def cpu_baseline_decode(torch, ops=None, dev=None):
     """The oracle's fused decode step (torch-CPU fp32) on one layer at batch 64; 2 warm-ups,
-    median of 5; scaled to 30 layers."""
+    median of 5; scaled to 30 layers. With a device it is also the checker: the first (untimed)
+    call's outputs are compared with the HIP kernel's on the same inputs (config 1's layer), and
+    config 2's full 8k chunked prefill is compared with the oracle's chunked form."""
     from oracle import mixer_ref as R
     torch.set_num_threads(cpu_threads())
     g_ = torch.Generator().manual_seed(0)
@@ -57,6 +67,14 @@ def cpu_baseline_decode(torch):
     g = -torch.nn.functional.softplus(torch.randn(B, HV, generator=g_))
     beta = torch.sigmoid(torch.randn(B, HV, generator=g_))
     S = torch.randn(B, HV, D, D, generator=g_) * 0.02
+    parity = None
+    if dev is not None:
+        Sd, csd = S.to(dev), cs.to(dev)
+        od = ops.delta_decode_step(qkv.to(dev), w.to(dev), csd, g.to(dev), beta.to(dev), Sd, HK, HV)
+        S0 = S.clone()
+        o0, cs0 = R.delta_decode_fused(qkv, w, cs, g, beta, S0, HK, HV, D)
+        parity = {"config1_decode": {"o": _errs(torch, od, o0), "state": _errs(torch, Sd, S0),
+                                     "conv_state_exact": bool(torch.equal(csd.cpu(), cs0))}}
     times = []
     for i in range(7):
         t0 = time.perf_counter()
@@ -64,9 +82,30 @@ def cpu_baseline_decode(torch):
         if i >= 2:
             times.append(time.perf_counter() - t0)
     per_layer = statistics.median(times)
-    return {"value": B / (per_layer * LAYERS), "unit": "tok/s", "cores": cpu_threads(), "kind": "port",
-            "sample": f"1 of {LAYERS} layers at B={B} (oracle.mixer_ref.delta_decode_fused, torch-CPU fp32), "
-                      f"median of 5 after 2 warm-ups, scaled x{LAYERS}; {per_layer * 1e3:.1f} ms per layer"}
+    out = {"value": B / (per_layer * LAYERS), "unit": "tok/s", "cores": cpu_threads(), "kind": "port",
+           "sample": f"1 of {LAYERS} layers at B={B} (oracle.mixer_ref.delta_decode_fused, torch-CPU fp32), "
+                     f"median of 5 after 2 warm-ups, scaled x{LAYERS}; {per_layer * 1e3:.1f} ms per layer"}
+    if dev is not None:
+        parity["config2_prefill"] = prefill_parity(torch, ops, dev, R)
+        out["parity"] = parity
+    return out
+
+
+def prefill_parity(torch, ops, dev, R):
+    """Config 2 at full size (B=1, T=8192, bf16 q/k/v normalised in-kernel, zero state): the HIP
+    chunked prefill (fp32 output) against the oracle's chunked form on the same values."""
+    bf = torch.bfloat16
+    q = ops.fill_normal(torch.empty(1, PREFILL_T, HK, D, device=dev, dtype=bf), 7101).transpose(1, 2)
+    k = ops.fill_normal(torch.empty(1, PREFILL_T, HK, D, device=dev, dtype=bf), 7102).transpose(1, 2)
+    v = ops.fill_normal(torch.empty(1, PREFILL_T, HV, D, device=dev, dtype=bf), 7103).transpose(1, 2)
+    g = -torch.nn.functional.softplus(ops.fill_normal(torch.empty(1, HV, PREFILL_T, device=dev), 7104))
+    beta = torch.sigmoid(ops.fill_normal(torch.empty(1, HV, PREFILL_T, device=dev), 7105))
+    od, Sd = ops.delta_rule_chunked(q, k, v, g, beta, None, normalize=True, qscale=D ** -0.5)
+    rep = HV // HK
+    qc = R.l2norm(q.float().cpu().repeat_interleave(rep, 1), 1e-6) * D ** -0.5
+    kc = R.l2norm(k.float().cpu().repeat_interleave(rep, 1), 1e-6)
+    oc, Sc = R.delta_rule_chunked(qc, kc, v.float().cpu(), g.cpu(), beta.cpu(), None)
+    return {"o": _errs(torch, od, oc), "state": _errs(torch, Sd, Sc)}
 
 
 PREFILL_T = 8192
@@ -506,7 +545,7 @@ def main():
         dst.copy_(src)
         torch.cuda.synchronize()
     if not args.no_cpu:
-        res["cpu_baseline"] = cpu_baseline_decode(torch)
+        res["cpu_baseline"] = cpu_baseline_decode(torch, ops, dev)
     print(json.dumps(res), flush=True)
 
 
