@@ -764,10 +764,10 @@ int launch_prefill_core(const float* q, Strides3 qs, const uint16_t* kc, const u
 
 // Wrappers for the layer stack: qn [B, T, H, HD], gate inside qg [B, T, H, 2 HD] (+HD),
 // out [B, T, H, HD] fp32.
-int stack_attn_decode(const float* qn, const uint16_t* kc, const uint16_t* vc, const float* qg, float* out, int B,
+int stack_attn_decode(const float* qn, const uint16_t* kc, const uint16_t* vc, const float* qg, uint16_t* out, int B,
                       int H, int KV, int L, int cap, float scale, void* ws, size_t ws_bytes, hipStream_t st) {
-    return launch_decode_core<float, float>(qn, kc, vc, qg + HD, 2 * HD, out, HD, B, H, KV, L, cap, scale, ws,
-                                            ws_bytes, st);
+    return launch_decode_core<float, uint16_t>(qn, kc, vc, qg + HD, 2 * HD, out, HD, B, H, KV, L, cap, scale, ws,
+                                               ws_bytes, st);
 }
 int stack_attn_prefill(const float* qn, const uint16_t* kc, const uint16_t* vc, const float* qg, float* out, int B,
                        int H, int KV, int T, int pos, int cap, float scale, hipStream_t st) {

@@ -43,16 +43,30 @@ __device__ __forceinline__ void st_stream(float* p, float4 v) {
     __builtin_nontemporal_store(v.w, p + 3);
 }
 
-template <int R, typename Tin, typename Tout>
+// Layer-stack form (kStack): the gates come from the b / a projection rows instead of g / beta
+// arrays (beta = sigmoid(b), g = -exp(A_log) softplus(a + dt_bias), as gates_from_proj), and the
+// output row of each value head goes through the gated norm w * rmsnorm(o) * silu(z) into bf16
+// (as gated_norm_bf16) inside the kernel: three launches of the stack's decode step become one.
+struct StackGates {
+    const float* ba;          // [B, 2 HV]: b, then a
+    const uint16_t* a_log;    // [HV] bf16
+    const uint16_t* dt_bias;  // [HV] bf16
+    const float* z;           // [B, HV * D]
+    const uint16_t* gnorm_w;  // [D] bf16
+    float gnorm_eps;
+};
+
+template <int R, typename Tin, typename Tout, bool kStack = false>
 __global__ void __launch_bounds__(256 * R) delta_decode_kernel(
     const Tin* __restrict__ qkv, const uint16_t* __restrict__ conv_w, float* __restrict__ conv_state,
     const float* __restrict__ g, const float* __restrict__ beta, float* __restrict__ state, Tout* __restrict__ out,
-    int HK, int HV, float qscale, float eps) {
+    int HK, int HV, float qscale, float eps, StackGates sg) {
     constexpr int NT = 256 * R;
     constexpr int NCH = 2 * D + R * D;
     __shared__ float sq[D], sk[D], sv[R][D];
     __shared__ float red[8];
     __shared__ float4 part[2][R][4][2][8];
+    __shared__ float so[kStack ? R : 1][kStack ? D : 1];
 
     const int kh = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
     const int C = 2 * HK * D + HV * D;
@@ -109,7 +123,17 @@ __global__ void __launch_bounds__(256 * R) delta_decode_kernel(
     }
     __syncthreads();
     const float kq = red[4] + red[5];
-    const float decay = expf(g[(size_t)b * HV + hv]), bt = beta[(size_t)b * HV + hv];
+    float decay, bt;
+    if constexpr (kStack) {
+        const float bb = sg.ba[(size_t)b * 2 * HV + hv], aa = sg.ba[(size_t)b * 2 * HV + HV + hv];
+        bt = 1.f / (1.f + expf(-bb));
+        const float xx = aa + bf2f(sg.dt_bias[hv]);
+        const float sp = xx > 20.f ? xx : log1pf(expf(xx));
+        decay = expf(-expf(bf2f(sg.a_log[hv])) * sp);
+    } else {
+        decay = expf(g[(size_t)b * HV + hv]);
+        bt = beta[(size_t)b * HV + hv];
+    }
     float kr[4], qr[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
@@ -167,11 +191,36 @@ __global__ void __launch_bounds__(256 * R) delta_decode_kernel(
             for (int i = 0; i < 4; i++) s[j & 1][i] = ld_stream(S + (size_t)(rbase + 32 * i) * D + 32 * (j + 2) + cg * 4);
         }
         if (w4 == 0 && rr == 0) {
-            Tout* o = out + ((size_t)b * HV + hv) * D + 32 * j + cg * 4;
-            Act<Tout>::st(o, 0, decay * SQ.x + kq * dl.x);
-            Act<Tout>::st(o, 1, decay * SQ.y + kq * dl.y);
-            Act<Tout>::st(o, 2, decay * SQ.z + kq * dl.z);
-            Act<Tout>::st(o, 3, decay * SQ.w + kq * dl.w);
+            if constexpr (kStack) {
+                float* o = so[hl] + 32 * j + cg * 4;
+                o[0] = decay * SQ.x + kq * dl.x;
+                o[1] = decay * SQ.y + kq * dl.y;
+                o[2] = decay * SQ.z + kq * dl.z;
+                o[3] = decay * SQ.w + kq * dl.w;
+            } else {
+                Tout* o = out + ((size_t)b * HV + hv) * D + 32 * j + cg * 4;
+                Act<Tout>::st(o, 0, decay * SQ.x + kq * dl.x);
+                Act<Tout>::st(o, 1, decay * SQ.y + kq * dl.y);
+                Act<Tout>::st(o, 2, decay * SQ.z + kq * dl.z);
+                Act<Tout>::st(o, 3, decay * SQ.w + kq * dl.w);
+            }
+        }
+    }
+    if constexpr (kStack) {
+        // gated norm of this head's output row by the head's first wave, in gated_norm_bf16's
+        // order (lane sums elements lane and lane + 64, then the wave sum)
+        __syncthreads();
+        if (w4 == 0) {
+            const float* o = so[hl];
+            float ss = 0.f;
+            for (int i = lane; i < D; i += WAVE) ss += o[i] * o[i];
+            ss = wave_sum(ss);
+            const float r = rsqrtf(ss / (float)D + sg.gnorm_eps);
+            const size_t base = ((size_t)b * HV + hv) * D;
+            for (int i = lane; i < D; i += WAVE) {
+                const float zz = sg.z[base + i];
+                Act<Tout>::st(out, base + i, bf2f(sg.gnorm_w[i]) * (o[i] * r) * (zz / (1.f + expf(-zz))));
+            }
         }
     }
 }
@@ -182,10 +231,11 @@ int launch_out(const void* qkv, const uint16_t* w, float* cs, const float* g, co
     dim3 grid(HK, B);
     if (out_dtype == AEGIST_F32)
         delta_decode_kernel<R, Tin, float><<<grid, 256 * R, 0, st>>>((const Tin*)qkv, w, cs, g, beta, state,
-                                                                    (float*)out, HK, HV, qscale, eps);
+                                                                    (float*)out, HK, HV, qscale, eps, StackGates{});
     else if (out_dtype == AEGIST_BF16)
         delta_decode_kernel<R, Tin, uint16_t><<<grid, 256 * R, 0, st>>>((const Tin*)qkv, w, cs, g, beta, state,
-                                                                       (uint16_t*)out, HK, HV, qscale, eps);
+                                                                       (uint16_t*)out, HK, HV, qscale, eps,
+                                                                       StackGates{});
     else
         return fail(AEGIST_ERR_DTYPE, "delta_decode_step: out dtype must be AEGIST_F32 or AEGIST_BF16");
     return after_launch("delta_decode_step");
@@ -204,6 +254,35 @@ int launch_in(const void* qkv, int in_dtype, const uint16_t* w, float* cs, const
 }  // namespace
 
 namespace aegist {
+// The layer stack's decode step: fp32 qkv projection rows, gates from the b / a projection rows,
+// gated norm into the bf16 input of the out projection (ob [B, HV * 128]).
+int launch_delta_decode_stack(const float* qkv, const uint16_t* conv_w, float* conv_state, const float* ba,
+                              const uint16_t* a_log, const uint16_t* dt_bias, const float* z, const uint16_t* gnorm_w,
+                              float gnorm_eps, float* state, uint16_t* ob, int B, int HK, int HV, float qscale,
+                              float eps, hipStream_t st) {
+    if (B < 0 || HK <= 0 || HV <= 0 || HV % HK) return fail(AEGIST_ERR_SHAPE, "stack decode: need HV % HK == 0");
+    if (B == 0) return 0;
+    const StackGates sg{ba, a_log, dt_bias, z, gnorm_w, gnorm_eps};
+    const dim3 grid(HK, B);
+    switch (HV / HK) {
+        case 1:
+            delta_decode_kernel<1, float, uint16_t, true><<<grid, 256, 0, st>>>(qkv, conv_w, conv_state, nullptr, nullptr,
+                                                                                state, ob, HK, HV, qscale, eps, sg);
+            break;
+        case 2:
+            delta_decode_kernel<2, float, uint16_t, true><<<grid, 512, 0, st>>>(qkv, conv_w, conv_state, nullptr, nullptr,
+                                                                                state, ob, HK, HV, qscale, eps, sg);
+            break;
+        case 4:
+            delta_decode_kernel<4, float, uint16_t, true><<<grid, 1024, 0, st>>>(qkv, conv_w, conv_state, nullptr,
+                                                                                 nullptr, state, ob, HK, HV, qscale, eps,
+                                                                                 sg);
+            break;
+        default: return fail(AEGIST_ERR_SHAPE, "stack decode: HV / HK must be 1, 2 or 4");
+    }
+    return after_launch("delta_decode_stack");
+}
+
 int launch_delta_decode(const void* qkv, int in_dtype, const uint16_t* conv_w, float* conv_state, const float* g,
                         const float* beta, float* state, void* out, int out_dtype, int B, int HK, int HV,
                         float qscale, float eps, hipStream_t st) {

@@ -27,10 +27,14 @@ int launch_gated_norm_bf16(const float* o, const float* z, const uint16_t* w, ui
 int launch_conv_silu_batched(const float* x, float* y, const uint16_t* w, float* state, int B, int T, int C,
                              hipStream_t st);
 int launch_embed_bf16(const uint16_t* table, const int* ids, float* out, int n, int D, hipStream_t st);
+int launch_delta_decode_stack(const float* qkv, const uint16_t* conv_w, float* conv_state, const float* ba,
+                              const uint16_t* a_log, const uint16_t* dt_bias, const float* z, const uint16_t* gnorm_w,
+                              float gnorm_eps, float* state, uint16_t* ob, int B, int HK, int HV, float qscale,
+                              float eps, hipStream_t st);
 int launch_attn_prep(const void* qg, const void* k, const void* v, int in_dtype, const uint16_t* qw,
                      const uint16_t* kw, float* qn, uint16_t* kc, uint16_t* vc, int B, int T, int H, int KV, int HD,
                      int RD, int pos0, int cap, float eps, float theta, hipStream_t stream, int* zero_ctr, int n_ctr);
-int stack_attn_decode(const float* qn, const uint16_t* kc, const uint16_t* vc, const float* qg, float* out, int B,
+int stack_attn_decode(const float* qn, const uint16_t* kc, const uint16_t* vc, const float* qg, uint16_t* out, int B,
                       int H, int KV, int L, int cap, float scale, void* ws, size_t ws_bytes, hipStream_t st);
 int stack_attn_prefill(const float* qn, const uint16_t* kc, const uint16_t* vc, const float* qg, float* out, int B,
                        int H, int KV, int T, int pos, int cap, float scale, hipStream_t st);
@@ -148,13 +152,16 @@ int delta_layer(Stack* s, const AegistLayerWeights& w, int sl, float* x, int B, 
         const long long ldy[4] = {C, HV * D, 2 * HV, 2 * HV};
         RC(gemm_group(s, s->hb, 4, W, Y, N, ldy, rows, dm, st));
     }
-    RC(launch_gates_from_proj(s->ba, w.a_log, w.dt_bias, s->g, s->beta, rows, HV, st));
     const float qscale = 1.f / sqrtf((float)D);
     if (T == 1) {
-        // decode: conv-state update + conv + SiLU + L2-norm + delta step, fused (hybrid.py:411-413)
-        RC(aegist_delta_decode_step(s->proj, AEGIST_F32, w.conv_w, conv, s->g, s->beta, rec, s->o, AEGIST_F32, B, HK,
-                                    HV, qscale, 1e-6f, st));
-    } else {
+        // decode: gates + conv-state update + conv + SiLU + L2-norm + delta step + gated norm,
+        // one launch (hybrid.py:401-419)
+        RC(launch_delta_decode_stack(s->proj, w.conv_w, conv, s->ba, w.a_log, w.dt_bias, s->z, w.gnorm_w, c.eps, rec,
+                                     s->ob, B, HK, HV, qscale, 1e-6f, st));
+        return gemm(s, s->ob, w.w_out, x, rows, dm, HV * D, dm, 1.f, st);
+    }
+    RC(launch_gates_from_proj(s->ba, w.a_log, w.dt_bias, s->g, s->beta, rows, HV, st));
+    {
         // prefill: conv over the chunk, then the fp32 token-by-token scan below 64 tokens (the
         // engine scans every length, hybrid.rs:845-852), the chunked WY form from 64 tokens up
         RC(launch_conv_silu_batched(s->proj, s->y, w.conv_w, conv, B, T, C, st));
@@ -190,12 +197,14 @@ int attn_layer(Stack* s, const AegistLayerWeights& w, int sl, float* x, int B, i
     RC(launch_attn_prep(s->proj, kp, vp, AEGIST_F32, w.q_norm, w.k_norm, s->y, kc, vc, B, T, H, KV, HD, c.rotary_dim,
                         s->length, (int)cap, c.eps, c.rope_theta, st, nullptr, 0));
     const float scale = 1.f / sqrtf((float)HD);
-    if (T == 1)
-        RC(stack_attn_decode(s->y, kc, vc, s->proj, s->o, B, H, KV, s->length + 1, (int)cap, scale, s->ws, s->ws_bytes,
-                             st));
-    else
+    if (T == 1) {
+        // the split / merge kernels write the gated output as bf16 (the out projection's input)
+        RC(stack_attn_decode(s->y, kc, vc, s->proj, s->ob, B, H, KV, s->length + 1, (int)cap, scale, s->ws,
+                             s->ws_bytes, st));
+    } else {
         RC(stack_attn_prefill(s->y, kc, vc, s->proj, s->o, B, H, KV, T, s->length, (int)cap, scale, st));
-    RC(launch_cast_bf16(s->o, s->ob, (size_t)rows * H * HD, st));
+        RC(launch_cast_bf16(s->o, s->ob, (size_t)rows * H * HD, st));
+    }
     return gemm(s, s->ob, w.w_o, x, rows, dm, H * HD, dm, 1.f, st);
 }
 
