@@ -304,6 +304,62 @@ __global__ void __launch_bounds__(256) znorm_bf16_kernel(const float* __restrict
     for (int i = threadIdx.x; i < D; i += 256) out[(size_t)blockIdx.x * D + i] = f2bf((xr[i] * inv) * (1.f + bf2f(w[i])));
 }
 
+// Row-resident ZNorm into bf16 for D % 1024 == 0, D <= 8192: each thread holds its D / 1024
+// 16-byte pieces of the row in registers (one read of x), block sum, 8-byte bf16 stores.
+template <int NV>
+__global__ void __launch_bounds__(256) znorm_bf16_vec_kernel(const float* __restrict__ x, const uint16_t* __restrict__ w,
+                                                             uint16_t* __restrict__ out, int D, float eps) {
+    __shared__ float red[4];
+    const float4* xr = (const float4*)(x + (size_t)blockIdx.x * D);
+    float4 v[NV];
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+        v[i] = xr[threadIdx.x + 256 * i];
+        ss += v[i].x * v[i].x + v[i].y * v[i].y + v[i].z * v[i].z + v[i].w * v[i].w;
+    }
+    ss = block_sum(ss, red);
+    const float inv = rsqrtf(ss / (float)D + eps);
+    uint2* orow = (uint2*)(out + (size_t)blockIdx.x * D);
+    const uint2* wr = (const uint2*)w;
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+        const int e = threadIdx.x + 256 * i;
+        const uint2 wp = wr[e];
+        orow[e] = uint2{f2bf2((v[i].x * inv) * (1.f + bf_lo(wp.x)), (v[i].y * inv) * (1.f + bf_hi(wp.x))),
+                        f2bf2((v[i].z * inv) * (1.f + bf_lo(wp.y)), (v[i].w * inv) * (1.f + bf_hi(wp.y)))};
+    }
+}
+
+// Gated norm into bf16 for DV % 128 == 0: half a wave (32 lanes, 16-byte loads) per (row, head).
+__global__ void __launch_bounds__(256) gated_norm_bf16_vec_kernel(const float* __restrict__ o,
+                                                                  const float* __restrict__ z,
+                                                                  const uint16_t* __restrict__ w,
+                                                                  uint16_t* __restrict__ out, int rows, int DV,
+                                                                  float eps) {
+    const int item = blockIdx.x * 8 + threadIdx.x / 32, l32 = threadIdx.x % 32;
+    const bool ok = item < rows;
+    const size_t base = (size_t)(ok ? item : 0) * DV;
+    float ss = 0.f;
+    for (int i = 4 * l32; i < DV; i += 128) {
+        const float4 a = *(const float4*)(o + base + i);
+        ss += a.x * a.x + a.y * a.y + a.z * a.z + a.w * a.w;
+    }
+#pragma unroll
+    for (int m = 16; m > 0; m >>= 1) ss += __shfl_xor(ss, m, WAVE);
+    if (!ok) return;
+    const float r = rsqrtf(ss / (float)DV + eps);
+    for (int i = 4 * l32; i < DV; i += 128) {
+        const float4 a = *(const float4*)(o + base + i);
+        const float4 zz = *(const float4*)(z + base + i);
+        const uint2 wp = *(const uint2*)(w + i);
+        auto gate = [](float v) { return v / (1.f + expf(-v)); };
+        *(uint2*)(out + base + i) =
+            uint2{f2bf2(bf_lo(wp.x) * (a.x * r) * gate(zz.x), bf_hi(wp.x) * (a.y * r) * gate(zz.y)),
+                  f2bf2(bf_lo(wp.y) * (a.z * r) * gate(zz.z), bf_hi(wp.y) * (a.w * r) * gate(zz.w))};
+    }
+}
+
 __global__ void cast_bf16_kernel(const float* __restrict__ x, uint16_t* __restrict__ y, size_t n) {
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
         y[i] = f2bf(x[i]);
@@ -391,7 +447,15 @@ __global__ void embed_bf16_kernel(const uint16_t* __restrict__ table, const int*
 namespace aegist {
 int launch_znorm_bf16(const float* x, const uint16_t* w, uint16_t* out, int rows, int D, float eps, hipStream_t st) {
     if (rows <= 0) return 0;
-    znorm_bf16_kernel<<<rows, 256, 0, st>>>(x, w, out, D, eps);
+    const bool vec = D % 1024 == 0 && D <= 8192 && (uintptr_t)x % 16 == 0 && (uintptr_t)out % 8 == 0 &&
+                     (uintptr_t)w % 8 == 0;
+    switch (vec ? D / 1024 : 0) {
+        case 1: znorm_bf16_vec_kernel<1><<<rows, 256, 0, st>>>(x, w, out, D, eps); break;
+        case 2: znorm_bf16_vec_kernel<2><<<rows, 256, 0, st>>>(x, w, out, D, eps); break;
+        case 4: znorm_bf16_vec_kernel<4><<<rows, 256, 0, st>>>(x, w, out, D, eps); break;
+        case 8: znorm_bf16_vec_kernel<8><<<rows, 256, 0, st>>>(x, w, out, D, eps); break;
+        default: znorm_bf16_kernel<<<rows, 256, 0, st>>>(x, w, out, D, eps);
+    }
     return after_launch("znorm_bf16");
 }
 int launch_cast_bf16(const float* x, uint16_t* y, size_t n, hipStream_t st) {
@@ -409,7 +473,11 @@ int launch_gates_from_proj(const float* ba, const uint16_t* a_log, const uint16_
 int launch_gated_norm_bf16(const float* o, const float* z, const uint16_t* w, uint16_t* out, int rows, int DV,
                            float eps, hipStream_t st) {
     if (rows <= 0) return 0;
-    gated_norm_bf16_kernel<<<(rows + 3) / 4, 256, 0, st>>>(o, z, w, out, rows, DV, eps);
+    if (DV % 128 == 0 && (uintptr_t)o % 16 == 0 && (uintptr_t)z % 16 == 0 && (uintptr_t)out % 8 == 0 &&
+        (uintptr_t)w % 8 == 0)
+        gated_norm_bf16_vec_kernel<<<(rows + 7) / 8, 256, 0, st>>>(o, z, w, out, rows, DV, eps);
+    else
+        gated_norm_bf16_kernel<<<(rows + 3) / 4, 256, 0, st>>>(o, z, w, out, rows, DV, eps);
     return after_launch("gated_norm_bf16");
 }
 int launch_conv_silu_batched(const float* x, float* y, const uint16_t* w, float* state, int B, int T, int C,
