@@ -45,10 +45,13 @@ struct DecodeSplit {
 // Splits sized so a launch has about 256 workgroups (one round of one workgroup per CU: the
 // kernel runs one wave per SIMD), each split a multiple of 128 keys (one 32-key tile per wave
 // per step), at most 256 splits per (sequence, KV head).
+#ifndef ATTN_SPLIT_TARGET
+#define ATTN_SPLIT_TARGET 192  // workgroups per decode launch the split count aims for (measured: 160-192 beat 128 and 224-1024)
+#endif
 DecodeSplit choose_split(int B, int KV, int L) {
     int units = std::max(1, B * KV);
     int max_split = std::min(256, std::max(1, (L + 127) / 128));
-    int ns = std::min(max_split, std::max(1, (256 + units - 1) / units));
+    int ns = std::min(max_split, std::max(1, (ATTN_SPLIT_TARGET + units - 1) / units));
     int per = (L + ns - 1) / ns;
     per = (per + 127) / 128 * 128;
     ns = (L + per - 1) / per;
