@@ -83,3 +83,36 @@ def test_stack_rejects_overflow(dev):
     stack.reset()
     assert stack.length == 0
     stack.close()
+
+
+@pytest.mark.parametrize("hk,hv", [(2, 2), (1, 4)])
+def test_stack_head_ratios(dev, hk, hv):
+    """The stack's fused decode core is built per value-to-QK head ratio (1, 2, 4): a 70-token
+    prefill (chunked path) and 3 decode steps at batch 2 against the oracle, for ratios 1 and 4."""
+    global CFG
+    saved = CFG
+    CFG = dict(saved, hk=hk, hv=hv)
+    try:
+        B, T, steps, cap = 2, 70, 3, 96
+        layers, dl = make_layers(5, dev)
+        c = CFG
+        C = 2 * hk * 128 + hv * 128
+        nd, na = KINDS.count("delta"), KINDS.count("attn")
+        cache = {"length": 0,
+                 "conv": [torch.zeros(B, C, 3) for _ in range(nd)],
+                 "state": [torch.zeros(B, hv, 128, 128) for _ in range(nd)],
+                 "k": [torch.zeros(B, c["n_kv"], cap, 256, dtype=torch.bfloat16) for _ in range(na)],
+                 "v": [torch.zeros(B, c["n_kv"], cap, 256, dtype=torch.bfloat16) for _ in range(na)]}
+        stack = ops.HybridStack(c, KINDS, dl, max_batch=B, max_tokens=B * T, max_context=cap)
+        g_ = torch.Generator().manual_seed(6)
+        for n in [T] + [1] * steps:
+            x = torch.randn(B, n, c["d_model"], generator=g_)
+            ref = R.hybrid_stack_forward(x.clone(), layers, KINDS, cache, c)
+            xd = x.to(dev)
+            stack.forward(xd)
+            torch.cuda.synchronize()
+            err = rel_err(xd - x.to(dev), ref - x)
+            assert err < 1e-2, (n, err)
+        stack.close()
+    finally:
+        CFG = saved
