@@ -275,7 +275,7 @@ def test_engine_delta_scan_long_prompt(dev):
 
 
 def test_chunked_multi_segment_on_side_stream(dev):
-    """Two 5000-token calls (3 segments each, so the overlapped two-stream schedule runs) on a
+    """Two 5000-token calls (3 segments each, so the fused K2 + next-segment K1 launches run) on a
     non-default stream, the second continuing from the first's state: equals the oracle over
     the 10000-token sequence. Small heads keep the CPU oracle quick."""
     HK, HV, T = 2, 4, 5000
