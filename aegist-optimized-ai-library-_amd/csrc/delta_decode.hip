@@ -79,9 +79,12 @@ __global__ void __launch_bounds__(256 * R) delta_decode_kernel(
     const int rbase = w4 * 8 + rr;
 
     // ---- 0. start streaming column slices 0 and 1 before the conv (independent of it)
-    float4 s[2][4];
+    // column slices in flight: two (4 workgroups' worth of state per CU at batch 64), all four in
+    // the stack form, whose batch-16 grid is a single round of one workgroup per CU
+    constexpr int NSF = kStack ? 4 : 2;
+    float4 s[NSF][4];
 #pragma unroll
-    for (int j = 0; j < 2; j++)
+    for (int j = 0; j < NSF; j++)
 #pragma unroll
         for (int i = 0; i < 4; i++) s[j][i] = ld_stream(S + (size_t)(rbase + 32 * i) * D + 32 * j + cg * 4);
 
@@ -147,7 +150,7 @@ __global__ void __launch_bounds__(256 * R) delta_decode_kernel(
         float4 pk = {0.f, 0.f, 0.f, 0.f}, pq = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const float4 x = s[j & 1][i];
+            const float4 x = s[j % NSF][i];
             pk.x += x.x * kr[i]; pk.y += x.y * kr[i]; pk.z += x.z * kr[i]; pk.w += x.w * kr[i];
             pq.x += x.x * qr[i]; pq.y += x.y * qr[i]; pq.z += x.z * qr[i]; pq.w += x.w * qr[i];
         }
@@ -178,7 +181,7 @@ __global__ void __launch_bounds__(256 * R) delta_decode_kernel(
         dl.w = (vv[3] - decay * SK.w) * bt;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const float4 x = s[j & 1][i];
+            const float4 x = s[j % NSF][i];
             float4 n;
             n.x = decay * x.x + kr[i] * dl.x;
             n.y = decay * x.y + kr[i] * dl.y;
@@ -186,9 +189,10 @@ __global__ void __launch_bounds__(256 * R) delta_decode_kernel(
             n.w = decay * x.w + kr[i] * dl.w;
             st_stream(S + (size_t)(rbase + 32 * i) * D + 32 * j + cg * 4, n);
         }
-        if (j < 2) {
+        if (j + NSF < 4) {
 #pragma unroll
-            for (int i = 0; i < 4; i++) s[j & 1][i] = ld_stream(S + (size_t)(rbase + 32 * i) * D + 32 * (j + 2) + cg * 4);
+            for (int i = 0; i < 4; i++)
+                s[j % NSF][i] = ld_stream(S + (size_t)(rbase + 32 * i) * D + 32 * (j + NSF) + cg * 4);
         }
         if (w4 == 0 && rr == 0) {
             if constexpr (kStack) {
