@@ -493,21 +493,6 @@ constexpr int KLD = HD + 8, VLD = HD + 16;
 
 typedef short short4v __attribute__((ext_vector_type(4)));
 
-// x0, x1 -> elements e, e + 1 of hi and lo: hi = x truncated to bf16 (so x - hi is exact in
-// fp32), lo = that remainder rounded to bf16; hi + lo carries ~16 significant bits of x
-__device__ __forceinline__ void split_pairs(float x0, float x1, bf16x8& hi, bf16x8& lo, int e) {
-    typedef float f2 __attribute__((ext_vector_type(2)));
-    typedef __bf16 b2 __attribute__((ext_vector_type(2)));
-    const uint32_t u0 = __float_as_uint(x0), u1 = __float_as_uint(x1);
-    const f2 r = {x0 - __uint_as_float(u0 & 0xffff0000u), x1 - __uint_as_float(u1 & 0xffff0000u)};
-    const uint32_t lp = __builtin_bit_cast(uint32_t, __builtin_convertvector(r, b2));
-    const uint32_t hp = __builtin_amdgcn_perm(u1, u0, 0x07060302u);
-    hi[e] = (short)(hp & 0xffffu);
-    hi[e + 1] = (short)(hp >> 16);
-    lo[e] = (short)(lp & 0xffffu);
-    lo[e + 1] = (short)(lp >> 16);
-}
-
 // A operand of O^T += V^T P^T for P V step ks and dim block db: lane (d, g) gets
 // V[32 ks + 4 g + e][16 db + d] (e < 4), then V[32 ks + 16 + 4 g + e][16 db + d]. In a transpose
 // read lane k addresses row R + k / 4, dims C + 4 (k % 4) .. +3; lane j receives rows R .. R + 3
