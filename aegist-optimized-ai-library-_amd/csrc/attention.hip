@@ -476,10 +476,12 @@ __global__ void __launch_bounds__(256) attn_prefill_simple_kernel(const float* _
 // the four lanes n, n + 16, n + 32, n + 48 (max: two cross-group shuffles; sum: kept per lane,
 // reduced once at the end).
 //
-// q * scale and the probabilities enter as bf16 hi + lo pairs (two MFMAs each): ~16
-// significant bits against the exact bf16 K and V. Base-2 softmax (log2 e folded into the q
-// scale); the accumulators are rescaled only when some query's running maximum moved;
-// output * sigmoid(gate). A wave whose queries cannot see any key of a tile skips it.
+// K and V tiles are converted to fp16 as they are staged into LDS (exact for bf16 values in
+// fp16's range), so q * scale and the probabilities enter as single fp16 operands (11
+// significant bits; errors ~2e-4 of max|out|). Base-2 softmax (log2 e folded into the q scale);
+// the accumulators are rescaled only when some query's running maximum moved; the causal mask
+// is applied only on tiles that reach past a wave's first query; output * sigmoid(gate). A
+// wave whose queries cannot see any key of a tile skips it.
 #ifndef PREFILL_PQ
 #define PREFILL_PQ 128
 #endif
