@@ -138,7 +138,7 @@ struct K1Smem {
     float cum_s[CH], beta_s[CH], g_s[CH];
     // intra is staged for fragment order in QV's space: q_n has been read into registers by then,
     // and v is written there only after the intra fragments have gone out. 53 KB in all for bf16
-    // inputs: three workgroups per CU.
+    // inputs: three workgroups per CU for the standalone K1 launch.
 };
 
 // step 5 reuses QV and Ks for the X fragments (hi + lo: 16 KB each) and As for the w staging tile
@@ -557,8 +557,8 @@ __device__ __forceinline__ void chunk_state_body(const unsigned char* __restrict
                 S[rt][ct][j] = load_state ? Sg[(size_t)(32 * wave + 16 * rt + 4 * gq + j) * D + col0 + 16 * ct + n] : 0.f;
 
     const size_t vbase = (size_t)(b * HV + hv) * nch, kbase = (size_t)(b * HK + kh) * nch;
-    // operands of one chunk that do not depend on S; the next chunk's are requested while the
-    // current chunk computes (register double buffer), hiding the L2 / HBM latency
+    // operands of one chunk that do not depend on S; each part is refilled with the next chunk's
+    // values while the current chunk computes (see step), hiding the L2 / HBM latency
     struct Ops {
         half8 wa[4], qa[4], ia[2], ka[2][2];
         f32x4 uu[NCT], ecum, edec;  // u fragment; e^{cum_i}, e^{cum_last - cum_i} for this lane's rows
