@@ -529,8 +529,10 @@ __global__ void __launch_bounds__(64 * PW) attn_prefill_mfma_kernel(const float*
                                                                      float* __restrict__ out, Strides3 os, int H,
                                                                      int KV, int T, int pos, int cap, float scale,
                                                                      int B, int per_xcd) {
-    __shared__ __attribute__((aligned(16))) uint16_t Kt[PK * KLD];
-    __shared__ __attribute__((aligned(16))) uint16_t Vt[PK * VLD];
+    // double-buffered tiles (2 x 68.6 KB): tile t + 1 is written while tile t is read, one
+    // barrier per tile
+    __shared__ __attribute__((aligned(16))) uint16_t Kt2[2][PK * KLD];
+    __shared__ __attribute__((aligned(16))) uint16_t Vt2[2][PK * VLD];
 
     // XCD-aware order (1-D grid of 8 per_xcd blocks, dealt round-robin to the 8 XCDs): XCD x
     // runs logical blocks [x per_xcd, (x + 1) per_xcd) in order, so the workgroups resident on
@@ -583,26 +585,35 @@ __global__ void __launch_bounds__(64 * PW) attn_prefill_mfma_kernel(const float*
         kreg[it] = *(const u32x4*)(kbase + off);
         vreg[it] = *(const u32x4*)(vbase + off);
     }
-    for (int kt = 0; kt < ntiles; kt++) {
-        const int key0 = kt * PK;
-        __syncthreads();  // previous tile's LDS reads done
+    auto stage = [&](int buf) {
 #pragma unroll
         for (int it = 0; it < NSTEP; it++) {
             const int r = r_own + it * RSTEP;
-            *(u32x4*)&Kt[r * KLD + c_own] = bf8_to_f16(kreg[it]);
-            *(u32x4*)&Vt[r * VLD + c_own] = bf8_to_f16(vreg[it]);
+            *(u32x4*)&Kt2[buf][r * KLD + c_own] = bf8_to_f16(kreg[it]);
+            *(u32x4*)&Vt2[buf][r * VLD + c_own] = bf8_to_f16(vreg[it]);
         }
-        __syncthreads();
-        {   // next tile (unconditional: static wait counts)
-            const int kn = min(kt + 1, ntiles - 1) * PK;
+    };
+    auto request = [&](int t) {  // tile t (clamped: static wait counts) into the registers
+        const int kn = min(t, ntiles - 1) * PK;
 #pragma unroll
-            for (int it = 0; it < NSTEP; it++) {
-                const size_t off = (size_t)min(kn + r_own + it * RSTEP, last_key) * HD + c_own;
-                kreg[it] = *(const u32x4*)(kbase + off);
-                vreg[it] = *(const u32x4*)(vbase + off);
-            }
+        for (int it = 0; it < NSTEP; it++) {
+            const size_t off = (size_t)min(kn + r_own + it * RSTEP, last_key) * HD + c_own;
+            kreg[it] = *(const u32x4*)(kbase + off);
+            vreg[it] = *(const u32x4*)(vbase + off);
         }
-        if (key0 > wave_last) continue;  // no query of this wave sees any key of this tile
+    };
+    stage(0);
+    request(1);
+    __syncthreads();
+    for (int kt = 0; kt < ntiles; kt++) {
+        const int key0 = kt * PK, cur = kt & 1;
+        const uint16_t* Kt = Kt2[cur];
+        const uint16_t* Vt = Vt2[cur];
+        // tile kt + 1 into the other buffer: its last reader (tile kt - 1) passed the barrier
+        // that ends the previous iteration
+        if (kt + 1 < ntiles) stage(cur ^ 1);
+        request(kt + 2);
+        if (key0 <= wave_last) {  // else no query of this wave sees any key of this tile
         // ---- S^T for 4 blocks of 16 keys: sc[nb][j] = score of key key0 + 16 nb + 4 g + j
         f32x4 sc[4];
 #pragma unroll
@@ -666,6 +677,8 @@ __global__ void __launch_bounds__(64 * PW) attn_prefill_mfma_kernel(const float*
                 const half8 va = __builtin_bit_cast(half8, vt_operand(Vt, ks, db, lane));
                 oacc[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pf[ks], oacc[db], 0, 0, 0);
             }
+        }
+        __syncthreads();  // tile kt + 1 staged by every wave; tile kt's reads done
     }
     // ---- normalise, gate, store: lane holds query n, dims 16 db + 4 g .. +4
     float l = l_part;
