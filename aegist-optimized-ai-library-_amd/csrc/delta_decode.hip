@@ -78,9 +78,25 @@ __global__ void __launch_bounds__(256 * R) delta_decode_kernel(
     float* S = state + ((size_t)b * HV + hv) * D * D;
     const int rbase = w4 * 8 + rr;
 
-    // ---- 0. start streaming column slices 0 and 1 before the conv (independent of it)
-    // column slices in flight: two (4 workgroups' worth of state per CU at batch 64), all four in
-    // the stack form, whose batch-16 grid is a single round of one workgroup per CU
+    // ---- 0. the inputs of this thread's first conv channel are requested first (the prologue
+    // needs them first, and vector-memory loads return in order), then the state column slices
+    // (independent of the conv): two in flight (4 workgroups' worth of state per CU at batch 64),
+    // all four in the stack form, whose batch-16 grid is a single round of one workgroup per CU
+    auto chan = [&](int ch) {
+        return ch < D ? kh * D + ch : ch < 2 * D ? HK * D + kh * D + (ch - D) : 2 * HK * D + kh * R * D + (ch - 2 * D);
+    };
+    float xv0 = 0.f, c0s0 = 0.f, c0s1 = 0.f, c0s2 = 0.f;
+    uint2 wp0 = {0u, 0u};
+    if (tid < NCH) {
+        const int c = chan(tid);
+        xv0 = Act<Tin>::ld(qkv, (size_t)b * C + c);
+        const float* st = conv_state + ((size_t)b * C + c) * 3;
+        c0s0 = st[0];
+        c0s1 = st[1];
+        c0s2 = st[2];
+        wp0 = *(const uint2*)(conv_w + (size_t)c * 4);
+    }
+    __builtin_amdgcn_sched_barrier(0);
     constexpr int NSF = kStack ? 4 : 2;
     float4 s[NSF][4];
 #pragma unroll
@@ -91,14 +107,17 @@ __global__ void __launch_bounds__(256 * R) delta_decode_kernel(
     // ---- 1. conv + SiLU + conv-state update for this workgroup's channels
     float ymine = 0.f;
     for (int ch = tid; ch < NCH; ch += NT) {
-        int c;
-        if (ch < D) c = kh * D + ch;
-        else if (ch < 2 * D) c = HK * D + kh * D + (ch - D);
-        else c = 2 * HK * D + kh * R * D + (ch - 2 * D);
-        const float xv = Act<Tin>::ld(qkv, (size_t)b * C + c);
+        const int c = chan(ch);
         float* st = conv_state + ((size_t)b * C + c) * 3;
-        const float s0 = st[0], s1 = st[1], s2 = st[2];
-        const uint2 wp = *(const uint2*)(conv_w + (size_t)c * 4);
+        float xv, s0, s1, s2;
+        uint2 wp;
+        if (ch == tid) {
+            xv = xv0; s0 = c0s0; s1 = c0s1; s2 = c0s2; wp = wp0;
+        } else {
+            xv = Act<Tin>::ld(qkv, (size_t)b * C + c);
+            s0 = st[0]; s1 = st[1]; s2 = st[2];
+            wp = *(const uint2*)(conv_w + (size_t)c * 4);
+        }
         const float acc = bf_lo(wp.x) * s0 + bf_hi(wp.x) * s1 + bf_lo(wp.y) * s2 + bf_hi(wp.y) * xv;
         const float y = silu_f(acc);
         st[0] = s1;
