@@ -12,8 +12,10 @@
 // The attention over the listed blocks is attention_gated_list (attention.hip).
 //
 // Scores use fp32 MFMA (v_mfma_f32_16x16x4f32) so the selection sees fp32 products like the
-// engine's; the selection builds the top-th largest score bit by bit from register-resident
-// scores (counting with ballots), then compacts in block order with wave ballots.
+// engine's; the selection finds the top-th largest score by a three-digit radix select over
+// register-resident scores (LDS histograms), then compacts in block order with wave ballots.
+// Few queries over many blocks split each row over several workgroups first (local tops),
+// then select among the candidates.
 #include "common.h"
 
 using namespace aegist;
@@ -150,37 +152,39 @@ __global__ void __launch_bounds__(256) idx_scores_kernel(const float* __restrict
     if (g == 0 && blk < nvis) sc[(size_t)t * nbmax + blk] = tot / sqrtf((float)IHD);
 }
 
-// One workgroup of 16 waves per query; thread tid holds the PER consecutive scores of blocks
-// [tid PER, tid PER + PER) in registers. The top-th largest score bit pattern T is built from
-// the most significant bit down, two bits per step: of the three candidates T | k << b (k = 1..3)
-// the largest with at least `top` scores >= it is kept (scores are non-negative, so bit patterns
-// order like values). A count is a compare-and-add over the thread's registers, wave totals from
-// ballots of the count's bits, and one barrier for the three sums over waves. The listing is an
-// exclusive prefix over threads of (above T, equal to T) counts, so each thread writes its own
-// blocks in order: every block above T and the lowest-numbered blocks equal to T.
-// PER = 0 (more than 32768 blocks): the thread's scores are re-read from global memory
+// Top-`top` of n values by (value desc, index asc), listed in index order. Values are
+// non-negative floats or encoded bit patterns below 2^31, so bit patterns order like values.
+// Thread tid holds the PER consecutive values [tid PER, tid PER + PER) in registers. The top-th
+// largest bit pattern T is found by a most-significant-digit radix select over digits of bits
+// 30..20, 19..10 and 9..0: each pass counts the values whose higher digits equal the ones decided
+// so far into an LDS histogram (LDS atomics), and a suffix sum over the bins (wave scans plus
+// one sum over waves) names the bin holding the still-wanted rank. The listing is an exclusive
+// prefix over threads of (above T, equal to T) counts, so each thread emits its own values in
+// order: every value above T and the lowest-indexed values equal to T. Requires n > top.
+// emit(pos, i, v) receives the output position, the value's index and its bit pattern.
+// PER = 0 (more than NT * 32 values): the thread's values are re-read from global memory
 // (L2-resident), chunk by chunk, instead of registers.
-constexpr int SEL_THREADS = 1024, SEL_WAVES = SEL_THREADS / WAVE;
+// digit widths (a wider first digit spreads the atomics of clustered scores over more bins but
+// lengthens the bin scans: 11 measured best of 11 / 12 / 13 at 32768 blocks)
+constexpr int SEL_D1 = 11, SEL_D2 = 10, SEL_D3 = 31 - SEL_D1 - SEL_D2;
+struct SelectLds {
+    unsigned hist[1 << SEL_D1];
+    unsigned wsum[16];   // per-wave bin totals (at most 16 waves)
+    unsigned pick[2];    // the chosen digit and the count of values in higher bins
+    unsigned wl[2][16];  // per-wave listing counts
+};
 
-template <int PER>
-__global__ void __launch_bounds__(SEL_THREADS) idx_select_kernel(const float* __restrict__ sc, int* __restrict__ blist,
-                                                                 int* __restrict__ nsel, int top, int R, int pos0,
-                                                                 int nbmax, int vec) {
-    __shared__ unsigned wc[2][4][SEL_WAVES];
-    const int t = blockIdx.x, tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
-    const int n = (pos0 + t + 1) / R;
-    const unsigned* sg = (const unsigned*)(sc + (size_t)t * nbmax);
-    int* out = blist + (size_t)t * top;
-    if (n <= top) {  // every complete block
-        for (int b = tid; b < n; b += SEL_THREADS) out[b] = b;
-        if (tid == 0) nsel[t] = n;
-        return;
-    }
-    // this thread's blocks: [lo, lo + per), per = PER or ceil(n / 1024)
-    const int per = PER > 0 ? PER : (n + SEL_THREADS - 1) / SEL_THREADS;
+template <int NT, int PER, typename Emit>
+__device__ __forceinline__ void select_top(const unsigned* __restrict__ sg, int n, int top, int vec, SelectLds& L,
+                                           Emit emit) {
+    constexpr int NW = NT / WAVE;
+    static_assert(NW <= 16 && SEL_D3 > 0, "select_top: at most 16 waves; three digits");
+    const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
+    const int per = PER > 0 ? PER : (n + NT - 1) / NT;
     const int lo = tid * per;
     constexpr int NREG = PER > 0 ? PER : 1;
     unsigned u[NREG];
+    for (int b = tid; b < (1 << SEL_D1); b += NT) L.hist[b] = 0u;
     if constexpr (PER > 0) {
 #pragma unroll
         for (int i = 0; i < PER; i += 4) {
@@ -192,7 +196,7 @@ __global__ void __launch_bounds__(SEL_THREADS) idx_select_kernel(const float* __
                 u[i + 3] = v.w;
             } else {
 #pragma unroll
-                for (int k = 0; k < 4; k++) u[i + k] = lo + i + k < n ? sg[lo + i + k] : 0u;  // 0 never counts
+                for (int k = 0; k < 4; k++) u[i + k] = lo + i + k < n ? sg[lo + i + k] : 0u;
             }
         }
     }
@@ -213,37 +217,58 @@ __global__ void __launch_bounds__(SEL_THREADS) idx_select_kernel(const float* __
         }
         return tot;
     };
-    int par = 0;
-    unsigned T = 0;
-    for (int bit = 29; bit >= -1; bit -= 2) {  // bits (30, 29), ..., (0, -); the sign bit is 0
-        const int sh = bit < 0 ? 0 : bit;
-        const int nk = bit < 0 ? 1 : 3;  // the last step decides bit 0 alone
-        unsigned c[3] = {0u, 0u, 0u};
+    unsigned T = 0, want = (unsigned)top;       // decided high digits; rank still wanted below them
+    __syncthreads();
+#pragma unroll
+    for (int pass = 0; pass < 3; pass++) {
+        const int nb = pass == 0 ? SEL_D1 : pass == 1 ? SEL_D2 : SEL_D3;
+        const int sh = pass == 0 ? 31 - SEL_D1 : pass == 1 ? SEL_D3 : 0;
+        const int nbins = 1 << nb, bpt = nbins > NT ? nbins / NT : 1;  // bins per thread (powers of 2)
+#pragma unroll
         for (int i = 0; i < per; i++) {
             const unsigned v = val(i);
-#pragma unroll
-            for (int k = 0; k < 3; k++) c[k] += v >= (T | ((unsigned)(k + 1) << sh));
-        }
-#pragma unroll
-        for (int k = 0; k < 3; k++) {
-            unsigned pre;
-            const unsigned wt = wave_count(c[k], pre);
-            if (lane == 0) wc[par][k][wave] = wt;
+            if (lo + i < n && (v >> (sh + nb)) == (T >> (sh + nb)))
+                atomicAdd(&L.hist[(v >> sh) & (nbins - 1)], 1u);
         }
         __syncthreads();
-        unsigned tot[3] = {0u, 0u, 0u};
-        for (int w = 0; w < SEL_WAVES; w++)
+        // this thread's bins [tid bpt, tid bpt + bpt), read into registers and cleared for the
+        // next pass (its first atomics come after this pass's last barrier)
+        unsigned h[(1 << SEL_D1) > NT ? (1 << SEL_D1) / NT : 1], own = 0;
 #pragma unroll
-            for (int k = 0; k < 3; k++) tot[k] += wc[par][k][w];
-        par ^= 1;  // the next step writes the other buffer: no second barrier needed
-        for (int k = nk - 1; k >= 0; k--)
-            if (tot[k] >= (unsigned)top) {
-                T |= (unsigned)(k + 1) << sh;
-                break;
+        for (int j = 0; j < bpt; j++) {
+            h[j] = tid < nbins ? L.hist[tid * bpt + j] : 0u;
+            own += h[j];
+            if (tid < nbins) L.hist[tid * bpt + j] = 0u;
+        }
+        unsigned suf = own;  // inclusive suffix sum over lanes >= this one
+#pragma unroll
+        for (int d = 1; d < WAVE; d <<= 1) {
+            const unsigned y = __shfl_down(suf, d, WAVE);
+            if (lane + d < WAVE) suf += y;
+        }
+        if (lane == 0) L.wsum[wave] = suf;
+        __syncthreads();
+        unsigned above = suf - own;
+        for (int w = wave + 1; w < NW; w++) above += L.wsum[w];
+        if (above < want && above + own >= want) {  // the wanted rank is in one of this thread's bins
+            bool found = false;
+#pragma unroll
+            for (int j = bpt - 1; j >= 0; j--) {
+                if (!found && above + h[j] >= want) {
+                    L.pick[0] = (unsigned)(tid * bpt + j);
+                    L.pick[1] = above;
+                    found = true;
+                }
+                above += h[j];
             }
+        }
+        __syncthreads();
+        T |= L.pick[0] << sh;
+        want -= L.pick[1];
     }
     // listing: per-thread counts above / equal to T, exclusive prefix over threads
     unsigned gtc = 0, eqc = 0;
+#pragma unroll
     for (int i = 0; i < per; i++) {
         const unsigned v = val(i);
         gtc += lo + i < n && v > T;
@@ -252,32 +277,106 @@ __global__ void __launch_bounds__(SEL_THREADS) idx_select_kernel(const float* __
     unsigned gpre, epre;
     const unsigned gw = wave_count(gtc, gpre), ew = wave_count(eqc, epre);
     if (lane == 0) {
-        wc[par][0][wave] = gw;
-        wc[par][1][wave] = ew;
+        L.wl[0][wave] = gw;
+        L.wl[1][wave] = ew;
     }
     __syncthreads();
     unsigned gt_before = gpre, eq_before = epre, gt_total = 0;
-    for (int w = 0; w < SEL_WAVES; w++) {
-        const unsigned g = wc[par][0][w], e = wc[par][1][w];
+    for (int w = 0; w < NW; w++) {
+        const unsigned g = L.wl[0][w], e = L.wl[1][w];
         gt_total += g;
         if (w < wave) {
             gt_before += g;
             eq_before += e;
         }
     }
-    const unsigned take_eq = (unsigned)top - gt_total;  // equal-valued blocks that make the top
-    // this thread's output position: blocks above T before it plus the equal ones taken before it
+    const unsigned take_eq = (unsigned)top - gt_total;  // equal-valued entries that make the top
+    // this thread's output position: values above T before it plus the equal ones taken before it
     unsigned pos = gt_before + min(eq_before, take_eq), eq_seen = eq_before;
+#pragma unroll
     for (int i = 0; i < per; i++) {
-        if (lo + i >= n) break;
         const unsigned v = val(i);
-        if (v > T) {
-            out[pos++] = lo + i;
-        } else if (v == T) {
-            if (eq_seen < take_eq) out[pos++] = lo + i;
-            eq_seen++;
-        }
+        const bool in = lo + i < n, eq = in && v == T;
+        const bool take = in && (v > T || (eq && eq_seen < take_eq));
+        eq_seen += eq;
+        if (take) emit(pos, lo + i, v);
+        pos += take;
     }
+}
+
+// One workgroup of 16 waves per query over all of its complete blocks.
+constexpr int SEL_THREADS = 1024, SEL_WAVES = SEL_THREADS / WAVE;
+
+template <int PER>
+__global__ void __launch_bounds__(SEL_THREADS) idx_select_kernel(const float* __restrict__ sc, int* __restrict__ blist,
+                                                                 int* __restrict__ nsel, int top, int R, int pos0,
+                                                                 int nbmax, int vec) {
+    __shared__ SelectLds L;
+    const int t = blockIdx.x, tid = threadIdx.x;
+    const int n = (pos0 + t + 1) / R;
+    int* out = blist + (size_t)t * top;
+    if (n <= top) {  // every complete block
+        for (int b = tid; b < n; b += SEL_THREADS) out[b] = b;
+        if (tid == 0) nsel[t] = n;
+        return;
+    }
+    select_top<SEL_THREADS, PER>((const unsigned*)(sc + (size_t)t * nbmax), n, top, vec, L,
+                                 [&](unsigned pos, int i, unsigned) { out[pos] = i; });
+    if (tid == 0) nsel[t] = top;
+}
+
+// Two-phase selection for few queries over many blocks (one workgroup per query leaves the rest
+// of the GPU idle). Phase 1: workgroup (p, t) takes query t's blocks [p S, p S + S) and lists its
+// local top `top` into candidate slots [(t P + p) top, ...) as (score bits + 1, block), in block
+// order; a range of at most `top` blocks is copied whole and unused slots hold 0. The query's top
+// blocks of the whole row are among the union of the ranges' local tops (a block beaten by `top`
+// others within its range is beaten by them in the row). Phase 2 selects `top` of the P top slots
+// of each query: valid slots are in block order, so ties still go to the lower block, and the
+// +1 encoding keeps empty slots (0) out of every count.
+constexpr int SEL1_THREADS = 256, SEL1_PER = 16, SEL1_RANGE = SEL1_THREADS * SEL1_PER;
+
+__global__ void __launch_bounds__(SEL1_THREADS) idx_select_part_kernel(const float* __restrict__ sc,
+                                                                       unsigned* __restrict__ cval,
+                                                                       int* __restrict__ cidx, int top, int R,
+                                                                       int pos0, int nbmax, int vec) {
+    __shared__ SelectLds L;
+    const int p = blockIdx.x, t = blockIdx.y, P = gridDim.x, tid = threadIdx.x;
+    const int n = (pos0 + t + 1) / R;
+    if (n <= top) return;  // phase 2 lists every block without reading the slots
+    const int lo = p * SEL1_RANGE, len = min(max(n - lo, 0), SEL1_RANGE);
+    const size_t base = ((size_t)t * P + p) * top;
+    const unsigned* sg = (const unsigned*)(sc + (size_t)t * nbmax) + lo;
+    if (len <= top) {
+        for (int i = tid; i < top; i += SEL1_THREADS) {
+            cval[base + i] = i < len ? sg[i] + 1u : 0u;
+            cidx[base + i] = lo + i;
+        }
+        return;
+    }
+    select_top<SEL1_THREADS, SEL1_PER>(sg, len, top, vec, L, [&](unsigned pos, int i, unsigned v) {
+        cval[base + pos] = v + 1u;
+        cidx[base + pos] = lo + i;
+    });
+}
+
+template <int PER>
+__global__ void __launch_bounds__(SEL_THREADS) idx_select_merge_kernel(const unsigned* __restrict__ cval,
+                                                                       const int* __restrict__ cidx,
+                                                                       int* __restrict__ blist, int* __restrict__ nsel,
+                                                                       int top, int R, int pos0, int P, int vec) {
+    __shared__ SelectLds L;
+    const int t = blockIdx.x, tid = threadIdx.x;
+    const int n = (pos0 + t + 1) / R;
+    int* out = blist + (size_t)t * top;
+    if (n <= top) {
+        for (int b = tid; b < n; b += SEL_THREADS) out[b] = b;
+        if (tid == 0) nsel[t] = n;
+        return;
+    }
+    const size_t m = (size_t)P * top;
+    const int* ci = cidx + t * m;
+    select_top<SEL_THREADS, PER>(cval + t * m, (int)m, top, vec, L,
+                                 [&](unsigned pos, int i, unsigned) { out[pos] = ci[i]; });
     if (tid == 0) nsel[t] = top;
 }
 
@@ -356,7 +455,23 @@ int aegist_idx_select(const float* sc, int* blist, int* nsel, int T, int top, in
     const int nmax = (pos0 + T) / R;  // the most complete blocks any of these queries sees
     const int vec = nbmax % 4 == 0 && (uintptr_t)sc % 16 == 0;
     hipStream_t st = AEG_STREAM(stream);
-    if (nmax <= 8 * SEL_THREADS)
+    const int P = (nmax + SEL1_RANGE - 1) / SEL1_RANGE;
+    const size_t m = (size_t)P * top;
+    // two phases when few queries see many blocks and the candidates are far fewer than the blocks
+    if (T <= 16 && nmax > 8 * SEL_THREADS && 4 * m <= (size_t)nmax && m <= (size_t)32 * SEL_THREADS) {
+        int rc = 0;
+        unsigned* cval = (unsigned*)mirror_workspace((size_t)T * m * 8, &rc);
+        if (rc) return rc;
+        int* cidx = (int*)(cval + (size_t)T * m);
+        idx_select_part_kernel<<<dim3(P, T), SEL1_THREADS, 0, st>>>(sc, cval, cidx, top, R, pos0, nbmax, vec);
+        const int vec2 = m % 4 == 0;
+        if (m <= 4 * SEL_THREADS)
+            idx_select_merge_kernel<4><<<T, SEL_THREADS, 0, st>>>(cval, cidx, blist, nsel, top, R, pos0, P, vec2);
+        else if (m <= 8 * SEL_THREADS)
+            idx_select_merge_kernel<8><<<T, SEL_THREADS, 0, st>>>(cval, cidx, blist, nsel, top, R, pos0, P, vec2);
+        else
+            idx_select_merge_kernel<32><<<T, SEL_THREADS, 0, st>>>(cval, cidx, blist, nsel, top, R, pos0, P, vec2);
+    } else if (nmax <= 8 * SEL_THREADS)
         idx_select_kernel<8><<<T, SEL_THREADS, 0, st>>>(sc, blist, nsel, top, R, pos0, nbmax, vec);
     else if (nmax <= 32 * SEL_THREADS)
         idx_select_kernel<32><<<T, SEL_THREADS, 0, st>>>(sc, blist, nsel, top, R, pos0, nbmax, vec);

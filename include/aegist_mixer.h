@@ -283,7 +283,9 @@ int aegist_idx_blocks(const float* kraw, const uint16_t* kw, float* bk, int b0, 
 int aegist_idx_scores(const float* qi, const float* bk, float* sc, int T, int H, int HD, int pos0, int R, int nbmax,
                       void* stream);
 /* idx_select, next.cu:543-625: per query, all n complete blocks when n <= top (nsel = n), else
- * the top highest scores (ties to the lower block), listed in block order (nsel = top) */
+ * the top highest scores (ties to the lower block), listed in block order (nsel = top). Up to 16
+ * queries over more than 8192 blocks stage candidates in the library's per-device workspace
+ * (grown by hipMalloc on first use). */
 int aegist_idx_select(const float* sc, int* blist, int* nsel, int T, int top, int R, int pos0, int nbmax,
                       void* stream);
 /* attention_gated_list, next.cu:627-705: attention_gated for query t over the R keys of each

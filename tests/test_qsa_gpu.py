@@ -82,10 +82,13 @@ def test_indexer_pipeline(dev, T, pos0):
     _check_lists(_lists(blist, nsel), lists_ref, sc_ref, top, RB, pos0)
 
 
-@pytest.mark.parametrize("T,pos0,nbits", [(37, 500, 0), (5, 131067, 0), (9, 4000, 3), (2, 160000, 0), (2, 160000, 2)])
+@pytest.mark.parametrize("T,pos0,nbits", [(37, 500, 0), (5, 131067, 0), (9, 4000, 3), (2, 160000, 0), (2, 160000, 2),
+                                                  (2, 131471, 0), (3, 131471, 1), (17, 131067, 2)])
 def test_select_exact_with_ties(dev, T, pos0, nbits):
     """Scores given directly (no arithmetic differences): lists equal the oracle's exactly,
-    including ties (scores rounded to few distinct values) and n = 32768 blocks."""
+    including ties (scores rounded to few distinct values), n = 32768 blocks, the two-phase
+    path (few queries over many blocks; pos0 131471 leaves a last range of 100 blocks, which is
+    copied whole) and the one-workgroup path at T = 17."""
     print(f"qsa select T={T} pos0={pos0} ties={nbits}", flush=True)
     g_ = _gen(pos0)
     RB, top = 4, 512 if pos0 > 100000 else 16
