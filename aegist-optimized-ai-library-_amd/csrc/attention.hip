@@ -150,7 +150,7 @@ struct KeyList {
     int top, R, pos0;
 };
 
-template <typename TG, typename Tout>
+template <typename TG, typename Tout, bool kList>
 __global__ void __launch_bounds__(256) attn_decode_split_kernel(const float* __restrict__ q,
                                                                 const uint16_t* __restrict__ kc,
                                                                 const uint16_t* __restrict__ vc,
@@ -174,11 +174,12 @@ __global__ void __launch_bounds__(256) attn_decode_split_kernel(const float* __r
     const int n = lane % 16, g = lane / 16;
     const int G = H / KV;
     // listed keys: this query's key count and the list -> cache position map (batch-1 cache)
-    const bool listed = kl.blist != nullptr;
-    int Lb = L, nsR = 0, tail0 = 0;
+    constexpr bool listed = kList;
+    int Lb = L, nsR = 0, tail0 = 0, pq = 0;
     const int* bl = nullptr;
     if (listed) {
         const int p = kl.pos0 + b, complete = (p + 1) / kl.R;
+        pq = p;
         nsR = kl.nsel[b] * kl.R;
         tail0 = complete * kl.R;
         Lb = nsR + (p + 1 - tail0);
@@ -186,18 +187,20 @@ __global__ void __launch_bounds__(256) attn_decode_split_kernel(const float* __r
     }
     const int k0 = split * per_split, k1 = min(Lb, k0 + per_split);
 
-    // ---- Q operand: rows 0..7 = hi(q*scale), rows 8..15 = lo; lane row n, k elems 8g..8g+7
+    // ---- Q operand: rows 0..7 = hi(q*scale), rows 8..15 = lo; lane row n, k elems 8g..8g+7.
+    // Rows past G read row 0 and scale it by 0: unconditional loads issue back to back.
     bf16x8 qa[8];
     {
         const int r = n & 7;
         const bool lo = n >= 8;
         const bool valid = r < G;
         const float* qrow = q + ((size_t)b * H + kvh * G + (valid ? r : 0)) * HD;
+        const float qscale = valid ? scale : 0.f;
 #pragma unroll
         for (int ks = 0; ks < 8; ks++) {
 #pragma unroll
             for (int i = 0; i < 8; i++) {
-                float x = valid ? qrow[ks * 32 + 8 * g + i] * scale : 0.f;
+                float x = qrow[ks * 32 + 8 * g + i] * qscale;
                 uint16_t h, l;
                 split_bf16(x, h, l);
                 qa[ks][i] = (short)(lo ? l : h);
@@ -208,7 +211,15 @@ __global__ void __launch_bounds__(256) attn_decode_split_kernel(const float* __r
     const size_t cache_row = listed ? (size_t)kvh : (size_t)b * KV + kvh;
     const uint16_t* kbase = kc + cache_row * (size_t)cap * HD;
     const uint16_t* vbase = vc + cache_row * (size_t)cap * HD;
-    auto key_pos = [&](int j) { return !listed ? j : j < nsR ? bl[j / kl.R] * kl.R + j % kl.R : tail0 + (j - nsR); };
+    // listed keys: lane l holds the cache position of row l % 32 of a tile, looked up one tile
+    // before the tile's fetch so the list load's wait never holds back the K / V loads in flight.
+    // The list entry is read at a clamped index whatever nsel says (no wait on nsel first); rows
+    // past the split map to cached positions <= p (finite data, probability 0).
+    auto tile_keys = [&](int t0) {
+        const int j = t0 + (lane & 31);
+        const int blk = bl[min(j / kl.R, kl.top - 1)];
+        return j < nsR ? blk * kl.R + j % kl.R : min(tail0 + (j - nsR), pq);
+    };
 
     // running softmax state for heads 4*(g%2)+j, j < 4 (duplicated in lanes g and g+2)
     float m_run[4], l_run[4];
@@ -228,17 +239,25 @@ __global__ void __launch_bounds__(256) attn_decode_split_kernel(const float* __r
     // iteration. Rows past the split are clamped to its last row (finite data, probability 0).
     constexpr int NST = (TILE * HD * 2) / (16 * WAVE);  // 16 steps per tensor
     uint4 kreg[NST], vreg[NST];
-    auto fetch = [&](int t0) {
+    auto fetch = [&](int t0, int kp) {
 #pragma unroll
         for (int it = 0; it < NST; it++) {
             const int idx = it * WAVE + lane, row = idx / (HD * 2 / 16), cc = idx % (HD * 2 / 16);
-            const int key = key_pos(min(t0 + row, k1 - 1));
+            const int key = listed ? __shfl(kp, row, WAVE) : min(t0 + row, k1 - 1);
             kreg[it] = *(const uint4*)(kbase + (size_t)key * HD + cc * 8);
             vreg[it] = *(const uint4*)(vbase + (size_t)key * HD + cc * 8);
         }
     };
     const int first = k0 + wave * TILE, stride = 4 * TILE;
-    if (first < k1) fetch(first);
+    int kp_next = 0;
+    if (first < k1) {
+        if constexpr (listed) {
+            fetch(first, tile_keys(first));
+            kp_next = tile_keys(min(first + stride, k1 - 1));
+        } else {
+            fetch(first, 0);
+        }
+    }
     for (int t0 = first; t0 < k1; t0 += stride) {
 #pragma unroll
         for (int it = 0; it < NST; it++) {
@@ -250,7 +269,8 @@ __global__ void __launch_bounds__(256) attn_decode_split_kernel(const float* __r
             dk[0] = uint2{kreg[it].x, kreg[it].y};
             dk[1] = uint2{kreg[it].z, kreg[it].w};
         }
-        fetch(min(t0 + stride, k1 - 1));  // next tile (unconditional: static wait counts)
+        fetch(min(t0 + stride, k1 - 1), kp_next);  // next tile (unconditional: static wait counts)
+        if constexpr (listed) kp_next = tile_keys(min(t0 + 2 * stride, k1 - 1));
         wave_sync();
         // ---- scores: two 16-key blocks
         f32x4 sc[2];
@@ -735,8 +755,12 @@ int launch_decode_core(const float* q, const uint16_t* kc, const uint16_t* vc, c
     float* part = (float*)ws;
     size_t part_bytes = ((size_t)B * KV * sp.nsplit * G * HD * 4 + 255) / 256 * 256;
     float* ml = (float*)((char*)ws + part_bytes);
-    attn_decode_split_kernel<TG, Tout><<<dim3(sp.nsplit, KV, B), 256, 0, st>>>(
-        q, kc, vc, part, ml, H, KV, L, cap, sp.per_split, scale, counters, gate, gate_stride, out, out_stride, kl);
+    if (kl.blist)
+        attn_decode_split_kernel<TG, Tout, true><<<dim3(sp.nsplit, KV, B), 256, 0, st>>>(
+            q, kc, vc, part, ml, H, KV, L, cap, sp.per_split, scale, counters, gate, gate_stride, out, out_stride, kl);
+    else
+        attn_decode_split_kernel<TG, Tout, false><<<dim3(sp.nsplit, KV, B), 256, 0, st>>>(
+            q, kc, vc, part, ml, H, KV, L, cap, sp.per_split, scale, counters, gate, gate_stride, out, out_stride, kl);
     int rc = after_launch("attention_decode_split");
     if (rc || counters) return rc;
     attn_decode_merge_kernel<TG, Tout><<<B * KV, 256, 0, st>>>(part, ml, gate, gate_stride, out, out_stride, H, KV,
