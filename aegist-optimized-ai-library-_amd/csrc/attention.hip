@@ -81,55 +81,73 @@ __device__ void merge_splits(const float* __restrict__ part, const float* __rest
     __shared__ float fw[8][256];
     const int tid = threadIdx.x, rr = tid / 32, t32 = tid % 32;
     const bool active = rr < G;
+    const int d0 = t32 * 8;
+    const size_t row = row0 + rr;
+    // every load of the statistics and the gate is issued before the first wait: (m, l) of
+    // splits t32 + 32 k (nsplit <= 256; indices past the last split re-read it, masked below)
+    float2 st[8];
+    float gv[8];
+    if (active) {
+#pragma unroll
+        for (int k = 0; k < 8; k++)
+            st[k] = *(const float2*)(ml + ((base + min(t32 + 32 * k, nsplit - 1)) * G + rr) * 2);
+#pragma unroll
+        for (int e = 0; e < 8; e++) gv[e] = gate ? Act<TG>::ld(gate, row * gate_stride + d0 + e) : 0.f;
+    }
     float mx = -INFINITY;
-    if (active)
-        for (int s = t32; s < nsplit; s += 32) mx = fmaxf(mx, ml[((base + s) * G + rr) * 2]);
+#pragma unroll
+    for (int k = 0; k < 8; k++)
+        if (active && t32 + 32 * k < nsplit) mx = fmaxf(mx, st[k].x);
 #pragma unroll
     for (int o = 16; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, WAVE));
     float ls = 0.f;
-    if (active)
-        for (int s = t32; s < nsplit; s += 32) {
-            const size_t pi = (base + s) * G + rr;
-            const float m = ml[pi * 2];
-            const float f = m == -INFINITY ? 0.f : __expf(m - mx);
-            fw[rr][s] = f;
-            ls += ml[pi * 2 + 1] * f;
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        const int sp = t32 + 32 * k;
+        if (active && sp < nsplit) {
+            const float f = st[k].x == -INFINITY ? 0.f : __expf(st[k].x - mx);
+            fw[rr][sp] = f;
+            ls += st[k].y * f;
         }
+    }
 #pragma unroll
     for (int o = 16; o > 0; o >>= 1) ls += __shfl_xor(ls, o, WAVE);
     __syncthreads();
     if (!active) return;
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    const int d0 = t32 * 8;
-    int s = 0;
-    for (; s + 4 <= nsplit; s += 4) {
-        float4 v[4][2];
+    // software-pipelined over batches of SB splits: the next batch's loads are in flight while
+    // this one accumulates (the partials come from other XCDs: each batch is a full memory
+    // latency); batch indices past the last split re-read it and are weighted 0
+    constexpr int SB = 4;
+    float4 cur[SB][2], nxt[SB][2];
+    auto load_batch = [&](float4 (&v)[SB][2], int s0) {
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-            const float4* p = (const float4*)(part + ((base + s + e) * G + rr) * HD + d0);
+        for (int e = 0; e < SB; e++) {
+            const float4* p = (const float4*)(part + ((base + min(s0 + e, nsplit - 1)) * G + rr) * HD + d0);
             v[e][0] = p[0];
             v[e][1] = p[1];
         }
+    };
+    load_batch(cur, 0);
+    for (int s = 0; s < nsplit; s += SB) {
+        load_batch(nxt, s + SB);
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-            const float f = fw[rr][s + e];
-            acc[0] += v[e][0].x * f; acc[1] += v[e][0].y * f; acc[2] += v[e][0].z * f; acc[3] += v[e][0].w * f;
-            acc[4] += v[e][1].x * f; acc[5] += v[e][1].y * f; acc[6] += v[e][1].z * f; acc[7] += v[e][1].w * f;
+        for (int e = 0; e < SB; e++) {
+            const float f = s + e < nsplit ? fw[rr][s + e] : 0.f;
+            acc[0] += cur[e][0].x * f; acc[1] += cur[e][0].y * f; acc[2] += cur[e][0].z * f; acc[3] += cur[e][0].w * f;
+            acc[4] += cur[e][1].x * f; acc[5] += cur[e][1].y * f; acc[6] += cur[e][1].z * f; acc[7] += cur[e][1].w * f;
+        }
+#pragma unroll
+        for (int e = 0; e < SB; e++) {
+            cur[e][0] = nxt[e][0];
+            cur[e][1] = nxt[e][1];
         }
     }
-    for (; s < nsplit; s++) {
-        const float4* p = (const float4*)(part + ((base + s) * G + rr) * HD + d0);
-        const float4 v0 = p[0], v1 = p[1];
-        const float f = fw[rr][s];
-        acc[0] += v0.x * f; acc[1] += v0.y * f; acc[2] += v0.z * f; acc[3] += v0.w * f;
-        acc[4] += v1.x * f; acc[5] += v1.y * f; acc[6] += v1.z * f; acc[7] += v1.w * f;
-    }
-    const size_t row = row0 + rr;
     const float inv = 1.f / ls;
 #pragma unroll
     for (int e = 0; e < 8; e++) {
         float y = acc[e] * inv;
-        if (gate) y *= sigmoid_f(Act<TG>::ld(gate, row * gate_stride + d0 + e));
+        if (gate) y *= sigmoid_f(gv[e]);
         Act<Tout>::st(out, row * out_stride + d0 + e, y);
     }
 }
