@@ -19,6 +19,8 @@
 // fp32 dot product to ~1e-5 relative; a bf16 X needs only the hi half.
 #include "common.h"
 
+#include <type_traits>
+
 using namespace aegist;
 
 namespace {
@@ -188,8 +190,15 @@ __global__ __launch_bounds__(64 * NWAVE) void proj_skinny_kernel(const TX* __res
     // The epilogue's row scales (and, when accumulating, the old Y values) of the tiles this
     // wave finishes (tile t by wave t % NWAVE) are requested now, so they arrive with the
     // weights instead of costing a round trip at the end.
+    // int8 weights (always with row scales): the loads are unconditional and their values are
+    // only used in the epilogue (a guarded load whose value is used inside its branch waits for
+    // it there, before the weight stream starts; measured 6% at M = 1). Without row scales or
+    // accumulation every lane reads one word that the epilogue ignores (one cache line). bf16
+    // weights (normally without scales) keep guarded loads, which then issue nothing.
+    constexpr bool kEarly = std::is_same<TW, int8_t>::value;
     constexpr int NFIN = (RT * MT + NWAVE - 1) / NWAVE;  // tiles finished per wave, at most
-    float fscale[NFIN][4], fy[NFIN][4];
+    uint16_t sraw[NFIN][4];
+    float fsc[NFIN][4], fy[NFIN][4];
 #pragma unroll
     for (int u = 0; u < NFIN; u++) {
         const int t = wave + NWAVE * u, rt = t / MT, mt = t % MT;
@@ -198,8 +207,14 @@ __global__ __launch_bounds__(64 * NWAVE) void proj_skinny_kernel(const TX* __res
         for (int j = 0; j < 4; j++) {
             const int n = n0 + 16 * rt + 4 * g + j;
             const bool ok = t < RT * MT && n < N && m < M;
-            fscale[u][j] = (ok && scale) ? bf2f(scale[n]) : 1.f;
-            fy[u][j] = (ok && accumulate) ? Y[(size_t)m * ldy + n] : 0.f;
+            if constexpr (kEarly) {
+                const int nn = ok ? n : 0, mm = ok ? m : 0;
+                sraw[u][j] = *(scale ? scale + nn : (const uint16_t*)W);
+                fy[u][j] = *(accumulate ? Y + (size_t)mm * ldy + nn : Y);
+            } else {
+                fsc[u][j] = (ok && scale) ? bf2f(scale[n]) : 1.f;
+                fy[u][j] = (ok && accumulate) ? Y[(size_t)m * ldy + n] : 0.f;
+            }
         }
     }
 
@@ -274,7 +289,10 @@ __global__ __launch_bounds__(64 * NWAVE) void proj_skinny_kernel(const TX* __res
         for (int j = 0; j < 4; j++) {
             const int n = n0 + 16 * rt + 4 * g + j;
             if (n >= N) continue;
-            yrow[n] = fy[u][j] + v[j] * fscale[u][j];
+            if constexpr (kEarly)
+                yrow[n] = (accumulate ? fy[u][j] : 0.f) + v[j] * (scale ? bf2f(sraw[u][j]) : 1.f);
+            else
+                yrow[n] = fy[u][j] + v[j] * fsc[u][j];
         }
     }
 }
