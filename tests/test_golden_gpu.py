@@ -1,0 +1,137 @@
+"""The HIP path against the reference's own outputs (tests/golden/*.npz, written by
+aegist/hybrid.py's modules in fp32; see tests/golden/make_fixtures.py).
+
+- Engine-ABI mirrors composed as HybridEngine::mixer composes them (hybrid.rs:787-861: fp32
+  activations, bf16 weights, batch 1), one batch row of the fixture at a time: the DeltaNet arm
+  (projections, delta_gates, conv_silu, l2norm_heads, delta_scan, gated_norm, out projection)
+  over prefill 130 -> decode 1 -> feed 70 -> decode 1, and the attention arm (projections,
+  attn_prep, attention_gated, out projection) over 300 -> 1 -> 20 -> 1. Bars: the north-star
+  tolerances, 1e-3 (DeltaNet) and 2e-3 (attention), on the mixer output. The attention arm keeps
+  its KV cache in bf16 as the engine does, while the fixture's fp32 model keeps fp32 keys and
+  values; that rounding alone moves the output by 1.5e-3 to 2.5e-3 (the CPU oracle with a bf16
+  cache, computed in the test). So the attention arm is held to 2e-3 against that oracle and,
+  against the fixture, to no more than 1.25x the distance the bf16 cache itself forces.
+- The batched stack (aegist_stack_*) on the 4-block fixture: bf16 activations into the
+  projections (a bf16 model's arithmetic), so its distance to the fp32 fixture is the bf16
+  rounding of every projection input. The CPU oracle with the same rounding measures 8.0e-3 /
+  6.7e-3 / 4.6e-3 / 3.6e-3 on the four feeds against the fixture; the bar is 1.2e-2."""
+import sys
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import rel_err
+from oracle import mixer_ref as R
+
+from aegist_mixer import ops
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+sys.path.insert(0, str(GOLDEN))
+import gen  # noqa: E402
+import make_fixtures as MF  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+C = gen.CFG
+
+
+def _fx(name):
+    return dict(np.load(GOLDEN / f"{name}.npz"))
+
+
+def _dev_w(W, dev):
+    return {k: torch.from_numpy(v).to(torch.bfloat16).to(dev).contiguous() for k, v in W.items()}
+
+
+def test_engine_deltanet_arm_matches_reference(dev):
+    fx = _fx("deltanet_mixer")
+    W = _dev_w(gen.layer_weights("dn.", "delta"), dev)
+    hk, hv = C["hk"], C["hv"]
+    Cc = 2 * hk * 128 + hv * 128
+    feeds = gen.feeds("dn.", MF.B, MF.DELTA_FEEDS)
+    for b in range(MF.B):
+        conv = torch.zeros(Cc, 3, device=dev)
+        state = torch.zeros(hv, 128, 128, device=dev)
+        for i, x in enumerate(feeds):
+            print(f"deltanet row {b} feed {i} T={x.shape[1]}", flush=True)
+            h = torch.from_numpy(x[b]).to(dev)
+            T = h.shape[0]
+            qkv = ops.linear(h, W["w_qkv"])
+            z = ops.linear(h, W["w_z"])
+            gb = ops.engine_delta_gates(h, W["w_b"], W["w_a"], W["a_log"], W["dt_bias"])
+            y = ops.engine_conv_silu(qkv, W["conv_w"], conv)
+            ops.engine_l2norm_heads(y, hk)
+            o = ops.engine_delta_scan(y, gb, state, hk, hv)
+            on = ops.engine_gated_norm(o, z.view(T, hv, 128), W["gnorm_w"])
+            out = ops.linear(on.view(T, hv * 128), W["w_out"])
+            torch.cuda.synchronize()
+            err = rel_err(out, torch.from_numpy(fx[f"y{i}"][b]))
+            print(f"  err {err:.3e}", flush=True)
+            assert err < 1e-3, (b, i, err)
+        assert rel_err(state, torch.from_numpy(fx["state"][b])) < 1e-3
+        # the conv state holds raw projection outputs: fp32-level agreement (the projection kernel
+        # sums in another order than torch's matmul)
+        assert rel_err(conv, torch.from_numpy(fx["conv"][b])) < 1e-5
+
+
+def test_engine_attention_arm_matches_reference(dev):
+    fx = _fx("attention_mixer")
+    W = _dev_w(gen.layer_weights("ga.", "attn"), dev)
+    H, KV, HD = C["n_heads"], C["n_kv"], C["head_dim"]
+    cap = 512
+    feeds = gen.feeds("ga.", MF.B, MF.ATTN_FEEDS)
+    Wc = {k: torch.from_numpy(v) for k, v in gen.layer_weights("ga.", "attn").items()}
+    okc = torch.zeros(MF.B, KV, cap, HD, dtype=torch.bfloat16)
+    ovc = torch.zeros_like(okc)
+    oref, opos = [], 0
+    for x in feeds:
+        oref.append(R.gated_attention_mixer(torch.from_numpy(x), Wc, okc, ovc, opos, H, KV, HD, C["rotary_dim"],
+                                            C["rope_theta"], C["eps"], round_in=False))
+        opos += x.shape[1]
+    for b in range(MF.B):
+        kc = torch.zeros(KV, cap, HD, dtype=torch.bfloat16, device=dev)
+        vc = torch.zeros_like(kc)
+        pos = 0
+        for i, x in enumerate(feeds):
+            print(f"attention row {b} feed {i} T={x.shape[1]} pos={pos}", flush=True)
+            h = torch.from_numpy(x[b]).to(dev)
+            T = h.shape[0]
+            qg = ops.linear(h, W["w_q"]).view(T, H, 2 * HD)
+            k = ops.linear(h, W["w_k"]).view(T, KV, HD)
+            v = ops.linear(h, W["w_v"]).view(T, KV, HD)
+            qn = ops.engine_attn_prep(qg, k, v, W["q_norm"], W["k_norm"], kc, vc, pos, C["rotary_dim"],
+                                      C["rope_theta"], C["eps"])
+            att = ops.engine_attention_gated(qn, kc, vc, qg, pos)
+            out = ops.linear(att.view(T, H * HD), W["w_o"])
+            torch.cuda.synchronize()
+            pos += T
+            err = rel_err(out, torch.from_numpy(fx[f"y{i}"][b]))
+            err_o = rel_err(out, oref[i][b])
+            forced = rel_err(oref[i][b], torch.from_numpy(fx[f"y{i}"][b]))
+            print(f"  err vs fixture {err:.3e} (bf16 cache forces {forced:.3e}), vs oracle {err_o:.3e}", flush=True)
+            assert err_o < 2e-3, (b, i, err_o)
+            assert err < max(2e-3, 1.25 * forced), (b, i, err, forced)
+        # the cache rows are the reference's fp32 rows rounded to bf16
+        ref_k = torch.from_numpy(fx["k_rows"][b]).to(torch.bfloat16).float()
+        got_k = kc[:, MF.K_ROWS].float().cpu()
+        assert rel_err(got_k, ref_k) < 2 ** -8
+        assert torch.equal(vc[:, MF.K_ROWS].cpu(), torch.from_numpy(fx["v_rows"][b]).to(torch.bfloat16))
+
+
+def test_stack_matches_reference_blocks(dev):
+    fx = _fx("stack4")
+    layers = [_dev_w(gen.layer_weights(f"st{i}.", k), dev) for i, k in enumerate(gen.KINDS)]
+    cfg = dict(d_model=C["d_model"], hk=C["hk"], hv=C["hv"], n_heads=C["n_heads"], n_kv=C["n_kv"],
+               head_dim=C["head_dim"], rotary_dim=C["rotary_dim"], rope_theta=C["rope_theta"], eps=C["eps"])
+    stack = ops.HybridStack(cfg, gen.KINDS, layers, max_batch=MF.B, max_tokens=MF.B * 128, max_context=256)
+    for i, x in enumerate(gen.feeds("st.", MF.B, MF.STACK_FEEDS)):
+        print(f"stack feed {i} T={x.shape[1]}", flush=True)
+        xd = torch.from_numpy(x).to(dev).contiguous()
+        x0 = xd.clone()
+        stack.forward(xd)
+        torch.cuda.synchronize()
+        err = rel_err(xd - x0, torch.from_numpy(fx[f"y{i}"] - x))
+        print(f"  err {err:.3e}", flush=True)
+        assert err < 1.2e-2, (i, err)
+    stack.close()
