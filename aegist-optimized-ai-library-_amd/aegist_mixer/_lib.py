@@ -23,6 +23,7 @@ SIGNATURES: dict[str, tuple] = {
     "aegist_last_error": (C.c_char_p, []),
     "aegist_version": (C.c_char_p, []),
     "aegist_set_device": (I, [I]),
+    "aegist_bind_workspace": (I, [P, SZ]),
     "aegist_malloc": (I, [C.POINTER(C.c_void_p), SZ]),
     "aegist_free": (I, [P]),
     "aegist_memcpy_htod": (I, [P, P, SZ, P]),
@@ -35,10 +36,14 @@ SIGNATURES: dict[str, tuple] = {
     "aegist_znorm": (I, [P, P, P, I, I, F, P]),
     "aegist_attn_prep": (I, [P, P, P, P, P, P, P, P, I, I, I, I, I, I, I, F, F, P]),
     "aegist_attention_gated": (I, [P, P, P, P, P, I, I, I, I, I, F, P]),
+    "aegist_attention_gated_workspace_bytes": (SZ, [I, I, I, I]),
+    "aegist_attention_gated_ws": (I, [P, P, P, P, P, I, I, I, I, I, F, P, SZ, P]),
     "aegist_delta_gates": (I, [P, P, P, P, P, P, I, I, I, P]),
     "aegist_conv_silu": (I, [P, P, P, P, I, I, P]),
     "aegist_l2norm_heads": (I, [P, I, I, I, I, F, F, P]),
     "aegist_delta_scan": (I, [P, P, P, P, I, I, I, I, P]),
+    "aegist_delta_scan_workspace_bytes": (SZ, [I, I, I]),
+    "aegist_delta_scan_ws": (I, [P, P, P, P, I, I, I, I, P, SZ, P]),
     "aegist_gated_norm": (I, [P, P, P, P, I, I, I, F, P]),
     "aegist_delta_decode_step": (I, [P, I, P, P, P, P, P, P, I, I, I, I, F, F, P]),
     "aegist_delta_recurrent": (I, [P, P, P, I, LL, LL, LL, LL, LL, LL, P, P, P, P, I, LL, LL, LL,
@@ -66,7 +71,11 @@ SIGNATURES: dict[str, tuple] = {
     "aegist_idx_blocks": (I, [P, P, P, I, I, I, I, I, F, F, P]),
     "aegist_idx_scores": (I, [P, P, P, I, I, I, I, I, I, P]),
     "aegist_idx_select": (I, [P, P, P, I, I, I, I, I, P]),
+    "aegist_idx_select_workspace_bytes": (SZ, [I, I, I, I]),
+    "aegist_idx_select_ws": (I, [P, P, P, I, I, I, I, I, P, SZ, P]),
     "aegist_attention_gated_list": (I, [P, P, P, P, P, I, I, I, I, I, F, P, P, I, I, P]),
+    "aegist_attention_gated_list_workspace_bytes": (SZ, [I, I, I, I, I, I]),
+    "aegist_attention_gated_list_ws": (I, [P, P, P, P, P, I, I, I, I, I, F, P, P, I, I, P, SZ, P]),
     "aegist_gated_norm2": (I, [P, P, P, P, I, I, I, F, I, P]),
     "aegist_gemv_i8": (I, [P, P, P, P, I, I, I, P]),
     "aegist_gemv_bf16": (I, [P, P, P, I, I, P]),
@@ -74,6 +83,8 @@ SIGNATURES: dict[str, tuple] = {
     "aegist_linear": (I, [P, I, LL, P, I, P, P, LL, I, I, I, I, P]),
     "aegist_linear_multi": (I, [P, I, LL, I, I, P, P, P, P, P, I, I, I, P]),
     "aegist_router_topk": (I, [P, P, P, P, I, I, I, I, P]),
+    "aegist_router_topk_workspace_bytes": (SZ, [I, I]),
+    "aegist_router_topk_ws": (I, [P, P, P, P, I, I, I, I, P, SZ, P]),
     "aegist_moe_workspace_bytes": (SZ, [I, I, I, I, I]),
     "aegist_moe_experts": (I, [P, P, P, P, P, I, I, I, I, I, P, P, P, SZ, P]),
     "aegist_shared_gate_add": (I, [P, P, P, P, I, I, P]),

@@ -46,7 +46,10 @@ _ws_cache: dict[tuple, torch.Tensor] = {}
 
 
 def _workspace(nbytes: int, device) -> torch.Tensor:
-    """Workspace tensor of at least nbytes (kept per device, grown on demand)."""
+    """Workspace tensor of at least nbytes (kept per device, grown on demand). The library
+    never allocates: this caller-side buffer is what the *_ws entry points receive. Reuse is
+    ordered on the current stream; a replaced buffer is released through torch's
+    stream-ordered caching allocator."""
     key = (str(device),)
     ws = _ws_cache.get(key)
     if ws is None or ws.numel() < nbytes:
@@ -217,7 +220,10 @@ def engine_attention_gated(qn, kc, vc, qg, pos0):
     T, H, HD = qn.shape
     KV, cap, _ = kc.shape
     out = torch.empty(T, H, HD, dtype=torch.float32, device=qn.device)
-    call("aegist_attention_gated", _p(qn), _p(kc), _p(vc), _p(qg), _p(out), T, H, KV, pos0, cap, HD ** -0.5,
+    need = lib().aegist_attention_gated_workspace_bytes(T, H, KV, pos0)
+    ws = _workspace(need, qn.device)
+    call("aegist_attention_gated_ws", _p(qn), _p(kc), _p(vc), _p(qg), _p(out), T, H, KV, pos0, cap, HD ** -0.5,
+         _p(ws), ws.numel(),
          _stream())
     return out
 
@@ -246,7 +252,8 @@ def engine_l2norm_heads(y, nq, dk=128, qscale=128 ** -0.5, eps=1e-6):
 def engine_delta_scan(y, gb, state, hk, hv):
     T, Cc = y.shape
     o = torch.empty(T, hv, 128, dtype=torch.float32, device=y.device)
-    call("aegist_delta_scan", _p(y), _p(gb), _p(state), _p(o), T, Cc, hk, hv, _stream())
+    ws = _workspace(lib().aegist_delta_scan_workspace_bytes(T, hk, hv), y.device)
+    call("aegist_delta_scan_ws", _p(y), _p(gb), _p(state), _p(o), T, Cc, hk, hv, _p(ws), ws.numel(), _stream())
     return o
 
 
@@ -285,7 +292,9 @@ def engine_idx_scores(qi, bk, sc, pos0: int, R: int):
 
 def engine_idx_select(sc, blist, nsel, top: int, R: int, pos0: int):
     _need_contig(sc, blist, nsel)
-    call("aegist_idx_select", _p(sc), _p(blist), _p(nsel), sc.shape[0], top, R, pos0, sc.shape[1], _stream())
+    ws = _workspace(lib().aegist_idx_select_workspace_bytes(sc.shape[0], top, R, pos0), sc.device)
+    call("aegist_idx_select_ws", _p(sc), _p(blist), _p(nsel), sc.shape[0], top, R, pos0, sc.shape[1], _p(ws),
+         ws.numel(), _stream())
     return blist, nsel
 
 
@@ -295,8 +304,9 @@ def engine_attention_gated_list(q, kc, vc, qg, pos0: int, blist, nsel, top: int,
     T, H, HD = q.shape
     KV, cap = kc.shape[0], kc.shape[1]
     out = torch.empty(T, H, HD, dtype=torch.float32, device=q.device)
-    call("aegist_attention_gated_list", _p(q), _p(kc), _p(vc), _p(qg), _p(out), T, H, KV, pos0, cap,
-         HD ** -0.5 if scale is None else scale, _p(blist), _p(nsel), top, R, _stream())
+    ws = _workspace(lib().aegist_attention_gated_list_workspace_bytes(T, H, KV, pos0, top, R), q.device)
+    call("aegist_attention_gated_list_ws", _p(q), _p(kc), _p(vc), _p(qg), _p(out), T, H, KV, pos0, cap,
+         HD ** -0.5 if scale is None else scale, _p(blist), _p(nsel), top, R, _p(ws), ws.numel(), _stream())
     return out
 
 
@@ -418,7 +428,8 @@ def router_topk(h, W, K: int):
     E = W.shape[0]
     idx = torch.empty(T, K, dtype=torch.int32, device=h.device)
     wts = torch.empty(T, K, dtype=torch.float32, device=h.device)
-    call("aegist_router_topk", _p(h), _p(W), _p(idx), _p(wts), T, D, E, K, _stream())
+    ws = _workspace(lib().aegist_router_topk_workspace_bytes(T, E), h.device)
+    call("aegist_router_topk_ws", _p(h), _p(W), _p(idx), _p(wts), T, D, E, K, _p(ws), ws.numel(), _stream())
     return idx, wts
 
 

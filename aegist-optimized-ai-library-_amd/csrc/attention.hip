@@ -887,21 +887,26 @@ int aegist_attention_core(const float* q, const uint16_t* kc, const uint16_t* vc
     return launch_prefill_core(q, qs, kc, vc, gate, gs, out, os, B, H, KV, T, pos, cap, scale, st);
 }
 
+size_t aegist_attention_gated_workspace_bytes(int T, int H, int KV, int pos0) {
+    if (T != 1 || H <= 0 || KV <= 0 || pos0 < 0) return 0;  // only the T == 1 split-K path uses scratch
+    return decode_workspace_bytes(1, H, KV, pos0 + 1, false);
+}
+
 // Engine mirror: q = qn [T, H, HD] fp32 (from attn_prep), gate inside qg [T, H, 2*HD],
-// out [T, H, HD]; batch 1, caches [KV, cap, HD].
-int aegist_attention_gated(const float* q, const uint16_t* kc, const uint16_t* vc, const float* qg, float* out, int T,
-                           int H, int KV, int pos0, int cap, float scale, void* stream) {
+// out [T, H, HD]; batch 1, caches [KV, cap, HD]. `ws` holds the split-K partials of T == 1.
+int aegist_attention_gated_ws(const float* q, const uint16_t* kc, const uint16_t* vc, const float* qg, float* out,
+                              int T, int H, int KV, int pos0, int cap, float scale, void* ws, size_t ws_bytes,
+                              void* stream) {
     AEG_REQUIRE(T >= 0 && H > 0 && KV > 0 && H % KV == 0, "attention_gated: need H % KV == 0");
     if (T == 0) return 0;
     hipStream_t st = AEG_STREAM(stream);
     if (T == 1) {
         AEG_REQUIRE(H / KV <= 8, "attention_gated: H/KV must be <= 8");
-        size_t need = decode_workspace_bytes(1, H, KV, pos0 + 1, false);
-        int rc = 0;
-        void* ws = mirror_workspace(need, &rc);
+        const size_t need = decode_workspace_bytes(1, H, KV, pos0 + 1, false);
+        int rc = check_workspace(ws, ws_bytes, need, "attention_gated");
         if (rc) return rc;
         return launch_decode_core<float, float>(q, kc, vc, qg + HD, 2 * HD, out, HD, 1, H, KV, pos0 + 1, cap, scale, ws,
-                                                need, st);
+                                                ws_bytes, st);
     }
     // engine layouts: q, out [T, H, HD]; gate rows inside qg [T, H, 2*HD]
     Strides3 qs{0, (long long)H * HD, HD};
@@ -909,24 +914,49 @@ int aegist_attention_gated(const float* q, const uint16_t* kc, const uint16_t* v
     return launch_prefill_core(q, qs, kc, vc, qg + HD, gs, out, qs, 1, H, KV, T, pos0, cap, scale, st);
 }
 
+// The reference signature (no workspace argument): T == 1 takes the workspace bound to this
+// thread (aegist_bind_workspace).
+int aegist_attention_gated(const float* q, const uint16_t* kc, const uint16_t* vc, const float* qg, float* out, int T,
+                           int H, int KV, int pos0, int cap, float scale, void* stream) {
+    size_t bound = 0;
+    void* ws = bound_workspace(&bound);
+    return aegist_attention_gated_ws(q, kc, vc, qg, out, T, H, KV, pos0, cap, scale, ws, bound, stream);
+}
+
+static int list_lmax(int T, int pos0, int top, int R) {
+    // longest key list: top blocks plus the keys of an incomplete block, and never more than the
+    // last query's position + 1
+    return std::min(top * R + R - 1, pos0 + T);
+}
+
+size_t aegist_attention_gated_list_workspace_bytes(int T, int H, int KV, int pos0, int top, int R) {
+    if (T <= 0 || H <= 0 || KV <= 0 || top <= 0 || R <= 0 || pos0 < 0) return 0;
+    return decode_workspace_bytes(T, H, KV, list_lmax(T, pos0, top, R), false);
+}
+
 // attention_gated over listed blocks (next.cu:648-705): the split-K decode kernel with one query
 // token per "sequence" and its keys taken from the block list. Engine layouts as attention_gated.
-int aegist_attention_gated_list(const float* q, const uint16_t* kc, const uint16_t* vc, const float* qg, float* out,
-                                int T, int H, int KV, int pos0, int cap, float scale, const int* blist,
-                                const int* nsel, int top, int R, void* stream) {
+int aegist_attention_gated_list_ws(const float* q, const uint16_t* kc, const uint16_t* vc, const float* qg,
+                                   float* out, int T, int H, int KV, int pos0, int cap, float scale, const int* blist,
+                                   const int* nsel, int top, int R, void* ws, size_t ws_bytes, void* stream) {
     AEG_REQUIRE(T >= 0 && H > 0 && KV > 0 && H % KV == 0 && H / KV <= 8,
                 "attention_gated_list: need H % KV == 0 and H/KV <= 8");
     AEG_REQUIRE(top > 0 && R > 0 && pos0 >= 0 && pos0 + T <= cap, "attention_gated_list: bad list or positions");
     if (T == 0) return 0;
-    // longest key list: top blocks plus the keys of an incomplete block, and never more than the
-    // last query's position + 1
-    const int Lmax = std::min(top * R + R - 1, pos0 + T);
-    const size_t need = decode_workspace_bytes(T, H, KV, Lmax, false);
-    int rc = 0;
-    void* ws = mirror_workspace(need, &rc);
+    const int Lmax = list_lmax(T, pos0, top, R);
+    int rc = check_workspace(ws, ws_bytes, decode_workspace_bytes(T, H, KV, Lmax, false), "attention_gated_list");
     if (rc) return rc;
-    return launch_decode_core<float, float>(q, kc, vc, qg + HD, 2 * HD, out, HD, T, H, KV, Lmax, cap, scale, ws, need,
-                                            AEG_STREAM(stream), nullptr, KeyList{blist, nsel, top, R, pos0});
+    return launch_decode_core<float, float>(q, kc, vc, qg + HD, 2 * HD, out, HD, T, H, KV, Lmax, cap, scale, ws,
+                                            ws_bytes, AEG_STREAM(stream), nullptr, KeyList{blist, nsel, top, R, pos0});
+}
+
+int aegist_attention_gated_list(const float* q, const uint16_t* kc, const uint16_t* vc, const float* qg, float* out,
+                                int T, int H, int KV, int pos0, int cap, float scale, const int* blist,
+                                const int* nsel, int top, int R, void* stream) {
+    size_t bound = 0;
+    void* ws = bound_workspace(&bound);
+    return aegist_attention_gated_list_ws(q, kc, vc, qg, out, T, H, KV, pos0, cap, scale, blist, nsel, top, R, ws,
+                                          bound, stream);
 }
 
 }  // extern "C"

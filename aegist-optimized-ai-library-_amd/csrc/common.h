@@ -87,8 +87,11 @@ void set_error(const std::string& msg);
 int fail(int code, const std::string& msg);
 int check_hip(hipError_t e, const char* what);
 int after_launch(const char* what);  // launch error check; honours AEGIST_SYNC_LAUNCH
-// Library-owned per-device workspace for the engine-ABI mirrors (grown on demand).
-void* mirror_workspace(size_t bytes, int* rc);
+// The workspace the calling thread bound on its current device (aegist_bind_workspace) and its
+// size; nullptr / 0 if none. Never allocates.
+void* bound_workspace(size_t* bytes);
+// AEGIST_ERR_WORKSPACE unless ws is non-null, 256-byte aligned and holds `need` bytes.
+int check_workspace(const void* ws, size_t ws_bytes, size_t need, const char* who);
 }  // namespace aegist
 
 #define AEG_REQUIRE(cond, msg)                                              \

@@ -936,15 +936,13 @@ int launch_delta_chunked(const void* q, const void* k, const void* v, int in_dty
 }
 
 // Engine mirror for T >= 64: y [T, C] rows q | k | v (already normalised), gb [T, 2HV].
+size_t delta_scan_chunked_ws_bytes(int T, int HK, int HV) { return delta_chunked_ws_bytes(1, T, HK, HV); }
+
 int delta_scan_chunked(const float* y, const float* gb, float* state, float* o, int T, int C, int HK, int HV,
-                       hipStream_t st) {
+                       void* ws, size_t ws_bytes, hipStream_t st) {
     SeqLayout a{0, C, D, 0, C, D, 0, (long long)HV * D, D, 0, 2 * HV};
-    size_t need = delta_chunked_ws_bytes(1, T, HK, HV);
-    int rc = 0;
-    void* ws = mirror_workspace(need, &rc);
-    if (rc) return rc;
     return launch_delta_chunked(y, y + (size_t)HK * D, y + (size_t)2 * HK * D, AEGIST_F32, a, gb, gb + HV, state, o,
-                                AEGIST_F32, 1, T, HK, HV, 0, 1.f, 0.f, ws, need, st);
+                                AEGIST_F32, 1, T, HK, HV, 0, 1.f, 0.f, ws, ws_bytes, st);
 }
 
 }  // namespace aegist

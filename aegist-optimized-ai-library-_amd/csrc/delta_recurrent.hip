@@ -146,17 +146,28 @@ extern "C" int aegist_delta_recurrent(const void* q, const void* k, const void* 
 // Engine mirror: y [T, C] fp32 rows q | k | v (already L2-normalised), gb [T, 2HV] (g, then
 // beta), state [HV, 128, 128], o [T, HV, 128]. Sequences of 64+ tokens take the chunked path.
 namespace aegist {
+size_t delta_scan_chunked_ws_bytes(int T, int HK, int HV);
 int delta_scan_chunked(const float* y, const float* gb, float* state, float* o, int T, int C, int HK, int HV,
+                       void* ws, size_t ws_bytes,
                        hipStream_t st);
 }
 
-extern "C" int aegist_delta_scan(const float* y, const float* gb, float* state, float* o, int T, int C, int HK, int HV,
-                                 void* stream) {
+extern "C" size_t aegist_delta_scan_workspace_bytes(int T, int HK, int HV) {
+    if (T < 64 || HK <= 0 || HV <= 0) return 0;
+    return delta_scan_chunked_ws_bytes(T, HK, HV);
+}
+
+extern "C" int aegist_delta_scan_ws(const float* y, const float* gb, float* state, float* o, int T, int C, int HK,
+                                    int HV, void* ws, size_t ws_bytes, void* stream) {
     if (T < 0 || HK <= 0 || HV <= 0 || HV % HK || C != 2 * HK * D + HV * D)
         return fail(AEGIST_ERR_SHAPE, "delta_scan: need C == 2*HK*128 + HV*128 and HV % HK == 0");
     if (T == 0) return 0;
     hipStream_t st = AEG_STREAM(stream);
-    if (T >= 64) return delta_scan_chunked(y, gb, state, o, T, C, HK, HV, st);
+    if (T >= 64) {
+        int rc = check_workspace(ws, ws_bytes, delta_scan_chunked_ws_bytes(T, HK, HV), "delta_scan");
+        if (rc) return rc;
+        return delta_scan_chunked(y, gb, state, o, T, C, HK, HV, ws, ws_bytes, st);
+    }
     // g and beta are interleaved per token in gb: present them through the strided kernel
     // by pointing g at gb and beta at gb + HV with a token stride of 2*HV.
     SeqArgs a{0, C, D, 0, C, D, 0, (long long)HV * D, D, 0, 2 * HV};
@@ -164,4 +175,13 @@ extern "C" int aegist_delta_scan(const float* y, const float* gb, float* state, 
     delta_recurrent_kernel<float, float><<<grid, 64, 0, st>>>(y, y + (size_t)HK * D, y + (size_t)2 * HK * D, gb,
                                                               gb + HV, state, o, a, T, HK, HV, 0, 1.f, 0.f);
     return after_launch("delta_scan");
+}
+
+// The reference signature (no workspace argument): T >= 64 takes the workspace bound to this
+// thread (aegist_bind_workspace).
+extern "C" int aegist_delta_scan(const float* y, const float* gb, float* state, float* o, int T, int C, int HK, int HV,
+                                 void* stream) {
+    size_t bound = 0;
+    void* ws = bound_workspace(&bound);
+    return aegist_delta_scan_ws(y, gb, state, o, T, C, HK, HV, ws, bound, stream);
 }

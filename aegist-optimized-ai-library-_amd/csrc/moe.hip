@@ -644,17 +644,21 @@ static MoePlan moe_plan(int T, int K, int D, int I, int E) {
 
 extern "C" {
 
-int aegist_router_topk(const float* h, const uint16_t* W, int* idx, float* wts, int T, int D, int E, int K,
-                       void* stream) {
+size_t aegist_router_topk_workspace_bytes(int T, int E) {
+    return T > 0 && E > 0 ? (size_t)T * E * 4 : 0;
+}
+
+int aegist_router_topk_ws(const float* h, const uint16_t* W, int* idx, float* wts, int T, int D, int E, int K,
+                          void* ws, size_t ws_bytes, void* stream) {
     AEG_REQUIRE(T >= 0 && D > 0 && D % 16 == 0, "router_topk: need D % 16 == 0");
     AEG_REQUIRE(E > 0 && E <= 64 * 64, "router_topk: need 0 < E <= 4096");
     AEG_REQUIRE(K > 0 && K <= 16 && K <= E, "router_topk: need 0 < K <= min(16, E)");
     if (T == 0) return 0;
     // logits [T, E] = h W^T on the projection kernel (fp32 h as bf16 hi + lo against the exact
-    // bf16 W), in the library's per-device scratch (stream-ordered reuse)
-    int rc = 0;
-    float* logits = (float*)mirror_workspace((size_t)T * E * 4, &rc);
+    // bf16 W), in the workspace
+    int rc = check_workspace(ws, ws_bytes, aegist_router_topk_workspace_bytes(T, E), "router_topk");
     if (rc) return rc;
+    float* logits = (float*)ws;
     hipStream_t st = AEG_STREAM(stream);
     rc = launch_proj(h, AEGIST_F32, D, W, AEGIST_BF16, nullptr, logits, E, T, E, D, 0, st);
     if (rc) return rc;
@@ -664,6 +668,13 @@ int aegist_router_topk(const float* h, const uint16_t* W, int* idx, float* wts, 
     else if (E <= 1024) router_topk_kernel<16><<<grid, 256, 0, st>>>(logits, idx, wts, T, E, K);
     else router_topk_kernel<64><<<grid, 256, 0, st>>>(logits, idx, wts, T, E, K);
     return after_launch("router_topk");
+}
+
+int aegist_router_topk(const float* h, const uint16_t* W, int* idx, float* wts, int T, int D, int E, int K,
+                       void* stream) {
+    size_t bound = 0;
+    void* ws = bound_workspace(&bound);
+    return aegist_router_topk_ws(h, W, idx, wts, T, D, E, K, ws, bound, stream);
 }
 
 size_t aegist_moe_workspace_bytes(int T, int K, int D, int I, int E) {

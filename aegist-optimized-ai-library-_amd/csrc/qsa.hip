@@ -447,8 +447,23 @@ int aegist_idx_scores(const float* qi, const float* bk, float* sc, int T, int H,
     return after_launch("idx_scores");
 }
 
-int aegist_idx_select(const float* sc, int* blist, int* nsel, int T, int top, int R, int pos0, int nbmax,
-                      void* stream) {
+// The two-phase form (few queries, many blocks) keeps its candidates in the workspace.
+static bool idx_select_two_phase(int T, int top, int R, int pos0, size_t* cand_bytes) {
+    const int nmax = (pos0 + T) / R;
+    const int P = (nmax + SEL1_RANGE - 1) / SEL1_RANGE;
+    const size_t m = (size_t)P * top;
+    *cand_bytes = (size_t)T * m * 8;
+    return T <= 16 && nmax > 8 * SEL_THREADS && 4 * m <= (size_t)nmax && m <= (size_t)32 * SEL_THREADS;
+}
+
+size_t aegist_idx_select_workspace_bytes(int T, int top, int R, int pos0) {
+    if (T <= 0 || top <= 0 || R <= 0 || pos0 < 0) return 0;
+    size_t cand = 0;
+    return idx_select_two_phase(T, top, R, pos0, &cand) ? cand : 0;
+}
+
+int aegist_idx_select_ws(const float* sc, int* blist, int* nsel, int T, int top, int R, int pos0, int nbmax, void* ws,
+                         size_t ws_bytes, void* stream) {
     AEG_REQUIRE(T >= 0 && top > 0 && R > 0 && pos0 >= 0, "idx_select: bad shape");
     AEG_REQUIRE((pos0 + T) / R <= nbmax, "idx_select: nbmax smaller than the number of complete blocks");
     if (T == 0) return 0;
@@ -458,10 +473,11 @@ int aegist_idx_select(const float* sc, int* blist, int* nsel, int T, int top, in
     const int P = (nmax + SEL1_RANGE - 1) / SEL1_RANGE;
     const size_t m = (size_t)P * top;
     // two phases when few queries see many blocks and the candidates are far fewer than the blocks
-    if (T <= 16 && nmax > 8 * SEL_THREADS && 4 * m <= (size_t)nmax && m <= (size_t)32 * SEL_THREADS) {
-        int rc = 0;
-        unsigned* cval = (unsigned*)mirror_workspace((size_t)T * m * 8, &rc);
+    size_t cand_bytes = 0;
+    if (idx_select_two_phase(T, top, R, pos0, &cand_bytes)) {
+        int rc = check_workspace(ws, ws_bytes, cand_bytes, "idx_select");
         if (rc) return rc;
+        unsigned* cval = (unsigned*)ws;
         int* cidx = (int*)(cval + (size_t)T * m);
         idx_select_part_kernel<<<dim3(P, T), SEL1_THREADS, 0, st>>>(sc, cval, cidx, top, R, pos0, nbmax, vec);
         const int vec2 = m % 4 == 0;
@@ -478,6 +494,13 @@ int aegist_idx_select(const float* sc, int* blist, int* nsel, int T, int top, in
     else
         idx_select_kernel<0><<<T, SEL_THREADS, 0, st>>>(sc, blist, nsel, top, R, pos0, nbmax, vec);
     return after_launch("idx_select");
+}
+
+int aegist_idx_select(const float* sc, int* blist, int* nsel, int T, int top, int R, int pos0, int nbmax,
+                      void* stream) {
+    size_t bound = 0;
+    void* ws = bound_workspace(&bound);
+    return aegist_idx_select_ws(sc, blist, nsel, T, top, R, pos0, nbmax, ws, bound, stream);
 }
 
 int aegist_gated_norm2(const float* o, const float* z, const uint16_t* w, float* out, int T, int HV, int DV, float eps,

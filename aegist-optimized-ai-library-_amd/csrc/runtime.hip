@@ -44,31 +44,33 @@ int after_launch(const char* what) {
     return 0;
 }
 
-// Library-owned per-device workspace for the engine-ABI mirrors whose reference signature has
-// no workspace argument. Grows on demand, never shrinks; freed at process exit by the runtime.
-void* mirror_workspace(size_t bytes, int* rc) {
-    static std::mutex mu;
-    static std::vector<std::pair<void*, size_t>> per_dev;
+// Workspace the engine-ABI mirrors use when their reference signature has no workspace
+// argument: bound by the caller (aegist_bind_workspace), per thread and per device, so the
+// library never allocates and two threads on two streams never share bytes. The engine
+// preallocates its scratch the same way (hybrid.rs:630-650).
+struct BoundWorkspace {
+    void* ptr = nullptr;
+    size_t bytes = 0;
+};
+static thread_local std::vector<BoundWorkspace> t_bound;
+
+void* bound_workspace(size_t* bytes) {
+    *bytes = 0;
     int dev = 0;
-    *rc = check_hip(hipGetDevice(&dev), "hipGetDevice");
-    if (*rc) return nullptr;
-    std::lock_guard<std::mutex> lock(mu);
-    if ((int)per_dev.size() <= dev) per_dev.resize(dev + 1, {nullptr, 0});
-    auto& slot = per_dev[dev];
-    if (slot.second < bytes) {
-        if (slot.first) {
-            // the previous buffer may still be in use by queued work on any stream
-            *rc = check_hip(hipDeviceSynchronize(), "hipDeviceSynchronize");
-            if (*rc) return nullptr;
-            (void)hipFree(slot.first);
-            slot = {nullptr, 0};
-        }
-        size_t grow = bytes < (64u << 20) ? (64u << 20) : bytes;
-        *rc = check_hip(hipMalloc(&slot.first, grow), "hipMalloc(mirror workspace)");
-        if (*rc) return nullptr;
-        slot.second = grow;
-    }
-    return slot.first;
+    if (hipGetDevice(&dev) != hipSuccess || dev >= (int)t_bound.size()) return nullptr;
+    *bytes = t_bound[dev].bytes;
+    return t_bound[dev].ptr;
+}
+
+int check_workspace(const void* ws, size_t ws_bytes, size_t need, const char* who) {
+    if (need == 0) return 0;
+    if (!ws || ws_bytes < need)
+        return fail(AEGIST_ERR_WORKSPACE, std::string(who) + ": workspace of " + std::to_string(need) +
+                                              " bytes required, got " + std::to_string(ws ? ws_bytes : 0) +
+                                              " (pass one to the *_ws form, or bind one with aegist_bind_workspace)");
+    if ((uintptr_t)ws % 256)
+        return fail(AEGIST_ERR_WORKSPACE, std::string(who) + ": workspace must be 256-byte aligned");
+    return 0;
 }
 
 }  // namespace aegist
@@ -82,6 +84,16 @@ const char* aegist_last_error(void) { return g_last_error.c_str(); }
 const char* aegist_version(void) { return "aegist_mixer 0.1 (gfx950)"; }
 
 int aegist_set_device(int device) { return check_hip(hipSetDevice(device), "hipSetDevice"); }
+
+int aegist_bind_workspace(void* ws, size_t bytes) {
+    int dev = 0;
+    int rc = check_hip(hipGetDevice(&dev), "hipGetDevice");
+    if (rc) return rc;
+    if (ws && (uintptr_t)ws % 256) return fail(AEGIST_ERR_WORKSPACE, "bind_workspace: must be 256-byte aligned");
+    if ((int)t_bound.size() <= dev) t_bound.resize(dev + 1);
+    t_bound[dev] = ws ? BoundWorkspace{ws, bytes} : BoundWorkspace{};
+    return 0;
+}
 
 int aegist_malloc(void** ptr, size_t bytes) { return check_hip(hipMalloc(ptr, bytes), "hipMalloc"); }
 

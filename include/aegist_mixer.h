@@ -11,12 +11,18 @@
  *  - Every function returns 0 on success, a positive hipError_t value on a runtime error, or
  *    a negative AEGIST_ERR_* code on a rejected argument. aegist_last_error() gives the text
  *    (thread-local). Nothing throws across the ABI.
- *  - All device pointers are caller-owned; kernels never allocate. Entry points that need
- *    scratch take a caller-provided workspace sized by the matching *_workspace_bytes query.
- *    The engine-ABI mirrors whose reference signature has no workspace argument
- *    (aegist_attention_gated, aegist_delta_scan) use a per-device workspace the library grows
- *    on demand; aegist_stack_create allocates the stack's states and scratch once. Nothing
- *    else allocates.
+ *  - All device pointers are caller-owned; no launch path allocates, frees or synchronises
+ *    the device. Entry points that need scratch take a caller-provided workspace sized by the
+ *    matching *_workspace_bytes query (256-byte aligned). The engine-ABI mirrors whose
+ *    reference signature has no workspace argument (aegist_attention_gated, aegist_delta_scan,
+ *    aegist_attention_gated_list, aegist_idx_select, aegist_router_topk) have an *_ws variant
+ *    taking (ws, ws_bytes) explicitly; the reference-signature form uses the workspace the
+ *    calling thread bound on its current device with aegist_bind_workspace (the engine's
+ *    preallocated scratch, hybrid.rs:630-650) and fails with AEGIST_ERR_WORKSPACE if none or
+ *    too little is bound. A bound workspace is reused by every such call of that thread:
+ *    calls on one stream are ordered, calls of one thread on two streams must not overlap.
+ *    aegist_stack_create allocates the stack's states and scratch once; aegist_malloc
+ *    allocates. Nothing else allocates.
  *  - `stream` is a hipStream_t (NULL = the device's null stream). Every launch is
  *    asynchronous on that stream; no entry point synchronises unless named *_sync. Setting
  *    AEGIST_SYNC_LAUNCH=1 synchronises after each launch and reports errors at the launch.
@@ -51,6 +57,11 @@ enum {
 const char* aegist_last_error(void);
 const char* aegist_version(void);
 int aegist_set_device(int device);
+/* Binds caller-owned device memory (256-byte aligned, `bytes` long; NULL unbinds) as the
+ * workspace of the reference-signature engine mirrors for the calling thread on its current
+ * device. The library never frees it. Replaces the engine's preallocated scratch buffers
+ * (hybrid.rs:630-650), which the reference kernels receive as plain pointers. */
+int aegist_bind_workspace(void* ws, size_t bytes);
 int aegist_malloc(void** ptr, size_t bytes);
 int aegist_free(void* ptr);
 int aegist_memcpy_htod(void* dst, const void* src, size_t bytes, void* stream);
@@ -88,6 +99,12 @@ int aegist_attn_prep(const float* qg, const float* k, const float* v, const uint
  * Replaces attention_gated, hybrid.cu:121-173 (launched hybrid.rs:810-818). */
 int aegist_attention_gated(const float* q, const uint16_t* kc, const uint16_t* vc, const float* qg, float* out, int T,
                            int H, int KV, int pos0, int cap, float scale, void* stream);
+/* Workspace of attention_gated (non-zero only for T == 1: the split-K partials). */
+size_t aegist_attention_gated_workspace_bytes(int T, int H, int KV, int pos0);
+/* attention_gated with an explicit workspace. */
+int aegist_attention_gated_ws(const float* q, const uint16_t* kc, const uint16_t* vc, const float* qg, float* out,
+                              int T, int H, int KV, int pos0, int cap, float scale, void* ws, size_t ws_bytes,
+                              void* stream);
 
 /* beta = sigmoid(h . Wb[j]); g = -exp(A_log[j]) * softplus(h . Wa[j] + dt_bias[j]).
  * gb [T, 2*HV]: g in [0, HV), beta in [HV, 2*HV).
@@ -112,6 +129,11 @@ int aegist_l2norm_heads(float* y, int T, int C, int nq, int dk, float qscale, fl
  * Replaces delta_scan, hybrid.cu:240-300 (launched hybrid.rs:845-852). */
 int aegist_delta_scan(const float* y, const float* gb, float* state, float* o, int T, int C, int HK, int HV,
                       void* stream);
+/* Workspace of delta_scan (non-zero only for T >= 64: the chunked prefill's per-chunk operands). */
+size_t aegist_delta_scan_workspace_bytes(int T, int HK, int HV);
+/* delta_scan with an explicit workspace. */
+int aegist_delta_scan_ws(const float* y, const float* gb, float* state, float* o, int T, int C, int HK, int HV,
+                         void* ws, size_t ws_bytes, void* stream);
 
 /* out = w * rmsnorm(o) * silu(z) per value head. o, z, out [T,HV,DV] fp32; w [DV] bf16.
  * Replaces gated_norm, hybrid.cu:303-311 (launched hybrid.rs:853-857). */
@@ -283,16 +305,23 @@ int aegist_idx_blocks(const float* kraw, const uint16_t* kw, float* bk, int b0, 
 int aegist_idx_scores(const float* qi, const float* bk, float* sc, int T, int H, int HD, int pos0, int R, int nbmax,
                       void* stream);
 /* idx_select, next.cu:543-625: per query, all n complete blocks when n <= top (nsel = n), else
- * the top highest scores (ties to the lower block), listed in block order (nsel = top). Up to 16
- * queries over more than 8192 blocks stage candidates in the library's per-device workspace
- * (grown by hipMalloc on first use). */
+ * the top highest scores (ties to the lower block), listed in block order (nsel = top). Scores
+ * must be finite and non-negative (idx_scores' relu guarantees it): they are ordered by their
+ * bit patterns. Up to 16 queries over more than 8192 blocks stage candidates in the workspace. */
 int aegist_idx_select(const float* sc, int* blist, int* nsel, int T, int top, int R, int pos0, int nbmax,
                       void* stream);
+size_t aegist_idx_select_workspace_bytes(int T, int top, int R, int pos0);
+int aegist_idx_select_ws(const float* sc, int* blist, int* nsel, int T, int top, int R, int pos0, int nbmax, void* ws,
+                         size_t ws_bytes, void* stream);
 /* attention_gated_list, next.cu:627-705: attention_gated for query t over the R keys of each
  * listed block plus its own incomplete block (positions (pos0 + t + 1) / R * R .. pos0 + t) */
 int aegist_attention_gated_list(const float* q, const uint16_t* kc, const uint16_t* vc, const float* qg, float* out,
                                 int T, int H, int KV, int pos0, int cap, float scale, const int* blist,
                                 const int* nsel, int top, int R, void* stream);
+size_t aegist_attention_gated_list_workspace_bytes(int T, int H, int KV, int pos0, int top, int R);
+int aegist_attention_gated_list_ws(const float* q, const uint16_t* kc, const uint16_t* vc, const float* qg,
+                                   float* out, int T, int H, int KV, int pos0, int cap, float scale, const int* blist,
+                                   const int* nsel, int top, int R, void* ws, size_t ws_bytes, void* stream);
 /* gated_norm2, next.cu:129-142: out = w * rmsnorm(o) * (sig ? sigmoid(z) : silu(z)) */
 int aegist_gated_norm2(const float* o, const float* z, const uint16_t* w, float* out, int T, int HV, int DV, float eps,
                        int sig, void* stream);
@@ -338,6 +367,10 @@ int aegist_linear_multi(const void* X, int x_dtype, long long ldx, int w_dtype, 
  * the lower expert); wts [T, K] = p / sum of the picked p. */
 int aegist_router_topk(const float* h, const uint16_t* W, int* idx, float* wts, int T, int D, int E, int K,
                        void* stream);
+/* Workspace of router_topk (the [T, E] fp32 logits). */
+size_t aegist_router_topk_workspace_bytes(int T, int E);
+int aegist_router_topk_ws(const float* h, const uint16_t* W, int* idx, float* wts, int T, int D, int E, int K,
+                          void* ws, size_t ws_bytes, void* stream);
 /* Workspace (device bytes) of aegist_moe_experts for up to T tokens. */
 size_t aegist_moe_workspace_bytes(int T, int K, int D, int I, int E);
 /* The routed experts (ExpertBank.forward, hybrid.py:608-628) added into the residual:

@@ -143,3 +143,23 @@ def test_indexer_entry_points_reject_shapes():
     assert L.aegist_gated_norm2(None, None, None, None, 1, 0, 128, 1e-6, 1, None) == -1
     # empty inputs are a no-op
     assert L.aegist_idx_select(None, None, None, 0, 16, 4, 0, 8, None) == 0
+
+
+def test_reference_signature_mirrors_need_a_bound_workspace():
+    """Mirrors whose reference signature has no workspace argument never allocate: with nothing
+    bound they return AEGIST_ERR_WORKSPACE (checked before any launch) and say how to bind one."""
+    L = _lib.lib()
+    assert L.aegist_attention_gated_workspace_bytes(1, 16, 2, 4096) > 0
+    assert L.aegist_attention_gated_workspace_bytes(5, 16, 2, 4096) == 0  # prefill uses no scratch
+    assert L.aegist_delta_scan_workspace_bytes(63, 16, 32) == 0
+    assert L.aegist_delta_scan_workspace_bytes(64, 16, 32) > 0
+    assert L.aegist_router_topk_workspace_bytes(4, 256) == 4 * 256 * 4
+    rc = L.aegist_attention_gated(None, None, None, None, None, 1, 16, 2, 4096, 8192, 0.0625, None)
+    assert rc == -2 and "aegist_bind_workspace" in _lib.last_error()
+    C_ = 2 * 16 * 128 + 32 * 128
+    assert L.aegist_delta_scan(None, None, None, None, 64, C_, 16, 32, None) == -2
+    assert L.aegist_router_topk(None, None, None, None, 4, 256, 256, 8, None) == -2
+    # an explicit workspace that is too small or misaligned is refused the same way
+    assert L.aegist_delta_scan_ws(None, None, None, None, 64, C_, 16, 32, None, 0, None) == -2
+    assert L.aegist_attention_gated_ws(None, None, None, None, None, 1, 16, 2, 4096, 8192, 0.0625, 8, 1 << 30,
+                                       None) == -2

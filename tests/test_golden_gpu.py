@@ -112,11 +112,13 @@ def test_engine_attention_arm_matches_reference(dev):
             print(f"  err vs fixture {err:.3e} (bf16 cache forces {forced:.3e}), vs oracle {err_o:.3e}", flush=True)
             assert err_o < 2e-3, (b, i, err_o)
             assert err < max(2e-3, 1.25 * forced), (b, i, err, forced)
-        # the cache rows are the reference's fp32 rows rounded to bf16
-        ref_k = torch.from_numpy(fx["k_rows"][b]).to(torch.bfloat16).float()
-        got_k = kc[:, MF.K_ROWS].float().cpu()
-        assert rel_err(got_k, ref_k) < 2 ** -8
-        assert torch.equal(vc[:, MF.K_ROWS].cpu(), torch.from_numpy(fx["v_rows"][b]).to(torch.bfloat16))
+        # the cache rows are the reference's fp32 rows rounded to bf16: within half a bf16 ulp of
+        # each element (at most 2^-8 relative) plus fp32-level differences in the projection and RoPE,
+        # which matter only for elements near zero (a roped value is a difference of two terms)
+        for got, name in ((kc, "k_rows"), (vc, "v_rows")):
+            ref = torch.from_numpy(fx[name][b])
+            d = (got[:, MF.K_ROWS].float().cpu() - ref).abs()
+            assert (d <= ref.abs() * 2 ** -8 + 1e-5 * ref.abs().max()).all(), name
 
 
 def test_stack_matches_reference_blocks(dev):
