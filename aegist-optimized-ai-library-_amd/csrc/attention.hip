@@ -21,6 +21,8 @@
 #include "common.h"
 
 #include <algorithm>
+#include <mutex>
+#include <string>
 
 using namespace aegist;
 
@@ -867,6 +869,53 @@ int aegist_attention_decode(const void* qg, const void* k_new, const void* v_new
                                                           pos + 1, cap, scale, workspace, core, st, ctr);
     }
     return fail(AEGIST_ERR_DTYPE, "attention_decode: dtypes must be AEGIST_F32 or AEGIST_BF16");
+}
+
+// ---------------------------------------------------------------------------------------------
+// attention_decode without a workspace argument and without allocating: its split-K partials,
+// statistics, normed queries and merge counters live in a file-scope device array (one copy per
+// GPU, held until the process ends). Host code never passes the array's name to a kernel: the
+// array's device address is looked up once per device with hipGetSymbolAddress and kept.
+constexpr size_t kNoAllocScratchBytes = (size_t)32 << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[64] = {};  // per device, filled on the first call on that device
+
+static int scratch_address(void** out) {
+    int dev = 0;
+    AEG_HIP(hipGetDevice(&dev));
+    if (dev < 0 || dev >= 64) return fail(AEGIST_ERR_SHAPE, "attention_decode_noalloc: device index beyond 63");
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        AEG_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return 0;
+}
+
+int aegist_attention_decode_noalloc(const void* qg, const void* k_new, const void* v_new, int in_dtype,
+                                    const uint16_t* q_norm_w, const uint16_t* k_norm_w, uint16_t* kc, uint16_t* vc,
+                                    void* out, int out_dtype, int B, int H, int KV, int HDv, int RD, int pos, int cap,
+                                    float eps, float theta, void* stream) {
+    AEG_REQUIRE(B >= 0 && H > 0 && KV > 0 && H % KV == 0 && H / KV <= 8 && pos >= 0,
+                "attention_decode_noalloc: need H % KV == 0, H/KV <= 8, pos >= 0");
+    if (B == 0) return 0;
+    const size_t need = decode_workspace_bytes(B, H, KV, pos + 1, true);
+    if (need > kNoAllocScratchBytes)
+        return fail(AEGIST_ERR_WORKSPACE, "attention_decode_noalloc: needs " + std::to_string(need) +
+                                              " bytes of scratch, more than its fixed " +
+                                              std::to_string(kNoAllocScratchBytes) +
+                                              "; use aegist_attention_decode with a workspace");
+    void* ws = nullptr;
+    int rc = scratch_address(&ws);
+    if (rc) return rc;
+    // the merge counters are zeroed by the prep kernel of every call, so the scratch needs no
+    // clearing between calls
+    return aegist_attention_decode(qg, k_new, v_new, in_dtype, q_norm_w, k_norm_w, kc, vc, out, out_dtype, B, H, KV,
+                                   HDv, RD, pos, cap, eps, theta, ws, kNoAllocScratchBytes, stream);
 }
 
 int aegist_attention_core(const float* q, const uint16_t* kc, const uint16_t* vc, const float* gate, float* out, int B,

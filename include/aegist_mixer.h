@@ -209,6 +209,18 @@ int aegist_attention_decode(const void* qg, const void* k_new, const void* v_new
                             void* out, int out_dtype, int B, int H, int KV, int HD, int RD, int pos, int cap,
                             float eps, float theta, void* workspace, size_t workspace_bytes, void* stream);
 
+/* aegist_attention_decode without a workspace argument, for callers that cannot allocate
+ * (code under HIP graph capture, serving loops that forbid hipMalloc). No counterpart in the
+ * reference. Its scratch is a fixed 32 MiB device array inside the library, one per GPU, held
+ * until the process ends; shapes needing more (aegist_attention_decode_workspace_bytes above
+ * 32 MiB: a batch of thousands of sequences) fail with AEGIST_ERR_WORKSPACE. Allocates nothing and
+ * clears what it needs on the stream. All calls on one GPU share the array: calls that overlap
+ * on one GPU (two streams, two threads) race and must not be issued. */
+int aegist_attention_decode_noalloc(const void* qg, const void* k_new, const void* v_new, int in_dtype,
+                                    const uint16_t* q_norm_w, const uint16_t* k_norm_w, uint16_t* kc, uint16_t* vc,
+                                    void* out, int out_dtype, int B, int H, int KV, int HDv, int RD, int pos, int cap,
+                                    float eps, float theta, void* stream);
+
 /* Attention core only (no prep): q [B, H, T, HD] fp32 already normed and roped, caches
  * [B, KV, cap, HD] bf16 holding rows [0, pos + T), gate [B, T, H*HD] fp32 or NULL (no gate).
  * out [B, T, H, HD] fp32. Causal with offset: query t sees rows [0, pos + t].
