@@ -135,7 +135,7 @@ struct K1Smem {
     // A, then X = (I + A)^-1 in place. Its upper block column 3 (rows 0..47, columns 48..63: zero
     // in A and X) carries the P tiles of the blocked inversion and is cleared afterwards.
     __attribute__((aligned(16))) float As[CH][A_LD];
-    float cum_s[CH], beta_s[CH], g_s[CH];
+    float cum_s[CH], beta_s[CH], g_s[CH], rq_s[CH], rk_s[CH];
     // intra is staged for fragment order in QV's space: q_n has been read into registers by then,
     // and v is written there only after the intra fragments have gone out. 53 KB in all for bf16
     // inputs: three workgroups per CU for the standalone K1 launch.
@@ -160,6 +160,8 @@ __device__ __forceinline__ void chunk_intra_body(const Tin* __restrict__ q, cons
     auto& cum_s = sm.cum_s;
     auto& beta_s = sm.beta_s;
     auto& g_s = sm.g_s;
+    auto& rq_s = sm.rq_s;
+    auto& rk_s = sm.rk_s;
     half_t (*It)[CH + 8] = (half_t (*)[CH + 8])&QV[0][0];
     // P tile of block column cb during the blocked inversion: As rows 16 cb.., columns 48..63
     auto Pt = [&](int cb, int i, int j) -> float& { return As[16 * cb + i][48 + j]; };
@@ -210,22 +212,34 @@ __device__ __forceinline__ void chunk_intra_body(const Tin* __restrict__ q, cons
         ssq += __shfl_xor(ssq, 2, WAVE);
         ssk += __shfl_xor(ssk, 1, WAVE);
         ssk += __shfl_xor(ssk, 2, WAVE);
-        const float rq = normalize ? rsqrtf(ssq + eps) : 1.f, sc = normalize ? qscale : 1.f;
+        const float rq = normalize ? rsqrtf(ssq + eps) * qscale : 1.f;
         const float rk = normalize ? rsqrtf(ssk + eps) : 1.f;
+        // the tiles keep the raw rows (exact in fp16 for bf16 inputs; fp32 inputs add a low fp16
+        // part, in Vl for k and in As's space for q, both free until step 3's products are done)
+        half_t (*Ql)[QK_LD] = (half_t (*)[QK_LD])&As[0][0];
 #pragma unroll
         for (int e = 0; e < 32; e += 8) {
-            half8 hq, hk;
+            half8 hq, hk, lq, lk;
 #pragma unroll
             for (int f = 0; f < 8; f++) {
-                hq[f] = (half_t)((xq[e + f] * rq) * sc);
-                hk[f] = (half_t)(xk[e + f] * rk);
+                hq[f] = (half_t)xq[e + f];
+                hk[f] = (half_t)xk[e + f];
+                lq[f] = (half_t)(xq[e + f] - (float)hq[f]);
+                lk[f] = (half_t)(xk[e + f] - (float)hk[f]);
             }
             *(half8*)&QV[row][qq * 32 + e] = hq;
             *(half8*)&Ks[row][qq * 32 + e] = hk;
+            if constexpr (kSplitV) {
+                *(half8*)&Ql[row][qq * 32 + e] = lq;
+                *(half8*)&Vl[row][qq * 32 + e] = lk;
+            }
         }
         if (qq == 0) {
             beta_s[row] = beta_r;
             g_s[row] = g_r;
+            // padding rows (past T) carry zero factors
+            rq_s[row] = valid ? rq : 0.f;
+            rk_s[row] = valid ? rk : 0.f;
         }
     }
     __syncthreads();
@@ -242,8 +256,8 @@ __device__ __forceinline__ void chunk_intra_body(const Tin* __restrict__ q, cons
         cum_s[lane] = x;
         const float last = __shfl(x, CH - 1, WAVE);
         float* dec = (float*)(ws + L.cum) + vu * 3 * CH;
-        dec[lane] = __expf(x);
-        dec[CH + lane] = __expf(last - x);
+        dec[lane] = rq_s[lane] * __expf(x);
+        dec[CH + lane] = rk_s[lane] * __expf(last - x);
         dec[2 * CH + lane] = __expf(last);
     }
     if (writes_qk) {
@@ -267,55 +281,74 @@ __device__ __forceinline__ void chunk_intra_body(const Tin* __restrict__ q, cons
     }
     __syncthreads();
 
-    // ---- 3. k_n k_n^T and q_n k_n^T on MFMA, lower 16 x 16 blocks only: 10 blocks of each, as
-    // 20 jobs of 4 MFMAs, 5 per wave: wave w forms the A blocks of row block w (w + 1 of them) and
-    // the intra blocks of row block 3 - w (4 - w of them), and clears the upper blocks of both
+    // ---- 3. k~ k~^T and q~ k~^T on MFMA over the raw rows (fp32 inputs: hi hi + hi lo + lo hi),
+    // lower 16 x 16 blocks only: 10 blocks of each, 5 per wave: wave w forms the A blocks of row
+    // block w (w + 1 of them) and the intra blocks of row block 3 - w (4 - w of them). All
+    // products first (the low parts of q live in As's space), then A and intra with every row
+    // factor (beta, the norms, the decays) applied in fp32, and the upper blocks cleared.
     {
         const int wv = __builtin_amdgcn_readfirstlane(wave);
-        const int ra = wv, rq = 3 - wv;
-        half8 ak[4], aq[4];
+        const int ra = wv, rb = 3 - wv;
+        half_t (*Ql)[QK_LD] = (half_t (*)[QK_LD])&As[0][0];
+        half8 ak[4], aq[4], akl[4], aql[4];
 #pragma unroll
         for (int ks = 0; ks < 4; ks++) {
             ak[ks] = ld_h8(&Ks[16 * ra + n][32 * ks + 8 * gq]);
-            aq[ks] = ld_h8(&QV[16 * rq + n][32 * ks + 8 * gq]);
+            aq[ks] = ld_h8(&QV[16 * rb + n][32 * ks + 8 * gq]);
+            if constexpr (kSplitV) {
+                akl[ks] = ld_h8(&Vl[16 * ra + n][32 * ks + 8 * gq]);
+                aql[ks] = ld_h8(&Ql[16 * rb + n][32 * ks + 8 * gq]);
+            }
         }
-        float ca[4], ba[4], cq[4];
+        f32x4 accA[4], accI[4];
+#pragma unroll
+        for (int cb = 0; cb < 4; cb++) {
+            accA[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+            accI[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+            if (cb > ra && cb > rb) continue;
+#pragma unroll
+            for (int ks = 0; ks < 4; ks++) {
+                const half8 bh = ld_h8(&Ks[16 * cb + n][32 * ks + 8 * gq]);
+                half8 bl;
+                if constexpr (kSplitV) bl = ld_h8(&Vl[16 * cb + n][32 * ks + 8 * gq]);
+                if (cb <= ra) {
+                    accA[cb] = mfma16(ak[ks], bh, accA[cb]);
+                    if constexpr (kSplitV) {
+                        accA[cb] = mfma16(ak[ks], bl, accA[cb]);
+                        accA[cb] = mfma16(akl[ks], bh, accA[cb]);
+                    }
+                }
+                if (cb <= rb) {
+                    accI[cb] = mfma16(aq[ks], bh, accI[cb]);
+                    if constexpr (kSplitV) {
+                        accI[cb] = mfma16(aq[ks], bl, accI[cb]);
+                        accI[cb] = mfma16(aql[ks], bh, accI[cb]);
+                    }
+                }
+            }
+        }
+        float ca[4], ba[4], cq[4], rqv[4];
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             ca[j] = cum_s[16 * ra + 4 * gq + j];
-            ba[j] = beta_s[16 * ra + 4 * gq + j];
-            cq[j] = cum_s[16 * rq + 4 * gq + j];
+            ba[j] = beta_s[16 * ra + 4 * gq + j] * rk_s[16 * ra + 4 * gq + j];
+            cq[j] = cum_s[16 * rb + 4 * gq + j];
+            rqv[j] = rq_s[16 * rb + 4 * gq + j];
         }
-        __syncthreads();  // every wave holds its q_n rows: It (QV's space) is written next
+        __syncthreads();  // every product is done: As and It (QV's space) are written next
+#pragma unroll
         for (int cb = 0; cb < 4; cb++) {
             const int jj = 16 * cb + n;
-            if (cb > ra) {
+            const float cj = cum_s[jj], rkj = rk_s[jj];
 #pragma unroll
-                for (int j = 0; j < 4; j++) As[16 * ra + 4 * gq + j][jj] = 0.f;
-            } else {
-                f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int ks = 0; ks < 4; ks++) acc = mfma16(ak[ks], ld_h8(&Ks[jj][32 * ks + 8 * gq]), acc);
-                const float cj = cum_s[jj];
-#pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    const int i = 16 * ra + 4 * gq + j;
-                    As[i][jj] = jj < i ? ba[j] * (__expf(ca[j] - cj) * acc[j]) : 0.f;
-                }
+            for (int j = 0; j < 4; j++) {
+                const int i = 16 * ra + 4 * gq + j;
+                As[i][jj] = cb <= ra && jj < i ? ba[j] * rkj * (__expf(ca[j] - cj) * accA[cb][j]) : 0.f;
             }
-            if (cb > rq) {
 #pragma unroll
-                for (int j = 0; j < 4; j++) It[16 * rq + 4 * gq + j][jj] = (half_t)0.f;
-            } else {
-                f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int ks = 0; ks < 4; ks++) acc = mfma16(aq[ks], ld_h8(&Ks[jj][32 * ks + 8 * gq]), acc);
-                const float cj = cum_s[jj];
-#pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    const int i = 16 * rq + 4 * gq + j;
-                    It[i][jj] = (half_t)(jj <= i ? __expf(cq[j] - cj) * acc[j] : 0.f);
-                }
+            for (int j = 0; j < 4; j++) {
+                const int i = 16 * rb + 4 * gq + j;
+                It[i][jj] = (half_t)(cb <= rb && jj <= i ? rqv[j] * rkj * (__expf(cq[j] - cj) * accI[cb][j]) : 0.f);
             }
         }
     }
@@ -404,7 +437,7 @@ __device__ __forceinline__ void chunk_intra_body(const Tin* __restrict__ q, cons
         As[e / 16][48 + e % 16] = 0.f;
     }
 
-    // ---- 5. u = X diag(beta) v and w = X diag(beta e^cum) k_n on MFMA, X as fp16 hi + lo.
+    // ---- 5. u = X diag(beta) v and w = X diag(beta e^cum rk) k~ on MFMA, X as fp16 hi + lo.
     // Wave = column tiles {2 wave, 2 wave + 1} of both, all four 16-row blocks.
     {
         float* u = (float*)(ws + L.u) + vu * CH * D;
@@ -439,7 +472,8 @@ __device__ __forceinline__ void chunk_intra_body(const Tin* __restrict__ q, cons
 #pragma unroll
                 for (int i = 0; i < 8; i++) {
                     const float x = i < 4 ? x0[i] : x1[i - 4];
-                    const float bu = beta_s[k0 + i], xu = x * bu, xw = x * (bu * __expf(cum_s[k0 + i]));
+                    const float bu = beta_s[k0 + i], xu = x * bu;
+                    const float xw = x * (bu * __expf(cum_s[k0 + i]) * rk_s[k0 + i]);
                     half_t hh = (half_t)xu;
                     uh[i] = hh;
                     ul[i] = (half_t)(xu - (float)hh);
