@@ -68,6 +68,15 @@ __device__ __forceinline__ void wave_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// Workgroup barrier that orders LDS traffic only: unlike __syncthreads it does not wait for the
+// wave's outstanding global stores (and loads), so a barrier after a burst of stores costs no
+// memory round trip. Global data passed between waves needs __syncthreads.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // Sum over the block; `red` holds one float per wave. Every thread gets the total.
 __device__ __forceinline__ float block_sum(float v, float* red) {
     int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE, nw = (blockDim.x + WAVE - 1) / WAVE;

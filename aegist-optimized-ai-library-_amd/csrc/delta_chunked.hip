@@ -23,9 +23,11 @@
 //     accumulator registers (fp32) for the whole segment; each chunk it is copied to LDS as
 //     fp16 (transposed, so the B operand is a 16-byte read), then w S and q_n S, intra v_new,
 //     and the rank-64 state update k_n^T v' run on MFMA.
-// Operands are fp16 (11-bit mantissa) rather than bf16: the per-row normalisation and every
-// decay / beta factor are applied in fp32 outside the products, and fp16 keeps the chunked
-// result within 5e-4 of fp64 at T = 8192, where bf16 operands give 4e-3 (over the 1e-3 bar).
+// Operands are fp16 (11-bit mantissa) rather than bf16, and the products that set the output's
+// accuracy carry a low fp16 part (hi hi + hi lo + lo hi, ~22 bits): the Gram products run on the
+// raw q / k rows (exact in fp16 for bf16 inputs) with the norms, beta and every decay applied in
+// fp32 afterwards, and intra v_new is split on both sides. At config-4 data (T = 2048, 32 heads)
+// o is within ~2e-4 of fp64; fp16-only intra v_new gives 6e-4, bf16 operands 4e-3.
 #include "common.h"
 
 
@@ -59,13 +61,13 @@ struct SeqLayout {
 };
 
 // Workspace of one segment. Per (b, hv, chunk): u fp32 [64][128] stored in K2's accumulator
-// fragment order (see u_frag), w fp16 [64][128], intra fp16 [64][64], and the decay factors
+// fragment order (see u_frag), w fp16 [64][128], intra fp16 hi and lo [64][64] each, and the decay factors
 // dec fp32 [3][64] = (e^{cum_i}, e^{cum_last - cum_i}, e^{cum_last}). Per (b, kh, chunk):
 // qn fp16 [64][128], knT fp16 [128][64]. w, intra, qn and knT are stored in MFMA A-operand
 // fragment order (afrag_coords).
 // Plus the carried state [B, HV, 128, 128] fp32 when the caller passes none.
 struct WsLayout {
-    size_t u, w, intra, cum, qn, knt, state, total;
+    size_t u, w, intra, intra_lo, cum, qn, knt, state, total;
 };
 
 __host__ __device__ inline size_t al256(size_t x) { return (x + 255) / 256 * 256; }
@@ -77,6 +79,7 @@ __host__ __device__ inline WsLayout ws_layout(int B, int HK, int HV, int nch) {
     L.u = off; off += al256(units_v * CH * D * 4);
     L.w = off; off += al256(units_v * CH * D * 2);
     L.intra = off; off += al256(units_v * CH * CH * 2);
+    L.intra_lo = off; off += al256(units_v * CH * CH * 2);
     L.cum = off; off += al256(units_v * 3 * CH * 4);
     L.qn = off; off += al256(units_k * CH * D * 2);
     L.knt = off; off += al256(units_k * CH * D * 2);
@@ -141,8 +144,10 @@ struct K1Smem {
     // inputs: three workgroups per CU for the standalone K1 launch.
 };
 
-// step 5 reuses QV and Ks for the X fragments (hi + lo: 16 KB each) and As for the w staging tile
+// step 5 reuses QV and Ks for the X fragments (hi + lo: 16 KB each) and As for the w staging tile;
+// intra is staged in fp32 (row pitch CH + 4) in QV's space
 static_assert(sizeof(half_t) * CH * QK_LD >= 2 * CH * CH * sizeof(half_t), "X fragments exceed the q / k tile");
+static_assert(sizeof(half_t) * CH * QK_LD >= CH * (CH + 4) * sizeof(float), "intra staging exceeds the q tile");
 static_assert(sizeof(float) * CH * A_LD >= sizeof(half_t) * CH * QK_LD, "w staging exceeds As");
 
 template <typename Tin>
@@ -162,7 +167,7 @@ __device__ __forceinline__ void chunk_intra_body(const Tin* __restrict__ q, cons
     auto& g_s = sm.g_s;
     auto& rq_s = sm.rq_s;
     auto& rk_s = sm.rk_s;
-    half_t (*It)[CH + 8] = (half_t (*)[CH + 8])&QV[0][0];
+    float (*It)[CH + 4] = (float (*)[CH + 4])&QV[0][0];
     // P tile of block column cb during the blocked inversion: As rows 16 cb.., columns 48..63
     auto Pt = [&](int cb, int i, int j) -> float& { return As[16 * cb + i][48 + j]; };
 
@@ -242,7 +247,7 @@ __device__ __forceinline__ void chunk_intra_body(const Tin* __restrict__ q, cons
             rk_s[row] = valid ? rk : 0.f;
         }
     }
-    __syncthreads();
+    lds_barrier();
 
     // ---- 2. cum = inclusive prefix sum of g (wave 0) and the decay factors K2 needs;
     // q_n rows and k_n^T for K2 (once per QK head)
@@ -279,7 +284,7 @@ __device__ __forceinline__ void chunk_intra_body(const Tin* __restrict__ q, cons
             knt[f] = v;
         }
     }
-    __syncthreads();
+    lds_barrier();
 
     // ---- 3. k~ k~^T and q~ k~^T on MFMA over the raw rows (fp32 inputs: hi hi + hi lo + lo hi),
     // lower 16 x 16 blocks only: 10 blocks of each, 5 per wave: wave w forms the A blocks of row
@@ -335,7 +340,7 @@ __device__ __forceinline__ void chunk_intra_body(const Tin* __restrict__ q, cons
             cq[j] = cum_s[16 * rb + 4 * gq + j];
             rqv[j] = rq_s[16 * rb + 4 * gq + j];
         }
-        __syncthreads();  // every product is done: As and It (QV's space) are written next
+        lds_barrier();  // every product is done: As and It (QV's space) are written next
 #pragma unroll
         for (int cb = 0; cb < 4; cb++) {
             const int jj = 16 * cb + n;
@@ -348,22 +353,33 @@ __device__ __forceinline__ void chunk_intra_body(const Tin* __restrict__ q, cons
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 const int i = 16 * rb + 4 * gq + j;
-                It[i][jj] = (half_t)(cb <= rb && jj <= i ? rqv[j] * rkj * (__expf(cq[j] - cj) * accI[cb][j]) : 0.f);
+                It[i][jj] = cb <= rb && jj <= i ? rqv[j] * rkj * (__expf(cq[j] - cj) * accI[cb][j]) : 0.f;
             }
         }
     }
-    __syncthreads();
-    {   // intra (A of intra v_new: 64 x 64) in fragment order
+    lds_barrier();
+    {   // intra (A of intra v_new: 64 x 64) in fragment order, as fp16 hi + lo (~22 bits: the
+        // intra v_new product carries most of the output's rounding error otherwise)
         half8* intra = (half8*)((half_t*)(ws + L.intra) + vu * CH * CH);
+        half8* intra_lo = (half8*)((half_t*)(ws + L.intra_lo) + vu * CH * CH);
 #pragma unroll
         for (int it = 0; it < 2; it++) {
             const int f = tid + 256 * it;
             int r, c0;
             afrag_coords(f, 2, r, c0);
-            intra[f] = ld_h8(&It[r][c0]);
+            const f32x4 x0 = *(const f32x4*)&It[r][c0], x1 = *(const f32x4*)&It[r][c0 + 4];
+            half8 hi, lo;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const float x = i < 4 ? x0[i] : x1[i - 4];
+                hi[i] = (half_t)x;
+                lo[i] = (half_t)(x - (float)hi[i]);
+            }
+            intra[f] = hi;
+            intra_lo[f] = lo;
         }
     }
-    __syncthreads();  // It (QV's space) has gone out; v is written there next
+    lds_barrier();  // It (QV's space) has gone out; v is written there next
 
     // ---- 4. v (fp16 hi / lo) into the q tile's space; X = (I + A)^-1, blocked by 16
 #pragma unroll
@@ -392,13 +408,13 @@ __device__ __forceinline__ void chunk_intra_body(const Tin* __restrict__ q, cons
                 s -= __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acol[i]), kk)) * x[kk];
             x[i] = s;
         }
-        __syncthreads();  // every wave has read its A block column before X overwrites it
+        lds_barrier();  // every wave has read its A block column before X overwrites it
         if (lane < 16) {
 #pragma unroll
             for (int i = 0; i < 16; i++) As[o + i][o + j] = x[i];
         }
     }
-    __syncthreads();
+    lds_barrier();
     // 4b. block row r: wave c < r forms P = sum_{k=c}^{r-1} A_rk X_kc (fp32 MFMA 16x16x4), then
     // X_rc = -X_rr P
     for (int r = 1; r < 4; r++) {
@@ -416,7 +432,7 @@ __device__ __forceinline__ void chunk_intra_body(const Tin* __restrict__ q, cons
 #pragma unroll
             for (int j = 0; j < 4; j++) Pt(cb, 4 * gq + j, n) = P[j];
         }
-        __syncthreads();  // all reads of A_r* done; P visible
+        lds_barrier();  // all reads of A_r* done; P visible
         if (cb < r) {
             f32x4 X = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -428,7 +444,7 @@ __device__ __forceinline__ void chunk_intra_body(const Tin* __restrict__ q, cons
 #pragma unroll
             for (int j = 0; j < 4; j++) As[16 * r + 4 * gq + j][16 * cb + n] = -X[j];
         }
-        __syncthreads();
+        lds_barrier();
     }
     // clear the P tiles: X is zero above its diagonal blocks (read after step 5's barrier)
 #pragma unroll
@@ -456,7 +472,7 @@ __device__ __forceinline__ void chunk_intra_body(const Tin* __restrict__ q, cons
                     kb[t][ks][i] = Ks[rr][col];
                 }
         }
-        __syncthreads();  // every wave holds its v / k_n operands: QV and Ks take the X fragments
+        lds_barrier();  // every wave holds its v / k_n operands: QV and Ks take the X fragments
         // X diag(beta) and X diag(beta e^cum), each as fp16 hi + lo (hi + lo carries ~22 bits),
         // converted once per workgroup into A-fragment order (afrag_coords, K = 64): thread =
         // (row r, 16 consecutive k); QV holds the u factors, Ks the w factors
@@ -489,7 +505,7 @@ __device__ __forceinline__ void chunk_intra_body(const Tin* __restrict__ q, cons
                 XW[512 + f] = wl;
             }
         }
-        __syncthreads();
+        lds_barrier();
         // w staging for fragment order, in As's space (X has been read)
         half_t (*Wst)[QK_LD] = (half_t (*)[QK_LD])&As[0][0];
 #pragma unroll
@@ -520,7 +536,7 @@ __device__ __forceinline__ void chunk_intra_body(const Tin* __restrict__ q, cons
                 for (int j = 0; j < 4; j++) Wst[16 * rb + 4 * gq + j][col] = (half_t)aw[j];
             }
         }
-        __syncthreads();
+        lds_barrier();
         // w (A of w S: 64 x 128) in fragment order
         half8* wf = (half8*)wout;
 #pragma unroll
@@ -553,7 +569,8 @@ struct K2Smem {
     // double-buffered by chunk parity: a wave cannot pass the next chunk's first barrier before
     // every wave has finished reading this chunk's tiles, so no end-of-chunk barrier is needed
     __attribute__((aligned(16))) half_t SsT[2][16 * NCT][D + 8];   // S^T (fp16): [column][dk]
-    __attribute__((aligned(16))) half_t VnT[2][16 * NCT][CH + 8];  // v_new^T (fp16)
+    __attribute__((aligned(16))) half_t VnT[2][16 * NCT][CH + 8];  // v_new^T (fp16 hi)
+    __attribute__((aligned(16))) half_t VlT[2][16 * NCT][CH + 8];  // v_new^T (fp16 lo)
     __attribute__((aligned(16))) half_t VdT[2][16 * NCT][CH + 8];  // (e^{cum_last-cum} v_new)^T
     __attribute__((aligned(16))) float Ot[4][16][16 * NCT + 4];  // output staging per wave
 };
@@ -565,6 +582,7 @@ __device__ __forceinline__ void chunk_state_body(const unsigned char* __restrict
                                                  K2Smem<NCT>& sm, int Lb) {
     auto& SsT = sm.SsT;
     auto& VnT = sm.VnT;
+    auto& VlT = sm.VlT;
     auto& VdT = sm.VdT;
     auto& Ot = sm.Ot;
 
@@ -594,7 +612,7 @@ __device__ __forceinline__ void chunk_state_body(const unsigned char* __restrict
     // operands of one chunk that do not depend on S; each part is refilled with the next chunk's
     // values while the current chunk computes (see step), hiding the L2 / HBM latency
     struct Ops {
-        half8 wa[4], qa[4], ia[2], ka[2][2];
+        half8 wa[4], qa[4], ia[2], il[2], ka[2][2];
         f32x4 uu[NCT], ecum, edec;  // u fragment; e^{cum_i}, e^{cum_last - cum_i} for this lane's rows
         float gamma;              // e^{cum_last}
     };
@@ -605,6 +623,7 @@ __device__ __forceinline__ void chunk_state_body(const unsigned char* __restrict
         const half_t* Qc = (const half_t*)(ws + L.qn) + ku * CH * D;
         const float* Uc = (const float*)(ws + L.u) + vu * CH * D;
         const half_t* Ic = (const half_t*)(ws + L.intra) + vu * CH * CH;
+        const half_t* Ilc = (const half_t*)(ws + L.intra_lo) + vu * CH * CH;
         const half_t* KTc = (const half_t*)(ws + L.knt) + ku * CH * D;
         const float* dec = (const float*)(ws + L.cum) + vu * 3 * CH;
         // fragment-order operands (written so by K1): one contiguous 1 KB load per fragment.
@@ -624,7 +643,10 @@ __device__ __forceinline__ void chunk_state_body(const unsigned char* __restrict
         }
         if (part < 0 || part == 2) {
 #pragma unroll
-            for (int ks = 0; ks < 2; ks++) o.ia[ks] = ld_h8(Ic + ((2 * wave + ks) * 64 + lane) * 8);
+            for (int ks = 0; ks < 2; ks++) {
+                o.ia[ks] = ld_h8(Ic + ((2 * wave + ks) * 64 + lane) * 8);
+                o.il[ks] = ld_h8(Ilc + ((2 * wave + ks) * 64 + lane) * 8);
+            }
             o.ecum = *(const f32x4*)(dec + 16 * wave + 4 * gq);
         }
         if (part < 0 || part == 3) {
@@ -650,6 +672,7 @@ __device__ __forceinline__ void chunk_state_body(const unsigned char* __restrict
         const half8* wa = cur.wa;
         const half8* qa = cur.qa;
         const half8* ia = cur.ia;
+        const half8* il = cur.il;
         const f32x4* uu = cur.uu;
 
         const int pb = c & 1;
@@ -687,14 +710,16 @@ __device__ __forceinline__ void chunk_state_body(const unsigned char* __restrict
         // (3) v_new = u - w S; decayed copy for the state update
 #pragma unroll
         for (int ct = 0; ct < NCT; ct++) {
-            half4 hn, hd;
+            half4 hn, ln, hd;
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 const float vn = uu[ct][j] - WS[ct][j];
                 hn[j] = (half_t)vn;
+                ln[j] = (half_t)(vn - (float)hn[j]);
                 hd[j] = (half_t)(cur.edec[j] * vn);
             }
             *(half4*)&VnT[pb][16 * ct + n][16 * wave + 4 * gq] = hn;
+            *(half4*)&VlT[pb][16 * ct + n][16 * wave + 4 * gq] = ln;
             *(half4*)&VdT[pb][16 * ct + n][16 * wave + 4 * gq] = hd;
         }
         issue(1);
@@ -707,7 +732,13 @@ __device__ __forceinline__ void chunk_state_body(const unsigned char* __restrict
         for (int ct = 0; ct < NCT; ct++) {
             ov[ct] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int ks = 0; ks < 2; ks++) ov[ct] = mfma16(ia[ks], ld_h8(&VnT[pb][16 * ct + n][32 * ks + 8 * gq]), ov[ct]);
+            for (int ks = 0; ks < 2; ks++) {
+                // intra v_new as hi hi + hi lo + lo hi
+                const half8 vh = ld_h8(&VnT[pb][16 * ct + n][32 * ks + 8 * gq]);
+                ov[ct] = mfma16(ia[ks], vh, ov[ct]);
+                ov[ct] = mfma16(ia[ks], ld_h8(&VlT[pb][16 * ct + n][32 * ks + 8 * gq]), ov[ct]);
+                ov[ct] = mfma16(il[ks], vh, ov[ct]);
+            }
         }
         {
             const float gamma = cur.gamma;

@@ -31,6 +31,14 @@ def rel_err(x, ref) -> float:
     return (x - ref).abs().max().item() / (den if den > 0 else 1.0)
 
 
+def rms_err(x, ref) -> float:
+    """||x - ref||_2 / ||ref||_2: blind to a few isolated rounding flips, sensitive to anything systematic."""
+    x = x.detach().double().cpu()
+    ref = ref.detach().double().cpu()
+    den = ref.norm().item()
+    return (x - ref).norm().item() / (den if den > 0 else 1.0)
+
+
 @pytest.fixture(scope="session")
 def dev():
     import torch

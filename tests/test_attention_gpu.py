@@ -120,3 +120,43 @@ def test_engine_attention_pipeline(dev):
         outs.append(ops.engine_attention_gated(qn, kc, vc, qgd, a))
     torch.cuda.synchronize()
     assert rel_err(torch.cat(outs, 0), ref) < ATTN_TOL
+
+
+@pytest.mark.slow
+@pytest.mark.parametrize("B,L", [(8, 32768), (32, 32768), (8, 131072), (32, 131072), (64, 32768)])
+def test_attention_decode_config3_points(dev, B, L):
+    """Config 3's large points at full size (16 query / 2 KV heads, head_dim 256, bf16 caches
+    ~N(0, 1) filled on the device): two of the B sequences against the CPU oracle, and the same two
+    run alone (B = 1, so a different split of the context and a different merge) against the batch
+    result. The B = 64 point is the north star's batch-64 decode."""
+    print(f"attention_decode config3 B={B} L={L}", flush=True)
+    H, KV, cap = 16, 2, L + 1
+    kc = ops.fill_normal(torch.empty(B, KV, cap, HD, dtype=torch.bfloat16, device=dev), 1000 + B)
+    vc = ops.fill_normal(torch.empty(B, KV, cap, HD, dtype=torch.bfloat16, device=dev), 2000 + B)
+    g_ = _gen(B + L)
+    qg = torch.randn(B, H, 2 * HD, generator=g_).to(torch.bfloat16)
+    kn = torch.randn(B, KV, HD, generator=g_).to(torch.bfloat16)
+    vn = torch.randn(B, KV, HD, generator=g_).to(torch.bfloat16)
+    qw = (torch.randn(HD, generator=g_) * 0.1).to(torch.bfloat16)
+    kw = (torch.randn(HD, generator=g_) * 0.1).to(torch.bfloat16)
+    rows = (0, B - 1)
+    kc_rows = [kc[b:b + 1].cpu() for b in rows]
+    vc_rows = [vc[b:b + 1].cpu() for b in rows]
+    out = ops.attention_decode(qg.to(dev), kn.to(dev), vn.to(dev), qw.to(dev), kw.to(dev), kc, vc, L, RD, THETA)
+    torch.cuda.synchronize()
+    for i, b in enumerate(rows):
+        ref = R.attention_decode(qg[b:b + 1].float(), kn[b:b + 1].float(), vn[b:b + 1].float(), qw.float(), kw.float(),
+                                 kc_rows[i], vc_rows[i], L, RD, THETA)
+        err = rel_err(out[b:b + 1], ref)
+        print(f"  row {b}: rel err vs oracle {err:.2e}", flush=True)
+        assert err < ATTN_TOL
+        # the same sequence alone: its own split of the context and merge
+        kc1, vc1 = kc_rows[i].to(dev), vc_rows[i].to(dev)
+        alone = ops.attention_decode(qg[b:b + 1].to(dev), kn[b:b + 1].to(dev), vn[b:b + 1].to(dev), qw.to(dev),
+                                     kw.to(dev), kc1, vc1, L, RD, THETA)
+        torch.cuda.synchronize()
+        err1 = rel_err(alone, out[b:b + 1])
+        print(f"  row {b}: batch vs alone {err1:.2e}", flush=True)
+        assert err1 < 1e-5
+    del kc, vc
+    torch.cuda.empty_cache()

@@ -1,0 +1,230 @@
+"""Config 4 at its own workload: d_model 2048, 16 QK / 32 V DeltaNet heads, 16 / 2 attention heads
+(head_dim 256), batch 16, a 2048-token prefill then decode steps (the
+reference loop is hybrid.py:812-843 with the MoE as identity).
+
+- The DeltaNet core (chunked prefill over the layer's own conv/gate outputs) against the fp64
+  recurrence: 1e-3 on o and on the final state.
+- One layer of each kind at full shape against the CPU oracle on two of the 16 sequences, over
+  prefill and two decode steps. Both sides round the out-projection input to bf16 as the
+  reference does (hybrid.py:361, 310), so one rounding that lands on the other side of a bf16
+  boundary moves an output by ulp(u_j) * |W_out[i, j]|; at config 4's gated-norm outputs
+  (|u| up to ~6, ulp 2^-5) that single flip is ~2.5e-3 of max|y|, whatever the core's accuracy
+  (an fp64-exact core against an fp64 reference flips ~1% of the 8.4M inputs). The bars are
+  therefore: rms error (||dy|| / ||y||, blind to isolated flips) below 1e-3, and max error below
+  1e-3 plus two such flips at the largest input, computed from the oracle's own tensors.
+- The 40-layer stack at B = 16 against properties that fix its semantics without a 40-layer CPU
+  run: a crop back to a snapshot and the same tokens fed again reproduce the outputs bit for
+  bit; every sequence of the batch equals its own batch-1 run and the decode steps equal the
+  same tokens inside one longer prefill, to an rms bar of twice what an ulp-sized change of the
+  input does to the same 40-layer run (the batch-1 and longer runs pick other GEMM tilings and
+  another core for the decode tokens, so their fp32 sums round differently; through 40 residual
+  layers with bf16 projection inputs any such difference grows to the same level)."""
+import pytest
+import torch
+
+import math
+
+from conftest import rel_err, rms_err
+from oracle import mixer_ref as R
+
+from aegist_mixer import ops
+
+pytestmark = pytest.mark.gpu
+
+CFG = dict(d_model=2048, hk=16, hv=32, n_heads=16, n_kv=2, head_dim=256, rotary_dim=64, rope_theta=1e7, eps=1e-6)
+B, T = 16, 2048
+C = 2 * 16 * 128 + 32 * 128
+
+
+def cpu_layer(kind, seed):
+    """Weights as in BASELINE config 4 (bf16 projections ~N(0, 0.02)), with non-trivial norm,
+    gate and decay parameters so every term of the layer is exercised."""
+    g_ = torch.Generator().manual_seed(seed)
+
+    def w(*shape, std=0.02, mean=0.0):
+        return (mean + std * torch.randn(*shape, generator=g_)).to(torch.bfloat16)
+    W = {"norm1": w(2048, std=0.1)}
+    if kind == "delta":
+        W.update(w_qkv=w(C, 2048), w_z=w(4096, 2048), w_b=w(32, 2048), w_a=w(32, 2048), conv_w=w(C, 4, std=0.05),
+                 a_log=w(32, std=0.5), dt_bias=w(32, std=0.5, mean=1.0), gnorm_w=w(128, std=0.1, mean=1.0),
+                 w_out=w(2048, 4096))
+    else:
+        W.update(w_q=w(8192, 2048), w_k=w(512, 2048), w_v=w(512, 2048), w_o=w(2048, 4096), q_norm=w(256, std=0.1),
+                 k_norm=w(256, std=0.1))
+    return W
+
+
+def oracle_cache(kinds, cap):
+    nd, na = kinds.count("delta"), kinds.count("attn")
+    return {"length": 0, "conv": [torch.zeros(1, C, 3) for _ in range(nd)],
+            "state": [torch.zeros(1, 32, 128, 128) for _ in range(nd)],
+            "k": [torch.zeros(1, 2, cap, 256, dtype=torch.bfloat16) for _ in range(na)],
+            "v": [torch.zeros(1, 2, cap, 256, dtype=torch.bfloat16) for _ in range(na)]}
+
+
+def test_config4_delta_core(dev):
+    """The north-star quantity at config-4 data: q, k, v, g, beta from the DeltaNet layer's own
+    projections, conv and gates on one 2048-token sequence; GPU chunked core vs fp64 recurrence."""
+    import torch.nn.functional as F
+    W = cpu_layer("delta", seed=40)
+    g_ = torch.Generator().manual_seed(7)
+    x = torch.randn(1, T, 2048, generator=g_)
+    h = R.znorm(x, W["norm1"].float(), 1e-6)
+
+    def lin(t, w):
+        return t.to(torch.bfloat16).float() @ w.float().t()
+    qkv, b, a = lin(h, W["w_qkv"]), lin(h, W["w_b"]), lin(h, W["w_a"])
+    y, _ = R.conv_silu(qkv, W["conv_w"].float(), None)
+    q, k, v = R.delta_prep(y, 16, 32, 128, 128)
+    beta = b.sigmoid().transpose(1, 2)
+    g = (-W["a_log"].float().exp() * F.softplus(a + W["dt_bias"].float())).transpose(1, 2)
+    o_ref, S_ref = R.delta_rule_recurrent(q.double(), k.double(), v.double(), g.double(), beta.double(), None)
+    yd = y.contiguous().to(dev)
+    qr = yd[..., :2048].reshape(1, T, 16, 128).transpose(1, 2)
+    kr = yd[..., 2048:4096].reshape(1, T, 16, 128).transpose(1, 2)
+    vr = yd[..., 4096:].reshape(1, T, 32, 128).transpose(1, 2)
+    print("config4 DeltaNet core: chunked prefill of 2048 tokens, 32 heads", flush=True)
+    o, S = ops.delta_rule_chunked(qr, kr, vr, g.to(dev), beta.to(dev), None, normalize=True, qscale=128 ** -0.5)
+    torch.cuda.synchronize()
+    eo, es = rel_err(o, o_ref), rel_err(S, S_ref)
+    print(f"  o {eo:.2e}  S {es:.2e}", flush=True)
+    assert eo < 1e-3 and es < 1e-3, (eo, es)
+
+
+def bf16_ulp(x: float) -> float:
+    return 2.0 ** (math.floor(math.log2(x)) - 7)
+
+
+@pytest.mark.parametrize("kind", ["delta", "attn"])
+def test_config4_layer_matches_oracle(dev, kind, monkeypatch):
+    steps, rows = 2, (0, 11)
+    W = cpu_layer(kind, seed=40 if kind == "delta" else 41)
+    w_out = W["w_out" if kind == "delta" else "w_o"]
+    stack = ops.HybridStack(CFG, [kind], [{k: v.to(dev) for k, v in W.items()}], max_batch=B, max_tokens=B * T,
+                            max_context=T + steps)
+    g_ = torch.Generator().manual_seed(7)
+    feeds = [torch.randn(B, T, 2048, generator=g_)] + [torch.randn(B, 1, 2048, generator=g_) for _ in range(steps)]
+    outs = []
+    for i, x in enumerate(feeds):
+        print(f"config4 {kind} layer: feed {i} ({x.shape[1]} tokens, B={B})", flush=True)
+        xd = x.to(dev)
+        stack.forward(xd)
+        torch.cuda.synchronize()
+        outs.append((xd - x.to(dev)).cpu())
+    stack.close()
+
+    # the largest out-projection input the oracle sees, for the rounding-flip allowance
+    seen = {}
+    lin = R._lin
+
+    def spy(x, w, round_in):
+        if w is w_out:
+            seen["u"] = x.abs().max().item()
+        return lin(x, w, round_in)
+    monkeypatch.setattr(R, "_lin", spy)
+    wmax = w_out.float().abs().max().item()
+    for b in rows:
+        cache = oracle_cache([kind], T + steps)
+        for i, x in enumerate(feeds):
+            xb = x[b:b + 1]
+            ref = R.hybrid_stack_forward(xb.clone(), [W], [kind], cache, CFG) - xb
+            flips = 2 * bf16_ulp(seen["u"]) * wmax / ref.abs().max().item()
+            em, er = rel_err(outs[i][b:b + 1], ref), rms_err(outs[i][b:b + 1], ref)
+            print(f"  row {b} feed {i}: max {em:.2e} (bar {1e-3 + flips:.2e})  rms {er:.2e}", flush=True)
+            assert er < 1e-3 and em < 1e-3 + flips, (kind, b, i, em, er)
+
+
+def gpu_layers(kinds, dev):
+    seed = [300]
+
+    def w(*shape, std=0.02, mean=0.0):
+        seed[0] += 1
+        return ops.fill_normal(torch.empty(*shape, device=dev, dtype=torch.bfloat16), seed[0], mean, std)
+    layers = []
+    for kind in kinds:
+        W = {"norm1": w(2048, std=0.1)}
+        if kind == "delta":
+            W.update(w_qkv=w(C, 2048), w_z=w(4096, 2048), w_b=w(32, 2048), w_a=w(32, 2048), conv_w=w(C, 4, std=0.05),
+                     a_log=w(32, std=0.5), dt_bias=w(32, std=0.5, mean=1.0), gnorm_w=w(128, std=0.1, mean=1.0),
+                     w_out=w(2048, 4096))
+        else:
+            W.update(w_q=w(8192, 2048), w_k=w(512, 2048), w_v=w(512, 2048), w_o=w(2048, 4096), q_norm=w(256, std=0.1),
+                     k_norm=w(256, std=0.1))
+        layers.append(W)
+    return layers
+
+
+def test_config4_stack_properties(dev):
+    kinds = (["delta"] * 3 + ["attn"]) * 10
+    steps = 4
+    layers = gpu_layers(kinds, dev)
+    g_ = torch.Generator().manual_seed(9)
+    x0 = torch.randn(B, T, 2048, generator=g_).to(dev) * 0.5
+    xs = [torch.randn(B, 1, 2048, generator=g_).to(dev) * 0.5 for _ in range(steps)]
+
+    print("config4 stack: B=16 prefill + decode", flush=True)
+    big = ops.HybridStack(CFG, kinds, layers, max_batch=B, max_tokens=B * (T + steps), max_context=T + steps)
+    y0 = x0.clone()
+    big.forward(y0)
+    big.snapshot()
+    ys = []
+    for x in xs:
+        y = x.clone()
+        big.forward(y)
+        ys.append(y)
+    torch.cuda.synchronize()
+    assert torch.isfinite(y0).all() and all(torch.isfinite(y).all() for y in ys)
+
+    # crop back to the snapshot and feed the same tokens: bit-exact
+    print("config4 stack: crop and refeed", flush=True)
+    assert big.crop(T) == T
+    for x, y in zip(xs, ys):
+        y2 = x.clone()
+        big.forward(y2)
+        assert torch.equal(y2, y)
+    big.close()
+
+    # each sequence equals its own batch-1 run (rows 0 and 9)
+    errs = []
+    one = ops.HybridStack(CFG, kinds, layers, max_batch=1, max_tokens=T + steps, max_context=T + steps)
+    for b in (0, 9):
+        print(f"config4 stack: batch-1 run of row {b}", flush=True)
+        one.reset()
+        z0 = x0[b:b + 1].clone()
+        one.forward(z0)
+        pairs = [(z0 - x0[b:b + 1], y0[b:b + 1] - x0[b:b + 1])]
+        for s, x in enumerate(xs):
+            z = x[b:b + 1].clone()
+            one.forward(z)
+            pairs.append((z - x[b:b + 1], ys[s][b:b + 1] - x[b:b + 1]))
+        for i, (u, r) in enumerate(pairs):
+            errs.append(("batch1", b, i, rms_err(u, r), rel_err(u, r)))
+    # the floor: the same batch-1 run with the input moved by ~1 fp32 ulp (relative 2^-24 noise),
+    # i.e. the smallest change any reordering of an fp32 sum makes
+    print("config4 stack: batch-1 run of row 0 with an ulp-sized input change", flush=True)
+    one.reset()
+    gp = torch.Generator(device=dev).manual_seed(11)
+    zp = x0[:1] * (1 + 2.0 ** -24 * torch.randn(x0[:1].shape, device=dev, generator=gp))
+    z0 = zp.clone()
+    one.forward(z0)
+    floor = [rms_err(z0 - zp, y0[:1] - x0[:1])]
+    for s, x in enumerate(xs):
+        z = x[:1].clone()
+        one.forward(z)
+        floor.append(rms_err(z - x[:1], ys[s][:1] - x[:1]))
+    # the decode steps equal the same tokens inside one prefill of T + steps (row 0)
+    print("config4 stack: one prefill of T + steps tokens", flush=True)
+    one.reset()
+    zl = torch.cat([x0[:1]] + [x[:1] for x in xs], 1).clone()
+    one.forward(zl)
+    torch.cuda.synchronize()
+    for s, x in enumerate(xs):
+        u, r = zl[:, T + s:T + s + 1] - x[:1], ys[s][:1] - x[:1]
+        errs.append(("prefill", 0, s, rms_err(u, r), rel_err(u, r)))
+    one.close()
+    for e in errs:
+        print("  %s row %d feed %d: rms %.2e max %.2e" % e, flush=True)
+    print("  ulp-perturbed run: rms " + " ".join("%.2e" % f for f in floor), flush=True)
+    bar = max(1e-3, 2 * max(floor))
+    for name, b, i, er, em in errs:
+        assert er < bar, (name, b, i, er, em, bar)
