@@ -20,6 +20,7 @@
 // engine kernels attn_prep / attention_gated (hybrid.cu:86-173).
 #include "common.h"
 
+#include <cstdlib>
 #include <algorithm>
 #include <mutex>
 #include <string>
@@ -50,10 +51,17 @@ struct DecodeSplit {
 #ifndef ATTN_SPLIT_TARGET
 #define ATTN_SPLIT_TARGET 192  // workgroups per decode launch the split count aims for (measured: 160-192 beat 128 and 224-1024)
 #endif
+int split_target() {
+    static const int t = [] {
+        const char* e = getenv("AEGIST_ATTN_SPLIT_TARGET");
+        return e && atoi(e) > 0 ? atoi(e) : ATTN_SPLIT_TARGET;
+    }();
+    return t;
+}
 DecodeSplit choose_split(int B, int KV, int L) {
     int units = std::max(1, B * KV);
     int max_split = std::min(256, std::max(1, (L + 127) / 128));
-    int ns = std::min(max_split, std::max(1, (ATTN_SPLIT_TARGET + units - 1) / units));
+    int ns = std::min(max_split, std::max(1, (split_target() + units - 1) / units));
     int per = (L + ns - 1) / ns;
     per = (per + 127) / 128 * 128;
     ns = (L + per - 1) / per;

@@ -310,11 +310,14 @@ def bench_moe(torch, ops, dev, reps=3):
         wts = torch.empty(T, K, device=dev)
         need = lib().aegist_moe_workspace_bytes(T, K, D, I, E)
         ws = torch.empty(need, dtype=torch.uint8, device=dev)
+        rneed = lib().aegist_router_topk_workspace_bytes(T, E)
+        rws = torch.empty(max(rneed, 1), dtype=torch.uint8, device=dev)
         uniq = []
 
         def run(li):
             rows, eptr, W = layers[li]
-            call("aegist_router_topk", h.data_ptr(), W.data_ptr(), idx.data_ptr(), wts.data_ptr(), T, D, E, K, stream)
+            call("aegist_router_topk_ws", h.data_ptr(), W.data_ptr(), idx.data_ptr(), wts.data_ptr(), T, D, E, K,
+                 rws.data_ptr(), rneed, stream)
             call("aegist_moe_experts", h.data_ptr(), eptr.data_ptr(), idx.data_ptr(), wts.data_ptr(), x.data_ptr(),
                  T, D, I, E, K, None, None, ws.data_ptr(), need, stream)
         for li in range(NL):
@@ -350,7 +353,7 @@ def bench_qsa(torch, ops, dev, reps=20):
     head count: the released config is not in the reference tree), then attention over the 512
     listed blocks + tail with 16 / 2 heads of 256. Times each kernel of the decode-time path
     (block scores, top-k select, listed attention) with HIP events."""
-    from aegist_mixer._lib import call
+    from aegist_mixer._lib import call, lib
     stream = torch.cuda.current_stream().cuda_stream
     L, RB, top, H, KV, HD, IH = 131072, 4, 512, 16, 2, 256, 16
     nb = L // RB
@@ -365,14 +368,18 @@ def bench_qsa(torch, ops, dev, reps=20):
     vc = ops.fill_normal(torch.empty(KV, L, HD, device=dev, dtype=torch.bfloat16), 75)
     qg = ops.fill_normal(torch.empty(1, H, 2 * HD, device=dev), 76)
     out = torch.empty(1, H, HD, device=dev)
+    sel_need = lib().aegist_idx_select_workspace_bytes(1, top, RB, pos0)
+    sel_ws = torch.empty(max(sel_need, 1), dtype=torch.uint8, device=dev)
+    lst_need = lib().aegist_attention_gated_list_workspace_bytes(1, H, KV, pos0, top, RB)
+    lst_ws = torch.empty(max(lst_need, 1), dtype=torch.uint8, device=dev)
     steps = {
         "scores": lambda: call("aegist_idx_scores", qi.data_ptr(), bk.data_ptr(), sc.data_ptr(), 1, IH, 128, pos0, RB,
                                nb, stream),
-        "select": lambda: call("aegist_idx_select", sc.data_ptr(), blist.data_ptr(), nsel.data_ptr(), 1, top, RB, pos0,
-                               nb, stream),
-        "attention_list": lambda: call("aegist_attention_gated_list", q.data_ptr(), kc.data_ptr(), vc.data_ptr(),
-                                       qg.data_ptr(), out.data_ptr(), 1, H, KV, pos0, L, HD ** -0.5, blist.data_ptr(),
-                                       nsel.data_ptr(), top, RB, stream),
+        "select": lambda: call("aegist_idx_select_ws", sc.data_ptr(), blist.data_ptr(), nsel.data_ptr(), 1, top, RB,
+                               pos0, nb, sel_ws.data_ptr(), sel_need, stream),
+        "attention_list": lambda: call("aegist_attention_gated_list_ws", q.data_ptr(), kc.data_ptr(),
+                                       vc.data_ptr(), qg.data_ptr(), out.data_ptr(), 1, H, KV, pos0, L, HD ** -0.5,
+                                       blist.data_ptr(), nsel.data_ptr(), top, RB, lst_ws.data_ptr(), lst_need, stream),
     }
     res = {"workload": f"QSA sparse decode, L={L}, R={RB}, top={top}, 16 index heads x 128, 16/2 heads x 256",
            "note": "16 index heads is an assumption (the released head count is not in the reference tree)"}
