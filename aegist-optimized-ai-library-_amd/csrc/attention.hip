@@ -128,7 +128,10 @@ __device__ void merge_splits(const float* __restrict__ part, const float* __rest
     // software-pipelined over batches of SB splits: the next batch's loads are in flight while
     // this one accumulates (the partials come from other XCDs: each batch is a full memory
     // latency); batch indices past the last split re-read it and are weighted 0
-    constexpr int SB = 4;
+#ifndef ATTN_MERGE_SB
+#define ATTN_MERGE_SB 4
+#endif
+    constexpr int SB = ATTN_MERGE_SB;
     float4 cur[SB][2], nxt[SB][2];
     auto load_batch = [&](float4 (&v)[SB][2], int s0) {
 #pragma unroll

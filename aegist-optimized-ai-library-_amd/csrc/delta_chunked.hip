@@ -13,10 +13,11 @@
 //  K1 delta_chunk_intra: one workgroup per (sequence, value head, chunk), fully parallel.
 //     Normalises q, k in fp32 and keeps them as fp16 in LDS; k_n k_n^T and q_n k_n^T on
 //     v_mfma_f32_16x16x32_f16 (lower-triangular blocks only); decay and beta applied in fp32 on
-//     the accumulators; the unit-lower-triangular solve runs in fp32 with one thread per
-//     right-hand-side column (256 columns = beta v | beta e^cum k_n), the matrix broadcast
-//     from LDS. Writes u (fp32), w (fp16), intra (fp16), cum, and - once per QK head - q_n
-//     and k_n^T (fp16).
+//     the accumulators; the inverses of the four 16 x 16 diagonal blocks of I + A by forward
+//     substitution, then u and w by blocked forward substitution over the 256 right-hand-side
+//     columns (beta v | beta e^cum k_n), each wave owning 64 columns of every row (no barrier).
+//     Writes u (fp32), w (fp16), intra (fp16 hi + lo), cum, and - once per QK head - q_n and
+//     k_n^T (fp16).
 //  K2 delta_chunk_state: one workgroup per (sequence, value head, 16-column slice of S); the
 //     columns of S are independent, so 8 slices per head run in parallel, the slices of one
 //     head on one XCD (they share its L2 for the chunk operands). S lives in MFMA
@@ -47,6 +48,7 @@ constexpr int QK_LD = D + 8; // fp16 row stride (elements) of the q/k tiles in L
 constexpr int A_LD = 68;     // fp32 row stride of the A matrix in LDS (16-byte aligned rows)
 
 typedef _Float16 half_t;
+typedef short short4v_t __attribute__((ext_vector_type(4)));
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 // raw buffer resource for the output stores: range (bytes) and the gfx9 word 3 (32-bit data,
 // no swizzle); kOutDrop lies past the range, so a store at that offset is discarded
@@ -135,8 +137,8 @@ struct K1Smem {
     __attribute__((aligned(16))) half_t QV[CH][QK_LD];  // q_n tile, then v (fp16 hi)
     __attribute__((aligned(16))) half_t Vl[kSplitV ? CH : 1][QK_LD];
     __attribute__((aligned(16))) half_t Ks[CH][QK_LD];
-    // A, then X = (I + A)^-1 in place. Its upper block column 3 (rows 0..47, columns 48..63: zero
-    // in A and X) carries the P tiles of the blocked inversion and is cleared afterwards.
+    // A (strict lower), with the inverses of the diagonal blocks of I + A written over its
+    // diagonal blocks; the w staging tile afterwards
     __attribute__((aligned(16))) float As[CH][A_LD];
     float cum_s[CH], beta_s[CH], g_s[CH], rq_s[CH], rk_s[CH];
     // intra is staged for fragment order in QV's space: q_n has been read into registers by then,
@@ -144,9 +146,7 @@ struct K1Smem {
     // inputs: three workgroups per CU for the standalone K1 launch.
 };
 
-// step 5 reuses QV and Ks for the X fragments (hi + lo: 16 KB each) and As for the w staging tile;
-// intra is staged in fp32 (row pitch CH + 4) in QV's space
-static_assert(sizeof(half_t) * CH * QK_LD >= 2 * CH * CH * sizeof(half_t), "X fragments exceed the q / k tile");
+// step 5 reuses As for the w staging tile; intra is staged in fp32 (row pitch CH + 4) in QV's space
 static_assert(sizeof(half_t) * CH * QK_LD >= CH * (CH + 4) * sizeof(float), "intra staging exceeds the q tile");
 static_assert(sizeof(float) * CH * A_LD >= sizeof(half_t) * CH * QK_LD, "w staging exceeds As");
 
@@ -168,8 +168,6 @@ __device__ __forceinline__ void chunk_intra_body(const Tin* __restrict__ q, cons
     auto& rq_s = sm.rq_s;
     auto& rk_s = sm.rk_s;
     float (*It)[CH + 4] = (float (*)[CH + 4])&QV[0][0];
-    // P tile of block column cb during the blocked inversion: As rows 16 cb.., columns 48..63
-    auto Pt = [&](int cb, int i, int j) -> float& { return As[16 * cb + i][48 + j]; };
 
     const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE, n = lane % 16, gq = lane / 16;
     const int R = HV / HK, kh = hv / R;
@@ -381,7 +379,7 @@ __device__ __forceinline__ void chunk_intra_body(const Tin* __restrict__ q, cons
     }
     lds_barrier();  // It (QV's space) has gone out; v is written there next
 
-    // ---- 4. v (fp16 hi / lo) into the q tile's space; X = (I + A)^-1, blocked by 16
+    // ---- 4. v (fp16 hi / lo) into the q tile's space; inverses of the diagonal blocks of I + A
 #pragma unroll
     for (int e = 0; e < 32; e += 8) {
         half8 hv8, lv8;
@@ -415,130 +413,128 @@ __device__ __forceinline__ void chunk_intra_body(const Tin* __restrict__ q, cons
         }
     }
     lds_barrier();
-    // 4b. block row r: wave c < r forms P = sum_{k=c}^{r-1} A_rk X_kc (fp32 MFMA 16x16x4), then
-    // X_rc = -X_rr P
-    for (int r = 1; r < 4; r++) {
-        f32x4 P = {0.f, 0.f, 0.f, 0.f};
-        const int cb = wave;
-        if (cb < r) {
-            for (int kb = cb; kb < r; kb++) {
-#pragma unroll
-                for (int s4 = 0; s4 < 4; s4++) {
-                    const float av = As[16 * r + n][16 * kb + 4 * s4 + gq];
-                    const float bv = As[16 * kb + 4 * s4 + gq][16 * cb + n];
-                    P = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, P, 0, 0, 0);
-                }
-            }
-#pragma unroll
-            for (int j = 0; j < 4; j++) Pt(cb, 4 * gq + j, n) = P[j];
-        }
-        lds_barrier();  // all reads of A_r* done; P visible
-        if (cb < r) {
-            f32x4 X = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int s4 = 0; s4 < 4; s4++) {
-                const float av = As[16 * r + n][16 * r + 4 * s4 + gq];
-                const float bv = Pt(cb, 4 * s4 + gq, n);
-                X = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, X, 0, 0, 0);
-            }
-#pragma unroll
-            for (int j = 0; j < 4; j++) As[16 * r + 4 * gq + j][16 * cb + n] = -X[j];
-        }
-        lds_barrier();
-    }
-    // clear the P tiles: X is zero above its diagonal blocks (read after step 5's barrier)
-#pragma unroll
-    for (int it = 0; it < 3; it++) {
-        const int e = tid + 256 * it;
-        As[e / 16][48 + e % 16] = 0.f;
-    }
-
-    // ---- 5. u = X diag(beta) v and w = X diag(beta e^cum rk) k~ on MFMA, X as fp16 hi + lo.
-    // Wave = column tiles {2 wave, 2 wave + 1} of both, all four 16-row blocks.
+    // ---- 5. u = (I + A)^-1 diag(beta) v and w = (I + A)^-1 diag(beta e^cum rk) k~ by blocked
+    // forward substitution over the four 16-row blocks: block row r of U is
+    //   U_r = D_r^-1 (R_r - sum_{k < r} A_rk U_k),   D_r^-1 = (I + A_rr)^-1 (step 4a),
+    // with the 256 right-hand-side columns split over the waves (waves 0, 1: u columns
+    // 64 (w % 2) ..; waves 2, 3: w columns), so a wave owns its columns of U for every row and
+    // needs no barrier. Products on v_mfma_f32_16x16x32_f16 with both sides as fp16 hi + lo.
+    // The k index of each product runs over two 16-row blocks in the order the accumulators hold
+    // them (lane group g: rows 4 g .. 4 g + 3 of the first block, then of the second), so an
+    // accumulator pair is a B operand as it stands; the A side reads A and D^-1 in that order.
     {
-        float* u = (float*)(ws + L.u) + vu * CH * D;
-        half_t* wout = (half_t*)(ws + L.w) + vu * CH * D;
-        half8 vbh[2][2], vbl[2][2], kb[2][2];
+        const bool isw = wave >= 2;
+        const int cbase = 64 * (wave & 1);
+        half_t (*src)[QK_LD] = isw ? Ks : QV;  // raw k rows / v rows (fp16)
+        typedef __attribute__((address_space(3))) short4v_t lds_s4;
+        // row factors of this lane's rows 16 r + 4 gq + j
+        f32x4 U[4][4];
 #pragma unroll
-        for (int t = 0; t < 2; t++) {
-            const int col = 16 * (2 * wave + t) + n;
+        for (int r = 0; r < 4; r++)
 #pragma unroll
-            for (int ks = 0; ks < 2; ks++)
+            for (int ct = 0; ct < 4; ct++) U[r][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+        // A-side operand (rows 16 r + n, k slots of block pair (kb0, kb0 + 1)), hi / lo, negated
+        // on request; columns of blocks >= nb_valid read as zero
+        auto aop = [&](int r, int kb0, bool second, bool neg, half8& hi, half8& lo) {
+            const f32x4 x0 = *(const f32x4*)&As[16 * r + n][16 * kb0 + 4 * gq];
+            f32x4 x1 = f32x4{0.f, 0.f, 0.f, 0.f};
+            if (second) x1 = *(const f32x4*)&As[16 * r + n][16 * (kb0 + 1) + 4 * gq];
 #pragma unroll
-                for (int i = 0; i < 8; i++) {
-                    const int rr = 32 * ks + 8 * gq + i;
-                    vbh[t][ks][i] = QV[rr][col];
-                    if constexpr (kSplitV) vbl[t][ks][i] = Vl[rr][col];
-                    kb[t][ks][i] = Ks[rr][col];
+            for (int i = 0; i < 8; i++) {
+                const float x = (i < 4 ? x0[i] : x1[i - 4]) * (neg ? -1.f : 1.f);
+                const half_t h = (half_t)x;
+                hi[i] = h;
+                lo[i] = (half_t)(x - (float)h);
+            }
+        };
+        auto split = [&](const f32x4& a, const f32x4& b, half8& hi, half8& lo) {
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const float x = i < 4 ? a[i] : b[i - 4];
+                const half_t h = (half_t)x;
+                hi[i] = h;
+                lo[i] = (half_t)(x - (float)h);
+            }
+        };
+        const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            float fr[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int t = 16 * r + 4 * gq + j;
+                fr[j] = isw ? beta_s[t] * __expf(cum_s[t]) * rk_s[t] : beta_s[t];
+            }
+            f32x4 acc[4];
+#pragma unroll
+            for (int ct = 0; ct < 4; ct++) {
+                // right-hand side rows 16 r + 4 gq .. +3 of column cbase + 16 ct + n: one
+                // transpose read (lane k of a 16-lane group addresses row R + k / 4, columns
+                // C + 4 (k % 4) .. +3; lane j receives rows R .. R + 3 of column C + j)
+                const int R0 = 16 * r + 4 * gq, C0 = cbase + 16 * ct;
+                const short4v_t h4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (lds_s4*)&src[R0 + (n >> 2)][C0 + 4 * (n & 3)]);
+                // (bit-cast the whole vector: clang's __builtin_bit_cast of a vector element
+                // reads element 0 whatever the index)
+                const half4 hh = __builtin_bit_cast(half4, h4);
+#pragma unroll
+                for (int j = 0; j < 4; j++) acc[ct][j] = fr[j] * (float)hh[j];
+                if constexpr (kSplitV) {
+                    if (!isw) {
+                        const short4v_t l4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                            (lds_s4*)&Vl[R0 + (n >> 2)][C0 + 4 * (n & 3)]);
+                        const half4 ll = __builtin_bit_cast(half4, l4);
+#pragma unroll
+                        for (int j = 0; j < 4; j++) acc[ct][j] += fr[j] * (float)ll[j];
+                    }
                 }
-        }
-        lds_barrier();  // every wave holds its v / k_n operands: QV and Ks take the X fragments
-        // X diag(beta) and X diag(beta e^cum), each as fp16 hi + lo (hi + lo carries ~22 bits),
-        // converted once per workgroup into A-fragment order (afrag_coords, K = 64): thread =
-        // (row r, 16 consecutive k); QV holds the u factors, Ks the w factors
-        half8* XU = (half8*)&QV[0][0];  // [hi: 512 fragments][lo: 512]
-        half8* XW = (half8*)&Ks[0][0];
-        {
-            const int r = tid / 4, kq = tid % 4;
+            }
+            // acc -= A_{r, (2m, 2m+1)} U_{(2m, 2m+1)} over the block pairs below r
 #pragma unroll
-            for (int h = 0; h < 2; h++) {
-                const int k0 = 16 * kq + 8 * h;
-                const f32x4 x0 = *(const f32x4*)&As[r][k0], x1 = *(const f32x4*)&As[r][k0 + 4];
-                half8 uh, ul, wh, wl;
+            for (int m = 0; 2 * m < r; m++) {
+                half8 ah, al;
+                aop(r, 2 * m, 2 * m + 1 < r, true, ah, al);
 #pragma unroll
-                for (int i = 0; i < 8; i++) {
-                    const float x = i < 4 ? x0[i] : x1[i - 4];
-                    const float bu = beta_s[k0 + i], xu = x * bu;
-                    const float xw = x * (bu * __expf(cum_s[k0 + i]) * rk_s[k0 + i]);
-                    half_t hh = (half_t)xu;
-                    uh[i] = hh;
-                    ul[i] = (half_t)(xu - (float)hh);
-                    hh = (half_t)xw;
-                    wh[i] = hh;
-                    wl[i] = (half_t)(xw - (float)hh);
+                for (int ct = 0; ct < 4; ct++) {
+                    half8 bh, bl;
+                    split(U[2 * m][ct], 2 * m + 1 < r ? U[2 * m + 1][ct] : zero4, bh, bl);
+                    acc[ct] = mfma16(ah, bh, acc[ct]);
+                    acc[ct] = mfma16(ah, bl, acc[ct]);
+                    acc[ct] = mfma16(al, bh, acc[ct]);
                 }
-                // fragment (mb, ks) lane l = r % 16 + 16 gq' holds k = 32 ks + 8 gq' + i
-                const int f = ((r / 16) * 2 + k0 / 32) * 64 + (r % 16) + 16 * ((k0 % 32) / 8);
-                XU[f] = uh;
-                XU[512 + f] = ul;
-                XW[f] = wh;
-                XW[512 + f] = wl;
+            }
+            // U_r = D_r^-1 acc (k slots of the second block are zero on both sides)
+            half8 dh, dl;
+            aop(r, r, false, false, dh, dl);
+#pragma unroll
+            for (int ct = 0; ct < 4; ct++) {
+                half8 bh, bl;
+                split(acc[ct], zero4, bh, bl);
+                f32x4 y = mfma16(dh, bh, zero4);
+                y = mfma16(dh, bl, y);
+                U[r][ct] = mfma16(dl, bh, y);
             }
         }
-        lds_barrier();
-        // w staging for fragment order, in As's space (X has been read)
+        if (!isw) {
+            float* u = (float*)(ws + L.u) + vu * CH * D;
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+#pragma unroll
+                for (int ct = 0; ct < 4; ct++)
+                    *(f32x4*)(u + u_frag(16 * r + 4 * gq, cbase + 16 * ct + n)) = U[r][ct];
+        }
+        lds_barrier();  // every wave is done with As and the v / k tiles: w is staged in As's space
         half_t (*Wst)[QK_LD] = (half_t (*)[QK_LD])&As[0][0];
+        if (isw) {
 #pragma unroll
-        for (int rb = 0; rb < 4; rb++) {
-            half8 xuh[2], xul[2], xwh[2], xwl[2];
+            for (int r = 0; r < 4; r++)
 #pragma unroll
-            for (int ks = 0; ks < 2; ks++) {
-                const int f = (rb * 2 + ks) * 64 + lane;
-                xuh[ks] = XU[f];
-                xul[ks] = XU[512 + f];
-                xwh[ks] = XW[f];
-                xwl[ks] = XW[512 + f];
-            }
+                for (int ct = 0; ct < 4; ct++)
 #pragma unroll
-            for (int t = 0; t < 2; t++) {
-                f32x4 au = {0.f, 0.f, 0.f, 0.f}, aw = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int ks = 0; ks < 2; ks++) {
-                    au = mfma16(xuh[ks], vbh[t][ks], au);
-                    au = mfma16(xul[ks], vbh[t][ks], au);
-                    if constexpr (kSplitV) au = mfma16(xuh[ks], vbl[t][ks], au);
-                    aw = mfma16(xwh[ks], kb[t][ks], aw);
-                    aw = mfma16(xwl[ks], kb[t][ks], aw);
-                }
-                const int col = 16 * (2 * wave + t) + n;
-                *(f32x4*)(u + u_frag(16 * rb + 4 * gq, col)) = au;
-#pragma unroll
-                for (int j = 0; j < 4; j++) Wst[16 * rb + 4 * gq + j][col] = (half_t)aw[j];
-            }
+                    for (int j = 0; j < 4; j++) Wst[16 * r + 4 * gq + j][cbase + 16 * ct + n] = (half_t)U[r][ct][j];
         }
         lds_barrier();
-        // w (A of w S: 64 x 128) in fragment order
-        half8* wf = (half8*)wout;
+        half8* wf = (half8*)((half_t*)(ws + L.w) + vu * CH * D);
 #pragma unroll
         for (int it = 0; it < 4; it++) {
             const int f = tid + 256 * it;

@@ -82,12 +82,111 @@ def cpu_baseline_decode(torch, ops=None, dev=None):
         if i >= 2:
             times.append(time.perf_counter() - t0)
     per_layer = statistics.median(times)
-    out = {"value": B / (per_layer * LAYERS), "unit": "tok/s", "cores": cpu_threads(), "kind": "port",
+    out = {"value": B / (per_layer * LAYERS), "unit": "tok/s", "cores": cpu_threads(), "cpu_model": cpu_model(),
+           "kind": "port",
            "sample": f"1 of {LAYERS} layers at B={B} (oracle.mixer_ref.delta_decode_fused, torch-CPU fp32), "
                      f"median of 5 after 2 warm-ups, scaled x{LAYERS}; {per_layer * 1e3:.1f} ms per layer"}
     if dev is not None:
         parity["config2_prefill"] = prefill_parity(torch, ops, dev, R)
         out["parity"] = parity
+    return out
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+    return platform.processor() or "unknown"
+
+
+def _median_time(fn, warm=1, n=3):
+    for _ in range(warm):
+        fn()
+    ts = []
+    for _ in range(n):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return statistics.median(ts)
+
+
+def cpu_baseline_configs(torch):
+    """The oracle (torch-CPU fp32, all host cores) on bounded samples of configs 0, 2, 3 and 4,
+    each reported in the unit of the matching GPU leg. Samples: config 0 in full (256 steps,
+    B = 1); config 2 on the first 1024 of 8192 tokens (the chunked form is linear in T);
+    config 3 at one point (B = 1, L = 32768); config 4 as one DeltaNet and one attention layer at
+    full shape (decode at B = 16 with 2048 cached tokens; prefill on 256 of 2048 tokens of one
+    sequence) scaled to 30 + 10 layers."""
+    from oracle import mixer_ref as R
+    torch.set_num_threads(cpu_threads())
+    F = torch.nn.functional
+    g_ = torch.Generator().manual_seed(1)
+    out = {}
+
+    def qkvgb(Bt, T, hv=HV):
+        q = R.l2norm(torch.randn(Bt, hv, T, D, generator=g_).to(torch.bfloat16).float()) * D ** -0.5
+        k = R.l2norm(torch.randn(Bt, hv, T, D, generator=g_).to(torch.bfloat16).float())
+        v = torch.randn(Bt, hv, T, D, generator=g_).to(torch.bfloat16).float()
+        g = -F.softplus(torch.randn(Bt, hv, T, generator=g_))
+        beta = torch.sigmoid(torch.randn(Bt, hv, T, generator=g_))
+        return q, k, v, g, beta
+
+    # config 0: 256 sequential steps, B = 1
+    q, k, v, g, beta = qkvgb(1, 256)
+    t = _median_time(lambda: R.delta_rule_recurrent(q, k, v, g, beta, None))
+    out["config0_recurrent"] = {"value": round(256 / t, 1), "unit": "tok/s", "sample": "full: B=1, 256 steps, 32 heads"}
+    # config 2: chunked prefill on a 1024-token sample
+    Ts = 1024
+    q, k, v, g, beta = qkvgb(1, Ts)
+    t = _median_time(lambda: R.delta_rule_chunked(q, k, v, g, beta, None))
+    out["config2_prefill"] = {"value": round(Ts / t, 1), "unit": "tok/s",
+                              "sample": f"first {Ts} of {PREFILL_T} tokens, B=1, 32 heads (linear in T)"}
+    # config 3: one decode point
+    L, Bt = 32768, 1
+    kc = torch.randn(Bt, ATTN_KV, L + 1, ATTN_HD, generator=g_).to(torch.bfloat16)
+    vc = torch.randn(Bt, ATTN_KV, L + 1, ATTN_HD, generator=g_).to(torch.bfloat16)
+    qg = torch.randn(Bt, ATTN_H, 2 * ATTN_HD, generator=g_).to(torch.bfloat16)
+    kn = torch.randn(Bt, ATTN_KV, ATTN_HD, generator=g_).to(torch.bfloat16)
+    vn = torch.randn(Bt, ATTN_KV, ATTN_HD, generator=g_).to(torch.bfloat16)
+    zw = torch.zeros(ATTN_HD)
+    t = _median_time(lambda: R.attention_decode(qg, kn, vn, zw, zw, kc, vc, L, ATTN_RD, ATTN_THETA))
+    out["config3_decode"] = {"value": round(Bt / t, 1), "unit": "tok/s", "sample": f"B={Bt}, L={L} (one of nine points)"}
+    del kc, vc
+    # config 4: one layer of each kind at full shape
+    Cc = 2 * HK * D + HV * D
+
+    def w(*shape, std=0.02):
+        return (torch.randn(*shape, generator=g_) * std).to(torch.bfloat16)
+    Wd = {"norm1": w(2048), "w_qkv": w(Cc, 2048), "w_z": w(4096, 2048), "w_b": w(32, 2048), "w_a": w(32, 2048),
+          "conv_w": w(Cc, 4, std=0.05), "a_log": w(32, std=0.5), "dt_bias": w(32, std=0.5),
+          "gnorm_w": w(128, std=0.1) + 1, "w_out": w(2048, 4096)}
+    Wa = {"norm1": w(2048), "w_q": w(8192, 2048), "w_k": w(512, 2048), "w_v": w(512, 2048), "w_o": w(2048, 4096),
+          "q_norm": w(256, std=0.1), "k_norm": w(256, std=0.1)}
+    B4, T4, Tp = 16, 2048, 256
+    conv, st = torch.zeros(B4, Cc, 3), torch.zeros(B4, HV, D, D)
+    kc4 = torch.zeros(B4, ATTN_KV, T4 + 1, ATTN_HD, dtype=torch.bfloat16)
+    vc4 = torch.zeros_like(kc4)
+    h1 = torch.randn(B4, 1, 2048, generator=g_)
+    td = _median_time(lambda: R.gated_deltanet_mixer(h1, Wd, conv, st.clone(), 1, HK, HV))
+    ta = _median_time(lambda: R.gated_attention_mixer(h1, Wa, kc4, vc4, T4, ATTN_H, ATTN_KV))
+    hp = torch.randn(1, Tp, 2048, generator=g_)
+    tdp = _median_time(lambda: R.gated_deltanet_mixer(hp, Wd, torch.zeros(1, Cc, 3), torch.zeros(1, HV, D, D), 0,
+                                                      HK, HV), warm=1, n=1)
+    tap = _median_time(lambda: R.gated_attention_mixer(hp, Wa, kc4[:1], vc4[:1], 0, ATTN_H, ATTN_KV), warm=1, n=1)
+    step = 30 * td + 10 * ta
+    # prefill: per-token cost of the 256-token sample (attention's quadratic part is a small
+    # share of its layer at T = 2048; the sample understates it, so the CPU figure is generous)
+    pre_tok_s = Tp / (30 * tdp + 10 * tap)
+    out["config4_stack"] = {"decode_tok_s": round(B4 / step, 2), "prefill_tok_s": round(pre_tok_s, 1),
+                            "unit": "tok/s",
+                            "sample": f"one DeltaNet + one attention layer at d 2048: decode at B={B4} over "
+                                      f"{T4} cached tokens, prefill on {Tp} tokens of one sequence; scaled to 30 + 10 "
+                                      f"layers"}
     return out
 
 
@@ -561,6 +660,7 @@ def main():
         torch.cuda.synchronize()
     if not args.no_cpu:
         res["cpu_baseline"] = cpu_baseline_decode(torch, ops, dev)
+        res["cpu_baseline"]["configs"] = cpu_baseline_configs(torch)
     print(json.dumps(res), flush=True)
 
 
