@@ -31,11 +31,11 @@ namespace aegist {
 struct RopeTable;
 int launch_attn_prep(const void* qg, const void* k, const void* v, int in_dtype, const uint16_t* qw,
                      const uint16_t* kw, float* qn, uint16_t* kc, uint16_t* vc, int B, int T, int H, int KV, int HD,
-                     int RD, int pos0, int cap, float eps, float theta, hipStream_t stream, int* zero_ctr,
-                     int n_ctr);
+                     int RD, int pos0, int cap, float eps, float theta, hipStream_t stream);
 }  // namespace aegist
 
 namespace {
+
 
 constexpr int HD = 256;
 constexpr int TILE = 32;             // keys per wave iteration
@@ -81,96 +81,12 @@ struct GateLd {
     static __device__ __forceinline__ float ld(const TG* p, size_t i) { return Act<TG>::ld(p, i); }
 };
 
-// Combine the nsplit (<= 256) partial results of one (sequence, KV head) for its G <= 8 query
-// heads: y = (sum_s e^{m_s - M} O_s) / (sum_s e^{m_s - M} l_s) * sigmoid(gate). 256 threads =
-// 8 heads x 32 threads; every head is merged at once (thread = 8 output dims), weights in LDS.
-template <typename TG, typename Tout>
-__device__ void merge_splits(const float* __restrict__ part, const float* __restrict__ ml, size_t base, int nsplit,
-                             int G, const TG* __restrict__ gate, long long gate_stride, Tout* __restrict__ out,
-                             long long out_stride, size_t row0) {
-    __shared__ float fw[8][256];
-    const int tid = threadIdx.x, rr = tid / 32, t32 = tid % 32;
-    const bool active = rr < G;
-    const int d0 = t32 * 8;
-    const size_t row = row0 + rr;
-    // every load of the statistics and the gate is issued before the first wait: (m, l) of
-    // splits t32 + 32 k (nsplit <= 256; indices past the last split re-read it, masked below)
-    float2 st[8];
-    float gv[8];
-    if (active) {
-#pragma unroll
-        for (int k = 0; k < 8; k++)
-            st[k] = *(const float2*)(ml + ((base + min(t32 + 32 * k, nsplit - 1)) * G + rr) * 2);
-#pragma unroll
-        for (int e = 0; e < 8; e++) gv[e] = gate ? Act<TG>::ld(gate, row * gate_stride + d0 + e) : 0.f;
-    }
-    float mx = -INFINITY;
-#pragma unroll
-    for (int k = 0; k < 8; k++)
-        if (active && t32 + 32 * k < nsplit) mx = fmaxf(mx, st[k].x);
-#pragma unroll
-    for (int o = 16; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, WAVE));
-    float ls = 0.f;
-#pragma unroll
-    for (int k = 0; k < 8; k++) {
-        const int sp = t32 + 32 * k;
-        if (active && sp < nsplit) {
-            const float f = st[k].x == -INFINITY ? 0.f : __expf(st[k].x - mx);
-            fw[rr][sp] = f;
-            ls += st[k].y * f;
-        }
-    }
-#pragma unroll
-    for (int o = 16; o > 0; o >>= 1) ls += __shfl_xor(ls, o, WAVE);
-    __syncthreads();
-    if (!active) return;
-    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    // software-pipelined over batches of SB splits: the next batch's loads are in flight while
-    // this one accumulates (the partials come from other XCDs: each batch is a full memory
-    // latency); batch indices past the last split re-read it and are weighted 0
-#ifndef ATTN_MERGE_SB
-#define ATTN_MERGE_SB 4
-#endif
-    constexpr int SB = ATTN_MERGE_SB;
-    float4 cur[SB][2], nxt[SB][2];
-    auto load_batch = [&](float4 (&v)[SB][2], int s0) {
-#pragma unroll
-        for (int e = 0; e < SB; e++) {
-            const float4* p = (const float4*)(part + ((base + min(s0 + e, nsplit - 1)) * G + rr) * HD + d0);
-            v[e][0] = p[0];
-            v[e][1] = p[1];
-        }
-    };
-    load_batch(cur, 0);
-    for (int s = 0; s < nsplit; s += SB) {
-        load_batch(nxt, s + SB);
-#pragma unroll
-        for (int e = 0; e < SB; e++) {
-            const float f = s + e < nsplit ? fw[rr][s + e] : 0.f;
-            acc[0] += cur[e][0].x * f; acc[1] += cur[e][0].y * f; acc[2] += cur[e][0].z * f; acc[3] += cur[e][0].w * f;
-            acc[4] += cur[e][1].x * f; acc[5] += cur[e][1].y * f; acc[6] += cur[e][1].z * f; acc[7] += cur[e][1].w * f;
-        }
-#pragma unroll
-        for (int e = 0; e < SB; e++) {
-            cur[e][0] = nxt[e][0];
-            cur[e][1] = nxt[e][1];
-        }
-    }
-    const float inv = 1.f / ls;
-#pragma unroll
-    for (int e = 0; e < 8; e++) {
-        float y = acc[e] * inv;
-        if (gate) y *= sigmoid_f(gv[e]);
-        Act<Tout>::st(out, row * out_stride + d0 + e, y);
-    }
-}
-
 // q:   [B, H, HD] fp32 (normed, roped), head h of KV head kvh is kvh*G + r
 // kc, vc: [B, KV, cap, HD] bf16
 // part: [B, KV, nsplit, G, HD] fp32 partial outputs (unnormalised), ml: [B, KV, nsplit, G, 2]
-// With `counters` set, the last workgroup of each (sequence, KV head) to finish merges all
-// splits and writes the gated output (the counter is zeroed by the prep kernel that runs
-// first and reset by that last workgroup); otherwise attn_decode_merge_kernel does it.
+// attn_decode_merge_wide_kernel then combines the splits (a second launch: a device-scope
+// release and counter atomic at the end of every split workgroup, with the last one merging,
+// cost far more than the launch).
 // Keys of a sparse (listed-block) query, attention_gated_list (next.cu:648-705): the query at
 // position p = pos0 + b sees the R keys of each of its nsel[b] listed blocks, in list order, then
 // the keys of its own incomplete block, positions complete R .. p (complete = (p + 1) / R).
@@ -181,16 +97,13 @@ struct KeyList {
     int top, R, pos0;
 };
 
-template <typename TG, typename Tout, bool kList>
+template <bool kList>
 __global__ void __launch_bounds__(256) attn_decode_split_kernel(const float* __restrict__ q,
                                                                 const uint16_t* __restrict__ kc,
                                                                 const uint16_t* __restrict__ vc,
                                                                 float* __restrict__ part, float* __restrict__ ml,
                                                                 int H, int KV, int L, int cap, int per_split,
-                                                                float scale, int* __restrict__ counters,
-                                                                const TG* __restrict__ gate, long long gate_stride,
-                                                                Tout* __restrict__ out, long long out_stride,
-                                                                KeyList kl) {
+                                                                float scale, KeyList kl) {
     // V staging per wave during the loop; the 4-wave merge buffer reuses the same bytes after it
     __shared__ __attribute__((aligned(16))) unsigned char vbuf_raw[4 * TILE * VROW];
     __shared__ __attribute__((aligned(16))) unsigned char kbuf[4][TILE * VROW];
@@ -435,29 +348,69 @@ __global__ void __launch_bounds__(256) attn_decode_split_kernel(const float* __r
             ml[pidx * 2 + 1] = Lsum;
         }
     }
-    if (counters == nullptr) return;
-    // ---- fused split merge: the last workgroup of this (b, kvh) combines every split
-    __shared__ int last;
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) last = atomicAdd(&counters[b * KV + kvh], 1) == nsplit - 1;
-    __syncthreads();
-    if (!last) return;
-    __threadfence();
-    merge_splits<TG, Tout>(part, ml, ((size_t)b * KV + kvh) * nsplit, nsplit, G, gate, gate_stride, out, out_stride,
-                           (size_t)b * H + kvh * G);
-    if (tid == 0) counters[b * KV + kvh] = 0;
 }
 
-// Standalone split merge (used when no counters are available): one block per (b, kvh).
+// Split merge spread over the GPU: one workgroup per (sequence, KV head, query head), so a
+// long context's many splits are combined by B KV G workgroups instead of B KV. Thread t holds
+// output dims 4 (t % 64) .. +3 for the splits s = t / 64 (mod 4); the four split groups are added
+// in a fixed order through LDS, so the result does not depend on timing.
 template <typename TG, typename Tout>
-__global__ void __launch_bounds__(256) attn_decode_merge_kernel(const float* __restrict__ part,
-                                                                const float* __restrict__ ml, const TG* __restrict__ gate,
-                                                                long long gate_row_stride, Tout* __restrict__ out,
-                                                                long long out_row_stride, int H, int KV, int nsplit) {
-    const int u = blockIdx.x, b = u / KV, kvh = u % KV, G = H / KV;
-    merge_splits<TG, Tout>(part, ml, (size_t)u * nsplit, nsplit, G, gate, gate_row_stride, out, out_row_stride,
-                           (size_t)b * H + kvh * G);
+__global__ void __launch_bounds__(256) attn_decode_merge_wide_kernel(const float* __restrict__ part,
+                                                                     const float* __restrict__ ml,
+                                                                     const TG* __restrict__ gate,
+                                                                     long long gate_row_stride, Tout* __restrict__ out,
+                                                                     long long out_row_stride, int H, int KV, int nsplit) {
+    __shared__ float fw[256];
+    __shared__ float red[2][4];
+    __shared__ f32x4 acc_s[3][64];
+    const int G = H / KV;
+    const int r = blockIdx.x % G, u = blockIdx.x / G, b = u / KV, kvh = u % KV;
+    const int tid = threadIdx.x, q4 = tid % 64, sg = tid / 64, lane = tid % WAVE, wave = tid / WAVE;
+    const size_t base = (size_t)u * nsplit;
+    // statistics: thread t holds split t (nsplit <= 256)
+    const float2 st = tid < nsplit ? *(const float2*)(ml + ((base + tid) * G + r) * 2) : float2{-INFINITY, 0.f};
+    const size_t row = (size_t)b * H + kvh * G + r;
+    float gv[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) gv[e] = gate ? Act<TG>::ld(gate, row * gate_row_stride + 4 * q4 + e) : 0.f;
+    float mx = wave_max(st.x);
+    if (lane == 0) red[0][wave] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
+    const float f = st.x == -INFINITY ? 0.f : __expf(st.x - mx);
+    fw[tid] = f;
+    float ls = wave_sum(st.y * f);
+    if (lane == 0) red[1][wave] = ls;
+    __syncthreads();
+    ls = (red[1][0] + red[1][1]) + (red[1][2] + red[1][3]);
+    // this thread's splits s = sg, sg + 4, ..., in batches of 8 loads in flight
+    f32x4 a = {0.f, 0.f, 0.f, 0.f};
+    constexpr int SB = 8;
+    for (int s0 = sg; s0 < nsplit; s0 += 4 * SB) {
+        f32x4 v[SB];
+#pragma unroll
+        for (int e = 0; e < SB; e++) {
+            const int sp = min(s0 + 4 * e, nsplit - 1);
+            v[e] = *(const f32x4*)(part + ((base + sp) * G + r) * HD + 4 * q4);
+        }
+#pragma unroll
+        for (int e = 0; e < SB; e++) {
+            const int sp = s0 + 4 * e;
+            a += v[e] * (sp < nsplit ? fw[sp] : 0.f);
+        }
+    }
+    if (sg > 0) acc_s[sg - 1][q4] = a;
+    __syncthreads();
+    if (sg == 0) {
+        a = ((a + acc_s[0][q4]) + acc_s[1][q4]) + acc_s[2][q4];
+        const float inv = 1.f / ls;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            float y = a[e] * inv;
+            if (gate) y *= sigmoid_f(gv[e]);
+            Act<Tout>::st(out, row * out_row_stride + 4 * q4 + e, y);
+        }
+    }
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -766,17 +719,15 @@ size_t decode_workspace_bytes(int B, int H, int KV, int L, bool with_q) {
     size_t part = (size_t)B * KV * sp.nsplit * G * HD * 4;
     size_t ml = (size_t)B * KV * sp.nsplit * G * 2 * 4;
     size_t qb = with_q ? (size_t)B * H * HD * 4 : 0;
-    size_t cnt = with_q ? (size_t)B * KV * 4 : 0;
     auto al = [](size_t x) { return (x + 255) / 256 * 256; };
-    return al(part) + al(ml) + al(qb) + al(cnt);
+    return al(part) + al(ml) + al(qb);
 }
 
 // q [B, H, HD] fp32 -> out rows (b*H + h) * out_row_stride, gate rows (b*H + h) * gate_row_stride
 template <typename TG, typename Tout>
 int launch_decode_core(const float* q, const uint16_t* kc, const uint16_t* vc, const TG* gate, long long gate_stride,
                        Tout* out, long long out_stride, int B, int H, int KV, int L, int cap, float scale,
-                       void* ws, size_t ws_bytes, hipStream_t st, int* counters = nullptr,
-                       KeyList kl = KeyList{nullptr, nullptr, 0, 0, 0}) {
+                       void* ws, size_t ws_bytes, hipStream_t st, KeyList kl = KeyList{nullptr, nullptr, 0, 0, 0}) {
     if (KV <= 0 || H % KV || H / KV > 8) return fail(AEGIST_ERR_SHAPE, "attention decode: need H % KV == 0 and H/KV <= 8");
     if (L <= 0 || L > cap) return fail(AEGIST_ERR_SHAPE, "attention decode: need 0 < L <= cap");
     DecodeSplit sp = choose_split(B, KV, L);
@@ -787,15 +738,15 @@ int launch_decode_core(const float* q, const uint16_t* kc, const uint16_t* vc, c
     size_t part_bytes = ((size_t)B * KV * sp.nsplit * G * HD * 4 + 255) / 256 * 256;
     float* ml = (float*)((char*)ws + part_bytes);
     if (kl.blist)
-        attn_decode_split_kernel<TG, Tout, true><<<dim3(sp.nsplit, KV, B), 256, 0, st>>>(
-            q, kc, vc, part, ml, H, KV, L, cap, sp.per_split, scale, counters, gate, gate_stride, out, out_stride, kl);
+        attn_decode_split_kernel<true><<<dim3(sp.nsplit, KV, B), 256, 0, st>>>(q, kc, vc, part, ml, H, KV, L, cap,
+                                                                             sp.per_split, scale, kl);
     else
-        attn_decode_split_kernel<TG, Tout, false><<<dim3(sp.nsplit, KV, B), 256, 0, st>>>(
-            q, kc, vc, part, ml, H, KV, L, cap, sp.per_split, scale, counters, gate, gate_stride, out, out_stride, kl);
+        attn_decode_split_kernel<false><<<dim3(sp.nsplit, KV, B), 256, 0, st>>>(q, kc, vc, part, ml, H, KV, L, cap,
+                                                                              sp.per_split, scale, kl);
     int rc = after_launch("attention_decode_split");
-    if (rc || counters) return rc;
-    attn_decode_merge_kernel<TG, Tout><<<B * KV, 256, 0, st>>>(part, ml, gate, gate_stride, out, out_stride, H, KV,
-                                                               sp.nsplit);
+    if (rc) return rc;
+    attn_decode_merge_wide_kernel<TG, Tout><<<B * KV * G, 256, 0, st>>>(part, ml, gate, gate_stride, out, out_stride,
+                                                                       H, KV, sp.nsplit);
     return after_launch("attention_decode_merge");
 }
 
@@ -856,9 +807,8 @@ int aegist_attention_decode(const void* qg, const void* k_new, const void* v_new
     hipStream_t st = AEG_STREAM(stream);
     size_t core = decode_workspace_bytes(B, H, KV, pos + 1, false);
     float* qn = (float*)((char*)workspace + core);
-    int* ctr = (int*)((char*)qn + ((size_t)B * H * HD * 4 + 255) / 256 * 256);
     int rc = launch_attn_prep(qg, k_new, v_new, in_dtype, q_norm_w, k_norm_w, qn, kc, vc, B, 1, H, KV, HD, RD, pos, cap,
-                              eps, theta, st, ctr, B * KV);
+                              eps, theta, st);
     if (rc) return rc;
     const float scale = 1.0f / sqrtf((float)HD);
     // gate = second half of each head's 2*HD row of qg
@@ -866,25 +816,25 @@ int aegist_attention_decode(const void* qg, const void* k_new, const void* v_new
         const float* gate = (const float*)qg + HD;
         if (out_dtype == AEGIST_F32)
             return launch_decode_core<float, float>(qn, kc, vc, gate, 2 * HD, (float*)out, HD, B, H, KV, pos + 1, cap,
-                                                    scale, workspace, core, st, ctr);
+                                                    scale, workspace, core, st);
         if (out_dtype == AEGIST_BF16)
             return launch_decode_core<float, uint16_t>(qn, kc, vc, gate, 2 * HD, (uint16_t*)out, HD, B, H, KV, pos + 1,
-                                                       cap, scale, workspace, core, st, ctr);
+                                                       cap, scale, workspace, core, st);
     } else if (in_dtype == AEGIST_BF16) {
         const uint16_t* gate = (const uint16_t*)qg + HD;
         if (out_dtype == AEGIST_F32)
             return launch_decode_core<uint16_t, float>(qn, kc, vc, gate, 2 * HD, (float*)out, HD, B, H, KV, pos + 1,
-                                                       cap, scale, workspace, core, st, ctr);
+                                                       cap, scale, workspace, core, st);
         if (out_dtype == AEGIST_BF16)
             return launch_decode_core<uint16_t, uint16_t>(qn, kc, vc, gate, 2 * HD, (uint16_t*)out, HD, B, H, KV,
-                                                          pos + 1, cap, scale, workspace, core, st, ctr);
+                                                          pos + 1, cap, scale, workspace, core, st);
     }
     return fail(AEGIST_ERR_DTYPE, "attention_decode: dtypes must be AEGIST_F32 or AEGIST_BF16");
 }
 
 // ---------------------------------------------------------------------------------------------
 // attention_decode without a workspace argument and without allocating: its split-K partials,
-// statistics, normed queries and merge counters live in a file-scope device array (one copy per
+// statistics and normed queries live in a file-scope device array (one copy per
 // GPU, held until the process ends). Host code never passes the array's name to a kernel: the
 // array's device address is looked up once per device with hipGetSymbolAddress and kept.
 constexpr size_t kNoAllocScratchBytes = (size_t)32 << 20;
@@ -923,8 +873,8 @@ int aegist_attention_decode_noalloc(const void* qg, const void* k_new, const voi
     void* ws = nullptr;
     int rc = scratch_address(&ws);
     if (rc) return rc;
-    // the merge counters are zeroed by the prep kernel of every call, so the scratch needs no
-    // clearing between calls
+    // every byte of the scratch a call reads was written earlier in the same call, so it needs
+    // no clearing between calls
     return aegist_attention_decode(qg, k_new, v_new, in_dtype, q_norm_w, k_norm_w, kc, vc, out, out_dtype, B, H, KV,
                                    HDv, RD, pos, cap, eps, theta, ws, kNoAllocScratchBytes, stream);
 }
@@ -1007,7 +957,7 @@ int aegist_attention_gated_list_ws(const float* q, const uint16_t* kc, const uin
     int rc = check_workspace(ws, ws_bytes, decode_workspace_bytes(T, H, KV, Lmax, false), "attention_gated_list");
     if (rc) return rc;
     return launch_decode_core<float, float>(q, kc, vc, qg + HD, 2 * HD, out, HD, T, H, KV, Lmax, cap, scale, ws,
-                                            ws_bytes, AEG_STREAM(stream), nullptr, KeyList{blist, nsel, top, R, pos0});
+                                            ws_bytes, AEG_STREAM(stream), KeyList{blist, nsel, top, R, pos0});
 }
 
 int aegist_attention_gated_list(const float* q, const uint16_t* kc, const uint16_t* vc, const float* qg, float* out,
@@ -1020,3 +970,4 @@ int aegist_attention_gated_list(const float* q, const uint16_t* kc, const uint16
 }
 
 }  // extern "C"
+

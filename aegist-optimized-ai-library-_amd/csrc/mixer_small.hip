@@ -42,11 +42,8 @@ template <typename Tin>
 __global__ void __launch_bounds__(256) attn_prep_kernel(
     const Tin* __restrict__ qg, const Tin* __restrict__ k, const Tin* __restrict__ v, const uint16_t* __restrict__ qw,
     const uint16_t* __restrict__ kw, float* __restrict__ qn, uint16_t* __restrict__ kc, uint16_t* __restrict__ vc,
-    int B, int T, int H, int KV, int HD, int RD, int pos0, int cap, float eps, RopeTable rope, int* zero_ctr,
-    int n_ctr) {
+    int B, int T, int H, int KV, int HD, int RD, int pos0, int cap, float eps, RopeTable rope) {
     __shared__ float buf[4][256];
-    if (zero_ctr && blockIdx.x == 0)
-        for (int i = threadIdx.x; i < n_ctr; i += blockDim.x) zero_ctr[i] = 0;
     const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
     const int item = blockIdx.x * 4 + wave;  // (b, t, head) flattened
     const int heads = H + KV;
@@ -120,8 +117,7 @@ int make_rope_table(RopeTable* tab, int RD, float theta) {
 // qn [B, T, H, HD] fp32 (the engine layout); caches [B, KV, cap, HD].
 int launch_attn_prep(const void* qg, const void* k, const void* v, int in_dtype, const uint16_t* qw,
                      const uint16_t* kw, float* qn, uint16_t* kc, uint16_t* vc, int B, int T, int H, int KV, int HD,
-                     int RD, int pos0, int cap, float eps, float theta, hipStream_t stream, int* zero_ctr,
-                     int n_ctr) {
+                     int RD, int pos0, int cap, float eps, float theta, hipStream_t stream) {
     if (HD <= 0 || HD > 256 || RD > HD) return fail(AEGIST_ERR_SHAPE, "attn_prep: need 0 < HD <= 256 and RD <= HD");
     if (pos0 < 0 || pos0 + T > cap) return fail(AEGIST_ERR_SHAPE, "attn_prep: positions exceed the cache capacity");
     RopeTable tab;
@@ -132,11 +128,11 @@ int launch_attn_prep(const void* qg, const void* k, const void* v, int in_dtype,
     dim3 grid((items + 3) / 4);
     if (in_dtype == AEGIST_F32)
         attn_prep_kernel<float><<<grid, 256, 0, stream>>>((const float*)qg, (const float*)k, (const float*)v, qw, kw, qn,
-                                                          kc, vc, B, T, H, KV, HD, RD, pos0, cap, eps, tab, zero_ctr, n_ctr);
+                                                          kc, vc, B, T, H, KV, HD, RD, pos0, cap, eps, tab);
     else if (in_dtype == AEGIST_BF16)
         attn_prep_kernel<uint16_t><<<grid, 256, 0, stream>>>((const uint16_t*)qg, (const uint16_t*)k,
                                                              (const uint16_t*)v, qw, kw, qn, kc, vc, B, T, H, KV, HD,
-                                                             RD, pos0, cap, eps, tab, zero_ctr, n_ctr);
+                                                             RD, pos0, cap, eps, tab);
     else
         return fail(AEGIST_ERR_DTYPE, "attn_prep: dtype must be AEGIST_F32 or AEGIST_BF16");
     return after_launch("attn_prep");
@@ -147,7 +143,7 @@ extern "C" int aegist_attn_prep(const float* qg, const float* k, const float* v,
                                 float* qn, uint16_t* kc, uint16_t* vc, int T, int H, int KV, int HD, int RD, int pos0,
                                 int cap, float eps, float theta, void* stream) {
     return launch_attn_prep(qg, k, v, AEGIST_F32, qw, kw, qn, kc, vc, 1, T, H, KV, HD, RD, pos0, cap, eps, theta,
-                            AEG_STREAM(stream), nullptr, 0);
+                            AEG_STREAM(stream));
 }
 
 // ---------------------------------------------------------------------------------------------

@@ -33,7 +33,7 @@ int launch_delta_decode_stack(const float* qkv, const uint16_t* conv_w, float* c
                               float eps, hipStream_t st);
 int launch_attn_prep(const void* qg, const void* k, const void* v, int in_dtype, const uint16_t* qw,
                      const uint16_t* kw, float* qn, uint16_t* kc, uint16_t* vc, int B, int T, int H, int KV, int HD,
-                     int RD, int pos0, int cap, float eps, float theta, hipStream_t stream, int* zero_ctr, int n_ctr);
+                     int RD, int pos0, int cap, float eps, float theta, hipStream_t stream);
 int stack_attn_decode(const float* qn, const uint16_t* kc, const uint16_t* vc, const float* qg, uint16_t* out, int B,
                       int H, int KV, int L, int cap, float scale, void* ws, size_t ws_bytes, hipStream_t st);
 int stack_attn_prefill(const float* qn, const uint16_t* kc, const uint16_t* vc, const float* qg, float* out, int B,
@@ -195,7 +195,7 @@ int attn_layer(Stack* s, const AegistLayerWeights& w, int sl, float* x, int B, i
         RC(gemm_group(s, s->hb, 3, W, Y, N, ldy, rows, dm, st));
     }
     RC(launch_attn_prep(s->proj, kp, vp, AEGIST_F32, w.q_norm, w.k_norm, s->y, kc, vc, B, T, H, KV, HD, c.rotary_dim,
-                        s->length, (int)cap, c.eps, c.rope_theta, st, nullptr, 0));
+                        s->length, (int)cap, c.eps, c.rope_theta, st));
     const float scale = 1.f / sqrtf((float)HD);
     if (T == 1) {
         // the split / merge kernels write the gated output as bf16 (the out projection's input)

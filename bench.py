@@ -258,7 +258,7 @@ def bench_attention_decode(torch, ops, dev, reps=20):
     bf = torch.bfloat16
     stream = torch.cuda.current_stream().cuda_stream
     for L in (4096, 32768, 131072):
-        for Bt in (1, 8, 32):
+        for Bt in (1, 8, 32, 64):
             cap = L + 1
             kc = ops.fill_normal(torch.empty(Bt, ATTN_KV, cap, ATTN_HD, device=dev, dtype=bf), 8001)
             vc = ops.fill_normal(torch.empty(Bt, ATTN_KV, cap, ATTN_HD, device=dev, dtype=bf), 8002)
@@ -544,10 +544,23 @@ def bench_stack(torch, ops, dev, B=16, T=2048, steps=256):
     torch.cuda.synchronize()
     pre_ms, dec_ms = e[0].elapsed_time(e[1]), e[1].elapsed_time(e[2])
     stack.close()
+    # decode roofline: algorithmic HBM bytes of one B-token step = every projection weight once,
+    # each DeltaNet layer's recurrent state read + written and conv state read + written, each
+    # attention layer's K and V rows read (mean context over the timed steps), the new K / V rows
+    nd, na = kinds.count("delta"), kinds.count("attn")
+    w_delta = (C + 4096 + 32 + 32) * 2048 * 2 + 2048 * 4096 * 2
+    w_attn = (8192 + 512 + 512) * 2048 * 2 + 2048 * 4096 * 2
+    st_bytes = B * (2 * 32 * 128 * 128 * 4 + 2 * C * 3 * 4)
+    mean_L = T + (steps + 1) / 2
+    kv_bytes = B * 2 * mean_L * 256 * 2 * 2
+    step_bytes = nd * (w_delta + st_bytes) + na * (w_attn + kv_bytes)
+    gbs = step_bytes / (dec_ms / steps * 1e-3) / 1e9
     return {"workload": f"config4: 40-layer mixer stack, d 2048, prefill {B}x{T} then {steps} decode steps at B={B}",
             "prefill_ms": round(pre_ms, 3), "prefill_tok_s": round(B * T / (pre_ms * 1e-3), 1),
             "decode_ms_per_step": round(dec_ms / steps, 4), "decode_tok_s": round(B * steps / (dec_ms * 1e-3), 1),
             "total_tok_s": round(B * (T + steps) / ((pre_ms + dec_ms) * 1e-3), 1),
+            "decode_roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes_per_step": int(step_bytes)},
             "finite": bool(torch.isfinite(xt).all().item())}
 
 
