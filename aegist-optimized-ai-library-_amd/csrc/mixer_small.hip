@@ -327,6 +327,44 @@ __global__ void __launch_bounds__(256) znorm_bf16_vec_kernel(const float* __rest
     }
 }
 
+// ZNorm of x + sum_s part[s] (the split-K slices of the previous out projection, added in
+// order s = 0, 1, ...): the sum is written back to x (the residual) and normed into bf16.
+template <int NV>
+__global__ void __launch_bounds__(256) znorm_bf16_acc_vec_kernel(float* __restrict__ x, const float* __restrict__ part,
+                                                                 int nks, size_t slice, const uint16_t* __restrict__ w,
+                                                                 uint16_t* __restrict__ out, int D, float eps) {
+    __shared__ float red[4];
+    float4* xr = (float4*)(x + (size_t)blockIdx.x * D);
+    float4 v[NV];
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+        const int e = threadIdx.x + 256 * i;
+        float4 a = xr[e];
+        float4 p = ((const float4*)(part + (size_t)blockIdx.x * D))[e];
+        for (int s = 1; s < nks; s++) {
+            const float4 q = ((const float4*)(part + s * slice + (size_t)blockIdx.x * D))[e];
+            p.x += q.x; p.y += q.y; p.z += q.z; p.w += q.w;
+        }
+        a.x += p.x; a.y += p.y; a.z += p.z; a.w += p.w;
+        xr[e] = a;
+        v[i] = a;
+        ss += a.x * a.x + a.y * a.y + a.z * a.z + a.w * a.w;
+    }
+    ss = block_sum(ss, red);
+    const float inv = rsqrtf(ss / (float)D + eps);
+    if (!out) return;
+    uint2* orow = (uint2*)(out + (size_t)blockIdx.x * D);
+    const uint2* wr = (const uint2*)w;
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+        const int e = threadIdx.x + 256 * i;
+        const uint2 wp = wr[e];
+        orow[e] = uint2{f2bf2((v[i].x * inv) * (1.f + bf_lo(wp.x)), (v[i].y * inv) * (1.f + bf_hi(wp.x))),
+                        f2bf2((v[i].z * inv) * (1.f + bf_lo(wp.y)), (v[i].w * inv) * (1.f + bf_hi(wp.y)))};
+    }
+}
+
 // Gated norm into bf16 for DV % 128 == 0: half a wave (32 lanes, 16-byte loads) per (row, head).
 __global__ void __launch_bounds__(256) gated_norm_bf16_vec_kernel(const float* __restrict__ o,
                                                                   const float* __restrict__ z,
@@ -453,6 +491,23 @@ int launch_znorm_bf16(const float* x, const uint16_t* w, uint16_t* out, int rows
         default: znorm_bf16_kernel<<<rows, 256, 0, st>>>(x, w, out, D, eps);
     }
     return after_launch("znorm_bf16");
+}
+// x += sum of the split-K slices (in order), then ZNorm into out (out == nullptr: the sum only).
+// Needs D % 1024 == 0, D <= 8192 and 16-byte aligned rows.
+int launch_znorm_bf16_acc(float* x, const float* part, int nks, const uint16_t* w, uint16_t* out, int rows, int D,
+                          float eps, hipStream_t st) {
+    if (rows <= 0) return 0;
+    if (D % 1024 || D > 8192 || (uintptr_t)x % 16 || (uintptr_t)part % 16)
+        return fail(AEGIST_ERR_SHAPE, "znorm_acc: need D % 1024 == 0, D <= 8192, aligned rows");
+    const size_t slice = (size_t)rows * D;
+    switch (D / 1024) {
+        case 1: znorm_bf16_acc_vec_kernel<1><<<rows, 256, 0, st>>>(x, part, nks, slice, w, out, D, eps); break;
+        case 2: znorm_bf16_acc_vec_kernel<2><<<rows, 256, 0, st>>>(x, part, nks, slice, w, out, D, eps); break;
+        case 4: znorm_bf16_acc_vec_kernel<4><<<rows, 256, 0, st>>>(x, part, nks, slice, w, out, D, eps); break;
+        case 8: znorm_bf16_acc_vec_kernel<8><<<rows, 256, 0, st>>>(x, part, nks, slice, w, out, D, eps); break;
+        default: return fail(AEGIST_ERR_SHAPE, "znorm_acc: D / 1024 must be 1, 2, 4 or 8");
+    }
+    return after_launch("znorm_bf16_acc");
 }
 int launch_cast_bf16(const float* x, uint16_t* y, size_t n, hipStream_t st) {
     if (n == 0) return 0;

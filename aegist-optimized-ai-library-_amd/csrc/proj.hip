@@ -19,11 +19,20 @@
 // fp32 dot product to ~1e-5 relative; a bf16 X needs only the hi half.
 #include "common.h"
 
+#include <cstdlib>
 #include <type_traits>
 
 using namespace aegist;
 
 namespace {
+
+bool stream_enabled() {
+    static const bool on = [] {
+        const char* e = getenv("AEGIST_PROJ_STREAM");
+        return !(e && e[0] == '0');
+    }();
+    return on;
+}
 
 constexpr int KSTEP = 64;  // k per wave step: 16 bytes of int8 (two MFMA k-blocks of 32) per lane
 #ifndef PROJ_TARGET_WAVES
@@ -227,8 +236,13 @@ __global__ __launch_bounds__(64 * NWAVE) void proj_skinny_kernel(const TX* __res
         const int k = step * KSTEP + 16 * g;
 #pragma unroll
         for (int rt = 0; rt < RT; rt++) wl[buf][rt].load(wrow[rt], k, K, wok[rt]);
+#ifndef PROJ_NOX
 #pragma unroll
         for (int mt = 0; mt < MT; mt++) xl[buf][mt].load(xrow[mt], k, K, xok[mt]);
+#else
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) xl[buf][mt].load(xrow[mt], 0, K, xok[mt]);
+#endif
     };
     auto compute = [&](int buf) {
         bf16x8 xa[MT], xb[MT], la[MT], lb[MT];
@@ -297,6 +311,174 @@ __global__ __launch_bounds__(64 * NWAVE) void proj_skinny_kernel(const TX* __res
     }
 }
 
+// ---------------------------------------------------------------------------------------------
+// Decode-size bf16 projections (M <= 16) with W staged through LDS. The row-tile pattern above
+// (lane = (row, 32-byte run)) reads 16 rows x 128 bytes per pair of load instructions, and the
+// DRAM side serves that at ~half the rate of contiguous reads (same box: a read-only kernel
+// with that pattern 51% of HBM on 50 MB, 1 KB-contiguous reads 67%). Here every load
+// instruction is a direct global -> LDS copy of 1 KB of one pair of W rows (512 bytes each) and
+// the MFMA A operands are read back from LDS. Per workgroup: 16 NW rows of W (16 per wave, so
+// a wave owns whole output rows and no cross-wave reduction is needed) over all of K, in chunks
+// of KC = 256 k through an NS-stage ring; the X rows of each chunk ride in the same stage.
+// Slots of 16 bytes in a staged row are XOR-swizzled by the row index (the global address of
+// each lane is permuted, the 1 KB it covers is not), so the 16 rows a fragment read touches
+// hit 16 different bank groups.
+constexpr int SKC = 256;  // k per chunk
+template <typename TX, int NW, int NS>
+struct StreamSmem {
+    static constexpr int XB = 16 * SKC * sizeof(TX);  // X bytes per stage (16 rows)
+    __attribute__((aligned(16))) unsigned char w[NS][16 * NW][SKC * 2];
+    __attribute__((aligned(16))) unsigned char x[NS][XB];
+};
+
+// 16 bytes per lane straight from global memory into LDS at lds + 16 lane (lds uniform). Kept
+// in a device function: the builtin in a kernel body keeps the host pass from emitting the
+// kernel's launch stub.
+__device__ __forceinline__ void g2lds16(const void* src, void* lds) {
+    __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
+}
+
+__device__ __forceinline__ void wait_vm(int n) {
+    // s_waitcnt vmcnt(n) with the other counters left alone (gfx9 encoding: vmcnt in bits 3:0
+    // and 15:14, expcnt 6:4, lgkmcnt 11:8)
+    switch (n) {
+#define AEG_W(N) case N: __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8)); break;
+        AEG_W(0) AEG_W(1) AEG_W(2) AEG_W(3) AEG_W(4) AEG_W(5) AEG_W(6) AEG_W(7) AEG_W(8) AEG_W(9) AEG_W(10)
+        AEG_W(11) AEG_W(12) AEG_W(13) AEG_W(14) AEG_W(15) AEG_W(16) AEG_W(20) AEG_W(24) AEG_W(28) AEG_W(32)
+        AEG_W(40) AEG_W(48)
+#undef AEG_W
+        default: __builtin_amdgcn_s_waitcnt(0);
+    }
+}
+
+template <typename TX, int NW, int NS>
+__global__ __launch_bounds__(64 * NW) void proj_stream_kernel(const TX* __restrict__ X, long long ldx,
+                                                               const ProjSegs segs, int M, int K, int accumulate,
+                                                               float* __restrict__ part) {
+    __shared__ StreamSmem<TX, NW, NS> sm;
+    constexpr int RW = 16 * NW;                       // W rows per workgroup
+    constexpr int WI = RW / 2 / NW;                   // W load instructions per wave per stage (= 8)
+    constexpr int XI = StreamSmem<TX, NW, NS>::XB / 1024 / NW;  // X load instructions per wave per stage
+    static_assert(XI * NW * 1024 == StreamSmem<TX, NW, NS>::XB, "X stage must split evenly over the waves");
+    constexpr int PER = WI + XI;                      // loads per wave per stage
+    const int lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
+    const int r16 = lane % 16, g = lane / 16;
+    int si = 0;
+#pragma unroll
+    for (int i = 1; i < MAX_SEG; i++)
+        if (i < segs.n && (int)blockIdx.x >= segs.tile0[i]) si = i;
+    const uint16_t* __restrict__ W = (const uint16_t*)segs.s[si].W;
+    float* __restrict__ Y = segs.s[si].Y;
+    const long long ldy = segs.s[si].ldy;
+    const int N = segs.s[si].N;
+    const int n0 = ((int)blockIdx.x - segs.tile0[si]) * RW;
+    // split K (gridDim.y > 1, one weight matrix): chunks [c0, c1) of this workgroup, partial sums
+    // to part[blockIdx.y][m][n] (the caller adds the splits in order)
+    const int nall = K / SKC, ks = blockIdx.y, nks = gridDim.y;
+    const int c0 = ks * nall / nks, c1 = (ks + 1) * nall / nks, nch = c1 - c0;
+
+    // stage loads of chunk c: this wave's WI pairs of W rows and XI kilobytes of X rows
+    auto issue = [&](int cc) {
+        const int st = cc % NS, c = c0 + cc;
+#pragma unroll
+        for (int i = 0; i < WI; i++) {
+            const int pr = wave * WI + i;             // row pair
+            const int row = 2 * pr + lane / 32, slot = (lane % 32) ^ (row & 15);
+            const int n = min(n0 + row, N - 1);
+            const uint16_t* src = W + (size_t)n * K + (size_t)c * SKC + slot * 8;
+            g2lds16(src, &sm.w[st][2 * pr][0]);
+        }
+        constexpr int XROWB = SKC * (int)sizeof(TX);   // bytes of one X row per chunk
+#pragma unroll
+        for (int i = 0; i < XI; i++) {
+            const int off = (wave * XI + i) * 1024 + lane * 16;  // byte offset in the stage's X block
+            const int m = off / XROWB, kb = off % XROWB;
+            const int mm = min(m, M - 1);
+            const unsigned char* src = (const unsigned char*)(X + (size_t)mm * ldx + (size_t)c * SKC) + kb;
+            g2lds16(src, &sm.x[st][(wave * XI + i) * 1024]);
+        }
+    };
+
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < NS - 1; c++)
+        if (c < nch) issue(c);
+    const int row = 16 * wave + r16;  // this lane's W row (A operand)
+    for (int c = 0; c < nch; c++) {
+        // chunk c's loads are done once only the later chunks' (at most NS - 2) are in flight
+        const int later = min(NS - 2, nch - 1 - c);
+        wait_vm(later * PER);
+        lds_barrier();
+        if (c + NS - 1 < nch) issue(c + NS - 1);  // into the stage chunk c - 1 used (all waves are past it)
+        const int st = c % NS;
+#pragma unroll
+        for (int i = 0; i < SKC / 32; i++) {
+            // k block i of the chunk: lane (row, g) takes slot 4 i + g of its row (swizzled)
+            const bf16x8 a = *(const bf16x8*)&sm.w[st][row][((4 * i + g) ^ (row & 15)) * 16];
+            if constexpr (sizeof(TX) == 2) {
+                const bf16x8 b = *(const bf16x8*)&sm.x[st][(r16 * SKC + 32 * i + 8 * g) * 2];
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0, 0);
+            } else {
+                const float* xp = (const float*)&sm.x[st][(r16 * SKC + 32 * i + 8 * g) * 4];
+                const f32x4 x0 = *(const f32x4*)xp, x1 = *(const f32x4*)(xp + 4);
+                uint32_t h[4], l[4];
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const float v0 = e < 2 ? x0[2 * e] : x1[2 * e - 4], v1 = e < 2 ? x0[2 * e + 1] : x1[2 * e - 3];
+                    h[e] = __builtin_amdgcn_perm(__float_as_uint(v1), __float_as_uint(v0), 0x07060302u);
+                    typedef float f2 __attribute__((ext_vector_type(2)));
+                    typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+                    const f2 lo = {v0 - __uint_as_float(__float_as_uint(v0) & 0xffff0000u),
+                                   v1 - __uint_as_float(__float_as_uint(v1) & 0xffff0000u)};
+                    l[e] = __builtin_bit_cast(uint32_t, __builtin_convertvector(lo, b2));
+                }
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, __builtin_bit_cast(bf16x8, h), acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, __builtin_bit_cast(bf16x8, l), acc, 0, 0, 0);
+            }
+        }
+    }
+    // lane (m = r16, g) holds Y[m][n0 + 16 wave + 4 g .. +3]
+    const int m = r16, nb = n0 + 16 * wave + 4 * g;
+    if (part) {
+        if (m < M && nb < N) {
+            float* pp = part + ((size_t)ks * M + m) * N + nb;
+            if (nb + 3 < N && (N % 4) == 0) {
+                *(f32x4*)pp = acc;
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+                    if (nb + j < N) pp[j] = acc[j];
+            }
+        }
+        return;
+    }
+    if (m < M && nb < N) {
+        float* yp = Y + (size_t)m * ldy + nb;
+        if (nb + 3 < N && ((uintptr_t)yp % 16) == 0) {
+            f32x4 v = acc;
+            if (accumulate) v += *(const f32x4*)yp;
+            *(f32x4*)yp = v;
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                if (nb + j < N) yp[j] = (accumulate ? yp[j] : 0.f) + acc[j];
+        }
+    }
+}
+
+template <typename TX, int NW, int NS>
+int launch_stream(const TX* X, long long ldx, ProjSegs segs, int M, int K, int accumulate, hipStream_t st,
+                  float* part = nullptr, int nks = 1) {
+    int t = 0;
+    for (int i = 0; i < segs.n; i++) {
+        segs.tile0[i] = t;
+        t += (segs.s[i].N + 16 * NW - 1) / (16 * NW);
+    }
+    segs.tile0[segs.n] = t;
+    proj_stream_kernel<TX, NW, NS><<<dim3(t, nks), 64 * NW, 0, st>>>(X, ldx, segs, M, K, accumulate, part);
+    return 0;
+}
+
 template <typename TW, typename TX, int MT, int RT, int NW>
 void launch_k(const TX* X, long long ldx, ProjSegs segs, int M, int K, int accumulate, hipStream_t st) {
     int t = 0;
@@ -323,6 +505,19 @@ void launch_mt(const TX* X, long long ldx, const ProjSegs& segs, int M, int K, i
     }
     constexpr int kTarget = PROJ_TARGET_WAVES;
 #define AEG_PROJ(RT, NW) return launch_k<TW, TX, MT, RT, NW>(X, ldx, segs, M, K, accumulate, st)
+#ifdef PROJ_CFG_ENV
+    if (const char* e = getenv("AEGIST_PROJ_CFG")) {
+        const int rt = e[0] - '0', nw = atoi(e + 2);
+        if (rt == 1 && nw == 4) AEG_PROJ(1, 4);
+        if (rt == 1 && nw == 8) AEG_PROJ(1, 8);
+        if (rt == 2 && nw == 4) AEG_PROJ(2, 4);
+        if (rt == 2 && nw == 8) AEG_PROJ(2, 8);
+        if (rt == 1 && nw == 2) AEG_PROJ(1, 2);
+        if (rt == 2 && nw == 2) AEG_PROJ(2, 2);
+        if (rt == 4 && nw == 4) AEG_PROJ(4, 4);
+        if (rt == 1 && nw == 16 && MT == 1) AEG_PROJ(1, 16);
+    }
+#endif
     if (t2 * 4 >= kTarget) AEG_PROJ(2, 4);
     if (t2 * 8 >= kTarget && nsteps >= 16) AEG_PROJ(2, 8);
     if (t1 * 4 >= kTarget) AEG_PROJ(1, 4);
@@ -338,6 +533,15 @@ void launch_mt(const TX* X, long long ldx, const ProjSegs& segs, int M, int K, i
 
 template <typename TW, typename TX>
 int run_proj(const TX* X, long long ldx, const ProjSegs& segs, int M, int K, int accumulate, hipStream_t st) {
+    // bf16 weights at M <= 16 with K a multiple of the chunk, no row scales: the LDS-staged stream
+    if constexpr (std::is_same<TW, uint16_t>::value) {
+        bool scaled = false;
+        for (int i = 0; i < segs.n; i++) scaled |= segs.s[i].scale != nullptr;
+        if (M <= 16 && K % SKC == 0 && !scaled && stream_enabled()) {
+            launch_stream<TX, 2, 3>(X, ldx, segs, M, K, accumulate, st);
+            return after_launch("proj_stream");
+        }
+    }
     // m tiles per workgroup: the whole batch up to 64 rows of bf16 X (32 of fp32 X, whose hi/lo
     // operands take twice the registers), so the weights are read once; larger M is covered by
     // a grid of row groups
@@ -384,6 +588,21 @@ int launch_proj_multi(const void* X, int x_dtype, long long ldx, int w_dtype, in
     if (w_dtype == AEGIST_BF16 && x_dtype == AEGIST_BF16)
         return run_proj<uint16_t, uint16_t>((const uint16_t*)X, ldx, segs, M, K, accumulate, st);
     return fail(AEGIST_ERR_DTYPE, "proj: W must be AEGIST_I8 or AEGIST_BF16, X AEGIST_F32 or AEGIST_BF16");
+}
+
+// Split-K form for decode sizes: part[ks][m][n] = sum over the ks-th of nks slices of K of
+// X[m, k] W[n, k] (bf16 X and W, M <= 16, K a multiple of 256 with at least nks chunks). The
+// caller adds the nks slices in order (the layer stack does it inside the next ZNorm).
+int launch_proj_splitk(const uint16_t* X, long long ldx, const uint16_t* W, float* part, int nks, int M, int N, int K,
+                       hipStream_t st) {
+    if (M < 1 || M > 16 || N < 1 || K % SKC || K / SKC < nks || nks < 1 || ldx < K || ldx % 8 || (uintptr_t)X % 16 ||
+        (uintptr_t)W % 16)
+        return fail(AEGIST_ERR_SHAPE, "proj_splitk: need M <= 16, K % 256 == 0, K / 256 >= splits, aligned rows");
+    ProjSegs segs{};
+    segs.s[0] = ProjSeg{W, nullptr, part, N, N};
+    segs.n = 1;
+    launch_stream<uint16_t, 2, 3>(X, ldx, segs, M, K, 0, st, part, nks);
+    return after_launch("proj_stream_splitk");
 }
 
 int launch_proj(const void* X, int x_dtype, long long ldx, const void* W, int w_dtype, const uint16_t* scale, float* Y,

@@ -19,6 +19,10 @@
 
 namespace aegist {
 int launch_znorm_bf16(const float* x, const uint16_t* w, uint16_t* out, int rows, int D, float eps, hipStream_t st);
+int launch_znorm_bf16_acc(float* x, const float* part, int nks, const uint16_t* w, uint16_t* out, int rows, int D,
+                          float eps, hipStream_t st);
+int launch_proj_splitk(const uint16_t* X, long long ldx, const uint16_t* W, float* part, int nks, int M, int N, int K,
+                       hipStream_t st);
 int launch_cast_bf16(const float* x, uint16_t* y, size_t n, hipStream_t st);
 int launch_gates_from_proj(const float* ba, const uint16_t* a_log, const uint16_t* dt_bias, float* g, float* beta,
                            int rows, int HV, hipStream_t st);
@@ -79,6 +83,8 @@ struct Stack {
     float* y = nullptr;        // conv out [rows, C], or attention q_n [rows, H, HD]
     float* o = nullptr;        // mixer core out [rows, max(HV 128, H HD)]
     uint16_t* ob = nullptr;    // bf16 copy of o (GEMM input)
+    float* part = nullptr;     // split-K slices of the last out projection [kOutSplits, 16, d]
+    int pend = 0;              // slices in `part` not yet added into the residual
     void* ws = nullptr;        // chunked prefill / attention decode workspace
     size_t ws_bytes = 0;
     // snapshots of the recurrent layers' conv and recurrent states (the KV cache is append-only,
@@ -117,6 +123,19 @@ int gemm(Stack* s, const uint16_t* A, const uint16_t* W, float* Y, int M, int N,
     if (st != rocblas_status_success)
         return fail(AEGIST_ERR_SHAPE, std::string("rocblas_gemm_ex: ") + rocblas_status_to_string(st));
     return after_launch("projection gemm");
+}
+
+// Out projection x += A W^T. At decode sizes (M <= 16) it runs as kOutSplits slices of K whose
+// partial sums the next layer's ZNorm (or the end of the forward) adds into x in a fixed order:
+// the d_model = 2048 rows of W alone give only 64 workgroups, a quarter of the GPU.
+constexpr int kOutSplits = 4;
+int out_proj(Stack* s, const uint16_t* A, const uint16_t* W, float* x, int M, int N, int K, hipStream_t stream) {
+    if (M <= 16 && K % 256 == 0 && K / 256 >= kOutSplits && N % 1024 == 0 && N <= 8192) {
+        int rc = launch_proj_splitk(A, K, W, s->part, kOutSplits, M, N, K, stream);
+        if (!rc) s->pend = kOutSplits;
+        return rc;
+    }
+    return gemm(s, A, W, x, M, N, K, N, 1.f, stream);
 }
 
 // The input projections of one layer (up to four weights sharing A): one grouped launch at
@@ -158,7 +177,7 @@ int delta_layer(Stack* s, const AegistLayerWeights& w, int sl, float* x, int B, 
         // one launch (hybrid.py:401-419)
         RC(launch_delta_decode_stack(s->proj, w.conv_w, conv, s->ba, w.a_log, w.dt_bias, s->z, w.gnorm_w, c.eps, rec,
                                      s->ob, B, HK, HV, qscale, 1e-6f, st));
-        return gemm(s, s->ob, w.w_out, x, rows, dm, HV * D, dm, 1.f, st);
+        return out_proj(s, s->ob, w.w_out, x, rows, dm, HV * D, st);
     }
     RC(launch_gates_from_proj(s->ba, w.a_log, w.dt_bias, s->g, s->beta, rows, HV, st));
     {
@@ -176,7 +195,7 @@ int delta_layer(Stack* s, const AegistLayerWeights& w, int sl, float* x, int B, 
                                 qscale, 1e-6f, s->ws, s->ws_bytes, st));
     }
     RC(launch_gated_norm_bf16(s->o, s->z, w.gnorm_w, s->ob, rows * HV, D, c.eps, st));
-    return gemm(s, s->ob, w.w_out, x, rows, dm, HV * D, dm, 1.f, st);
+    return out_proj(s, s->ob, w.w_out, x, rows, dm, HV * D, st);
 }
 
 int attn_layer(Stack* s, const AegistLayerWeights& w, int sl, float* x, int B, int T, hipStream_t st) {
@@ -205,7 +224,7 @@ int attn_layer(Stack* s, const AegistLayerWeights& w, int sl, float* x, int B, i
         RC(stack_attn_prefill(s->y, kc, vc, s->proj, s->o, B, H, KV, T, s->length, (int)cap, scale, st));
         RC(launch_cast_bf16(s->o, s->ob, (size_t)rows * H * HD, st));
     }
-    return gemm(s, s->ob, w.w_o, x, rows, dm, H * HD, dm, 1.f, st);
+    return out_proj(s, s->ob, w.w_o, x, rows, dm, H * HD, st);
 }
 
 }  // namespace
@@ -241,6 +260,7 @@ int aegist_stack_create(const AegistStackConfig* cfg, void** handle) {
     A((void**)&s->kc, (size_t)std::max(1, s->n_attn) * mb * KV * c.max_context * HD * 2);
     A((void**)&s->vc, (size_t)std::max(1, s->n_attn) * mb * KV * c.max_context * HD * 2);
     A((void**)&s->hb, rows * c.d_model * 2);
+    A((void**)&s->part, (size_t)kOutSplits * std::min<size_t>(rows, 16) * c.d_model * 4);
     A((void**)&s->proj, rows * std::max<size_t>(C, (size_t)2 * H * HD) * 4);
     A((void**)&s->z, rows * HV * D * 4);
     A((void**)&s->kv2, 2 * rows * KV * HD * 4);
@@ -438,11 +458,23 @@ int aegist_stack_forward(void* handle, float* x, int B, int T, void* stream) {
     hipStream_t st = AEG_STREAM(stream);
     if (rocblas_set_stream(s->blas, st) != rocblas_status_success) return fail(AEGIST_ERR_SHAPE, "rocblas_set_stream");
     const int rows = B * T;
+    s->pend = 0;
     for (int l = 0; l < c.n_layers; l++) {
         const AegistLayerWeights& w = s->w[l];
-        RC(launch_znorm_bf16(x, w.norm1, s->hb, rows, c.d_model, c.eps, st));
+        if (s->pend) {
+            const int p = s->pend;
+            s->pend = 0;
+            RC(launch_znorm_bf16_acc(x, s->part, p, w.norm1, s->hb, rows, c.d_model, c.eps, st));
+        } else {
+            RC(launch_znorm_bf16(x, w.norm1, s->hb, rows, c.d_model, c.eps, st));
+        }
         if (c.layer_is_attn[l]) RC(attn_layer(s, w, s->slot[l], x, B, T, st));
         else RC(delta_layer(s, w, s->slot[l], x, B, T, st));
+    }
+    if (s->pend) {
+        const int p = s->pend;
+        s->pend = 0;
+        RC(launch_znorm_bf16_acc(x, s->part, p, nullptr, nullptr, rows, c.d_model, c.eps, st));
     }
     s->length += T;
     return 0;
