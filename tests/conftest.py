@@ -45,3 +45,13 @@ def dev():
     if not torch.cuda.is_available():
         pytest.skip("no GPU")
     return torch.device("cuda:0")
+
+
+def perturb(x, seed: int, rel: float = 2.0 ** -20):
+    """x with every element scaled by (1 + rel u), u ~ U(-1, 1): a change far below anything a
+    kernel's arithmetic does, whose only visible effect downstream is which way the bf16 roundings
+    of the projection inputs go. Running the oracle on it measures the floor that those roundings
+    put under any comparison of two implementations that both round to bf16."""
+    import torch
+    g = torch.Generator().manual_seed(seed)
+    return x * (1 + rel * (2 * torch.rand(x.shape, generator=g, dtype=x.dtype) - 1))

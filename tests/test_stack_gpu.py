@@ -1,12 +1,20 @@
 """GPU parity of the hybrid mixer stack (config 4 composite: x = x + mixer(znorm(x)) per
 layer, MoE as identity) against the oracle composite, on a reduced shape: d_model 256, 2 QK /
 4 V DeltaNet heads, 4 / 2 attention heads (head_dim 256), 8 layers (3 DeltaNet + 1 attention,
-twice). Prefill of 100 tokens then 3 decode steps at batch 2. Both sides round the projection
-inputs to bf16; the bar for the 8-layer composite is 5e-3 (per-op bars: 1e-3 / 2e-3)."""
+twice). Prefill of 100 tokens then 3 decode steps at batch 2.
+
+Both sides round the projection inputs to bf16, and which way each rounding goes changes with
+the last bits of the fp32 value rounded; through 8 residual layers those flips compound. The
+bar is therefore measured, not set: the oracle is run a second time on the same feeds with every
+input element moved by at most 2^-20 of itself (conftest.perturb), which changes nothing but
+rounding directions, and the GPU must stay within twice that floor (norm-wise max and rms) plus
+1e-4. Measured over these feeds and the op-list test's: the floor is 1.2e-3 to 4.4e-3 and the
+GPU's distance 0.8e-3 to 4.9e-3, 0.7x to 1.5x the floor of the same feed. The single-layer and
+single-op tests hold the kernels themselves to 1e-3 / 2e-3."""
 import pytest
 import torch
 
-from conftest import rel_err
+from conftest import perturb, rel_err, rms_err
 from oracle import mixer_ref as R
 
 from aegist_mixer import ops
@@ -41,6 +49,15 @@ def make_layers(seed, dev):
     return layers, dev_layers
 
 
+def check_stack_feed(got, ref, ref_p, what):
+    """got / ref / ref_p: the feed's mixer updates (output - input) from the GPU, the oracle and the
+    oracle on the perturbed input. Bar: twice the perturbation floor, norm-wise max and rms."""
+    fmax, frms = rel_err(ref_p, ref), rms_err(ref_p, ref)
+    emax, erms = rel_err(got, ref), rms_err(got, ref)
+    print(f"{what}: max {emax:.2e} rms {erms:.2e} (floor {fmax:.2e} / {frms:.2e})", flush=True)
+    assert emax < 2 * fmax + 1e-4 and erms < 2 * frms + 1e-4, (what, emax, erms, fmax, frms)
+
+
 def test_stack_prefill_then_decode(dev):
     B, T, steps, cap = 2, 100, 3, 128
     layers, dl = make_layers(0, dev)
@@ -54,19 +71,17 @@ def test_stack_prefill_then_decode(dev):
              "v": [torch.zeros(B, c["n_kv"], cap, 256, dtype=torch.bfloat16) for _ in range(na)]}
     stack = ops.HybridStack(c, KINDS, dl, max_batch=B, max_tokens=B * T, max_context=cap)
     g_ = torch.Generator().manual_seed(1)
-    x = torch.randn(B, T, c["d_model"], generator=g_)
-    ref = R.hybrid_stack_forward(x.clone(), layers, KINDS, cache, c)
-    xd = x.to(dev)
-    stack.forward(xd)
-    torch.cuda.synchronize()
-    assert rel_err(xd - x.to(dev), ref - x) < 5e-3, rel_err(xd - x.to(dev), ref - x)
-    for s in range(steps):
-        xt = torch.randn(B, 1, c["d_model"], generator=g_)
-        ref = R.hybrid_stack_forward(xt.clone(), layers, KINDS, cache, c)
-        xdt = xt.to(dev)
-        stack.forward(xdt)
+    cache_p = {k: ([t.clone() for t in v] if isinstance(v, list) else v) for k, v in cache.items()}
+    feeds = [torch.randn(B, T, c["d_model"], generator=g_)] + [torch.randn(B, 1, c["d_model"], generator=g_)
+                                                              for _ in range(steps)]
+    for i, x in enumerate(feeds):
+        ref = R.hybrid_stack_forward(x.clone(), layers, KINDS, cache, c)
+        xp = perturb(x, 100 + i)
+        ref_p = R.hybrid_stack_forward(xp.clone(), layers, KINDS, cache_p, c)
+        xd = x.to(dev)
+        stack.forward(xd)
         torch.cuda.synchronize()
-        assert rel_err(xdt - xt.to(dev), ref - xt) < 5e-3, (s, rel_err(xdt - xt.to(dev), ref - xt))
+        check_stack_feed(xd.cpu() - x, ref - x, ref_p - xp, f"feed {i} ({x.shape[1]} tokens)")
     assert stack.length == T + steps
     stack.close()
 
@@ -104,15 +119,17 @@ def test_stack_head_ratios(dev, hk, hv):
                  "k": [torch.zeros(B, c["n_kv"], cap, 256, dtype=torch.bfloat16) for _ in range(na)],
                  "v": [torch.zeros(B, c["n_kv"], cap, 256, dtype=torch.bfloat16) for _ in range(na)]}
         stack = ops.HybridStack(c, KINDS, dl, max_batch=B, max_tokens=B * T, max_context=cap)
+        cache_p = {k: ([t.clone() for t in v] if isinstance(v, list) else v) for k, v in cache.items()}
         g_ = torch.Generator().manual_seed(6)
-        for n in [T] + [1] * steps:
+        for i, n in enumerate([T] + [1] * steps):
             x = torch.randn(B, n, c["d_model"], generator=g_)
             ref = R.hybrid_stack_forward(x.clone(), layers, KINDS, cache, c)
+            xp = perturb(x, 200 + i)
+            ref_p = R.hybrid_stack_forward(xp.clone(), layers, KINDS, cache_p, c)
             xd = x.to(dev)
             stack.forward(xd)
             torch.cuda.synchronize()
-            err = rel_err(xd - x.to(dev), ref - x)
-            assert err < 1e-2, (n, err)
+            check_stack_feed(xd.cpu() - x, ref - x, ref_p - xp, f"ratio {hv // hk} feed {i} ({n} tokens)")
         stack.close()
     finally:
         CFG = saved
