@@ -8,8 +8,8 @@
 //
 // Two kernels per segment of up to SEG tokens (a segment's workspace stays resident in the
 // MALL between the two launches). With more than one segment the workspace holds two segment
-// buffers and K1 of segment s+1 runs on a second stream while K2 of segment s runs on the
-// caller's (K2 keeps one workgroup per CU busy, K1 fills the rest of the CU):
+// buffers, and K2 of segment s and K1 of segment s+1 run as one grid (delta_chunk_fused) on the
+// caller's stream: K2's few long-lived workgroups keep part of each CU busy, K1's fill the rest.
 //  K1 delta_chunk_intra: one workgroup per (sequence, value head, chunk), fully parallel.
 //     Normalises q, k in fp32 and keeps them as fp16 in LDS; k_n k_n^T and q_n k_n^T on
 //     v_mfma_f32_16x16x32_f16 (lower-triangular blocks only); decay and beta applied in fp32 on
@@ -18,8 +18,8 @@
 //     columns (beta v | beta e^cum k_n), each wave owning 64 columns of every row (no barrier).
 //     Writes u (fp32), w (fp16), intra (fp16 hi + lo), cum, and - once per QK head - q_n and
 //     k_n^T (fp16).
-//  K2 delta_chunk_state: one workgroup per (sequence, value head, 16-column slice of S); the
-//     columns of S are independent, so 8 slices per head run in parallel, the slices of one
+//  K2 delta_chunk_state: one workgroup per (sequence, value head, 32-column slice of S); the
+//     columns of S are independent, so 4 slices per head run in parallel, the slices of one
 //     head on one XCD (they share its L2 for the chunk operands). S lives in MFMA
 //     accumulator registers (fp32) for the whole segment; each chunk it is copied to LDS as
 //     fp16 (transposed, so the B operand is a 16-byte read), then w S and q_n S, intra v_new,

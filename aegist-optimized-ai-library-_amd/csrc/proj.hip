@@ -236,13 +236,8 @@ __global__ __launch_bounds__(64 * NWAVE) void proj_skinny_kernel(const TX* __res
         const int k = step * KSTEP + 16 * g;
 #pragma unroll
         for (int rt = 0; rt < RT; rt++) wl[buf][rt].load(wrow[rt], k, K, wok[rt]);
-#ifndef PROJ_NOX
 #pragma unroll
         for (int mt = 0; mt < MT; mt++) xl[buf][mt].load(xrow[mt], k, K, xok[mt]);
-#else
-#pragma unroll
-        for (int mt = 0; mt < MT; mt++) xl[buf][mt].load(xrow[mt], 0, K, xok[mt]);
-#endif
     };
     auto compute = [&](int buf) {
         bf16x8 xa[MT], xb[MT], la[MT], lb[MT];
@@ -505,19 +500,6 @@ void launch_mt(const TX* X, long long ldx, const ProjSegs& segs, int M, int K, i
     }
     constexpr int kTarget = PROJ_TARGET_WAVES;
 #define AEG_PROJ(RT, NW) return launch_k<TW, TX, MT, RT, NW>(X, ldx, segs, M, K, accumulate, st)
-#ifdef PROJ_CFG_ENV
-    if (const char* e = getenv("AEGIST_PROJ_CFG")) {
-        const int rt = e[0] - '0', nw = atoi(e + 2);
-        if (rt == 1 && nw == 4) AEG_PROJ(1, 4);
-        if (rt == 1 && nw == 8) AEG_PROJ(1, 8);
-        if (rt == 2 && nw == 4) AEG_PROJ(2, 4);
-        if (rt == 2 && nw == 8) AEG_PROJ(2, 8);
-        if (rt == 1 && nw == 2) AEG_PROJ(1, 2);
-        if (rt == 2 && nw == 2) AEG_PROJ(2, 2);
-        if (rt == 4 && nw == 4) AEG_PROJ(4, 4);
-        if (rt == 1 && nw == 16 && MT == 1) AEG_PROJ(1, 16);
-    }
-#endif
     if (t2 * 4 >= kTarget) AEG_PROJ(2, 4);
     if (t2 * 8 >= kTarget && nsteps >= 16) AEG_PROJ(2, 8);
     if (t1 * 4 >= kTarget) AEG_PROJ(1, 4);

@@ -213,8 +213,8 @@ int aegist_attention_decode(const void* qg, const void* k_new, const void* v_new
  * (code under HIP graph capture, serving loops that forbid hipMalloc). No counterpart in the
  * reference. Its scratch is a fixed 32 MiB device array inside the library, one per GPU, held
  * until the process ends; shapes needing more (aegist_attention_decode_workspace_bytes above
- * 32 MiB: a batch of thousands of sequences) fail with AEGIST_ERR_WORKSPACE. Allocates nothing and
- * clears what it needs on the stream. All calls on one GPU share the array: calls that overlap
+ * 32 MiB: a batch of thousands of sequences) fail with AEGIST_ERR_WORKSPACE. Allocates nothing;
+ * every scratch byte a call reads it wrote earlier in the same call, so nothing is cleared. All calls on one GPU share the array: calls that overlap
  * on one GPU (two streams, two threads) race and must not be issued. */
 int aegist_attention_decode_noalloc(const void* qg, const void* k_new, const void* v_new, int in_dtype,
                                     const uint16_t* q_norm_w, const uint16_t* k_norm_w, uint16_t* kc, uint16_t* vc,
