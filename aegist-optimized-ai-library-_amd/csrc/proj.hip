@@ -314,7 +314,8 @@ __global__ __launch_bounds__(64 * NWAVE) void proj_skinny_kernel(const TX* __res
 // instruction is a direct global -> LDS copy of 1 KB of one pair of W rows (512 bytes each) and
 // the MFMA A operands are read back from LDS. Per workgroup: 16 NW rows of W (16 per wave, so
 // a wave owns whole output rows and no cross-wave reduction is needed) over all of K, in chunks
-// of KC = 256 k through an NS-stage ring; the X rows of each chunk ride in the same stage.
+// of KC = 256 k through an NS-stage ring (NS = 2 measured best: 3 to 5 stages were 2-50%
+// slower); the X rows of each chunk ride in the same stage.
 // Slots of 16 bytes in a staged row are XOR-swizzled by the row index (the global address of
 // each lane is permuted, the 1 KB it covers is not), so the 16 rows a fragment read touches
 // hit 16 different bank groups.
@@ -519,8 +520,15 @@ int run_proj(const TX* X, long long ldx, const ProjSegs& segs, int M, int K, int
     if constexpr (std::is_same<TW, uint16_t>::value) {
         bool scaled = false;
         for (int i = 0; i < segs.n; i++) scaled |= segs.s[i].scale != nullptr;
-        if (M <= 16 && K % SKC == 0 && !scaled && stream_enabled()) {
-            launch_stream<TX, 2, 3>(X, ldx, segs, M, K, accumulate, st);
+        // ... when it takes more than one workgroup per CU: at <= 256 workgroups (N <= 8192) the
+        // row-tile kernel below, with its K split over the waves of a workgroup, keeps more loads
+        // in flight (8192 x 2048: 10.9 against 11.7 us; 2048 x 4096: 10.5 against 14.9 us), and
+        // above it the row-tile kernel's 8-wave workgroups need a second round on part of the
+        // CUs (9216 x 2048: 16.3 against 12.8 us; 12352 x 2048: 16.9 against 13.3 us)
+        long long tiles = 0;
+        for (int i = 0; i < segs.n; i++) tiles += (segs.s[i].N + 31) / 32;
+        if (M <= 16 && K % SKC == 0 && !scaled && tiles > 256 && stream_enabled()) {
+            launch_stream<TX, 2, 2>(X, ldx, segs, M, K, accumulate, st);
             return after_launch("proj_stream");
         }
     }
@@ -583,7 +591,7 @@ int launch_proj_splitk(const uint16_t* X, long long ldx, const uint16_t* W, floa
     ProjSegs segs{};
     segs.s[0] = ProjSeg{W, nullptr, part, N, N};
     segs.n = 1;
-    launch_stream<uint16_t, 2, 3>(X, ldx, segs, M, K, 0, st, part, nks);
+    launch_stream<uint16_t, 2, 2>(X, ldx, segs, M, K, 0, st, part, nks);
     return after_launch("proj_stream_splitk");
 }
 

@@ -50,6 +50,27 @@ def test_linear_bf16_weight_bf16x(dev, M, N, K):
     assert rel_err(out, ref) < TOL_BF16X
 
 
+@pytest.mark.parametrize("M,N,K,xdt,acc", [(16, 12352, 2048, torch.bfloat16, False),
+                                            (1, 9216, 2048, torch.bfloat16, True),
+                                            (7, 8224, 512, torch.bfloat16, False),
+                                            (16, 8320, 768, torch.float32, True),
+                                            (3, 8200, 256, torch.float32, False)])
+def test_linear_bf16_weight_streamed(dev, M, N, K, xdt, acc):
+    """bf16 weights at M <= 16 over more than 8192 rows (K a multiple of 256) take the
+    LDS-staged stream kernel: ragged last row tiles (N not a multiple of 32), bf16 and fp32
+    activations, the residual accumulate."""
+    print(f"linear streamed M={M} N={N} K={K} x={xdt} acc={acc}", flush=True)
+    g = torch.Generator().manual_seed(M * 11 + N + K)
+    w = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16)
+    x = torch.randn(M, K, generator=g).to(xdt)
+    y0 = torch.randn(M, N, generator=g)
+    ref = R.qlinear_engine(x.float(), w.float(), None, y0.clone() if acc else None, accumulate=acc)
+    out = y0.to(dev) if acc else None
+    out = ops.linear(x.to(dev), w.to(dev), out=out, accumulate=acc)
+    torch.cuda.synchronize()
+    assert rel_err(out, ref) < (TOL_BF16X if xdt == torch.bfloat16 else TOL_F32X)
+
+
 def test_linear_accumulate_and_strides(dev):
     """Residual add into a strided Y (ldy > N) from a strided X (ldx > K), bf16 weights, fp32 X."""
     M, N, K = 9, 96, 640
@@ -113,4 +134,20 @@ def test_linear_multi_matches_separate(dev, M):
         assert rel_err(o, R.qlinear_engine(x, q, s)) < TOL_F32X
     assert outs[3].numel() == 0
     for w, o in zip(wb, outs_b):
+        assert rel_err(o, R.qlinear_engine(xb.float(), w.float(), None)) < TOL_BF16X
+
+
+def test_linear_multi_streamed_layer_group(dev):
+    """A DeltaNet layer's input group at config-4 width (in_qkv 8192, in_z 4096, in_b 32,
+    in_a 32 rows over K 2048, bf16 weights and activations, M = 16): one stream-kernel launch,
+    each output equal to the oracle per weight."""
+    print("linear_multi streamed group", flush=True)
+    g = torch.Generator().manual_seed(99)
+    K, M = 2048, 16
+    Ns = [8192, 4096, 32, 32]
+    wb = [(torch.randn(n, K, generator=g) * 0.02).to(torch.bfloat16) for n in Ns]
+    xb = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    outs = ops.linear_multi(xb.to(dev), [w.to(dev) for w in wb])
+    torch.cuda.synchronize()
+    for w, o in zip(wb, outs):
         assert rel_err(o, R.qlinear_engine(xb.float(), w.float(), None)) < TOL_BF16X
