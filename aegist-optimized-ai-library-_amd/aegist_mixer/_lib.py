@@ -56,6 +56,7 @@ SIGNATURES: dict[str, tuple] = {
     "aegist_attention_decode": (I, [P, P, P, I, P, P, P, P, P, I, I, I, I, I, I, I, I, F, F, P, SZ, P]),
     "aegist_attention_decode_noalloc": (I, [P, P, P, I, P, P, P, P, P, I, I, I, I, I, I, I, I, F, F, P]),
     "aegist_attention_core": (I, [P, P, P, P, P, I, I, I, I, I, I, F, P, SZ, P]),
+    "aegist_attention_core_workspace_bytes": (SZ, [I, I, I, I, I]),
     "aegist_stack_create": (I, [P, C.POINTER(C.c_void_p)]),
     "aegist_stack_destroy": (I, [P]),
     "aegist_stack_set_layer": (I, [P, I, P]),

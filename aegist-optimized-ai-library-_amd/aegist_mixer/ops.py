@@ -181,15 +181,18 @@ def attention_decode(qg, k_new, v_new, q_norm_w, k_norm_w, kc, vc, pos: int, rot
     return out
 
 
-def attention_core(q, kc, vc, gate, pos: int, scale: float | None = None):
+def attention_core(q, kc, vc, gate, pos: int, scale: float | None = None, f16_copy: bool = True):
     """Causal GQA attention core (hybrid.py:297-310). q [B, H, T, HD] fp32 (normed and roped);
     caches [B, KV, cap, HD] bf16 holding rows [0, pos + T); gate [B, T, H*HD] fp32 or None.
-    Returns [B, T, H, HD] fp32 (gated when gate is given)."""
+    Returns [B, T, H, HD] fp32 (gated when gate is given). For T > 1, f16_copy=False withholds
+    the workspace of the fp16 cache copy (the kernel then converts its tiles as it stages them)."""
     B, H, T, HD = q.shape
     KV, cap = kc.shape[1], kc.shape[2]
     _need_contig(q, kc, vc, gate)
     out = torch.empty(B, T, H, HD, dtype=torch.float32, device=q.device)
     nbytes = lib().aegist_attention_decode_workspace_bytes(B, H, KV, pos + 1)
+    if T > 1 and f16_copy:
+        nbytes = max(nbytes, lib().aegist_attention_core_workspace_bytes(B, H, KV, T, pos))
     ws = _workspace(nbytes, q.device)
     sc = HD ** -0.5 if scale is None else scale
     call("aegist_attention_core", _p(q), _p(kc), _p(vc), _p(gate), _p(out), B, H, KV, T, pos, cap, sc, _p(ws),

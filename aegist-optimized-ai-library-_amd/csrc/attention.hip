@@ -464,9 +464,10 @@ __global__ void __launch_bounds__(256) attn_prefill_simple_kernel(const float* _
 }
 
 // ---------------------------------------------------------------------------------------------
-// Causal flash prefill on v_mfma_f32_16x16x32_bf16. One workgroup of 8 waves per (sequence,
-// query head, 128 queries); wave w owns queries [16w, 16w + 16). Key tiles of 64 rows: K and V
-// are staged in LDS as the cache's own bf16 rows (a plain copy, no conversion).
+// Causal flash prefill on v_mfma_f32_16x16x32_f16, 16 queries per wave. One workgroup of 8 waves
+// per (sequence, query head, 128 queries); wave w owns queries [16w, 16w + 16). Key tiles of 64
+// rows. The 32-query kernels further down replace it; it serves the caches whose rows of one
+// (sequence, KV head) pass 2 GiB (their buffer ranges are 32-bit) and A/B builds.
 //
 // Everything is computed transposed, so that a lane owns one query throughout:
 //   S^T = K q^T     (A = K rows from LDS, B = q): lane (n, g) holds query n's scores for keys
@@ -477,8 +478,8 @@ __global__ void __launch_bounds__(256) attn_prefill_simple_kernel(const float* _
 // registers hold them (lane group g: keys 4 g .. 4 g + 3 of block 2 ks, then of block 2 ks + 1);
 // the V operand reads the same keys (ds_read_b64_tr_b16 hands lane j four consecutive keys of
 // one dim), so P never goes through LDS and the online-softmax statistics of a query live in
-// the four lanes n, n + 16, n + 32, n + 48 (max: two cross-group shuffles; sum: kept per lane,
-// reduced once at the end).
+// the four lanes n, n + 16, n + 32, n + 48 (max: two lane swaps; sum: kept per lane, reduced
+// once at the end).
 //
 // K and V tiles are converted to fp16 as they are staged into LDS (exact for bf16 values in
 // fp16's range), so q * scale and the probabilities enter as single fp16 operands (11
@@ -486,10 +487,15 @@ __global__ void __launch_bounds__(256) attn_prefill_simple_kernel(const float* _
 // the accumulators are rescaled only when some query's running maximum moved; the causal mask
 // is applied only on tiles that reach past a wave's first query; output * sigmoid(gate). A
 // wave whose queries cannot see any key of a tile skips it.
-#ifndef PREFILL_PQ
-#define PREFILL_PQ 128
+// compile-time switches for A/B builds: PREFILL_W32 = 0 keeps every prefill on the 16-query
+// kernel below, PREFILL_F16 = 0 ignores the workspace for the fp16 cache copy
+#ifndef PREFILL_F16
+#define PREFILL_F16 1
 #endif
-constexpr int PQ = PREFILL_PQ, PK = 64;  // queries per workgroup, keys per tile
+#ifndef PREFILL_W32
+#define PREFILL_W32 1
+#endif
+constexpr int PQ = 128, PK = 64;  // queries per workgroup, keys per tile
 constexpr int PW = PQ / 16;              // waves per workgroup
 // LDS row strides (bf16 elements). K: 132 words = 4 mod 64 banks, so the 16 rows a 16-lane
 // group reads with 16-byte loads cover all 64 banks. V: 136 words = 8 mod 64 banks: a transpose
@@ -517,6 +523,22 @@ __device__ __forceinline__ u32x4 bf8_to_f16(u32x4 x) {
     return r;
 }
 
+// max / sum over the four lanes n, n + 16, n + 32, n + 48 of a wave (its lane groups) by VALU
+// lane swaps; a shuffle would be an LDS permute, whose wait also drains every LDS read in flight.
+// Both halves of a swap pair combine in the same order, so every lane gets the same sum.
+__device__ __forceinline__ float group4_max(float x) {
+    const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto c = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(c[0]), __uint_as_float(c[1]));
+}
+__device__ __forceinline__ float group4_sum(float x) {
+    const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto c = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(c[0]) + __uint_as_float(c[1]);
+}
+
 __device__ __forceinline__ bf16x8 vt_operand(const uint16_t* vt, int ks, int db, int lane) {
     const int g = lane / 16, k = lane % 16;
     const uint16_t* p = vt + (size_t)(32 * ks + 4 * g + (k >> 2)) * VLD + 16 * db + 4 * (k & 3);
@@ -526,7 +548,7 @@ __device__ __forceinline__ bf16x8 vt_operand(const uint16_t* vt, int ks, int db,
     return bf16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
 }
 
-__global__ void __launch_bounds__(64 * PW) attn_prefill_mfma_kernel(const float* __restrict__ q, Strides3 qs,
+__global__ void __launch_bounds__(64 * PW, 8 / PW) attn_prefill_mfma_kernel(const float* __restrict__ q, Strides3 qs,
                                                                      const uint16_t* __restrict__ kc,
                                                                      const uint16_t* __restrict__ vc,
                                                                      const float* __restrict__ gate, Strides3 gs,
@@ -638,22 +660,17 @@ __global__ void __launch_bounds__(64 * PW) attn_prefill_mfma_kernel(const float*
                 for (int j = 0; j < 4; j++)
                     if (key0 + 16 * nb + 4 * g + j > qpos) sc[nb][j] = -INFINITY;
         }
-        // ---- online softmax for query n (its 64 keys over this lane's 16 and lanes n + 16 g)
         float mt = sc[0][0];
 #pragma unroll
         for (int nb = 0; nb < 4; nb++)
 #pragma unroll
             for (int j = 0; j < 4; j++) mt = fmaxf(mt, sc[nb][j]);
-        mt = fmaxf(mt, __shfl_xor(mt, 16, WAVE));
-        mt = fmaxf(mt, __shfl_xor(mt, 32, WAVE));
+        mt = group4_max(mt);
         const float mn = fmaxf(m_run, mt);
-        // a query with no visible key yet keeps m = -inf: use 0 as the reference so exp2() is 0
         const float ref = mn == -INFINITY ? 0.f : mn;
         const float corr = exp2f(m_run - ref);
         const bool moved = mn != m_run;
         m_run = mn;
-        // P^T operand of step ks: keys 4 g + e of block 2 ks (e < 4), then of block 2 ks + 1, as
-        // fp16 (p in [0, 1]: 11 significant bits); the row sum takes the fp32 values
         half8 pf[2];
         float ps = 0.f;
 #pragma unroll
@@ -661,7 +678,6 @@ __global__ void __launch_bounds__(64 * PW) attn_prefill_mfma_kernel(const float*
 #pragma unroll
             for (int e = 0; e < 8; e++) {
                 const int nb = 2 * ks + (e >> 2), j = e & 3;
-                // arguments <= 0 (or -inf): the hardware exp2 needs no range fix-up here
                 const float p = __builtin_amdgcn_exp2f(sc[nb][j] - ref);
                 ps += p;
                 pf[ks][e] = (_Float16)p;
@@ -673,7 +689,6 @@ __global__ void __launch_bounds__(64 * PW) attn_prefill_mfma_kernel(const float*
 #pragma unroll
                 for (int j = 0; j < 4; j++) oacc[i][j] *= corr;
         }
-        // ---- O^T += V^T P^T (16 dim blocks, 64 keys in 2 steps)
 #pragma unroll
         for (int db = 0; db < 16; db++)
 #pragma unroll
@@ -685,27 +700,654 @@ __global__ void __launch_bounds__(64 * PW) attn_prefill_mfma_kernel(const float*
         __syncthreads();  // tile kt + 1 staged by every wave; tile kt's reads done
     }
     // ---- normalise, gate, store: lane holds query n, dims 16 db + 4 g .. +4
-    float l = l_part;
-    l += __shfl_xor(l, 16, WAVE);
-    l += __shfl_xor(l, 32, WAVE);
+    const float l = group4_sum(l_part);
+    // all sixteen gate loads are issued together (from a clamped row for queries past T, whose
+    // stores are skipped): written per dim block behind the gate test, they had been issued and
+    // waited for one at a time, ~13 us per workgroup at B = 16
     const int t = q0 + 16 * wave + n;
-    if (t >= T) return;
-    float* orow = out + b * os.b + (long long)t * os.t + h * os.h;
-    const float* grow = gate ? gate + b * gs.b + (long long)t * gs.t + h * gs.h : nullptr;
+    const int tc = min(t, T - 1);
+    f32x4 gf[16];
+    if (gate) {
+        const float* grow = gate + b * gs.b + (long long)tc * gs.t + h * gs.h;
+#pragma unroll
+        for (int db = 0; db < 16; db++) gf[db] = *(const f32x4*)(grow + 16 * db + 4 * g);
+#pragma unroll
+        for (int db = 0; db < 16; db++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) gf[db][j] = sigmoid_f(gf[db][j]);
+    } else {
+#pragma unroll
+        for (int db = 0; db < 16; db++) gf[db] = f32x4{1.f, 1.f, 1.f, 1.f};
+    }
+    float* orow = out + b * os.b + (long long)tc * os.t + h * os.h;
     const float inv = 1.f / l;
+    if (t < T) {
 #pragma unroll
-    for (int db = 0; db < 16; db++) {
-        float y[4];
-#pragma unroll
-        for (int j = 0; j < 4; j++) y[j] = oacc[db][j] * inv;
-        if (grow) {
-            const float4 gv = *(const float4*)(grow + 16 * db + 4 * g);
-            y[0] *= sigmoid_f(gv.x);
-            y[1] *= sigmoid_f(gv.y);
-            y[2] *= sigmoid_f(gv.z);
-            y[3] *= sigmoid_f(gv.w);
+        for (int db = 0; db < 16; db++) {
+            const f32x4 y = oacc[db] * inv * gf[db];
+            *(float4*)(orow + 16 * db + 4 * g) = float4{y[0], y[1], y[2], y[3]};
         }
-        *(float4*)(orow + 16 * db + 4 * g) = float4{y[0], y[1], y[2], y[3]};
+    }
+}
+
+
+// ---------------------------------------------------------------------------------------------
+// Causal prefill with 32 queries per wave: 4 waves x 32 queries = 128 queries per workgroup,
+// one wave per SIMD (up to 512 registers: the 2 x 16 output tiles live in accumulators). Each K
+// fragment and each V^T fragment read from LDS feeds two products (one per 16-query tile), half
+// the LDS bytes per FLOP of the 16-query layout. One wave per SIMD leaves no other wave to fill
+// the matrix pipe while a wave runs its softmax or stages tiles, so the loop is software-
+// pipelined across tiles and the order of each iteration is fixed by scheduling fences:
+//   phase 1: S^T of tile t + 1 (64 products), between them the fp16 staging of V tile t + 1 into
+//            the other V buffer and the requests of K tile t + 2;
+//   phase 2: O^T += V^T P^T of tile t (64 products), between them the softmax of tile t + 1, the
+//            staging of K tile t + 2 into the K buffer tile t used and the requests of V t + 2;
+//   barrier.
+// K runs a tile ahead of V: iteration t reads K(t + 1) and V(t), writes K(t + 2) and V(t + 1).
+// Both buffers written in an iteration were last read before the barrier that ended the
+// previous one. The softmax reference is lazy: it moves only when a query's tile maximum exceeds
+// it by more than 2^8, so probabilities stay <= 2^8 (exact range for fp16) and the accumulators
+// are rescaled rarely - at the start of the next iteration, after P V of the tile that used the
+// old reference. All four waves run every tile of their block; a tile none of a wave's queries
+// sees gets fully masked (probabilities 0), which keeps the control flow uniform.
+constexpr int WQ = 32, PQ2 = 128, PW2 = PQ2 / WQ;
+constexpr int NST2 = (PK * HD) / (8 * 64 * PW2);  // 16-byte chunks per thread per tile (K; V alike)
+constexpr int RST2 = 64 * PW2 / (HD / 8);         // key rows between a thread's chunks
+constexpr float kLazyRef = 8.f;                    // log2 units
+constexpr int kBufWord3 = 0x00020000;              // buffer resource word 3 on gfx9: 32-bit data, no swizzle
+
+__global__ void __launch_bounds__(64 * PW2, 1) attn_prefill_w32_kernel(const float* __restrict__ q, Strides3 qs,
+                                                                       const uint16_t* __restrict__ kc,
+                                                                       const uint16_t* __restrict__ vc,
+                                                                       const float* __restrict__ gate, Strides3 gs,
+                                                                       float* __restrict__ out, Strides3 os, int H,
+                                                                       int KV, int T, int pos, int cap, float scale,
+                                                                       int B, int per_xcd) {
+    __shared__ __attribute__((aligned(16))) uint16_t Kt2[2][PK * KLD];
+    __shared__ __attribute__((aligned(16))) uint16_t Vt2[2][PK * VLD];
+
+    // same XCD-aware block order as attn_prefill_mfma_kernel
+    const int nqb = (T + PQ2 - 1) / PQ2, G = H / KV;
+    const int li = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+    if (li >= nqb * H * B) return;
+    const int qb = nqb - 1 - li % nqb, hh = (li / nqb) % G, kvh = (li / (nqb * G)) % KV, b = li / (nqb * H);
+    const int h = kvh * G + hh;
+    const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE, n = lane % 16, g = lane / 16;
+    const int q0 = qb * PQ2;
+    const uint16_t* kbase = kc + ((size_t)b * KV + kvh) * (size_t)cap * HD;
+    const uint16_t* vbase = vc + ((size_t)b * KV + kvh) * (size_t)cap * HD;
+    const int last_key = pos + min(q0 + PQ2, T) - 1;
+    const int ntiles = last_key / PK + 1;
+    const int wave_first = pos + q0 + WQ * wave;  // keys up to here need no mask
+
+    // staging: chunk it of a thread is key row r_own + it RST2, dims c_own .. +7, read by raw
+    // buffer loads whose range ends at the block's last key (rows past it, and tiles past the
+    // last, read as zeros: those keys are masked for every query of the block)
+    const int r_own = tid / (HD / 8), c_own = (tid % (HD / 8)) * 8;
+    const int voff = (r_own * HD + c_own) * 2;
+    const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc((void*)kbase, (short)0, (last_key + 1) * HD * 2,
+                                                                       kBufWord3);
+    const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc((void*)vbase, (short)0, (last_key + 1) * HD * 2,
+                                                                       kBufWord3);
+    auto kload = [&](int t, int it) {
+        return __builtin_amdgcn_raw_buffer_load_b128(krs, voff, (t * PK + it * RST2) * HD * 2, 0);
+    };
+    auto vload = [&](int t, int it) {
+        return __builtin_amdgcn_raw_buffer_load_b128(vrs, voff, (t * PK + it * RST2) * HD * 2, 0);
+    };
+    u32x4 kreg[NST2], vreg[NST2];
+#pragma unroll
+    for (int it = 0; it < NST2; it++) {
+        kreg[it] = kload(0, it);
+        vreg[it] = vload(0, it);
+    }
+
+    // q operands: tile qt = query q0 + 32 wave + 16 qt + n, dims 32 ks + 8 g .. +8, scaled into
+    // the log2 domain, fp16
+    half8 qf[2][8];
+    int qpos[2];
+#pragma unroll
+    for (int qt = 0; qt < 2; qt++) {
+        const int tq = q0 + WQ * wave + 16 * qt + n;
+        qpos[qt] = pos + tq;
+        const float* qr = q + b * qs.b + (long long)min(tq, T - 1) * qs.t + h * qs.h;
+        const float sl = scale * 1.4426950408889634f;
+#pragma unroll
+        for (int ks = 0; ks < 8; ks++) {
+            const float4 a0 = *(const float4*)(qr + 32 * ks + 8 * g);
+            const float4 a1 = *(const float4*)(qr + 32 * ks + 8 * g + 4);
+            qf[qt][ks] = half8{(_Float16)(a0.x * sl), (_Float16)(a0.y * sl), (_Float16)(a0.z * sl),
+                               (_Float16)(a0.w * sl), (_Float16)(a1.x * sl), (_Float16)(a1.y * sl),
+                               (_Float16)(a1.z * sl), (_Float16)(a1.w * sl)};
+        }
+    }
+
+    auto kdst = [&](int buf, int it) { return (u32x4*)&Kt2[buf][(r_own + it * RST2) * KLD + c_own]; };
+    auto vdst = [&](int buf, int it) { return (u32x4*)&Vt2[buf][(r_own + it * RST2) * VLD + c_own]; };
+    // tile 0 into buffers 0 and K(1) into K buffer 1; V(1) requested into the staging registers
+    // (one set serves both tensors in the loop: V(t + 1) arrives there during the previous
+    // iteration's P V phase and is converted in the S phase, which then requests K(t + 2) into
+    // the same registers for the P V phase to convert)
+#pragma unroll
+    for (int it = 0; it < NST2; it++) {
+        *kdst(0, it) = bf8_to_f16(kreg[it]);
+        *vdst(0, it) = bf8_to_f16(vreg[it]);
+    }
+#pragma unroll
+    for (int it = 0; it < NST2; it++) kreg[it] = kload(1, it);
+#pragma unroll
+    for (int it = 0; it < NST2; it++) *kdst(1, it) = bf8_to_f16(kreg[it]);
+    u32x4 sreg[NST2];
+#pragma unroll
+    for (int it = 0; it < NST2; it++) sreg[it] = vload(1, it);
+    __syncthreads();
+
+    // S^T of the tile in K buffer kb_: sc[qt][nb][j] = score of key 16 nb + 4 g + j for query
+    // tile qt. Dim step outer; K fragments two steps ahead through a 3-deep ring; `side(ks)` runs
+    // after the products of step ks (its work is fenced into that step).
+    f32x4 sc[2][4];
+    auto scores = [&](const uint16_t* Kt, auto side) {
+        half8 kb[3][4];
+#pragma unroll
+        for (int nb = 0; nb < 4; nb++) {
+            kb[0][nb] = *(const half8*)&Kt[(16 * nb + n) * KLD + 8 * g];
+            kb[1][nb] = *(const half8*)&Kt[(16 * nb + n) * KLD + 32 + 8 * g];
+#pragma unroll
+            for (int qt = 0; qt < 2; qt++) sc[qt][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+#pragma unroll
+        for (int ks = 0; ks < 8; ks++) {
+#pragma unroll
+            for (int nb = 0; nb < 4; nb++)
+#pragma unroll
+                for (int qt = 0; qt < 2; qt++)
+                    sc[qt][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kb[ks % 3][nb], qf[qt][ks], sc[qt][nb], 0, 0, 0);
+            if (ks + 2 < 8) {
+#pragma unroll
+                for (int nb = 0; nb < 4; nb++)
+                    kb[(ks + 2) % 3][nb] = *(const half8*)&Kt[(16 * nb + n) * KLD + 32 * (ks + 2) + 8 * g];
+            }
+            side(ks);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    auto mask = [&](int key0) {
+        if (key0 + PK - 1 > wave_first) {
+#pragma unroll
+            for (int qt = 0; qt < 2; qt++)
+#pragma unroll
+                for (int nb = 0; nb < 4; nb++)
+#pragma unroll
+                    for (int j = 0; j < 4; j++)
+                        if (key0 + 16 * nb + 4 * g + j > qpos[qt]) sc[qt][nb][j] = -INFINITY;
+        }
+    };
+
+    // softmax state per query tile: lazy reference, this lane's share of the row sum
+    float ref[2] = {-INFINITY, -INFINITY}, lsum[2] = {0.f, 0.f}, corr[2] = {1.f, 1.f}, mt[2];
+    half8 pcur[2][2], pnext[2][2];
+    bool pend = false;
+    // softmax of the scores in sc, in pieces (so they can be spread between products):
+    // piece 0 / 1: tile maximum of query tile 0 / 1; 2: cross-lane max; 3: reference update;
+    // 4 .. 11: probabilities of 4 scores each (p = 2^(s - ref)); 12: pending-rescale flag
+    auto softmax_piece = [&](int piece) {
+        if (piece < 2) {
+            const int qt = piece;
+            float m = sc[qt][0][0];
+#pragma unroll
+            for (int nb = 0; nb < 4; nb++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) m = fmaxf(m, sc[qt][nb][j]);
+            mt[qt] = m;
+        } else if (piece == 2) {
+#pragma unroll
+            for (int qt = 0; qt < 2; qt++) mt[qt] = group4_max(mt[qt]);
+        } else if (piece == 3) {
+            bool need_any = false;
+#pragma unroll
+            for (int qt = 0; qt < 2; qt++) {
+                const bool need = mt[qt] > ref[qt] + kLazyRef;  // -inf tile maxima never move it
+                corr[qt] = need ? exp2f(ref[qt] - mt[qt]) : 1.f;
+                lsum[qt] *= corr[qt];
+                ref[qt] = need ? mt[qt] : ref[qt];
+                need_any |= need;
+            }
+            pend = __ballot(need_any) != 0;
+        } else if (piece < 12) {
+            const int e4 = piece - 4;  // scores 4 e4 .. 4 e4 + 3 of the 32: qt = e4 / 4, nb = e4 % 4
+            const int qt = e4 >> 2, nb = e4 & 3;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const float p = __builtin_amdgcn_exp2f(sc[qt][nb][j] - ref[qt]);
+                lsum[qt] += p;
+                // P^T operand of step ks = nb / 2: element 4 (nb % 2) + j
+                pnext[qt][nb >> 1][4 * (nb & 1) + j] = (_Float16)p;
+            }
+        }
+    };
+    f32x4 oacc[2][16];
+#pragma unroll
+    for (int qt = 0; qt < 2; qt++)
+#pragma unroll
+        for (int db = 0; db < 16; db++) oacc[qt][db] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    // tile 0: S, mask, softmax (the accumulators are zero: nothing to rescale)
+    scores(Kt2[0], [&](int) {});
+    mask(0);
+#pragma unroll
+    for (int piece = 0; piece < 12; piece++) softmax_piece(piece);
+    pend = false;
+#pragma unroll
+    for (int qt = 0; qt < 2; qt++) {
+        pcur[qt][0] = pnext[qt][0];
+        pcur[qt][1] = pnext[qt][1];
+    }
+    __syncthreads();
+
+    // O^T += V^T P^T from V buffer Vt with pcur: 16 dim blocks of 4 products; V^T fragments three
+    // blocks ahead through a 4-deep ring; `side(db)` runs after the products of block db
+    auto pv = [&](const uint16_t* Vt, auto side) {
+        bf16x8 vb[4][2];
+#pragma unroll
+        for (int d = 0; d < 3; d++) {
+            vb[d][0] = vt_operand(Vt, 0, d, lane);
+            vb[d][1] = vt_operand(Vt, 1, d, lane);
+        }
+#pragma unroll
+        for (int db = 0; db < 16; db++) {
+            if (db + 3 < 16) {
+                vb[(db + 3) & 3][0] = vt_operand(Vt, 0, db + 3, lane);
+                vb[(db + 3) & 3][1] = vt_operand(Vt, 1, db + 3, lane);
+            }
+#pragma unroll
+            for (int ks = 0; ks < 2; ks++)  // the two products into one accumulator are not adjacent
+#pragma unroll
+                for (int qt = 0; qt < 2; qt++)
+                    oacc[qt][db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, vb[db & 3][ks]),
+                                                                          pcur[qt][ks], oacc[qt][db], 0, 0, 0);
+            side(db);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    auto rescale = [&]() {
+        if (pend) {
+#pragma unroll
+            for (int qt = 0; qt < 2; qt++)
+#pragma unroll
+                for (int db = 0; db < 16; db++) oacc[qt][db] *= corr[qt];
+        }
+        pend = false;
+    };
+
+    for (int t = 0; t + 1 < ntiles; t++) {
+        const int b1 = (t + 1) & 1, b0 = t & 1;
+        // ---- phase 1: accumulators rescaled for tile t's reference; S^T of tile t + 1, with
+        // V(t + 1) staged (chunk ks) and K(t + 2) requested (chunk ks) between the products
+        rescale();
+        scores(Kt2[b1], [&](int ks) {
+            *vdst(b1, ks) = bf8_to_f16(sreg[ks]);
+            sreg[ks] = kload(t + 2, ks);
+        });
+        mask((t + 1) * PK);
+        // ---- phase 2: P V of tile t; the softmax of tile t + 1 over blocks 0 .. 11, K(t + 2)
+        // staged and V(t + 2) requested over blocks 8 .. 15
+        pv(Vt2[b0], [&](int db) {
+            if (db < 12) softmax_piece(db);
+            if (db >= 8) {
+                const int it = db - 8;
+                *kdst(b0, it) = bf8_to_f16(sreg[it]);
+                sreg[it] = vload(t + 2, it);
+            }
+        });
+#pragma unroll
+        for (int qt = 0; qt < 2; qt++) {
+            pcur[qt][0] = pnext[qt][0];
+            pcur[qt][1] = pnext[qt][1];
+        }
+        __syncthreads();
+    }
+    rescale();
+    pv(Vt2[(ntiles - 1) & 1], [&](int) {});
+
+    // ---- normalise, gate, store: lane holds query tile qt's query n, dims 16 db + 4 g .. +3;
+    // all gate loads of a query tile issued together (clamped rows past T, stores skipped)
+#pragma unroll
+    for (int qt = 0; qt < 2; qt++) {
+        const float l = group4_sum(lsum[qt]);
+        const int tq = q0 + WQ * wave + 16 * qt + n;
+        const int tc = min(tq, T - 1);
+        f32x4 gf[16];
+        if (gate) {
+            const float* grow = gate + b * gs.b + (long long)tc * gs.t + h * gs.h;
+#pragma unroll
+            for (int db = 0; db < 16; db++) gf[db] = *(const f32x4*)(grow + 16 * db + 4 * g);
+#pragma unroll
+            for (int db = 0; db < 16; db++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) gf[db][j] = sigmoid_f(gf[db][j]);
+        } else {
+#pragma unroll
+            for (int db = 0; db < 16; db++) gf[db] = f32x4{1.f, 1.f, 1.f, 1.f};
+        }
+        float* orow = out + b * os.b + (long long)tc * os.t + h * os.h;
+        const float inv = 1.f / l;
+        if (tq < T) {
+#pragma unroll
+            for (int db = 0; db < 16; db++) {
+                const f32x4 y = oacc[qt][db] * inv * gf[db];
+                *(float4*)(orow + 16 * db + 4 * g) = float4{y[0], y[1], y[2], y[3]};
+            }
+        }
+    }
+}
+
+
+// ---------------------------------------------------------------------------------------------
+// fp16 copies of the K / V cache rows [0, rows) of every (sequence, KV head), rows padded to a
+// whole tile with zeros: dst [B][KV][rows_pad][HD]. bf16 -> fp16 is exact for the values the
+// normed keys and projected values hold (8-bit significand into 11). Converting once here
+// replaces the per-tile conversion that every query block of every query head would repeat.
+__global__ void attn_kv_f16_kernel(const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc,
+                                   uint16_t* __restrict__ kf, uint16_t* __restrict__ vf, int KV, int cap, int rows,
+                                   int rows_pad, long long nchunks) {
+    for (long long c = blockIdx.x * (long long)blockDim.x + threadIdx.x; c < nchunks;
+         c += (long long)gridDim.x * blockDim.x) {
+        const long long e = c * 8;                       // element offset in dst (one tensor)
+        const long long bkv = e / ((long long)rows_pad * HD);
+        const int r = (int)((e / HD) % rows_pad), d = (int)(e % HD);
+        u32x4 ko = {0u, 0u, 0u, 0u}, vo = {0u, 0u, 0u, 0u};
+        if (r < rows) {
+            const size_t src = ((size_t)bkv * cap + r) * HD + d;
+            ko = bf8_to_f16(*(const u32x4*)(kc + src));
+            vo = bf8_to_f16(*(const u32x4*)(vc + src));
+        }
+        *(u32x4*)(kf + e) = ko;
+        *(u32x4*)(vf + e) = vo;
+    }
+}
+
+// The 32-query kernel fed from the fp16 copies: every tile arrives in LDS by direct buffer ->
+// LDS loads (1 KB = two key rows per instruction, no registers, no conversion), issued at the
+// start of the S phase and waited for before the iteration's barrier. LDS rows are unpadded
+// (512 bytes); 16-byte slots are XOR-swizzled by the row (K: slot ^ (row & 15), V: slot ^
+// 2 (row & 15)) through the global address each lane fetches, so the K fragment reads (16 rows,
+// one slot each) and the V^T transpose reads (4 rows x 2 slots per 16 lanes) hit distinct banks.
+// The loop is unrolled by two so that each buffer is its own array and the compiler can tell the
+// direct loads into one buffer from the reads of the other.
+constexpr int KSW = 1, VSW = 2;  // swizzle multipliers of (row & 15)
+
+__device__ __forceinline__ int sw_slot(int slot, int row, int mul) { return slot ^ ((row & 15) * mul); }
+
+__device__ __forceinline__ bf16x8 vt_operand_sw(const uint16_t* vt, int ks, int db, int lane) {
+    const int g = lane / 16, k = lane % 16;
+    const int r0 = 32 * ks + 4 * g + (k >> 2), r1 = r0 + 16;
+    const int gs = 2 * db + ((k & 3) >> 1), within = (k & 1) * 4;
+    typedef __attribute__((address_space(3))) short4v lds_short4;
+    const short4v a = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (lds_short4*)(vt + r0 * HD + sw_slot(gs, r0, VSW) * 8 + within));
+    const short4v b = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (lds_short4*)(vt + r1 * HD + sw_slot(gs, r1, VSW) * 8 + within));
+    return bf16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+}
+
+__global__ void __launch_bounds__(64 * PW2, 1) attn_prefill_w32f_kernel(const float* __restrict__ q, Strides3 qs,
+                                                                        const uint16_t* __restrict__ kf,
+                                                                        const uint16_t* __restrict__ vf, int rows_pad,
+                                                                        const float* __restrict__ gate, Strides3 gs,
+                                                                        float* __restrict__ out, Strides3 os, int H,
+                                                                        int KV, int T, int pos, float scale, int B,
+                                                                        int per_xcd) {
+    __shared__ __attribute__((aligned(1024))) uint16_t K0[PK * HD];
+    __shared__ __attribute__((aligned(1024))) uint16_t K1[PK * HD];
+    __shared__ __attribute__((aligned(1024))) uint16_t V0[PK * HD];
+    __shared__ __attribute__((aligned(1024))) uint16_t V1[PK * HD];
+
+    const int nqb = (T + PQ2 - 1) / PQ2, G = H / KV;
+    const int li = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+    if (li >= nqb * H * B) return;
+    const int qb = nqb - 1 - li % nqb, hh = (li / nqb) % G, kvh = (li / (nqb * G)) % KV, b = li / (nqb * H);
+    const int h = kvh * G + hh;
+    const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE, n = lane % 16, g = lane / 16;
+    const int q0 = qb * PQ2;
+    const size_t base = ((size_t)b * KV + kvh) * (size_t)rows_pad * HD;
+    const int last_key = pos + min(q0 + PQ2, T) - 1;
+    const int ntiles = last_key / PK + 1;
+    const int wave_first = pos + q0 + WQ * wave;
+
+    // direct loads: instruction i of this wave fills key rows 2 j, 2 j + 1 (j = 8 wave + i) of a
+    // tile; lane L writes LDS slot L % 32 of row 2 j + L / 32 with global slot (L % 32) ^ swizzle
+    const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc((void*)(kf + base), (short)0,
+                                                                       rows_pad * HD * 2, kBufWord3);
+    const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc((void*)(vf + base), (short)0,
+                                                                       rows_pad * HD * 2, kBufWord3);
+    int koff[8], voff[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const int row = 2 * (8 * wave + i) + lane / 32, s = lane % 32;
+        koff[i] = (row * HD + sw_slot(s, row, KSW) * 8) * 2;
+        voff[i] = (row * HD + sw_slot(s, row, VSW) * 8) * 2;
+    }
+    typedef __attribute__((address_space(3))) void lds_void;
+    auto load_k = [&](uint16_t* dst, int t) {
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (lds_void*)(dst + (8 * wave + i) * 2 * HD), 16, koff[i],
+                                                     t * PK * HD * 2, 0, 0);
+    };
+    auto load_v = [&](uint16_t* dst, int t) {
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (lds_void*)(dst + (8 * wave + i) * 2 * HD), 16, voff[i],
+                                                     t * PK * HD * 2, 0, 0);
+    };
+    load_k(K0, 0);
+    load_v(V0, 0);
+    if (ntiles > 1) load_k(K1, 1);
+
+    half8 qf[2][8];
+    int qpos[2];
+#pragma unroll
+    for (int qt = 0; qt < 2; qt++) {
+        const int tq = q0 + WQ * wave + 16 * qt + n;
+        qpos[qt] = pos + tq;
+        const float* qr = q + b * qs.b + (long long)min(tq, T - 1) * qs.t + h * qs.h;
+        const float sl = scale * 1.4426950408889634f;
+#pragma unroll
+        for (int ks = 0; ks < 8; ks++) {
+            const float4 a0 = *(const float4*)(qr + 32 * ks + 8 * g);
+            const float4 a1 = *(const float4*)(qr + 32 * ks + 8 * g + 4);
+            qf[qt][ks] = half8{(_Float16)(a0.x * sl), (_Float16)(a0.y * sl), (_Float16)(a0.z * sl),
+                               (_Float16)(a0.w * sl), (_Float16)(a1.x * sl), (_Float16)(a1.y * sl),
+                               (_Float16)(a1.z * sl), (_Float16)(a1.w * sl)};
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+
+    f32x4 sc[2][4];
+    auto scores = [&](const uint16_t* Kt) {
+        half8 kb[3][4];
+        auto kaddr = [&](int nb, int ks) {
+            const int row = 16 * nb + n;
+            return (const half8*)&Kt[row * HD + sw_slot(4 * ks + g, row, KSW) * 8];
+        };
+#pragma unroll
+        for (int nb = 0; nb < 4; nb++) {
+            kb[0][nb] = *kaddr(nb, 0);
+            kb[1][nb] = *kaddr(nb, 1);
+#pragma unroll
+            for (int qt = 0; qt < 2; qt++) sc[qt][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+#pragma unroll
+        for (int ks = 0; ks < 8; ks++) {
+#pragma unroll
+            for (int nb = 0; nb < 4; nb++)
+#pragma unroll
+                for (int qt = 0; qt < 2; qt++)
+                    sc[qt][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kb[ks % 3][nb], qf[qt][ks], sc[qt][nb], 0, 0, 0);
+            if (ks + 2 < 8) {
+#pragma unroll
+                for (int nb = 0; nb < 4; nb++) kb[(ks + 2) % 3][nb] = *kaddr(nb, ks + 2);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    auto mask = [&](int key0) {
+        if (key0 + PK - 1 > wave_first) {
+#pragma unroll
+            for (int qt = 0; qt < 2; qt++)
+#pragma unroll
+                for (int nb = 0; nb < 4; nb++)
+#pragma unroll
+                    for (int j = 0; j < 4; j++)
+                        if (key0 + 16 * nb + 4 * g + j > qpos[qt]) sc[qt][nb][j] = -INFINITY;
+        }
+    };
+    float ref[2] = {-INFINITY, -INFINITY}, lsum[2] = {0.f, 0.f}, corr[2] = {1.f, 1.f}, mt[2];
+    half8 pcur[2][2], pnext[2][2];
+    bool pend = false;
+    auto softmax_piece = [&](int piece) {
+        if (piece < 2) {
+            const int qt = piece;
+            float m = sc[qt][0][0];
+#pragma unroll
+            for (int nb = 0; nb < 4; nb++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) m = fmaxf(m, sc[qt][nb][j]);
+            mt[qt] = m;
+        } else if (piece == 2) {
+#pragma unroll
+            for (int qt = 0; qt < 2; qt++) mt[qt] = group4_max(mt[qt]);
+        } else if (piece == 3) {
+            bool need_any = false;
+#pragma unroll
+            for (int qt = 0; qt < 2; qt++) {
+                const bool need = mt[qt] > ref[qt] + kLazyRef;
+                corr[qt] = need ? exp2f(ref[qt] - mt[qt]) : 1.f;
+                lsum[qt] *= corr[qt];
+                ref[qt] = need ? mt[qt] : ref[qt];
+                need_any |= need;
+            }
+            pend = __ballot(need_any) != 0;
+        } else if (piece < 12) {
+            const int e4 = piece - 4;
+            const int qt = e4 >> 2, nb = e4 & 3;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const float p = __builtin_amdgcn_exp2f(sc[qt][nb][j] - ref[qt]);
+                lsum[qt] += p;
+                pnext[qt][nb >> 1][4 * (nb & 1) + j] = (_Float16)p;
+            }
+        }
+    };
+    f32x4 oacc[2][16];
+#pragma unroll
+    for (int qt = 0; qt < 2; qt++)
+#pragma unroll
+        for (int db = 0; db < 16; db++) oacc[qt][db] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    scores(K0);
+    mask(0);
+#pragma unroll
+    for (int piece = 0; piece < 12; piece++) softmax_piece(piece);
+    pend = false;
+#pragma unroll
+    for (int qt = 0; qt < 2; qt++) {
+        pcur[qt][0] = pnext[qt][0];
+        pcur[qt][1] = pnext[qt][1];
+    }
+    __syncthreads();  // K0 free for K(2)
+
+    auto pv = [&](const uint16_t* Vt, auto side) {
+        bf16x8 vb[4][2];
+#pragma unroll
+        for (int d = 0; d < 3; d++) {
+            vb[d][0] = vt_operand_sw(Vt, 0, d, lane);
+            vb[d][1] = vt_operand_sw(Vt, 1, d, lane);
+        }
+#pragma unroll
+        for (int db = 0; db < 16; db++) {
+            if (db + 3 < 16) {
+                vb[(db + 3) & 3][0] = vt_operand_sw(Vt, 0, db + 3, lane);
+                vb[(db + 3) & 3][1] = vt_operand_sw(Vt, 1, db + 3, lane);
+            }
+#pragma unroll
+            for (int ks = 0; ks < 2; ks++)
+#pragma unroll
+                for (int qt = 0; qt < 2; qt++)
+                    oacc[qt][db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, vb[db & 3][ks]),
+                                                                          pcur[qt][ks], oacc[qt][db], 0, 0, 0);
+            side(db);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    auto rescale = [&]() {
+        if (pend) {
+#pragma unroll
+            for (int qt = 0; qt < 2; qt++)
+#pragma unroll
+                for (int db = 0; db < 16; db++) oacc[qt][db] *= corr[qt];
+        }
+        pend = false;
+    };
+    // iteration t: S of K(t + 1) (buffer Kn), P V of V(t) (buffer Vc); loads of K(t + 2) into
+    // the K buffer tile t used (Kc) and of V(t + 1) into the other V buffer (Vn)
+    auto iteration = [&](int t, uint16_t* Kc, uint16_t* Kn, uint16_t* Vc, uint16_t* Vn) {
+        load_v(Vn, t + 1);
+        if (t + 2 < ntiles) load_k(Kc, t + 2);
+        rescale();
+        scores(Kn);
+        mask((t + 1) * PK);
+        pv(Vc, [&](int db) {
+            if (db < 12) softmax_piece(db);
+        });
+#pragma unroll
+        for (int qt = 0; qt < 2; qt++) {
+            pcur[qt][0] = pnext[qt][0];
+            pcur[qt][1] = pnext[qt][1];
+        }
+        __builtin_amdgcn_s_waitcnt(0);  // this wave's direct loads have landed
+        __syncthreads();
+    };
+    int t = 0;
+    for (; t + 2 < ntiles; t += 2) {
+        iteration(t, K0, K1, V0, V1);
+        iteration(t + 1, K1, K0, V1, V0);
+    }
+    if (t + 1 < ntiles) {
+        iteration(t, K0, K1, V0, V1);
+        t++;
+    }
+    rescale();
+    pv((t & 1) ? V1 : V0, [&](int) {});
+
+#pragma unroll
+    for (int qt = 0; qt < 2; qt++) {
+        const float l = group4_sum(lsum[qt]);
+        const int tq = q0 + WQ * wave + 16 * qt + n;
+        const int tc = min(tq, T - 1);
+        f32x4 gf[16];
+        if (gate) {
+            const float* grow = gate + b * gs.b + (long long)tc * gs.t + h * gs.h;
+#pragma unroll
+            for (int db = 0; db < 16; db++) gf[db] = *(const f32x4*)(grow + 16 * db + 4 * g);
+#pragma unroll
+            for (int db = 0; db < 16; db++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) gf[db][j] = sigmoid_f(gf[db][j]);
+        } else {
+#pragma unroll
+            for (int db = 0; db < 16; db++) gf[db] = f32x4{1.f, 1.f, 1.f, 1.f};
+        }
+        float* orow = out + b * os.b + (long long)tc * os.t + h * os.h;
+        const float inv = 1.f / l;
+        if (tq < T) {
+#pragma unroll
+            for (int db = 0; db < 16; db++) {
+                const f32x4 y = oacc[qt][db] * inv * gf[db];
+                *(float4*)(orow + 16 * db + 4 * g) = float4{y[0], y[1], y[2], y[3]};
+            }
+        }
     }
 }
 
@@ -750,9 +1392,15 @@ int launch_decode_core(const float* q, const uint16_t* kc, const uint16_t* vc, c
     return after_launch("attention_decode_merge");
 }
 
+// bytes of the fp16 K / V copies the prefill kernel reads when given that much workspace
+size_t prefill_f16_bytes(int B, int KV, int rows) {
+    const size_t rows_pad = (size_t)(rows + PK - 1) / PK * PK;
+    return 2 * (size_t)B * KV * rows_pad * HD * 2;
+}
+
 int launch_prefill_core(const float* q, Strides3 qs, const uint16_t* kc, const uint16_t* vc, const float* gate,
                         Strides3 gs, float* out, Strides3 os, int B, int H, int KV, int T, int pos, int cap,
-                        float scale, hipStream_t st) {
+                        float scale, hipStream_t st, void* ws = nullptr, size_t ws_bytes = 0) {
     if (KV <= 0 || H % KV) return fail(AEGIST_ERR_SHAPE, "attention prefill: need H % KV == 0");
     if (pos < 0 || pos + T > cap) return fail(AEGIST_ERR_SHAPE, "attention prefill: rows exceed the cache capacity");
     // the MFMA kernel reads q and gate and writes out as 16-byte rows
@@ -760,7 +1408,27 @@ int launch_prefill_core(const float* q, Strides3 qs, const uint16_t* kc, const u
         return (uintptr_t)p % 16 == 0 && s.b % 4 == 0 && s.t % 4 == 0 && s.h % 4 == 0;
     };
     const bool vec = rows16(q, qs) && rows16(out, os) && (!gate || rows16(gate, gs));
-    if (T >= 16 && vec) {
+    // the 32-query kernel addresses the cache rows of a (sequence, KV head) through a buffer
+    // range in bytes (32-bit)
+    const bool w32 = PREFILL_W32 && (long long)(pos + T) * HD * 2 <= 0x7fffffffLL;
+    const int rows = pos + T, rows_pad = (rows + PK - 1) / PK * PK;
+    if (T >= 16 && vec && w32 && ws && ws_bytes >= prefill_f16_bytes(B, KV, rows) && PREFILL_F16 &&
+        (long long)rows_pad * HD * 2 <= 0x7fffffffLL && (uintptr_t)ws % 256 == 0) {
+        uint16_t* kf = (uint16_t*)ws;
+        uint16_t* vf = kf + (size_t)B * KV * rows_pad * HD;
+        const long long nchunks = (long long)B * KV * rows_pad * HD / 8;
+        const int cblocks = (int)std::min<long long>((nchunks + 255) / 256, 4096);
+        attn_kv_f16_kernel<<<cblocks, 256, 0, st>>>(kc, vc, kf, vf, KV, cap, rows, rows_pad, nchunks);
+        int rc = after_launch("attention_prefill_f16_copy");
+        if (rc) return rc;
+        const int nblk = (T + PQ2 - 1) / PQ2 * H * B, per_xcd = (nblk + 7) / 8;
+        attn_prefill_w32f_kernel<<<8 * per_xcd, 64 * PW2, 0, st>>>(q, qs, kf, vf, rows_pad, gate, gs, out, os, H, KV,
+                                                                   T, pos, scale, B, per_xcd);
+    } else if (T >= 16 && vec && w32) {
+        const int nblk = (T + PQ2 - 1) / PQ2 * H * B, per_xcd = (nblk + 7) / 8;
+        attn_prefill_w32_kernel<<<8 * per_xcd, 64 * PW2, 0, st>>>(q, qs, kc, vc, gate, gs, out, os, H, KV, T, pos, cap,
+                                                                  scale, B, per_xcd);
+    } else if (T >= 16 && vec) {
         const int nblk = (T + PQ - 1) / PQ * H * B, per_xcd = (nblk + 7) / 8;
         attn_prefill_mfma_kernel<<<8 * per_xcd, 64 * PW, 0, st>>>(q, qs, kc, vc, gate, gs, out, os, H, KV, T, pos, cap,
                                                                   scale, B, per_xcd);
@@ -779,10 +1447,10 @@ int stack_attn_decode(const float* qn, const uint16_t* kc, const uint16_t* vc, c
                                                ws_bytes, st);
 }
 int stack_attn_prefill(const float* qn, const uint16_t* kc, const uint16_t* vc, const float* qg, float* out, int B,
-                       int H, int KV, int T, int pos, int cap, float scale, hipStream_t st) {
+                       int H, int KV, int T, int pos, int cap, float scale, void* ws, size_t ws_bytes, hipStream_t st) {
     Strides3 qs{(long long)T * H * HD, (long long)H * HD, HD};
     Strides3 gs{(long long)T * H * 2 * HD, (long long)H * 2 * HD, 2 * HD};
-    return launch_prefill_core(qn, qs, kc, vc, qg + HD, gs, out, qs, B, H, KV, T, pos, cap, scale, st);
+    return launch_prefill_core(qn, qs, kc, vc, qg + HD, gs, out, qs, B, H, KV, T, pos, cap, scale, st, ws, ws_bytes);
 }
 
 }  // namespace aegist
@@ -894,7 +1562,14 @@ int aegist_attention_core(const float* q, const uint16_t* kc, const uint16_t* vc
     Strides3 qs{(long long)H * T * HD, HD, (long long)T * HD};
     Strides3 gs{(long long)T * H * HD, (long long)H * HD, HD};
     Strides3 os = gs;
-    return launch_prefill_core(q, qs, kc, vc, gate, gs, out, os, B, H, KV, T, pos, cap, scale, st);
+    return launch_prefill_core(q, qs, kc, vc, gate, gs, out, os, B, H, KV, T, pos, cap, scale, st, workspace,
+                               workspace_bytes);
+}
+
+size_t aegist_attention_core_workspace_bytes(int B, int H, int KV, int T, int pos) {
+    if (B <= 0 || T <= 0 || H <= 0 || KV <= 0) return 0;
+    if (T == 1) return aegist::decode_workspace_bytes(B, H, KV, pos + 1, false);
+    return aegist::prefill_f16_bytes(B, KV, pos + T);
 }
 
 size_t aegist_attention_gated_workspace_bytes(int T, int H, int KV, int pos0) {

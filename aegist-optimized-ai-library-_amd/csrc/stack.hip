@@ -41,7 +41,8 @@ int launch_attn_prep(const void* qg, const void* k, const void* v, int in_dtype,
 int stack_attn_decode(const float* qn, const uint16_t* kc, const uint16_t* vc, const float* qg, uint16_t* out, int B,
                       int H, int KV, int L, int cap, float scale, void* ws, size_t ws_bytes, hipStream_t st);
 int stack_attn_prefill(const float* qn, const uint16_t* kc, const uint16_t* vc, const float* qg, float* out, int B,
-                       int H, int KV, int T, int pos, int cap, float scale, hipStream_t st);
+                       int H, int KV, int T, int pos, int cap, float scale, void* ws, size_t ws_bytes, hipStream_t st);
+size_t prefill_f16_bytes(int B, int KV, int rows);
 size_t decode_workspace_bytes(int B, int H, int KV, int L, bool with_q);
 int launch_proj(const void* X, int x_dtype, long long ldx, const void* W, int w_dtype, const uint16_t* scale, float* Y,
                 long long ldy, int M, int N, int K, int accumulate, hipStream_t st);
@@ -221,7 +222,8 @@ int attn_layer(Stack* s, const AegistLayerWeights& w, int sl, float* x, int B, i
         RC(stack_attn_decode(s->y, kc, vc, s->proj, s->ob, B, H, KV, s->length + 1, (int)cap, scale, s->ws,
                              s->ws_bytes, st));
     } else {
-        RC(stack_attn_prefill(s->y, kc, vc, s->proj, s->o, B, H, KV, T, s->length, (int)cap, scale, st));
+        RC(stack_attn_prefill(s->y, kc, vc, s->proj, s->o, B, H, KV, T, s->length, (int)cap, scale, s->ws,
+                              s->ws_bytes, st));
         RC(launch_cast_bf16(s->o, s->ob, (size_t)rows * H * HD, st));
     }
     return out_proj(s, s->ob, w.w_o, x, rows, dm, H * HD, st);
@@ -272,6 +274,10 @@ int aegist_stack_create(const AegistStackConfig* cfg, void** handle) {
     A((void**)&s->ob, rows * wide * 2);
     s->ws_bytes = std::max(aegist_delta_chunked_workspace_bytes(c.max_batch, (int)std::min<size_t>(rows, 1 << 30), HV),
                            decode_workspace_bytes(c.max_batch, H, KV, c.max_context, false));
+    // the attention prefill's fp16 copy of the cache rows, when it stays within 2 GiB (beyond
+    // that the prefill converts its tiles itself)
+    if (s->n_attn > 0 && prefill_f16_bytes(c.max_batch, KV, c.max_context) <= ((size_t)2 << 30))
+        s->ws_bytes = std::max(s->ws_bytes, prefill_f16_bytes(c.max_batch, KV, c.max_context));
     A(&s->ws, s->ws_bytes);
     for (int i = 0; i < AEGIST_STACK_SNAPSHOTS; i++) {
         A((void**)&s->snap_conv[i], s->conv_bytes());

@@ -299,7 +299,7 @@ def bench_attention_prefill(torch, ops, dev, T=2048, reps=40):
     """Causal gated GQA prefill (config 4's attention layers): T=2048, 16 q heads, 2 KV heads,
     HD 256, cache rows [0, T), at config 4's B=16 (the headline fields) and at B=1 (`points`).
     FLOPs = 4 * B * H * HD * T (T + 1) / 2 (QK^T and PV)."""
-    from aegist_mixer._lib import call
+    from aegist_mixer._lib import call, lib
     bf = torch.bfloat16
     stream = torch.cuda.current_stream().cuda_stream
     points = []
@@ -309,10 +309,14 @@ def bench_attention_prefill(torch, ops, dev, T=2048, reps=40):
         vc = ops.fill_normal(torch.empty(B, ATTN_KV, T, ATTN_HD, device=dev, dtype=bf), 9003)
         gate = ops.fill_normal(torch.empty(B, T, ATTN_H * ATTN_HD, device=dev), 9004)
         out = torch.empty(B, T, ATTN_H, ATTN_HD, device=dev)
+        # the fp16 copy of the cache rows the kernel reads (allocated outside the timing; its
+        # conversion pass runs inside every timed call)
+        nws = lib().aegist_attention_core_workspace_bytes(B, ATTN_H, ATTN_KV, T, 0)
+        ws = torch.empty(nws, dtype=torch.uint8, device=dev)
 
         def run():
             call("aegist_attention_core", q.data_ptr(), kc.data_ptr(), vc.data_ptr(), gate.data_ptr(), out.data_ptr(),
-                 B, ATTN_H, ATTN_KV, T, 0, T, ATTN_HD ** -0.5, None, 0, stream)
+                 B, ATTN_H, ATTN_KV, T, 0, T, ATTN_HD ** -0.5, ws.data_ptr(), nws, stream)
         for _ in range(2):
             run()
         torch.cuda.synchronize()
@@ -326,7 +330,7 @@ def bench_attention_prefill(torch, ops, dev, T=2048, reps=40):
         us = e0.elapsed_time(e1) * 1e3 / n
         tf = 4 * B * ATTN_H * ATTN_HD * T * (T + 1) / 2 / (us * 1e-6) / 1e12
         points.append({"B": B, "us": round(us, 2), "tflops": round(tf, 2), "mfma_frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4)})
-        del q, kc, vc, gate, out
+        del q, kc, vc, gate, out, ws
     p16 = points[-1]
     return {"workload": f"causal gated GQA prefill, T={T}, 16/2 heads, HD 256 (headline fields: config 4's B=16; "
                         f"B=1 in points)",

@@ -224,8 +224,12 @@ int aegist_attention_decode_noalloc(const void* qg, const void* k_new, const voi
 /* Attention core only (no prep): q [B, H, T, HD] fp32 already normed and roped, caches
  * [B, KV, cap, HD] bf16 holding rows [0, pos + T), gate [B, T, H*HD] fp32 or NULL (no gate).
  * out [B, T, H, HD] fp32. Causal with offset: query t sees rows [0, pos + t].
- * T == 1 uses split-K (workspace as above with L = pos + 1); T > 1 the flash kernel
- * (no workspace). */
+ * T == 1 uses split-K (workspace as above with L = pos + 1); T > 1 the flash kernel, whose
+ * workspace is optional: with aegist_attention_core_workspace_bytes(B, H, KV, T, pos) bytes
+ * (256-byte aligned) the cache rows are converted to fp16 once into it and the kernel loads
+ * them straight into LDS; with less (or NULL) each workgroup converts the tiles it stages.
+ * Both give the same results (the conversion is exact). */
+size_t aegist_attention_core_workspace_bytes(int B, int H, int KV, int T, int pos);
 int aegist_attention_core(const float* q, const uint16_t* kc, const uint16_t* vc, const float* gate, float* out,
                           int B, int H, int KV, int T, int pos, int cap, float scale, void* workspace,
                           size_t workspace_bytes, void* stream);

@@ -78,8 +78,9 @@ def test_attention_decode_bf16_out(dev):
                                                 (1, 16, 2, 260, 0, 3.0, 1), (1, 8, 2, 200, 40, 0.5, 300),
                                                 (1, 8, 2, 200, 40, 0.5, 1e-3)])
 def test_attention_core_prefill(dev, B, H, KV, T, pos, qs, vs):
-    """The MFMA prefill stages K / V tiles as fp16 (exact for bf16 values in fp16's range) and
-    takes q and P as fp16: ~11 significant bits against the fp64 loop."""
+    """The MFMA prefill takes K / V as fp16 (exact for bf16 values in fp16's range; converted once
+    into the workspace, or per tile without it) and q and P as fp16: ~11 significant bits against
+    the fp64 loop."""
     print(f"attention_core prefill B={B} H={H} KV={KV} T={T} pos={pos} q*{qs} v*{vs}", flush=True)
     g_ = _gen(T)
     q = torch.randn(B, H, T, HD, generator=g_) * qs
@@ -88,10 +89,14 @@ def test_attention_core_prefill(dev, B, H, KV, T, pos, qs, vs):
     gate = torch.randn(B, T, H * HD, generator=g_)
     ref = R.gated_attention_out(R.attention_core(q, kc, vc, pos, KV), gate).reshape(B, T, H, HD)
     out = ops.attention_core(q.to(dev), kc.to(dev), vc.to(dev), gate.to(dev), pos)
+    # without the fp16-copy workspace the kernel converts its tiles itself: same values, same
+    # order of operations, so the same bits
+    out2 = ops.attention_core(q.to(dev), kc.to(dev), vc.to(dev), gate.to(dev), pos, f16_copy=False)
     torch.cuda.synchronize()
     err = rel_err(out, ref)
     print(f"  rel err {err:.2e}", flush=True)
     assert err < ATTN_TOL
+    assert torch.equal(out, out2)
 
 
 def test_engine_attention_pipeline(dev):
