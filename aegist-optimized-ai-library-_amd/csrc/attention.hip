@@ -97,6 +97,34 @@ struct KeyList {
     int top, R, pos0;
 };
 
+// Reductions inside a wave without LDS permutes (a shuffle's wait would also drain the K / V
+// reads in flight): over the 16 lanes of a row by DPP (quad xor 1, quad xor 2, half-row mirror,
+// row mirror - the same lane pairs as an xor butterfly, so every lane ends with the same value,
+// for sums too), and across the two wave halves by v_permlane32_swap.
+__device__ __forceinline__ float dpp_f(float x, int ctrl_sel) {
+    switch (ctrl_sel) {
+        case 0: return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0xB1, 0xF, 0xF, false));
+        case 1: return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x4E, 0xF, 0xF, false));
+        case 2: return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x141, 0xF, 0xF, false));
+        default: return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x140, 0xF, 0xF, false));
+    }
+}
+__device__ __forceinline__ float row16_max(float x) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) x = fmaxf(x, dpp_f(x, i));
+    return x;
+}
+__device__ __forceinline__ float row16_sum(float x) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) x = x + dpp_f(x, i);
+    return x;
+}
+// x[l] + x[l ^ 32]
+__device__ __forceinline__ float half_swap_sum(float x) {
+    const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(a[0]) + __uint_as_float(a[1]);
+}
+
 template <bool kList>
 __global__ void __launch_bounds__(256) attn_decode_split_kernel(const float* __restrict__ q,
                                                                 const uint16_t* __restrict__ kc,
@@ -231,8 +259,7 @@ __global__ void __launch_bounds__(256) attn_decode_split_kernel(const float* __r
             // rows 4g+j; combine hi (g<2) and lo (g>=2) parts: lane g and g^2 hold h and h+8
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                float other = __shfl_xor(acc[j], 32, WAVE);
-                float s = acc[j] + other;
+                const float s = half_swap_sum(acc[j]);
                 sc[nb][j] = key < k1 ? s : -INFINITY;
             }
         }
@@ -240,11 +267,7 @@ __global__ void __launch_bounds__(256) attn_decode_split_kernel(const float* __r
         float p0[4], p1[4];
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            float mt = fmaxf(sc[0][j], sc[1][j]);
-            mt = fmaxf(mt, __shfl_xor(mt, 1, WAVE));
-            mt = fmaxf(mt, __shfl_xor(mt, 2, WAVE));
-            mt = fmaxf(mt, __shfl_xor(mt, 4, WAVE));
-            mt = fmaxf(mt, __shfl_xor(mt, 8, WAVE));
+            const float mt = row16_max(fmaxf(sc[0][j], sc[1][j]));
             float mn = fmaxf(m_run[j], mt);  // finite: every tile has at least one valid key
             float corr = __expf(m_run[j] - mn);
             p0[j] = __expf(sc[0][j] - mn);
@@ -295,17 +318,12 @@ __global__ void __launch_bounds__(256) attn_decode_split_kernel(const float* __r
     // ---- combine hi/lo rows and reduce l over the 16 key lanes
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-        float l = l_run[j];
-        l += __shfl_xor(l, 1, WAVE);
-        l += __shfl_xor(l, 2, WAVE);
-        l += __shfl_xor(l, 4, WAVE);
-        l += __shfl_xor(l, 8, WAVE);
-        l_run[j] = l;
+        l_run[j] = row16_sum(l_run[j]);
     }
 #pragma unroll
     for (int i = 0; i < 16; i++)
 #pragma unroll
-        for (int j = 0; j < 4; j++) oacc[i][j] += __shfl_xor(oacc[i][j], 32, WAVE);
+        for (int j = 0; j < 4; j++) oacc[i][j] = half_swap_sum(oacc[i][j]);
     if (g < 2) {
 #pragma unroll
         for (int j = 0; j < 4; j++) {
