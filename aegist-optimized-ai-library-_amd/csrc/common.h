@@ -60,6 +60,25 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
+// Lane exchanges without LDS permutes (a permute's wait also drains every LDS read in flight):
+// lane_xor<M> returns x from lane l ^ M for M = 1, 2 (DPP quad permutes) and 8 (DPP rotate of a
+// 16-lane row by 8); pair_sum16 / pair_sum32 return x[l] + x[l ^ 16] / x[l] + x[l ^ 32]
+// (v_permlane16_swap / v_permlane32_swap), the same bits on both lanes of a pair.
+template <int M>
+__device__ __forceinline__ float lane_xor(float x) {
+    static_assert(M == 1 || M == 2 || M == 8, "lane_xor: M = 1, 2 or 8");
+    constexpr int ctrl = M == 1 ? 0xB1 : M == 2 ? 0x4E : 0x128;
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), ctrl, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float pair_sum16(float x) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(a[0]) + __uint_as_float(a[1]);
+}
+__device__ __forceinline__ float pair_sum32(float x) {
+    const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(a[0]) + __uint_as_float(a[1]);
+}
+
 // Orders LDS traffic between the lanes of one wave (no workgroup barrier needed for
 // wave-private buffers): stops compiler code motion and waits for outstanding LDS ops.
 __device__ __forceinline__ void wave_sync() {

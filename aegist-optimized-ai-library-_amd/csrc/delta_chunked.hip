@@ -211,10 +211,10 @@ __device__ __forceinline__ void chunk_intra_body(const Tin* __restrict__ q, cons
             ssq += xq[e] * xq[e];
             ssk += xk[e] * xk[e];
         }
-        ssq += __shfl_xor(ssq, 1, WAVE);
-        ssq += __shfl_xor(ssq, 2, WAVE);
-        ssk += __shfl_xor(ssk, 1, WAVE);
-        ssk += __shfl_xor(ssk, 2, WAVE);
+        ssq += lane_xor<1>(ssq);
+        ssq += lane_xor<2>(ssq);
+        ssk += lane_xor<1>(ssk);
+        ssk += lane_xor<2>(ssk);
         const float rq = normalize ? rsqrtf(ssq + eps) * qscale : 1.f;
         const float rk = normalize ? rsqrtf(ssk + eps) : 1.f;
         // the tiles keep the raw rows (exact in fp16 for bf16 inputs; fp32 inputs add a low fp16

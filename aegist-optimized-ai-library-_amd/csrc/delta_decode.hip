@@ -173,13 +173,10 @@ __global__ void __launch_bounds__(256 * R) delta_decode_kernel(
             pk.x += x.x * kr[i]; pk.y += x.y * kr[i]; pk.z += x.z * kr[i]; pk.w += x.w * kr[i];
             pq.x += x.x * qr[i]; pq.y += x.y * qr[i]; pq.z += x.z * qr[i]; pq.w += x.w * qr[i];
         }
-#pragma unroll
-        for (int o = 8; o < WAVE; o <<= 1) {
-            pk.x += __shfl_xor(pk.x, o, WAVE); pk.y += __shfl_xor(pk.y, o, WAVE);
-            pk.z += __shfl_xor(pk.z, o, WAVE); pk.w += __shfl_xor(pk.w, o, WAVE);
-            pq.x += __shfl_xor(pq.x, o, WAVE); pq.y += __shfl_xor(pq.y, o, WAVE);
-            pq.z += __shfl_xor(pq.z, o, WAVE); pq.w += __shfl_xor(pq.w, o, WAVE);
-        }
+        // sums over the lanes l ^ 8, l ^ 16, l ^ 32 (DPP and lane swaps, no LDS permutes)
+        auto red = [](float x) { return pair_sum32(pair_sum16(x + lane_xor<8>(x))); };
+        pk.x = red(pk.x); pk.y = red(pk.y); pk.z = red(pk.z); pk.w = red(pk.w);
+        pq.x = red(pq.x); pq.y = red(pq.y); pq.z = red(pq.z); pq.w = red(pq.w);
         if (rr == 0) {
             part[j & 1][hl][w4][0][cg] = pk;
             part[j & 1][hl][w4][1][cg] = pq;

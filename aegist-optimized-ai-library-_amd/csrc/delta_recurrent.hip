@@ -81,8 +81,7 @@ __global__ void __launch_bounds__(64) delta_recurrent_kernel(const Tin* __restri
             s[r] *= decay;
             kv += s[r] * sk[rg * 32 + r];
         }
-        kv += __shfl_xor(kv, 16, WAVE);
-        kv += __shfl_xor(kv, 32, WAVE);
+        kv = pair_sum32(pair_sum16(kv));
         const float delta = (vv - kv) * bt;
         float o = 0.f;
 #pragma unroll
@@ -90,8 +89,7 @@ __global__ void __launch_bounds__(64) delta_recurrent_kernel(const Tin* __restri
             s[r] += sk[rg * 32 + r] * delta;
             o += s[r] * sq[rg * 32 + r];
         }
-        o += __shfl_xor(o, 16, WAVE);
-        o += __shfl_xor(o, 32, WAVE);
+        o = pair_sum32(pair_sum16(o));
         if (rg == 0) Act<Tout>::st(out, b * a.sb_o + t * a.st_o + hv * a.sh_o + col, o);
     }
     if (S) {
