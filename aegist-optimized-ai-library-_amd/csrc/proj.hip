@@ -24,6 +24,12 @@
 
 using namespace aegist;
 
+namespace aegist {
+bool gemm_bf16_fits(const void* X, long long ldx, const void* W, long long ldw, int M, int N, int K);
+int launch_gemm_bf16(const uint16_t* X, long long ldx, const uint16_t* W, long long ldw, float* Y, long long ldy, int M,
+                     int N, int K, int accumulate, hipStream_t st);
+}  // namespace aegist
+
 namespace {
 
 bool stream_enabled() {
@@ -516,6 +522,20 @@ void launch_mt(const TX* X, long long ldx, const ProjSegs& segs, int M, int K, i
 
 template <typename TW, typename TX>
 int run_proj(const TX* X, long long ldx, const ProjSegs& segs, int M, int K, int accumulate, hipStream_t st) {
+    // bf16 weights and activations past 64 rows: the tiled MFMA GEMM, one launch per weight
+    if constexpr (std::is_same<TW, uint16_t>::value && std::is_same<TX, uint16_t>::value) {
+        bool ok = M > 64;
+        for (int i = 0; i < segs.n && ok; i++)
+            ok = segs.s[i].scale == nullptr && gemm_bf16_fits(X, ldx, segs.s[i].W, K, M, segs.s[i].N, K);
+        if (ok) {
+            for (int i = 0; i < segs.n; i++) {
+                int rc = launch_gemm_bf16(X, ldx, (const uint16_t*)segs.s[i].W, K, segs.s[i].Y, segs.s[i].ldy, M,
+                                          segs.s[i].N, K, accumulate, st);
+                if (rc) return rc;
+            }
+            return 0;
+        }
+    }
     // bf16 weights at M <= 16 with K a multiple of the chunk, no row scales: the LDS-staged stream
     if constexpr (std::is_same<TW, uint16_t>::value) {
         bool scaled = false;

@@ -43,6 +43,9 @@ int stack_attn_decode(const float* qn, const uint16_t* kc, const uint16_t* vc, c
 int stack_attn_prefill(const float* qn, const uint16_t* kc, const uint16_t* vc, const float* qg, float* out, int B,
                        int H, int KV, int T, int pos, int cap, float scale, void* ws, size_t ws_bytes, hipStream_t st);
 size_t prefill_f16_bytes(int B, int KV, int rows);
+bool gemm_bf16_fits(const void* X, long long ldx, const void* W, long long ldw, int M, int N, int K);
+int launch_gemm_bf16(const uint16_t* X, long long ldx, const uint16_t* W, long long ldw, float* Y, long long ldy, int M,
+                     int N, int K, int accumulate, hipStream_t st);
 size_t decode_workspace_bytes(int B, int H, int KV, int L, bool with_q);
 int launch_proj(const void* X, int x_dtype, long long ldx, const void* W, int w_dtype, const uint16_t* scale, float* Y,
                 long long ldy, int M, int N, int K, int accumulate, hipStream_t st);
@@ -106,14 +109,27 @@ int alloc(Stack* s, void** p, size_t bytes) {
     return rc;
 }
 
+// Prefill-sized GEMMs go to rocBLAS unless AEGIST_GEMM_OWN=1 selects this library's tiled MFMA
+// GEMM (at config 4's shapes it reaches 75-85% of rocBLAS's rate: 16 x 2048 prefill 159 against
+// 151 ms)
+bool gemm_rocblas() {
+    static const bool on = [] {
+        const char* e = getenv("AEGIST_GEMM_OWN");
+        return !(e && e[0] == '1');
+    }();
+    return on;
+}
+
 // Y[M, N] (row-major, leading dim ldy) = A[M, K] (bf16 row-major) . W[N, K]^T (bf16 row-major)
 //                                          + beta * Y,   beta in {0, 1}
-// Decode-sized M (<= 64 rows) goes to this library's weight-streaming kernel (one pass over W,
-// no host-side algorithm lookup); larger M to rocBLAS on the caller's stream.
+// Decode-sized M (<= 64 rows) goes to the weight-streaming kernels (one pass over W), larger M
+// to rocBLAS, or to the tiled MFMA GEMM on request.
 int gemm(Stack* s, const uint16_t* A, const uint16_t* W, float* Y, int M, int N, int K, int ldy, float beta,
          hipStream_t stream) {
     if (M <= 64 && K % 16 == 0)
         return launch_proj(A, AEGIST_BF16, K, W, AEGIST_BF16, nullptr, Y, ldy, M, N, K, beta != 0.f, stream);
+    if (!gemm_rocblas() && gemm_bf16_fits(A, K, W, K, M, N, K))
+        return launch_gemm_bf16(A, K, W, K, Y, ldy, M, N, K, beta != 0.f, stream);
     if (rocblas_set_stream(s->blas, stream) != rocblas_status_success)
         return fail(AEGIST_ERR_SHAPE, "rocblas_set_stream failed");
     const float alpha = 1.f;

@@ -337,6 +337,46 @@ def bench_attention_prefill(torch, ops, dev, T=2048, reps=40):
             "us": p16["us"], "tflops": p16["tflops"], "mfma_frac": p16["mfma_frac"], "points": points}
 
 
+def bench_gemm(torch, ops, dev, reps=10):
+    """Prefill-sized projections of config 4 (M = 16 x 2048 tokens, bf16 weights and activations,
+    fp32 out): the library's tiled MFMA GEMM through `aegist_linear`, and torch's bf16 matmul
+    (hipBLASLt / rocBLAS, bf16 out) on the same operands as a library reference. FLOPs = 2 M N K."""
+    M = 16 * 2048
+    shapes = [(8192, 2048, False, "in_qkv / attention q|gate"), (4096, 2048, False, "in_z"),
+              (2048, 4096, True, "out projection (+= residual)")]
+    points = []
+    for N, K, acc, what in shapes:
+        x = ops.fill_normal(torch.empty(M, K, device=dev, dtype=torch.bfloat16), 7001)
+        w = ops.fill_normal(torch.empty(N, K, device=dev, dtype=torch.bfloat16), 7002, std=0.02)
+        y = torch.zeros(M, N, device=dev)
+
+        def ours():
+            ops.linear(x, w, out=y, accumulate=acc)
+
+        def lib_ref():
+            torch.matmul(x, w.t())
+
+        row = {"N": N, "K": K, "what": what}
+        for name, fn in (("ours", ours), ("torch_bf16_out", lib_ref)):
+            for _ in range(2):
+                fn()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(reps):
+                fn()
+            e1.record()
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) * 1e3 / reps
+            tf = 2.0 * M * N * K / (us * 1e-6) / 1e12
+            row[name + "_us"] = round(us, 1)
+            row[name + "_tflops"] = round(tf, 1)
+        row["mfma_frac"] = round(row["ours_tflops"] / MFMA_BF16_PEAK_TFLOPS, 4)
+        points.append(row)
+        del x, w, y
+    return {"workload": f"config4 prefill projections, M={M}, bf16 x bf16 -> fp32", "points": points}
+
+
 def bench_proj(torch, ops, dev, reps=3):
     """Decode-sized projections (QLinear int8 + bf16 scale with fp32 activations, as the engine
     ships them; bf16 weights with bf16 activations, as config 4 runs them). The timed loop walks
@@ -576,7 +616,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run a 1 GiB device copy (calibrates rocprof FETCH_SIZE / WRITE_SIZE)")
-    ap.add_argument("--legs", type=str, default="prefill,attention_decode,attention_prefill,proj,qsa,moe,stack",
+    ap.add_argument("--legs", type=str, default="prefill,attention_decode,attention_prefill,gemm,proj,qsa,moe,stack",
                     help="comma list of the extra legs to run after the decode headline (default: all); "
                          "'none' for the headline only")
     ap.add_argument("--traffic", type=str, default=str(ROOT / "profiles" / "delta_decode_traffic.json"),
@@ -662,7 +702,7 @@ def main():
             res["roofline"]["traffic"] = json.load(f).get("bytes_per_launch")
     legs = {"prefill": bench_prefill, "attention_decode": bench_attention_decode,
             "attention_prefill": bench_attention_prefill, "proj": bench_proj, "qsa": bench_qsa,
-            "moe": bench_moe, "stack": bench_stack}
+            "moe": bench_moe, "stack": bench_stack, "gemm": bench_gemm}
     want = [] if args.legs.strip() == "none" else [x.strip() for x in args.legs.split(",") if x.strip()]
     unknown = [x for x in want if x not in legs]
     if unknown:
