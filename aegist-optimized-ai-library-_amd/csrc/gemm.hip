@@ -145,6 +145,174 @@ __global__ void __launch_bounds__(512, 1) gemm_bf16_kernel(const uint16_t* __res
     }
 }
 
+
+// ---------------------------------------------------------------------------------------------
+// The engine's QLinear GEMM past 64 rows: Y[M, N] (+)= scale[n] X[M, K] W[N, K]^T with fp32 X,
+// int8 W and bf16 row scales (aegist.cu:126-172). Same tiling, waves and order as above, K in
+// steps of 32 through a 3-stage ring: per stage the W tile is 256 rows x 32 bytes (8 KB) and the X
+// tile 256 rows x 128 bytes (32 KB), both by direct loads issued two steps ahead (120 KB of LDS:
+// the destinations of direct loads stay below 128 KB). W fragments convert to bf16 exactly
+// (|q| <= 127 keeps 8 significant bits); X fragments split into bf16 hi (truncated) + lo
+// (rounded), two products per pair, so the result is within 2^-16 of an fp32 dot product, as in
+// the weight-streaming kernel. Swizzles: W rows (2 slots of 16 bytes) by (row >> 3) & 1, X rows
+// (8 slots) by (row >> 1) & 7, both conflict-free for 16-row fragment reads.
+constexpr int GBK8 = 32;
+constexpr int kWTile8 = GBM * GBK8;       // int8 W tile (8 KB)
+constexpr int kXTile32 = GBM * GBK8 * 4;  // fp32 X tile (32 KB)
+__device__ __forceinline__ int sww(int row) { return (row >> 3) & 1; }
+__device__ __forceinline__ int swx(int row) { return (row >> 1) & 7; }
+
+#define GEMM_WAIT_VM(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (7 << 4) | (15 << 8))
+
+__global__ void __launch_bounds__(512, 1) gemm_i8f32_kernel(const float* __restrict__ X, int ldx,
+                                                            const int8_t* __restrict__ W, int ldw,
+                                                            const uint16_t* __restrict__ scale,
+                                                            float* __restrict__ Y, int ldy, int M, int N, int K,
+                                                            int accumulate, int tiles_n, int ntiles, int per_xcd) {
+    __shared__ __attribute__((aligned(1024))) unsigned char S0[kWTile8 + kXTile32];  // W tile, then X tile
+    __shared__ __attribute__((aligned(1024))) unsigned char S1[kWTile8 + kXTile32];
+    __shared__ __attribute__((aligned(1024))) unsigned char S2[kWTile8 + kXTile32];
+
+    const int li = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+    if (li >= ntiles) return;
+    const int tiles_m = (ntiles + tiles_n - 1) / tiles_n;
+    const int grp = li / (kGroupM * tiles_n), first_m = grp * kGroupM;
+    const int gsize = min(tiles_m - first_m, kGroupM);
+    const int inner = li - grp * kGroupM * tiles_n;
+    const int m0 = (first_m + inner % gsize) * GBM, n0 = (inner / gsize) * GBN;
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid / WAVE), lane = tid % WAVE;
+    const int r16 = lane % 16, g = lane / 16;
+    const int wm = wave >> 1, wn = wave & 1;
+
+    // loads per stage: 8 W pieces (32 rows x 32 bytes) and 32 X pieces (8 rows x 128 bytes), 5 per
+    // wave: W piece `wave`, X pieces 4 wave .. 4 wave + 3
+    const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc((void*)W, (short)0, 0x7fffffff, kBufWord3);
+    const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc((void*)X, (short)0, 0x7fffffff, kBufWord3);
+    int voff[5];
+    {
+        const int row = 32 * wave + lane / 2, gslot = (lane % 2) ^ sww(row);
+        voff[0] = min(n0 + row, N - 1) * ldw + 16 * gslot;
+    }
+#pragma unroll
+    for (int jj = 0; jj < 4; jj++) {
+        const int row = 8 * (4 * wave + jj) + lane / 8, gslot = (lane % 8) ^ swx(row);
+        voff[1 + jj] = min(m0 + row, M - 1) * ldx * 4 + 16 * gslot;
+    }
+    const int nk = K / GBK8;
+    typedef __attribute__((address_space(3))) void lds_void;
+    auto load = [&](unsigned char* St, int step) {
+        if (step >= nk) return;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(wrs, (lds_void*)(St + wave * 1024), 16, voff[0], step * GBK8, 0, 0);
+#pragma unroll
+        for (int jj = 0; jj < 4; jj++)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, (lds_void*)(St + kWTile8 + (4 * wave + jj) * 1024), 16,
+                                                     voff[1 + jj], step * GBK8 * 4, 0, 0);
+    };
+    // wait until this wave's loads of step t have landed, given the last step issued so far
+    auto wait_step = [&](int t, int issued) {
+        const int later = min(issued, nk - 1) - t;
+        if (later >= 1) GEMM_WAIT_VM(5);
+        else GEMM_WAIT_VM(0);
+    };
+
+    f32x4 acc[8][4];
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    // W fragment (row 128 wn + 16 i + r16, k 8 g .. +7): 8 bytes at slot g / 2, half g % 2; X
+    // fragment (row 64 wm + 16 j + r16, same k): 32 bytes = slots 2 g, 2 g + 1
+    auto compute = [&](const unsigned char* St) {
+        bf16x8 a[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const int row = 128 * wn + 16 * i + r16;
+            const uint2 q = *(const uint2*)(St + row * 32 + ((g / 2) ^ sww(row)) * 16 + (g % 2) * 8);
+            uint32_t p[4];
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const uint32_t d = h ? q.y : q.x;
+                const float f0 = (float)(int8_t)d, f1 = (float)(int8_t)(d >> 8);
+                const float f2 = (float)(int8_t)(d >> 16), f3 = (float)(int8_t)(d >> 24);
+                p[2 * h] = __builtin_amdgcn_perm(__float_as_uint(f1), __float_as_uint(f0), 0x07060302u);
+                p[2 * h + 1] = __builtin_amdgcn_perm(__float_as_uint(f3), __float_as_uint(f2), 0x07060302u);
+            }
+            a[i] = __builtin_bit_cast(bf16x8, p);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int row = 64 * wm + 16 * j + r16;
+            const unsigned char* xr = St + kWTile8 + row * 128;
+            const f32x4 x0 = *(const f32x4*)(xr + ((2 * g) ^ swx(row)) * 16);
+            const f32x4 x1 = *(const f32x4*)(xr + ((2 * g + 1) ^ swx(row)) * 16);
+            uint32_t hh[4], ll[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const float v0 = e < 2 ? x0[2 * e] : x1[2 * e - 4], v1 = e < 2 ? x0[2 * e + 1] : x1[2 * e - 3];
+                hh[e] = __builtin_amdgcn_perm(__float_as_uint(v1), __float_as_uint(v0), 0x07060302u);
+                typedef float f2 __attribute__((ext_vector_type(2)));
+                typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+                const f2 lo = {v0 - __uint_as_float(__float_as_uint(v0) & 0xffff0000u),
+                               v1 - __uint_as_float(__float_as_uint(v1) & 0xffff0000u)};
+                ll[e] = __builtin_bit_cast(uint32_t, __builtin_convertvector(lo, b2));
+            }
+            const bf16x8 bh = __builtin_bit_cast(bf16x8, hh), bl = __builtin_bit_cast(bf16x8, ll);
+#pragma unroll
+            for (int i = 0; i < 8; i++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], bh, acc[i][j], 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 8; i++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], bl, acc[i][j], 0, 0, 0);
+        }
+    };
+    // step t: loads of step t + 2 into the stage step t - 1 used, products of step t, then this
+    // wave's loads of step t + 1 waited for and published by the barrier
+    auto step = [&](int t, unsigned char* Sc, unsigned char* Sn2) {
+        load(Sn2, t + 2);
+        compute(Sc);
+        wait_step(t + 1, t + 2);
+        __syncthreads();
+    };
+    load(S0, 0);
+    load(S1, 1);
+    wait_step(0, 1);
+    __syncthreads();
+    // unrolled by three so each stage is a separate array
+    int s = 0;
+    for (; s + 3 <= nk; s += 3) {
+        step(s, S0, S2);
+        step(s + 1, S1, S0);
+        step(s + 2, S2, S1);
+    }
+    if (s < nk) step(s, S0, S2);
+    if (s + 1 < nk) step(s + 1, S1, S0);
+
+    const bool vec = (ldy % 4) == 0 && ((uintptr_t)Y % 16) == 0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const int n = n0 + 128 * wn + 16 * i + 4 * g;
+        float sc[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) sc[e] = scale ? bf2f(scale[min(n + e, N - 1)]) : 1.f;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int m = m0 + 64 * wm + 16 * j + r16;
+            if (m >= M) continue;
+            float* yrow = Y + (size_t)m * ldy;
+            if (vec && n + 3 < N) {
+                f32x4 v = acc[i][j];
+#pragma unroll
+                for (int e = 0; e < 4; e++) v[e] *= sc[e];
+                if (accumulate) v += *(const f32x4*)(yrow + n);
+                *(f32x4*)(yrow + n) = v;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    if (n + e < N) yrow[n + e] = (accumulate ? yrow[n + e] : 0.f) + acc[i][j][e] * sc[e];
+            }
+        }
+    }
+}
+
 }  // namespace
 
 namespace aegist {
@@ -153,6 +321,25 @@ namespace aegist {
 bool gemm_bf16_fits(const void* X, long long ldx, const void* W, long long ldw, int M, int N, int K) {
     return K > 0 && K % GBK == 0 && ldx >= K && ldw >= K && ldx % 8 == 0 && ldw % 8 == 0 && (uintptr_t)X % 16 == 0 &&
            (uintptr_t)W % 16 == 0 && (long long)M * ldx * 2 < 0x7fffffffLL && (long long)N * ldw * 2 < 0x7fffffffLL;
+}
+
+// whether launch_gemm_i8f32 takes these operands
+bool gemm_i8f32_fits(const void* X, long long ldx, const void* W, long long ldw, int M, int N, int K) {
+    return K > 0 && K % GBK8 == 0 && ldx >= K && ldw >= K && ldx % 4 == 0 && ldw % 16 == 0 && (uintptr_t)X % 16 == 0 &&
+           (uintptr_t)W % 16 == 0 && (long long)M * ldx * 4 < 0x7fffffffLL && (long long)N * ldw < 0x7fffffffLL;
+}
+
+// Y[M, N] (+)= scale[n] X[M, K] W[N, K]^T, fp32 X, int8 W, bf16 scale (NULL = 1), fp32 Y.
+int launch_gemm_i8f32(const float* X, long long ldx, const int8_t* W, long long ldw, const uint16_t* scale, float* Y,
+                      long long ldy, int M, int N, int K, int accumulate, hipStream_t st) {
+    if (M <= 0 || N <= 0) return 0;
+    if (!gemm_i8f32_fits(X, ldx, W, ldw, M, N, K) || ldy < N)
+        return fail(AEGIST_ERR_SHAPE, "gemm_i8: need K % 32 == 0, ld >= K, 16-byte aligned rows, operands < 2 GiB");
+    const int tiles_m = (M + GBM - 1) / GBM, tiles_n = (N + GBN - 1) / GBN, ntiles = tiles_m * tiles_n;
+    const int per_xcd = (ntiles + 7) / 8;
+    gemm_i8f32_kernel<<<8 * per_xcd, 512, 0, st>>>(X, (int)ldx, W, (int)ldw, scale, Y, (int)ldy, M, N, K, accumulate,
+                                                   tiles_n, ntiles, per_xcd);
+    return after_launch("gemm_i8");
 }
 
 // Y[M, N] (+)= X[M, K] W[N, K]^T, bf16 X (row stride ldx) and W (row stride ldw), fp32 Y (row

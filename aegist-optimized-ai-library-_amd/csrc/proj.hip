@@ -26,6 +26,9 @@ using namespace aegist;
 
 namespace aegist {
 bool gemm_bf16_fits(const void* X, long long ldx, const void* W, long long ldw, int M, int N, int K);
+bool gemm_i8f32_fits(const void* X, long long ldx, const void* W, long long ldw, int M, int N, int K);
+int launch_gemm_i8f32(const float* X, long long ldx, const int8_t* W, long long ldw, const uint16_t* scale, float* Y,
+                      long long ldy, int M, int N, int K, int accumulate, hipStream_t st);
 int launch_gemm_bf16(const uint16_t* X, long long ldx, const uint16_t* W, long long ldw, float* Y, long long ldy, int M,
                      int N, int K, int accumulate, hipStream_t st);
 }  // namespace aegist
@@ -522,6 +525,19 @@ void launch_mt(const TX* X, long long ldx, const ProjSegs& segs, int M, int K, i
 
 template <typename TW, typename TX>
 int run_proj(const TX* X, long long ldx, const ProjSegs& segs, int M, int K, int accumulate, hipStream_t st) {
+    // int8 weights with fp32 activations past 64 rows (the engine's gemm_i8): the tiled GEMM
+    if constexpr (std::is_same<TW, int8_t>::value && std::is_same<TX, float>::value) {
+        bool ok = M > 64;
+        for (int i = 0; i < segs.n && ok; i++) ok = gemm_i8f32_fits(X, ldx, segs.s[i].W, K, M, segs.s[i].N, K);
+        if (ok) {
+            for (int i = 0; i < segs.n; i++) {
+                int rc = launch_gemm_i8f32(X, ldx, (const int8_t*)segs.s[i].W, K, segs.s[i].scale, segs.s[i].Y,
+                                           segs.s[i].ldy, M, segs.s[i].N, K, accumulate, st);
+                if (rc) return rc;
+            }
+            return 0;
+        }
+    }
     // bf16 weights and activations past 64 rows: the tiled MFMA GEMM, one launch per weight
     if constexpr (std::is_same<TW, uint16_t>::value && std::is_same<TX, uint16_t>::value) {
         bool ok = M > 64;

@@ -374,7 +374,32 @@ def bench_gemm(torch, ops, dev, reps=10):
         row["mfma_frac"] = round(row["ours_tflops"] / MFMA_BF16_PEAK_TFLOPS, 4)
         points.append(row)
         del x, w, y
-    return {"workload": f"config4 prefill projections, M={M}, bf16 x bf16 -> fp32", "points": points}
+    # the engine's QLinear GEMM (int8 weights, bf16 row scales, fp32 activations) on a 1024-token
+    # prefill chunk
+    from aegist_mixer._lib import call
+    Mi, Ni, Ki = 1024, 8192, 2048
+    xi = ops.fill_normal(torch.empty(Mi, Ki, device=dev), 7003)
+    qi = torch.randint(-127, 128, (Ni, Ki), device=dev, dtype=torch.int8)
+    si = ops.fill_normal(torch.empty(Ni, device=dev, dtype=torch.bfloat16), 7004, mean=0.01, std=0.001)
+    yi = torch.zeros(Mi, Ni, device=dev)
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def gi8():
+        call("aegist_gemm_i8", xi.data_ptr(), qi.data_ptr(), si.data_ptr(), yi.data_ptr(), Mi, Ni, Ki, 0, stream)
+    for _ in range(2):
+        gi8()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        gi8()
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / reps
+    i8 = {"M": Mi, "N": Ni, "K": Ki, "us": round(us, 1), "tflops": round(2.0 * Mi * Ni * Ki / (us * 1e-6) / 1e12, 1)}
+    del xi, qi, si, yi
+    return {"workload": f"config4 prefill projections, M={M}, bf16 x bf16 -> fp32", "points": points,
+            "gemm_i8": i8}
 
 
 def bench_proj(torch, ops, dev, reps=3):

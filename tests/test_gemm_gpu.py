@@ -1,7 +1,9 @@
-"""GPU parity of the tiled MFMA GEMM that `aegist_linear` uses for bf16 weights and activations
-past 64 rows (the prefill-sized projections of the layer stack), against the oracle's engine
-formula (fp64 dot products of the exact bf16 values). bf16 x bf16 products are exact and the
-kernel sums in fp32, so the bar is the fp32-level 1e-5 norm-wise relative error. Shapes cover
+"""GPU parity of the tiled MFMA GEMMs that `aegist_linear` uses past 64 rows - bf16 weights and
+activations (the prefill-sized projections of the layer stack) and int8 QLinear weights with
+fp32 activations (the engine's gemm_i8) - against the oracle's engine formula (fp64 dot products
+of the exact weight values). bf16 x bf16 products are exact and the kernel sums in fp32, so the
+bar is the fp32-level 1e-5 norm-wise relative error; the fp32 activations of the int8 path enter
+as bf16 hi + lo (within 2^-16 of fp32), bar 2e-5 as for the weight-streaming kernel. Shapes cover
 M just past the decode range, ragged M / N / K tails against the 256 x 256 x 64 tiles, the
 residual accumulate into a strided Y, and the stack's full prefill shape (M = 16 x 2048),
 checked on a sample of rows."""
@@ -47,8 +49,10 @@ def test_gemm_accumulate_strided(dev):
     y0 = torch.randn(M, N + 32)
     ref = y0.clone()
     ref[:, :N] = R.qlinear_engine(x[:, :K].float(), w.float(), None, y0[:, :N], accumulate=True)
-    xd, yd = x.to(dev), y0.to(dev)
-    call("aegist_linear", xd.data_ptr(), BF16, K + 64, w.to(dev).data_ptr(), BF16, None, yd.data_ptr(), N + 32, M, N, K,
+    # device tensors held in names: a temporary's memory could be reused by the next copy before
+    # the kernel reads it
+    xd, yd, wd = x.to(dev), y0.to(dev), w.to(dev)
+    call("aegist_linear", xd.data_ptr(), BF16, K + 64, wd.data_ptr(), BF16, None, yd.data_ptr(), N + 32, M, N, K,
          1, torch.cuda.current_stream().cuda_stream)
     torch.cuda.synchronize()
     assert rel_err(yd, ref) < TOL
@@ -72,3 +76,22 @@ def test_gemm_stack_prefill_shape(dev, N, K, acc):
     err = rel_err(out[rows.to(dev)], ref)
     print(f"  rel err {err:.2e}", flush=True)
     assert err < TOL
+
+
+@pytest.mark.parametrize("M,N,K,acc", [(65, 256, 64, False), (300, 1000, 128, True), (1024, 8192, 2048, False),
+                                       (777, 2048, 4096, True)])
+def test_gemm_i8_matches_oracle(dev, M, N, K, acc):
+    """The engine's gemm_i8 (aegist.cu:126-172): int8 W, bf16 row scales, fp32 X, fused residual."""
+    print(f"gemm_i8 M={M} N={N} K={K} acc={acc}", flush=True)
+    g = torch.Generator().manual_seed(M * 3 + N + K)
+    q, sc = R.qlinear_quantize(torch.randn(N, K, generator=g) * 0.02)
+    x = torch.randn(M, K, generator=g)
+    y0 = torch.randn(M, N, generator=g)
+    ref = R.qlinear_engine(x, q, sc, y0.clone() if acc else None, accumulate=acc)
+    yd, xd, qd, sd = y0.to(dev), x.to(dev), q.to(dev), sc.to(dev)
+    call("aegist_gemm_i8", xd.data_ptr(), qd.data_ptr(), sd.data_ptr(), yd.data_ptr(), M, N, K, int(acc),
+         torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    err = rel_err(yd, ref)
+    print(f"  rel err {err:.2e}", flush=True)
+    assert err < 2e-5

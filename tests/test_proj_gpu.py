@@ -82,7 +82,8 @@ def test_linear_accumulate_and_strides(dev):
     ref[:, :N] = R.qlinear_engine(xbig[:, :K], w.float(), None, ybig[:, :N], accumulate=True)
     xd, yd = xbig.to(dev), ybig.to(dev)
     from aegist_mixer._lib import BF16, F32, call
-    call("aegist_linear", xd.data_ptr(), F32, K + 64, w.to(dev).data_ptr(), BF16, None, yd.data_ptr(), N + 32, M, N, K,
+    wd = w.to(dev)  # held: a temporary's memory could be reused before the kernel reads it
+    call("aegist_linear", xd.data_ptr(), F32, K + 64, wd.data_ptr(), BF16, None, yd.data_ptr(), N + 32, M, N, K,
          1, torch.cuda.current_stream().cuda_stream)
     torch.cuda.synchronize()
     assert rel_err(yd, ref) < TOL_F32X
