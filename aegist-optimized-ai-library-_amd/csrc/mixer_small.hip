@@ -223,9 +223,15 @@ __global__ void __launch_bounds__(256) conv_silu_kernel(const float* __restrict_
     }
 }
 
+namespace aegist {
+int launch_conv_silu_batched(const float* x, float* y, const uint16_t* w, float* state, int B, int T, int C,
+                             hipStream_t st);
+}
 extern "C" int aegist_conv_silu(const float* x, float* y, const uint16_t* w, float* state, int T, int C, void* stream) {
     AEG_REQUIRE(T >= 0 && C > 0, "conv_silu: bad shape");
     if (T == 0) return 0;
+    if (C % 4 == 0 && (uintptr_t)x % 16 == 0 && (uintptr_t)y % 16 == 0 && (uintptr_t)w % 8 == 0)
+        return launch_conv_silu_batched(x, y, w, state, 1, T, C, AEG_STREAM(stream));
     conv_silu_kernel<<<(C + 63) / 64, 256, 0, AEG_STREAM(stream)>>>(x, y, w, state, T, C);
     return after_launch("conv_silu");
 }
@@ -467,6 +473,75 @@ __global__ void __launch_bounds__(256) conv_silu_batched_kernel(const float* __r
     }
 }
 
+// Batched conv + SiLU over token chunks, for C % 4 == 0 and 16-byte rows: x, y [B, T, C];
+// state [B, C, 3] (oldest first). Each thread owns 4 channels x kConvTT consecutive tokens and
+// keeps the last 3 inputs in registers, so every input is loaded once (plus a 3-token halo per
+// thread) and a wave moves 1 KB per load and store instruction; the earlier layout (one channel
+// per thread over every 4th token) loaded each input 4 times. The state is only read here (the
+// inputs before token 0); conv_state_tail_kernel replaces it afterwards, in a second launch, since
+// the chunk that reads the old state and the one that sees the last inputs are different
+// workgroups.
+constexpr int kConvTT = 16;
+__global__ void __launch_bounds__(256) conv_silu_chunk_kernel(const float* __restrict__ x, float* __restrict__ y,
+                                                              const uint16_t* __restrict__ w,
+                                                              const float* __restrict__ state, int T, int C) {
+    const int b = blockIdx.z, c = (blockIdx.x * 64 + threadIdx.x % 64) * 4;
+    const int t0 = (blockIdx.y * 4 + threadIdx.x / 64) * kConvTT;
+    if (c >= C || t0 >= T) return;
+    x += (size_t)b * T * C;
+    y += (size_t)b * T * C;
+    state += (size_t)b * C * 3;
+    float wt[4][4];  // [channel][tap], tap 3 multiplies the newest input
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const uint2 wp = *(const uint2*)(w + (size_t)(c + e) * 4);
+        wt[e][0] = bf_lo(wp.x);
+        wt[e][1] = bf_hi(wp.x);
+        wt[e][2] = bf_lo(wp.y);
+        wt[e][3] = bf_hi(wp.y);
+    }
+    auto input = [&](int t) -> f32x4 {  // x[t] for t >= 0, the state's inputs for t in [-3, 0)
+        if (t >= 0) return *(const f32x4*)(x + (size_t)t * C + c);
+        f32x4 r;
+#pragma unroll
+        for (int e = 0; e < 4; e++) r[e] = state[(size_t)(c + e) * 3 + 3 + t];
+        return r;
+    };
+    f32x4 h0 = input(t0 - 3), h1 = input(t0 - 2), h2 = input(t0 - 1);
+    f32x4 xin[kConvTT];
+#pragma unroll
+    for (int i = 0; i < kConvTT; i++)
+        xin[i] = t0 + i < T ? *(const f32x4*)(x + (size_t)(t0 + i) * C + c) : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < kConvTT; i++) {
+        if (t0 + i < T) {
+            f32x4 o;
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                o[e] = silu_f(wt[e][0] * h0[e] + wt[e][1] * h1[e] + wt[e][2] * h2[e] + wt[e][3] * xin[i][e]);
+            *(f32x4*)(y + (size_t)(t0 + i) * C + c) = o;
+        }
+        h0 = h1;
+        h1 = h2;
+        h2 = xin[i];
+    }
+}
+
+// The conv state after a T-token feed: the last 3 inputs, taking the old state where T < 3.
+__global__ void conv_state_tail_kernel(const float* __restrict__ x, float* __restrict__ state, int T, int C) {
+    const int b = blockIdx.y, c = blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= C) return;
+    x += (size_t)b * T * C;
+    float* st = state + ((size_t)b * C + c) * 3;
+    const float s1 = st[1], s2 = st[2];
+    const float n0 = T >= 3 ? x[(size_t)(T - 3) * C + c] : (T == 2 ? s2 : s1);
+    const float n1 = T >= 2 ? x[(size_t)(T - 2) * C + c] : s2;
+    const float n2 = x[(size_t)(T - 1) * C + c];
+    st[0] = n0;
+    st[1] = n1;
+    st[2] = n2;
+}
+
 // Embedding rows: out[i] = fp32(table[ids[i]]), D per row.
 __global__ void embed_bf16_kernel(const uint16_t* __restrict__ table, const int* __restrict__ ids,
                                   float* __restrict__ out, int n, int D) {
@@ -534,6 +609,14 @@ int launch_gated_norm_bf16(const float* o, const float* z, const uint16_t* w, ui
 int launch_conv_silu_batched(const float* x, float* y, const uint16_t* w, float* state, int B, int T, int C,
                              hipStream_t st) {
     if (B <= 0 || T <= 0) return 0;
+    if (C % 4 == 0 && (uintptr_t)x % 16 == 0 && (uintptr_t)y % 16 == 0 && (uintptr_t)w % 8 == 0) {
+        conv_silu_chunk_kernel<<<dim3((C / 4 + 63) / 64, (T + 4 * kConvTT - 1) / (4 * kConvTT), B), 256, 0, st>>>(
+            x, y, w, state, T, C);
+        int rc = after_launch("conv_silu_chunk");
+        if (rc) return rc;
+        conv_state_tail_kernel<<<dim3((C + 255) / 256, B), 256, 0, st>>>(x, state, T, C);
+        return after_launch("conv_state_tail");
+    }
     conv_silu_batched_kernel<<<dim3((C + 63) / 64, B), 256, 0, st>>>(x, y, w, state, T, C);
     return after_launch("conv_silu_batched");
 }
