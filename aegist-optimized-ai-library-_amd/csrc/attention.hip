@@ -769,16 +769,20 @@ __global__ void __launch_bounds__(64 * PW, 8 / PW) attn_prefill_mfma_kernel(cons
 // old reference. All four waves run every tile of their block; a tile none of a wave's queries
 // sees gets fully masked (probabilities 0), which keeps the control flow uniform.
 constexpr int WQ = 32, PQ2 = 128, PW2 = PQ2 / WQ;
+// 4 consecutive outputs as fp32 (16 bytes) or bf16 (8 bytes, rounded to nearest even)
+__device__ __forceinline__ void store4(float* p, f32x4 y) { *(float4*)p = float4{y[0], y[1], y[2], y[3]}; }
+__device__ __forceinline__ void store4(uint16_t* p, f32x4 y) { *(uint2*)p = uint2{f2bf2(y[0], y[1]), f2bf2(y[2], y[3])}; }
 constexpr int NST2 = (PK * HD) / (8 * 64 * PW2);  // 16-byte chunks per thread per tile (K; V alike)
 constexpr int RST2 = 64 * PW2 / (HD / 8);         // key rows between a thread's chunks
 constexpr float kLazyRef = 8.f;                    // log2 units
 constexpr int kBufWord3 = 0x00020000;              // buffer resource word 3 on gfx9: 32-bit data, no swizzle
 
+template <typename Tout>
 __global__ void __launch_bounds__(64 * PW2, 1) attn_prefill_w32_kernel(const float* __restrict__ q, Strides3 qs,
                                                                        const uint16_t* __restrict__ kc,
                                                                        const uint16_t* __restrict__ vc,
                                                                        const float* __restrict__ gate, Strides3 gs,
-                                                                       float* __restrict__ out, Strides3 os, int H,
+                                                                       Tout* __restrict__ out, Strides3 os, int H,
                                                                        int KV, int T, int pos, int cap, float scale,
                                                                        int B, int per_xcd) {
     __shared__ __attribute__((aligned(16))) uint16_t Kt2[2][PK * KLD];
@@ -1047,14 +1051,11 @@ __global__ void __launch_bounds__(64 * PW2, 1) attn_prefill_w32_kernel(const flo
 #pragma unroll
             for (int db = 0; db < 16; db++) gf[db] = f32x4{1.f, 1.f, 1.f, 1.f};
         }
-        float* orow = out + b * os.b + (long long)tc * os.t + h * os.h;
+        Tout* orow = out + b * os.b + (long long)tc * os.t + h * os.h;
         const float inv = 1.f / l;
         if (tq < T) {
 #pragma unroll
-            for (int db = 0; db < 16; db++) {
-                const f32x4 y = oacc[qt][db] * inv * gf[db];
-                *(float4*)(orow + 16 * db + 4 * g) = float4{y[0], y[1], y[2], y[3]};
-            }
+            for (int db = 0; db < 16; db++) store4(orow + 16 * db + 4 * g, oacc[qt][db] * inv * gf[db]);
         }
     }
 }
@@ -1108,11 +1109,12 @@ __device__ __forceinline__ bf16x8 vt_operand_sw(const uint16_t* vt, int ks, int 
     return bf16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
 }
 
+template <typename Tout>
 __global__ void __launch_bounds__(64 * PW2, 1) attn_prefill_w32f_kernel(const float* __restrict__ q, Strides3 qs,
                                                                         const uint16_t* __restrict__ kf,
                                                                         const uint16_t* __restrict__ vf, int rows_pad,
                                                                         const float* __restrict__ gate, Strides3 gs,
-                                                                        float* __restrict__ out, Strides3 os, int H,
+                                                                        Tout* __restrict__ out, Strides3 os, int H,
                                                                         int KV, int T, int pos, float scale, int B,
                                                                         int per_xcd) {
     __shared__ __attribute__((aligned(1024))) uint16_t K0[PK * HD];
@@ -1357,14 +1359,11 @@ __global__ void __launch_bounds__(64 * PW2, 1) attn_prefill_w32f_kernel(const fl
 #pragma unroll
             for (int db = 0; db < 16; db++) gf[db] = f32x4{1.f, 1.f, 1.f, 1.f};
         }
-        float* orow = out + b * os.b + (long long)tc * os.t + h * os.h;
+        Tout* orow = out + b * os.b + (long long)tc * os.t + h * os.h;
         const float inv = 1.f / l;
         if (tq < T) {
 #pragma unroll
-            for (int db = 0; db < 16; db++) {
-                const f32x4 y = oacc[qt][db] * inv * gf[db];
-                *(float4*)(orow + 16 * db + 4 * g) = float4{y[0], y[1], y[2], y[3]};
-            }
+            for (int db = 0; db < 16; db++) store4(orow + 16 * db + 4 * g, oacc[qt][db] * inv * gf[db]);
         }
     }
 }
@@ -1418,7 +1417,11 @@ size_t prefill_f16_bytes(int B, int KV, int rows) {
 
 int launch_prefill_core(const float* q, Strides3 qs, const uint16_t* kc, const uint16_t* vc, const float* gate,
                         Strides3 gs, float* out, Strides3 os, int B, int H, int KV, int T, int pos, int cap,
-                        float scale, hipStream_t st, void* ws = nullptr, size_t ws_bytes = 0) {
+                        float scale, hipStream_t st, void* ws = nullptr, size_t ws_bytes = 0,
+                        uint16_t* out_bf16 = nullptr, bool* wrote_bf16 = nullptr) {
+    // out_bf16: the 32-query kernels may write the output as bf16 there instead (same strides);
+    // *wrote_bf16 says whether they did (the other kernels write fp32 to out)
+    if (wrote_bf16) *wrote_bf16 = false;
     if (KV <= 0 || H % KV) return fail(AEGIST_ERR_SHAPE, "attention prefill: need H % KV == 0");
     if (pos < 0 || pos + T > cap) return fail(AEGIST_ERR_SHAPE, "attention prefill: rows exceed the cache capacity");
     // the MFMA kernel reads q and gate and writes out as 16-byte rows
@@ -1440,12 +1443,25 @@ int launch_prefill_core(const float* q, Strides3 qs, const uint16_t* kc, const u
         int rc = after_launch("attention_prefill_f16_copy");
         if (rc) return rc;
         const int nblk = (T + PQ2 - 1) / PQ2 * H * B, per_xcd = (nblk + 7) / 8;
-        attn_prefill_w32f_kernel<<<8 * per_xcd, 64 * PW2, 0, st>>>(q, qs, kf, vf, rows_pad, gate, gs, out, os, H, KV,
-                                                                   T, pos, scale, B, per_xcd);
+        if (out_bf16) {
+            attn_prefill_w32f_kernel<uint16_t><<<8 * per_xcd, 64 * PW2, 0, st>>>(q, qs, kf, vf, rows_pad, gate, gs,
+                                                                                out_bf16, os, H, KV, T, pos, scale, B,
+                                                                                per_xcd);
+            if (wrote_bf16) *wrote_bf16 = true;
+        } else {
+            attn_prefill_w32f_kernel<float><<<8 * per_xcd, 64 * PW2, 0, st>>>(q, qs, kf, vf, rows_pad, gate, gs, out,
+                                                                             os, H, KV, T, pos, scale, B, per_xcd);
+        }
     } else if (T >= 16 && vec && w32) {
         const int nblk = (T + PQ2 - 1) / PQ2 * H * B, per_xcd = (nblk + 7) / 8;
-        attn_prefill_w32_kernel<<<8 * per_xcd, 64 * PW2, 0, st>>>(q, qs, kc, vc, gate, gs, out, os, H, KV, T, pos, cap,
-                                                                  scale, B, per_xcd);
+        if (out_bf16) {
+            attn_prefill_w32_kernel<uint16_t><<<8 * per_xcd, 64 * PW2, 0, st>>>(q, qs, kc, vc, gate, gs, out_bf16, os, H,
+                                                                               KV, T, pos, cap, scale, B, per_xcd);
+            if (wrote_bf16) *wrote_bf16 = true;
+        } else {
+            attn_prefill_w32_kernel<float><<<8 * per_xcd, 64 * PW2, 0, st>>>(q, qs, kc, vc, gate, gs, out, os, H, KV, T,
+                                                                            pos, cap, scale, B, per_xcd);
+        }
     } else if (T >= 16 && vec) {
         const int nblk = (T + PQ - 1) / PQ * H * B, per_xcd = (nblk + 7) / 8;
         attn_prefill_mfma_kernel<<<8 * per_xcd, 64 * PW, 0, st>>>(q, qs, kc, vc, gate, gs, out, os, H, KV, T, pos, cap,
@@ -1465,10 +1481,12 @@ int stack_attn_decode(const float* qn, const uint16_t* kc, const uint16_t* vc, c
                                                ws_bytes, st);
 }
 int stack_attn_prefill(const float* qn, const uint16_t* kc, const uint16_t* vc, const float* qg, float* out, int B,
-                       int H, int KV, int T, int pos, int cap, float scale, void* ws, size_t ws_bytes, hipStream_t st) {
+                       int H, int KV, int T, int pos, int cap, float scale, void* ws, size_t ws_bytes, hipStream_t st,
+                       uint16_t* out_bf16, bool* wrote_bf16) {
     Strides3 qs{(long long)T * H * HD, (long long)H * HD, HD};
     Strides3 gs{(long long)T * H * 2 * HD, (long long)H * 2 * HD, 2 * HD};
-    return launch_prefill_core(qn, qs, kc, vc, qg + HD, gs, out, qs, B, H, KV, T, pos, cap, scale, st, ws, ws_bytes);
+    return launch_prefill_core(qn, qs, kc, vc, qg + HD, gs, out, qs, B, H, KV, T, pos, cap, scale, st, ws, ws_bytes,
+                               out_bf16, wrote_bf16);
 }
 
 }  // namespace aegist

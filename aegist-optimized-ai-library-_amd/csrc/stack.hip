@@ -41,7 +41,8 @@ int launch_attn_prep(const void* qg, const void* k, const void* v, int in_dtype,
 int stack_attn_decode(const float* qn, const uint16_t* kc, const uint16_t* vc, const float* qg, uint16_t* out, int B,
                       int H, int KV, int L, int cap, float scale, void* ws, size_t ws_bytes, hipStream_t st);
 int stack_attn_prefill(const float* qn, const uint16_t* kc, const uint16_t* vc, const float* qg, float* out, int B,
-                       int H, int KV, int T, int pos, int cap, float scale, void* ws, size_t ws_bytes, hipStream_t st);
+                       int H, int KV, int T, int pos, int cap, float scale, void* ws, size_t ws_bytes, hipStream_t st,
+                       uint16_t* out_bf16, bool* wrote_bf16);
 size_t prefill_f16_bytes(int B, int KV, int rows);
 bool gemm_bf16_fits(const void* X, long long ldx, const void* W, long long ldw, int M, int N, int K);
 int launch_gemm_bf16(const uint16_t* X, long long ldx, const uint16_t* W, long long ldw, float* Y, long long ldy, int M,
@@ -238,9 +239,12 @@ int attn_layer(Stack* s, const AegistLayerWeights& w, int sl, float* x, int B, i
         RC(stack_attn_decode(s->y, kc, vc, s->proj, s->ob, B, H, KV, s->length + 1, (int)cap, scale, s->ws,
                              s->ws_bytes, st));
     } else {
+        // the attention output goes straight to the out projection's bf16 input when the prefill
+        // kernel can write bf16, else through fp32 and a cast
+        bool wrote_bf16 = false;
         RC(stack_attn_prefill(s->y, kc, vc, s->proj, s->o, B, H, KV, T, s->length, (int)cap, scale, s->ws,
-                              s->ws_bytes, st));
-        RC(launch_cast_bf16(s->o, s->ob, (size_t)rows * H * HD, st));
+                              s->ws_bytes, st, s->ob, &wrote_bf16));
+        if (!wrote_bf16) RC(launch_cast_bf16(s->o, s->ob, (size_t)rows * H * HD, st));
     }
     return out_proj(s, s->ob, w.w_o, x, rows, dm, H * HD, st);
 }
