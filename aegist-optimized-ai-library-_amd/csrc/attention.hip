@@ -21,6 +21,7 @@
 #include "common.h"
 
 #include <cstdlib>
+#include <type_traits>
 #include <algorithm>
 #include <mutex>
 #include <string>
@@ -732,7 +733,7 @@ __global__ void __launch_bounds__(64 * PW, 8 / PW) attn_prefill_mfma_kernel(cons
 #pragma unroll
         for (int db = 0; db < 16; db++)
 #pragma unroll
-            for (int j = 0; j < 4; j++) gf[db][j] = sigmoid_f(gf[db][j]);
+            for (int j = 0; j < 4; j++) gf[db][j] = sigmoid_rcp(gf[db][j]);
     } else {
 #pragma unroll
         for (int db = 0; db < 16; db++) gf[db] = f32x4{1.f, 1.f, 1.f, 1.f};
@@ -1046,7 +1047,7 @@ __global__ void __launch_bounds__(64 * PW2, 1) attn_prefill_w32_kernel(const flo
 #pragma unroll
             for (int db = 0; db < 16; db++)
 #pragma unroll
-                for (int j = 0; j < 4; j++) gf[db][j] = sigmoid_f(gf[db][j]);
+                for (int j = 0; j < 4; j++) gf[db][j] = sigmoid_rcp(gf[db][j]);
         } else {
 #pragma unroll
             for (int db = 0; db < 16; db++) gf[db] = f32x4{1.f, 1.f, 1.f, 1.f};
@@ -1212,8 +1213,10 @@ __global__ void __launch_bounds__(64 * PW2, 1) attn_prefill_w32f_kernel(const fl
             __builtin_amdgcn_sched_barrier(0);
         }
     };
-    auto mask = [&](int key0) {
-        if (key0 + PK - 1 > wave_first) {
+    // masked: the tile may hold keys past some query of the block; tiles wholly before the block's
+    // first query take the unmasked form (no compares or selects)
+    auto mask = [&](int key0, auto masked) {
+        if (decltype(masked)::value && key0 + PK - 1 > wave_first) {
 #pragma unroll
             for (int qt = 0; qt < 2; qt++)
 #pragma unroll
@@ -1267,7 +1270,7 @@ __global__ void __launch_bounds__(64 * PW2, 1) attn_prefill_w32f_kernel(const fl
         for (int db = 0; db < 16; db++) oacc[qt][db] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     scores(K0);
-    mask(0);
+    mask(0, std::true_type{});
 #pragma unroll
     for (int piece = 0; piece < 12; piece++) softmax_piece(piece);
     pend = false;
@@ -1312,12 +1315,12 @@ __global__ void __launch_bounds__(64 * PW2, 1) attn_prefill_w32f_kernel(const fl
     };
     // iteration t: S of K(t + 1) (buffer Kn), P V of V(t) (buffer Vc); loads of K(t + 2) into
     // the K buffer tile t used (Kc) and of V(t + 1) into the other V buffer (Vn)
-    auto iteration = [&](int t, uint16_t* Kc, uint16_t* Kn, uint16_t* Vc, uint16_t* Vn) {
+    auto iteration = [&](int t, uint16_t* Kc, uint16_t* Kn, uint16_t* Vc, uint16_t* Vn, auto masked) {
         load_v(Vn, t + 1);
         if (t + 2 < ntiles) load_k(Kc, t + 2);
         rescale();
         scores(Kn);
-        mask((t + 1) * PK);
+        mask((t + 1) * PK, masked);
         pv(Vc, [&](int db) {
             if (db < 12) softmax_piece(db);
         });
@@ -1329,13 +1332,19 @@ __global__ void __launch_bounds__(64 * PW2, 1) attn_prefill_w32f_kernel(const fl
         __builtin_amdgcn_s_waitcnt(0);  // this wave's direct loads have landed
         __syncthreads();
     };
+    // tiles below nfree end at or before the block's first query: no key of theirs is masked
+    const int nfree = (pos + q0 + 1) / PK;
     int t = 0;
+    for (; t + 2 < ntiles && t + 2 < nfree; t += 2) {
+        iteration(t, K0, K1, V0, V1, std::false_type{});
+        iteration(t + 1, K1, K0, V1, V0, std::false_type{});
+    }
     for (; t + 2 < ntiles; t += 2) {
-        iteration(t, K0, K1, V0, V1);
-        iteration(t + 1, K1, K0, V1, V0);
+        iteration(t, K0, K1, V0, V1, std::true_type{});
+        iteration(t + 1, K1, K0, V1, V0, std::true_type{});
     }
     if (t + 1 < ntiles) {
-        iteration(t, K0, K1, V0, V1);
+        iteration(t, K0, K1, V0, V1, std::true_type{});
         t++;
     }
     rescale();
@@ -1354,7 +1363,7 @@ __global__ void __launch_bounds__(64 * PW2, 1) attn_prefill_w32f_kernel(const fl
 #pragma unroll
             for (int db = 0; db < 16; db++)
 #pragma unroll
-                for (int j = 0; j < 4; j++) gf[db][j] = sigmoid_f(gf[db][j]);
+                for (int j = 0; j < 4; j++) gf[db][j] = sigmoid_rcp(gf[db][j]);
         } else {
 #pragma unroll
             for (int db = 0; db < 16; db++) gf[db] = f32x4{1.f, 1.f, 1.f, 1.f};

@@ -46,6 +46,9 @@ template <> struct Act<uint16_t> {
 
 __device__ __forceinline__ float silu_f(float x) { return x / (1.f + __expf(-x)); }
 __device__ __forceinline__ float sigmoid_f(float x) { return 1.f / (1.f + __expf(-x)); }
+// sigmoid with the hardware reciprocal (1 ulp) in place of the IEEE division sequence; for
+// epilogues that apply it to whole output tiles
+__device__ __forceinline__ float sigmoid_rcp(float x) { return __builtin_amdgcn_rcpf(1.f + __expf(-x)); }
 
 // ---------------------------------------------------------------------------------------------
 // wave64 reductions (butterfly; every lane ends with the result).
