@@ -1116,264 +1116,282 @@ __global__ void __launch_bounds__(64 * PW2, 1) attn_prefill_w32f_kernel(const fl
                                                                         const uint16_t* __restrict__ vf, int rows_pad,
                                                                         const float* __restrict__ gate, Strides3 gs,
                                                                         Tout* __restrict__ out, Strides3 os, int H,
-                                                                        int KV, int T, int pos, float scale, int B,
-                                                                        int per_xcd) {
+                                                                        int KV, int T, int pos, float scale, int B) {
     __shared__ __attribute__((aligned(1024))) uint16_t K0[PK * HD];
     __shared__ __attribute__((aligned(1024))) uint16_t K1[PK * HD];
     __shared__ __attribute__((aligned(1024))) uint16_t V0[PK * HD];
     __shared__ __attribute__((aligned(1024))) uint16_t V1[PK * HD];
 
-    const int nqb = (T + PQ2 - 1) / PQ2, G = H / KV;
-    const int li = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
-    if (li >= nqb * H * B) return;
-    const int qb = nqb - 1 - li % nqb, hh = (li / nqb) % G, kvh = (li / (nqb * G)) % KV, b = li / (nqb * H);
-    const int h = kvh * G + hh;
-    const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE, n = lane % 16, g = lane / 16;
-    const int q0 = qb * PQ2;
-    const size_t base = ((size_t)b * KV + kvh) * (size_t)rows_pad * HD;
-    const int last_key = pos + min(q0 + PQ2, T) - 1;
-    const int ntiles = last_key / PK + 1;
-    const int wave_first = pos + q0 + WQ * wave;
+    // persistent workgroups (one per CU) walk a static schedule of (query block, head, sequence)
+    // items, longest query blocks first, so no CU waits on the dispatcher between items. The items
+    // of a (sequence, KV head) pair stay on few XCDs, whose workgroups share the pair's K / V rows
+    // in their L2: with pairs a multiple of 8, XCD x owns pairs x, x + 8, ...; with pairs dividing
+    // 8, the rep = 8 / pairs XCDs x = p (mod pairs) split pair p's query heads (head x / pairs,
+    // then every rep-th). Items of one query block index form a round, and rounds alternate
+    // direction over the workgroups.
+    const int nqb = (T + PQ2 - 1) / PQ2, G = H / KV, npairs = B * KV, xcd = blockIdx.x % 8;
+    const bool g8 = gridDim.x % 8 == 0;
+    const int rep = g8 && npairs % 8 == 0 ? 1 : (g8 && 8 % npairs == 0 && G % (8 / npairs) == 0 ? 8 / npairs : 0);
+    const bool aff = rep != 0;
+    const int np_x = !aff ? npairs : (rep == 1 ? npairs / 8 : 1), hpx = aff ? G / rep : G;
+    const int P = aff ? gridDim.x / 8 : gridDim.x, jw = aff ? blockIdx.x / 8 : blockIdx.x;
+    const int items = np_x * hpx * nqb;
+    for (int round = 0;; round++) {
+        const int m = round * P + ((round & 1) ? P - 1 - jw : jw);
+        if (m >= items) break;
+        const int qb = nqb - 1 - m / (np_x * hpx), pi = (m % (np_x * hpx)) / hpx, hl = m % hpx;
+        const int pair = !aff ? pi : (rep == 1 ? xcd + 8 * pi : xcd % npairs);
+        const int hh = rep > 1 ? hl * rep + xcd / npairs : hl;
+        const int kvh = pair % KV, b = pair / KV;
+        const int h = kvh * G + hh;
+        const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE, n = lane % 16, g = lane / 16;
+        const int q0 = qb * PQ2;
+        const size_t base = ((size_t)b * KV + kvh) * (size_t)rows_pad * HD;
+        const int last_key = pos + min(q0 + PQ2, T) - 1;
+        const int ntiles = last_key / PK + 1;
+        const int wave_first = pos + q0 + WQ * wave;
 
-    // direct loads: instruction i of this wave fills key rows 2 j, 2 j + 1 (j = 8 wave + i) of a
-    // tile; lane L writes LDS slot L % 32 of row 2 j + L / 32 with global slot (L % 32) ^ swizzle
-    const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc((void*)(kf + base), (short)0,
-                                                                       rows_pad * HD * 2, kBufWord3);
-    const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc((void*)(vf + base), (short)0,
-                                                                       rows_pad * HD * 2, kBufWord3);
-    int koff[8], voff[8];
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-        const int row = 2 * (8 * wave + i) + lane / 32, s = lane % 32;
-        koff[i] = (row * HD + sw_slot(s, row, KSW) * 8) * 2;
-        voff[i] = (row * HD + sw_slot(s, row, VSW) * 8) * 2;
-    }
-    typedef __attribute__((address_space(3))) void lds_void;
-    auto load_k = [&](uint16_t* dst, int t) {
-#pragma unroll
-        for (int i = 0; i < 8; i++)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (lds_void*)(dst + (8 * wave + i) * 2 * HD), 16, koff[i],
-                                                     t * PK * HD * 2, 0, 0);
-    };
-    auto load_v = [&](uint16_t* dst, int t) {
-#pragma unroll
-        for (int i = 0; i < 8; i++)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (lds_void*)(dst + (8 * wave + i) * 2 * HD), 16, voff[i],
-                                                     t * PK * HD * 2, 0, 0);
-    };
-    load_k(K0, 0);
-    load_v(V0, 0);
-    if (ntiles > 1) load_k(K1, 1);
-
-    half8 qf[2][8];
-    int qpos[2];
-#pragma unroll
-    for (int qt = 0; qt < 2; qt++) {
-        const int tq = q0 + WQ * wave + 16 * qt + n;
-        qpos[qt] = pos + tq;
-        const float* qr = q + b * qs.b + (long long)min(tq, T - 1) * qs.t + h * qs.h;
-        const float sl = scale * 1.4426950408889634f;
-#pragma unroll
-        for (int ks = 0; ks < 8; ks++) {
-            const float4 a0 = *(const float4*)(qr + 32 * ks + 8 * g);
-            const float4 a1 = *(const float4*)(qr + 32 * ks + 8 * g + 4);
-            qf[qt][ks] = half8{(_Float16)(a0.x * sl), (_Float16)(a0.y * sl), (_Float16)(a0.z * sl),
-                               (_Float16)(a0.w * sl), (_Float16)(a1.x * sl), (_Float16)(a1.y * sl),
-                               (_Float16)(a1.z * sl), (_Float16)(a1.w * sl)};
+        // direct loads: instruction i of this wave fills key rows 2 j, 2 j + 1 (j = 8 wave + i) of a
+        // tile; lane L writes LDS slot L % 32 of row 2 j + L / 32 with global slot (L % 32) ^ swizzle
+        const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc((void*)(kf + base), (short)0,
+                                                                           rows_pad * HD * 2, kBufWord3);
+        const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc((void*)(vf + base), (short)0,
+                                                                           rows_pad * HD * 2, kBufWord3);
+        int koff[8], voff[8];
+    #pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const int row = 2 * (8 * wave + i) + lane / 32, s = lane % 32;
+            koff[i] = (row * HD + sw_slot(s, row, KSW) * 8) * 2;
+            voff[i] = (row * HD + sw_slot(s, row, VSW) * 8) * 2;
         }
-    }
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-
-    f32x4 sc[2][4];
-    auto scores = [&](const uint16_t* Kt) {
-        half8 kb[3][4];
-        auto kaddr = [&](int nb, int ks) {
-            const int row = 16 * nb + n;
-            return (const half8*)&Kt[row * HD + sw_slot(4 * ks + g, row, KSW) * 8];
+        typedef __attribute__((address_space(3))) void lds_void;
+        auto load_k = [&](uint16_t* dst, int t) {
+    #pragma unroll
+            for (int i = 0; i < 8; i++)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (lds_void*)(dst + (8 * wave + i) * 2 * HD), 16, koff[i],
+                                                         t * PK * HD * 2, 0, 0);
         };
-#pragma unroll
-        for (int nb = 0; nb < 4; nb++) {
-            kb[0][nb] = *kaddr(nb, 0);
-            kb[1][nb] = *kaddr(nb, 1);
-#pragma unroll
-            for (int qt = 0; qt < 2; qt++) sc[qt][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
-        }
-#pragma unroll
-        for (int ks = 0; ks < 8; ks++) {
-#pragma unroll
-            for (int nb = 0; nb < 4; nb++)
-#pragma unroll
-                for (int qt = 0; qt < 2; qt++)
-                    sc[qt][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kb[ks % 3][nb], qf[qt][ks], sc[qt][nb], 0, 0, 0);
-            if (ks + 2 < 8) {
-#pragma unroll
-                for (int nb = 0; nb < 4; nb++) kb[(ks + 2) % 3][nb] = *kaddr(nb, ks + 2);
+        auto load_v = [&](uint16_t* dst, int t) {
+    #pragma unroll
+            for (int i = 0; i < 8; i++)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (lds_void*)(dst + (8 * wave + i) * 2 * HD), 16, voff[i],
+                                                         t * PK * HD * 2, 0, 0);
+        };
+        load_k(K0, 0);
+        load_v(V0, 0);
+        if (ntiles > 1) load_k(K1, 1);
+
+        half8 qf[2][8];
+        int qpos[2];
+    #pragma unroll
+        for (int qt = 0; qt < 2; qt++) {
+            const int tq = q0 + WQ * wave + 16 * qt + n;
+            qpos[qt] = pos + tq;
+            const float* qr = q + b * qs.b + (long long)min(tq, T - 1) * qs.t + h * qs.h;
+            const float sl = scale * 1.4426950408889634f;
+    #pragma unroll
+            for (int ks = 0; ks < 8; ks++) {
+                const float4 a0 = *(const float4*)(qr + 32 * ks + 8 * g);
+                const float4 a1 = *(const float4*)(qr + 32 * ks + 8 * g + 4);
+                qf[qt][ks] = half8{(_Float16)(a0.x * sl), (_Float16)(a0.y * sl), (_Float16)(a0.z * sl),
+                                   (_Float16)(a0.w * sl), (_Float16)(a1.x * sl), (_Float16)(a1.y * sl),
+                                   (_Float16)(a1.z * sl), (_Float16)(a1.w * sl)};
             }
-            __builtin_amdgcn_sched_barrier(0);
         }
-    };
-    // masked: the tile may hold keys past some query of the block; tiles wholly before the block's
-    // first query take the unmasked form (no compares or selects)
-    auto mask = [&](int key0, auto masked) {
-        if (decltype(masked)::value && key0 + PK - 1 > wave_first) {
-#pragma unroll
-            for (int qt = 0; qt < 2; qt++)
-#pragma unroll
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+
+        f32x4 sc[2][4];
+        auto scores = [&](const uint16_t* Kt) {
+            half8 kb[3][4];
+            auto kaddr = [&](int nb, int ks) {
+                const int row = 16 * nb + n;
+                return (const half8*)&Kt[row * HD + sw_slot(4 * ks + g, row, KSW) * 8];
+            };
+    #pragma unroll
+            for (int nb = 0; nb < 4; nb++) {
+                kb[0][nb] = *kaddr(nb, 0);
+                kb[1][nb] = *kaddr(nb, 1);
+    #pragma unroll
+                for (int qt = 0; qt < 2; qt++) sc[qt][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+            }
+    #pragma unroll
+            for (int ks = 0; ks < 8; ks++) {
+    #pragma unroll
                 for (int nb = 0; nb < 4; nb++)
-#pragma unroll
-                    for (int j = 0; j < 4; j++)
-                        if (key0 + 16 * nb + 4 * g + j > qpos[qt]) sc[qt][nb][j] = -INFINITY;
-        }
-    };
-    float ref[2] = {-INFINITY, -INFINITY}, lsum[2] = {0.f, 0.f}, corr[2] = {1.f, 1.f}, mt[2];
-    half8 pcur[2][2], pnext[2][2];
-    bool pend = false;
-    auto softmax_piece = [&](int piece) {
-        if (piece < 2) {
-            const int qt = piece;
-            float m = sc[qt][0][0];
-#pragma unroll
-            for (int nb = 0; nb < 4; nb++)
-#pragma unroll
-                for (int j = 0; j < 4; j++) m = fmaxf(m, sc[qt][nb][j]);
-            mt[qt] = m;
-        } else if (piece == 2) {
-#pragma unroll
-            for (int qt = 0; qt < 2; qt++) mt[qt] = group4_max(mt[qt]);
-        } else if (piece == 3) {
-            bool need_any = false;
-#pragma unroll
-            for (int qt = 0; qt < 2; qt++) {
-                const bool need = mt[qt] > ref[qt] + kLazyRef;
-                corr[qt] = need ? exp2f(ref[qt] - mt[qt]) : 1.f;
-                lsum[qt] *= corr[qt];
-                ref[qt] = need ? mt[qt] : ref[qt];
-                need_any |= need;
+    #pragma unroll
+                    for (int qt = 0; qt < 2; qt++)
+                        sc[qt][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kb[ks % 3][nb], qf[qt][ks], sc[qt][nb], 0, 0, 0);
+                if (ks + 2 < 8) {
+    #pragma unroll
+                    for (int nb = 0; nb < 4; nb++) kb[(ks + 2) % 3][nb] = *kaddr(nb, ks + 2);
+                }
+                __builtin_amdgcn_sched_barrier(0);
             }
-            pend = __ballot(need_any) != 0;
-        } else if (piece < 12) {
-            const int e4 = piece - 4;
-            const int qt = e4 >> 2, nb = e4 & 3;
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const float p = __builtin_amdgcn_exp2f(sc[qt][nb][j] - ref[qt]);
-                lsum[qt] += p;
-                pnext[qt][nb >> 1][4 * (nb & 1) + j] = (_Float16)p;
-            }
-        }
-    };
-    f32x4 oacc[2][16];
-#pragma unroll
-    for (int qt = 0; qt < 2; qt++)
-#pragma unroll
-        for (int db = 0; db < 16; db++) oacc[qt][db] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-    scores(K0);
-    mask(0, std::true_type{});
-#pragma unroll
-    for (int piece = 0; piece < 12; piece++) softmax_piece(piece);
-    pend = false;
-#pragma unroll
-    for (int qt = 0; qt < 2; qt++) {
-        pcur[qt][0] = pnext[qt][0];
-        pcur[qt][1] = pnext[qt][1];
-    }
-    __syncthreads();  // K0 free for K(2)
-
-    auto pv = [&](const uint16_t* Vt, auto side) {
-        bf16x8 vb[4][2];
-#pragma unroll
-        for (int d = 0; d < 3; d++) {
-            vb[d][0] = vt_operand_sw(Vt, 0, d, lane);
-            vb[d][1] = vt_operand_sw(Vt, 1, d, lane);
-        }
-#pragma unroll
-        for (int db = 0; db < 16; db++) {
-            if (db + 3 < 16) {
-                vb[(db + 3) & 3][0] = vt_operand_sw(Vt, 0, db + 3, lane);
-                vb[(db + 3) & 3][1] = vt_operand_sw(Vt, 1, db + 3, lane);
-            }
-#pragma unroll
-            for (int ks = 0; ks < 2; ks++)
-#pragma unroll
+        };
+        // masked: the tile may hold keys past some query of the block; tiles wholly before the block's
+        // first query take the unmasked form (no compares or selects)
+        auto mask = [&](int key0, auto masked) {
+            if (decltype(masked)::value && key0 + PK - 1 > wave_first) {
+    #pragma unroll
                 for (int qt = 0; qt < 2; qt++)
-                    oacc[qt][db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, vb[db & 3][ks]),
-                                                                          pcur[qt][ks], oacc[qt][db], 0, 0, 0);
-            side(db);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-    };
-    auto rescale = [&]() {
-        if (pend) {
-#pragma unroll
-            for (int qt = 0; qt < 2; qt++)
-#pragma unroll
-                for (int db = 0; db < 16; db++) oacc[qt][db] *= corr[qt];
-        }
+    #pragma unroll
+                    for (int nb = 0; nb < 4; nb++)
+    #pragma unroll
+                        for (int j = 0; j < 4; j++)
+                            if (key0 + 16 * nb + 4 * g + j > qpos[qt]) sc[qt][nb][j] = -INFINITY;
+            }
+        };
+        float ref[2] = {-INFINITY, -INFINITY}, lsum[2] = {0.f, 0.f}, corr[2] = {1.f, 1.f}, mt[2];
+        half8 pcur[2][2], pnext[2][2];
+        bool pend = false;
+        auto softmax_piece = [&](int piece) {
+            if (piece < 2) {
+                const int qt = piece;
+                float m = sc[qt][0][0];
+    #pragma unroll
+                for (int nb = 0; nb < 4; nb++)
+    #pragma unroll
+                    for (int j = 0; j < 4; j++) m = fmaxf(m, sc[qt][nb][j]);
+                mt[qt] = m;
+            } else if (piece == 2) {
+    #pragma unroll
+                for (int qt = 0; qt < 2; qt++) mt[qt] = group4_max(mt[qt]);
+            } else if (piece == 3) {
+                bool need_any = false;
+    #pragma unroll
+                for (int qt = 0; qt < 2; qt++) {
+                    const bool need = mt[qt] > ref[qt] + kLazyRef;
+                    corr[qt] = need ? exp2f(ref[qt] - mt[qt]) : 1.f;
+                    lsum[qt] *= corr[qt];
+                    ref[qt] = need ? mt[qt] : ref[qt];
+                    need_any |= need;
+                }
+                pend = __ballot(need_any) != 0;
+            } else if (piece < 12) {
+                const int e4 = piece - 4;
+                const int qt = e4 >> 2, nb = e4 & 3;
+    #pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const float p = __builtin_amdgcn_exp2f(sc[qt][nb][j] - ref[qt]);
+                    lsum[qt] += p;
+                    pnext[qt][nb >> 1][4 * (nb & 1) + j] = (_Float16)p;
+                }
+            }
+        };
+        f32x4 oacc[2][16];
+    #pragma unroll
+        for (int qt = 0; qt < 2; qt++)
+    #pragma unroll
+            for (int db = 0; db < 16; db++) oacc[qt][db] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+        scores(K0);
+        mask(0, std::true_type{});
+    #pragma unroll
+        for (int piece = 0; piece < 12; piece++) softmax_piece(piece);
         pend = false;
-    };
-    // iteration t: S of K(t + 1) (buffer Kn), P V of V(t) (buffer Vc); loads of K(t + 2) into
-    // the K buffer tile t used (Kc) and of V(t + 1) into the other V buffer (Vn)
-    auto iteration = [&](int t, uint16_t* Kc, uint16_t* Kn, uint16_t* Vc, uint16_t* Vn, auto masked) {
-        load_v(Vn, t + 1);
-        if (t + 2 < ntiles) load_k(Kc, t + 2);
-        rescale();
-        scores(Kn);
-        mask((t + 1) * PK, masked);
-        pv(Vc, [&](int db) {
-            if (db < 12) softmax_piece(db);
-        });
-#pragma unroll
+    #pragma unroll
         for (int qt = 0; qt < 2; qt++) {
             pcur[qt][0] = pnext[qt][0];
             pcur[qt][1] = pnext[qt][1];
         }
-        __builtin_amdgcn_s_waitcnt(0);  // this wave's direct loads have landed
-        __syncthreads();
-    };
-    // tiles below nfree end at or before the block's first query: no key of theirs is masked
-    const int nfree = (pos + q0 + 1) / PK;
-    int t = 0;
-    for (; t + 2 < ntiles && t + 2 < nfree; t += 2) {
-        iteration(t, K0, K1, V0, V1, std::false_type{});
-        iteration(t + 1, K1, K0, V1, V0, std::false_type{});
-    }
-    for (; t + 2 < ntiles; t += 2) {
-        iteration(t, K0, K1, V0, V1, std::true_type{});
-        iteration(t + 1, K1, K0, V1, V0, std::true_type{});
-    }
-    if (t + 1 < ntiles) {
-        iteration(t, K0, K1, V0, V1, std::true_type{});
-        t++;
-    }
-    rescale();
-    pv((t & 1) ? V1 : V0, [&](int) {});
+        __syncthreads();  // K0 free for K(2)
 
-#pragma unroll
-    for (int qt = 0; qt < 2; qt++) {
-        const float l = group4_sum(lsum[qt]);
-        const int tq = q0 + WQ * wave + 16 * qt + n;
-        const int tc = min(tq, T - 1);
-        f32x4 gf[16];
-        if (gate) {
-            const float* grow = gate + b * gs.b + (long long)tc * gs.t + h * gs.h;
-#pragma unroll
-            for (int db = 0; db < 16; db++) gf[db] = *(const f32x4*)(grow + 16 * db + 4 * g);
-#pragma unroll
-            for (int db = 0; db < 16; db++)
-#pragma unroll
-                for (int j = 0; j < 4; j++) gf[db][j] = sigmoid_rcp(gf[db][j]);
-        } else {
-#pragma unroll
-            for (int db = 0; db < 16; db++) gf[db] = f32x4{1.f, 1.f, 1.f, 1.f};
+        auto pv = [&](const uint16_t* Vt, auto side) {
+            bf16x8 vb[4][2];
+    #pragma unroll
+            for (int d = 0; d < 3; d++) {
+                vb[d][0] = vt_operand_sw(Vt, 0, d, lane);
+                vb[d][1] = vt_operand_sw(Vt, 1, d, lane);
+            }
+    #pragma unroll
+            for (int db = 0; db < 16; db++) {
+                if (db + 3 < 16) {
+                    vb[(db + 3) & 3][0] = vt_operand_sw(Vt, 0, db + 3, lane);
+                    vb[(db + 3) & 3][1] = vt_operand_sw(Vt, 1, db + 3, lane);
+                }
+    #pragma unroll
+                for (int ks = 0; ks < 2; ks++)
+    #pragma unroll
+                    for (int qt = 0; qt < 2; qt++)
+                        oacc[qt][db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, vb[db & 3][ks]),
+                                                                              pcur[qt][ks], oacc[qt][db], 0, 0, 0);
+                side(db);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        };
+        auto rescale = [&]() {
+            if (pend) {
+    #pragma unroll
+                for (int qt = 0; qt < 2; qt++)
+    #pragma unroll
+                    for (int db = 0; db < 16; db++) oacc[qt][db] *= corr[qt];
+            }
+            pend = false;
+        };
+        // iteration t: S of K(t + 1) (buffer Kn), P V of V(t) (buffer Vc); loads of K(t + 2) into
+        // the K buffer tile t used (Kc) and of V(t + 1) into the other V buffer (Vn)
+        auto iteration = [&](int t, uint16_t* Kc, uint16_t* Kn, uint16_t* Vc, uint16_t* Vn, auto masked) {
+            load_v(Vn, t + 1);
+            if (t + 2 < ntiles) load_k(Kc, t + 2);
+            rescale();
+            scores(Kn);
+            mask((t + 1) * PK, masked);
+            pv(Vc, [&](int db) {
+                if (db < 12) softmax_piece(db);
+            });
+    #pragma unroll
+            for (int qt = 0; qt < 2; qt++) {
+                pcur[qt][0] = pnext[qt][0];
+                pcur[qt][1] = pnext[qt][1];
+            }
+            __builtin_amdgcn_s_waitcnt(0);  // this wave's direct loads have landed
+            __syncthreads();
+        };
+        // tiles below nfree end at or before the block's first query: no key of theirs is masked
+        const int nfree = (pos + q0 + 1) / PK;
+        int t = 0;
+        for (; t + 2 < ntiles && t + 2 < nfree; t += 2) {
+            iteration(t, K0, K1, V0, V1, std::false_type{});
+            iteration(t + 1, K1, K0, V1, V0, std::false_type{});
         }
-        Tout* orow = out + b * os.b + (long long)tc * os.t + h * os.h;
-        const float inv = 1.f / l;
-        if (tq < T) {
-#pragma unroll
-            for (int db = 0; db < 16; db++) store4(orow + 16 * db + 4 * g, oacc[qt][db] * inv * gf[db]);
+        for (; t + 2 < ntiles; t += 2) {
+            iteration(t, K0, K1, V0, V1, std::true_type{});
+            iteration(t + 1, K1, K0, V1, V0, std::true_type{});
         }
+        if (t + 1 < ntiles) {
+            iteration(t, K0, K1, V0, V1, std::true_type{});
+            t++;
+        }
+        rescale();
+        pv((t & 1) ? V1 : V0, [&](int) {});
+
+    #pragma unroll
+        for (int qt = 0; qt < 2; qt++) {
+            const float l = group4_sum(lsum[qt]);
+            const int tq = q0 + WQ * wave + 16 * qt + n;
+            const int tc = min(tq, T - 1);
+            f32x4 gf[16];
+            if (gate) {
+                const float* grow = gate + b * gs.b + (long long)tc * gs.t + h * gs.h;
+    #pragma unroll
+                for (int db = 0; db < 16; db++) gf[db] = *(const f32x4*)(grow + 16 * db + 4 * g);
+    #pragma unroll
+                for (int db = 0; db < 16; db++)
+    #pragma unroll
+                    for (int j = 0; j < 4; j++) gf[db][j] = sigmoid_rcp(gf[db][j]);
+            } else {
+    #pragma unroll
+                for (int db = 0; db < 16; db++) gf[db] = f32x4{1.f, 1.f, 1.f, 1.f};
+            }
+            Tout* orow = out + b * os.b + (long long)tc * os.t + h * os.h;
+            const float inv = 1.f / l;
+            if (tq < T) {
+    #pragma unroll
+                for (int db = 0; db < 16; db++) store4(orow + 16 * db + 4 * g, oacc[qt][db] * inv * gf[db]);
+            }
+        }
+        __syncthreads();  // every wave is done with the tile buffers before the next item's loads
     }
 }
 
@@ -1418,6 +1436,19 @@ int launch_decode_core(const float* q, const uint16_t* kc, const uint16_t* vc, c
     return after_launch("attention_decode_merge");
 }
 
+// compute units of the current device (cached per device; the persistent prefill grid)
+static int device_cus() {
+    static int cus[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (!cus[dev]) {
+        int c = 0;
+        if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0) c = 256;
+        cus[dev] = c;
+    }
+    return cus[dev];
+}
+
 // bytes of the fp16 K / V copies the prefill kernel reads when given that much workspace
 size_t prefill_f16_bytes(int B, int KV, int rows) {
     const size_t rows_pad = (size_t)(rows + PK - 1) / PK * PK;
@@ -1451,15 +1482,15 @@ int launch_prefill_core(const float* q, Strides3 qs, const uint16_t* kc, const u
         attn_kv_f16_kernel<<<cblocks, 256, 0, st>>>(kc, vc, kf, vf, KV, cap, rows, rows_pad, nchunks);
         int rc = after_launch("attention_prefill_f16_copy");
         if (rc) return rc;
-        const int nblk = (T + PQ2 - 1) / PQ2 * H * B, per_xcd = (nblk + 7) / 8;
+        const int nblk = (T + PQ2 - 1) / PQ2 * H * B;
+        const int grid = std::min(nblk, device_cus());  // one workgroup per CU (128 KB of LDS each)
         if (out_bf16) {
-            attn_prefill_w32f_kernel<uint16_t><<<8 * per_xcd, 64 * PW2, 0, st>>>(q, qs, kf, vf, rows_pad, gate, gs,
-                                                                                out_bf16, os, H, KV, T, pos, scale, B,
-                                                                                per_xcd);
+            attn_prefill_w32f_kernel<uint16_t><<<grid, 64 * PW2, 0, st>>>(q, qs, kf, vf, rows_pad, gate, gs, out_bf16,
+                                                                         os, H, KV, T, pos, scale, B);
             if (wrote_bf16) *wrote_bf16 = true;
         } else {
-            attn_prefill_w32f_kernel<float><<<8 * per_xcd, 64 * PW2, 0, st>>>(q, qs, kf, vf, rows_pad, gate, gs, out,
-                                                                             os, H, KV, T, pos, scale, B, per_xcd);
+            attn_prefill_w32f_kernel<float><<<grid, 64 * PW2, 0, st>>>(q, qs, kf, vf, rows_pad, gate, gs, out, os, H,
+                                                                      KV, T, pos, scale, B);
         }
     } else if (T >= 16 && vec && w32) {
         const int nblk = (T + PQ2 - 1) / PQ2 * H * B, per_xcd = (nblk + 7) / 8;
