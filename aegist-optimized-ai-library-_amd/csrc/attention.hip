@@ -1277,6 +1277,10 @@ __global__ void __launch_bounds__(64 * PW2, 1) attn_prefill_w32f_kernel(const fl
                     lsum[qt] += p;
                     pnext[qt][nb >> 1][4 * (nb & 1) + j] = (_Float16)p;
                 }
+                // pin the exponentials here, among this tile's products: otherwise they are sunk to their
+                // first use after the loop's barrier, where nothing overlaps them
+                if (nb & 1) asm volatile("" : "+v"(pnext[qt][nb >> 1]));
+                asm volatile("" : "+v"(lsum[qt]));
             }
         };
         f32x4 oacc[2][16];
