@@ -313,23 +313,25 @@ __global__ void __launch_bounds__(256) znorm_bf16_vec_kernel(const float* __rest
                                                              uint16_t* __restrict__ out, int D, float eps) {
     __shared__ float red[4];
     const float4* xr = (const float4*)(x + (size_t)blockIdx.x * D);
+    const uint2* wr = (const uint2*)w;
     float4 v[NV];
+    uint2 wp[NV];  // the norm weights are loaded with x, ahead of the block sum
     float ss = 0.f;
 #pragma unroll
     for (int i = 0; i < NV; i++) {
         v[i] = xr[threadIdx.x + 256 * i];
-        ss += v[i].x * v[i].x + v[i].y * v[i].y + v[i].z * v[i].z + v[i].w * v[i].w;
+        wp[i] = wr[threadIdx.x + 256 * i];
     }
+#pragma unroll
+    for (int i = 0; i < NV; i++) ss += v[i].x * v[i].x + v[i].y * v[i].y + v[i].z * v[i].z + v[i].w * v[i].w;
     ss = block_sum(ss, red);
     const float inv = rsqrtf(ss / (float)D + eps);
     uint2* orow = (uint2*)(out + (size_t)blockIdx.x * D);
-    const uint2* wr = (const uint2*)w;
 #pragma unroll
     for (int i = 0; i < NV; i++) {
         const int e = threadIdx.x + 256 * i;
-        const uint2 wp = wr[e];
-        orow[e] = uint2{f2bf2((v[i].x * inv) * (1.f + bf_lo(wp.x)), (v[i].y * inv) * (1.f + bf_hi(wp.x))),
-                        f2bf2((v[i].z * inv) * (1.f + bf_lo(wp.y)), (v[i].w * inv) * (1.f + bf_hi(wp.y)))};
+        orow[e] = uint2{f2bf2((v[i].x * inv) * (1.f + bf_lo(wp[i].x)), (v[i].y * inv) * (1.f + bf_hi(wp[i].x))),
+                        f2bf2((v[i].z * inv) * (1.f + bf_lo(wp[i].y)), (v[i].w * inv) * (1.f + bf_hi(wp[i].y)))};
     }
 }
 
@@ -341,33 +343,51 @@ __global__ void __launch_bounds__(256) znorm_bf16_acc_vec_kernel(float* __restri
                                                                  uint16_t* __restrict__ out, int D, float eps) {
     __shared__ float red[4];
     float4* xr = (float4*)(x + (size_t)blockIdx.x * D);
+    const uint2* wr = (const uint2*)w;
+    // every load is issued before the first use: the norm weights (needed only after the block
+    // sum), x and the first four slices (clamped indices past nks, masked out of the sum)
+    uint2 wp[NV];
+    float4 a[NV], ps[4][NV];
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+        const int e = threadIdx.x + 256 * i;
+        if (out) wp[i] = wr[e];
+        a[i] = xr[e];
+#pragma unroll
+        for (int s = 0; s < 4; s++)
+            ps[s][i] = ((const float4*)(part + (size_t)(s < nks ? s : 0) * slice + (size_t)blockIdx.x * D))[e];
+    }
     float4 v[NV];
     float ss = 0.f;
 #pragma unroll
     for (int i = 0; i < NV; i++) {
         const int e = threadIdx.x + 256 * i;
-        float4 a = xr[e];
-        float4 p = ((const float4*)(part + (size_t)blockIdx.x * D))[e];
-        for (int s = 1; s < nks; s++) {
+        // slices added in order s = 0, 1, ...
+        float4 p = ps[0][i];
+#pragma unroll
+        for (int s = 1; s < 4; s++)
+            if (s < nks) {
+                p.x += ps[s][i].x; p.y += ps[s][i].y; p.z += ps[s][i].z; p.w += ps[s][i].w;
+            }
+        for (int s = 4; s < nks; s++) {
             const float4 q = ((const float4*)(part + s * slice + (size_t)blockIdx.x * D))[e];
             p.x += q.x; p.y += q.y; p.z += q.z; p.w += q.w;
         }
-        a.x += p.x; a.y += p.y; a.z += p.z; a.w += p.w;
-        xr[e] = a;
-        v[i] = a;
-        ss += a.x * a.x + a.y * a.y + a.z * a.z + a.w * a.w;
+        float4 y = a[i];
+        y.x += p.x; y.y += p.y; y.z += p.z; y.w += p.w;
+        xr[e] = y;
+        v[i] = y;
+        ss += y.x * y.x + y.y * y.y + y.z * y.z + y.w * y.w;
     }
     ss = block_sum(ss, red);
     const float inv = rsqrtf(ss / (float)D + eps);
     if (!out) return;
     uint2* orow = (uint2*)(out + (size_t)blockIdx.x * D);
-    const uint2* wr = (const uint2*)w;
 #pragma unroll
     for (int i = 0; i < NV; i++) {
         const int e = threadIdx.x + 256 * i;
-        const uint2 wp = wr[e];
-        orow[e] = uint2{f2bf2((v[i].x * inv) * (1.f + bf_lo(wp.x)), (v[i].y * inv) * (1.f + bf_hi(wp.x))),
-                        f2bf2((v[i].z * inv) * (1.f + bf_lo(wp.y)), (v[i].w * inv) * (1.f + bf_hi(wp.y)))};
+        orow[e] = uint2{f2bf2((v[i].x * inv) * (1.f + bf_lo(wp[i].x)), (v[i].y * inv) * (1.f + bf_hi(wp[i].x))),
+                        f2bf2((v[i].z * inv) * (1.f + bf_lo(wp[i].y)), (v[i].w * inv) * (1.f + bf_hi(wp[i].y)))};
     }
 }
 
