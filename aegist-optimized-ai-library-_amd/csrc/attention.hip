@@ -392,6 +392,18 @@ __global__ void __launch_bounds__(256) attn_decode_merge_wide_kernel(const float
     float gv[4];
 #pragma unroll
     for (int e = 0; e < 4; e++) gv[e] = gate ? Act<TG>::ld(gate, row * gate_row_stride + 4 * q4 + e) : 0.f;
+    // this thread's splits s = sg, sg + 4, ..., in batches of SB loads in flight; the first batch
+    // is issued here, ahead of the statistics' reductions
+    constexpr int SB = 8;
+    f32x4 v[SB];
+    auto load_batch = [&](int s0) {
+#pragma unroll
+        for (int e = 0; e < SB; e++) {
+            const int sp = min(s0 + 4 * e, nsplit - 1);
+            v[e] = *(const f32x4*)(part + ((base + sp) * G + r) * HD + 4 * q4);
+        }
+    };
+    load_batch(sg);
     float mx = wave_max(st.x);
     if (lane == 0) red[0][wave] = mx;
     __syncthreads();
@@ -402,16 +414,9 @@ __global__ void __launch_bounds__(256) attn_decode_merge_wide_kernel(const float
     if (lane == 0) red[1][wave] = ls;
     __syncthreads();
     ls = (red[1][0] + red[1][1]) + (red[1][2] + red[1][3]);
-    // this thread's splits s = sg, sg + 4, ..., in batches of 8 loads in flight
     f32x4 a = {0.f, 0.f, 0.f, 0.f};
-    constexpr int SB = 8;
     for (int s0 = sg; s0 < nsplit; s0 += 4 * SB) {
-        f32x4 v[SB];
-#pragma unroll
-        for (int e = 0; e < SB; e++) {
-            const int sp = min(s0 + 4 * e, nsplit - 1);
-            v[e] = *(const f32x4*)(part + ((base + sp) * G + r) * HD + 4 * q4);
-        }
+        if (s0 != sg) load_batch(s0);
 #pragma unroll
         for (int e = 0; e < SB; e++) {
             const int sp = s0 + 4 * e;

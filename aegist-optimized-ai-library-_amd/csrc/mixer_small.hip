@@ -54,19 +54,24 @@ __global__ void __launch_bounds__(256) attn_prep_kernel(
     const int h = isq ? hh : hh - H;
     const Tin* src = isq ? qg + (((size_t)b * T + t) * H + h) * 2 * HD : k + (((size_t)b * T + t) * KV + h) * HD;
     const uint16_t* nw = isq ? qw : kw;
-    float x[4], ss = 0.f;
+    const Tin* vs = v + (((size_t)b * T + t) * KV + (isq ? 0 : h)) * HD;
+    // the row, its norm weights and (key heads) the value row are all loaded up front
+    float x[4], wn[4], vv[4], ss = 0.f;
 #pragma unroll
     for (int r = 0; r < 4; r++) {
         int i = lane + r * WAVE;
         x[r] = i < HD ? Act<Tin>::ld(src, i) : 0.f;
-        ss += x[r] * x[r];
+        wn[r] = i < HD ? bf2f(nw[i]) : 0.f;
+        vv[r] = i < HD && !isq ? Act<Tin>::ld(vs, i) : 0.f;
     }
+#pragma unroll
+    for (int r = 0; r < 4; r++) ss += x[r] * x[r];
     ss = wave_sum(ss);
     const float inv = rsqrtf(ss / (float)HD + eps);
 #pragma unroll
     for (int r = 0; r < 4; r++) {
         int i = lane + r * WAVE;
-        x[r] = i < HD ? (x[r] * inv) * (1.f + bf2f(nw[i])) : 0.f;
+        x[r] = i < HD ? (x[r] * inv) * (1.f + wn[r]) : 0.f;
         buf[wave][i] = x[r];
     }
     __syncthreads();
@@ -95,13 +100,12 @@ __global__ void __launch_bounds__(256) attn_prep_kernel(
         }
     } else {
         size_t o = (((size_t)b * KV + h) * cap + pos) * HD;
-        const Tin* vs = v + (((size_t)b * T + t) * KV + h) * HD;
 #pragma unroll
         for (int r = 0; r < 4; r++) {
             int i = lane + r * WAVE;
             if (i < HD) {
                 kc[o + i] = f2bf(outv[r]);
-                vc[o + i] = f2bf(Act<Tin>::ld(vs, i));
+                vc[o + i] = f2bf(vv[r]);
             }
         }
     }
