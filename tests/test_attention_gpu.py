@@ -74,6 +74,9 @@ def test_attention_decode_bf16_out(dev):
                                                 (2, 8, 2, 64, 0, 0.5, 1), (1, 16, 2, 130, 5, 0.5, 1),
                                                 (1, 16, 2, 1000, 0, 0.5, 1), (2, 16, 2, 300, 500, 0.5, 1),
                                                 (1, 4, 4, 77, 3, 0.5, 1),
+                                                # (sequence, KV head) pairs a multiple of 8: the
+                                                # persistent schedule's per-XCD pair ownership
+                                                (4, 16, 2, 300, 0, 0.5, 1), (8, 8, 2, 256, 20, 0.5, 1),
                                                 # sharp softmax (scores ~ +-30) and large / small V
                                                 (1, 16, 2, 260, 0, 3.0, 1), (1, 8, 2, 200, 40, 0.5, 300),
                                                 (1, 8, 2, 200, 40, 0.5, 1e-3)])
