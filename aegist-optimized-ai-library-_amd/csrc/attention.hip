@@ -1207,86 +1207,116 @@ __global__ void __launch_bounds__(64 * PW2, 1) attn_prefill_w32f_kernel(const fl
         __syncthreads();
 
         f32x4 sc[2][4];
-        auto scores = [&](const uint16_t* Kt) {
-            half8 kb[3][4];
-            auto kaddr = [&](int nb, int ks) {
-                const int row = 16 * nb + n;
-                return (const half8*)&Kt[row * HD + sw_slot(4 * ks + g, row, KSW) * 8];
-            };
-    #pragma unroll
-            for (int nb = 0; nb < 4; nb++) {
-                kb[0][nb] = *kaddr(nb, 0);
-                kb[1][nb] = *kaddr(nb, 1);
-    #pragma unroll
-                for (int qt = 0; qt < 2; qt++) sc[qt][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
-            }
-    #pragma unroll
-            for (int ks = 0; ks < 8; ks++) {
-    #pragma unroll
-                for (int nb = 0; nb < 4; nb++)
-    #pragma unroll
-                    for (int qt = 0; qt < 2; qt++)
-                        sc[qt][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kb[ks % 3][nb], qf[qt][ks], sc[qt][nb], 0, 0, 0);
-                if (ks + 2 < 8) {
-    #pragma unroll
-                    for (int nb = 0; nb < 4; nb++) kb[(ks + 2) % 3][nb] = *kaddr(nb, ks + 2);
-                }
-                __builtin_amdgcn_sched_barrier(0);
-            }
-        };
-        // masked: the tile may hold keys past some query of the block; tiles wholly before the block's
-        // first query take the unmasked form (no compares or selects)
-        auto mask = [&](int key0, auto masked) {
+        float ref[2] = {-INFINITY, -INFINITY}, lsum[2] = {0.f, 0.f}, corr[2] = {1.f, 1.f};
+        float lsave[2], mx[2];
+        half8 pcur[2][2], pnext[2][2];
+        bool pend = false;
+        // masked: the tile may hold keys past some query of the block; tiles wholly before the
+        // block's first query take the unmasked form (no compares or selects). nb0: first of the
+        // two key blocks of 16 it covers.
+        auto mask = [&](int key0, int nb0, auto masked) __attribute__((always_inline)) {
             if (decltype(masked)::value && key0 + PK - 1 > wave_first) {
     #pragma unroll
                 for (int qt = 0; qt < 2; qt++)
     #pragma unroll
-                    for (int nb = 0; nb < 4; nb++)
+                    for (int nb = nb0; nb < nb0 + 2; nb++)
     #pragma unroll
                         for (int j = 0; j < 4; j++)
                             if (key0 + 16 * nb + 4 * g + j > qpos[qt]) sc[qt][nb][j] = -INFINITY;
             }
         };
-        float ref[2] = {-INFINITY, -INFINITY}, lsum[2] = {0.f, 0.f}, corr[2] = {1.f, 1.f}, mt[2];
-        half8 pcur[2][2], pnext[2][2];
-        bool pend = false;
-        auto softmax_piece = [&](int piece) {
-            if (piece < 2) {
-                const int qt = piece;
-                float m = sc[qt][0][0];
+        // Softmax of a tile, in pieces placed among the products. The exponentials are taken
+        // against the current (lazy) reference straight away, so the first two key blocks' pieces
+        // run among the last score products of the tile; each piece also keeps this lane's
+        // maximum. finish() then checks whether some row's maximum passed the reference by more
+        // than 2^8: only then (the first tile, and rarely after) are the row maxima reduced and,
+        // where needed, the reference moved, the row sum rescaled and the exponentials taken again
+        // - the same values and order of operations as reducing the maxima first.
+        auto begin_tile = [&]() __attribute__((always_inline)) {
     #pragma unroll
-                for (int nb = 0; nb < 4; nb++)
+            for (int qt = 0; qt < 2; qt++) {
+                lsave[qt] = lsum[qt];
+                mx[qt] = -INFINITY;
+            }
+        };
+        auto exp_piece = [&](int qt, int nb) __attribute__((always_inline)) {
     #pragma unroll
-                    for (int j = 0; j < 4; j++) m = fmaxf(m, sc[qt][nb][j]);
-                mt[qt] = m;
-            } else if (piece == 2) {
+            for (int j = 0; j < 4; j++) {
+                mx[qt] = fmaxf(mx[qt], sc[qt][nb][j]);
+                const float p = __builtin_amdgcn_exp2f(sc[qt][nb][j] - ref[qt]);
+                lsum[qt] += p;
+                pnext[qt][nb >> 1][4 * (nb & 1) + j] = (_Float16)p;
+            }
+            // pin the exponentials here, among this tile's products: otherwise they are sunk to
+            // their first use after the loop's barrier, where nothing overlaps them
+            if (nb & 1) asm volatile("" : "+v"(pnext[qt][nb >> 1]));
+            asm volatile("" : "+v"(lsum[qt]));
+        };
+        auto finish = [&]() __attribute__((always_inline)) {
+            bool over = false;
     #pragma unroll
-                for (int qt = 0; qt < 2; qt++) mt[qt] = group4_max(mt[qt]);
-            } else if (piece == 3) {
+            for (int qt = 0; qt < 2; qt++) over |= mx[qt] > ref[qt] + kLazyRef;
+            pend = false;
+            if (__ballot(over) != 0) {
                 bool need_any = false;
     #pragma unroll
                 for (int qt = 0; qt < 2; qt++) {
-                    const bool need = mt[qt] > ref[qt] + kLazyRef;
-                    corr[qt] = need ? exp2f(ref[qt] - mt[qt]) : 1.f;
-                    lsum[qt] *= corr[qt];
-                    ref[qt] = need ? mt[qt] : ref[qt];
+                    const float mt = group4_max(mx[qt]);
+                    const bool need = mt > ref[qt] + kLazyRef;
+                    corr[qt] = need ? exp2f(ref[qt] - mt) : 1.f;
+                    lsum[qt] = lsave[qt] * corr[qt];
+                    ref[qt] = need ? mt : ref[qt];
                     need_any |= need;
+    #pragma unroll
+                    for (int nb = 0; nb < 4; nb++)
+    #pragma unroll
+                        for (int j = 0; j < 4; j++) {
+                            const float p = __builtin_amdgcn_exp2f(sc[qt][nb][j] - ref[qt]);
+                            lsum[qt] += p;
+                            pnext[qt][nb >> 1][4 * (nb & 1) + j] = (_Float16)p;
+                        }
                 }
                 pend = __ballot(need_any) != 0;
-            } else if (piece < 12) {
-                const int e4 = piece - 4;
-                const int qt = e4 >> 2, nb = e4 & 3;
-    #pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    const float p = __builtin_amdgcn_exp2f(sc[qt][nb][j] - ref[qt]);
-                    lsum[qt] += p;
-                    pnext[qt][nb >> 1][4 * (nb & 1) + j] = (_Float16)p;
-                }
-                // pin the exponentials here, among this tile's products: otherwise they are sunk to their
-                // first use after the loop's barrier, where nothing overlaps them
-                if (nb & 1) asm volatile("" : "+v"(pnext[qt][nb >> 1]));
-                asm volatile("" : "+v"(lsum[qt]));
             }
+        };
+        // scores of a tile in two halves (key blocks 0-1, then 2-3), each over the 8 k steps;
+        // the first half's masked softmax pieces run among the second half's products
+        auto scores = [&](const uint16_t* Kt, int key0, auto masked) __attribute__((always_inline)) {
+            auto kaddr = [&](int nb, int ks) {
+                const int row = 16 * nb + n;
+                return (const half8*)&Kt[row * HD + sw_slot(4 * ks + g, row, KSW) * 8];
+            };
+    #pragma unroll
+            for (int h = 0; h < 2; h++) {
+                half8 kb[3][2];
+    #pragma unroll
+                for (int i = 0; i < 2; i++) {
+                    kb[0][i] = *kaddr(2 * h + i, 0);
+                    kb[1][i] = *kaddr(2 * h + i, 1);
+    #pragma unroll
+                    for (int qt = 0; qt < 2; qt++) sc[qt][2 * h + i] = f32x4{0.f, 0.f, 0.f, 0.f};
+                }
+    #pragma unroll
+                for (int ks = 0; ks < 8; ks++) {
+    #pragma unroll
+                    for (int i = 0; i < 2; i++)
+    #pragma unroll
+                        for (int qt = 0; qt < 2; qt++)
+                            sc[qt][2 * h + i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kb[ks % 3][i], qf[qt][ks],
+                                                                                     sc[qt][2 * h + i], 0, 0, 0);
+                    if (ks + 2 < 8) {
+    #pragma unroll
+                        for (int i = 0; i < 2; i++) kb[(ks + 2) % 3][i] = *kaddr(2 * h + i, ks + 2);
+                    }
+                    if (h == 1 && ks < 4) exp_piece(ks >> 1, ks & 1);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                if (h == 0) {
+                    mask(key0, 0, masked);
+                    begin_tile();
+                }
+            }
+            mask(key0, 2, masked);
         };
         f32x4 oacc[2][16];
     #pragma unroll
@@ -1294,10 +1324,10 @@ __global__ void __launch_bounds__(64 * PW2, 1) attn_prefill_w32f_kernel(const fl
     #pragma unroll
             for (int db = 0; db < 16; db++) oacc[qt][db] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-        scores(K0);
-        mask(0, std::true_type{});
+        scores(K0, 0, std::true_type{});
     #pragma unroll
-        for (int piece = 0; piece < 12; piece++) softmax_piece(piece);
+        for (int e = 0; e < 4; e++) exp_piece(e >> 1, 2 + (e & 1));
+        finish();
         pend = false;
     #pragma unroll
         for (int qt = 0; qt < 2; qt++) {
@@ -1344,11 +1374,11 @@ __global__ void __launch_bounds__(64 * PW2, 1) attn_prefill_w32f_kernel(const fl
             load_v(Vn, t + 1);
             if (t + 2 < ntiles) load_k(Kc, t + 2);
             rescale();
-            scores(Kn);
-            mask((t + 1) * PK, masked);
+            scores(Kn, (t + 1) * PK, masked);
             pv(Vc, [&](int db) {
-                if (db < 12) softmax_piece(db);
+                if (db < 4) exp_piece(db >> 1, 2 + (db & 1));
             });
+            finish();
     #pragma unroll
             for (int qt = 0; qt < 2; qt++) {
                 pcur[qt][0] = pnext[qt][0];
