@@ -111,6 +111,77 @@ __global__ void __launch_bounds__(256) attn_prep_kernel(
     }
 }
 
+// 4 consecutive activations as fp32 (one 16-byte load for fp32, one 8-byte load for bf16)
+template <typename T> __device__ __forceinline__ void ld4(const T* p, float* o);
+template <> __device__ __forceinline__ void ld4<float>(const float* p, float* o) {
+    const float4 a = *(const float4*)p;
+    o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w;
+}
+template <> __device__ __forceinline__ void ld4<uint16_t>(const uint16_t* p, float* o) {
+    const uint2 a = *(const uint2*)p;
+    o[0] = bf_lo(a.x); o[1] = bf_hi(a.x); o[2] = bf_lo(a.y); o[3] = bf_hi(a.y);
+}
+
+// The same per (token, head) wave with 4 consecutive elements per lane (16-byte loads and
+// stores) and the RoPE partner - element e +- RD/2, which sits RD/8 lanes away with the same
+// slot - taken by lane shuffle, so there is no LDS exchange or workgroup barrier. For HD a
+// multiple of 4 up to 256 and RD a multiple of 8.
+template <typename Tin>
+__global__ void __launch_bounds__(256) attn_prep_vec_kernel(
+    const Tin* __restrict__ qg, const Tin* __restrict__ k, const Tin* __restrict__ v, const uint16_t* __restrict__ qw,
+    const uint16_t* __restrict__ kw, float* __restrict__ qn, uint16_t* __restrict__ kc, uint16_t* __restrict__ vc,
+    int B, int T, int H, int KV, int HD, int RD, int pos0, int cap, float eps, RopeTable rope) {
+    const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+    const int item = blockIdx.x * 4 + wave;  // (b, t, head) flattened
+    const int heads = H + KV;
+    if (item >= B * T * heads) return;
+    const int hh = item % heads, t = (item / heads) % T, b = item / (heads * T);
+    const bool isq = hh < H;
+    const int h = isq ? hh : hh - H;
+    const Tin* src = isq ? qg + (((size_t)b * T + t) * H + h) * 2 * HD : k + (((size_t)b * T + t) * KV + h) * HD;
+    const Tin* vs = v + (((size_t)b * T + t) * KV + (isq ? 0 : h)) * HD;
+    const uint16_t* nw = isq ? qw : kw;
+    const int e0 = 4 * lane;
+    const bool act = e0 < HD;
+    // the row, its norm weights and (key heads) the value row, all requested up front
+    float x[4] = {0.f, 0.f, 0.f, 0.f}, vv[4] = {0.f, 0.f, 0.f, 0.f}, wn[4] = {0.f, 0.f, 0.f, 0.f};
+    if (act) {
+        ld4<Tin>(src + e0, x);
+        const uint2 wp = *(const uint2*)(nw + e0);
+        wn[0] = bf_lo(wp.x); wn[1] = bf_hi(wp.x); wn[2] = bf_lo(wp.y); wn[3] = bf_hi(wp.y);
+        if (!isq) ld4<Tin>(vs + e0, vv);
+    }
+    float ss = (x[0] * x[0] + x[1] * x[1]) + (x[2] * x[2] + x[3] * x[3]);
+    ss = wave_sum(ss);
+    const float inv = rsqrtf(ss / (float)HD + eps);
+    float y[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) y[r] = (x[r] * inv) * (1.f + wn[r]);
+    const int half = RD / 2, pos = pos0 + t;
+    const int plane = e0 < half ? lane + half / 4 : lane - half / 4;  // partner lane (RoPE dims)
+    float outv[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const float yp = __shfl(y[r], plane < 0 ? 0 : (plane > 63 ? 63 : plane), WAVE);
+        const int i = e0 + r;
+        outv[r] = y[r];
+        if (i < RD) {
+            const int j = i < half ? i : i - half;
+            float sn, c;
+            sincosf((float)pos * rope.inv[j], &sn, &c);
+            outv[r] = y[r] * c + (i < half ? -yp : yp) * sn;
+        }
+    }
+    if (!act) return;
+    if (isq) {
+        *(float4*)(qn + (((size_t)b * T + t) * H + h) * HD + e0) = float4{outv[0], outv[1], outv[2], outv[3]};
+    } else {
+        const size_t o = (((size_t)b * KV + h) * cap + pos) * HD + e0;
+        *(uint2*)(kc + o) = uint2{f2bf2(outv[0], outv[1]), f2bf2(outv[2], outv[3])};
+        *(uint2*)(vc + o) = uint2{f2bf2(vv[0], vv[1]), f2bf2(vv[2], vv[3])};
+    }
+}
+
 namespace aegist {
 int make_rope_table(RopeTable* tab, int RD, float theta) {
     if (RD <= 0 || (RD & 1) || RD > 256) return fail(AEGIST_ERR_SHAPE, "rope: rotary dim must be even and in [2, 256]");
@@ -130,6 +201,22 @@ int launch_attn_prep(const void* qg, const void* k, const void* v, int in_dtype,
     int items = B * T * (H + KV);
     if (items == 0) return 0;
     dim3 grid((items + 3) / 4);
+    // 16-byte (fp32) or 8-byte (bf16) element runs: every row start and the bases aligned so
+    const size_t es = in_dtype == AEGIST_F32 ? 4 : 2;
+    const bool vec = HD % 4 == 0 && RD % 8 == 0 && (uintptr_t)qg % (4 * es) == 0 && (uintptr_t)k % (4 * es) == 0 &&
+                     (uintptr_t)v % (4 * es) == 0 && (uintptr_t)qn % 16 == 0 && (uintptr_t)kc % 8 == 0 &&
+                     (uintptr_t)vc % 8 == 0 && (uintptr_t)qw % 8 == 0 && (uintptr_t)kw % 8 == 0;
+    if (vec && in_dtype == AEGIST_F32) {
+        attn_prep_vec_kernel<float><<<grid, 256, 0, stream>>>((const float*)qg, (const float*)k, (const float*)v, qw, kw,
+                                                              qn, kc, vc, B, T, H, KV, HD, RD, pos0, cap, eps, tab);
+        return after_launch("attn_prep");
+    }
+    if (vec && in_dtype == AEGIST_BF16) {
+        attn_prep_vec_kernel<uint16_t><<<grid, 256, 0, stream>>>((const uint16_t*)qg, (const uint16_t*)k,
+                                                                 (const uint16_t*)v, qw, kw, qn, kc, vc, B, T, H, KV,
+                                                                 HD, RD, pos0, cap, eps, tab);
+        return after_launch("attn_prep");
+    }
     if (in_dtype == AEGIST_F32)
         attn_prep_kernel<float><<<grid, 256, 0, stream>>>((const float*)qg, (const float*)k, (const float*)v, qw, kw, qn,
                                                           kc, vc, B, T, H, KV, HD, RD, pos0, cap, eps, tab);
