@@ -1,982 +1,923 @@
-// Chunked (C = 64) WY-form prefill of the gated delta rule on gfx950 MFMA.
+// Chunked (C = 64) WY-form prefill of the gated delta rule on gfx950 MFMA, fused and
+// sequence-parallel.
 //
-// Per chunk with cum = cumsum(g) and the L2-normalised rows q_n, k_n (hybrid.py:327-361):
-//   A     = strict_lower( beta_i e^{cum_i - cum_j} k_n,i . k_n,j )
-//   u     = (I + A)^-1 (beta v),   w = (I + A)^-1 (beta e^{cum} k_n)
-//   intra = lower_incl( e^{cum_i - cum_j} q_n,i . k_n,j )
-//   v_new = u - w S;  o = e^{cum} (q_n S) + intra v_new;  S = e^{cum_last} S + k_n^T (e^{cum_last - cum} v_new)
+// Per chunk, with cum = cumsum(g), row norms rq, rk (L2 normalisation, q scale folded into rq)
+// and the raw q, k, v rows (hybrid.py:327-361):
+//   A      = strict_lower( beta_i rk_i rk_j e^{cum_i - cum_j} k_i . k_j )
+//   v_new  = (I + A)^-1 ( beta v - beta rk e^{cum} (k S) )            [= u - w S]
+//   o      = rq e^{cum} (q S) + intra v_new,   intra = lower_incl( rq_i rk_j e^{cum_i - cum_j} q_i . k_j )
+//   S      = e^{cum_last} S + k^T ( rk e^{cum_last - cum} v_new )
 //
-// Two kernels per segment of up to SEG tokens (a segment's workspace stays resident in the
-// MALL between the two launches). With more than one segment the workspace holds two segment
-// buffers, and K2 of segment s and K1 of segment s+1 run as one grid (delta_chunk_fused) on the
-// caller's stream: K2's few long-lived workgroups keep part of each CU busy, K1's fill the rest.
-//  K1 delta_chunk_intra: one workgroup per (sequence, value head, chunk), fully parallel.
-//     Normalises q, k in fp32 and keeps them as fp16 in LDS; k_n k_n^T and q_n k_n^T on
-//     v_mfma_f32_16x16x32_f16 (lower-triangular blocks only); decay and beta applied in fp32 on
-//     the accumulators; the inverses of the four 16 x 16 diagonal blocks of I + A by forward
-//     substitution, then u and w by blocked forward substitution over the 256 right-hand-side
-//     columns (beta v | beta e^cum k_n), each wave owning 64 columns of every row (no barrier).
-//     Writes u (fp32), w (fp16), intra (fp16 hi + lo), cum, and - once per QK head - q_n and
-//     k_n^T (fp16).
-//  K2 delta_chunk_state: one workgroup per (sequence, value head, 32-column slice of S); the
-//     columns of S are independent, so 4 slices per head run in parallel, the slices of one
-//     head on one XCD (they share its L2 for the chunk operands). S lives in MFMA
-//     accumulator registers (fp32) for the whole segment; each chunk it is copied to LDS as
-//     fp16 (transposed, so the B operand is a 16-byte read), then w S and q_n S, intra v_new,
-//     and the rank-64 state update k_n^T v' run on MFMA.
-// Operands are fp16 (11-bit mantissa) rather than bf16, and the products that set the output's
-// accuracy carry a low fp16 part (hi hi + hi lo + lo hi, ~22 bits): the Gram products run on the
-// raw q / k rows (exact in fp16 for bf16 inputs) with the norms, beta and every decay applied in
-// fp32 afterwards, and intra v_new is split on both sides. At config-4 data (T = 2048, 32 heads)
-// o is within ~2e-4 of fp64; fp16-only intra v_new gives 6e-4, bf16 operands 4e-3.
+// One workgroup (4 waves, one per SIMD) owns one (sequence, value head, segment of chunks) and
+// walks its chunks with the state S [128 x 128] fp32 in MFMA accumulators, wave w owning value
+// columns [32 w, 32 w + 32). Nothing per chunk goes through HBM: each period computes the chain
+// of chunk c (the S-dependent products) and, interleaved with it, the intra-chunk operands of
+// chunk c + 1 (Gram products, A, its diagonal-block inverses, intra), which land in
+// double-buffered LDS. The triangular solve is a blocked forward substitution over the four
+// 16-row blocks inside the chain (v_new_r = D_r (R_r - sum_{k<r} A_rk v_new_k), D_r the inverse
+// of the r-th diagonal block of I + A, computed in fp32 per chunk), so it costs no separate
+// inverse. Every product runs on v_mfma_f32_16x16x32_f16 (the substitution on 16x16x16);
+// operands whose rounding reaches the output or the state carry an fp16 low part:
+// R = (I + A) v_new's right-hand side and the state update's v_new (hi + lo), intra and v_new in
+// the output (hi hi + hi lo + lo hi). The k, q, v tiles are the raw rows (exact in fp16 for bf16
+// inputs) with every row factor applied in fp32 on the accumulators, so the fp16 operands stay
+// well-scaled. Products keep their contraction index in a fixed permutation (within each 32
+// block: 4g..4g+3 then 16+4g..16+4g+3 for lane group g) so that accumulator tiles are the next
+// product's operands without any data movement.
+//
+// Sequence parallelism (batch x heads too few to fill the GPU, e.g. B = 1, 32 heads, 8192
+// tokens): the chunks are split into P segments. Launch 1 runs segments 0..P-2 from a zero state
+// (segment 0 from the initial state) while also carrying the segment's transition matrix M
+// (S_end = M S_start + N, M propagated from I through the same chunk maps with no v term);
+// a short combine launch chains S_{s+1} = M_s S_s + N_s over the segment boundaries; launch 2
+// runs every segment again from its true start state and writes the outputs. With enough
+// sequences x heads (P = 1) only launch 2 runs.
 #include "common.h"
 
-
 #include <algorithm>
+#include <atomic>
 
 using namespace aegist;
 
 namespace {
 
 constexpr int D = 128;
-constexpr int CH = 64;       // chunk length
-constexpr int SEG = 2048;    // tokens per segment (workspace granularity)
-#ifndef K2_NCT
-#define K2_NCT 2              // 16-column tiles per K2 workgroup (4 workgroups per value head)
-#endif
-constexpr int QK_LD = D + 8; // fp16 row stride (elements) of the q/k tiles in LDS
-constexpr int A_LD = 68;     // fp32 row stride of the A matrix in LDS (16-byte aligned rows)
+constexpr int CH = 64;
+constexpr int NW = 4;              // waves per workgroup
+constexpr int NT = NW * WAVE;      // threads per workgroup
+constexpr int RS = D + 8;          // fp16 row stride of the 64 x 128 tiles in LDS (bank spread)
+constexpr int RA = CH + 8;         // fp16 row stride of the 64 x 64 tiles
+constexpr int DWS = 20;            // fp32 row stride of a wave's 16 x 16 diagonal block
+constexpr int MIN_SEG_CHUNKS = 4;  // shortest segment the sequence split makes
 
 typedef _Float16 half_t;
 typedef short short4v_t __attribute__((ext_vector_type(4)));
-typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
-// raw buffer resource for the output stores: range (bytes) and the gfx9 word 3 (32-bit data,
-// no swizzle); kOutDrop lies past the range, so a store at that offset is discarded
-constexpr int kOutRange = 0x40000000;
-constexpr int kOutDrop = 0x7ffffff0;
-constexpr int kBufWord3 = 0x00020000;
-constexpr int kFusedLdsPad = 2048;  // dynamic LDS bytes added to the fused launch (occupancy cap)
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) short4v_t lds_s4;
 
 struct SeqLayout {
     long long sb_qk, st_qk, sh_qk, sb_v, st_v, sh_v, sb_o, st_o, sh_o;
     long long sb_g, st_g;  // g / beta strides by sequence and token; value head contiguous
 };
 
-// Workspace of one segment. Per (b, hv, chunk): u fp32 [64][128] stored in K2's accumulator
-// fragment order (see u_frag), w fp16 [64][128], intra fp16 hi and lo [64][64] each, and the decay factors
-// dec fp32 [3][64] = (e^{cum_i}, e^{cum_last - cum_i}, e^{cum_last}). Per (b, kh, chunk):
-// qn fp16 [64][128], knT fp16 [128][64]. w, intra, qn and knT are stored in MFMA A-operand
-// fragment order (afrag_coords).
-// Plus the carried state [B, HV, 128, 128] fp32 when the caller passes none.
-struct WsLayout {
-    size_t u, w, intra, intra_lo, cum, qn, knt, state, total;
+// Per-token factor arrays of one chunk (fp32, 64 entries each) and the chunk decay.
+struct Fact {
+    float cum[CH], beta[CH], brk[CH], rk[CH], rq[CH], fx[CH], fp[CH];
+    float gam;
+    float pad[3];
 };
 
-__host__ __device__ inline size_t al256(size_t x) { return (x + 255) / 256 * 256; }
+// LDS of one workgroup. kLo (fp32 inputs): the rows also keep their fp16 low parts, which the
+// Gram products (k k^T, k q^T), the right-hand side's v and the state update use.
+template <bool kLo>
+struct Smem {
+    static constexpr int NL = kLo ? 2 : 0;
+    __attribute__((aligned(16))) half_t K[2][CH][RS];    // k rows (fp16), by chunk parity
+    __attribute__((aligned(16))) half_t Q[CH][RS];       // rq e^cum q rows (fp16)
+    __attribute__((aligned(16))) half_t V[CH][RS];       // v rows (fp16)
+    __attribute__((aligned(16))) half_t AD[CH][RA];      // -A (strict lower blocks), D_r on the diagonal
+    __attribute__((aligned(16))) half_t IH[CH][RA];      // intra (fp16 hi)
+    __attribute__((aligned(16))) half_t IL[CH][RA];      // intra (fp16 lo)
+    __attribute__((aligned(16))) Fact F[2];
+    __attribute__((aligned(16))) float Dw[NW][16][DWS];  // fp32 diagonal block of A, per wave
+    __attribute__((aligned(16))) half_t KL[NL][CH][RS];  // k low parts, by chunk parity
+    __attribute__((aligned(16))) half_t VL[NL / 2][CH][RS];  // v low parts
+};
 
-__host__ __device__ inline WsLayout ws_layout(int B, int HK, int HV, int nch) {
-    WsLayout L;
-    size_t units_v = (size_t)B * HV * nch, units_k = (size_t)B * HK * nch;
-    size_t off = 0;
-    L.u = off; off += al256(units_v * CH * D * 4);
-    L.w = off; off += al256(units_v * CH * D * 2);
-    L.intra = off; off += al256(units_v * CH * CH * 2);
-    L.intra_lo = off; off += al256(units_v * CH * CH * 2);
-    L.cum = off; off += al256(units_v * 3 * CH * 4);
-    L.qn = off; off += al256(units_k * CH * D * 2);
-    L.knt = off; off += al256(units_k * CH * D * 2);
-    L.state = off; off += al256((size_t)B * HV * D * D * 4);
-    L.total = off;
-    return L;
+static_assert(sizeof(Smem<false>) <= 160 * 1024 && sizeof(Smem<true>) <= 160 * 1024, "LDS of one workgroup exceeds a CU");
+
+// Kernel parameters (one struct so both launches and the combine share them).
+struct Params {
+    const void* q;
+    const void* k;
+    const void* v;
+    const float* g;
+    const float* beta;
+    void* out;
+    SeqLayout a;
+    int T, B, HK, HV, nch, P, L;  // P segments of L chunks
+    int normalize;
+    float qscale, eps;
+    const float* init;  // initial state [B, HV, 128, 128] or null (zero)
+    float* final_state; // where the last segment's end state goes (launch 2)
+    float* starts;      // [B, HV, P, 128, 128] start state of every segment (P > 1)
+    float* nbuf;        // [B, HV, P - 1, 128, 128] segment end state from the segment's start
+    half_t* mbuf;       // [B, HV, P - 1, 128, 128] segment transition (row-major, fp16)
+};
+
+__device__ __forceinline__ f32x4 mfma32(half8 a, half8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mfma16(half4 a, half4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ half8 cat8(half4 a, half4 b) {
+    return half8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+}
+// fp32 x4 -> fp16 x4, round to nearest even
+__device__ __forceinline__ half4 h4(f32x4 x) {
+    const half2v a = __builtin_convertvector((f32x2{x[0], x[1]}), half2v);
+    const half2v b = __builtin_convertvector((f32x2{x[2], x[3]}), half2v);
+    return half4{a[0], a[1], b[0], b[1]};
+}
+// hi + lo split: hi = fp16(x), lo = fp16(x - hi); hi + lo carries ~22 significant bits
+__device__ __forceinline__ void split4(f32x4 x, half4& hi, half4& lo) {
+    hi = h4(x);
+    lo = h4(f32x4{x[0] - (float)hi[0], x[1] - (float)hi[1], x[2] - (float)hi[2], x[3] - (float)hi[3]});
+}
+__device__ __forceinline__ half4 ld4(const half_t* p) { return *(const half4*)p; }
+// two 4-element runs of one row: the permuted 8-slot operand of one 32-wide k step
+__device__ __forceinline__ half8 ld_perm(const half_t* row, int m, int g) {
+    return cat8(ld4(row + 32 * m + 4 * g), ld4(row + 32 * m + 16 + 4 * g));
+}
+// transpose read: lane n of group g gets rows R..R+3 (R per group) of column C + n of a
+// row-major fp16 tile with row stride `stride` (halfs)
+__device__ __forceinline__ half4 ld_tr(const half_t* tile, int stride, int R, int C, int n) {
+    const short4v_t s = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(tile + (R + (n >> 2)) * stride + C + 4 * (n & 3)));
+    return __builtin_bit_cast(half4, s);
 }
 
-__device__ __forceinline__ half8 ld_h8(const half_t* p) { return *(const half8*)p; }
+// Raw inputs of one chunk held by one wave: k and v rows of token tile `wave`, q rows of token
+// tile 3 - wave; lane (n, g) holds features 32 ks + 8 g .. +7 of its row for ks = 0..3.
+template <typename Tin> struct Raw;
+template <> struct Raw<uint16_t> {
+    uint4 k[4], q[4], v[4];
+};
+template <> struct Raw<float> {
+    float4 k[8], q[8], v[8];
+};
+struct RawGB {
+    float g, beta;
+};
 
-// MFMA A-operand fragment order. For A [M][K] (M % 16 == 0, K % 32 == 0), fragment (mb, ks)
-// holds for lane l the 8 halves A[16 mb + l % 16][32 ks + 8 (l / 16) + i], i < 8 - exactly what
-// lane l passes to v_mfma_f32_16x16x32_f16 for row block mb and k block ks. Fragments are
-// stored contiguously, offset ((mb * K / 32 + ks) * 64 + l) * 8 halves, so a wave loads one
-// operand with a single 1 KB contiguous access. Returns the (row, first column) of fragment
-// slot f.
-__device__ __forceinline__ void afrag_coords(int f, int KS, int& r, int& c0) {
-    const int l = f % 64, ks = (f / 64) % KS, mb = f / (64 * KS);
-    r = 16 * mb + l % 16;
-    c0 = 32 * ks + 8 * (l / 16);
-}
-
-// 8 consecutive activations as fp32 (two 16-byte loads for fp32, one for bf16)
-template <typename T> __device__ __forceinline__ void ld8(const T* p, float* o);
-template <> __device__ __forceinline__ void ld8<float>(const float* p, float* o) {
-    const float4 a = ((const float4*)p)[0], b = ((const float4*)p)[1];
-    o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w; o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w;
-}
-template <> __device__ __forceinline__ void ld8<uint16_t>(const uint16_t* p, float* o) {
-    const uint4 a = *(const uint4*)p;
+__device__ __forceinline__ void unpack8(const uint4* src, int ks, float* o) {
+    const uint4 a = src[ks];
     o[0] = bf_lo(a.x); o[1] = bf_hi(a.x); o[2] = bf_lo(a.y); o[3] = bf_hi(a.y);
     o[4] = bf_lo(a.z); o[5] = bf_hi(a.z); o[6] = bf_lo(a.w); o[7] = bf_hi(a.w);
 }
-
-// Offset (in floats) of u[i][col] inside one chunk's u block, laid out as K2 reads it: slice
-// sl = col / 32, wave wv = i / 16, column tile ct, then the 64 lanes (gq = (i % 16) / 4,
-// n = col % 16) of a 16x16 accumulator, each holding rows 4gq .. 4gq+3 contiguously.
-__device__ __forceinline__ int u_frag(int i, int col) {
-    const int sl = col / 32, ct = (col % 32) / 16, n = col % 16, wv = i / 16, gq = (i % 16) / 4, j = i % 4;
-    return ((((sl * 4 + wv) * 2 + ct) * 64) + gq * 16 + n) * 4 + j;
+__device__ __forceinline__ void unpack8(const float4* src, int ks, float* o) {
+    const float4 a = src[2 * ks], b = src[2 * ks + 1];
+    o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w; o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w;
 }
 
-__device__ __forceinline__ f32x4 mfma16(half8 a, half8 b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+// 32 features (4 runs of 8 at 32 ks + 8 g) of one row; zeros when !ok
+__device__ __forceinline__ void load_rows(const uint16_t* row, bool ok, int g, uint4* dst) {
+#pragma unroll
+    for (int ks = 0; ks < 4; ks++) {
+        uint4 x = *(const uint4*)(row + 32 * ks + 8 * g);
+        if (!ok) x = uint4{0u, 0u, 0u, 0u};
+        dst[ks] = x;
+    }
+}
+__device__ __forceinline__ void load_rows(const float* row, bool ok, int g, float4* dst) {
+#pragma unroll
+    for (int ks = 0; ks < 4; ks++) {
+        float4 x0 = *(const float4*)(row + 32 * ks + 8 * g), x1 = *(const float4*)(row + 32 * ks + 8 * g + 4);
+        if (!ok) x0 = x1 = float4{0.f, 0.f, 0.f, 0.f};
+        dst[2 * ks] = x0;
+        dst[2 * ks + 1] = x1;
+    }
 }
 
-// ---------------------------------------------------------------------------------------------
-// K1: intra-chunk work, one workgroup of 256 threads (4 waves) per (chunk c, value head hv,
-// sequence b). The body is shared by the standalone kernel (grid (nch, HV, B)) and the fused
-// launch below; its LDS is one struct so the fused kernel can overlay it with K2's.
-template <bool kSplitV>
-struct K1Smem {
-    __attribute__((aligned(16))) half_t QV[CH][QK_LD];  // q_n tile, then v (fp16 hi)
-    __attribute__((aligned(16))) half_t Vl[kSplitV ? CH : 1][QK_LD];
-    __attribute__((aligned(16))) half_t Ks[CH][QK_LD];
-    // A (strict lower), with the inverses of the diagonal blocks of I + A written over its
-    // diagonal blocks; the w staging tile afterwards
-    __attribute__((aligned(16))) float As[CH][A_LD];
-    float cum_s[CH], beta_s[CH], g_s[CH], rq_s[CH], rk_s[CH];
-    // intra is staged for fragment order in QV's space: q_n has been read into registers by then,
-    // and v is written there only after the intra fragments have gone out. 53 KB in all for bf16
-    // inputs: three workgroups per CU for the standalone K1 launch.
+// Issue the global loads of chunk c (tokens past T read a clamped row and are zeroed).
+template <typename Tin>
+__device__ __forceinline__ void load_chunk(const Params& p, int b, int hv, int c, int wave, int n, int g, int lane,
+                                           Raw<Tin>& r, RawGB& gb) {
+    const int R = p.HV / p.HK, kh = hv / R;
+    const int tk = c * CH + 16 * wave + n, tq = c * CH + 16 * (3 - wave) + n;
+    const bool okk = tk < p.T, okq = tq < p.T;
+    const int tkc = okk ? tk : p.T - 1, tqc = okq ? tq : p.T - 1;
+    const Tin* q = (const Tin*)p.q;
+    const Tin* k = (const Tin*)p.k;
+    const Tin* v = (const Tin*)p.v;
+    load_rows(k + b * p.a.sb_qk + (long long)tkc * p.a.st_qk + kh * p.a.sh_qk, okk, g, r.k);
+    load_rows(q + b * p.a.sb_qk + (long long)tqc * p.a.st_qk + kh * p.a.sh_qk, okq, g, r.q);
+    load_rows(v + b * p.a.sb_v + (long long)tkc * p.a.st_v + hv * p.a.sh_v, okk, g, r.v);
+    const int t = c * CH + lane;
+    const bool ok = t < p.T;
+    const long long go = b * p.a.sb_g + (long long)(ok ? t : p.T - 1) * p.a.st_g + hv;
+    gb.g = ok ? p.g[go] : 0.f;
+    gb.beta = ok ? p.beta[go] : 0.f;
+}
+
+// Converted rows a wave keeps between the two prep phases (lo parts: fp32 inputs only).
+template <bool kLo>
+struct Conv {
+    static constexpr int NL = kLo ? 4 : 0;
+    half8 k[4], q[4], v[4];     // natural feature order (pieces 32 ks + 8 g)
+    half8 kl[NL], ql[NL], vl[NL];
+    float rk, rq;               // own k row (tile wave), own q row (tile 3 - wave)
 };
 
-// step 5 reuses As for the w staging tile; intra is staged in fp32 (row pitch CH + 4) in QV's space
-static_assert(sizeof(half_t) * CH * QK_LD >= CH * (CH + 4) * sizeof(float), "intra staging exceeds the q tile");
-static_assert(sizeof(float) * CH * A_LD >= sizeof(half_t) * CH * QK_LD, "w staging exceeds As");
+// Operands of chunk c that prep B computes in registers and the next period writes to LDS
+// (AD, IH, IL are single-buffered: the chain of chunk c - 1 reads them until the period ends).
+struct Deferred {
+    half4 am[3];        // -A blocks (wave, jt) for jt < wave
+    half4 d;            // D_wave rows 4 g .. 4 g + 3 of column n
+    half4 ih[4], il[4]; // intra blocks (3 - wave, jt) for jt <= 3 - wave
+};
 
-template <typename Tin>
-__device__ __forceinline__ void chunk_intra_body(const Tin* __restrict__ q, const Tin* __restrict__ k,
-                                                 const Tin* __restrict__ v, const float* __restrict__ g,
-                                                 const float* __restrict__ beta, const SeqLayout& a, int t0, int T,
-                                                 int HK, int HV, int normalize, float qscale, float eps,
-                                                 unsigned char* __restrict__ ws, const WsLayout& L, int vec_in,
-                                                 K1Smem<sizeof(Tin) == 4>& sm, int c, int hv, int b, int nch) {
-    constexpr bool kSplitV = sizeof(Tin) == 4;  // fp32 v needs a low fp16 part; bf16 v is exact in fp16
-    auto& QV = sm.QV;
-    auto& Vl = sm.Vl;
-    auto& Ks = sm.Ks;
-    auto& As = sm.As;
-    auto& cum_s = sm.cum_s;
-    auto& beta_s = sm.beta_s;
-    auto& g_s = sm.g_s;
-    auto& rq_s = sm.rq_s;
-    auto& rk_s = sm.rk_s;
-    float (*It)[CH + 4] = (float (*)[CH + 4])&QV[0][0];
+__device__ __forceinline__ half8 cvt8(const float* x) {
+    const half4 a = h4(f32x4{x[0], x[1], x[2], x[3]}), b = h4(f32x4{x[4], x[5], x[6], x[7]});
+    return cat8(a, b);
+}
+__device__ __forceinline__ half8 lo8(const float* x, half8 h) {
+    float y[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) y[e] = x[e] - (float)h[e];
+    return cvt8(y);
+}
 
-    const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE, n = lane % 16, gq = lane / 16;
-    const int R = HV / HK, kh = hv / R;
-    const bool writes_qk = (hv % R) == 0;
-    const int tok0 = t0 + c * CH;
-    const size_t vu = (size_t)(b * HV + hv) * nch + c;
-
-    // ---- 1. q, k, v rows (thread = row, 32-element quarter); fp32 row norms; fp16 q_n, k_n
-    const int row = tid / 4, qq = tid % 4, tok = tok0 + row;
-    const bool valid = tok < T;
-    float xv[32];
-    {
-        // beta / g first: their latency overlaps the row loads
-        float beta_r = 0.f, g_r = 0.f;
-        if (qq == 0 && valid) {
-            beta_r = beta[b * a.sb_g + (long long)tok * a.st_g + hv];
-            g_r = g[b * a.sb_g + (long long)tok * a.st_g + hv];
-        }
-        const Tin* qp = q + b * a.sb_qk + (long long)tok * a.st_qk + kh * a.sh_qk + qq * 32;
-        const Tin* kp = k + b * a.sb_qk + (long long)tok * a.st_qk + kh * a.sh_qk + qq * 32;
-        const Tin* vp = v + b * a.sb_v + (long long)tok * a.st_v + hv * a.sh_v + qq * 32;
-        float xq[32], xk[32];
-        if (valid && vec_in) {
+// Prep phase A for chunk c into parity buffer `buf`: fp16 rows, norms, cumulative decays and the
+// per-token factors; writes K[buf] rows of token tile `wave` and this wave's entries of F[buf].
+template <typename Tin, bool kLo>
+__device__ __forceinline__ void prep_a(const Params& p, Smem<kLo>& sm, int buf, const Raw<Tin>& r, const RawGB& gb,
+                                       int wave, int n, int g, int lane, Conv<kLo>& cv) {
+    float ssk = 0.f, ssq = 0.f;
 #pragma unroll
-            for (int e = 0; e < 32; e += 8) {
-                ld8<Tin>(qp + e, xq + e);
-                ld8<Tin>(kp + e, xk + e);
-                ld8<Tin>(vp + e, xv + e);
-            }
-        } else {
+    for (int ks = 0; ks < 4; ks++) {
+        float x[8];
+        unpack8(r.k, ks, x);
 #pragma unroll
-            for (int e = 0; e < 32; e++) {
-                xq[e] = valid ? Act<Tin>::ld(qp, e) : 0.f;
-                xk[e] = valid ? Act<Tin>::ld(kp, e) : 0.f;
-                xv[e] = valid ? Act<Tin>::ld(vp, e) : 0.f;
-            }
-        }
-        float ssq = 0.f, ssk = 0.f;
+        for (int e = 0; e < 8; e++) ssk += x[e] * x[e];
+        cv.k[ks] = cvt8(x);
+        if constexpr (kLo) cv.kl[ks] = lo8(x, cv.k[ks]);
+        unpack8(r.q, ks, x);
 #pragma unroll
-        for (int e = 0; e < 32; e++) {
-            ssq += xq[e] * xq[e];
-            ssk += xk[e] * xk[e];
-        }
-        ssq += lane_xor<1>(ssq);
-        ssq += lane_xor<2>(ssq);
-        ssk += lane_xor<1>(ssk);
-        ssk += lane_xor<2>(ssk);
-        const float rq = normalize ? rsqrtf(ssq + eps) * qscale : 1.f;
-        const float rk = normalize ? rsqrtf(ssk + eps) : 1.f;
-        // the tiles keep the raw rows (exact in fp16 for bf16 inputs; fp32 inputs add a low fp16
-        // part, in Vl for k and in As's space for q, both free until step 3's products are done)
-        half_t (*Ql)[QK_LD] = (half_t (*)[QK_LD])&As[0][0];
-#pragma unroll
-        for (int e = 0; e < 32; e += 8) {
-            half8 hq, hk, lq, lk;
-#pragma unroll
-            for (int f = 0; f < 8; f++) {
-                hq[f] = (half_t)xq[e + f];
-                hk[f] = (half_t)xk[e + f];
-                lq[f] = (half_t)(xq[e + f] - (float)hq[f]);
-                lk[f] = (half_t)(xk[e + f] - (float)hk[f]);
-            }
-            *(half8*)&QV[row][qq * 32 + e] = hq;
-            *(half8*)&Ks[row][qq * 32 + e] = hk;
-            if constexpr (kSplitV) {
-                *(half8*)&Ql[row][qq * 32 + e] = lq;
-                *(half8*)&Vl[row][qq * 32 + e] = lk;
-            }
-        }
-        if (qq == 0) {
-            beta_s[row] = beta_r;
-            g_s[row] = g_r;
-            // padding rows (past T) carry zero factors
-            rq_s[row] = valid ? rq : 0.f;
-            rk_s[row] = valid ? rk : 0.f;
-        }
+        for (int e = 0; e < 8; e++) ssq += x[e] * x[e];
+        cv.q[ks] = cvt8(x);
+        if constexpr (kLo) cv.ql[ks] = lo8(x, cv.q[ks]);
+        unpack8(r.v, ks, x);
+        cv.v[ks] = cvt8(x);
+        if constexpr (kLo) cv.vl[ks] = lo8(x, cv.v[ks]);
     }
-    lds_barrier();
-
-    // ---- 2. cum = inclusive prefix sum of g (wave 0) and the decay factors K2 needs;
-    // q_n rows and k_n^T for K2 (once per QK head)
-    if (wave == 0) {
-        float x = g_s[lane];
+    ssk = pair_sum32(pair_sum16(ssk));
+    ssq = pair_sum32(pair_sum16(ssq));
+    cv.rk = p.normalize ? rsqrtf(ssk + p.eps) : 1.f;
+    cv.rq = p.normalize ? rsqrtf(ssq + p.eps) * p.qscale : 1.f;
+    // k rows of tile `wave` (natural order)
 #pragma unroll
-        for (int d = 1; d < WAVE; d <<= 1) {
-            float y = __shfl_up(x, d, WAVE);
-            if (lane >= d) x += y;
-        }
-        cum_s[lane] = x;
-        const float last = __shfl(x, CH - 1, WAVE);
-        float* dec = (float*)(ws + L.cum) + vu * 3 * CH;
-        dec[lane] = rq_s[lane] * __expf(x);
-        dec[CH + lane] = rk_s[lane] * __expf(last - x);
-        dec[2 * CH + lane] = __expf(last);
+    for (int ks = 0; ks < 4; ks++) {
+        *(half8*)&sm.K[buf][16 * wave + n][32 * ks + 8 * g] = cv.k[ks];
+        if constexpr (kLo) *(half8*)&sm.KL[buf][16 * wave + n][32 * ks + 8 * g] = cv.kl[ks];
     }
-    if (writes_qk) {
-        // q_n (A of q_n S: 64 x 128) and k_n^T (A of the state update: 128 dk x 64 rows) in
-        // fragment order
-        const size_t ku = ((size_t)(b * HK + kh) * nch + c);
-        half8* qn = (half8*)((half_t*)(ws + L.qn) + ku * CH * D);
-        half8* knt = (half8*)((half_t*)(ws + L.knt) + ku * CH * D);
+    // inclusive prefix sum of g over the chunk (lane = token)
+    float x = gb.g;
 #pragma unroll
-        for (int it = 0; it < 4; it++) {
-            const int f = tid + 256 * it;
-            int r, c0;
-            afrag_coords(f, 4, r, c0);
-            qn[f] = ld_h8(&QV[r][c0]);
-            afrag_coords(f, 2, r, c0);  // r = dk, c0 = first chunk row
-            half8 v;
-#pragma unroll
-            for (int i = 0; i < 8; i++) v[i] = Ks[c0 + i][r];
-            knt[f] = v;
-        }
+    for (int d = 1; d < WAVE; d <<= 1) {
+        const float y = __shfl_up(x, d, WAVE);
+        if (lane >= d) x += y;
     }
-    lds_barrier();
+    const float cl = __shfl(x, CH - 1, WAVE);
+    // this wave's tokens 16 wave + n: factors need rk (known here) and cum / beta of that token
+    const int tw = 16 * wave + n;
+    const float cum_t = __shfl(x, tw, WAVE), beta_t = __shfl(gb.beta, tw, WAVE);
+    Fact& F = sm.F[buf];
+    if (g == 0) {
+        F.cum[tw] = cum_t;
+        F.beta[tw] = beta_t;
+        F.rk[tw] = cv.rk;
+        F.brk[tw] = beta_t * cv.rk;
+        F.fx[tw] = beta_t * cv.rk * __expf(cum_t);
+        F.fp[tw] = cv.rk * __expf(cl - cum_t);
+        F.rq[16 * (3 - wave) + n] = cv.rq;
+    }
+    if (wave == 0 && lane == 0) F.gam = __expf(cl);
+}
 
-    // ---- 3. k~ k~^T and q~ k~^T on MFMA over the raw rows (fp32 inputs: hi hi + hi lo + lo hi),
-    // lower 16 x 16 blocks only: 10 blocks of each, 5 per wave: wave w forms the A blocks of row
-    // block w (w + 1 of them) and the intra blocks of row block 3 - w (4 - w of them). All
-    // products first (the low parts of q live in As's space), then A and intra with every row
-    // factor (beta, the norms, the decays) applied in fp32, and the upper blocks cleared.
-    {
-        const int wv = __builtin_amdgcn_readfirstlane(wave);
-        const int ra = wv, rb = 3 - wv;
-        half_t (*Ql)[QK_LD] = (half_t (*)[QK_LD])&As[0][0];
-        half8 ak[4], aq[4], akl[4], aql[4];
+// Prep phase B for chunk c (after a barrier: K[buf] and F[buf] complete): the Gram products, -A
+// blocks, the diagonal-block inverse D_wave and intra into `df` (written to LDS by the next
+// period), and the q and v rows into Q and V.
+template <bool kLo>
+__device__ __forceinline__ void prep_b(Smem<kLo>& sm, int buf, const Conv<kLo>& cv, int wave, int n, int g,
+                                       Deferred& df) {
+    const Fact& F = sm.F[buf];
+    const int wv = wave;
+    // Gram tiles: C(jt, it) = MFMA(A = k rows of tile jt, B = rows of tile it), which holds
+    // X[i = 16 it + n][j = 16 jt + 4 g + r] in lane (n, g) (the Gram matrix is symmetric).
+    // G: it = wv, jt <= wv.  k q^T: it = 3 - wv, jt <= 3 - wv.
+    const int iq = 3 - wv;
+    // factors of this lane's rows
+    const float cum_i = F.cum[16 * wv + n], brk_i = F.brk[16 * wv + n];
+    const float cumq_i = F.cum[16 * iq + n], rq_i = F.rq[16 * iq + n];
+#pragma unroll
+    for (int jt = 0; jt < 4; jt++) {
+        if (jt > wv && jt > iq) continue;
+        half8 ka[4], kal[4];
 #pragma unroll
         for (int ks = 0; ks < 4; ks++) {
-            ak[ks] = ld_h8(&Ks[16 * ra + n][32 * ks + 8 * gq]);
-            aq[ks] = ld_h8(&QV[16 * rb + n][32 * ks + 8 * gq]);
-            if constexpr (kSplitV) {
-                akl[ks] = ld_h8(&Vl[16 * ra + n][32 * ks + 8 * gq]);
-                aql[ks] = ld_h8(&Ql[16 * rb + n][32 * ks + 8 * gq]);
-            }
+            ka[ks] = jt == wv ? cv.k[ks] : *(const half8*)&sm.K[buf][16 * jt + n][32 * ks + 8 * g];
+            if constexpr (kLo) kal[ks] = jt == wv ? cv.kl[ks] : *(const half8*)&sm.KL[buf][16 * jt + n][32 * ks + 8 * g];
         }
-        f32x4 accA[4], accI[4];
-#pragma unroll
-        for (int cb = 0; cb < 4; cb++) {
-            accA[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
-            accI[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
-            if (cb > ra && cb > rb) continue;
+        const f32x4 cumj = *(const f32x4*)&F.cum[16 * jt + 4 * g];
+        const f32x4 rkj = *(const f32x4*)&F.rk[16 * jt + 4 * g];
+        if (jt <= wv) {
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int ks = 0; ks < 4; ks++) {
-                const half8 bh = ld_h8(&Ks[16 * cb + n][32 * ks + 8 * gq]);
-                half8 bl;
-                if constexpr (kSplitV) bl = ld_h8(&Vl[16 * cb + n][32 * ks + 8 * gq]);
-                if (cb <= ra) {
-                    accA[cb] = mfma16(ak[ks], bh, accA[cb]);
-                    if constexpr (kSplitV) {
-                        accA[cb] = mfma16(ak[ks], bl, accA[cb]);
-                        accA[cb] = mfma16(akl[ks], bh, accA[cb]);
-                    }
-                }
-                if (cb <= rb) {
-                    accI[cb] = mfma16(aq[ks], bh, accI[cb]);
-                    if constexpr (kSplitV) {
-                        accI[cb] = mfma16(aq[ks], bl, accI[cb]);
-                        accI[cb] = mfma16(aql[ks], bh, accI[cb]);
-                    }
+                acc = mfma32(ka[ks], cv.k[ks], acc);
+                if constexpr (kLo) {
+                    acc = mfma32(ka[ks], cv.kl[ks], acc);
+                    acc = mfma32(kal[ks], cv.k[ks], acc);
                 }
             }
-        }
-        float ca[4], ba[4], cq[4], rqv[4];
+            f32x4 av;
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            ca[j] = cum_s[16 * ra + 4 * gq + j];
-            ba[j] = beta_s[16 * ra + 4 * gq + j] * rk_s[16 * ra + 4 * gq + j];
-            cq[j] = cum_s[16 * rb + 4 * gq + j];
-            rqv[j] = rq_s[16 * rb + 4 * gq + j];
-        }
-        lds_barrier();  // every product is done: As and It (QV's space) are written next
-#pragma unroll
-        for (int cb = 0; cb < 4; cb++) {
-            const int jj = 16 * cb + n;
-            const float cj = cum_s[jj], rkj = rk_s[jj];
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const int i = 16 * ra + 4 * gq + j;
-                As[i][jj] = cb <= ra && jj < i ? ba[j] * rkj * (__expf(ca[j] - cj) * accA[cb][j]) : 0.f;
+            for (int r = 0; r < 4; r++) {
+                const int j = 16 * jt + 4 * g + r, i = 16 * wv + n;
+                av[r] = j < i ? brk_i * rkj[r] * __expf(cum_i - cumj[r]) * acc[r] : 0.f;
             }
+            if (jt < wv) df.am[jt < 3 ? jt : 2] = h4(-av);
+            else *(f32x4*)&sm.Dw[wv][n][4 * g] = av;
+        }
+        if (jt <= iq) {
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const int i = 16 * rb + 4 * gq + j;
-                It[i][jj] = cb <= rb && jj <= i ? rqv[j] * rkj * (__expf(cq[j] - cj) * accI[cb][j]) : 0.f;
+            for (int ks = 0; ks < 4; ks++) {
+                acc = mfma32(ka[ks], cv.q[ks], acc);
+                if constexpr (kLo) {
+                    acc = mfma32(ka[ks], cv.ql[ks], acc);
+                    acc = mfma32(kal[ks], cv.q[ks], acc);
+                }
             }
+            f32x4 iv;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int j = 16 * jt + 4 * g + r, i = 16 * iq + n;
+                iv[r] = j <= i ? rq_i * rkj[r] * __expf(cumq_i - cumj[r]) * acc[r] : 0.f;
+            }
+            split4(iv, df.ih[jt], df.il[jt]);
         }
     }
-    lds_barrier();
-    {   // intra (A of intra v_new: 64 x 64) in fragment order, as fp16 hi + lo (~22 bits: the
-        // intra v_new product carries most of the output's rounding error otherwise)
-        half8* intra = (half8*)((half_t*)(ws + L.intra) + vu * CH * CH);
-        half8* intra_lo = (half8*)((half_t*)(ws + L.intra_lo) + vu * CH * CH);
+    // q rows (scaled by rq e^cum) of tile iq and v rows of tile wv
+    {
+        const float f = rq_i * __expf(cumq_i);
 #pragma unroll
-        for (int it = 0; it < 2; it++) {
-            const int f = tid + 256 * it;
-            int r, c0;
-            afrag_coords(f, 2, r, c0);
-            const f32x4 x0 = *(const f32x4*)&It[r][c0], x1 = *(const f32x4*)&It[r][c0 + 4];
-            half8 hi, lo;
+        for (int ks = 0; ks < 4; ks++) {
+            half8 y;
 #pragma unroll
-            for (int i = 0; i < 8; i++) {
-                const float x = i < 4 ? x0[i] : x1[i - 4];
-                hi[i] = (half_t)x;
-                lo[i] = (half_t)(x - (float)hi[i]);
+            for (int e = 0; e < 8; e++) {
+                float x = (float)cv.q[ks][e];
+                if constexpr (kLo) x += (float)cv.ql[ks][e];
+                y[e] = (half_t)(f * x);
             }
-            intra[f] = hi;
-            intra_lo[f] = lo;
+            *(half8*)&sm.Q[16 * iq + n][32 * ks + 8 * g] = y;
+            *(half8*)&sm.V[16 * wv + n][32 * ks + 8 * g] = cv.v[ks];
+            if constexpr (kLo) *(half8*)&sm.VL[0][16 * wv + n][32 * ks + 8 * g] = cv.vl[ks];
         }
     }
-    lds_barrier();  // It (QV's space) has gone out; v is written there next
-
-    // ---- 4. v (fp16 hi / lo) into the q tile's space; inverses of the diagonal blocks of I + A
-#pragma unroll
-    for (int e = 0; e < 32; e += 8) {
-        half8 hv8, lv8;
-#pragma unroll
-        for (int f = 0; f < 8; f++) {
-            const half_t h = (half_t)xv[e + f];
-            hv8[f] = h;
-            lv8[f] = (half_t)(xv[e + f] - (float)h);
-        }
-        *(half8*)&QV[row][qq * 32 + e] = hv8;
-        if constexpr (kSplitV) *(half8*)&Vl[row][qq * 32 + e] = lv8;
-    }
-    {   // 4a. diagonal block wave: lane j < 16 solves column j of (I + A_ww)^-1; A[i][k] of the
-        // block is broadcast from lane k with readlane
-        const int j = lane & 15, o = 16 * wave;
-        float acol[16], x[16];
-#pragma unroll
-        for (int i = 0; i < 16; i++) acol[i] = As[o + i][o + j];
+    // D_wv = (I + A_ww)^-1 by forward substitution in fp32, lane n (of every group) solving
+    // column n; the block's rows are read as broadcasts from the wave's own scratch
+    wave_sync();
+    {
+        float xs[16];
 #pragma unroll
         for (int i = 0; i < 16; i++) {
-            float s = i == j ? 1.f : 0.f;
+            float sacc = i == n ? 1.f : 0.f;
 #pragma unroll
-            for (int kk = 0; kk < i; kk++)
-                s -= __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acol[i]), kk)) * x[kk];
-            x[i] = s;
+            for (int kk = 0; kk < i; kk++) sacc -= sm.Dw[wv][i][kk] * xs[kk];
+            xs[i] = sacc;
         }
-        lds_barrier();  // every wave has read its A block column before X overwrites it
-        if (lane < 16) {
-#pragma unroll
-            for (int i = 0; i < 16; i++) As[o + i][o + j] = x[i];
-        }
-    }
-    lds_barrier();
-    // ---- 5. u = (I + A)^-1 diag(beta) v and w = (I + A)^-1 diag(beta e^cum rk) k~ by blocked
-    // forward substitution over the four 16-row blocks: block row r of U is
-    //   U_r = D_r^-1 (R_r - sum_{k < r} A_rk U_k),   D_r^-1 = (I + A_rr)^-1 (step 4a),
-    // with the 256 right-hand-side columns split over the waves (waves 0, 1: u columns
-    // 64 (w % 2) ..; waves 2, 3: w columns), so a wave owns its columns of U for every row and
-    // needs no barrier. Products on v_mfma_f32_16x16x32_f16 with both sides as fp16 hi + lo.
-    // The k index of each product runs over two 16-row blocks in the order the accumulators hold
-    // them (lane group g: rows 4 g .. 4 g + 3 of the first block, then of the second), so an
-    // accumulator pair is a B operand as it stands; the A side reads A and D^-1 in that order.
-    {
-        const bool isw = wave >= 2;
-        const int cbase = 64 * (wave & 1);
-        half_t (*src)[QK_LD] = isw ? Ks : QV;  // raw k rows / v rows (fp16)
-        typedef __attribute__((address_space(3))) short4v_t lds_s4;
-        // row factors of this lane's rows 16 r + 4 gq + j
-        f32x4 U[4][4];
-#pragma unroll
-        for (int r = 0; r < 4; r++)
-#pragma unroll
-            for (int ct = 0; ct < 4; ct++) U[r][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
-        // A-side operand (rows 16 r + n, k slots of block pair (kb0, kb0 + 1)), hi / lo, negated
-        // on request; columns of blocks >= nb_valid read as zero
-        auto aop = [&](int r, int kb0, bool second, bool neg, half8& hi, half8& lo) {
-            const f32x4 x0 = *(const f32x4*)&As[16 * r + n][16 * kb0 + 4 * gq];
-            f32x4 x1 = f32x4{0.f, 0.f, 0.f, 0.f};
-            if (second) x1 = *(const f32x4*)&As[16 * r + n][16 * (kb0 + 1) + 4 * gq];
-#pragma unroll
-            for (int i = 0; i < 8; i++) {
-                const float x = (i < 4 ? x0[i] : x1[i - 4]) * (neg ? -1.f : 1.f);
-                const half_t h = (half_t)x;
-                hi[i] = h;
-                lo[i] = (half_t)(x - (float)h);
-            }
-        };
-        auto split = [&](const f32x4& a, const f32x4& b, half8& hi, half8& lo) {
-#pragma unroll
-            for (int i = 0; i < 8; i++) {
-                const float x = i < 4 ? a[i] : b[i - 4];
-                const half_t h = (half_t)x;
-                hi[i] = h;
-                lo[i] = (half_t)(x - (float)h);
-            }
-        };
-        const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
+        // group g keeps rows 4 g .. 4 g + 3 of column n
+        f32x4 dv;
 #pragma unroll
         for (int r = 0; r < 4; r++) {
-            float fr[4];
+            float val = xs[r];
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const int t = 16 * r + 4 * gq + j;
-                fr[j] = isw ? beta_s[t] * __expf(cum_s[t]) * rk_s[t] : beta_s[t];
-            }
-            f32x4 acc[4];
-#pragma unroll
-            for (int ct = 0; ct < 4; ct++) {
-                // right-hand side rows 16 r + 4 gq .. +3 of column cbase + 16 ct + n: one
-                // transpose read (lane k of a 16-lane group addresses row R + k / 4, columns
-                // C + 4 (k % 4) .. +3; lane j receives rows R .. R + 3 of column C + j)
-                const int R0 = 16 * r + 4 * gq, C0 = cbase + 16 * ct;
-                const short4v_t h4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                    (lds_s4*)&src[R0 + (n >> 2)][C0 + 4 * (n & 3)]);
-                // (bit-cast the whole vector: clang's __builtin_bit_cast of a vector element
-                // reads element 0 whatever the index)
-                const half4 hh = __builtin_bit_cast(half4, h4);
-#pragma unroll
-                for (int j = 0; j < 4; j++) acc[ct][j] = fr[j] * (float)hh[j];
-                if constexpr (kSplitV) {
-                    if (!isw) {
-                        const short4v_t l4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                            (lds_s4*)&Vl[R0 + (n >> 2)][C0 + 4 * (n & 3)]);
-                        const half4 ll = __builtin_bit_cast(half4, l4);
-#pragma unroll
-                        for (int j = 0; j < 4; j++) acc[ct][j] += fr[j] * (float)ll[j];
-                    }
-                }
-            }
-            // acc -= A_{r, (2m, 2m+1)} U_{(2m, 2m+1)} over the block pairs below r
-#pragma unroll
-            for (int m = 0; 2 * m < r; m++) {
-                half8 ah, al;
-                aop(r, 2 * m, 2 * m + 1 < r, true, ah, al);
-#pragma unroll
-                for (int ct = 0; ct < 4; ct++) {
-                    half8 bh, bl;
-                    split(U[2 * m][ct], 2 * m + 1 < r ? U[2 * m + 1][ct] : zero4, bh, bl);
-                    acc[ct] = mfma16(ah, bh, acc[ct]);
-                    acc[ct] = mfma16(ah, bl, acc[ct]);
-                    acc[ct] = mfma16(al, bh, acc[ct]);
-                }
-            }
-            // U_r = D_r^-1 acc (k slots of the second block are zero on both sides)
-            half8 dh, dl;
-            aop(r, r, false, false, dh, dl);
-#pragma unroll
-            for (int ct = 0; ct < 4; ct++) {
-                half8 bh, bl;
-                split(acc[ct], zero4, bh, bl);
-                f32x4 y = mfma16(dh, bh, zero4);
-                y = mfma16(dh, bl, y);
-                U[r][ct] = mfma16(dl, bh, y);
-            }
+            for (int gg = 1; gg < 4; gg++)
+                if (gg == g) val = xs[4 * gg + r];
+            dv[r] = val;
         }
-        if (!isw) {
-            float* u = (float*)(ws + L.u) + vu * CH * D;
-#pragma unroll
-            for (int r = 0; r < 4; r++)
-#pragma unroll
-                for (int ct = 0; ct < 4; ct++)
-                    *(f32x4*)(u + u_frag(16 * r + 4 * gq, cbase + 16 * ct + n)) = U[r][ct];
-        }
-        lds_barrier();  // every wave is done with As and the v / k tiles: w is staged in As's space
-        half_t (*Wst)[QK_LD] = (half_t (*)[QK_LD])&As[0][0];
-        if (isw) {
-#pragma unroll
-            for (int r = 0; r < 4; r++)
-#pragma unroll
-                for (int ct = 0; ct < 4; ct++)
-#pragma unroll
-                    for (int j = 0; j < 4; j++) Wst[16 * r + 4 * gq + j][cbase + 16 * ct + n] = (half_t)U[r][ct][j];
-        }
-        lds_barrier();
-        half8* wf = (half8*)((half_t*)(ws + L.w) + vu * CH * D);
-#pragma unroll
-        for (int it = 0; it < 4; it++) {
-            const int f = tid + 256 * it;
-            int r, c0;
-            afrag_coords(f, 4, r, c0);
-            wf[f] = ld_h8(&Wst[r][c0]);
-        }
+        df.d = h4(dv);
     }
 }
 
-template <typename Tin>
-__global__ void __launch_bounds__(256, 3) delta_chunk_intra(const Tin* __restrict__ q, const Tin* __restrict__ k,
-                                                         const Tin* __restrict__ v, const float* __restrict__ g,
-                                                         const float* __restrict__ beta, SeqLayout a, int t0, int T,
-                                                         int HK, int HV, int normalize, float qscale, float eps,
-                                                         unsigned char* __restrict__ ws, WsLayout L, int vec_in) {
-    __shared__ K1Smem<sizeof(Tin) == 4> sm;
-    chunk_intra_body<Tin>(q, k, v, g, beta, a, t0, T, HK, HV, normalize, qscale, eps, ws, L, vec_in, sm, blockIdx.x,
-                          blockIdx.y, blockIdx.z, gridDim.x);
+// The deferred operands of one chunk into AD / IH / IL.
+template <bool kLo>
+__device__ __forceinline__ void write_deferred(Smem<kLo>& sm, const Deferred& df, int wave, int n, int g) {
+    const int wv = wave, iq = 3 - wave;
+#pragma unroll
+    for (int jt = 0; jt < 3; jt++)
+        if (jt < wv) *(half4*)&sm.AD[16 * wv + n][16 * jt + 4 * g] = df.am[jt];
+#pragma unroll
+    for (int r = 0; r < 4; r++) sm.AD[16 * wv + 4 * g + r][16 * wv + n] = df.d[r];
+#pragma unroll
+    for (int jt = 0; jt < 4; jt++)
+        if (jt <= iq) {
+            *(half4*)&sm.IH[16 * iq + n][16 * jt + 4 * g] = df.ih[jt];
+            *(half4*)&sm.IL[16 * iq + n][16 * jt + 4 * g] = df.il[jt];
+        }
+    if ((iq & 1) == 0) {  // the zero partner block of the 32-wide k step holding the diagonal
+        *(half4*)&sm.IH[16 * iq + n][16 * (iq + 1) + 4 * g] = half4{0, 0, 0, 0};
+        *(half4*)&sm.IL[16 * iq + n][16 * (iq + 1) + 4 * g] = half4{0, 0, 0, 0};
+    }
 }
 
 // ---------------------------------------------------------------------------------------------
-// K2: sequential recurrence over the chunks of a segment. 1-D grid of (B HV rounded up to 8) x
-// 128 / (16 NCT) blocks, 256 threads; Lb is the block's index in that grid.
-// Wave w holds S rows [32w, 32w+32) x the slice's 16 NCT columns as 2 x NCT MFMA tiles.
-template <int NCT>
-struct K2Smem {
-    // double-buffered by chunk parity: a wave cannot pass the next chunk's first barrier before
-    // every wave has finished reading this chunk's tiles, so no end-of-chunk barrier is needed
-    __attribute__((aligned(16))) half_t SsT[2][16 * NCT][D + 8];   // S^T (fp16): [column][dk]
-    __attribute__((aligned(16))) half_t VnT[2][16 * NCT][CH + 8];  // v_new^T (fp16 hi)
-    __attribute__((aligned(16))) half_t VlT[2][16 * NCT][CH + 8];  // v_new^T (fp16 lo)
-    __attribute__((aligned(16))) half_t VdT[2][16 * NCT][CH + 8];  // (e^{cum_last-cum} v_new)^T
-    __attribute__((aligned(16))) float Ot[4][16][16 * NCT + 4];  // output staging per wave
-};
+// The chain of one chunk for the 32 columns of one wave.
 
-template <typename Tout, int NCT, bool VEC>
-__device__ __forceinline__ void chunk_state_body(const unsigned char* __restrict__ ws, const WsLayout& L,
-                                                 float* __restrict__ state, int load_state, Tout* __restrict__ out,
-                                                 const SeqLayout& a, int t0, int T, int nch, int B, int HK, int HV,
-                                                 K2Smem<NCT>& sm, int Lb) {
-    auto& SsT = sm.SsT;
-    auto& VnT = sm.VnT;
-    auto& VlT = sm.VlT;
-    auto& VdT = sm.VdT;
-    auto& Ot = sm.Ot;
+// X = k S (tokens x columns), C layout [token tile][column tile]
+template <bool kLo>
+__device__ __forceinline__ void chain_x(const Smem<kLo>& sm, int buf, const half8 (&shi)[4][2], int n, int g,
+                                        f32x4 (&X)[4][2]) {
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        X[t][0] = X[t][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int m = 0; m < 4; m++) {
+            const half8 a = ld_perm(&sm.K[buf][16 * t + n][0], m, g);
+            X[t][0] = mfma32(a, shi[m][0], X[t][0]);
+            X[t][1] = mfma32(a, shi[m][1], X[t][1]);
+        }
+    }
+}
 
-    // XCD-aware block mapping (1-D grid): blocks are dealt to the 8 XCDs round-robin, so unit
-    // u = (m / NS) * 8 + xcd keeps all NS column slices of one (sequence, head) on one XCD,
-    // where they share the chunk operands in that XCD's L2.
-    constexpr int NS = D / (16 * NCT);
-    const int xcd = Lb % 8, m = Lb / 8;
-    const int unit = (m / NS) * 8 + xcd, sl = m % NS;
-    if (unit >= B * HV) return;  // grid padded to a multiple of 8 units
-    const int hv = unit % HV, b = unit / HV;
-    const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE, n = lane % 16, gq = lane / 16;
-    const int R = HV / HK, kh = hv / R;
-    const int col0 = sl * 16 * NCT;
-    float* Sg = state + (size_t)(b * HV + hv) * D * D;
-
-    f32x4 S[2][NCT];
+// Right-hand side R = beta v - fx X (kWithV) or -fx X
+template <bool kWithV, bool kLo>
+__device__ __forceinline__ void chain_r(const Smem<kLo>& sm, int buf, int wave, int n, int g, f32x4 (&X)[4][2]) {
+    const Fact& F = sm.F[buf];
 #pragma unroll
-    for (int rt = 0; rt < 2; rt++)
+    for (int t = 0; t < 4; t++) {
+        const f32x4 fx = *(const f32x4*)&F.fx[16 * t + 4 * g];
+        f32x4 bt;
+        if constexpr (kWithV) bt = *(const f32x4*)&F.beta[16 * t + 4 * g];
 #pragma unroll
-        for (int ct = 0; ct < NCT; ct++)
+        for (int ct = 0; ct < 2; ct++) {
+            f32x4 r = -(fx * X[t][ct]);
+            if constexpr (kWithV) {
+                const half4 vv = ld_tr(&sm.V[0][0], RS, 16 * t + 4 * g, 32 * wave + 16 * ct, n);
+                half4 vl = {0, 0, 0, 0};
+                if constexpr (kLo) vl = ld_tr(&sm.VL[0][0][0], RS, 16 * t + 4 * g, 32 * wave + 16 * ct, n);
 #pragma unroll
-            for (int j = 0; j < 4; j++)
-                S[rt][ct][j] = load_state ? Sg[(size_t)(32 * wave + 16 * rt + 4 * gq + j) * D + col0 + 16 * ct + n] : 0.f;
-
-    const size_t vbase = (size_t)(b * HV + hv) * nch, kbase = (size_t)(b * HK + kh) * nch;
-    // operands of one chunk that do not depend on S; each part is refilled with the next chunk's
-    // values while the current chunk computes (see step), hiding the L2 / HBM latency
-    struct Ops {
-        half8 wa[4], qa[4], ia[2], il[2], ka[2][2];
-        f32x4 uu[NCT], ecum, edec;  // u fragment; e^{cum_i}, e^{cum_last - cum_i} for this lane's rows
-        float gamma;              // e^{cum_last}
-    };
-    // part < 0: every operand; part 0..4: the slice of the fetch issued at that phase of step()
-    auto fetch = [&](int c, Ops& o, int part = -1) {
-        const size_t vu = vbase + c, ku = kbase + c;
-        const half_t* Wc = (const half_t*)(ws + L.w) + vu * CH * D;
-        const half_t* Qc = (const half_t*)(ws + L.qn) + ku * CH * D;
-        const float* Uc = (const float*)(ws + L.u) + vu * CH * D;
-        const half_t* Ic = (const half_t*)(ws + L.intra) + vu * CH * CH;
-        const half_t* Ilc = (const half_t*)(ws + L.intra_lo) + vu * CH * CH;
-        const half_t* KTc = (const half_t*)(ws + L.knt) + ku * CH * D;
-        const float* dec = (const float*)(ws + L.cum) + vu * 3 * CH;
-        // fragment-order operands (written so by K1): one contiguous 1 KB load per fragment.
-        // Parts in the order step() consumes them: 0 = w, q_n (w S, q_n S); 1 = u, e^{cum_last -
-        // cum} (v_new); 2 = intra, e^{cum} (output); 3 = k_n^T, e^{cum_last} (state update)
-        if (part < 0 || part == 0)
-#pragma unroll
-            for (int ks = 0; ks < 4; ks++) {
-                o.wa[ks] = ld_h8(Wc + ((4 * wave + ks) * 64 + lane) * 8);
-                o.qa[ks] = ld_h8(Qc + ((4 * wave + ks) * 64 + lane) * 8);
-            }
-        if (part < 0 || part == 1) {
-#pragma unroll
-            for (int ct = 0; ct < NCT; ct++)
-                o.uu[ct] = *(const f32x4*)(Uc + u_frag(16 * wave + 4 * gq, col0 + 16 * ct + n));
-            o.edec = *(const f32x4*)(dec + CH + 16 * wave + 4 * gq);
-        }
-        if (part < 0 || part == 2) {
-#pragma unroll
-            for (int ks = 0; ks < 2; ks++) {
-                o.ia[ks] = ld_h8(Ic + ((2 * wave + ks) * 64 + lane) * 8);
-                o.il[ks] = ld_h8(Ilc + ((2 * wave + ks) * 64 + lane) * 8);
-            }
-            o.ecum = *(const f32x4*)(dec + 16 * wave + 4 * gq);
-        }
-        if (part < 0 || part == 3) {
-#pragma unroll
-            for (int rt = 0; rt < 2; rt++)
-#pragma unroll
-                for (int ks = 0; ks < 2; ks++)
-                    o.ka[rt][ks] = ld_h8(KTc + ((2 * (2 * wave + rt) + ks) * 64 + lane) * 8);
-            o.gamma = dec[2 * CH];
-        }
-    };
-    // per-chunk compute on operands `op`. Each part of `op` is refilled with chunk cn's values
-    // right after its last use, so one register set suffices and the vector-memory path streams
-    // the next chunk's operands while this chunk computes (a load burst would stall the wave at
-    // issue; the operand volume per chunk is the bound of this loop)
-    auto step = [&](int c, Ops& op, int cn) {
-        const Ops& cur = op;
-        auto issue = [&](int part) {
-            __builtin_amdgcn_sched_barrier(0);
-            fetch(cn, op, part);
-            __builtin_amdgcn_sched_barrier(0);
-        };
-        const half8* wa = cur.wa;
-        const half8* qa = cur.qa;
-        const half8* ia = cur.ia;
-        const half8* il = cur.il;
-        const f32x4* uu = cur.uu;
-
-        const int pb = c & 1;
-        // (1) S -> LDS as fp16, transposed (a lane's 4 rows are adjacent in S^T: one 8-byte write)
-#pragma unroll
-        for (int rt = 0; rt < 2; rt++)
-#pragma unroll
-            for (int ct = 0; ct < NCT; ct++) {
-                const half4 h = {(half_t)S[rt][ct][0], (half_t)S[rt][ct][1], (half_t)S[rt][ct][2], (half_t)S[rt][ct][3]};
-                *(half4*)&SsT[pb][16 * ct + n][32 * wave + 16 * rt + 4 * gq] = h;
-            }
-        __syncthreads();
-
-        // (2) w S, then q_n S, for chunk rows [16 wave, 16 wave + 16): v_new needs only w S, so
-        // its VALU work overlaps the q_n S products in the MFMA pipe
-        half8 sb[NCT][4];
-#pragma unroll
-        for (int ct = 0; ct < NCT; ct++)
-#pragma unroll
-            for (int ks = 0; ks < 4; ks++) sb[ct][ks] = ld_h8(&SsT[pb][16 * ct + n][32 * ks + 8 * gq]);
-        f32x4 WS[NCT], QS[NCT];
-#pragma unroll
-        for (int ct = 0; ct < NCT; ct++) {
-            WS[ct] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int ks = 0; ks < 4; ks++) WS[ct] = mfma16(wa[ks], sb[ct][ks], WS[ct]);
-        }
-#pragma unroll
-        for (int ct = 0; ct < NCT; ct++) {
-            QS[ct] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int ks = 0; ks < 4; ks++) QS[ct] = mfma16(qa[ks], sb[ct][ks], QS[ct]);
-        }
-        issue(0);
-        // (3) v_new = u - w S; decayed copy for the state update
-#pragma unroll
-        for (int ct = 0; ct < NCT; ct++) {
-            half4 hn, ln, hd;
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const float vn = uu[ct][j] - WS[ct][j];
-                hn[j] = (half_t)vn;
-                ln[j] = (half_t)(vn - (float)hn[j]);
-                hd[j] = (half_t)(cur.edec[j] * vn);
-            }
-            *(half4*)&VnT[pb][16 * ct + n][16 * wave + 4 * gq] = hn;
-            *(half4*)&VlT[pb][16 * ct + n][16 * wave + 4 * gq] = ln;
-            *(half4*)&VdT[pb][16 * ct + n][16 * wave + 4 * gq] = hd;
-        }
-        issue(1);
-        __syncthreads();
-
-        // (4) intra v_new, then (5) S = e^{cum_last} S + k_n^T v' in the MFMA pipe; the output
-        // staging and stores below overlap the state update
-        f32x4 ov[NCT];
-#pragma unroll
-        for (int ct = 0; ct < NCT; ct++) {
-            ov[ct] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int ks = 0; ks < 2; ks++) {
-                // intra v_new as hi hi + hi lo + lo hi
-                const half8 vh = ld_h8(&VnT[pb][16 * ct + n][32 * ks + 8 * gq]);
-                ov[ct] = mfma16(ia[ks], vh, ov[ct]);
-                ov[ct] = mfma16(ia[ks], ld_h8(&VlT[pb][16 * ct + n][32 * ks + 8 * gq]), ov[ct]);
-                ov[ct] = mfma16(il[ks], vh, ov[ct]);
-            }
-        }
-        {
-            const float gamma = cur.gamma;
-#pragma unroll
-            for (int rt = 0; rt < 2; rt++)
-#pragma unroll
-                for (int ct = 0; ct < NCT; ct++) {
-                    f32x4 acc = S[rt][ct] * gamma;
-#pragma unroll
-                    for (int ks = 0; ks < 2; ks++)
-                        acc = mfma16(cur.ka[rt][ks], ld_h8(&VdT[pb][16 * ct + n][32 * ks + 8 * gq]), acc);
-                    S[rt][ct] = acc;
+                for (int e = 0; e < 4; e++) {
+                    float x = (float)vv[e];
+                    if constexpr (kLo) x += (float)vl[e];
+                    r[e] += bt[e] * x;
                 }
+            }
+            X[t][ct] = r;
         }
-        // o = e^{cum} q_n S + intra v_new
+    }
+}
+
+// v_new = (I + A)^-1 R by blocked forward substitution; R in, V out (both C layout), Vh = fp16(V).
+// kZlo: the right-hand side of each D_r product as fp16 hi + lo.
+template <bool kZlo, bool kLo>
+__device__ __forceinline__ void chain_solve(const Smem<kLo>& sm, int n, int g, const f32x4 (&R)[4][2],
+                                            f32x4 (&V)[4][2], half4 (&Vh)[4][2]) {
 #pragma unroll
-        for (int ct = 0; ct < NCT; ct++)
+    for (int r = 0; r < 4; r++) {
+        f32x4 z[2] = {R[r][0], R[r][1]};
 #pragma unroll
-            for (int j = 0; j < 4; j++) Ot[wave][4 * gq + j][16 * ct + n] = cur.ecum[j] * QS[ct][j] + ov[ct][j];
-        wave_sync();
-        {   // this wave's 16 rows x 16 NCT columns: lane = (row, 8-column part), 64 / LPR rows
-            // per pass
-            constexpr int LPR = 2 * NCT;  // lanes per row
-            constexpr int RPP = WAVE / LPR;
-            const int tc = t0 + c * CH;  // first token of the chunk
-            if constexpr (VEC) {
-                // Raw buffer stores, issued on every lane: rows past T (or past the wave's 16)
-                // get an offset beyond num_records and the hardware drops them. A store count
-                // that does not depend on a branch lets the compiler's wait for the next chunk's
-                // operands (issued before these stores) leave the stores in flight.
-                const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-                    out + b * a.sb_o + (long long)tc * a.st_o + hv * a.sh_o + col0, (short)0, kOutRange, kBufWord3);
+        for (int kk = 0; kk < r; kk++) {
+            const half4 a = ld4(&sm.AD[16 * r + n][16 * kk + 4 * g]);  // -A_rk
+            z[0] = mfma16(a, Vh[kk][0], z[0]);
+            z[1] = mfma16(a, Vh[kk][1], z[1]);
+        }
+        const half4 dr = ld4(&sm.AD[16 * r + n][16 * r + 4 * g]);
 #pragma unroll
-                for (int r0 = 0; r0 < 16; r0 += RPP) {
-                    const int r = r0 + lane / LPR, p8 = (lane % LPR) * 8, row = 16 * wave + r;
-                    const bool ok = r < 16 && tc + row < T;
-                    const int off = ok ? (int)(((long long)row * a.st_o + p8) * (long long)sizeof(Tout)) : kOutDrop;
-                    // two 16-byte LDS reads per lane (row pitch and p8 keep them aligned)
-                    const f32x4 s0 = *(const f32x4*)&Ot[wave][r & 15][p8];
-                    const f32x4 s1 = *(const f32x4*)&Ot[wave][r & 15][p8 + 4];
-                    if constexpr (sizeof(Tout) == 2) {
-                        const u32x4 pk = {f2bf2(s0[0], s0[1]), f2bf2(s0[2], s0[3]), f2bf2(s1[0], s1[1]),
-                                          f2bf2(s1[2], s1[3])};
-                        __builtin_amdgcn_raw_buffer_store_b128(pk, rs, off, 0, 0);
-                    } else {
-                        const u32x4 lo = __builtin_bit_cast(u32x4, s0);
-                        const u32x4 hi = __builtin_bit_cast(u32x4, s1);
-                        __builtin_amdgcn_raw_buffer_store_b128(lo, rs, off, 0, 0);
-                        __builtin_amdgcn_raw_buffer_store_b128(hi, rs, ok ? off + 16 : kOutDrop, 0, 0);
-                    }
-                }
+        for (int ct = 0; ct < 2; ct++) {
+            half4 zh, zl;
+            if constexpr (kZlo) {
+                split4(z[ct], zh, zl);
+                V[r][ct] = mfma16(dr, zl, mfma16(dr, zh, f32x4{0.f, 0.f, 0.f, 0.f}));
             } else {
+                V[r][ct] = mfma16(dr, h4(z[ct]), f32x4{0.f, 0.f, 0.f, 0.f});
+            }
+            Vh[r][ct] = h4(V[r][ct]);
+        }
+    }
+}
+
+// S = gam S + k^T (fp V). kPlo: the B operand fp V as fp16 hi + lo (else hi); with kLo the k low
+// parts add a third product.
+template <bool kPlo, bool kLo>
+__device__ __forceinline__ void chain_update(const Smem<kLo>& sm, int buf, int n, int g, const f32x4 (&V)[4][2],
+                                             f32x4 (&S)[8][2]) {
+    const Fact& F = sm.F[buf];
+    half4 ph[4][2], pl[4][2];
 #pragma unroll
-                for (int r0 = 0; r0 < 16; r0 += RPP) {
-                    const int r = r0 + lane / LPR, p8 = (lane % LPR) * 8, tok = tc + 16 * wave + r;
-                    if (r < 16 && tok < T) {
-                        Tout* dst = out + b * a.sb_o + (long long)tok * a.st_o + hv * a.sh_o + col0 + p8;
-                        const float* src = &Ot[wave][r][p8];
+    for (int t = 0; t < 4; t++) {
+        const f32x4 fp = *(const f32x4*)&F.fp[16 * t + 4 * g];
 #pragma unroll
-                        for (int e = 0; e < 8; e++) Act<Tout>::st(dst, e, src[e]);
+        for (int ct = 0; ct < 2; ct++) {
+            if constexpr (kPlo) split4(fp * V[t][ct], ph[t][ct], pl[t][ct]);
+            else ph[t][ct] = h4(fp * V[t][ct]);
+        }
+    }
+    const float gam = F.gam;
+#pragma unroll
+    for (int ft = 0; ft < 8; ft++) {
+        half8 a[2], al[2];
+#pragma unroll
+        for (int m = 0; m < 2; m++) {
+            a[m] = cat8(ld_tr(&sm.K[buf][0][0], RS, 32 * m + 4 * g, 16 * ft, n),
+                        ld_tr(&sm.K[buf][0][0], RS, 32 * m + 16 + 4 * g, 16 * ft, n));
+            if constexpr (kLo && kPlo)
+                al[m] = cat8(ld_tr(&sm.KL[buf][0][0], RS, 32 * m + 4 * g, 16 * ft, n),
+                             ld_tr(&sm.KL[buf][0][0], RS, 32 * m + 16 + 4 * g, 16 * ft, n));
+        }
+#pragma unroll
+        for (int ct = 0; ct < 2; ct++) {
+            f32x4 acc = S[ft][ct] * gam;
+#pragma unroll
+            for (int m = 0; m < 2; m++) {
+                const half8 bh = cat8(ph[2 * m][ct], ph[2 * m + 1][ct]);
+                acc = mfma32(a[m], bh, acc);
+                if constexpr (kPlo) acc = mfma32(a[m], cat8(pl[2 * m][ct], pl[2 * m + 1][ct]), acc);
+                if constexpr (kLo && kPlo) acc = mfma32(al[m], bh, acc);
+            }
+            S[ft][ct] = acc;
+        }
+    }
+}
+
+__device__ __forceinline__ void make_shi(const f32x4 (&S)[8][2], half8 (&shi)[4][2]) {
+#pragma unroll
+    for (int m = 0; m < 4; m++)
+#pragma unroll
+        for (int ct = 0; ct < 2; ct++) shi[m][ct] = cat8(h4(S[2 * m][ct]), h4(S[2 * m + 1][ct]));
+}
+
+// C-layout tiles of a [128][128] fp32 row-major matrix for this wave's 32 columns
+__device__ __forceinline__ void load_state(const float* src, int wave, int n, int g, f32x4 (&S)[8][2]) {
+#pragma unroll
+    for (int ft = 0; ft < 8; ft++)
+#pragma unroll
+        for (int ct = 0; ct < 2; ct++)
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+                S[ft][ct][r] = src ? src[(size_t)(16 * ft + 4 * g + r) * D + 32 * wave + 16 * ct + n] : 0.f;
+}
+__device__ __forceinline__ void store_state(float* dst, int wave, int n, int g, const f32x4 (&S)[8][2]) {
+#pragma unroll
+    for (int ft = 0; ft < 8; ft++)
+#pragma unroll
+        for (int ct = 0; ct < 2; ct++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) dst[(size_t)(16 * ft + 4 * g + r) * D + 32 * wave + 16 * ct + n] = S[ft][ct][r];
+}
+
+// Workgroup -> (sequence, value head, segment). The value heads sharing a QK head go to the same
+// XCD (block ids congruent mod 8), so their q / k rows are read through one L2.
+__device__ __forceinline__ bool unit_of(int x, const Params& p, int nseg, int& b, int& hv, int& s) {
+    const int R = p.HV / p.HK, xcd = x % 8, m = x / 8;
+    const int r = m % R, grp = (m / R) * 8 + xcd;
+    const int ngrp = p.B * nseg * p.HK;
+    if (grp >= ngrp) return false;
+    const int kh = grp % p.HK;
+    s = (grp / p.HK) % nseg;
+    b = grp / (p.HK * nseg);
+    hv = kh * R + r;
+    return true;
+}
+
+// ---------------------------------------------------------------------------------------------
+// kOut: launch 2 (outputs from the segment's start state). !kOut: launch 1 (segment end state
+// N and transition M from a zero start, segment 0 from the initial state).
+template <typename Tin, typename Tout, bool kOut>
+__global__ void __launch_bounds__(NT, 1) delta_seg_kernel(Params p) {
+    constexpr bool kLo = sizeof(Tin) == 4;
+    extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
+    Smem<kLo>& sm = *(Smem<kLo>*)smem_raw;
+    int b, hv, s;
+    if (!unit_of(blockIdx.x, p, kOut ? p.P : p.P - 1, b, hv, s)) return;
+    const int tid = threadIdx.x, lane = tid % WAVE, n = lane % 16, g = lane / 16;
+    const int wave = __builtin_amdgcn_readfirstlane(tid / WAVE);
+    const int c0 = s * p.L, c1 = min(p.nch, c0 + p.L);
+    const size_t unit = (size_t)(b * p.HV + hv);
+    constexpr size_t DD = (size_t)D * D;
+
+    f32x4 S[8][2];
+    f32x4 M[8][2];
+    if constexpr (kOut) {
+        const float* src = p.P > 1 ? p.starts + (unit * p.P + s) * DD : (p.init ? p.init + unit * DD : nullptr);
+        load_state(src, wave, n, g, S);
+    } else {
+        load_state(s == 0 && p.init ? p.init + unit * DD : nullptr, wave, n, g, S);
+        if (s == 0) store_state(p.starts + unit * p.P * DD, wave, n, g, S);
+#pragma unroll
+        for (int ft = 0; ft < 8; ft++)
+#pragma unroll
+            for (int ct = 0; ct < 2; ct++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) M[ft][ct][r] = (16 * ft + 4 * g + r == 32 * wave + 16 * ct + n) ? 1.f : 0.f;
+    }
+
+    Raw<Tin> raw;
+    RawGB gb;
+    Conv<kLo> cv;
+    Deferred df;
+    // prologue: chunk c0's operands
+    load_chunk<Tin>(p, b, hv, c0, wave, n, g, lane, raw, gb);
+    prep_a<Tin, kLo>(p, sm, c0 & 1, raw, gb, wave, n, g, lane, cv);
+    load_chunk<Tin>(p, b, hv, c0 + 1, wave, n, g, lane, raw, gb);
+    lds_barrier();
+    prep_b<kLo>(sm, c0 & 1, cv, wave, n, g, df);
+    lds_barrier();
+
+    for (int c = c0; c < c1; c++) {
+        const int buf = c & 1, nb = buf ^ 1;
+        // ---- phase 1: chain products on S; chunk c's A / D / intra into LDS; prep A of chunk c + 1
+        write_deferred<kLo>(sm, df, wave, n, g);
+        half8 shi[4][2];
+        make_shi(S, shi);
+        f32x4 X[4][2];
+        chain_x(sm, buf, shi, n, g, X);
+        f32x4 O[2][4];
+        if constexpr (kOut) {
+            // o^T = S^T (rq e^cum q)^T: A = S as it stands, B = the scaled q rows
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                O[0][t] = O[1][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int m = 0; m < 4; m++) {
+                    const half8 bq = ld_perm(&sm.Q[16 * t + n][0], m, g);
+                    O[0][t] = mfma32(shi[m][0], bq, O[0][t]);
+                    O[1][t] = mfma32(shi[m][1], bq, O[1][t]);
+                }
+            }
+        }
+        chain_r<true, kLo>(sm, buf, wave, n, g, X);
+        prep_a<Tin, kLo>(p, sm, nb, raw, gb, wave, n, g, lane, cv);
+        load_chunk<Tin>(p, b, hv, c + 2, wave, n, g, lane, raw, gb);
+        // Q / V of chunk c are consumed; AD / IH / IL of chunk c and K[nb], F[nb] of chunk c + 1 are
+        // complete
+        lds_barrier();
+
+        // ---- phase 2: substitution, output, state update; prep B of chunk c + 1
+        f32x4 V[4][2];
+        half4 Vh[4][2];
+        chain_solve<true, kLo>(sm, n, g, X, V, Vh);
+        if constexpr (kOut) {
+            // o^T += v_new^T intra^T (hi hi + hi lo + lo hi), k steps below the diagonal only
+            half4 Vl[4][2];
+#pragma unroll
+            for (int t = 0; t < 4; t++)
+#pragma unroll
+                for (int ct = 0; ct < 2; ct++) {
+                    const f32x4 d = V[t][ct];
+                    Vl[t][ct] = h4(f32x4{d[0] - (float)Vh[t][ct][0], d[1] - (float)Vh[t][ct][1],
+                                         d[2] - (float)Vh[t][ct][2], d[3] - (float)Vh[t][ct][3]});
+                }
+#pragma unroll
+            for (int it = 0; it < 4; it++) {
+#pragma unroll
+                for (int m = 0; m <= it / 2; m++) {
+                    const half8 ih = ld_perm(&sm.IH[16 * it + n][0], m, g);
+                    const half8 il = ld_perm(&sm.IL[16 * it + n][0], m, g);
+#pragma unroll
+                    for (int ct = 0; ct < 2; ct++) {
+                        const half8 vh = cat8(Vh[2 * m][ct], Vh[2 * m + 1][ct]);
+                        const half8 vl = cat8(Vl[2 * m][ct], Vl[2 * m + 1][ct]);
+                        O[ct][it] = mfma32(vh, ih, O[ct][it]);
+                        O[ct][it] = mfma32(vh, il, O[ct][it]);
+                        O[ct][it] = mfma32(vl, ih, O[ct][it]);
+                    }
+                }
+            }
+            // lane (n, g) of tile (ct, t) holds o[token 16 t + n][32 wave + 16 ct + 4 g .. + 3]
+            Tout* out = (Tout*)p.out;
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                const int tok = c * CH + 16 * t + n;
+                if (tok < p.T) {
+                    Tout* dst = out + b * p.a.sb_o + (long long)tok * p.a.st_o + hv * p.a.sh_o + 32 * wave + 4 * g;
+#pragma unroll
+                    for (int ct = 0; ct < 2; ct++) {
+                        if constexpr (sizeof(Tout) == 2) {
+                            const f32x4 o = O[ct][t];
+                            *(uint2*)(dst + 16 * ct) = uint2{f2bf2(o[0], o[1]), f2bf2(o[2], o[3])};
+                        } else {
+                            *(f32x4*)(dst + 16 * ct) = O[ct][t];
+                        }
                     }
                 }
             }
         }
-        issue(2);
-        issue(3);
-    };
-    // the first chunk's operands in the order the loop refills them, with a discarded store where
-    // the loop body has its output store, so the loop entry and the back edge carry the same
-    // sequence of memory operations (static wait counts)
-    Ops op;
-    fetch(0, op, 0);
-    fetch(0, op, 1);
-    if constexpr (VEC) {
-        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(out, (short)0, kOutRange, kBufWord3);
-        __builtin_amdgcn_raw_buffer_store_b128(u32x4{0u, 0u, 0u, 0u}, rs, kOutDrop, 0, 0);
-        if constexpr (sizeof(Tout) == 4)
-            __builtin_amdgcn_raw_buffer_store_b128(u32x4{0u, 0u, 0u, 0u}, rs, kOutDrop - 64, 0, 0);
+        chain_update<true, kLo>(sm, buf, n, g, V, S);
+        if constexpr (!kOut) {
+            // the transition's products after the state's, so their temporaries do not overlap
+            half8 mhi[4][2];
+            make_shi(M, mhi);
+            f32x4 XM[4][2];
+            chain_x(sm, buf, mhi, n, g, XM);
+            chain_r<false, kLo>(sm, buf, wave, n, g, XM);
+            f32x4 VM[4][2];
+            half4 VMh[4][2];
+            chain_solve<true, kLo>(sm, n, g, XM, VM, VMh);
+            chain_update<false, kLo>(sm, buf, n, g, VM, M);
+        }
+        prep_b<kLo>(sm, nb, cv, wave, n, g, df);
+        lds_barrier();
     }
-    fetch(0, op, 2);
-    fetch(0, op, 3);
-    // the next-chunk index is clamped, not skipped, so every step issues the same loads
-    for (int c = 0; c < nch; c++) step(c, op, min(c + 1, nch - 1));
-#pragma unroll
-    for (int rt = 0; rt < 2; rt++)
-#pragma unroll
-        for (int ct = 0; ct < NCT; ct++)
-#pragma unroll
-            for (int j = 0; j < 4; j++) Sg[(size_t)(32 * wave + 16 * rt + 4 * gq + j) * D + col0 + 16 * ct + n] = S[rt][ct][j];
-}
 
-template <typename Tout, int NCT, bool VEC>
-__global__ void __launch_bounds__(256, 2) delta_chunk_state(const unsigned char* __restrict__ ws, WsLayout L,
-                                                         float* __restrict__ state, int load_state, Tout* __restrict__ out,
-                                                         SeqLayout a, int t0, int T, int nch, int B, int HK,
-                                                         int HV) {
-    __shared__ K2Smem<NCT> sm;
-    chunk_state_body<Tout, NCT, VEC>(ws, L, state, load_state, out, a, t0, T, nch, B, HK, HV, sm, blockIdx.x);
-}
-
-// One launch holding K2 of one segment (blocks [0, nk2)) and K1 of the next segment (the
-// remaining blocks, chunk fastest): the two are independent (different workspace buffers), so
-// the K1 workgroups fill the CUs around K2's without a second stream or events. LDS is the
-// union of the two bodies' needs.
-template <typename Tin, typename Tout, int NCT, bool VEC>
-__global__ void __launch_bounds__(256, 3) delta_chunk_fused(
-    // K2 of segment s
-    const unsigned char* __restrict__ ws2, WsLayout L2, float* __restrict__ state, int load_state,
-    Tout* __restrict__ out, int t0s, int nch2, int nk2,
-    // K1 of segment s + 1
-    const Tin* __restrict__ q, const Tin* __restrict__ k, const Tin* __restrict__ v, const float* __restrict__ g,
-    const float* __restrict__ beta, int t0i, int nch1, unsigned char* __restrict__ ws1, WsLayout L1, int vec_in,
-    int normalize, float qscale, float eps,
-    // shared
-    SeqLayout a, int T, int B, int HK, int HV) {
-    __shared__ union {
-        K1Smem<sizeof(Tin) == 4> k1;
-        K2Smem<NCT> k2;
-    } sm;
-    if ((int)blockIdx.x < nk2) {
-        chunk_state_body<Tout, NCT, VEC>(ws2, L2, state, load_state, out, a, t0s, T, nch2, B, HK, HV, sm.k2,
-                                         blockIdx.x);
+    if constexpr (kOut) {
+        if (s == p.P - 1) store_state(p.final_state + unit * DD, wave, n, g, S);
     } else {
-        const int r = blockIdx.x - nk2, c = r % nch1, hv = (r / nch1) % HV, b = r / (nch1 * HV);
-        chunk_intra_body<Tin>(q, k, v, g, beta, a, t0i, T, HK, HV, normalize, qscale, eps, ws1, L1, vec_in, sm.k1, c,
-                              hv, b, nch1);
+        const size_t seg = unit * (p.P - 1) + s;
+        store_state(p.nbuf + seg * DD, wave, n, g, S);
+        half_t* mb = p.mbuf + seg * DD;
+#pragma unroll
+        for (int ft = 0; ft < 8; ft++)
+#pragma unroll
+            for (int ct = 0; ct < 2; ct++)
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+                    mb[(size_t)(16 * ft + 4 * g + r) * D + 32 * wave + 16 * ct + n] = (half_t)M[ft][ct][r];
     }
 }
 
-// Chunks per segment: SEG tokens (the workspace of one segment, ~72 MB at B = 1 with 32 value
-// heads, stays resident in the MALL between the two kernels that touch it).
-int seg_chunks(int B, int T, int HV) {
-    (void)B;
-    (void)HV;
-    return (std::min(T, SEG) + CH - 1) / CH;
+// Segment boundaries: S_1 = N_0, S_{s+1} = M_s S_s + N_s. One wave per (sequence, head,
+// 16-column slice); M_s as the fp16 A operand, S_s as fp16 hi + lo.
+__global__ void __launch_bounds__(WAVE) delta_seg_combine(Params p) {
+    const int unit = blockIdx.x / 8, slice = blockIdx.x % 8;
+    if (unit >= p.B * p.HV) return;
+    const int lane = threadIdx.x, n = lane % 16, g = lane / 16;
+    const int col = 16 * slice + n;
+    constexpr size_t DD = (size_t)D * D;
+    const float* N = p.nbuf + (size_t)unit * (p.P - 1) * DD;
+    const half_t* Mb = p.mbuf + (size_t)unit * (p.P - 1) * DD;
+    float* st = p.starts + (size_t)unit * p.P * DD;
+    f32x4 S[8];
+#pragma unroll
+    for (int ft = 0; ft < 8; ft++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) S[ft][r] = N[(size_t)(16 * ft + 4 * g + r) * D + col];
+#pragma unroll
+    for (int ft = 0; ft < 8; ft++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) st[DD + (size_t)(16 * ft + 4 * g + r) * D + col] = S[ft][r];
+    for (int s = 1; s + 1 < p.P; s++) {
+        half8 bh[4], bl[4];
+#pragma unroll
+        for (int m = 0; m < 4; m++) {
+            half4 h0, l0, h1, l1;
+            split4(S[2 * m], h0, l0);
+            split4(S[2 * m + 1], h1, l1);
+            bh[m] = cat8(h0, h1);
+            bl[m] = cat8(l0, l1);
+        }
+        const float* Ns = N + (size_t)s * DD;
+        const half_t* Ms = Mb + (size_t)s * DD;
+#pragma unroll
+        for (int ft = 0; ft < 8; ft++) {
+            f32x4 acc;
+#pragma unroll
+            for (int r = 0; r < 4; r++) acc[r] = Ns[(size_t)(16 * ft + 4 * g + r) * D + col];
+            const half_t* row = Ms + (size_t)(16 * ft + n) * D;
+#pragma unroll
+            for (int m = 0; m < 4; m++) {
+                const half8 a = cat8(*(const half4*)(row + 32 * m + 4 * g), *(const half4*)(row + 32 * m + 16 + 4 * g));
+                acc = mfma32(a, bh[m], acc);
+                acc = mfma32(a, bl[m], acc);
+            }
+            S[ft] = acc;
+        }
+        float* dst = st + (size_t)(s + 1) * DD;
+#pragma unroll
+        for (int ft = 0; ft < 8; ft++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) dst[(size_t)(16 * ft + 4 * g + r) * D + col] = S[ft][r];
+    }
+}
+
+__host__ __device__ inline size_t al256(size_t x) { return (x + 255) / 256 * 256; }
+
+// Segment split: enough (sequence, head, segment) units to cover the GPU's CUs, segments of at
+// least MIN_SEG_CHUNKS chunks.
+struct Split {
+    int nch, P, L;
+};
+Split split_for(int B, int T, int HV, int cus) {
+    Split sp;
+    sp.nch = (T + CH - 1) / CH;
+    const int units = B * HV;
+    int P = units >= cus ? 1 : std::max(1, cus / std::max(1, units));
+    P = std::min(P, std::max(1, sp.nch / MIN_SEG_CHUNKS));
+    sp.L = (sp.nch + P - 1) / P;
+    sp.P = (sp.nch + sp.L - 1) / sp.L;
+    return sp;
+}
+
+// CU count of the current device (256 when there is none), cached per device
+int device_cus() {
+    static std::atomic<int> cache[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 256;
+    if (dev < 64) {
+        const int c = cache[dev].load(std::memory_order_relaxed);
+        if (c > 0) return c;
+    }
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+    if (dev < 64) cache[dev].store(cus, std::memory_order_relaxed);
+    return cus;
+}
+
+struct WsPlan {
+    size_t state, starts, nbuf, mbuf, total;
+};
+WsPlan ws_plan(int B, int HV, const Split& sp, bool need_state) {
+    WsPlan w;
+    const size_t DD = (size_t)D * D, units = (size_t)B * HV;
+    size_t off = 0;
+    w.state = off;
+    if (need_state) off += al256(units * DD * 4);
+    w.starts = off;
+    if (sp.P > 1) {
+        off += al256(units * sp.P * DD * 4);
+        w.nbuf = off;
+        off += al256(units * (sp.P - 1) * DD * 4);
+        w.mbuf = off;
+        off += al256(units * (sp.P - 1) * DD * 2);
+    } else {
+        w.nbuf = w.mbuf = off;
+    }
+    w.total = std::max<size_t>(off, 256);
+    return w;
 }
 
 }  // namespace
 
 namespace aegist {
 
-// Workspace: [carried state (when the caller passes none)][segment buffer 0][segment buffer 1]
-// (the second buffer only when there is more than one segment: the intra-chunk work of the
-// next segment then writes one buffer while the state work of this segment reads the other).
-struct WsPlan {
-    size_t state_off, seg_bytes, total;
-    int nch_seg, nbuf;
-};
-static WsPlan ws_plan(int B, int T, int HK, int HV) {
-    WsPlan p;
-    p.nch_seg = seg_chunks(B, T, HV);
-    p.seg_bytes = ws_layout(B, HK, HV, p.nch_seg).state;  // the per-segment part, 256-aligned
-    p.nbuf = (T + CH - 1) / CH > p.nch_seg ? 2 : 1;
-    p.state_off = 0;
-    p.total = al256((size_t)B * HV * D * D * 4) + p.nbuf * p.seg_bytes;
-    return p;
-}
-
 size_t delta_chunked_ws_bytes(int B, int T, int HK, int HV) {
-    if (B <= 0 || T <= 0 || HK <= 0 || HV <= 0) return 256;
-    return ws_plan(B, T, HK, HV).total;
+    (void)HK;
+    if (B <= 0 || T <= 0 || HV <= 0) return 256;
+    return ws_plan(B, HV, split_for(B, T, HV, device_cus()), true).total;
 }
-
-template <typename Tin, typename Tout, bool VEC>
-int run_segments(const Tin* q, const Tin* k, const Tin* v, const float* g, const float* beta, float* S,
-                 bool has_state, Tout* out, const SeqLayout& a, int B, int T, int HK, int HV, int normalize,
-                 float qscale, float eps, unsigned char* const segbuf[2], const WsPlan& plan, int vec_in,
-                 hipStream_t st);
 
 template <typename Tin, typename Tout>
 int run_chunked(const Tin* q, const Tin* k, const Tin* v, const float* g, const float* beta, float* state, Tout* out,
                 const SeqLayout& a, int B, int T, int HK, int HV, int normalize, float qscale, float eps, void* ws,
                 size_t ws_bytes, hipStream_t st) {
-    const WsPlan plan = ws_plan(B, T, HK, HV);
-    if (!ws || ws_bytes < plan.total) return fail(AEGIST_ERR_WORKSPACE, "delta_chunked: workspace too small");
+    const Split sp = split_for(B, T, HV, device_cus());
+    const WsPlan wp = ws_plan(B, HV, sp, state == nullptr);
+    if (wp.total > 256 || state == nullptr) {
+        if (!ws || ws_bytes < wp.total) return fail(AEGIST_ERR_WORKSPACE, "delta_chunked: workspace too small");
+    }
+    // 16-byte row loads need 16-byte aligned rows; the output stores 8 (bf16) / 16 (fp32) bytes
+    const long long ei = 16 / (long long)sizeof(Tin), eo = 4;
+    const bool aligned = ((uintptr_t)q % 16 == 0) && ((uintptr_t)k % 16 == 0) && ((uintptr_t)v % 16 == 0) &&
+                         a.sb_qk % ei == 0 && a.st_qk % ei == 0 && a.sh_qk % ei == 0 && a.sb_v % ei == 0 &&
+                         a.st_v % ei == 0 && a.sh_v % ei == 0 && ((uintptr_t)out % (4 * sizeof(Tout)) == 0) &&
+                         a.sb_o % eo == 0 && a.st_o % eo == 0 && a.sh_o % eo == 0;
+    if (!aligned)
+        return fail(AEGIST_ERR_SHAPE, "delta_chunked: q, k, v rows must be 16-byte aligned and output rows 4-element aligned");
     unsigned char* w = (unsigned char*)ws;
-    // the carried state: the caller's, or the workspace copy (starts at zero: K2 does not load it)
-    float* S = state ? state : (float*)(w + plan.state_off);
-    unsigned char* segbuf[2] = {w + al256((size_t)B * HV * D * D * 4), nullptr};
-    segbuf[1] = segbuf[0] + plan.seg_bytes;
-    // 16-byte input loads need 16-byte aligned rows (and 8-element runs)
-    const long long ei = 16 / (long long)sizeof(Tin);
-    const int vec_in = ((uintptr_t)q % 16 == 0) && ((uintptr_t)k % 16 == 0) && ((uintptr_t)v % 16 == 0) &&
-                       a.sb_qk % ei == 0 && a.st_qk % ei == 0 && a.sh_qk % ei == 0 && a.sb_v % ei == 0 &&
-                       a.st_v % ei == 0 && a.sh_v % ei == 0;
-    // 16-byte buffer stores need 16-byte aligned rows, and the byte offsets of one chunk's rows
-    // from its first must stay below the buffer range
-    const long long ev = 16 / (long long)sizeof(Tout);
-    const bool vec_out = ((uintptr_t)out % 16 == 0) && a.sb_o % ev == 0 && a.st_o % ev == 0 && a.sh_o % ev == 0 &&
-                         a.st_o >= 0 && (long long)CH * a.st_o * (long long)sizeof(Tout) < kOutRange;
-    return vec_out ? run_segments<Tin, Tout, true>(q, k, v, g, beta, S, state != nullptr, out, a, B, T, HK, HV,
-                                                  normalize, qscale, eps, segbuf, plan, vec_in, st)
-                   : run_segments<Tin, Tout, false>(q, k, v, g, beta, S, state != nullptr, out, a, B, T, HK, HV,
-                                                   normalize, qscale, eps, segbuf, plan, vec_in, st);
-}
-
-template <typename Tin, typename Tout, bool VEC>
-int run_segments(const Tin* q, const Tin* k, const Tin* v, const float* g, const float* beta, float* S,
-                 bool has_state, Tout* out, const SeqLayout& a, int B, int T, int HK, int HV, int normalize,
-                 float qscale, float eps, unsigned char* const segbuf[2], const WsPlan& plan, int vec_in,
-                 hipStream_t st) {
-    const int seg = plan.nch_seg * CH;
-    const int nseg = (T + seg - 1) / seg;
-    const int units8 = (B * HV + 7) / 8 * 8;
-
-    auto seg_layout = [&](int s) {
-        const int t0 = s * seg, nch = (std::min(seg, T - t0) + CH - 1) / CH;
-        return std::make_pair(nch, ws_layout(B, HK, HV, nch));
+    Params p;
+    p.q = q;
+    p.k = k;
+    p.v = v;
+    p.g = g;
+    p.beta = beta;
+    p.out = out;
+    p.a = a;
+    p.T = T;
+    p.B = B;
+    p.HK = HK;
+    p.HV = HV;
+    p.nch = sp.nch;
+    p.P = sp.P;
+    p.L = sp.L;
+    p.normalize = normalize;
+    p.qscale = qscale;
+    p.eps = eps;
+    p.init = state;  // null: zero initial state
+    p.final_state = state ? state : (float*)(w + wp.state);
+    p.starts = sp.P > 1 ? (float*)(w + wp.starts) : nullptr;
+    p.nbuf = sp.P > 1 ? (float*)(w + wp.nbuf) : nullptr;
+    p.mbuf = sp.P > 1 ? (half_t*)(w + wp.mbuf) : nullptr;
+    const size_t lds = sizeof(Smem<sizeof(Tin) == 4>);
+    auto grid_for = [&](int nseg) {
+        const int R = HV / HK, ngrp = B * nseg * HK;
+        return (ngrp + 7) / 8 * 8 * R;
     };
-    const int nk2 = units8 * (D / (16 * K2_NCT));
-    // segment 0's K1 alone; then K2 of segment s with K1 of segment s + 1 in one launch; the last
-    // K2 alone. Stream order carries every dependency: K1(s + 1) rewrites the buffer K2(s - 1)
-    // read one launch earlier.
-    {
-        const auto [nch, Ls] = seg_layout(0);
-        delta_chunk_intra<Tin><<<dim3(nch, HV, B), 256, 0, st>>>(q, k, v, g, beta, a, 0, T, HK, HV, normalize, qscale,
-                                                                eps, segbuf[0], Ls, vec_in);
-        int rc = after_launch("delta_chunk_intra");
+    if (sp.P > 1) {
+        delta_seg_kernel<Tin, Tout, false><<<grid_for(sp.P - 1), NT, lds, st>>>(p);
+        int rc = after_launch("delta_seg_kernel(transition)");
+        if (rc) return rc;
+        delta_seg_combine<<<B * HV * 8, WAVE, 0, st>>>(p);
+        rc = after_launch("delta_seg_combine");
         if (rc) return rc;
     }
-    for (int s = 0; s < nseg; s++) {
-        const auto [nch2, L2] = seg_layout(s);
-        const int load = (has_state || s > 0) ? 1 : 0;
-        if (s + 1 < nseg) {
-            const auto [nch1, L1] = seg_layout(s + 1);
-            // 2 KB of (unused) dynamic LDS on top of the 53 KB union: at most two workgroups per
-            // CU, so a K2 workgroup shares its CU with one K1 workgroup instead of two (measured
-            // 0.233 -> 0.228 ms per 8k call). Padding the static union instead lets the compiler
-            // see the lower occupancy and spend ~20 more VGPRs, which loses the gain.
-            delta_chunk_fused<Tin, Tout, K2_NCT, VEC><<<nk2 + nch1 * HV * B, 256, kFusedLdsPad, st>>>(
-                segbuf[s & 1], L2, S, load, out, s * seg, nch2, nk2, q, k, v, g, beta, (s + 1) * seg, nch1,
-                segbuf[(s + 1) & 1], L1, vec_in, normalize, qscale, eps, a, T, B, HK, HV);
-            int rc = after_launch("delta_chunk_fused");
-            if (rc) return rc;
-        } else {
-            delta_chunk_state<Tout, K2_NCT, VEC><<<nk2, 256, 0, st>>>(segbuf[s & 1], L2, S, load, out, a, s * seg, T,
-                                                                       nch2, B, HK, HV);
-            int rc = after_launch("delta_chunk_state");
-            if (rc) return rc;
-        }
-    }
-    return 0;
+    delta_seg_kernel<Tin, Tout, true><<<grid_for(sp.P), NT, lds, st>>>(p);
+    return after_launch("delta_seg_kernel(output)");
+}
+
+template <typename Tin, typename Tout>
+static int set_lds_limits() {
+    static int done = [] {
+        const int bytes = (int)sizeof(Smem<sizeof(Tin) == 4>);
+        const hipError_t e1 = hipFuncSetAttribute((const void*)delta_seg_kernel<Tin, Tout, false>,
+                                                  hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+        const hipError_t e2 = hipFuncSetAttribute((const void*)delta_seg_kernel<Tin, Tout, true>,
+                                                  hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+        return e1 == hipSuccess && e2 == hipSuccess ? 1 : -1;
+    }();
+    return done;
 }
 
 int launch_delta_chunked(const void* q, const void* k, const void* v, int in_dtype, const SeqLayout& a,
@@ -986,12 +927,13 @@ int launch_delta_chunked(const void* q, const void* k, const void* v, int in_dty
     if (B < 0 || T < 0 || HK <= 0 || HV <= 0 || HV % HK) return fail(AEGIST_ERR_SHAPE, "delta_chunked: need HV % HK == 0");
     if (B == 0 || T == 0) return 0;
 #define AEG_CHUNKED(TI, TO)                                                                                          \
+    set_lds_limits<TI, TO>();                                                                                        \
     return run_chunked<TI, TO>((const TI*)q, (const TI*)k, (const TI*)v, g, beta, state, (TO*)out, a, B, T, HK, HV, \
                                normalize, qscale, eps, ws, ws_bytes, st)
-    if (in_dtype == AEGIST_F32 && out_dtype == AEGIST_F32) AEG_CHUNKED(float, float);
-    if (in_dtype == AEGIST_F32 && out_dtype == AEGIST_BF16) AEG_CHUNKED(float, uint16_t);
-    if (in_dtype == AEGIST_BF16 && out_dtype == AEGIST_F32) AEG_CHUNKED(uint16_t, float);
-    if (in_dtype == AEGIST_BF16 && out_dtype == AEGIST_BF16) AEG_CHUNKED(uint16_t, uint16_t);
+    if (in_dtype == AEGIST_F32 && out_dtype == AEGIST_F32) { AEG_CHUNKED(float, float); }
+    if (in_dtype == AEGIST_F32 && out_dtype == AEGIST_BF16) { AEG_CHUNKED(float, uint16_t); }
+    if (in_dtype == AEGIST_BF16 && out_dtype == AEGIST_F32) { AEG_CHUNKED(uint16_t, float); }
+    if (in_dtype == AEGIST_BF16 && out_dtype == AEGIST_BF16) { AEG_CHUNKED(uint16_t, uint16_t); }
 #undef AEG_CHUNKED
     return fail(AEGIST_ERR_DTYPE, "delta_chunked: dtypes must be AEGIST_F32 or AEGIST_BF16");
 }
@@ -1009,11 +951,12 @@ int delta_scan_chunked(const float* y, const float* gb, float* state, float* o, 
 }  // namespace aegist
 
 extern "C" size_t aegist_delta_chunked_workspace_bytes(int B, int T, int HV) {
-    // HK only changes the q_n / k_n^T share; size for HK = HV (the largest). The segment length
-    // depends on B, so take the largest need over batches 1..B: a workspace sized for (B, T)
-    // then serves every call with B' <= B sequences of T' <= T tokens.
+    // the sequence split depends on B and T: take the largest need over batches 1..B and lengths
+    // up to T (in chunk steps), so a workspace sized for (B, T) serves every smaller call
     size_t need = 256;
-    for (int b = 1; b <= B; b++) need = std::max(need, delta_chunked_ws_bytes(b, T, HV, HV));
+    const int nch = (std::max(T, 1) + CH - 1) / CH;
+    for (int b = 1; b <= B; b++)
+        for (int c = 1; c <= nch; c++) need = std::max(need, delta_chunked_ws_bytes(b, c * CH, HV, HV));
     return need;
 }
 
