@@ -45,13 +45,17 @@ constexpr int D = 128;
 constexpr int CH = 64;
 constexpr int NW = 4;              // waves per workgroup
 constexpr int NT = NW * WAVE;      // threads per workgroup
-constexpr int RS = D + 8;          // fp16 row stride of the 64 x 128 tiles in LDS (bank spread)
-constexpr int RA = CH + 8;         // fp16 row stride of the 64 x 64 tiles
-constexpr int DWS = 20;            // fp32 row stride of a wave's 16 x 16 diagonal block
+// fp16 row strides in LDS. The chain reads 8 bytes per lane from 16 rows x 32 contiguous bytes
+// (4 lanes per row): a row stride of 8 banks (mod 64) spreads the 16 rows over all 64 banks in
+// two passes without conflicts.
+constexpr int RS = D + 16;         // 64 x 128 tiles read by the chain (288 B: 72 banks)
+constexpr int RSL = D + 8;         // low-part tiles of fp32 inputs (272 B)
+constexpr int RA = CH + 16;        // 64 x 64 tiles (160 B: 40 banks)
 constexpr int MIN_SEG_CHUNKS = 4;  // shortest segment the sequence split makes
 
 typedef _Float16 half_t;
 typedef short short4v_t __attribute__((ext_vector_type(4)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) short4v_t lds_s4;
@@ -80,9 +84,8 @@ struct Smem {
     __attribute__((aligned(16))) half_t IH[CH][RA];      // intra (fp16 hi)
     __attribute__((aligned(16))) half_t IL[CH][RA];      // intra (fp16 lo)
     __attribute__((aligned(16))) Fact F[2];
-    __attribute__((aligned(16))) float Dw[NW][16][DWS];  // fp32 diagonal block of A, per wave
-    __attribute__((aligned(16))) half_t KL[NL][CH][RS];  // k low parts, by chunk parity
-    __attribute__((aligned(16))) half_t VL[NL / 2][CH][RS];  // v low parts
+    __attribute__((aligned(16))) half_t KL[NL][CH][RSL];      // k low parts, by chunk parity
+    __attribute__((aligned(16))) half_t VL[NL / 2][CH][RSL];  // v low parts
 };
 
 static_assert(sizeof(Smem<false>) <= 160 * 1024 && sizeof(Smem<true>) <= 160 * 1024, "LDS of one workgroup exceeds a CU");
@@ -161,44 +164,60 @@ __device__ __forceinline__ void unpack8(const float4* src, int ks, float* o) {
     o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w; o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w;
 }
 
-// 32 features (4 runs of 8 at 32 ks + 8 g) of one row; zeros when !ok
-__device__ __forceinline__ void load_rows(const uint16_t* row, bool ok, int g, uint4* dst) {
-#pragma unroll
-    for (int ks = 0; ks < 4; ks++) {
-        uint4 x = *(const uint4*)(row + 32 * ks + 8 * g);
-        if (!ok) x = uint4{0u, 0u, 0u, 0u};
-        dst[ks] = x;
-    }
+// Buffer resource over [base, base + bytes): loads past the end return zeros, stores are dropped
+// (gfx9 word 3: 32-bit data, no swizzle).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, long long bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, (int)min(bytes, 0x7fffffffLL), 0x00020000);
 }
-__device__ __forceinline__ void load_rows(const float* row, bool ok, int g, float4* dst) {
+
+// 32 features (4 runs of 8 at 32 ks + 8 g) of the row at byte offset `off`; rows past the
+// resource's range read as zeros
+__device__ __forceinline__ void load_rows(__amdgpu_buffer_rsrc_t rs, int off, int g, uint4* dst) {
+#pragma unroll
+    for (int ks = 0; ks < 4; ks++)
+        dst[ks] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, off + 2 * (32 * ks + 8 * g), 0, 0));
+}
+__device__ __forceinline__ void load_rows(__amdgpu_buffer_rsrc_t rs, int off, int g, float4* dst) {
 #pragma unroll
     for (int ks = 0; ks < 4; ks++) {
-        float4 x0 = *(const float4*)(row + 32 * ks + 8 * g), x1 = *(const float4*)(row + 32 * ks + 8 * g + 4);
-        if (!ok) x0 = x1 = float4{0.f, 0.f, 0.f, 0.f};
-        dst[2 * ks] = x0;
-        dst[2 * ks + 1] = x1;
+        dst[2 * ks] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rs, off + 4 * (32 * ks + 8 * g), 0, 0));
+        dst[2 * ks + 1] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rs, off + 4 * (32 * ks + 8 * g + 4), 0, 0));
     }
 }
 
-// Issue the global loads of chunk c (tokens past T read a clamped row and are zeroed).
-template <typename Tin>
-__device__ __forceinline__ void load_chunk(const Params& p, int b, int hv, int c, int wave, int n, int g, int lane,
-                                           Raw<Tin>& r, RawGB& gb) {
+// Resources of one (sequence, value head): q / k rows of its QK head, v rows, g / beta, output.
+struct Rsrc {
+    __amdgpu_buffer_rsrc_t q, k, v, g, beta, out;
+};
+
+template <typename Tin, typename Tout>
+__device__ __forceinline__ Rsrc make_rsrc(const Params& p, int b, int hv) {
     const int R = p.HV / p.HK, kh = hv / R;
+    const long long last = (long long)(p.T - 1);
+    Rsrc r;
+    const long long off_qk = b * p.a.sb_qk + kh * p.a.sh_qk, len_qk = (last * p.a.st_qk + D) * (long long)sizeof(Tin);
+    r.q = rsrc((const Tin*)p.q + off_qk, len_qk);
+    r.k = rsrc((const Tin*)p.k + off_qk, len_qk);
+    r.v = rsrc((const Tin*)p.v + b * p.a.sb_v + hv * p.a.sh_v, (last * p.a.st_v + D) * (long long)sizeof(Tin));
+    const long long off_g = b * p.a.sb_g + hv, len_g = (last * p.a.st_g + 1) * 4;
+    r.g = rsrc(p.g + off_g, len_g);
+    r.beta = rsrc(p.beta + off_g, len_g);
+    r.out = rsrc((Tout*)p.out + b * p.a.sb_o + hv * p.a.sh_o, (last * p.a.st_o + D) * (long long)sizeof(Tout));
+    return r;
+}
+
+// Issue the global loads of chunk c (tokens past T read as zeros).
+template <typename Tin>
+__device__ __forceinline__ void load_chunk(const Params& p, const Rsrc& rs, int c, int wave, int n, int g, int lane,
+                                           Raw<Tin>& r, RawGB& gb) {
     const int tk = c * CH + 16 * wave + n, tq = c * CH + 16 * (3 - wave) + n;
-    const bool okk = tk < p.T, okq = tq < p.T;
-    const int tkc = okk ? tk : p.T - 1, tqc = okq ? tq : p.T - 1;
-    const Tin* q = (const Tin*)p.q;
-    const Tin* k = (const Tin*)p.k;
-    const Tin* v = (const Tin*)p.v;
-    load_rows(k + b * p.a.sb_qk + (long long)tkc * p.a.st_qk + kh * p.a.sh_qk, okk, g, r.k);
-    load_rows(q + b * p.a.sb_qk + (long long)tqc * p.a.st_qk + kh * p.a.sh_qk, okq, g, r.q);
-    load_rows(v + b * p.a.sb_v + (long long)tkc * p.a.st_v + hv * p.a.sh_v, okk, g, r.v);
-    const int t = c * CH + lane;
-    const bool ok = t < p.T;
-    const long long go = b * p.a.sb_g + (long long)(ok ? t : p.T - 1) * p.a.st_g + hv;
-    gb.g = ok ? p.g[go] : 0.f;
-    gb.beta = ok ? p.beta[go] : 0.f;
+    const int sz = (int)sizeof(Tin);
+    load_rows(rs.k, tk * (int)p.a.st_qk * sz, g, r.k);
+    load_rows(rs.q, tq * (int)p.a.st_qk * sz, g, r.q);
+    load_rows(rs.v, tk * (int)p.a.st_v * sz, g, r.v);
+    const int go = (c * CH + lane) * (int)p.a.st_g * 4;
+    gb.g = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs.g, go, 0, 0));
+    gb.beta = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs.beta, go, 0, 0));
 }
 
 // Converted rows a wave keeps between the two prep phases (lo parts: fp32 inputs only).
@@ -214,7 +233,7 @@ struct Conv {
 // (AD, IH, IL are single-buffered: the chain of chunk c - 1 reads them until the period ends).
 struct Deferred {
     half4 am[3];        // -A blocks (wave, jt) for jt < wave
-    half4 d;            // D_wave rows 4 g .. 4 g + 3 of column n
+    half4 d;            // D_wave[n][4 g .. 4 g + 3]
     half4 ih[4], il[4]; // intra blocks (3 - wave, jt) for jt <= 3 - wave
 };
 
@@ -328,8 +347,32 @@ __device__ __forceinline__ void prep_b(Smem<kLo>& sm, int buf, const Conv<kLo>& 
                 const int j = 16 * jt + 4 * g + r, i = 16 * wv + n;
                 av[r] = j < i ? brk_i * rkj[r] * __expf(cum_i - cumj[r]) * acc[r] : 0.f;
             }
-            if (jt < wv) df.am[jt < 3 ? jt : 2] = h4(-av);
-            else *(f32x4*)&sm.Dw[wv][n][4 * g] = av;
+            if (jt < wv) {
+                df.am[jt < 3 ? jt : 2] = h4(-av);
+            } else {
+                // D = (I + N)^-1 = (I - N)(I + N^2)(I + N^4)(I + N^8) for the strictly lower
+                // 16 x 16 block N = A_ww, on 16x16x16 MFMAs. Registers R(X) (lane (n, g) holding
+                // X[n][4 g + r]) used as A are X, as B are X^T, and an MFMA's accumulator comes
+                // back as R(C^T): so mfma(R(X^T), R(Y), C = R(Y)) = R(Y + Y X). N^T's entries are
+                // the same Gram values (G is symmetric) with the factors of the swapped indices.
+                const float rk_i = F.rk[16 * wv + n];
+                const f32x4 brkj = *(const f32x4*)&F.brk[16 * wv + 4 * g];
+                f32x4 avt, p0;
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    avt[r] = n < 4 * g + r ? brkj[r] * rk_i * __expf(cumj[r] - cum_i) * acc[r] : 0.f;
+                    p0[r] = (n == 4 * g + r ? 1.f : 0.f) - av[r];
+                }
+                const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
+                const half4 hn = h4(av), hnt = h4(avt);
+                const half4 n2t = h4(mfma16(hn, hnt, z4)), n2 = h4(mfma16(hnt, hn, z4));
+                const half4 n4t = h4(mfma16(n2, n2t, z4)), n4 = h4(mfma16(n2t, n2, z4));
+                const half4 n8t = h4(mfma16(n4, n4t, z4));
+                f32x4 pp = mfma16(n2t, h4(p0), p0);
+                pp = mfma16(n4t, h4(pp), pp);
+                pp = mfma16(n8t, h4(pp), pp);
+                df.d = h4(pp);
+            }
         }
         if (jt <= iq) {
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -367,30 +410,6 @@ __device__ __forceinline__ void prep_b(Smem<kLo>& sm, int buf, const Conv<kLo>& 
             if constexpr (kLo) *(half8*)&sm.VL[0][16 * wv + n][32 * ks + 8 * g] = cv.vl[ks];
         }
     }
-    // D_wv = (I + A_ww)^-1 by forward substitution in fp32, lane n (of every group) solving
-    // column n; the block's rows are read as broadcasts from the wave's own scratch
-    wave_sync();
-    {
-        float xs[16];
-#pragma unroll
-        for (int i = 0; i < 16; i++) {
-            float sacc = i == n ? 1.f : 0.f;
-#pragma unroll
-            for (int kk = 0; kk < i; kk++) sacc -= sm.Dw[wv][i][kk] * xs[kk];
-            xs[i] = sacc;
-        }
-        // group g keeps rows 4 g .. 4 g + 3 of column n
-        f32x4 dv;
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-            float val = xs[r];
-#pragma unroll
-            for (int gg = 1; gg < 4; gg++)
-                if (gg == g) val = xs[4 * gg + r];
-            dv[r] = val;
-        }
-        df.d = h4(dv);
-    }
 }
 
 // The deferred operands of one chunk into AD / IH / IL.
@@ -400,8 +419,7 @@ __device__ __forceinline__ void write_deferred(Smem<kLo>& sm, const Deferred& df
 #pragma unroll
     for (int jt = 0; jt < 3; jt++)
         if (jt < wv) *(half4*)&sm.AD[16 * wv + n][16 * jt + 4 * g] = df.am[jt];
-#pragma unroll
-    for (int r = 0; r < 4; r++) sm.AD[16 * wv + 4 * g + r][16 * wv + n] = df.d[r];
+    *(half4*)&sm.AD[16 * wv + n][16 * wv + 4 * g] = df.d;
 #pragma unroll
     for (int jt = 0; jt < 4; jt++)
         if (jt <= iq) {
@@ -448,7 +466,7 @@ __device__ __forceinline__ void chain_r(const Smem<kLo>& sm, int buf, int wave, 
             if constexpr (kWithV) {
                 const half4 vv = ld_tr(&sm.V[0][0], RS, 16 * t + 4 * g, 32 * wave + 16 * ct, n);
                 half4 vl = {0, 0, 0, 0};
-                if constexpr (kLo) vl = ld_tr(&sm.VL[0][0][0], RS, 16 * t + 4 * g, 32 * wave + 16 * ct, n);
+                if constexpr (kLo) vl = ld_tr(&sm.VL[0][0][0], RSL, 16 * t + 4 * g, 32 * wave + 16 * ct, n);
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
                     float x = (float)vv[e];
@@ -515,8 +533,8 @@ __device__ __forceinline__ void chain_update(const Smem<kLo>& sm, int buf, int n
             a[m] = cat8(ld_tr(&sm.K[buf][0][0], RS, 32 * m + 4 * g, 16 * ft, n),
                         ld_tr(&sm.K[buf][0][0], RS, 32 * m + 16 + 4 * g, 16 * ft, n));
             if constexpr (kLo && kPlo)
-                al[m] = cat8(ld_tr(&sm.KL[buf][0][0], RS, 32 * m + 4 * g, 16 * ft, n),
-                             ld_tr(&sm.KL[buf][0][0], RS, 32 * m + 16 + 4 * g, 16 * ft, n));
+                al[m] = cat8(ld_tr(&sm.KL[buf][0][0], RSL, 32 * m + 4 * g, 16 * ft, n),
+                             ld_tr(&sm.KL[buf][0][0], RSL, 32 * m + 16 + 4 * g, 16 * ft, n));
         }
 #pragma unroll
         for (int ct = 0; ct < 2; ct++) {
@@ -605,14 +623,15 @@ __global__ void __launch_bounds__(NT, 1) delta_seg_kernel(Params p) {
                 for (int r = 0; r < 4; r++) M[ft][ct][r] = (16 * ft + 4 * g + r == 32 * wave + 16 * ct + n) ? 1.f : 0.f;
     }
 
+    const Rsrc rs = make_rsrc<Tin, Tout>(p, b, hv);
     Raw<Tin> raw;
     RawGB gb;
     Conv<kLo> cv;
     Deferred df;
     // prologue: chunk c0's operands
-    load_chunk<Tin>(p, b, hv, c0, wave, n, g, lane, raw, gb);
+    load_chunk<Tin>(p, rs, c0, wave, n, g, lane, raw, gb);
     prep_a<Tin, kLo>(p, sm, c0 & 1, raw, gb, wave, n, g, lane, cv);
-    load_chunk<Tin>(p, b, hv, c0 + 1, wave, n, g, lane, raw, gb);
+    load_chunk<Tin>(p, rs, c0 + 1, wave, n, g, lane, raw, gb);
     lds_barrier();
     prep_b<kLo>(sm, c0 & 1, cv, wave, n, g, df);
     lds_barrier();
@@ -641,7 +660,7 @@ __global__ void __launch_bounds__(NT, 1) delta_seg_kernel(Params p) {
         }
         chain_r<true, kLo>(sm, buf, wave, n, g, X);
         prep_a<Tin, kLo>(p, sm, nb, raw, gb, wave, n, g, lane, cv);
-        load_chunk<Tin>(p, b, hv, c + 2, wave, n, g, lane, raw, gb);
+        load_chunk<Tin>(p, rs, c + 2, wave, n, g, lane, raw, gb);
         // Q / V of chunk c are consumed; AD / IH / IL of chunk c and K[nb], F[nb] of chunk c + 1 are
         // complete
         lds_barrier();
@@ -677,21 +696,20 @@ __global__ void __launch_bounds__(NT, 1) delta_seg_kernel(Params p) {
                     }
                 }
             }
-            // lane (n, g) of tile (ct, t) holds o[token 16 t + n][32 wave + 16 ct + 4 g .. + 3]
-            Tout* out = (Tout*)p.out;
+            // lane (n, g) of tile (ct, t) holds o[token 16 t + n][32 wave + 16 ct + 4 g .. + 3];
+            // rows past T fall outside the resource and are dropped
 #pragma unroll
             for (int t = 0; t < 4; t++) {
-                const int tok = c * CH + 16 * t + n;
-                if (tok < p.T) {
-                    Tout* dst = out + b * p.a.sb_o + (long long)tok * p.a.st_o + hv * p.a.sh_o + 32 * wave + 4 * g;
+                const int off = ((c * CH + 16 * t + n) * (int)p.a.st_o + 32 * wave + 4 * g) * (int)sizeof(Tout);
 #pragma unroll
-                    for (int ct = 0; ct < 2; ct++) {
-                        if constexpr (sizeof(Tout) == 2) {
-                            const f32x4 o = O[ct][t];
-                            *(uint2*)(dst + 16 * ct) = uint2{f2bf2(o[0], o[1]), f2bf2(o[2], o[3])};
-                        } else {
-                            *(f32x4*)(dst + 16 * ct) = O[ct][t];
-                        }
+                for (int ct = 0; ct < 2; ct++) {
+                    const f32x4 o = O[ct][t];
+                    if constexpr (sizeof(Tout) == 2) {
+                        typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+                        __builtin_amdgcn_raw_buffer_store_b64(u32x2{f2bf2(o[0], o[1]), f2bf2(o[2], o[3])}, rs.out,
+                                                              off + 32 * ct, 0, 0);
+                    } else {
+                        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o), rs.out, off + 64 * ct, 0, 0);
                     }
                 }
             }
