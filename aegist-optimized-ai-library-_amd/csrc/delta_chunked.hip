@@ -65,9 +65,12 @@ struct SeqLayout {
     long long sb_g, st_g;  // g / beta strides by sequence and token; value head contiguous
 };
 
-// Per-token factor arrays of one chunk (fp32, 64 entries each) and the chunk decay.
+// Per-token factor arrays of one chunk (fp32, 64 entries each) and the chunk decay. The Gram
+// factors are kept as base-2 logarithms, so A_ij = 2^(la_i - mk_j) G_ij and
+// intra_ij = 2^(lq_i - mk_j) (q k^T)_ij take one exponential per element:
+// la = cum log2(e) + log2(beta rk), lq = cum log2(e) + log2(rq), mk = cum log2(e) - log2(rk).
 struct Fact {
-    float cum[CH], beta[CH], brk[CH], rk[CH], rq[CH], fx[CH], fp[CH];
+    float la[CH], lq[CH], mk[CH], beta[CH], fx[CH], fp[CH];
     float gam;
     float pad[3];
 };
@@ -124,10 +127,28 @@ __device__ __forceinline__ half4 h4(f32x4 x) {
     const half2v b = __builtin_convertvector((f32x2{x[2], x[3]}), half2v);
     return half4{a[0], a[1], b[0], b[1]};
 }
+// x - (float)h for the fp16 in the low (res_l) or high (res_h) half of a packed pair: one
+// v_fma_mix_f32 (h * -1 + x, the fp16 operand widened exactly), where the compiler would convert
+// and subtract
+__device__ __forceinline__ float res_l(uint32_t h, float x) {
+    float r;
+    asm("v_fma_mix_f32 %0, %1, -1.0, %2 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(h), "v"(x));
+    return r;
+}
+__device__ __forceinline__ float res_h(uint32_t h, float x) {
+    float r;
+    asm("v_fma_mix_f32 %0, %1, -1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(h), "v"(x));
+    return r;
+}
+// fp16 of x - hi (the low part of a hi + lo split whose high part is hi)
+__device__ __forceinline__ half4 lo4(f32x4 x, half4 hi) {
+    const uint2 hp = __builtin_bit_cast(uint2, hi);
+    return h4(f32x4{res_l(hp.x, x[0]), res_h(hp.x, x[1]), res_l(hp.y, x[2]), res_h(hp.y, x[3])});
+}
 // hi + lo split: hi = fp16(x), lo = fp16(x - hi); hi + lo carries ~22 significant bits
 __device__ __forceinline__ void split4(f32x4 x, half4& hi, half4& lo) {
     hi = h4(x);
-    lo = h4(f32x4{x[0] - (float)hi[0], x[1] - (float)hi[1], x[2] - (float)hi[2], x[3] - (float)hi[3]});
+    lo = lo4(x, hi);
 }
 __device__ __forceinline__ half4 ld4(const half_t* p) { return *(const half4*)p; }
 // two 4-element runs of one row: the permuted 8-slot operand of one 32-wide k step
@@ -237,6 +258,17 @@ struct Deferred {
     half4 ih[4], il[4]; // intra blocks (3 - wave, jt) for jt <= 3 - wave
 };
 
+// acc + the sum of squares of 8 bf16 values (packed dot products), and a no-op form for fp32
+__device__ __forceinline__ float dot2sq(const uint4* src, int ks, float acc) {
+    typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+    const uint4 a = src[ks];
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf2, a.x), __builtin_bit_cast(bf2, a.x), acc, false);
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf2, a.y), __builtin_bit_cast(bf2, a.y), acc, false);
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf2, a.z), __builtin_bit_cast(bf2, a.z), acc, false);
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf2, a.w), __builtin_bit_cast(bf2, a.w), acc, false);
+}
+__device__ __forceinline__ float dot2sq(const float4*, int, float acc) { return acc; }
+
 __device__ __forceinline__ half8 cvt8(const float* x) {
     const half4 a = h4(f32x4{x[0], x[1], x[2], x[3]}), b = h4(f32x4{x[4], x[5], x[6], x[7]});
     return cat8(a, b);
@@ -258,13 +290,21 @@ __device__ __forceinline__ void prep_a(const Params& p, Smem<kLo>& sm, int buf, 
     for (int ks = 0; ks < 4; ks++) {
         float x[8];
         unpack8(r.k, ks, x);
+        if constexpr (kLo) {
 #pragma unroll
-        for (int e = 0; e < 8; e++) ssk += x[e] * x[e];
+            for (int e = 0; e < 8; e++) ssk += x[e] * x[e];
+        } else {
+            ssk = dot2sq(r.k, ks, ssk);
+        }
         cv.k[ks] = cvt8(x);
         if constexpr (kLo) cv.kl[ks] = lo8(x, cv.k[ks]);
         unpack8(r.q, ks, x);
+        if constexpr (kLo) {
 #pragma unroll
-        for (int e = 0; e < 8; e++) ssq += x[e] * x[e];
+            for (int e = 0; e < 8; e++) ssq += x[e] * x[e];
+        } else {
+            ssq = dot2sq(r.q, ks, ssq);
+        }
         cv.q[ks] = cvt8(x);
         if constexpr (kLo) cv.ql[ks] = lo8(x, cv.q[ks]);
         unpack8(r.v, ks, x);
@@ -289,18 +329,19 @@ __device__ __forceinline__ void prep_a(const Params& p, Smem<kLo>& sm, int buf, 
         if (lane >= d) x += y;
     }
     const float cl = __shfl(x, CH - 1, WAVE);
-    // this wave's tokens 16 wave + n: factors need rk (known here) and cum / beta of that token
-    const int tw = 16 * wave + n;
-    const float cum_t = __shfl(x, tw, WAVE), beta_t = __shfl(gb.beta, tw, WAVE);
+    // this wave's tokens: factors of k rows (tile wave) and q rows (tile 3 - wave)
+    constexpr float kLog2e = 1.4426950408889634f;
+    const int tw = 16 * wave + n, tq = 16 * (3 - wave) + n;
+    const float cum_t = __shfl(x, tw, WAVE), beta_t = __shfl(gb.beta, tw, WAVE), cum_q = __shfl(x, tq, WAVE);
     Fact& F = sm.F[buf];
     if (g == 0) {
-        F.cum[tw] = cum_t;
+        const float c2 = cum_t * kLog2e, brk = beta_t * cv.rk, lrk = __builtin_amdgcn_logf(cv.rk);
+        F.la[tw] = c2 + __builtin_amdgcn_logf(brk);
+        F.mk[tw] = c2 - lrk;
         F.beta[tw] = beta_t;
-        F.rk[tw] = cv.rk;
-        F.brk[tw] = beta_t * cv.rk;
-        F.fx[tw] = beta_t * cv.rk * __expf(cum_t);
+        F.fx[tw] = brk * __expf(cum_t);
         F.fp[tw] = cv.rk * __expf(cl - cum_t);
-        F.rq[16 * (3 - wave) + n] = cv.rq;
+        F.lq[tq] = cum_q * kLog2e + __builtin_amdgcn_logf(cv.rq);
     }
     if (wave == 0 && lane == 0) F.gam = __expf(cl);
 }
@@ -318,8 +359,7 @@ __device__ __forceinline__ void prep_b(Smem<kLo>& sm, int buf, const Conv<kLo>& 
     // G: it = wv, jt <= wv.  k q^T: it = 3 - wv, jt <= 3 - wv.
     const int iq = 3 - wv;
     // factors of this lane's rows
-    const float cum_i = F.cum[16 * wv + n], brk_i = F.brk[16 * wv + n];
-    const float cumq_i = F.cum[16 * iq + n], rq_i = F.rq[16 * iq + n];
+    const float la_i = F.la[16 * wv + n], lq_i = F.lq[16 * iq + n], mk_i = F.mk[16 * wv + n];
 #pragma unroll
     for (int jt = 0; jt < 4; jt++) {
         if (jt > wv && jt > iq) continue;
@@ -329,8 +369,7 @@ __device__ __forceinline__ void prep_b(Smem<kLo>& sm, int buf, const Conv<kLo>& 
             ka[ks] = jt == wv ? cv.k[ks] : *(const half8*)&sm.K[buf][16 * jt + n][32 * ks + 8 * g];
             if constexpr (kLo) kal[ks] = jt == wv ? cv.kl[ks] : *(const half8*)&sm.KL[buf][16 * jt + n][32 * ks + 8 * g];
         }
-        const f32x4 cumj = *(const f32x4*)&F.cum[16 * jt + 4 * g];
-        const f32x4 rkj = *(const f32x4*)&F.rk[16 * jt + 4 * g];
+        const f32x4 mkj = *(const f32x4*)&F.mk[16 * jt + 4 * g];
         if (jt <= wv) {
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -345,7 +384,7 @@ __device__ __forceinline__ void prep_b(Smem<kLo>& sm, int buf, const Conv<kLo>& 
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const int j = 16 * jt + 4 * g + r, i = 16 * wv + n;
-                av[r] = j < i ? brk_i * rkj[r] * __expf(cum_i - cumj[r]) * acc[r] : 0.f;
+                av[r] = j < i ? __builtin_amdgcn_exp2f(la_i - mkj[r]) * acc[r] : 0.f;
             }
             if (jt < wv) {
                 df.am[jt < 3 ? jt : 2] = h4(-av);
@@ -355,12 +394,11 @@ __device__ __forceinline__ void prep_b(Smem<kLo>& sm, int buf, const Conv<kLo>& 
                 // X[n][4 g + r]) used as A are X, as B are X^T, and an MFMA's accumulator comes
                 // back as R(C^T): so mfma(R(X^T), R(Y), C = R(Y)) = R(Y + Y X). N^T's entries are
                 // the same Gram values (G is symmetric) with the factors of the swapped indices.
-                const float rk_i = F.rk[16 * wv + n];
-                const f32x4 brkj = *(const f32x4*)&F.brk[16 * wv + 4 * g];
+                const f32x4 laj = *(const f32x4*)&F.la[16 * wv + 4 * g];
                 f32x4 avt, p0;
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
-                    avt[r] = n < 4 * g + r ? brkj[r] * rk_i * __expf(cumj[r] - cum_i) * acc[r] : 0.f;
+                    avt[r] = n < 4 * g + r ? __builtin_amdgcn_exp2f(laj[r] - mk_i) * acc[r] : 0.f;
                     p0[r] = (n == 4 * g + r ? 1.f : 0.f) - av[r];
                 }
                 const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
@@ -388,14 +426,14 @@ __device__ __forceinline__ void prep_b(Smem<kLo>& sm, int buf, const Conv<kLo>& 
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const int j = 16 * jt + 4 * g + r, i = 16 * iq + n;
-                iv[r] = j <= i ? rq_i * rkj[r] * __expf(cumq_i - cumj[r]) * acc[r] : 0.f;
+                iv[r] = j <= i ? __builtin_amdgcn_exp2f(lq_i - mkj[r]) * acc[r] : 0.f;
             }
             split4(iv, df.ih[jt], df.il[jt]);
         }
     }
     // q rows (scaled by rq e^cum) of tile iq and v rows of tile wv
     {
-        const float f = rq_i * __expf(cumq_i);
+        const float f = __builtin_amdgcn_exp2f(lq_i);
 #pragma unroll
         for (int ks = 0; ks < 4; ks++) {
             half8 y;
@@ -594,15 +632,13 @@ __device__ __forceinline__ bool unit_of(int x, const Params& p, int nseg, int& b
 // ---------------------------------------------------------------------------------------------
 // kOut: launch 2 (outputs from the segment's start state). !kOut: launch 1 (segment end state
 // N and transition M from a zero start, segment 0 from the initial state).
-template <typename Tin, typename Tout, bool kOut>
-__global__ void __launch_bounds__(NT, 1) delta_seg_kernel(Params p) {
+// The body of one wave; WV (the wave index) is a template parameter so that every wave-dependent
+// choice of the prep work is resolved at compile time and each period is one basic block.
+template <typename Tin, typename Tout, bool kOut, int WV>
+__device__ __forceinline__ void seg_body(const Params& p, Smem<sizeof(Tin) == 4>& sm, int b, int hv, int s, int lane) {
     constexpr bool kLo = sizeof(Tin) == 4;
-    extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
-    Smem<kLo>& sm = *(Smem<kLo>*)smem_raw;
-    int b, hv, s;
-    if (!unit_of(blockIdx.x, p, kOut ? p.P : p.P - 1, b, hv, s)) return;
-    const int tid = threadIdx.x, lane = tid % WAVE, n = lane % 16, g = lane / 16;
-    const int wave = __builtin_amdgcn_readfirstlane(tid / WAVE);
+    constexpr int wave = WV;
+    const int n = lane % 16, g = lane / 16;
     const int c0 = s * p.L, c1 = min(p.nch, c0 + p.L);
     const size_t unit = (size_t)(b * p.HV + hv);
     constexpr size_t DD = (size_t)D * D;
@@ -676,9 +712,7 @@ __global__ void __launch_bounds__(NT, 1) delta_seg_kernel(Params p) {
             for (int t = 0; t < 4; t++)
 #pragma unroll
                 for (int ct = 0; ct < 2; ct++) {
-                    const f32x4 d = V[t][ct];
-                    Vl[t][ct] = h4(f32x4{d[0] - (float)Vh[t][ct][0], d[1] - (float)Vh[t][ct][1],
-                                         d[2] - (float)Vh[t][ct][2], d[3] - (float)Vh[t][ct][3]});
+                    Vl[t][ct] = lo4(V[t][ct], Vh[t][ct]);
                 }
 #pragma unroll
             for (int it = 0; it < 4; it++) {
@@ -746,6 +780,22 @@ __global__ void __launch_bounds__(NT, 1) delta_seg_kernel(Params p) {
                     mb[(size_t)(16 * ft + 4 * g + r) * D + 32 * wave + 16 * ct + n] = (half_t)M[ft][ct][r];
     }
 }
+
+template <typename Tin, typename Tout, bool kOut>
+__global__ void __launch_bounds__(NT, 1) delta_seg_kernel(Params p) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
+    Smem<sizeof(Tin) == 4>& sm = *(Smem<sizeof(Tin) == 4>*)smem_raw;
+    int b, hv, s;
+    if (!unit_of(blockIdx.x, p, kOut ? p.P : p.P - 1, b, hv, s)) return;
+    const int lane = threadIdx.x % WAVE;
+    switch (__builtin_amdgcn_readfirstlane(threadIdx.x / WAVE)) {
+        case 0: seg_body<Tin, Tout, kOut, 0>(p, sm, b, hv, s, lane); break;
+        case 1: seg_body<Tin, Tout, kOut, 1>(p, sm, b, hv, s, lane); break;
+        case 2: seg_body<Tin, Tout, kOut, 2>(p, sm, b, hv, s, lane); break;
+        default: seg_body<Tin, Tout, kOut, 3>(p, sm, b, hv, s, lane); break;
+    }
+}
+
 
 // Segment boundaries: S_1 = N_0, S_{s+1} = M_s S_s + N_s. One wave per (sequence, head,
 // 16-column slice); M_s as the fp16 A operand, S_s as fp16 hi + lo.
