@@ -43,8 +43,8 @@ namespace {
 
 constexpr int D = 128;
 constexpr int CH = 64;
-constexpr int NW = 4;              // waves per workgroup
-constexpr int NT = NW * WAVE;      // threads per workgroup
+constexpr int NW = 4;              // chain waves per workgroup (and as many prep waves)
+constexpr int NT2 = 2 * NW * WAVE; // threads per workgroup
 // fp16 row strides in LDS: rows padded by 16 bytes, the measured best of 8 / 16 / 32 bytes for
 // the chain's mix of 8-byte row reads, transpose reads and 16-byte row writes.
 constexpr int RS = D + 8;          // 64 x 128 tiles (272 B rows)
@@ -477,18 +477,46 @@ __device__ __forceinline__ void write_deferred(Smem<kLo>& sm, const Deferred& df
 // RSL, the -A / D blocks with stride RA.
 
 // X = k S (tokens x columns), C layout [token tile][column tile]
-template <int NC>
-__device__ __forceinline__ void chain_x(const half_t* K, const half8 (&shi)[4][NC], int n, int g, f32x4 (&X)[4][NC]) {
+// Scheduling fence: keeps a prefetch stage's loads ahead of the products of the stage before.
+#define SCHED_FENCE() __builtin_amdgcn_sched_barrier(0)
+
+// X = k S and, with Q, o^T = S^T q~^T (the output's first term, transposed so a lane ends with 4
+// consecutive columns of one token: A = S as it stands, B = the scaled q rows). The fragments of
+// token tile t + 1 are requested before the products of tile t.
+template <bool kQ, int NC>
+__device__ __forceinline__ void chain_xo(const half_t* K, const half_t* Q, const half8 (&shi)[4][NC], int n, int g,
+                                         f32x4 (&X)[4][NC], f32x4 (&O)[NC][4]) {
+    // stages (t, k-product) then (t, q-product) (kQ), four fragments each, the next stage's
+    // requested before this stage's products
+    constexpr int ns = kQ ? 8 : 4;
+    half8 fa[2][4];
+    auto load = [&](int st, int sl) {
+        const int t = kQ ? st / 2 : st;
+        const half_t* base = (kQ && (st & 1)) ? Q : K;
 #pragma unroll
-    for (int t = 0; t < 4; t++) {
+        for (int m = 0; m < 4; m++) fa[sl][m] = ld_perm(base + (16 * t + n) * RS, m, g);
+    };
+    load(0, 0);
 #pragma unroll
-        for (int ct = 0; ct < NC; ct++) X[t][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int st = 0; st < ns; st++) {
+        const int sl = st & 1, t = kQ ? st / 2 : st;
+        const bool isq = kQ && (st & 1);
+        if (st + 1 < ns) load(st + 1, sl ^ 1);
+        SCHED_FENCE();
+        f32x4 acc[NC];
 #pragma unroll
-        for (int m = 0; m < 4; m++) {
-            const half8 a = ld_perm(K + (16 * t + n) * RS, m, g);
+        for (int ct = 0; ct < NC; ct++) acc[ct] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int ct = 0; ct < NC; ct++) X[t][ct] = mfma32(a, shi[m][ct], X[t][ct]);
+        for (int m = 0; m < 4; m++)
+#pragma unroll
+            for (int ct = 0; ct < NC; ct++)
+                acc[ct] = isq ? mfma32(shi[m][ct], fa[sl][m], acc[ct]) : mfma32(fa[sl][m], shi[m][ct], acc[ct]);
+#pragma unroll
+        for (int ct = 0; ct < NC; ct++) {
+            if (isq) O[ct][t] = acc[ct];
+            else X[t][ct] = acc[ct];
         }
+        SCHED_FENCE();
     }
 }
 
@@ -521,6 +549,11 @@ __device__ __forceinline__ void chain_r(const Fact& F, const half_t* V, const ha
 template <bool kZlo, int NC>
 __device__ __forceinline__ void chain_solve(const half_t* AD, int n, int g, const f32x4 (&R)[4][NC],
                                             f32x4 (&V)[4][NC], half4 (&Vh)[4][NC]) {
+    half4 blk[4][4];  // -A_rk (k < r) and D_r, all requested up front
+#pragma unroll
+    for (int r = 0; r < 4; r++)
+#pragma unroll
+        for (int kk = 0; kk <= r; kk++) blk[r][kk] = ld4(AD + (16 * r + n) * RA + 16 * kk + 4 * g);
 #pragma unroll
     for (int r = 0; r < 4; r++) {
         f32x4 z[NC];
@@ -528,11 +561,10 @@ __device__ __forceinline__ void chain_solve(const half_t* AD, int n, int g, cons
         for (int ct = 0; ct < NC; ct++) z[ct] = R[r][ct];
 #pragma unroll
         for (int kk = 0; kk < r; kk++) {
-            const half4 a = ld4(AD + (16 * r + n) * RA + 16 * kk + 4 * g);  // -A_rk
 #pragma unroll
-            for (int ct = 0; ct < NC; ct++) z[ct] = mfma16(a, Vh[kk][ct], z[ct]);
+            for (int ct = 0; ct < NC; ct++) z[ct] = mfma16(blk[r][kk], Vh[kk][ct], z[ct]);
         }
-        const half4 dr = ld4(AD + (16 * r + n) * RA + 16 * r + 4 * g);
+        const half4 dr = blk[r][r];
 #pragma unroll
         for (int ct = 0; ct < NC; ct++) {
             half4 zh, zl;
@@ -563,15 +595,24 @@ __device__ __forceinline__ void chain_update(const Fact& F, const half_t* K, con
         }
     }
     const float gam = F.gam;
-#pragma unroll
-    for (int ft = 0; ft < 8; ft++) {
-        half8 a[2], al[2];
+    half8 ka[2][2], kl[2][2];  // k^T fragments of feature tile ft, double-buffered
+    auto load = [&](int ft, int sl) {
 #pragma unroll
         for (int m = 0; m < 2; m++) {
-            a[m] = cat8(ld_tr(K, RS, 32 * m + 4 * g, 16 * ft, n), ld_tr(K, RS, 32 * m + 16 + 4 * g, 16 * ft, n));
+            ka[sl][m] = cat8(ld_tr(K, RS, 32 * m + 4 * g, 16 * ft, n), ld_tr(K, RS, 32 * m + 16 + 4 * g, 16 * ft, n));
             if (kPlo && KL)
-                al[m] = cat8(ld_tr(KL, RSL, 32 * m + 4 * g, 16 * ft, n), ld_tr(KL, RSL, 32 * m + 16 + 4 * g, 16 * ft, n));
+                kl[sl][m] = cat8(ld_tr(KL, RSL, 32 * m + 4 * g, 16 * ft, n),
+                                 ld_tr(KL, RSL, 32 * m + 16 + 4 * g, 16 * ft, n));
         }
+    };
+    load(0, 0);
+#pragma unroll
+    for (int ft = 0; ft < 8; ft++) {
+        const int sl = ft & 1;
+        if (ft < 7) load(ft + 1, sl ^ 1);
+        SCHED_FENCE();
+        const half8* a = ka[sl];
+        const half8* al = kl[sl];
 #pragma unroll
         for (int ct = 0; ct < NC; ct++) {
             f32x4 acc = S[ft][ct] * gam;
@@ -584,6 +625,7 @@ __device__ __forceinline__ void chain_update(const Fact& F, const half_t* K, con
             }
             S[ft][ct] = acc;
         }
+        SCHED_FENCE();
     }
 }
 
@@ -656,20 +698,6 @@ __device__ __forceinline__ bool unit_of(int x, const Params& p, int nseg, int& b
 // token: o^T = S^T (rq e^cum q)^T with A = S as it stands (the B-operand registers of S) and B =
 // the scaled q rows, then o^T += v_new^T intra^T (hi hi + hi lo + lo hi) over the k steps on or
 // below the diagonal.
-template <int NC>
-__device__ __forceinline__ void out_qs(const half_t* Q, const half8 (&shi)[4][NC], int n, int g, f32x4 (&O)[NC][4]) {
-#pragma unroll
-    for (int t = 0; t < 4; t++) {
-#pragma unroll
-        for (int ct = 0; ct < NC; ct++) O[ct][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int m = 0; m < 4; m++) {
-            const half8 bq = ld_perm(Q + (16 * t + n) * RS, m, g);
-#pragma unroll
-            for (int ct = 0; ct < NC; ct++) O[ct][t] = mfma32(shi[m][ct], bq, O[ct][t]);
-        }
-    }
-}
 template <int NC, typename Tout>
 __device__ __forceinline__ void out_intra_store(const half_t* IH, const half_t* IL, const f32x4 (&V)[4][NC],
                                                 const half4 (&Vh)[4][NC], f32x4 (&O)[NC][4],
@@ -679,12 +707,22 @@ __device__ __forceinline__ void out_intra_store(const half_t* IH, const half_t* 
     for (int t = 0; t < 4; t++)
 #pragma unroll
         for (int ct = 0; ct < NC; ct++) Vl[t][ct] = lo4(V[t][ct], Vh[t][ct]);
+    // the six (token tile, k step) fragment pairs on or below the diagonal, each requested one
+    // step ahead of its products
+    constexpr int kIt[6] = {0, 1, 2, 2, 3, 3}, kM[6] = {0, 0, 0, 1, 0, 1};
+    half8 fh[2], fl[2];
+    fh[0] = ld_perm(IH + n * RA, 0, g);
+    fl[0] = ld_perm(IL + n * RA, 0, g);
 #pragma unroll
-    for (int it = 0; it < 4; it++) {
-#pragma unroll
-        for (int m = 0; m <= it / 2; m++) {
-            const half8 ih = ld_perm(IH + (16 * it + n) * RA, m, g);
-            const half8 il = ld_perm(IL + (16 * it + n) * RA, m, g);
+    for (int q = 0; q < 6; q++) {
+        const int it = kIt[q], m = kM[q], sl = q & 1;
+        if (q < 5) {
+            fh[sl ^ 1] = ld_perm(IH + (16 * kIt[q + 1] + n) * RA, kM[q + 1], g);
+            fl[sl ^ 1] = ld_perm(IL + (16 * kIt[q + 1] + n) * RA, kM[q + 1], g);
+        }
+        SCHED_FENCE();
+        {
+            const half8 ih = fh[sl], il = fl[sl];
 #pragma unroll
             for (int ct = 0; ct < NC; ct++) {
                 const half8 vh = cat8(Vh[2 * m][ct], Vh[2 * m + 1][ct]);
@@ -694,6 +732,7 @@ __device__ __forceinline__ void out_intra_store(const half_t* IH, const half_t* 
                 O[ct][it] = mfma32(vl, ih, O[ct][it]);
             }
         }
+        SCHED_FENCE();
     }
     // lane (n, g) of tile (ct, t) holds o[token tok0 + 16 t + n][col0 + 16 ct + 4 g .. + 3]; rows
     // past T fall outside the resource and are dropped
@@ -722,8 +761,8 @@ __device__ __forceinline__ void chain_transition(const Fact& F, const half_t* K,
                                                  f32x4 (&M)[8][NC]) {
     half8 mhi[4][NC];
     make_shi(M, mhi);
-    f32x4 XM[4][NC];
-    chain_x(K, mhi, n, g, XM);
+    f32x4 XM[4][NC], unused[NC][4];
+    chain_xo<false>(K, nullptr, mhi, n, g, XM, unused);
     chain_r<false>(F, nullptr, nullptr, 0, n, g, XM);
     f32x4 VM[4][NC];
     half4 VMh[4][NC];
@@ -758,13 +797,17 @@ __device__ __forceinline__ void seg_end(const Params& p, size_t unit, int s, int
     }
 }
 
-// The body of one wave of the 4-wave form (fp32 inputs); WV (the wave index) is a template
-// parameter so that every wave-dependent choice of the prep work is resolved at compile time and
-// each period is one basic block.
+// The workgroup is 8 waves, two per SIMD: waves 0..3 run the chain (wave w owning the value
+// columns [32 w, 32 w + 32)), waves 4..7 the prep work of the next chunk (wave 4 + w: token tile w
+// of the conversions, its five Gram tiles), so each SIMD interleaves one chain wave and one prep
+// wave and neither carries the other's registers. Both roles meet at the two barriers of every
+// period. WV (the wave index) is a template parameter so every wave-dependent choice is resolved
+// at compile time and each period is one basic block.
 template <typename Tin, typename Tout, bool kOut, int WV>
-__device__ __forceinline__ void seg_body(const Params& p, Smem<sizeof(Tin) == 4>& sm, int b, int hv, int s, int lane) {
+__device__ __forceinline__ void chain_body(const Params& p, Smem<sizeof(Tin) == 4>& sm, int b, int hv, int s,
+                                           int lane) {
     constexpr bool kLo = sizeof(Tin) == 4;
-    constexpr int wave = WV, col0 = 32 * WV;
+    constexpr int col0 = 32 * WV;
     const int n = lane % 16, g = lane / 16;
     const int c0 = s * p.L, c1 = min(p.nch, c0 + p.L);
     const size_t unit = (size_t)(b * p.HV + hv);
@@ -772,38 +815,22 @@ __device__ __forceinline__ void seg_body(const Params& p, Smem<sizeof(Tin) == 4>
     f32x4 S[8][2], M[8][2];
     seg_start<kOut>(p, unit, s, col0, n, g, S, M);
     const Rsrc rs = make_rsrc<Tin, Tout>(p, b, hv);
-    Raw<Tin> raw;
-    RawGB gb;
-    Conv<kLo> cv;
-    Deferred df;
-    // prologue: chunk c0's operands
-    load_chunk<Tin>(p, rs, c0, wave, n, g, lane, raw, gb);
-    prep_a<Tin, kLo>(p, sm, c0 & 1, raw, gb, wave, n, g, lane, cv);
-    load_chunk<Tin>(p, rs, c0 + 1, wave, n, g, lane, raw, gb);
-    lds_barrier();
-    prep_b<kLo>(sm, c0 & 1, cv, wave, n, g, df);
+    lds_barrier();  // the prep waves' prologue: chunk c0's operands
     lds_barrier();
 
     const half_t* VL = kLo ? &sm.VL[0][0][0] : nullptr;
     for (int c = c0; c < c1; c++) {
-        const int buf = c & 1, nb = buf ^ 1;
+        const int buf = c & 1;
         const half_t* KL = kLo ? &sm.KL[buf][0][0] : nullptr;
-        // ---- phase 1: chain products on S; chunk c's A / D / intra into LDS; prep A of chunk c + 1
-        write_deferred<kLo>(sm, df, wave, n, g);
+        // ---- phase 1: the products on S (the prep waves write chunk c's A / D / intra meanwhile)
         half8 shi[4][2];
         make_shi(S, shi);
-        f32x4 X[4][2];
-        chain_x(&sm.K[buf][0][0], shi, n, g, X);
-        f32x4 O[2][4];
-        if constexpr (kOut) out_qs(&sm.Q[0][0], shi, n, g, O);
+        f32x4 X[4][2], O[2][4];
+        chain_xo<kOut>(&sm.K[buf][0][0], &sm.Q[0][0], shi, n, g, X, O);
         chain_r<true>(sm.F[buf], &sm.V[0][0], VL, col0, n, g, X);
-        prep_a<Tin, kLo>(p, sm, nb, raw, gb, wave, n, g, lane, cv);
-        load_chunk<Tin>(p, rs, c + 2, wave, n, g, lane, raw, gb);
-        // Q / V of chunk c are consumed; AD / IH / IL of chunk c and K[nb], F[nb] of chunk c + 1 are
-        // complete
-        lds_barrier();
+        lds_barrier();  // Q / V of chunk c are consumed; AD / IH / IL of chunk c are complete
 
-        // ---- phase 2: substitution, output, state update; prep B of chunk c + 1
+        // ---- phase 2: substitution, output, state update
         f32x4 V[4][2];
         half4 Vh[4][2];
         chain_solve<true>(&sm.AD[0][0], n, g, X, V, Vh);
@@ -811,305 +838,71 @@ __device__ __forceinline__ void seg_body(const Params& p, Smem<sizeof(Tin) == 4>
             out_intra_store<2, Tout>(&sm.IH[0][0], &sm.IL[0][0], V, Vh, O, rs.out, c * CH, (int)p.a.st_o, col0, n, g);
         chain_update<true>(sm.F[buf], &sm.K[buf][0][0], KL, n, g, V, S);
         if constexpr (!kOut) {
-            __builtin_amdgcn_sched_barrier(0);
-            chain_transition(sm.F[buf], &sm.K[buf][0][0], &sm.AD[0][0], n, g, M);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-        prep_b<kLo>(sm, nb, cv, wave, n, g, df);
-        lds_barrier();
-    }
-    seg_end<kOut>(p, unit, s, col0, n, g, S, M);
-}
-
-// ---------------------------------------------------------------------------------------------
-// 8-wave form (bf16 inputs): two waves per SIMD, wave w owning the 16 value columns [16 w, 16 w +
-// 16), so one wave's LDS and MFMA latencies are covered by the other's work. The prep work is
-// split by tokens (prep A: 8 rows of q, k, v per wave) and by 16 x 16 Gram tiles (prep B: a
-// static table of 2-3 tiles per wave, 5 per SIMD).
-constexpr int NW8 = 8, NT8 = NW8 * WAVE;
-
-struct Smem8 {
-    __attribute__((aligned(16))) half_t K[2][CH][RS];   // k rows (fp16), by chunk parity
-    __attribute__((aligned(16))) half_t QR[CH][RS];     // raw q rows (fp16) for the k q^T products
-    __attribute__((aligned(16))) half_t Q[CH][RS];      // rq e^cum q rows (fp16)
-    __attribute__((aligned(16))) half_t V[CH][RS];      // v rows (fp16)
-    __attribute__((aligned(16))) half_t AD[CH][RA];
-    __attribute__((aligned(16))) half_t IH[CH][RA];
-    __attribute__((aligned(16))) half_t IL[CH][RA];
-    __attribute__((aligned(16))) Fact F[2];
-};
-static_assert(sizeof(Smem8) <= 160 * 1024, "LDS of one workgroup exceeds a CU");
-
-// Raw rows of one chunk held by a wave: token 8 w + (lane >> 3), features 16 (lane & 7) .. + 15.
-struct Raw8 {
-    uint4 k[2], q[2], v[2];
-};
-struct Conv8 {
-    half8 qt[2], v[2];  // scaled q and v pieces written by prep B
-};
-
-__device__ __forceinline__ void load_chunk8(const Params& p, const Rsrc& rs, int c, int wave, int lane, Raw8& r,
-                                            RawGB& gb) {
-    const int t = c * CH + 8 * wave + (lane >> 3), f = 16 * (lane & 7);
-    const int oqk = (t * (int)p.a.st_qk + f) * 2, ov = (t * (int)p.a.st_v + f) * 2;
-#pragma unroll
-    for (int h = 0; h < 2; h++) {
-        r.k[h] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs.k, oqk + 16 * h, 0, 0));
-        r.q[h] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs.q, oqk + 16 * h, 0, 0));
-        r.v[h] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs.v, ov + 16 * h, 0, 0));
-    }
-    const int go = (c * CH + lane) * (int)p.a.st_g * 4;
-    gb.g = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs.g, go, 0, 0));
-    gb.beta = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs.beta, go, 0, 0));
-}
-
-// sum over the 8 lanes of one token (lane bits 0..2)
-__device__ __forceinline__ float sum8(float x) {
-    x += lane_xor<1>(x);
-    x += lane_xor<2>(x);
-    return x + __shfl_xor(x, 4, WAVE);
-}
-
-__device__ __forceinline__ void prep8_a(const Params& p, Smem8& sm, int buf, const Raw8& r, const RawGB& gb, int wave,
-                                        int lane, Conv8& cv) {
-    const int tn = lane >> 3, fc = lane & 7, tw = 8 * wave + tn;
-    float kf[16], qf[16], vf[16];
-    unpack8(r.k, 0, kf);
-    unpack8(r.k, 1, kf + 8);
-    unpack8(r.q, 0, qf);
-    unpack8(r.q, 1, qf + 8);
-    unpack8(r.v, 0, vf);
-    unpack8(r.v, 1, vf + 8);
-    float ssk = dot2sq(r.k, 1, dot2sq(r.k, 0, 0.f)), ssq = dot2sq(r.q, 1, dot2sq(r.q, 0, 0.f));
-    ssk = sum8(ssk);
-    ssq = sum8(ssq);
-    const float rk = p.normalize ? rsqrtf(ssk + p.eps) : 1.f;
-    const float rq = p.normalize ? rsqrtf(ssq + p.eps) * p.qscale : 1.f;
-    *(half8*)&sm.K[buf][tw][16 * fc] = cvt8(kf);
-    *(half8*)&sm.K[buf][tw][16 * fc + 8] = cvt8(kf + 8);
-    *(half8*)&sm.QR[tw][16 * fc] = cvt8(qf);
-    *(half8*)&sm.QR[tw][16 * fc + 8] = cvt8(qf + 8);
-    cv.v[0] = cvt8(vf);
-    cv.v[1] = cvt8(vf + 8);
-    // inclusive prefix sum of g over the chunk (lane = token)
-    float x = gb.g;
-#pragma unroll
-    for (int d = 1; d < WAVE; d <<= 1) {
-        const float y = __shfl_up(x, d, WAVE);
-        if (lane >= d) x += y;
-    }
-    const float cl = __shfl(x, CH - 1, WAVE);
-    const float cum_t = __shfl(x, tw, WAVE), beta_t = __shfl(gb.beta, tw, WAVE);
-    const float fq = rq * __expf(cum_t);
-#pragma unroll
-    for (int e = 0; e < 16; e++) qf[e] *= fq;
-    cv.qt[0] = cvt8(qf);
-    cv.qt[1] = cvt8(qf + 8);
-    constexpr float kLog2e = 1.4426950408889634f;
-    Fact& F = sm.F[buf];
-    if (fc == 0) {
-        const float c2 = cum_t * kLog2e, brk = beta_t * rk;
-        F.la[tw] = c2 + __builtin_amdgcn_logf(brk);
-        F.mk[tw] = c2 - __builtin_amdgcn_logf(rk);
-        F.lq[tw] = c2 + __builtin_amdgcn_logf(rq);
-        F.beta[tw] = beta_t;
-        F.fx[tw] = brk * __expf(cum_t);
-        F.fp[tw] = rk * __expf(cl - cum_t);
-    }
-    if (wave == 0 && lane == 0) F.gam = __expf(cl);
-}
-
-// Gram tiles of prep B: type 0 = A block (it, jt < it), 1 = diagonal A block (-> D), 2 = intra
-// block (it, jt <= it). Per wave (waves w and w + 4 share a SIMD: 5 tiles per SIMD).
-struct Item {
-    int type, it, jt;
-};
-__device__ __host__ constexpr int n_items(int w) { return w < 4 ? 3 : 2; }
-__device__ __host__ constexpr Item item_of(int w, int i) {
-    constexpr Item tab[8][3] = {
-        {{1, 0, 0}, {2, 0, 0}, {2, 3, 0}}, {{1, 1, 1}, {2, 1, 0}, {2, 3, 1}},
-        {{1, 2, 2}, {2, 1, 1}, {2, 3, 2}}, {{1, 3, 3}, {2, 2, 0}, {2, 3, 3}},
-        {{0, 1, 0}, {0, 3, 2}, {0, 0, 0}}, {{0, 2, 0}, {2, 2, 1}, {0, 0, 0}},
-        {{0, 2, 1}, {0, 3, 0}, {0, 0, 0}}, {{0, 3, 1}, {2, 2, 2}, {0, 0, 0}}};
-    return tab[w][i];
-}
-struct Deferred8 {
-    half4 h[3], l[3];
-};
-
-template <int WV>
-__device__ __forceinline__ void prep8_b(Smem8& sm, int buf, const Conv8& cv, int lane, Deferred8& df) {
-    const Fact& F = sm.F[buf];
-    const int n = lane % 16, g = lane / 16;
-#pragma unroll
-    for (int i = 0; i < n_items(WV); i++) {
-        const Item itm = item_of(WV, i);
-        const half_t* Bt = itm.type == 2 ? &sm.QR[16 * itm.it + n][0] : &sm.K[buf][16 * itm.it + n][0];
-        const half_t* At = &sm.K[buf][16 * itm.jt + n][0];
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int ks = 0; ks < 4; ks++)
-            acc = mfma32(*(const half8*)(At + 32 * ks + 8 * g), *(const half8*)(Bt + 32 * ks + 8 * g), acc);
-        const f32x4 mkj = *(const f32x4*)&F.mk[16 * itm.jt + 4 * g];
-        const int i_row = 16 * itm.it + n;
-        if (itm.type == 2) {
-            const float lq_i = F.lq[i_row];
-            f32x4 iv;
-#pragma unroll
-            for (int r = 0; r < 4; r++)
-                iv[r] = 16 * itm.jt + 4 * g + r <= i_row ? __builtin_amdgcn_exp2f(lq_i - mkj[r]) * acc[r] : 0.f;
-            split4(iv, df.h[i], df.l[i]);
-        } else {
-            const float la_i = F.la[i_row];
-            f32x4 av;
-#pragma unroll
-            for (int r = 0; r < 4; r++)
-                av[r] = 16 * itm.jt + 4 * g + r < i_row ? __builtin_amdgcn_exp2f(la_i - mkj[r]) * acc[r] : 0.f;
-            if (itm.type == 0) {
-                df.h[i] = h4(-av);
-            } else {
-                // D = (I + N)^-1 = (I - N)(I + N^2)(I + N^4)(I + N^8) on 16x16x16 MFMAs (see prep_b)
-                const float mk_i = F.mk[i_row];
-                const f32x4 laj = *(const f32x4*)&F.la[16 * itm.it + 4 * g];
-                f32x4 avt, p0;
-#pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    avt[r] = n < 4 * g + r ? __builtin_amdgcn_exp2f(laj[r] - mk_i) * acc[r] : 0.f;
-                    p0[r] = (n == 4 * g + r ? 1.f : 0.f) - av[r];
-                }
-                const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
-                const half4 hn = h4(av), hnt = h4(avt);
-                const half4 n2t = h4(mfma16(hn, hnt, z4)), n2 = h4(mfma16(hnt, hn, z4));
-                const half4 n4t = h4(mfma16(n2, n2t, z4)), n4 = h4(mfma16(n2t, n2, z4));
-                const half4 n8t = h4(mfma16(n4, n4t, z4));
-                f32x4 pp = mfma16(n2t, h4(p0), p0);
-                pp = mfma16(n4t, h4(pp), pp);
-                pp = mfma16(n8t, h4(pp), pp);
-                df.h[i] = h4(pp);
-            }
-        }
-    }
-    // the scaled q and the v rows of this wave's tokens
-    const int tw = 8 * WV + (lane >> 3), fc = lane & 7;
-    *(half8*)&sm.Q[tw][16 * fc] = cv.qt[0];
-    *(half8*)&sm.Q[tw][16 * fc + 8] = cv.qt[1];
-    *(half8*)&sm.V[tw][16 * fc] = cv.v[0];
-    *(half8*)&sm.V[tw][16 * fc + 8] = cv.v[1];
-}
-
-template <int WV>
-__device__ __forceinline__ void write8_deferred(Smem8& sm, const Deferred8& df, int lane) {
-    const int n = lane % 16, g = lane / 16;
-#pragma unroll
-    for (int i = 0; i < n_items(WV); i++) {
-        const Item itm = item_of(WV, i);
-        const int row = 16 * itm.it + n, col = 16 * itm.jt + 4 * g;
-        if (itm.type == 2) {
-            *(half4*)&sm.IH[row][col] = df.h[i];
-            *(half4*)&sm.IL[row][col] = df.l[i];
-            if (itm.jt == itm.it && (itm.it & 1) == 0) {  // zero partner block of the 32-wide k step
-                *(half4*)&sm.IH[row][col + 16] = half4{0, 0, 0, 0};
-                *(half4*)&sm.IL[row][col + 16] = half4{0, 0, 0, 0};
-            }
-        } else {
-            *(half4*)&sm.AD[row][col] = df.h[i];
-        }
-    }
-}
-
-template <typename Tout, bool kOut, int WV>
-__device__ __forceinline__ void seg8_body(const Params& p, Smem8& sm, int b, int hv, int s, int lane) {
-    constexpr int col0 = 16 * WV;
-    const int n = lane % 16, g = lane / 16;
-    const int c0 = s * p.L, c1 = min(p.nch, c0 + p.L);
-    const size_t unit = (size_t)(b * p.HV + hv);
-
-    f32x4 S[8][1], M[8][1];
-    seg_start<kOut>(p, unit, s, col0, n, g, S, M);
-    const Rsrc rs = make_rsrc<uint16_t, Tout>(p, b, hv);
-    Raw8 raw;
-    RawGB gb;
-    Conv8 cv;
-    Deferred8 df;
-    load_chunk8(p, rs, c0, WV, lane, raw, gb);
-    prep8_a(p, sm, c0 & 1, raw, gb, WV, lane, cv);
-    load_chunk8(p, rs, c0 + 1, WV, lane, raw, gb);
-    lds_barrier();
-    prep8_b<WV>(sm, c0 & 1, cv, lane, df);
-    lds_barrier();
-
-    for (int c = c0; c < c1; c++) {
-        const int buf = c & 1, nb = buf ^ 1;
-        // ---- phase 1: chunk c's A / D / intra into LDS; products on S; prep A of chunk c + 1
-        write8_deferred<WV>(sm, df, lane);
-        half8 shi[4][1];
-        make_shi(S, shi);
-        f32x4 X[4][1];
-        chain_x(&sm.K[buf][0][0], shi, n, g, X);
-        f32x4 O[1][4];
-        if constexpr (kOut) out_qs(&sm.Q[0][0], shi, n, g, O);
-        chain_r<true>(sm.F[buf], &sm.V[0][0], nullptr, col0, n, g, X);
-        prep8_a(p, sm, nb, raw, gb, WV, lane, cv);
-        load_chunk8(p, rs, c + 2, WV, lane, raw, gb);
-        lds_barrier();
-
-        // ---- phase 2: substitution, output, state update; prep B of chunk c + 1
-        f32x4 V[4][1];
-        half4 Vh[4][1];
-        chain_solve<true>(&sm.AD[0][0], n, g, X, V, Vh);
-        if constexpr (kOut)
-            out_intra_store<1, Tout>(&sm.IH[0][0], &sm.IL[0][0], V, Vh, O, rs.out, c * CH, (int)p.a.st_o, col0, n, g);
-        chain_update<true>(sm.F[buf], &sm.K[buf][0][0], nullptr, n, g, V, S);
-        if constexpr (!kOut) {
             // a scheduling fence keeps the transition's temporaries from overlapping the state's
             __builtin_amdgcn_sched_barrier(0);
             chain_transition(sm.F[buf], &sm.K[buf][0][0], &sm.AD[0][0], n, g, M);
-            __builtin_amdgcn_sched_barrier(0);
         }
-        prep8_b<WV>(sm, nb, cv, lane, df);
         lds_barrier();
     }
     seg_end<kOut>(p, unit, s, col0, n, g, S, M);
 }
 
+template <typename Tin, typename Tout, int WV>
+__device__ __forceinline__ void prep_body(const Params& p, Smem<sizeof(Tin) == 4>& sm, int b, int hv, int s,
+                                          int lane) {
+    constexpr bool kLo = sizeof(Tin) == 4;
+    constexpr int wave = WV - 4;  // token tile of this prep wave
+    const int n = lane % 16, g = lane / 16;
+    const int c0 = s * p.L, c1 = min(p.nch, c0 + p.L);
+    const Rsrc rs = make_rsrc<Tin, Tout>(p, b, hv);
+    Raw<Tin> raw;
+    RawGB gb;
+    Conv<kLo> cv;
+    Deferred df;
+    load_chunk<Tin>(p, rs, c0, wave, n, g, lane, raw, gb);
+    prep_a<Tin, kLo>(p, sm, c0 & 1, raw, gb, wave, n, g, lane, cv);
+    load_chunk<Tin>(p, rs, c0 + 1, wave, n, g, lane, raw, gb);
+    lds_barrier();
+    prep_b<kLo>(sm, c0 & 1, cv, wave, n, g, df);
+    lds_barrier();
+    for (int c = c0; c < c1; c++) {
+        const int nb = (c & 1) ^ 1;
+        // ---- phase 1: chunk c's A / D / intra into LDS; prep A of chunk c + 1
+        write_deferred<kLo>(sm, df, wave, n, g);
+        prep_a<Tin, kLo>(p, sm, nb, raw, gb, wave, n, g, lane, cv);
+        load_chunk<Tin>(p, rs, c + 2, wave, n, g, lane, raw, gb);
+        lds_barrier();
+        // ---- phase 2: prep B of chunk c + 1 (Q and V are rewritten: the chain read them in phase 1)
+        prep_b<kLo>(sm, nb, cv, wave, n, g, df);
+        lds_barrier();
+    }
+}
+
 template <typename Tin, typename Tout, bool kOut>
-__global__ void __launch_bounds__(NT, 1) delta_seg_kernel(Params p) {
+__global__ void __launch_bounds__(NT2, 2) delta_seg_kernel(Params p) {
     extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
     Smem<sizeof(Tin) == 4>& sm = *(Smem<sizeof(Tin) == 4>*)smem_raw;
     int b, hv, s;
     if (!unit_of(blockIdx.x, p, kOut ? p.P : p.P - 1, b, hv, s)) return;
     const int lane = threadIdx.x % WAVE;
     switch (__builtin_amdgcn_readfirstlane(threadIdx.x / WAVE)) {
-        case 0: seg_body<Tin, Tout, kOut, 0>(p, sm, b, hv, s, lane); break;
-        case 1: seg_body<Tin, Tout, kOut, 1>(p, sm, b, hv, s, lane); break;
-        case 2: seg_body<Tin, Tout, kOut, 2>(p, sm, b, hv, s, lane); break;
-        default: seg_body<Tin, Tout, kOut, 3>(p, sm, b, hv, s, lane); break;
-    }
-}
-
-template <typename Tout, bool kOut>
-__global__ void __launch_bounds__(NT8, 2) delta_seg8_kernel(Params p) {
-    extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
-    Smem8& sm = *(Smem8*)smem_raw;
-    int b, hv, s;
-    if (!unit_of(blockIdx.x, p, kOut ? p.P : p.P - 1, b, hv, s)) return;
-    const int lane = threadIdx.x % WAVE;
-    switch (__builtin_amdgcn_readfirstlane(threadIdx.x / WAVE)) {
-        case 0: seg8_body<Tout, kOut, 0>(p, sm, b, hv, s, lane); break;
-        case 1: seg8_body<Tout, kOut, 1>(p, sm, b, hv, s, lane); break;
-        case 2: seg8_body<Tout, kOut, 2>(p, sm, b, hv, s, lane); break;
-        case 3: seg8_body<Tout, kOut, 3>(p, sm, b, hv, s, lane); break;
-        case 4: seg8_body<Tout, kOut, 4>(p, sm, b, hv, s, lane); break;
-        case 5: seg8_body<Tout, kOut, 5>(p, sm, b, hv, s, lane); break;
-        case 6: seg8_body<Tout, kOut, 6>(p, sm, b, hv, s, lane); break;
-        default: seg8_body<Tout, kOut, 7>(p, sm, b, hv, s, lane); break;
+        case 0: chain_body<Tin, Tout, kOut, 0>(p, sm, b, hv, s, lane); break;
+        case 1: chain_body<Tin, Tout, kOut, 1>(p, sm, b, hv, s, lane); break;
+        case 2: chain_body<Tin, Tout, kOut, 2>(p, sm, b, hv, s, lane); break;
+        case 3: chain_body<Tin, Tout, kOut, 3>(p, sm, b, hv, s, lane); break;
+        case 4: prep_body<Tin, Tout, 4>(p, sm, b, hv, s, lane); break;
+        case 5: prep_body<Tin, Tout, 5>(p, sm, b, hv, s, lane); break;
+        case 6: prep_body<Tin, Tout, 6>(p, sm, b, hv, s, lane); break;
+        default: prep_body<Tin, Tout, 7>(p, sm, b, hv, s, lane); break;
     }
 }
 
 // Segment boundaries: S_1 = N_0, S_{s+1} = M_s S_s + N_s. One wave per (sequence, head,
 // 16-column slice); M_s as the fp16 A operand, S_s as fp16 hi + lo.
 __global__ void __launch_bounds__(WAVE) delta_seg_combine(Params p) {
-    const int unit = blockIdx.x / 8, slice = blockIdx.x % 8;
+    // the 8 column slices of one (sequence, head) on one XCD (block ids congruent mod 8), where
+    // they share each M_s through that XCD's L2
+    const int x = blockIdx.x, unit = (x / 64) * 8 + x % 8, slice = (x / 8) % 8;
     if (unit >= p.B * p.HV) return;
     const int lane = threadIdx.x, n = lane % 16, g = lane / 16;
     const int col = 16 * slice + n;
@@ -1117,16 +910,37 @@ __global__ void __launch_bounds__(WAVE) delta_seg_combine(Params p) {
     const float* N = p.nbuf + (size_t)unit * (p.P - 1) * DD;
     const half_t* Mb = p.mbuf + (size_t)unit * (p.P - 1) * DD;
     float* st = p.starts + (size_t)unit * p.P * DD;
+    // the operands of one boundary step: M_s rows as A fragments and N_s as the accumulators;
+    // the next step's are requested before this step's products (they do not depend on S)
+    struct Ops {
+        half8 a[8][4];
+        f32x4 acc[8];
+    };
+    auto load = [&](int s, Ops& o) {
+        const float* Ns = N + (size_t)s * DD;
+        const half_t* Ms = Mb + (size_t)s * DD;
+#pragma unroll
+        for (int ft = 0; ft < 8; ft++) {
+#pragma unroll
+            for (int r = 0; r < 4; r++) o.acc[ft][r] = Ns[(size_t)(16 * ft + 4 * g + r) * D + col];
+            const half_t* row = Ms + (size_t)(16 * ft + n) * D;
+#pragma unroll
+            for (int m = 0; m < 4; m++)
+                o.a[ft][m] = cat8(*(const half4*)(row + 32 * m + 4 * g), *(const half4*)(row + 32 * m + 16 + 4 * g));
+        }
+    };
     f32x4 S[8];
+    Ops ops[2];
 #pragma unroll
     for (int ft = 0; ft < 8; ft++)
 #pragma unroll
         for (int r = 0; r < 4; r++) S[ft][r] = N[(size_t)(16 * ft + 4 * g + r) * D + col];
+    if (p.P > 2) load(1, ops[0]);
 #pragma unroll
     for (int ft = 0; ft < 8; ft++)
 #pragma unroll
         for (int r = 0; r < 4; r++) st[DD + (size_t)(16 * ft + 4 * g + r) * D + col] = S[ft][r];
-    for (int s = 1; s + 1 < p.P; s++) {
+    auto step = [&](int s, const Ops& cur) {
         half8 bh[4], bl[4];
 #pragma unroll
         for (int m = 0; m < 4; m++) {
@@ -1136,27 +950,29 @@ __global__ void __launch_bounds__(WAVE) delta_seg_combine(Params p) {
             bh[m] = cat8(h0, h1);
             bl[m] = cat8(l0, l1);
         }
-        const float* Ns = N + (size_t)s * DD;
-        const half_t* Ms = Mb + (size_t)s * DD;
 #pragma unroll
-        for (int ft = 0; ft < 8; ft++) {
-            f32x4 acc;
+        for (int ft = 0; ft < 8; ft++) S[ft] = cur.acc[ft];
 #pragma unroll
-            for (int r = 0; r < 4; r++) acc[r] = Ns[(size_t)(16 * ft + 4 * g + r) * D + col];
-            const half_t* row = Ms + (size_t)(16 * ft + n) * D;
+        for (int m = 0; m < 4; m++)
 #pragma unroll
-            for (int m = 0; m < 4; m++) {
-                const half8 a = cat8(*(const half4*)(row + 32 * m + 4 * g), *(const half4*)(row + 32 * m + 16 + 4 * g));
-                acc = mfma32(a, bh[m], acc);
-                acc = mfma32(a, bl[m], acc);
+            for (int ft = 0; ft < 8; ft++) {
+                S[ft] = mfma32(cur.a[ft][m], bh[m], S[ft]);
+                S[ft] = mfma32(cur.a[ft][m], bl[m], S[ft]);
             }
-            S[ft] = acc;
-        }
         float* dst = st + (size_t)(s + 1) * DD;
 #pragma unroll
         for (int ft = 0; ft < 8; ft++)
 #pragma unroll
             for (int r = 0; r < 4; r++) dst[(size_t)(16 * ft + 4 * g + r) * D + col] = S[ft][r];
+    };
+    // two steps per iteration with alternating operand sets, so no set is copied (a copy would
+    // wait for its loads)
+    for (int s = 1; s + 1 < p.P; s += 2) {
+        if (s + 2 < p.P) load(s + 1, ops[1]);
+        step(s, ops[0]);
+        if (s + 2 >= p.P) break;
+        if (s + 3 < p.P) load(s + 2, ops[0]);
+        step(s + 1, ops[1]);
     }
 }
 
@@ -1267,44 +1083,31 @@ int run_chunked(const Tin* q, const Tin* k, const Tin* v, const float* g, const 
     p.starts = sp.P > 1 ? (float*)(w + wp.starts) : nullptr;
     p.nbuf = sp.P > 1 ? (float*)(w + wp.nbuf) : nullptr;
     p.mbuf = sp.P > 1 ? (half_t*)(w + wp.mbuf) : nullptr;
-    constexpr bool k8 = sizeof(Tin) == 2;  // bf16 inputs: the 8-wave form
-    const size_t lds = k8 ? sizeof(Smem8) : sizeof(Smem<sizeof(Tin) == 4>);
-    const int nthr = k8 ? NT8 : NT;
+    const size_t lds = sizeof(Smem<sizeof(Tin) == 4>);
     auto grid_for = [&](int nseg) {
         const int R = HV / HK, ngrp = B * nseg * HK;
         return (ngrp + 7) / 8 * 8 * R;
     };
     if (sp.P > 1) {
-        if constexpr (k8) delta_seg8_kernel<Tout, false><<<grid_for(sp.P - 1), nthr, lds, st>>>(p);
-        else delta_seg_kernel<Tin, Tout, false><<<grid_for(sp.P - 1), nthr, lds, st>>>(p);
+        delta_seg_kernel<Tin, Tout, false><<<grid_for(sp.P - 1), NT2, lds, st>>>(p);
         int rc = after_launch("delta_seg_kernel(transition)");
         if (rc) return rc;
-        delta_seg_combine<<<B * HV * 8, WAVE, 0, st>>>(p);
+        delta_seg_combine<<<(B * HV + 7) / 8 * 64, WAVE, 0, st>>>(p);
         rc = after_launch("delta_seg_combine");
         if (rc) return rc;
     }
-    if constexpr (k8) delta_seg8_kernel<Tout, true><<<grid_for(sp.P), nthr, lds, st>>>(p);
-    else delta_seg_kernel<Tin, Tout, true><<<grid_for(sp.P), nthr, lds, st>>>(p);
+    delta_seg_kernel<Tin, Tout, true><<<grid_for(sp.P), NT2, lds, st>>>(p);
     return after_launch("delta_seg_kernel(output)");
 }
 
 template <typename Tin, typename Tout>
 static int set_lds_limits() {
     static int done = [] {
-        hipError_t e1, e2;
-        if constexpr (sizeof(Tin) == 2) {
-            const int bytes = (int)sizeof(Smem8);
-            e1 = hipFuncSetAttribute((const void*)delta_seg8_kernel<Tout, false>,
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
-            e2 = hipFuncSetAttribute((const void*)delta_seg8_kernel<Tout, true>,
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
-        } else {
-            const int bytes = (int)sizeof(Smem<true>);
-            e1 = hipFuncSetAttribute((const void*)delta_seg_kernel<Tin, Tout, false>,
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
-            e2 = hipFuncSetAttribute((const void*)delta_seg_kernel<Tin, Tout, true>,
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
-        }
+        const int bytes = (int)sizeof(Smem<sizeof(Tin) == 4>);
+        const hipError_t e1 = hipFuncSetAttribute((const void*)delta_seg_kernel<Tin, Tout, false>,
+                                                  hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+        const hipError_t e2 = hipFuncSetAttribute((const void*)delta_seg_kernel<Tin, Tout, true>,
+                                                  hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
         return e1 == hipSuccess && e2 == hipSuccess ? 1 : -1;
     }();
     return done;

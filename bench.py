@@ -221,8 +221,10 @@ def bench_prefill(torch, ops, dev, reps=40):
     q = ops.fill_normal(torch.empty(1, PREFILL_T, HK, D, device=dev, dtype=bf), 7001).transpose(1, 2)
     k = ops.fill_normal(torch.empty(1, PREFILL_T, HK, D, device=dev, dtype=bf), 7002).transpose(1, 2)
     v = ops.fill_normal(torch.empty(1, PREFILL_T, HV, D, device=dev, dtype=bf), 7003).transpose(1, 2)
-    g = -torch.nn.functional.softplus(ops.fill_normal(torch.empty(1, HV, PREFILL_T, device=dev), 7004))
-    beta = torch.sigmoid(ops.fill_normal(torch.empty(1, HV, PREFILL_T, device=dev), 7005))
+    # g / beta generated token-major ([B, T, HV], the engine's gb layout) and passed as [B, HV, T]
+    # views, so the binding's layout change is a no-op and the timed call is the kernels alone
+    g = -torch.nn.functional.softplus(ops.fill_normal(torch.empty(1, PREFILL_T, HV, device=dev), 7004)).transpose(1, 2)
+    beta = torch.sigmoid(ops.fill_normal(torch.empty(1, PREFILL_T, HV, device=dev), 7005)).transpose(1, 2)
     S = torch.zeros(1, HV, D, D, device=dev)
     run = lambda: ops.delta_rule_chunked(q, k, v, g, beta, S, normalize=True, qscale=D ** -0.5, out_dtype=bf)
     # ~100 ms of warm-up: after the CPU-side legs the GPU clocks need that long to ramp back up
