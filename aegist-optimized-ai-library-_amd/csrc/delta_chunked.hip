@@ -244,8 +244,8 @@ __device__ __forceinline__ void load_chunk(const Params& p, const Rsrc& rs, int 
 template <bool kLo>
 struct Conv {
     static constexpr int NL = kLo ? 4 : 0;
-    half8 k[4], q[4], v[4];     // natural feature order (pieces 32 ks + 8 g)
-    half8 kl[NL], ql[NL], vl[NL];
+    half8 q[4], v[4];           // natural feature order (pieces 32 ks + 8 g); k goes to LDS
+    half8 ql[NL], vl[NL];
     float rk, rq;               // own k row (tile wave), own q row (tile 3 - wave)
 };
 
@@ -285,6 +285,7 @@ template <typename Tin, bool kLo>
 __device__ __forceinline__ void prep_a(const Params& p, Smem<kLo>& sm, int buf, const Raw<Tin>& r, const RawGB& gb,
                                        int wave, int n, int g, int lane, Conv<kLo>& cv) {
     float ssk = 0.f, ssq = 0.f;
+    half8 k8[4], kl8[4];
 #pragma unroll
     for (int ks = 0; ks < 4; ks++) {
         float x[8];
@@ -295,8 +296,8 @@ __device__ __forceinline__ void prep_a(const Params& p, Smem<kLo>& sm, int buf, 
         } else {
             ssk = dot2sq(r.k, ks, ssk);
         }
-        cv.k[ks] = cvt8(x);
-        if constexpr (kLo) cv.kl[ks] = lo8(x, cv.k[ks]);
+        k8[ks] = cvt8(x);
+        if constexpr (kLo) kl8[ks] = lo8(x, k8[ks]);
         unpack8(r.q, ks, x);
         if constexpr (kLo) {
 #pragma unroll
@@ -317,8 +318,8 @@ __device__ __forceinline__ void prep_a(const Params& p, Smem<kLo>& sm, int buf, 
     // k rows of tile `wave` (natural order)
 #pragma unroll
     for (int ks = 0; ks < 4; ks++) {
-        *(half8*)&sm.K[buf][16 * wave + n][32 * ks + 8 * g] = cv.k[ks];
-        if constexpr (kLo) *(half8*)&sm.KL[buf][16 * wave + n][32 * ks + 8 * g] = cv.kl[ks];
+        *(half8*)&sm.K[buf][16 * wave + n][32 * ks + 8 * g] = k8[ks];
+        if constexpr (kLo) *(half8*)&sm.KL[buf][16 * wave + n][32 * ks + 8 * g] = kl8[ks];
     }
     // inclusive prefix sum of g over the chunk (lane = token)
     float x = gb.g;
@@ -359,24 +360,31 @@ __device__ __forceinline__ void prep_b(Smem<kLo>& sm, int buf, const Conv<kLo>& 
     const int iq = 3 - wv;
     // factors of this lane's rows
     const float la_i = F.la[16 * wv + n], lq_i = F.lq[16 * iq + n], mk_i = F.mk[16 * wv + n];
+    // this wave's own k rows (the B operand of its Gram row block), read back from LDS
+    half8 kb[4], kbl[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ks++) {
+        kb[ks] = *(const half8*)&sm.K[buf][16 * wv + n][32 * ks + 8 * g];
+        if constexpr (kLo) kbl[ks] = *(const half8*)&sm.KL[buf][16 * wv + n][32 * ks + 8 * g];
+    }
 #pragma unroll
     for (int jt = 0; jt < 4; jt++) {
         if (jt > wv && jt > iq) continue;
         half8 ka[4], kal[4];
 #pragma unroll
         for (int ks = 0; ks < 4; ks++) {
-            ka[ks] = jt == wv ? cv.k[ks] : *(const half8*)&sm.K[buf][16 * jt + n][32 * ks + 8 * g];
-            if constexpr (kLo) kal[ks] = jt == wv ? cv.kl[ks] : *(const half8*)&sm.KL[buf][16 * jt + n][32 * ks + 8 * g];
+            ka[ks] = *(const half8*)&sm.K[buf][16 * jt + n][32 * ks + 8 * g];
+            if constexpr (kLo) kal[ks] = *(const half8*)&sm.KL[buf][16 * jt + n][32 * ks + 8 * g];
         }
         const f32x4 mkj = *(const f32x4*)&F.mk[16 * jt + 4 * g];
         if (jt <= wv) {
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int ks = 0; ks < 4; ks++) {
-                acc = mfma32(ka[ks], cv.k[ks], acc);
+                acc = mfma32(ka[ks], kb[ks], acc);
                 if constexpr (kLo) {
-                    acc = mfma32(ka[ks], cv.kl[ks], acc);
-                    acc = mfma32(kal[ks], cv.k[ks], acc);
+                    acc = mfma32(ka[ks], kbl[ks], acc);
+                    acc = mfma32(kal[ks], kb[ks], acc);
                 }
             }
             f32x4 av;
