@@ -104,7 +104,7 @@ def cpu_model() -> str:
     return platform.processor() or "unknown"
 
 
-def _median_time(fn, warm=1, n=3):
+def _median_time(fn, warm=2, n=5):
     for _ in range(warm):
         fn()
     ts = []
@@ -121,7 +121,8 @@ def cpu_baseline_configs(torch):
     B = 1); config 2 on the first 1024 of 8192 tokens (the chunked form is linear in T);
     config 3 at one point (B = 1, L = 32768); config 4 as one DeltaNet and one attention layer at
     full shape (decode at B = 16 with 2048 cached tokens; prefill on 256 of 2048 tokens of one
-    sequence) scaled to 30 + 10 layers."""
+    sequence) scaled to 30 + 10 layers. Every figure is the median of 5 timed runs after 2
+    untimed warm-ups."""
     from oracle import mixer_ref as R
     torch.set_num_threads(cpu_threads())
     F = torch.nn.functional
@@ -176,8 +177,8 @@ def cpu_baseline_configs(torch):
     ta = _median_time(lambda: R.gated_attention_mixer(h1, Wa, kc4, vc4, T4, ATTN_H, ATTN_KV))
     hp = torch.randn(1, Tp, 2048, generator=g_)
     tdp = _median_time(lambda: R.gated_deltanet_mixer(hp, Wd, torch.zeros(1, Cc, 3), torch.zeros(1, HV, D, D), 0,
-                                                      HK, HV), warm=1, n=1)
-    tap = _median_time(lambda: R.gated_attention_mixer(hp, Wa, kc4[:1], vc4[:1], 0, ATTN_H, ATTN_KV), warm=1, n=1)
+                                                      HK, HV))
+    tap = _median_time(lambda: R.gated_attention_mixer(hp, Wa, kc4[:1], vc4[:1], 0, ATTN_H, ATTN_KV))
     step = 30 * td + 10 * ta
     # prefill: per-token cost of the 256-token sample (attention's quadratic part is a small
     # share of its layer at T = 2048; the sample understates it, so the CPU figure is generous)
