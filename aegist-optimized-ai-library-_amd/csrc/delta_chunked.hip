@@ -227,13 +227,13 @@ __device__ __forceinline__ Rsrc make_rsrc(const Params& p, int b, int hv) {
 }
 
 // Issue the global loads of chunk c (tokens past T read as zeros).
-template <typename Tin>
+template <typename Tin, bool kQ>
 __device__ __forceinline__ void load_chunk(const Params& p, const Rsrc& rs, int c, int wave, int n, int g, int lane,
                                            Raw<Tin>& r, RawGB& gb) {
     const int tk = c * CH + 16 * wave + n, tq = c * CH + 16 * (3 - wave) + n;
     const int sz = (int)sizeof(Tin);
     load_rows(rs.k, tk * (int)p.a.st_qk * sz, g, r.k);
-    load_rows(rs.q, tq * (int)p.a.st_qk * sz, g, r.q);
+    if constexpr (kQ) load_rows(rs.q, tq * (int)p.a.st_qk * sz, g, r.q);
     load_rows(rs.v, tk * (int)p.a.st_v * sz, g, r.v);
     const int go = (c * CH + lane) * (int)p.a.st_g * 4;
     gb.g = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs.g, go, 0, 0));
@@ -281,7 +281,7 @@ __device__ __forceinline__ half8 lo8(const float* x, half8 h) {
 
 // Prep phase A for chunk c into parity buffer `buf`: fp16 rows, norms, cumulative decays and the
 // per-token factors; writes K[buf] rows of token tile `wave` and this wave's entries of F[buf].
-template <typename Tin, bool kLo>
+template <typename Tin, bool kLo, bool kQ>
 __device__ __forceinline__ void prep_a(const Params& p, Smem<kLo>& sm, int buf, const Raw<Tin>& r, const RawGB& gb,
                                        int wave, int n, int g, int lane, Conv<kLo>& cv) {
     float ssk = 0.f, ssq = 0.f;
@@ -298,23 +298,27 @@ __device__ __forceinline__ void prep_a(const Params& p, Smem<kLo>& sm, int buf, 
         }
         k8[ks] = cvt8(x);
         if constexpr (kLo) kl8[ks] = lo8(x, k8[ks]);
-        unpack8(r.q, ks, x);
-        if constexpr (kLo) {
+        if constexpr (kQ) {
+            unpack8(r.q, ks, x);
+            if constexpr (kLo) {
 #pragma unroll
-            for (int e = 0; e < 8; e++) ssq += x[e] * x[e];
-        } else {
-            ssq = dot2sq(r.q, ks, ssq);
+                for (int e = 0; e < 8; e++) ssq += x[e] * x[e];
+            } else {
+                ssq = dot2sq(r.q, ks, ssq);
+            }
+            cv.q[ks] = cvt8(x);
+            if constexpr (kLo) cv.ql[ks] = lo8(x, cv.q[ks]);
         }
-        cv.q[ks] = cvt8(x);
-        if constexpr (kLo) cv.ql[ks] = lo8(x, cv.q[ks]);
         unpack8(r.v, ks, x);
         cv.v[ks] = cvt8(x);
         if constexpr (kLo) cv.vl[ks] = lo8(x, cv.v[ks]);
     }
     ssk = pair_sum32(pair_sum16(ssk));
-    ssq = pair_sum32(pair_sum16(ssq));
     cv.rk = p.normalize ? rsqrtf(ssk + p.eps) : 1.f;
-    cv.rq = p.normalize ? rsqrtf(ssq + p.eps) * p.qscale : 1.f;
+    if constexpr (kQ) {
+        ssq = pair_sum32(pair_sum16(ssq));
+        cv.rq = p.normalize ? rsqrtf(ssq + p.eps) * p.qscale : 1.f;
+    }
     // k rows of tile `wave` (natural order)
 #pragma unroll
     for (int ks = 0; ks < 4; ks++) {
@@ -341,7 +345,7 @@ __device__ __forceinline__ void prep_a(const Params& p, Smem<kLo>& sm, int buf, 
         F.beta[tw] = beta_t;
         F.fx[tw] = brk * __expf(cum_t);
         F.fp[tw] = cv.rk * __expf(cl - cum_t);
-        F.lq[tq] = cum_q * kLog2e + __builtin_amdgcn_logf(cv.rq);
+        if constexpr (kQ) F.lq[tq] = cum_q * kLog2e + __builtin_amdgcn_logf(cv.rq);
     }
     if (wave == 0 && lane == 0) F.gam = __expf(cl);
 }
@@ -349,7 +353,7 @@ __device__ __forceinline__ void prep_a(const Params& p, Smem<kLo>& sm, int buf, 
 // Prep phase B for chunk c (after a barrier: K[buf] and F[buf] complete): the Gram products, -A
 // blocks, the diagonal-block inverse D_wave and intra into `df` (written to LDS by the next
 // period), and the q and v rows into Q and V.
-template <bool kLo>
+template <bool kLo, bool kQ>
 __device__ __forceinline__ void prep_b(Smem<kLo>& sm, int buf, const Conv<kLo>& cv, int wave, int n, int g,
                                        Deferred& df) {
     const Fact& F = sm.F[buf];
@@ -359,7 +363,7 @@ __device__ __forceinline__ void prep_b(Smem<kLo>& sm, int buf, const Conv<kLo>& 
     // G: it = wv, jt <= wv.  k q^T: it = 3 - wv, jt <= 3 - wv.
     const int iq = 3 - wv;
     // factors of this lane's rows
-    const float la_i = F.la[16 * wv + n], lq_i = F.lq[16 * iq + n], mk_i = F.mk[16 * wv + n];
+    const float la_i = F.la[16 * wv + n], lq_i = kQ ? F.lq[16 * iq + n] : 0.f, mk_i = F.mk[16 * wv + n];
     // this wave's own k rows (the B operand of its Gram row block), read back from LDS
     half8 kb[4], kbl[4];
 #pragma unroll
@@ -369,7 +373,7 @@ __device__ __forceinline__ void prep_b(Smem<kLo>& sm, int buf, const Conv<kLo>& 
     }
 #pragma unroll
     for (int jt = 0; jt < 4; jt++) {
-        if (jt > wv && jt > iq) continue;
+        if (jt > wv && (!kQ || jt > iq)) continue;
         half8 ka[4], kal[4];
 #pragma unroll
         for (int ks = 0; ks < 4; ks++) {
@@ -419,7 +423,7 @@ __device__ __forceinline__ void prep_b(Smem<kLo>& sm, int buf, const Conv<kLo>& 
                 df.d = h4(pp);
             }
         }
-        if (jt <= iq) {
+        if (kQ && jt <= iq) {
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int ks = 0; ks < 4; ks++) {
@@ -443,14 +447,16 @@ __device__ __forceinline__ void prep_b(Smem<kLo>& sm, int buf, const Conv<kLo>& 
         const float f = __builtin_amdgcn_exp2f(lq_i);
 #pragma unroll
         for (int ks = 0; ks < 4; ks++) {
-            half8 y;
+            if constexpr (kQ) {
+                half8 y;
 #pragma unroll
-            for (int e = 0; e < 8; e++) {
-                float x = (float)cv.q[ks][e];
-                if constexpr (kLo) x += (float)cv.ql[ks][e];
-                y[e] = (half_t)(f * x);
+                for (int e = 0; e < 8; e++) {
+                    float x = (float)cv.q[ks][e];
+                    if constexpr (kLo) x += (float)cv.ql[ks][e];
+                    y[e] = (half_t)(f * x);
+                }
+                *(half8*)&sm.Q[16 * iq + n][32 * ks + 8 * g] = y;
             }
-            *(half8*)&sm.Q[16 * iq + n][32 * ks + 8 * g] = y;
             *(half8*)&sm.V[16 * wv + n][32 * ks + 8 * g] = cv.v[ks];
             if constexpr (kLo) *(half8*)&sm.VL[0][16 * wv + n][32 * ks + 8 * g] = cv.vl[ks];
         }
@@ -458,13 +464,14 @@ __device__ __forceinline__ void prep_b(Smem<kLo>& sm, int buf, const Conv<kLo>& 
 }
 
 // The deferred operands of one chunk into AD / IH / IL.
-template <bool kLo>
+template <bool kLo, bool kQ>
 __device__ __forceinline__ void write_deferred(Smem<kLo>& sm, const Deferred& df, int wave, int n, int g) {
     const int wv = wave, iq = 3 - wave;
 #pragma unroll
     for (int jt = 0; jt < 3; jt++)
         if (jt < wv) *(half4*)&sm.AD[16 * wv + n][16 * jt + 4 * g] = df.am[jt];
     *(half4*)&sm.AD[16 * wv + n][16 * wv + 4 * g] = df.d;
+    if constexpr (!kQ) return;
 #pragma unroll
     for (int jt = 0; jt < 4; jt++)
         if (jt <= iq) {
@@ -855,7 +862,7 @@ __device__ __forceinline__ void chain_body(const Params& p, Smem<sizeof(Tin) == 
     seg_end<kOut>(p, unit, s, col0, n, g, S, M);
 }
 
-template <typename Tin, typename Tout, int WV>
+template <typename Tin, typename Tout, bool kQ, int WV>
 __device__ __forceinline__ void prep_body(const Params& p, Smem<sizeof(Tin) == 4>& sm, int b, int hv, int s,
                                           int lane) {
     constexpr bool kLo = sizeof(Tin) == 4;
@@ -867,21 +874,21 @@ __device__ __forceinline__ void prep_body(const Params& p, Smem<sizeof(Tin) == 4
     RawGB gb;
     Conv<kLo> cv;
     Deferred df;
-    load_chunk<Tin>(p, rs, c0, wave, n, g, lane, raw, gb);
-    prep_a<Tin, kLo>(p, sm, c0 & 1, raw, gb, wave, n, g, lane, cv);
-    load_chunk<Tin>(p, rs, c0 + 1, wave, n, g, lane, raw, gb);
+    load_chunk<Tin, kQ>(p, rs, c0, wave, n, g, lane, raw, gb);
+    prep_a<Tin, kLo, kQ>(p, sm, c0 & 1, raw, gb, wave, n, g, lane, cv);
+    load_chunk<Tin, kQ>(p, rs, c0 + 1, wave, n, g, lane, raw, gb);
     lds_barrier();
-    prep_b<kLo>(sm, c0 & 1, cv, wave, n, g, df);
+    prep_b<kLo, kQ>(sm, c0 & 1, cv, wave, n, g, df);
     lds_barrier();
     for (int c = c0; c < c1; c++) {
         const int nb = (c & 1) ^ 1;
         // ---- phase 1: chunk c's A / D / intra into LDS; prep A of chunk c + 1
-        write_deferred<kLo>(sm, df, wave, n, g);
-        prep_a<Tin, kLo>(p, sm, nb, raw, gb, wave, n, g, lane, cv);
-        load_chunk<Tin>(p, rs, c + 2, wave, n, g, lane, raw, gb);
+        write_deferred<kLo, kQ>(sm, df, wave, n, g);
+        prep_a<Tin, kLo, kQ>(p, sm, nb, raw, gb, wave, n, g, lane, cv);
+        load_chunk<Tin, kQ>(p, rs, c + 2, wave, n, g, lane, raw, gb);
         lds_barrier();
         // ---- phase 2: prep B of chunk c + 1 (Q and V are rewritten: the chain read them in phase 1)
-        prep_b<kLo>(sm, nb, cv, wave, n, g, df);
+        prep_b<kLo, kQ>(sm, nb, cv, wave, n, g, df);
         lds_barrier();
     }
 }
@@ -898,10 +905,10 @@ __global__ void __launch_bounds__(NT2, 2) delta_seg_kernel(Params p) {
         case 1: chain_body<Tin, Tout, kOut, 1>(p, sm, b, hv, s, lane); break;
         case 2: chain_body<Tin, Tout, kOut, 2>(p, sm, b, hv, s, lane); break;
         case 3: chain_body<Tin, Tout, kOut, 3>(p, sm, b, hv, s, lane); break;
-        case 4: prep_body<Tin, Tout, 4>(p, sm, b, hv, s, lane); break;
-        case 5: prep_body<Tin, Tout, 5>(p, sm, b, hv, s, lane); break;
-        case 6: prep_body<Tin, Tout, 6>(p, sm, b, hv, s, lane); break;
-        default: prep_body<Tin, Tout, 7>(p, sm, b, hv, s, lane); break;
+        case 4: prep_body<Tin, Tout, kOut, 4>(p, sm, b, hv, s, lane); break;
+        case 5: prep_body<Tin, Tout, kOut, 5>(p, sm, b, hv, s, lane); break;
+        case 6: prep_body<Tin, Tout, kOut, 6>(p, sm, b, hv, s, lane); break;
+        default: prep_body<Tin, Tout, kOut, 7>(p, sm, b, hv, s, lane); break;
     }
 }
 
