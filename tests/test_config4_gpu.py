@@ -228,3 +228,53 @@ def test_config4_stack_properties(dev):
     bar = max(1e-3, 2 * max(floor))
     for name, b, i, er, em in errs:
         assert er < bar, (name, b, i, er, em, bar)
+
+
+@pytest.mark.parametrize("kind", ["delta", "attn"])
+def test_config4_decode_256_steps(dev, kind, monkeypatch):
+    """Config 4's full decode length (hybrid.py:812-843: 256 steps after the 2048-token prefill)
+    on one layer of each kind at full shape and B = 16: sequence 5 against the CPU oracle run on
+    that sequence alone, every step, to the same bars as the two-step layer test (the KV cache
+    grows from 2048 to 2304 rows, so the attention core's split counts change on the way)."""
+    steps, row = 256, 5
+    W = cpu_layer(kind, seed=50 if kind == "delta" else 51)
+    w_out = W["w_out" if kind == "delta" else "w_o"]
+    stack = ops.HybridStack(CFG, [kind], [{k: v.to(dev) for k, v in W.items()}], max_batch=B, max_tokens=B * T,
+                            max_context=T + steps)
+    g_ = torch.Generator().manual_seed(17)
+    x0 = torch.randn(B, T, 2048, generator=g_)
+    xs = torch.randn(steps, B, 1, 2048, generator=g_)
+    print(f"config4 {kind} layer: prefill {T} + {steps} decode steps, B={B}", flush=True)
+    outs = []
+    xd = x0.to(dev)
+    stack.forward(xd)
+    outs.append((xd - x0.to(dev))[row:row + 1].cpu())
+    for s in range(steps):
+        xd = xs[s].to(dev)
+        stack.forward(xd)
+        outs.append((xd - xs[s].to(dev))[row:row + 1].cpu())
+    torch.cuda.synchronize()
+    stack.close()
+
+    seen = {}
+    lin = R._lin
+
+    def spy(x, w, round_in):
+        if w is w_out:
+            seen["u"] = max(seen.get("u", 0.0), x.abs().max().item())
+        return lin(x, w, round_in)
+    monkeypatch.setattr(R, "_lin", spy)
+    wmax = w_out.float().abs().max().item()
+    cache = oracle_cache([kind], T + steps)
+    feeds = [x0[row:row + 1]] + [xs[s][row:row + 1] for s in range(steps)]
+    worst = (0.0, 0.0, -1)
+    for i, xb in enumerate(feeds):
+        seen.clear()
+        ref = R.hybrid_stack_forward(xb.clone(), [W], [kind], cache, CFG) - xb
+        flips = 2 * bf16_ulp(seen["u"]) * wmax / ref.abs().max().item()
+        em, er = rel_err(outs[i], ref), rms_err(outs[i], ref)
+        if i in (0, 1, 64, 128, steps) or er > worst[1]:
+            print(f"  feed {i}: max {em:.2e} (bar {1e-3 + flips:.2e})  rms {er:.2e}", flush=True)
+        worst = max(worst, (em, er, i), key=lambda t: t[1])
+        assert er < 1e-3 and em < 1e-3 + flips, (kind, i, em, er)
+    assert cache["length"] == T + steps
