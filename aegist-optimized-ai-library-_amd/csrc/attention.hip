@@ -7,14 +7,16 @@
 // query heads twice, as a bf16 hi part (rows 0-7) and the bf16 residual (rows 8-15), so
 // q (fp32) and P (fp32) enter the products with ~16 significant bits while K and V are the
 // exact bf16 cache values; row h + row h+8 recovers the fp32-accurate result.
-//   - K operand: lane (key n, group g) loads K[key n][32 ks + 8 g .. +8] straight from HBM.
-//   - V operand: the wave stages its 32-key V tile row-major in LDS and reads 4 dims x 8
-//     keys per lane with 64-bit LDS reads, repacking pairs of keys into the bf16x8 operand;
-//     output column block 4p+j, lane column n is dim 64p + 4n + j.
+//   - K and V: each wave's next 32-key tile is requested a tile ahead into registers and staged
+//     row-major in the wave's LDS (16-byte row pad); the K operand of lane (key n, group g) is
+//     K[key n][32 ks + 8 g .. +8]; the V operand is read as 4 dims x 8 keys per lane with 64-bit
+//     LDS reads, repacking pairs of keys into the bf16x8 operand; output column block 4p+j,
+//     lane column n is dim 64p + 4n + j.
 //   - P is transposed from the score layout to the A-operand layout through 1 KiB of LDS.
 // Each wave runs its own online softmax over its tiles; the 4 waves merge in LDS and the
 // workgroup writes (m, l, O) for its split. A merge kernel combines the splits with
-// log-sum-exp weights and applies the sigmoid output gate.
+// log-sum-exp weights and applies the sigmoid output gate. The decode entry point's prep (ZNorm,
+// RoPE, cache append) runs inside the split launch when the rotary dim is 64.
 //
 // Semantics: hybrid.py:280-310 (grouped SDPA at T == 1, causal SDPA otherwise, sigmoid gate);
 // engine kernels attn_prep / attention_gated (hybrid.cu:86-173).
@@ -126,13 +128,63 @@ __device__ __forceinline__ float half_swap_sum(float x) {
     return __uint_as_float(a[0]) + __uint_as_float(a[1]);
 }
 
-template <bool kList>
+// The decode step's own prep folded into the split launch (rotary dim 64): every workgroup
+// normalises and rotates its G query rows straight from qg while its first K / V tile is in
+// flight, and the workgroup of the last split normalises and rotates the new key, appends the
+// key and value rows to the cache at row pos and substitutes them into its staged tile (the tile
+// it fetched holds whatever row pos held before). Same arithmetic as attn_prep_vec_kernel, so
+// the appended rows and the queries are bit-identical to the separate prep launch's.
+struct FusedPrep {
+    const void* qg;            // [B, H, 2 HD]: query | gate (Tin)
+    const void* kn;            // [B, KV, HD] new key rows (Tin)
+    const void* vn;            // [B, KV, HD] new value rows (Tin)
+    const uint16_t* qw;        // q / k ZNorm weights (bf16, applied as 1 + w)
+    const uint16_t* kw;
+    uint16_t* kc;              // the caches, written at row pos
+    uint16_t* vc;
+    int pos;
+    float eps;
+    float inv[32];             // RoPE inverse frequencies, rotary dim 64
+};
+constexpr int kFusedRD = 64;
+
+// 4 consecutive elements as raw words (bf16: 8 bytes in .x, .y; fp32: 16 bytes) and unpacked
+template <typename T> __device__ __forceinline__ uint4 ld_raw4(const T* p);
+template <> __device__ __forceinline__ uint4 ld_raw4<uint16_t>(const uint16_t* p) {
+    const uint2 a = *(const uint2*)p;
+    return uint4{a.x, a.y, 0u, 0u};
+}
+template <> __device__ __forceinline__ uint4 ld_raw4<float>(const float* p) { return *(const uint4*)p; }
+template <typename T> __device__ __forceinline__ void unpack4(uint4 a, float* o);
+template <> __device__ __forceinline__ void unpack4<uint16_t>(uint4 a, float* o) {
+    o[0] = bf_lo(a.x); o[1] = bf_hi(a.x); o[2] = bf_lo(a.y); o[3] = bf_hi(a.y);
+}
+template <> __device__ __forceinline__ void unpack4<float>(uint4 a, float* o) {
+    o[0] = __uint_as_float(a.x); o[1] = __uint_as_float(a.y); o[2] = __uint_as_float(a.z); o[3] = __uint_as_float(a.w);
+}
+
+// piece ks (8 consecutive elements) of a raw row held as 16-byte words
+template <typename T> __device__ __forceinline__ void unpack8(const uint4* raw, int ks, float* o);
+template <> __device__ __forceinline__ void unpack8<uint16_t>(const uint4* raw, int ks, float* o) {
+    const uint4 a = raw[ks];
+    o[0] = bf_lo(a.x); o[1] = bf_hi(a.x); o[2] = bf_lo(a.y); o[3] = bf_hi(a.y);
+    o[4] = bf_lo(a.z); o[5] = bf_hi(a.z); o[6] = bf_lo(a.w); o[7] = bf_hi(a.w);
+}
+template <> __device__ __forceinline__ void unpack8<float>(const uint4* raw, int ks, float* o) {
+    const uint4 a = raw[2 * ks], c = raw[2 * ks + 1];
+    o[0] = __uint_as_float(a.x); o[1] = __uint_as_float(a.y); o[2] = __uint_as_float(a.z); o[3] = __uint_as_float(a.w);
+    o[4] = __uint_as_float(c.x); o[5] = __uint_as_float(c.y); o[6] = __uint_as_float(c.z); o[7] = __uint_as_float(c.w);
+}
+
+// TQ: float = the queries come normed and rotated in q; uint16_t / float with kFused = the prep
+// is done here from fp.qg (bf16 / fp32 inputs).
+template <bool kList, bool kFused = false, typename Tin = float>
 __global__ void __launch_bounds__(256) attn_decode_split_kernel(const float* __restrict__ q,
                                                                 const uint16_t* __restrict__ kc,
                                                                 const uint16_t* __restrict__ vc,
                                                                 float* __restrict__ part, float* __restrict__ ml,
                                                                 int H, int KV, int L, int cap, int per_split,
-                                                                float scale, KeyList kl) {
+                                                                float scale, KeyList kl, FusedPrep fp) {
     // V staging per wave during the loop; the 4-wave merge buffer reuses the same bytes after it
     __shared__ __attribute__((aligned(16))) unsigned char vbuf_raw[4 * TILE * VROW];
     __shared__ __attribute__((aligned(16))) unsigned char kbuf[4][TILE * VROW];
@@ -163,7 +215,7 @@ __global__ void __launch_bounds__(256) attn_decode_split_kernel(const float* __r
     // ---- Q operand: rows 0..7 = hi(q*scale), rows 8..15 = lo; lane row n, k elems 8g..8g+7.
     // Rows past G read row 0 and scale it by 0: unconditional loads issue back to back.
     bf16x8 qa[8];
-    {
+    if constexpr (!kFused) {
         const int r = n & 7;
         const bool lo = n >= 8;
         const bool valid = r < G;
@@ -182,6 +234,10 @@ __global__ void __launch_bounds__(256) attn_decode_split_kernel(const float* __r
     }
 
     const size_t cache_row = listed ? (size_t)kvh : (size_t)b * KV + kvh;
+    // the new key / value rows (bf16, as appended) for the last split's staged tile
+    __shared__ __attribute__((aligned(16))) uint16_t knew[HD], vnew[HD];
+    // the wave of the last split whose tile holds row pos (tiles are dealt to the 4 waves in turn)
+    const bool owns_new = kFused && split == nsplit - 1 && wave == ((fp.pos - k0) / TILE) % 4;
     const uint16_t* kbase = kc + cache_row * (size_t)cap * HD;
     const uint16_t* vbase = vc + cache_row * (size_t)cap * HD;
     // listed keys: lane l holds the cache position of row l % 32 of a tile, looked up one tile
@@ -221,6 +277,36 @@ __global__ void __launch_bounds__(256) attn_decode_split_kernel(const float* __r
             vreg[it] = *(const uint4*)(vbase + (size_t)key * HD + cc * 8);
         }
     };
+    // fused prep: the raw query rows and norm weights are requested before the first tile, and
+    // lane j holds cos / sin of pos * inv_freq[j % 32] (the 32 frequencies selected from scalar
+    // registers: no vector-memory access behind the tile's loads)
+    uint4 qraw[kFused ? 8 * sizeof(Tin) / 2 : 1], wraw[kFused ? 8 : 1];
+    float rc = 0.f, rs = 0.f;
+    uint4 knraw{}, vnraw{}, kwraw{};
+    if constexpr (kFused) {
+        const int r = n & 7;
+        const Tin* qrow = (const Tin*)fp.qg + ((size_t)b * H + kvh * G + (r < G ? r : 0)) * 2 * HD;
+#pragma unroll
+        for (int ks = 0; ks < 8; ks++) {
+            if constexpr (sizeof(Tin) == 2) {
+                qraw[ks] = *(const uint4*)(qrow + ks * 32 + 8 * g);
+            } else {
+                qraw[2 * ks] = *(const uint4*)(qrow + ks * 32 + 8 * g);
+                qraw[2 * ks + 1] = *(const uint4*)(qrow + ks * 32 + 8 * g + 4);
+            }
+            wraw[ks] = *(const uint4*)(fp.qw + ks * 32 + 8 * g);
+        }
+        if (owns_new) {
+            const size_t o = ((size_t)b * KV + kvh) * HD + 4 * lane;
+            knraw = ld_raw4<Tin>((const Tin*)fp.kn + o);
+            vnraw = ld_raw4<Tin>((const Tin*)fp.vn + o);
+            kwraw = ld_raw4<uint16_t>(fp.kw + 4 * lane);
+        }
+        float f = 0.f;
+#pragma unroll
+        for (int j = 0; j < 32; j++) f = (lane & 31) == j ? fp.inv[j] : f;
+        sincosf((float)fp.pos * f, &rs, &rc);
+    }
     const int first = k0 + wave * TILE, stride = 4 * TILE;
     int kp_next = 0;
     if (first < k1) {
@@ -229,6 +315,78 @@ __global__ void __launch_bounds__(256) attn_decode_split_kernel(const float* __r
             kp_next = tile_keys(min(first + stride, k1 - 1));
         } else {
             fetch(first, 0);
+        }
+    }
+    if constexpr (kFused) {
+        // query rows: ZNorm (sum of squares over the 4 lanes g of a row) and RoPE on dims < 64,
+        // whose partners d, d + 32 sit in pieces ks = 0 and 1 of the same lane. The raw rows
+        // were requested before the first tile (loads return in order).
+        const bool lo = n >= 8, valid = (n & 7) < G;
+        float ss = 0.f;
+#pragma unroll
+        for (int ks = 0; ks < 8; ks++) {
+            float x[8];
+            unpack8<Tin>(qraw, ks, x);
+#pragma unroll
+            for (int i = 0; i < 8; i++) ss += x[i] * x[i];
+        }
+        ss += __shfl_xor(ss, 16, WAVE);
+        ss += __shfl_xor(ss, 32, WAVE);
+        const float inv = rsqrtf(ss / (float)HD + fp.eps), qscale = valid ? scale : 0.f;
+#pragma unroll
+        for (int ks = 0; ks < 8; ks += 2) {
+            float x0[8], x1[8], w0[8], w1[8];
+            unpack8<Tin>(qraw, ks, x0);
+            unpack8<Tin>(qraw, ks + 1, x1);
+            unpack8<uint16_t>(wraw, ks, w0);
+            unpack8<uint16_t>(wraw, ks + 1, w1);
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                float y0 = (x0[i] * inv) * (1.f + w0[i]), y1 = (x1[i] * inv) * (1.f + w1[i]);
+                if (ks == 0) {
+                    const float c = __shfl(rc, 8 * g + i, WAVE), sn = __shfl(rs, 8 * g + i, WAVE);
+                    const float r0 = y0 * c + (-y1) * sn, r1 = y1 * c + y0 * sn;
+                    y0 = r0;
+                    y1 = r1;
+                }
+                uint16_t h, l;
+                split_bf16(y0 * qscale, h, l);
+                qa[ks][i] = (short)(lo ? l : h);
+                split_bf16(y1 * qscale, h, l);
+                qa[ks + 1][i] = (short)(lo ? l : h);
+            }
+        }
+        if (owns_new) {
+            // the new key row: lane l holds dims 4l .. 4l + 3 (the prep kernel's layout and order)
+            const size_t rkv = (size_t)b * KV + kvh;
+            const int e0 = 4 * lane;
+            float x[4], vv[4], wn[4];
+            unpack4<Tin>(knraw, x);
+            unpack4<Tin>(vnraw, vv);
+            unpack4<uint16_t>(kwraw, wn);
+            float sk = (x[0] * x[0] + x[1] * x[1]) + (x[2] * x[2] + x[3] * x[3]);
+            sk = wave_sum(sk);
+            const float ik = rsqrtf(sk / (float)HD + fp.eps);
+            float y[4], o4[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) y[e] = (x[e] * ik) * (1.f + wn[e]);
+            constexpr int half = kFusedRD / 2;
+            const int plane = e0 < half ? lane + half / 4 : lane - half / 4;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const float yp = __shfl(y[e], plane < 0 ? 0 : (plane > 63 ? 63 : plane), WAVE);
+                const int i = e0 + e;
+                o4[e] = y[e];
+                const float ce = __shfl(rc, i & (half - 1), WAVE), se = __shfl(rs, i & (half - 1), WAVE);
+                if (i < kFusedRD) o4[e] = y[e] * ce + (i < half ? -yp : yp) * se;
+            }
+            const uint2 kb2 = uint2{f2bf2(o4[0], o4[1]), f2bf2(o4[2], o4[3])};
+            const uint2 vb2 = uint2{f2bf2(vv[0], vv[1]), f2bf2(vv[2], vv[3])};
+            const size_t o = (rkv * cap + fp.pos) * HD + e0;
+            *(uint2*)(fp.kc + o) = kb2;
+            *(uint2*)(fp.vc + o) = vb2;
+            *(uint2*)&knew[e0] = kb2;
+            *(uint2*)&vnew[e0] = vb2;  // read back only by this wave (LDS ops of a wave run in order)
         }
     }
     for (int t0 = first; t0 < k1; t0 += stride) {
@@ -241,6 +399,17 @@ __global__ void __launch_bounds__(256) attn_decode_split_kernel(const float* __r
             uint2* dk = (uint2*)(kb_l + row * VROW + cc * 16);
             dk[0] = uint2{kreg[it].x, kreg[it].y};
             dk[1] = uint2{kreg[it].z, kreg[it].w};
+        }
+        if constexpr (kFused) {
+            // the last split's tile holding row pos: that row and the rows clamped to it (keys
+            // past the split) take the new key / value, so no stale cache bytes enter P V
+            if (owns_new && t0 + TILE > fp.pos) {
+                for (int rr = max(fp.pos - t0, 0) + (lane >> 5); rr < TILE; rr += 2) {
+                    const int cc = lane & 31;
+                    *(uint4*)(kb_l + rr * VROW + cc * 16) = *(const uint4*)&knew[8 * cc];
+                    *(uint4*)(vb + rr * VROW + cc * 16) = *(const uint4*)&vnew[8 * cc];
+                }
+            }
         }
         fetch(min(t0 + stride, k1 - 1), kp_next);  // next tile (unconditional: static wait counts)
         if constexpr (listed) kp_next = tile_keys(min(t0 + 2 * stride, k1 - 1));
@@ -1452,7 +1621,8 @@ size_t decode_workspace_bytes(int B, int H, int KV, int L, bool with_q) {
 template <typename TG, typename Tout>
 int launch_decode_core(const float* q, const uint16_t* kc, const uint16_t* vc, const TG* gate, long long gate_stride,
                        Tout* out, long long out_stride, int B, int H, int KV, int L, int cap, float scale,
-                       void* ws, size_t ws_bytes, hipStream_t st, KeyList kl = KeyList{nullptr, nullptr, 0, 0, 0}) {
+                       void* ws, size_t ws_bytes, hipStream_t st, KeyList kl = KeyList{nullptr, nullptr, 0, 0, 0},
+                       const FusedPrep* fused = nullptr, int fused_dtype = 0) {
     if (KV <= 0 || H % KV || H / KV > 8) return fail(AEGIST_ERR_SHAPE, "attention decode: need H % KV == 0 and H/KV <= 8");
     if (L <= 0 || L > cap) return fail(AEGIST_ERR_SHAPE, "attention decode: need 0 < L <= cap");
     DecodeSplit sp = choose_split(B, KV, L);
@@ -1462,12 +1632,19 @@ int launch_decode_core(const float* q, const uint16_t* kc, const uint16_t* vc, c
     float* part = (float*)ws;
     size_t part_bytes = ((size_t)B * KV * sp.nsplit * G * HD * 4 + 255) / 256 * 256;
     float* ml = (float*)((char*)ws + part_bytes);
-    if (kl.blist)
-        attn_decode_split_kernel<true><<<dim3(sp.nsplit, KV, B), 256, 0, st>>>(q, kc, vc, part, ml, H, KV, L, cap,
-                                                                             sp.per_split, scale, kl);
+    const dim3 grid(sp.nsplit, KV, B);
+    if (fused && fused_dtype == AEGIST_BF16)
+        attn_decode_split_kernel<false, true, uint16_t><<<grid, 256, 0, st>>>(q, kc, vc, part, ml, H, KV, L, cap,
+                                                                             sp.per_split, scale, kl, *fused);
+    else if (fused)
+        attn_decode_split_kernel<false, true, float><<<grid, 256, 0, st>>>(q, kc, vc, part, ml, H, KV, L, cap,
+                                                                          sp.per_split, scale, kl, *fused);
+    else if (kl.blist)
+        attn_decode_split_kernel<true><<<grid, 256, 0, st>>>(q, kc, vc, part, ml, H, KV, L, cap, sp.per_split, scale,
+                                                             kl, FusedPrep{});
     else
-        attn_decode_split_kernel<false><<<dim3(sp.nsplit, KV, B), 256, 0, st>>>(q, kc, vc, part, ml, H, KV, L, cap,
-                                                                              sp.per_split, scale, kl);
+        attn_decode_split_kernel<false><<<grid, 256, 0, st>>>(q, kc, vc, part, ml, H, KV, L, cap, sp.per_split, scale,
+                                                              kl, FusedPrep{});
     int rc = after_launch("attention_decode_split");
     if (rc) return rc;
     attn_decode_merge_wide_kernel<TG, Tout><<<B * KV * G, 256, 0, st>>>(part, ml, gate, gate_stride, out, out_stride,
@@ -1590,27 +1767,40 @@ int aegist_attention_decode(const void* qg, const void* k_new, const void* v_new
     hipStream_t st = AEG_STREAM(stream);
     size_t core = decode_workspace_bytes(B, H, KV, pos + 1, false);
     float* qn = (float*)((char*)workspace + core);
-    int rc = launch_attn_prep(qg, k_new, v_new, in_dtype, q_norm_w, k_norm_w, qn, kc, vc, B, 1, H, KV, HD, RD, pos, cap,
-                              eps, theta, st);
-    if (rc) return rc;
+    // rotary dim 64 (the model's): the prep runs inside the split launch; otherwise its own launch
+    FusedPrep fpp{qg, k_new, v_new, q_norm_w, k_norm_w, kc, vc, pos, eps, {}};
+    const bool fuse = RD == kFusedRD && (in_dtype == AEGIST_BF16 || in_dtype == AEGIST_F32) &&
+                      (uintptr_t)qg % 16 == 0 && (uintptr_t)k_new % 16 == 0 && (uintptr_t)v_new % 16 == 0 &&
+                      (uintptr_t)q_norm_w % 16 == 0 && (uintptr_t)k_norm_w % 8 == 0 && (uintptr_t)kc % 8 == 0 &&
+                      (uintptr_t)vc % 8 == 0;
+    const FusedPrep* fused = nullptr;
+    if (fuse) {
+        int rc = aegist_rope_inv_freq(fpp.inv, RD, theta);
+        if (rc) return rc;
+        fused = &fpp;
+    } else {
+        int rc = launch_attn_prep(qg, k_new, v_new, in_dtype, q_norm_w, k_norm_w, qn, kc, vc, B, 1, H, KV, HD, RD, pos,
+                                  cap, eps, theta, st);
+        if (rc) return rc;
+    }
     const float scale = 1.0f / sqrtf((float)HD);
     // gate = second half of each head's 2*HD row of qg
     if (in_dtype == AEGIST_F32) {
         const float* gate = (const float*)qg + HD;
         if (out_dtype == AEGIST_F32)
             return launch_decode_core<float, float>(qn, kc, vc, gate, 2 * HD, (float*)out, HD, B, H, KV, pos + 1, cap,
-                                                    scale, workspace, core, st);
+                                                    scale, workspace, core, st, {}, fused, in_dtype);
         if (out_dtype == AEGIST_BF16)
             return launch_decode_core<float, uint16_t>(qn, kc, vc, gate, 2 * HD, (uint16_t*)out, HD, B, H, KV, pos + 1,
-                                                       cap, scale, workspace, core, st);
+                                                       cap, scale, workspace, core, st, {}, fused, in_dtype);
     } else if (in_dtype == AEGIST_BF16) {
         const uint16_t* gate = (const uint16_t*)qg + HD;
         if (out_dtype == AEGIST_F32)
             return launch_decode_core<uint16_t, float>(qn, kc, vc, gate, 2 * HD, (float*)out, HD, B, H, KV, pos + 1,
-                                                       cap, scale, workspace, core, st);
+                                                       cap, scale, workspace, core, st, {}, fused, in_dtype);
         if (out_dtype == AEGIST_BF16)
             return launch_decode_core<uint16_t, uint16_t>(qn, kc, vc, gate, 2 * HD, (uint16_t*)out, HD, B, H, KV,
-                                                          pos + 1, cap, scale, workspace, core, st);
+                                                          pos + 1, cap, scale, workspace, core, st, {}, fused, in_dtype);
     }
     return fail(AEGIST_ERR_DTYPE, "attention_decode: dtypes must be AEGIST_F32 or AEGIST_BF16");
 }

@@ -252,6 +252,89 @@ def bench_prefill(torch, ops, dev, reps=40):
 ATTN_H, ATTN_KV, ATTN_HD, ATTN_RD, ATTN_THETA = 16, 2, 256, 64, 1e7
 
 
+def attn_decode_bytes(Bt, L):
+    """Algorithmic bytes of one gated attention decode call over L cached rows (+ the new one):
+    bf16 K and V rows read, q and gate in, new k / v in and appended, output out."""
+    return 2048 * Bt * (L + 1) + Bt * ATTN_H * ATTN_HD * 2 * 3 + Bt * ATTN_KV * ATTN_HD * 2 * 2
+
+
+def bench_decode_step(torch, ops, dev, L=4096, reps=10):
+    """The north-star decode step at batch 64: the 30 DeltaNet layers (config 1's fused decode
+    launch, each on its own state) and the 10 gated-attention layers (config 3's decode at
+    L = 4096, each on its own K / V cache), interleaved 3 : 1 as in the stack, inputs resident
+    in HBM. Roofline: the sum of both kinds' algorithmic bytes over the step time."""
+    from aegist_mixer._lib import BF16, call, lib
+    bf = torch.bfloat16
+    stream = torch.cuda.current_stream().cuda_stream
+    delta, attn = [], []
+    for l in range(LAYERS):
+        st = ops.fill_normal(torch.empty(B, HV, D, D, device=dev), 1000 + l, 0.0, 0.02)
+        qkv = ops.fill_normal(torch.empty(B, C, device=dev, dtype=bf), 2000 + l)
+        cs = ops.fill_normal(torch.empty(B, C, 3, device=dev), 3000 + l)
+        w = ops.fill_normal(torch.empty(C, 4, device=dev, dtype=bf), 4000 + l, 0.0, 0.05)
+        g = -torch.nn.functional.softplus(ops.fill_normal(torch.empty(B, HV, device=dev), 5000 + l))
+        beta = torch.sigmoid(ops.fill_normal(torch.empty(B, HV, device=dev), 6000 + l))
+        delta.append((qkv, w, cs, g, beta, st, torch.empty(B, HV, D, device=dev, dtype=bf)))
+    cap = L + 1
+    nbytes = lib().aegist_attention_decode_workspace_bytes(B, ATTN_H, ATTN_KV, cap)
+    ws = torch.empty(nbytes, device=dev, dtype=torch.uint8)
+    for l in range(LAYERS // 3):
+        kc = ops.fill_normal(torch.empty(B, ATTN_KV, cap, ATTN_HD, device=dev, dtype=bf), 8001 + 10 * l)
+        vc = ops.fill_normal(torch.empty(B, ATTN_KV, cap, ATTN_HD, device=dev, dtype=bf), 8002 + 10 * l)
+        qg = ops.fill_normal(torch.empty(B, ATTN_H, 2 * ATTN_HD, device=dev, dtype=bf), 8003 + 10 * l)
+        kn = ops.fill_normal(torch.empty(B, ATTN_KV, ATTN_HD, device=dev, dtype=bf), 8004 + 10 * l)
+        vn = ops.fill_normal(torch.empty(B, ATTN_KV, ATTN_HD, device=dev, dtype=bf), 8005 + 10 * l)
+        nw = ops.fill_normal(torch.empty(2, ATTN_HD, device=dev, dtype=bf), 8006 + 10 * l, 0.0, 0.1)
+        attn.append((qg, kn, vn, nw, kc, vc, torch.empty(B, ATTN_H, ATTN_HD, device=dev, dtype=bf)))
+    torch.cuda.synchronize()
+
+    def run_delta(t):
+        qkv, w, cs, g, beta, st, out = t
+        call("aegist_delta_decode_step", qkv.data_ptr(), BF16, w.data_ptr(), cs.data_ptr(), g.data_ptr(),
+             beta.data_ptr(), st.data_ptr(), out.data_ptr(), BF16, B, HK, HV, D ** -0.5, 1e-6, stream)
+
+    def run_attn(t):
+        qg, kn, vn, nw, kc, vc, o = t
+        # position L: the new row is written at L (the same slot every step) and attended with the L before it
+        call("aegist_attention_decode", qg.data_ptr(), kn.data_ptr(), vn.data_ptr(), BF16, nw[0].data_ptr(),
+             nw[1].data_ptr(), kc.data_ptr(), vc.data_ptr(), o.data_ptr(), BF16, B, ATTN_H, ATTN_KV, ATTN_HD,
+             ATTN_RD, L, cap, 1e-6, ATTN_THETA, ws.data_ptr(), nbytes, stream)
+
+    def step():
+        for l in range(LAYERS // 3):
+            for j in range(3):
+                run_delta(delta[3 * l + j])
+            run_attn(attn[l])
+
+    def timed(fn, n):
+        for _ in range(2):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(n):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / n
+    ms = timed(step, reps)
+    ms_attn = timed(lambda: [run_attn(t) for t in attn], reps)
+    byt_d = LAYERS * decode_bytes_per_launch()
+    byt_a = (LAYERS // 3) * attn_decode_bytes(B, L)
+    gbs = (byt_d + byt_a) / (ms * 1e-3) / 1e9
+    a_gbs = byt_a / (ms_attn * 1e-3) / 1e9
+    del delta, attn, ws
+    torch.cuda.empty_cache()
+    return {"workload": f"batch-{B} decode step: 30 DeltaNet layers (config 1) + 10 gated GQA layers "
+                        f"(16 q / 2 KV heads, HD 256, L={L} cached rows each, distinct caches)",
+            "ms_per_step": round(ms, 4), "tok_s": round(B / (ms * 1e-3), 1),
+            "bytes_per_step": byt_d + byt_a,
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(gbs / HBM_PEAK_GBS, 4)},
+            "attention_only": {"ms_10_layers": round(ms_attn, 4), "GB_s": round(a_gbs, 1),
+                               "hbm_frac": round(a_gbs / HBM_PEAK_GBS, 4)}}
+
+
 def bench_attention_decode(torch, ops, dev, reps=20):
     """Config 3: gated GQA decode (ZNorm + RoPE of q and the new k, cache append, split-K
     attention over L+1 rows, sigmoid gate) at L in {4k, 32k, 128k} x B in {1, 8, 32}.
@@ -288,7 +371,7 @@ def bench_attention_decode(torch, ops, dev, reps=20):
             e1.record()
             torch.cuda.synchronize()
             us = e0.elapsed_time(e1) * 1e3 / reps
-            byt = 2048 * Bt * (L + 1) + Bt * ATTN_H * ATTN_HD * 2 * 3 + Bt * ATTN_KV * ATTN_HD * 2 * 2
+            byt = attn_decode_bytes(Bt, L)
             gbs = byt / (us * 1e-6) / 1e9
             out.append({"L": L, "B": Bt, "us": round(us, 2), "tok_s": round(Bt / (us * 1e-6), 1),
                         "GB_s": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)})
@@ -644,7 +727,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run a 1 GiB device copy (calibrates rocprof FETCH_SIZE / WRITE_SIZE)")
-    ap.add_argument("--legs", type=str, default="prefill,attention_decode,attention_prefill,gemm,proj,qsa,moe,stack",
+    ap.add_argument("--legs", type=str, default="prefill,decode_step,attention_decode,attention_prefill,gemm,proj,qsa,moe,stack",
                     help="comma list of the extra legs to run after the decode headline (default: all); "
                          "'none' for the headline only")
     ap.add_argument("--traffic", type=str, default=str(ROOT / "profiles" / "delta_decode_traffic.json"),
@@ -728,7 +811,7 @@ def main():
     if args.traffic and os.path.exists(args.traffic):
         with open(args.traffic) as f:
             res["roofline"]["traffic"] = json.load(f).get("bytes_per_launch")
-    legs = {"prefill": bench_prefill, "attention_decode": bench_attention_decode,
+    legs = {"prefill": bench_prefill, "decode_step": bench_decode_step, "attention_decode": bench_attention_decode,
             "attention_prefill": bench_attention_prefill, "proj": bench_proj, "qsa": bench_qsa,
             "moe": bench_moe, "stack": bench_stack, "gemm": bench_gemm}
     want = [] if args.legs.strip() == "none" else [x.strip() for x in args.legs.split(",") if x.strip()]

@@ -130,6 +130,35 @@ def test_engine_attention_pipeline(dev):
     assert rel_err(torch.cat(outs, 0), ref) < ATTN_TOL
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("B,L", [(3, 0), (3, 37), (2, 4096), (1, 4159)])
+def test_attention_decode_fused_prep(dev, B, L, dtype):
+    """The decode launch that does its own prep (rotary dim 64): the rows it appends equal the
+    separate prep kernel's bit for bit, and the cache's old contents at row L and past it never
+    reach the output (they are set to NaN first; the last split stages the new row in their place).
+    L = 0 has no cached rows at all; 37 and 4159 put row L mid-tile of the last split."""
+    print(f"attention_decode fused prep B={B} L={L} {dtype}", flush=True)
+    H, KV, cap = 16, 2, L + 8
+    qg, kn, vn, qw, kw, kc, vc = decode_case(B, H, KV, L, cap, 300 + L, dtype)
+    kc[:, :, L:] = float("nan")
+    vc[:, :, L:] = float("nan")
+    ref = R.attention_decode(qg.float(), kn.float(), vn.float(), qw.float(), kw.float(), kc.clone(), vc.clone(), L, RD,
+                             THETA)
+    kc_d, vc_d = kc.to(dev), vc.to(dev)
+    out = ops.attention_decode(qg.to(dev), kn.to(dev), vn.to(dev), qw.to(dev), kw.to(dev), kc_d, vc_d, L, RD, THETA)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+    assert rel_err(out, ref) < ATTN_TOL
+    for b in range(B):
+        kp = kc[b].clone().to(dev)
+        vp = vc[b].clone().to(dev)
+        ops.engine_attn_prep(qg[b:b + 1].float().to(dev), kn[b:b + 1].float().to(dev), vn[b:b + 1].float().to(dev),
+                             qw.to(dev), kw.to(dev), kp, vp, L, RD, THETA)
+        torch.cuda.synchronize()
+        assert torch.equal(kc_d[b, :, L].view(torch.int16), kp[:, L].view(torch.int16)), b
+        assert torch.equal(vc_d[b, :, L].view(torch.int16), vp[:, L].view(torch.int16)), b
+
+
 @pytest.mark.slow
 @pytest.mark.parametrize("B,L", [(8, 32768), (32, 32768), (8, 131072), (32, 131072), (64, 32768)])
 def test_attention_decode_config3_points(dev, B, L):
