@@ -374,21 +374,28 @@ __device__ __forceinline__ void prep_b(Smem<kLo>& sm, int buf, const Conv<kLo>& 
 #pragma unroll
     for (int jt = 0; jt < 4; jt++) {
         if (jt > wv && (!kQ || jt > iq)) continue;
+        // fp32 inputs: the k rows of tile jt are re-read per product (registers for the lo parts)
         half8 ka[4], kal[4];
+        if constexpr (!kLo) {
 #pragma unroll
-        for (int ks = 0; ks < 4; ks++) {
-            ka[ks] = *(const half8*)&sm.K[buf][16 * jt + n][32 * ks + 8 * g];
-            if constexpr (kLo) kal[ks] = *(const half8*)&sm.KL[buf][16 * jt + n][32 * ks + 8 * g];
+            for (int ks = 0; ks < 4; ks++) ka[ks] = *(const half8*)&sm.K[buf][16 * jt + n][32 * ks + 8 * g];
         }
+        auto kat = [&](int ks) -> half8 {
+            if constexpr (kLo) return *(const half8*)&sm.K[buf][16 * jt + n][32 * ks + 8 * g];
+            else return ka[ks];
+        };
+        auto kalt = [&](int ks) -> half8 { return *(const half8*)&sm.KL[buf][16 * jt + n][32 * ks + 8 * g]; };
+        (void)kal;
         const f32x4 mkj = *(const f32x4*)&F.mk[16 * jt + 4 * g];
         if (jt <= wv) {
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int ks = 0; ks < 4; ks++) {
-                acc = mfma32(ka[ks], kb[ks], acc);
+                const half8 a = kat(ks);
+                acc = mfma32(a, kb[ks], acc);
                 if constexpr (kLo) {
-                    acc = mfma32(ka[ks], kbl[ks], acc);
-                    acc = mfma32(kal[ks], kb[ks], acc);
+                    acc = mfma32(a, kbl[ks], acc);
+                    acc = mfma32(kalt(ks), kb[ks], acc);
                 }
             }
             f32x4 av;
@@ -427,10 +434,11 @@ __device__ __forceinline__ void prep_b(Smem<kLo>& sm, int buf, const Conv<kLo>& 
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int ks = 0; ks < 4; ks++) {
-                acc = mfma32(ka[ks], cv.q[ks], acc);
+                const half8 a = kat(ks);
+                acc = mfma32(a, cv.q[ks], acc);
                 if constexpr (kLo) {
-                    acc = mfma32(ka[ks], cv.ql[ks], acc);
-                    acc = mfma32(kal[ks], cv.q[ks], acc);
+                    acc = mfma32(a, cv.ql[ks], acc);
+                    acc = mfma32(kalt(ks), cv.q[ks], acc);
                 }
             }
             f32x4 iv;
@@ -885,10 +893,16 @@ __device__ __forceinline__ void prep_body(const Params& p, Smem<sizeof(Tin) == 4
         // ---- phase 1: chunk c's A / D / intra into LDS; prep A of chunk c + 1
         write_deferred<kLo, kQ>(sm, df, wave, n, g);
         prep_a<Tin, kLo, kQ>(p, sm, nb, raw, gb, wave, n, g, lane, cv);
-        load_chunk<Tin, kQ>(p, rs, c + 2, wave, n, g, lane, raw, gb);
+        // fp32 inputs: chunk c + 2's rows are requested after prep B instead, so their 96
+        // registers are not live across it
+        if constexpr (!kLo) load_chunk<Tin, kQ>(p, rs, c + 2, wave, n, g, lane, raw, gb);
         lds_barrier();
         // ---- phase 2: prep B of chunk c + 1 (Q and V are rewritten: the chain read them in phase 1)
         prep_b<kLo, kQ>(sm, nb, cv, wave, n, g, df);
+        if constexpr (kLo) {
+            __builtin_amdgcn_sched_barrier(0);  // the loads stay below prep B
+            load_chunk<Tin, kQ>(p, rs, c + 2, wave, n, g, lane, raw, gb);
+        }
         lds_barrier();
     }
 }
