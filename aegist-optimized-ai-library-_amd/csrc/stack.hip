@@ -8,11 +8,9 @@
 //
 // Projections are plain GEMMs (bf16 operands, fp32 accumulation and output; the out-projections
 // accumulate straight into the fp32 residual): decode-sized ones on this library's
-// weight-streaming MFMA kernel, prefill-sized ones on rocBLAS; every other op is one of this
-// library's kernels.
+// weight-streaming MFMA kernel, prefill-sized ones on its tiled MFMA GEMM; every op is one of
+// this library's kernels (no vendor BLAS).
 #include "common.h"
-
-#include <rocblas/rocblas.h>
 
 #include <algorithm>
 #include <vector>
@@ -71,7 +69,6 @@ struct Stack {
     std::vector<AegistLayerWeights> w;
     std::vector<int> slot;  // per layer: index among its kind
     int n_delta = 0, n_attn = 0, length = 0, device = 0;
-    rocblas_handle blas = nullptr;
     // states
     float* conv = nullptr;     // [n_delta, maxB, C, 3]
     float* rec = nullptr;      // [n_delta, maxB, HV, 128, 128]
@@ -110,37 +107,18 @@ int alloc(Stack* s, void** p, size_t bytes) {
     return rc;
 }
 
-// Prefill-sized GEMMs go to rocBLAS unless AEGIST_GEMM_OWN=1 selects this library's tiled MFMA
-// GEMM (at config 4's shapes it reaches 75-85% of rocBLAS's rate: 16 x 2048 prefill 159 against
-// 151 ms)
-bool gemm_rocblas() {
-    static const bool on = [] {
-        const char* e = getenv("AEGIST_GEMM_OWN");
-        return !(e && e[0] == '1');
-    }();
-    return on;
-}
-
 // Y[M, N] (row-major, leading dim ldy) = A[M, K] (bf16 row-major) . W[N, K]^T (bf16 row-major)
 //                                          + beta * Y,   beta in {0, 1}
 // Decode-sized M (<= 64 rows) goes to the weight-streaming kernels (one pass over W), larger M
-// to rocBLAS, or to the tiled MFMA GEMM on request.
-int gemm(Stack* s, const uint16_t* A, const uint16_t* W, float* Y, int M, int N, int K, int ldy, float beta,
+// to the tiled MFMA GEMM; shapes the GEMM does not take (K not a multiple of its k step) to the
+// streaming kernels' row-group form.
+int gemm(Stack*, const uint16_t* A, const uint16_t* W, float* Y, int M, int N, int K, int ldy, float beta,
          hipStream_t stream) {
-    if (M <= 64 && K % 16 == 0)
-        return launch_proj(A, AEGIST_BF16, K, W, AEGIST_BF16, nullptr, Y, ldy, M, N, K, beta != 0.f, stream);
-    if (!gemm_rocblas() && gemm_bf16_fits(A, K, W, K, M, N, K))
+    if (M > 64 && gemm_bf16_fits(A, K, W, K, M, N, K))
         return launch_gemm_bf16(A, K, W, K, Y, ldy, M, N, K, beta != 0.f, stream);
-    if (rocblas_set_stream(s->blas, stream) != rocblas_status_success)
-        return fail(AEGIST_ERR_SHAPE, "rocblas_set_stream failed");
-    const float alpha = 1.f;
-    rocblas_status st = rocblas_gemm_ex(s->blas, rocblas_operation_transpose, rocblas_operation_none, N, M, K, &alpha, W,
-                                        rocblas_datatype_bf16_r, K, A, rocblas_datatype_bf16_r, K, &beta, Y,
-                                        rocblas_datatype_f32_r, ldy, Y, rocblas_datatype_f32_r, ldy,
-                                        rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0);
-    if (st != rocblas_status_success)
-        return fail(AEGIST_ERR_SHAPE, std::string("rocblas_gemm_ex: ") + rocblas_status_to_string(st));
-    return after_launch("projection gemm");
+    if (K % 16 == 0)
+        return launch_proj(A, AEGIST_BF16, K, W, AEGIST_BF16, nullptr, Y, ldy, M, N, K, beta != 0.f, stream);
+    return fail(AEGIST_ERR_SHAPE, "stack: projection K must be a multiple of 16");
 }
 
 // Out projection x += A W^T. At decode sizes (M <= 16) it runs as kOutSplits slices of K whose
@@ -269,8 +247,6 @@ int aegist_stack_create(const AegistStackConfig* cfg, void** handle) {
     s->slot.resize(c.n_layers);
     for (int l = 0; l < c.n_layers; l++) s->slot[l] = c.layer_is_attn[l] ? s->n_attn++ : s->n_delta++;
     int rc = check_hip(hipGetDevice(&s->device), "hipGetDevice");
-    if (!rc && rocblas_create_handle(&s->blas) != rocblas_status_success)
-        rc = fail(AEGIST_ERR_SHAPE, "rocblas_create_handle failed");
     const size_t rows = c.max_tokens, C = s->C(), mb = c.max_batch;
     const int H = c.n_heads, KV = c.n_kv, HD = c.head_dim, HV = c.hv;
     const size_t wide = std::max<size_t>((size_t)HV * D, (size_t)H * HD);
@@ -316,7 +292,6 @@ int aegist_stack_destroy(void* handle) {
     if (!s) return 0;
     (void)hipDeviceSynchronize();
     for (void* p : s->allocs) (void)hipFree(p);
-    if (s->blas) rocblas_destroy_handle(s->blas);
     delete s;
     return 0;
 }
@@ -482,7 +457,6 @@ int aegist_stack_forward(void* handle, float* x, int B, int T, void* stream) {
     for (int l = 0; l < c.n_layers; l++)
         if (!s->w[l].norm1) return fail(AEGIST_ERR_SHAPE, "stack_forward: layer " + std::to_string(l) + " has no weights");
     hipStream_t st = AEG_STREAM(stream);
-    if (rocblas_set_stream(s->blas, st) != rocblas_status_success) return fail(AEGIST_ERR_SHAPE, "rocblas_set_stream");
     const int rows = B * T;
     s->pend = 0;
     for (int l = 0; l < c.n_layers; l++) {

@@ -683,7 +683,7 @@ def bench_stack(torch, ops, dev, B=16, T=2048, steps=256):
     stack = ops.HybridStack(cfg, kinds, layers, max_batch=B, max_tokens=B * T, max_context=T + steps)
     ids = torch.randint(0, 4096, (B, T + steps), generator=torch.Generator().manual_seed(5), dtype=torch.int32).to(dev)
     e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
-    # warm-up pass (also builds rocBLAS kernels), then the timed run from a reset state
+    # warm-up pass, then the timed run from a reset state
     x = ops.embed(table, ids[:, :T].reshape(-1)).view(B, T, 2048)
     stack.forward(x)
     stack.reset()

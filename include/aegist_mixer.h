@@ -240,8 +240,8 @@ int aegist_attention_core(const float* q, const uint16_t* kc, const uint16_t* vc
  * aegist_rs/src/hybrid.rs:760-861). The stack owns every layer's recurrent state, conv state
  * and bf16 KV cache (HybridCache, hybrid.py:171-260; engine buffers hybrid.rs:607-629); all
  * sequences of a batch share one length. Projections: bf16 operands, fp32 accumulation; up to
- * 64 rows on this library's weight-streaming kernel (aegist_linear), more on rocBLAS; everything
- * else on this library's kernels. Weights are caller-owned bf16,
+ * 64 rows on this library's weight-streaming kernel (aegist_linear), more on its tiled MFMA
+ * GEMM; every op runs on this library's kernels. Weights are caller-owned bf16,
  * row-major [out, in] as torch nn.Linear stores them.
  * ------------------------------------------------------------------------------------- */
 #define AEGIST_MAX_LAYERS 64
