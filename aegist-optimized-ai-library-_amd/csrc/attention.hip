@@ -1736,6 +1736,17 @@ int stack_attn_decode(const float* qn, const uint16_t* kc, const uint16_t* vc, c
     return launch_decode_core<float, uint16_t>(qn, kc, vc, qg + HD, 2 * HD, out, HD, B, H, KV, L, cap, scale, ws,
                                                ws_bytes, st);
 }
+// The stack's decode with the prep folded into the split launch (fp32 projections: qg [B, H, 2 HD],
+// k / v [B, KV, HD]; rotary dim 64): appends row pos and writes the gated output as bf16.
+int stack_attn_decode_fused(const float* qg, const float* kn, const float* vn, const uint16_t* qw, const uint16_t* kw,
+                            uint16_t* kc, uint16_t* vc, uint16_t* out, int B, int H, int KV, int pos, int cap, float eps,
+                            float theta, void* ws, size_t ws_bytes, hipStream_t st) {
+    FusedPrep fp{qg, kn, vn, qw, kw, kc, vc, pos, eps, {}};
+    int rc = aegist_rope_inv_freq(fp.inv, kFusedRD, theta);
+    if (rc) return rc;
+    return launch_decode_core<float, uint16_t>(nullptr, kc, vc, qg + HD, 2 * HD, out, HD, B, H, KV, pos + 1, cap,
+                                               1.0f / sqrtf((float)HD), ws, ws_bytes, st, {}, &fp, AEGIST_F32);
+}
 int stack_attn_prefill(const float* qn, const uint16_t* kc, const uint16_t* vc, const float* qg, float* out, int B,
                        int H, int KV, int T, int pos, int cap, float scale, void* ws, size_t ws_bytes, hipStream_t st,
                        uint16_t* out_bf16, bool* wrote_bf16) {

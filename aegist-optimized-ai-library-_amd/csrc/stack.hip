@@ -38,6 +38,9 @@ int launch_attn_prep(const void* qg, const void* k, const void* v, int in_dtype,
                      int RD, int pos0, int cap, float eps, float theta, hipStream_t stream);
 int stack_attn_decode(const float* qn, const uint16_t* kc, const uint16_t* vc, const float* qg, uint16_t* out, int B,
                       int H, int KV, int L, int cap, float scale, void* ws, size_t ws_bytes, hipStream_t st);
+int stack_attn_decode_fused(const float* qg, const float* kn, const float* vn, const uint16_t* qw, const uint16_t* kw,
+                            uint16_t* kc, uint16_t* vc, uint16_t* out, int B, int H, int KV, int pos, int cap, float eps,
+                            float theta, void* ws, size_t ws_bytes, hipStream_t st);
 int stack_attn_prefill(const float* qn, const uint16_t* kc, const uint16_t* vc, const float* qg, float* out, int B,
                        int H, int KV, int T, int pos, int cap, float scale, void* ws, size_t ws_bytes, hipStream_t st,
                        uint16_t* out_bf16, bool* wrote_bf16);
@@ -208,6 +211,12 @@ int attn_layer(Stack* s, const AegistLayerWeights& w, int sl, float* x, int B, i
         const int N[3] = {2 * H * HD, KV * HD, KV * HD};
         const long long ldy[3] = {2 * H * HD, KV * HD, KV * HD};
         RC(gemm_group(s, s->hb, 3, W, Y, N, ldy, rows, dm, st));
+    }
+    if (T == 1 && c.rotary_dim == 64) {
+        // decode: ZNorm, RoPE and the cache append inside the split launch
+        RC(stack_attn_decode_fused(s->proj, kp, vp, w.q_norm, w.k_norm, kc, vc, s->ob, B, H, KV, s->length, (int)cap,
+                                   c.eps, c.rope_theta, s->ws, s->ws_bytes, st));
+        return out_proj(s, s->ob, w.w_o, x, rows, dm, H * HD, st);
     }
     RC(launch_attn_prep(s->proj, kp, vp, AEGIST_F32, w.q_norm, w.k_norm, s->y, kc, vc, B, T, H, KV, HD, c.rotary_dim,
                         s->length, (int)cap, c.eps, c.rope_theta, st));
