@@ -46,11 +46,12 @@ _ws_cache: dict[tuple, torch.Tensor] = {}
 
 
 def _workspace(nbytes: int, device) -> torch.Tensor:
-    """Workspace tensor of at least nbytes (kept per device, grown on demand). The library
-    never allocates: this caller-side buffer is what the *_ws entry points receive. Reuse is
-    ordered on the current stream; a replaced buffer is released through torch's
-    stream-ordered caching allocator."""
-    key = (str(device),)
+    """Workspace tensor of at least nbytes (kept per device and stream, grown on demand). The
+    library never allocates: this caller-side buffer is what the *_ws entry points receive.
+    One buffer per (device, current stream), so calls on different streams never share scratch
+    bytes, and reuse on one stream is ordered by that stream; a replaced buffer is released
+    through torch's stream-ordered caching allocator."""
+    key = (str(device), torch.cuda.current_stream(device).cuda_stream)
     ws = _ws_cache.get(key)
     if ws is None or ws.numel() < nbytes:
         ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)

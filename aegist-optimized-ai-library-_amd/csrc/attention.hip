@@ -25,6 +25,7 @@
 #include <cstdlib>
 #include <type_traits>
 #include <algorithm>
+#include <atomic>
 #include <mutex>
 #include <string>
 
@@ -705,14 +706,21 @@ typedef short short4v __attribute__((ext_vector_type(4)));
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));  // (HIP's uint4 blocks register promotion)
 
 // 8 bf16 (one 16-byte chunk of a cache row) -> 8 fp16, exact for |x| in fp16's normal range
-// (bf16's 8-bit significand fits fp16's 11); the prefill kernel stages K and V tiles as fp16
+// (bf16's 8-bit significand fits fp16's 11); the prefill kernel stages K and V tiles as fp16.
+// Values beyond fp16's largest finite 65504 saturate to +-65504 (the output stays finite; bf16
+// cache values that large differ from the reference by the clamp); below its normal range they
+// round to fp16 subnormals.
 __device__ __forceinline__ u32x4 bf8_to_f16(u32x4 x) {
     typedef float f2 __attribute__((ext_vector_type(2)));
     typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    constexpr float kMax = 65504.f;
     u32x4 r;
 #pragma unroll
-    for (int i = 0; i < 4; i++)
-        r[i] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f2{bf_lo(x[i]), bf_hi(x[i])}), h2));
+    for (int i = 0; i < 4; i++) {
+        const float a = __builtin_amdgcn_fmed3f(bf_lo(x[i]), -kMax, kMax);
+        const float b = __builtin_amdgcn_fmed3f(bf_hi(x[i]), -kMax, kMax);
+        r[i] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f2{a, b}), h2));
+    }
     return r;
 }
 
@@ -1654,15 +1662,15 @@ int launch_decode_core(const float* q, const uint16_t* kc, const uint16_t* vc, c
 
 // compute units of the current device (cached per device; the persistent prefill grid)
 static int device_cus() {
-    static int cus[64] = {};
+    static std::atomic<int> cus[64];  // per device; racing first calls store the same value
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    if (!cus[dev]) {
-        int c = 0;
+    int c = cus[dev].load(std::memory_order_relaxed);
+    if (c <= 0) {
         if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0) c = 256;
-        cus[dev] = c;
+        cus[dev].store(c, std::memory_order_relaxed);
     }
-    return cus[dev];
+    return c;
 }
 
 // bytes of the fp16 K / V copies the prefill kernel reads when given that much workspace

@@ -228,7 +228,8 @@ int aegist_attention_decode_noalloc(const void* qg, const void* k_new, const voi
  * workspace is optional: with aegist_attention_core_workspace_bytes(B, H, KV, T, pos) bytes
  * (256-byte aligned) the cache rows are converted to fp16 once into it and the kernel loads
  * them straight into LDS; with less (or NULL) each workgroup converts the tiles it stages.
- * Both give the same results (the conversion is exact). */
+ * Both give the same results (the same fp16 conversion: exact for bf16 values within fp16's
+ * range; values beyond +-65504 saturate there, where the reference would keep them). */
 size_t aegist_attention_core_workspace_bytes(int B, int H, int KV, int T, int pos);
 int aegist_attention_core(const float* q, const uint16_t* kc, const uint16_t* vc, const float* gate, float* out,
                           int B, int H, int KV, int T, int pos, int cap, float scale, void* workspace,

@@ -60,6 +60,24 @@ def test_attention_decode_long(dev, B, L):
     assert rel_err(out, ref) < ATTN_TOL
 
 
+def test_attention_prefill_saturates_beyond_fp16(dev):
+    """The prefill stages K / V as fp16: cache values beyond +-65504 saturate there (a V column
+    around 1e5 gives a finite output equal to the reference on the clamped cache), where a plain
+    conversion would make them infinite and the output NaN."""
+    B, H, KV, T, pos = 1, 8, 2, 150, 10
+    g_ = _gen(77)
+    q = torch.randn(B, H, T, HD, generator=g_) * 0.5
+    kc = torch.randn(B, KV, pos + T, HD, generator=g_).to(torch.bfloat16)
+    vc = torch.randn(B, KV, pos + T, HD, generator=g_)
+    vc[..., 5] = 1e5 * torch.sign(vc[..., 5])
+    vc = vc.to(torch.bfloat16)
+    out = ops.attention_core(q.to(dev), kc.to(dev), vc.to(dev), None, pos)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+    ref = R.attention_core(q, kc, vc.float().clamp(-65504, 65504).to(torch.bfloat16), pos, KV).transpose(1, 2)
+    assert rel_err(out, ref) < ATTN_TOL
+
+
 def test_attention_decode_bf16_out(dev):
     qg, kn, vn, qw, kw, kc, vc = decode_case(2, 16, 2, 500, 505, seed=9)
     ref = R.attention_decode(qg.float(), kn.float(), vn.float(), qw.float(), kw.float(), kc.clone(), vc.clone(),
@@ -79,7 +97,10 @@ def test_attention_decode_bf16_out(dev):
                                                 (4, 16, 2, 300, 0, 0.5, 1), (8, 8, 2, 256, 20, 0.5, 1),
                                                 # sharp softmax (scores ~ +-30) and large / small V
                                                 (1, 16, 2, 260, 0, 3.0, 1), (1, 8, 2, 200, 40, 0.5, 300),
-                                                (1, 8, 2, 200, 40, 0.5, 1e-3)])
+                                                (1, 8, 2, 200, 40, 0.5, 1e-3),
+                                                # 128 (sequence, KV head) pairs and 9 query blocks
+                                                # each: several rounds per workgroup
+                                                (8, 16, 2, 1100, 64, 0.5, 1)])
 def test_attention_core_prefill(dev, B, H, KV, T, pos, qs, vs):
     """The MFMA prefill takes K / V as fp16 (exact for bf16 values in fp16's range; converted once
     into the workspace, or per tile without it) and q and P as fp16: ~11 significant bits against

@@ -95,3 +95,30 @@ def test_gemm_i8_matches_oracle(dev, M, N, K, acc):
     err = rel_err(yd, ref)
     print(f"  rel err {err:.2e}", flush=True)
     assert err < 2e-5
+
+
+def test_gemm_i8_hi_lo_bound(dev):
+    """gemm_i8 past 64 rows splits each fp32 X value into bf16 hi + lo (|x - hi - lo| <=
+    2^-16 |x|), so each output is within 2^-16 sum_k |x_k w_k s| (plus fp32 accumulation) of the
+    exact dot product; checked with X around 1e3 of mixed signs, where the lo term carries bits
+    that bf16 alone would drop. (The engine kernel sums in plain fp32: results are not
+    bit-compatible with it, only within this bound.)"""
+    M, N, K = 96, 512, 2048
+    g = torch.Generator().manual_seed(5)
+    q, sc = R.qlinear_quantize(torch.randn(N, K, generator=g) * 0.02)
+    x = torch.randn(M, K, generator=g) * 1e3
+    yd = torch.empty(M, N, device=dev)
+    xd, qd, sd = x.to(dev), q.to(dev), sc.to(dev)
+    call("aegist_gemm_i8", xd.data_ptr(), qd.data_ptr(), sd.data_ptr(), yd.data_ptr(), M, N, K, 0,
+         torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    w = q.double() * sc.double()[:, None]
+    exact = x.double() @ w.t()
+    mag = x.double().abs() @ w.abs().t()
+    bound = (2.0 ** -16 + K * 2.0 ** -24) * mag
+    diff = (yd.double().cpu() - exact).abs()
+    print(f"  max diff / bound {(diff / bound).max().item():.3f}", flush=True)
+    assert (diff <= bound).all()
+    # a bf16-only X would miss the bound: the lo term is doing work here
+    xb = x.to(torch.bfloat16).double()
+    assert ((xb @ w.t() - exact).abs() > bound).any()
