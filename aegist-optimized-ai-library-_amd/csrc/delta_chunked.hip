@@ -69,7 +69,7 @@ struct SeqLayout {
 // intra_ij = 2^(lq_i - mk_j) (q k^T)_ij take one exponential per element:
 // la = cum log2(e) + log2(beta rk), lq = cum log2(e) + log2(rq), mk = cum log2(e) - log2(rk).
 struct Fact {
-    float la[CH], lq[CH], mk[CH], beta[CH], fx[CH], fp[CH];
+    float la[CH], mk[CH], beta[CH], fx[CH], fp[CH];
     float gam;
     float pad[3];
 };
@@ -226,27 +226,29 @@ __device__ __forceinline__ Rsrc make_rsrc(const Params& p, int b, int hv) {
     return r;
 }
 
-// Issue the global loads of chunk c (tokens past T read as zeros).
-template <typename Tin, bool kQ>
+// Issue the global loads of chunk c (tokens past T read as zeros): kParts 1 = the k rows, g and
+// beta (prep A's inputs), 2 = the q and v rows (prep B's), 3 = both.
+template <typename Tin, bool kQ, int kParts = 3>
 __device__ __forceinline__ void load_chunk(const Params& p, const Rsrc& rs, int c, int wave, int n, int g, int lane,
                                            Raw<Tin>& r, RawGB& gb) {
     const int tk = c * CH + 16 * wave + n, tq = c * CH + 16 * (3 - wave) + n;
     const int sz = (int)sizeof(Tin);
-    load_rows(rs.k, tk * (int)p.a.st_qk * sz, g, r.k);
-    if constexpr (kQ) load_rows(rs.q, tq * (int)p.a.st_qk * sz, g, r.q);
-    load_rows(rs.v, tk * (int)p.a.st_v * sz, g, r.v);
-    const int go = (c * CH + lane) * (int)p.a.st_g * 4;
-    gb.g = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs.g, go, 0, 0));
-    gb.beta = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs.beta, go, 0, 0));
+    if constexpr (kParts & 1) {
+        load_rows(rs.k, tk * (int)p.a.st_qk * sz, g, r.k);
+        const int go = (c * CH + lane) * (int)p.a.st_g * 4;
+        gb.g = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs.g, go, 0, 0));
+        gb.beta = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs.beta, go, 0, 0));
+    }
+    if constexpr (kParts & 2) {
+        if constexpr (kQ) load_rows(rs.q, tq * (int)p.a.st_qk * sz, g, r.q);
+        load_rows(rs.v, tk * (int)p.a.st_v * sz, g, r.v);
+    }
 }
 
-// Converted rows a wave keeps between the two prep phases (lo parts: fp32 inputs only).
-template <bool kLo>
+// What prep A hands to prep B of the same chunk besides LDS: the cumulative decay at this
+// lane's q row (tile 3 - wave).
 struct Conv {
-    static constexpr int NL = kLo ? 4 : 0;
-    half8 q[4], v[4];           // natural feature order (pieces 32 ks + 8 g); k goes to LDS
-    half8 ql[NL], vl[NL];
-    float rk, rq;               // own k row (tile wave), own q row (tile 3 - wave)
+    float cum_q;
 };
 
 // Operands of chunk c that prep B computes in registers and the next period writes to LDS
@@ -283,8 +285,8 @@ __device__ __forceinline__ half8 lo8(const float* x, half8 h) {
 // per-token factors; writes K[buf] rows of token tile `wave` and this wave's entries of F[buf].
 template <typename Tin, bool kLo, bool kQ>
 __device__ __forceinline__ void prep_a(const Params& p, Smem<kLo>& sm, int buf, const Raw<Tin>& r, const RawGB& gb,
-                                       int wave, int n, int g, int lane, Conv<kLo>& cv) {
-    float ssk = 0.f, ssq = 0.f;
+                                       int wave, int n, int g, int lane, Conv& cv) {
+    float ssk = 0.f;
     half8 k8[4], kl8[4];
 #pragma unroll
     for (int ks = 0; ks < 4; ks++) {
@@ -298,27 +300,9 @@ __device__ __forceinline__ void prep_a(const Params& p, Smem<kLo>& sm, int buf, 
         }
         k8[ks] = cvt8(x);
         if constexpr (kLo) kl8[ks] = lo8(x, k8[ks]);
-        if constexpr (kQ) {
-            unpack8(r.q, ks, x);
-            if constexpr (kLo) {
-#pragma unroll
-                for (int e = 0; e < 8; e++) ssq += x[e] * x[e];
-            } else {
-                ssq = dot2sq(r.q, ks, ssq);
-            }
-            cv.q[ks] = cvt8(x);
-            if constexpr (kLo) cv.ql[ks] = lo8(x, cv.q[ks]);
-        }
-        unpack8(r.v, ks, x);
-        cv.v[ks] = cvt8(x);
-        if constexpr (kLo) cv.vl[ks] = lo8(x, cv.v[ks]);
     }
     ssk = pair_sum32(pair_sum16(ssk));
-    cv.rk = p.normalize ? rsqrtf(ssk + p.eps) : 1.f;
-    if constexpr (kQ) {
-        ssq = pair_sum32(pair_sum16(ssq));
-        cv.rq = p.normalize ? rsqrtf(ssq + p.eps) * p.qscale : 1.f;
-    }
+    const float rk = p.normalize ? rsqrtf(ssk + p.eps) : 1.f;
     // k rows of tile `wave` (natural order)
 #pragma unroll
     for (int ks = 0; ks < 4; ks++) {
@@ -336,16 +320,16 @@ __device__ __forceinline__ void prep_a(const Params& p, Smem<kLo>& sm, int buf, 
     // this wave's tokens: factors of k rows (tile wave) and q rows (tile 3 - wave)
     constexpr float kLog2e = 1.4426950408889634f;
     const int tw = 16 * wave + n, tq = 16 * (3 - wave) + n;
-    const float cum_t = __shfl(x, tw, WAVE), beta_t = __shfl(gb.beta, tw, WAVE), cum_q = __shfl(x, tq, WAVE);
+    const float cum_t = __shfl(x, tw, WAVE), beta_t = __shfl(gb.beta, tw, WAVE);
+    if constexpr (kQ) cv.cum_q = __shfl(x, tq, WAVE);
     Fact& F = sm.F[buf];
     if (g == 0) {
-        const float c2 = cum_t * kLog2e, brk = beta_t * cv.rk, lrk = __builtin_amdgcn_logf(cv.rk);
+        const float c2 = cum_t * kLog2e, brk = beta_t * rk, lrk = __builtin_amdgcn_logf(rk);
         F.la[tw] = c2 + __builtin_amdgcn_logf(brk);
         F.mk[tw] = c2 - lrk;
         F.beta[tw] = beta_t;
         F.fx[tw] = brk * __expf(cum_t);
-        F.fp[tw] = cv.rk * __expf(cl - cum_t);
-        if constexpr (kQ) F.lq[tq] = cum_q * kLog2e + __builtin_amdgcn_logf(cv.rq);
+        F.fp[tw] = rk * __expf(cl - cum_t);
     }
     if (wave == 0 && lane == 0) F.gam = __expf(cl);
 }
@@ -353,17 +337,41 @@ __device__ __forceinline__ void prep_a(const Params& p, Smem<kLo>& sm, int buf, 
 // Prep phase B for chunk c (after a barrier: K[buf] and F[buf] complete): the Gram products, -A
 // blocks, the diagonal-block inverse D_wave and intra into `df` (written to LDS by the next
 // period), and the q and v rows into Q and V.
-template <bool kLo, bool kQ>
-__device__ __forceinline__ void prep_b(Smem<kLo>& sm, int buf, const Conv<kLo>& cv, int wave, int n, int g,
-                                       Deferred& df) {
+template <typename Tin, bool kLo, bool kQ>
+__device__ __forceinline__ void prep_b(const Params& p, Smem<kLo>& sm, int buf, const Raw<Tin>& r, const Conv& cv,
+                                       int wave, int n, int g, Deferred& df) {
     const Fact& F = sm.F[buf];
     const int wv = wave;
+    // this wave's q rows (tile 3 - wave: their norm and log factor) and v rows (tile wave), fp16
+    // (+ lo parts for fp32 inputs)
+    constexpr int NL = kLo ? 4 : 1;
+    half8 cq[4], cql[NL];
+    float lq_i = 0.f;
+    if constexpr (kQ) {
+        float ssq = 0.f;
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) {
+            float x[8];
+            unpack8(r.q, ks, x);
+            if constexpr (kLo) {
+#pragma unroll
+                for (int e = 0; e < 8; e++) ssq += x[e] * x[e];
+            } else {
+                ssq = dot2sq(r.q, ks, ssq);
+            }
+            cq[ks] = cvt8(x);
+            if constexpr (kLo) cql[ks] = lo8(x, cq[ks]);
+        }
+        ssq = pair_sum32(pair_sum16(ssq));
+        const float rq = p.normalize ? rsqrtf(ssq + p.eps) * p.qscale : 1.f;
+        lq_i = cv.cum_q * 1.4426950408889634f + __builtin_amdgcn_logf(rq);
+    }
     // Gram tiles: C(jt, it) = MFMA(A = k rows of tile jt, B = rows of tile it), which holds
     // X[i = 16 it + n][j = 16 jt + 4 g + r] in lane (n, g) (the Gram matrix is symmetric).
     // G: it = wv, jt <= wv.  k q^T: it = 3 - wv, jt <= 3 - wv.
     const int iq = 3 - wv;
     // factors of this lane's rows
-    const float la_i = F.la[16 * wv + n], lq_i = kQ ? F.lq[16 * iq + n] : 0.f, mk_i = F.mk[16 * wv + n];
+    const float la_i = F.la[16 * wv + n], mk_i = F.mk[16 * wv + n];
     // this wave's own k rows (the B operand of its Gram row block), read back from LDS
     half8 kb[4], kbl[4];
 #pragma unroll
@@ -435,10 +443,10 @@ __device__ __forceinline__ void prep_b(Smem<kLo>& sm, int buf, const Conv<kLo>& 
 #pragma unroll
             for (int ks = 0; ks < 4; ks++) {
                 const half8 a = kat(ks);
-                acc = mfma32(a, cv.q[ks], acc);
+                acc = mfma32(a, cq[ks], acc);
                 if constexpr (kLo) {
-                    acc = mfma32(a, cv.ql[ks], acc);
-                    acc = mfma32(kalt(ks), cv.q[ks], acc);
+                    acc = mfma32(a, cql[ks], acc);
+                    acc = mfma32(kalt(ks), cq[ks], acc);
                 }
             }
             f32x4 iv;
@@ -459,14 +467,17 @@ __device__ __forceinline__ void prep_b(Smem<kLo>& sm, int buf, const Conv<kLo>& 
                 half8 y;
 #pragma unroll
                 for (int e = 0; e < 8; e++) {
-                    float x = (float)cv.q[ks][e];
-                    if constexpr (kLo) x += (float)cv.ql[ks][e];
+                    float x = (float)cq[ks][e];
+                    if constexpr (kLo) x += (float)cql[ks][e];
                     y[e] = (half_t)(f * x);
                 }
                 *(half8*)&sm.Q[16 * iq + n][32 * ks + 8 * g] = y;
             }
-            *(half8*)&sm.V[16 * wv + n][32 * ks + 8 * g] = cv.v[ks];
-            if constexpr (kLo) *(half8*)&sm.VL[0][16 * wv + n][32 * ks + 8 * g] = cv.vl[ks];
+            float x[8];
+            unpack8(r.v, ks, x);
+            const half8 vh = cvt8(x);
+            *(half8*)&sm.V[16 * wv + n][32 * ks + 8 * g] = vh;
+            if constexpr (kLo) *(half8*)&sm.VL[0][16 * wv + n][32 * ks + 8 * g] = lo8(x, vh);
         }
     }
 }
@@ -880,29 +891,28 @@ __device__ __forceinline__ void prep_body(const Params& p, Smem<sizeof(Tin) == 4
     const Rsrc rs = make_rsrc<Tin, Tout>(p, b, hv);
     Raw<Tin> raw;
     RawGB gb;
-    Conv<kLo> cv;
+    Conv cv;
     Deferred df;
+    // prep A (phase 1) reads the k rows, g and beta, prep B (phase 2) the q and v rows: each set
+    // is requested right after its last use, a period ahead of its next
     load_chunk<Tin, kQ>(p, rs, c0, wave, n, g, lane, raw, gb);
     prep_a<Tin, kLo, kQ>(p, sm, c0 & 1, raw, gb, wave, n, g, lane, cv);
-    load_chunk<Tin, kQ>(p, rs, c0 + 1, wave, n, g, lane, raw, gb);
+    load_chunk<Tin, kQ, 1>(p, rs, c0 + 1, wave, n, g, lane, raw, gb);
     lds_barrier();
-    prep_b<kLo, kQ>(sm, c0 & 1, cv, wave, n, g, df);
+    prep_b<Tin, kLo, kQ>(p, sm, c0 & 1, raw, cv, wave, n, g, df);
+    load_chunk<Tin, kQ, 2>(p, rs, c0 + 1, wave, n, g, lane, raw, gb);
     lds_barrier();
     for (int c = c0; c < c1; c++) {
         const int nb = (c & 1) ^ 1;
         // ---- phase 1: chunk c's A / D / intra into LDS; prep A of chunk c + 1
         write_deferred<kLo, kQ>(sm, df, wave, n, g);
         prep_a<Tin, kLo, kQ>(p, sm, nb, raw, gb, wave, n, g, lane, cv);
-        // fp32 inputs: chunk c + 2's rows are requested after prep B instead, so their 96
-        // registers are not live across it
-        if constexpr (!kLo) load_chunk<Tin, kQ>(p, rs, c + 2, wave, n, g, lane, raw, gb);
+        load_chunk<Tin, kQ, 1>(p, rs, c + 2, wave, n, g, lane, raw, gb);
         lds_barrier();
         // ---- phase 2: prep B of chunk c + 1 (Q and V are rewritten: the chain read them in phase 1)
-        prep_b<kLo, kQ>(sm, nb, cv, wave, n, g, df);
-        if constexpr (kLo) {
-            __builtin_amdgcn_sched_barrier(0);  // the loads stay below prep B
-            load_chunk<Tin, kQ>(p, rs, c + 2, wave, n, g, lane, raw, gb);
-        }
+        prep_b<Tin, kLo, kQ>(p, sm, nb, raw, cv, wave, n, g, df);
+        __builtin_amdgcn_sched_barrier(0);  // the loads stay below prep B
+        load_chunk<Tin, kQ, 2>(p, rs, c + 2, wave, n, g, lane, raw, gb);
         lds_barrier();
     }
 }
