@@ -807,7 +807,7 @@ __device__ __forceinline__ void chain_transition(const Fact& F, const half_t* K,
 // Start / end of a segment's state (and transition) for the columns col0 .. col0 + 16 NC.
 template <bool kOut, int NC>
 __device__ __forceinline__ void seg_start(const Params& p, size_t unit, int s, int col0, int n, int g,
-                                          f32x4 (&S)[8][NC], f32x4 (&M)[8][NC]) {
+                                          f32x4 (&S)[8][NC]) {
     constexpr size_t DD = (size_t)D * D;
     if constexpr (kOut) {
         const float* src = p.P > 1 ? p.starts + (unit * p.P + s) * DD : (p.init ? p.init + unit * DD : nullptr);
@@ -815,19 +815,16 @@ __device__ __forceinline__ void seg_start(const Params& p, size_t unit, int s, i
     } else {
         load_state(s == 0 && p.init ? p.init + unit * DD : nullptr, col0, n, g, S);
         if (s == 0) store_state(p.starts + unit * p.P * DD, col0, n, g, S);
-        init_identity(col0, n, g, M);
     }
 }
 template <bool kOut, int NC>
 __device__ __forceinline__ void seg_end(const Params& p, size_t unit, int s, int col0, int n, int g,
-                                        const f32x4 (&S)[8][NC], const f32x4 (&M)[8][NC]) {
+                                        const f32x4 (&S)[8][NC]) {
     constexpr size_t DD = (size_t)D * D;
     if constexpr (kOut) {
         if (s == p.P - 1) store_state(p.final_state + unit * DD, col0, n, g, S);
     } else {
-        const size_t seg = unit * (p.P - 1) + s;
-        store_state(p.nbuf + seg * DD, col0, n, g, S);
-        store_transition(p.mbuf + seg * DD, col0, n, g, M);
+        store_state(p.nbuf + (unit * (p.P - 1) + s) * DD, col0, n, g, S);
     }
 }
 
@@ -846,8 +843,8 @@ __device__ __forceinline__ void chain_body(const Params& p, Smem<sizeof(Tin) == 
     const int c0 = s * p.L, c1 = min(p.nch, c0 + p.L);
     const size_t unit = (size_t)(b * p.HV + hv);
 
-    f32x4 S[8][2], M[8][2];
-    seg_start<kOut>(p, unit, s, col0, n, g, S, M);
+    f32x4 S[8][2];
+    seg_start<kOut>(p, unit, s, col0, n, g, S);
     const Rsrc rs = make_rsrc<Tin, Tout>(p, b, hv);
     lds_barrier();  // the prep waves' prologue: chunk c0's operands
     lds_barrier();
@@ -871,14 +868,9 @@ __device__ __forceinline__ void chain_body(const Params& p, Smem<sizeof(Tin) == 
         if constexpr (kOut)
             out_intra_store<2, Tout>(&sm.IH[0][0], &sm.IL[0][0], V, Vh, O, rs.out, c * CH, (int)p.a.st_o, col0, n, g);
         chain_update<true>(sm.F[buf], &sm.K[buf][0][0], KL, n, g, V, S);
-        if constexpr (!kOut) {
-            // a scheduling fence keeps the transition's temporaries from overlapping the state's
-            __builtin_amdgcn_sched_barrier(0);
-            chain_transition(sm.F[buf], &sm.K[buf][0][0], &sm.AD[0][0], n, g, M);
-        }
         lds_barrier();
     }
-    seg_end<kOut>(p, unit, s, col0, n, g, S, M);
+    seg_end<kOut>(p, unit, s, col0, n, g, S);
 }
 
 template <typename Tin, typename Tout, bool kQ, int WV>
@@ -893,6 +885,11 @@ __device__ __forceinline__ void prep_body(const Params& p, Smem<sizeof(Tin) == 4
     RawGB gb;
     Conv cv;
     Deferred df;
+    // the transition launch: the segment's transition M (the chain on the identity with v = 0) runs
+    // here, on these waves' spare phase-2 time; wave 4 + w owns the columns [32 w, 32 w + 32)
+    constexpr bool kM = !kQ;
+    f32x4 M[kM ? 8 : 1][2];
+    if constexpr (kM) init_identity(32 * wave, n, g, M);
     // prep A (phase 1) reads the k rows, g and beta, prep B (phase 2) the q and v rows: each set
     // is requested right after its last use, a period ahead of its next
     load_chunk<Tin, kQ>(p, rs, c0, wave, n, g, lane, raw, gb);
@@ -913,7 +910,16 @@ __device__ __forceinline__ void prep_body(const Params& p, Smem<sizeof(Tin) == 4
         prep_b<Tin, kLo, kQ>(p, sm, nb, raw, cv, wave, n, g, df);
         __builtin_amdgcn_sched_barrier(0);  // the loads stay below prep B
         load_chunk<Tin, kQ, 2>(p, rs, c + 2, wave, n, g, lane, raw, gb);
+        if constexpr (kM) {
+            // chunk c's transition step (AD holds chunk c's blocks until the next period)
+            __builtin_amdgcn_sched_barrier(0);
+            chain_transition(sm.F[c & 1], &sm.K[c & 1][0][0], &sm.AD[0][0], n, g, M);
+        }
         lds_barrier();
+    }
+    if constexpr (kM) {
+        constexpr size_t DD = (size_t)D * D;
+        store_transition(p.mbuf + ((size_t)(b * p.HV + hv) * (p.P - 1) + s) * DD, 32 * wave, n, g, M);
     }
 }
 
