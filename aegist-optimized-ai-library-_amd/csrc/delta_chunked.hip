@@ -942,82 +942,95 @@ __global__ void __launch_bounds__(NT2, 2) delta_seg_kernel(Params p) {
     }
 }
 
-// Segment boundaries: S_1 = N_0, S_{s+1} = M_s S_s + N_s. One wave per (sequence, head,
-// 16-column slice); M_s as the fp16 A operand, S_s as fp16 hi + lo.
-__global__ void __launch_bounds__(WAVE) delta_seg_combine(Params p) {
+// Segment boundaries: S_1 = N_0, S_{s+1} = M_s S_s + N_s. One workgroup of 4 waves per
+// (sequence, head, 16-column slice); wave w owns the rows [32 w, 32 w + 32). Computed transposed,
+// S^T_{s+1} = S^T_s M_s^T + N^T_s, so a lane's accumulator holds 4 consecutive columns of one row
+// (16-byte loads of N and stores of the start states) and M's rows enter as B operands with
+// 16-byte loads; S^T_s, the A operand, goes through LDS as fp16 hi + lo (double-buffered, one
+// barrier per step). Each wave's M / N operands are requested DEPTH steps ahead.
+constexpr int CB_DEPTH = 3;
+__global__ void __launch_bounds__(4 * WAVE) delta_seg_combine(Params p) {
     // the 8 column slices of one (sequence, head) on one XCD (block ids congruent mod 8), where
     // they share each M_s through that XCD's L2
     const int x = blockIdx.x, unit = (x / 64) * 8 + x % 8, slice = (x / 8) % 8;
     if (unit >= p.B * p.HV) return;
-    const int lane = threadIdx.x, n = lane % 16, g = lane / 16;
-    const int col = 16 * slice + n;
+    __shared__ __attribute__((aligned(16))) half_t sth[2][16][D + 8], stl[2][16][D + 8];
+    const int lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE, n = lane % 16, g = lane / 16;
+    const int c0 = 16 * slice;
     constexpr size_t DD = (size_t)D * D;
     const float* N = p.nbuf + (size_t)unit * (p.P - 1) * DD;
     const half_t* Mb = p.mbuf + (size_t)unit * (p.P - 1) * DD;
     float* st = p.starts + (size_t)unit * p.P * DD;
-    // the operands of one boundary step: M_s rows as A fragments and N_s as the accumulators;
-    // the next step's are requested before this step's products (they do not depend on S)
+    // step s's operands of this lane: M_s row (32 wave + 16 ft + n) as B fragments (k = 32 kb +
+    // 8 g ..), N_s[row][c0 + 4 g ..] as the accumulator
     struct Ops {
-        half8 a[8][4];
-        f32x4 acc[8];
+        half8 b[2][4];
+        f32x4 n[2];
     };
     auto load = [&](int s, Ops& o) {
         const float* Ns = N + (size_t)s * DD;
         const half_t* Ms = Mb + (size_t)s * DD;
 #pragma unroll
-        for (int ft = 0; ft < 8; ft++) {
+        for (int ft = 0; ft < 2; ft++) {
+            const int row = 32 * wave + 16 * ft + n;
+            o.n[ft] = *(const f32x4*)(Ns + (size_t)row * D + c0 + 4 * g);
 #pragma unroll
-            for (int r = 0; r < 4; r++) o.acc[ft][r] = Ns[(size_t)(16 * ft + 4 * g + r) * D + col];
-            const half_t* row = Ms + (size_t)(16 * ft + n) * D;
-#pragma unroll
-            for (int m = 0; m < 4; m++)
-                o.a[ft][m] = cat8(*(const half4*)(row + 32 * m + 4 * g), *(const half4*)(row + 32 * m + 16 + 4 * g));
+            for (int kb = 0; kb < 4; kb++) o.b[ft][kb] = *(const half8*)(Ms + (size_t)row * D + 32 * kb + 8 * g);
         }
     };
-    f32x4 S[8];
-    Ops ops[2];
+    // S^T rows of this lane's two tiles into LDS (hi + lo) and the fp32 start state to HBM
+    auto publish = [&](int buf, int s1, const f32x4 (&v)[2]) {
 #pragma unroll
-    for (int ft = 0; ft < 8; ft++)
+        for (int ft = 0; ft < 2; ft++) {
+            const int row = 32 * wave + 16 * ft + n;
+            half4 h, l;
+            split4(v[ft], h, l);
 #pragma unroll
-        for (int r = 0; r < 4; r++) S[ft][r] = N[(size_t)(16 * ft + 4 * g + r) * D + col];
-    if (p.P > 2) load(1, ops[0]);
-#pragma unroll
-    for (int ft = 0; ft < 8; ft++)
-#pragma unroll
-        for (int r = 0; r < 4; r++) st[DD + (size_t)(16 * ft + 4 * g + r) * D + col] = S[ft][r];
-    auto step = [&](int s, const Ops& cur) {
-        half8 bh[4], bl[4];
-#pragma unroll
-        for (int m = 0; m < 4; m++) {
-            half4 h0, l0, h1, l1;
-            split4(S[2 * m], h0, l0);
-            split4(S[2 * m + 1], h1, l1);
-            bh[m] = cat8(h0, h1);
-            bl[m] = cat8(l0, l1);
-        }
-#pragma unroll
-        for (int ft = 0; ft < 8; ft++) S[ft] = cur.acc[ft];
-#pragma unroll
-        for (int m = 0; m < 4; m++)
-#pragma unroll
-            for (int ft = 0; ft < 8; ft++) {
-                S[ft] = mfma32(cur.a[ft][m], bh[m], S[ft]);
-                S[ft] = mfma32(cur.a[ft][m], bl[m], S[ft]);
+            for (int r = 0; r < 4; r++) {
+                sth[buf][4 * g + r][row] = h[r];
+                stl[buf][4 * g + r][row] = l[r];
             }
-        float* dst = st + (size_t)(s + 1) * DD;
-#pragma unroll
-        for (int ft = 0; ft < 8; ft++)
-#pragma unroll
-            for (int r = 0; r < 4; r++) dst[(size_t)(16 * ft + 4 * g + r) * D + col] = S[ft][r];
+            *(f32x4*)(st + (size_t)s1 * DD + (size_t)row * D + c0 + 4 * g) = v[ft];
+        }
     };
-    // two steps per iteration with alternating operand sets, so no set is copied (a copy would
-    // wait for its loads)
-    for (int s = 1; s + 1 < p.P; s += 2) {
-        if (s + 2 < p.P) load(s + 1, ops[1]);
-        step(s, ops[0]);
-        if (s + 2 >= p.P) break;
-        if (s + 3 < p.P) load(s + 2, ops[0]);
-        step(s + 1, ops[1]);
+    Ops ops[CB_DEPTH];
+    f32x4 cur[2];
+    {
+        Ops o0;
+        load(0, o0);  // (only its N part is used: S_1 = N_0)
+#pragma unroll
+        for (int d = 0; d < CB_DEPTH; d++)
+            if (1 + d < p.P - 1) load(1 + d, ops[d]);
+        cur[0] = o0.n[0];
+        cur[1] = o0.n[1];
+    }
+    publish(0, 1, cur);  // S_1 = N_0
+    lds_barrier();
+    // steps s = 1 .. P - 2 (unrolled by the ring depth so every operand set is named statically)
+    for (int s0 = 1; s0 < p.P - 1; s0 += CB_DEPTH) {
+#pragma unroll
+        for (int d = 0; d < CB_DEPTH; d++) {
+            const int s = s0 + d;
+            if (s >= p.P - 1) break;
+            const int rb = (s - 1) & 1;  // S_s lives in buffer (s - 1) & 1
+            half8 ah[4], al[4];
+#pragma unroll
+            for (int kb = 0; kb < 4; kb++) {
+                ah[kb] = *(const half8*)&sth[rb][n][32 * kb + 8 * g];
+                al[kb] = *(const half8*)&stl[rb][n][32 * kb + 8 * g];
+            }
+            f32x4 acc[2] = {ops[d].n[0], ops[d].n[1]};
+#pragma unroll
+            for (int kb = 0; kb < 4; kb++)
+#pragma unroll
+                for (int ft = 0; ft < 2; ft++) {
+                    acc[ft] = mfma32(ah[kb], ops[d].b[ft][kb], acc[ft]);
+                    acc[ft] = mfma32(al[kb], ops[d].b[ft][kb], acc[ft]);
+                }
+            if (s + CB_DEPTH < p.P - 1) load(s + CB_DEPTH, ops[d]);
+            publish(rb ^ 1, s + 1, acc);
+            lds_barrier();
+        }
     }
 }
 
@@ -1137,7 +1150,7 @@ int run_chunked(const Tin* q, const Tin* k, const Tin* v, const float* g, const 
         delta_seg_kernel<Tin, Tout, false><<<grid_for(sp.P - 1), NT2, lds, st>>>(p);
         int rc = after_launch("delta_seg_kernel(transition)");
         if (rc) return rc;
-        delta_seg_combine<<<(B * HV + 7) / 8 * 64, WAVE, 0, st>>>(p);
+        delta_seg_combine<<<(B * HV + 7) / 8 * 64, 4 * WAVE, 0, st>>>(p);
         rc = after_launch("delta_seg_combine");
         if (rc) return rc;
     }
