@@ -49,6 +49,15 @@ __device__ __forceinline__ float sigmoid_f(float x) { return 1.f / (1.f + __expf
 // sigmoid with the hardware reciprocal (1 ulp) in place of the IEEE division sequence; for
 // epilogues that apply it to whole output tiles
 __device__ __forceinline__ float sigmoid_rcp(float x) { return __builtin_amdgcn_rcpf(1.f + __expf(-x)); }
+// silu of the 4-tap causal conv at one channel: taps w0..w3 on inputs t-3, t-2, t-1, t, summed
+// oldest first with explicit FMAs, so every prefill conv path rounds alike; the sigmoid takes the
+// hardware reciprocal (1 ulp) instead of an IEEE division, which the GEMM epilogue that runs it
+// over whole tiles cannot hide
+__device__ __forceinline__ float conv4_silu(float w0, float w1, float w2, float w3, float h0, float h1, float h2,
+                                            float x) {
+    const float a = __builtin_fmaf(w3, x, __builtin_fmaf(w2, h2, __builtin_fmaf(w1, h1, w0 * h0)));
+    return a * sigmoid_rcp(a);
+}
 
 // ---------------------------------------------------------------------------------------------
 // wave64 reductions (butterfly; every lane ends with the result).

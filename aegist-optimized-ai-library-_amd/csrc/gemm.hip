@@ -27,16 +27,40 @@ constexpr int kBufWord3 = 0x00020000;               // buffer resource word 3 on
 // orders, so the 16 rows of a fragment read hit 16 distinct bank groups.
 __device__ __forceinline__ int sw(int row) { return (row >> 1) & 7; }
 
-__global__ void __launch_bounds__(512, 1) gemm_bf16_kernel(const uint16_t* __restrict__ X, int ldx,
-                                                           const uint16_t* __restrict__ W, int ldw,
-                                                           float* __restrict__ Y, int ldy, int M, int N, int K,
-                                                           int accumulate, int tiles_n, int ntiles, int per_xcd) {
+// Up to three weight matrices stacked along N: rows [n0, n0 + N) of the combined W (and columns of
+// the combined output) belong to segment s, whose W rows have stride ldw and whose outputs go to
+// Y (row stride ldy). Every segment but the last has N a multiple of 8 (one load piece never
+// spans two segments).
+constexpr int kMaxGemmSeg = 3;
+struct GemmSeg {
+    const uint16_t* W;
+    float* Y;
+    long long ldy;
+    int n0, N, ldw;
+};
+struct GemmArgs {
+    const uint16_t* X;
+    GemmSeg seg[kMaxGemmSeg];
+    const uint16_t* conv_w;  // conv epilogue: [N][4] bf16 taps, tap 3 on the newest row
+    float* edge;             // conv epilogue: [M / 256][6][N] raw rows 0..2 and 253..255 of every tile
+    int nseg, ldx, M, N, K, accumulate, tiles_n, ntiles, per_xcd;
+};
+
+// kConv: the output is silu(causal depthwise conv4 over rows) of the product instead of the
+// product itself (the DeltaNet input projection followed by its short convolution): every M tile
+// is 256 consecutive tokens of one sequence, a row's three predecessors come from neighbouring
+// lanes (DPP row rotations), the previous 16-row tile or, across waves, LDS; the first three rows
+// of a tile have their predecessors in another tile, so their outputs are left to
+// conv_edge_kernel, which gets the raw first and last three rows of every tile through `edge`.
+template <bool kConv>
+__global__ void __launch_bounds__(512, 1) gemm_bf16_kernel(const GemmArgs ga) {
     __shared__ __attribute__((aligned(1024))) unsigned char A0[kTileBytes];  // W tile, buffer 0
     __shared__ __attribute__((aligned(1024))) unsigned char B0[kTileBytes];  // X tile, buffer 0
     __shared__ __attribute__((aligned(1024))) unsigned char A1[kTileBytes];
     __shared__ __attribute__((aligned(1024))) unsigned char B1[kTileBytes];
 
-    const int li = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+    const int M = ga.M, N = ga.N, K = ga.K, tiles_n = ga.tiles_n, ntiles = ga.ntiles;
+    const int li = (blockIdx.x % 8) * ga.per_xcd + blockIdx.x / 8;
     if (li >= ntiles) return;
     // grouped order: kGroupM M tiles x all N tiles per group, M fastest, so the ~32 workgroups
     // an XCD runs at once form a kGroupM x 8 block sharing X and W tiles in its L2
@@ -52,16 +76,28 @@ __global__ void __launch_bounds__(512, 1) gemm_bf16_kernel(const uint16_t* __res
 
     // loads: the 64 1-KB pieces of a step (32 per operand, 8 rows x 128 bytes each: whole cache
     // lines) are dealt 8 per wave; piece j covers rows 8 (j % 32) .. +7, lane L row 8 (j % 32) +
-    // L / 8, LDS slot L % 8, which holds global slot (L % 8) ^ sw(row)
-    const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc((void*)W, (short)0, 0x7fffffff, kBufWord3);
-    const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc((void*)X, (short)0, 0x7fffffff, kBufWord3);
+    // L / 8, LDS slot L % 8, which holds global slot (L % 8) ^ sw(row). A W piece reads the
+    // segment its first row falls in (rows past the last segment repeat its last row).
+    const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc((void*)ga.X, (short)0, 0x7fffffff, kBufWord3);
+    __amdgpu_buffer_rsrc_t prs[8];
     int voff[8];
 #pragma unroll
     for (int jj = 0; jj < 8; jj++) {
         const int j = wave * 8 + jj, tensor = j / 32, row = 8 * (j % 32) + lane / 8;
         const int gslot = (lane % 8) ^ sw(row);
-        voff[jj] = tensor == 0 ? (min(n0 + row, N - 1) * ldw + 8 * gslot) * 2
-                               : (min(m0 + row, M - 1) * ldx + 8 * gslot) * 2;
+        if (tensor == 0) {
+            const int prow = n0 + 8 * (j % 32);  // uniform
+            int si = 0;
+#pragma unroll
+            for (int q = 1; q < kMaxGemmSeg; q++)
+                if (q < ga.nseg && prow >= ga.seg[q].n0) si = q;
+            const GemmSeg& sg = ga.seg[si];
+            prs[jj] = __builtin_amdgcn_make_buffer_rsrc((void*)sg.W, (short)0, 0x7fffffff, kBufWord3);
+            voff[jj] = (min(n0 + row - sg.n0, sg.N - 1) * sg.ldw + 8 * gslot) * 2;
+        } else {
+            prs[jj] = xrs;
+            voff[jj] = (min(m0 + row, M - 1) * ga.ldx + 8 * gslot) * 2;
+        }
     }
     typedef __attribute__((address_space(3))) void lds_void;
     auto load_step = [&](unsigned char* At, unsigned char* Bt, int k0) {
@@ -69,8 +105,7 @@ __global__ void __launch_bounds__(512, 1) gemm_bf16_kernel(const uint16_t* __res
         for (int jj = 0; jj < 8; jj++) {
             const int j = wave * 8 + jj, tensor = j / 32;
             unsigned char* dst = (tensor == 0 ? At : Bt) + (j % 32) * 1024;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(tensor == 0 ? wrs : xrs, (lds_void*)dst, 16, voff[jj], k0 * 2, 0,
-                                                     0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(prs[jj], (lds_void*)dst, 16, voff[jj], k0 * 2, 0, 0);
         }
     };
 
@@ -123,26 +158,139 @@ __global__ void __launch_bounds__(512, 1) gemm_bf16_kernel(const uint16_t* __res
 
     // lane (c = r16, g) of tile (i, j) holds Y[m][n .. n + 3], m = m0 + 64 wm + 16 j + c,
     // n = n0 + 128 wn + 16 i + 4 g
-    const bool vec = (ldy % 4) == 0 && ((uintptr_t)Y % 16) == 0;
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const int m = m0 + 64 * wm + 16 * j + r16;
-        if (m >= M) continue;
-        float* yrow = Y + (size_t)m * ldy;
+    if constexpr (!kConv) {
 #pragma unroll
         for (int i = 0; i < 8; i++) {
             const int n = n0 + 128 * wn + 16 * i + 4 * g;
-            if (vec && n + 3 < N) {
-                f32x4 v = acc[i][j];
-                if (accumulate) v += *(const f32x4*)(yrow + n);
-                *(f32x4*)(yrow + n) = v;
-            } else {
+            if (n >= N) continue;
+            int si = 0;
 #pragma unroll
-                for (int e = 0; e < 4; e++)
-                    if (n + e < N) yrow[n + e] = (accumulate ? yrow[n + e] : 0.f) + acc[i][j][e];
+            for (int q = 1; q < kMaxGemmSeg; q++)
+                if (q < ga.nseg && n >= ga.seg[q].n0) si = q;
+            const GemmSeg& sg = ga.seg[si];
+            const int nl = n - sg.n0;  // 4-aligned; segment boundaries are multiples of 8
+            const bool vec = (sg.ldy % 4) == 0 && ((uintptr_t)sg.Y % 16) == 0 && nl + 3 < sg.N;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int m = m0 + 64 * wm + 16 * j + r16;
+                if (m >= M) continue;
+                float* y = sg.Y + (size_t)m * sg.ldy + nl;
+                if (vec) {
+                    f32x4 v = acc[i][j];
+                    if (ga.accumulate) v += *(const f32x4*)y;
+                    *(f32x4*)y = v;
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; e++)
+                        if (nl + e < sg.N) y[e] = (ga.accumulate ? y[e] : 0.f) + acc[i][j][e];
+                }
+            }
+        }
+    } else {
+        // one segment, M a multiple of 256, no accumulation (the launcher checks). The previous
+        // wave along M (wave - 2) publishes its last 16-row tile through LDS.
+        __syncthreads();  // every wave is past its last LDS operand read
+        // [8 i][64 lanes] per wave, waves 0..3 in A0 and 4..7 in B0 (32 KB each)
+        auto xch = [&](int w, int i) { return (f32x4*)(w < 4 ? A0 : B0) + ((w % 4) * 8 + i) * WAVE; };
+#pragma unroll
+        for (int i = 0; i < 8; i++) xch(wave, i)[lane] = acc[i][3];
+        __syncthreads();
+        const GemmSeg& sg = ga.seg[0];
+        const int tile_m = m0 / GBM;
+        // DPP row rotate right by k: lane r16 of each 16-lane row takes lane (r16 - k) mod 16
+        auto ror = [](f32x4 v, auto kc) {
+            f32x4 r;
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                r[e] = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v[e]), 0x120 + decltype(kc)::value, 0xf,
+                                                               0xf, false));
+            return r;
+        };
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const int n = n0 + 128 * wn + 16 * i + 4 * g;
+            const bool nok = n < N;  // N is a multiple of 4
+            const int nc = nok ? n : 0;
+            const uint4 w01 = *(const uint4*)(ga.conv_w + (size_t)nc * 4);      // columns n, n + 1
+            const uint4 w23 = *(const uint4*)(ga.conv_w + (size_t)nc * 4 + 8);  // columns n + 2, n + 3
+            float wt[4][4];
+            {
+                const uint32_t wv[8] = {w01.x, w01.y, w01.z, w01.w, w23.x, w23.y, w23.z, w23.w};
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    wt[e][0] = bf_lo(wv[2 * e]);
+                    wt[e][1] = bf_hi(wv[2 * e]);
+                    wt[e][2] = bf_lo(wv[2 * e + 1]);
+                    wt[e][3] = bf_hi(wv[2 * e + 1]);
+                }
+            }
+            // rows 13..15 of the previous wave's last tile, rotated as ror would
+            f32x4 pw[3];
+#pragma unroll
+            for (int k = 1; k <= 3; k++)
+                pw[k - 1] = wm > 0 ? xch(wave - 2, i)[16 * g + ((r16 - k) & 15)] : f32x4{0.f, 0.f, 0.f, 0.f};
+            f32x4 prev_r1 = pw[0], prev_r2 = pw[1], prev_r3 = pw[2];  // rotations of the tile above
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const f32x4 x = acc[i][j];
+                const f32x4 r1 = ror(x, std::integral_constant<int, 1>{});
+                const f32x4 r2 = ror(x, std::integral_constant<int, 2>{});
+                const f32x4 r3 = ror(x, std::integral_constant<int, 3>{});
+                const f32x4 h2 = r16 >= 1 ? r1 : prev_r1;  // row m - 1
+                const f32x4 h1 = r16 >= 2 ? r2 : prev_r2;  // row m - 2
+                const f32x4 h0 = r16 >= 3 ? r3 : prev_r3;  // row m - 3
+                prev_r1 = r1;
+                prev_r2 = r2;
+                prev_r3 = r3;
+                const int lr = 64 * wm + 16 * j + r16, m = m0 + lr;
+                if (!nok) continue;
+                if (lr >= 3) {
+                    f32x4 o;
+#pragma unroll
+                    for (int e = 0; e < 4; e++)
+                        o[e] = conv4_silu(wt[e][0], wt[e][1], wt[e][2], wt[e][3], h0[e], h1[e], h2[e], x[e]);
+                    *(f32x4*)(sg.Y + (size_t)m * sg.ldy + n) = o;
+                }
+                if (lr < 3 || lr >= GBM - 3)
+                    *(f32x4*)(ga.edge + ((size_t)tile_m * 6 + (lr < 3 ? lr : lr - (GBM - 6))) * N + n) = x;
             }
         }
     }
+}
+
+// The conv outputs of the first three rows of every 256-row tile and the new conv state, from
+// the raw edge rows the conv GEMM saved. One thread per (sequence, channel) walks the sequence's
+// tiles in order: the rows before tile 0 are the old state (its inputs before token 0), before
+// tile t > 0 the last three raw rows of tile t - 1; the state afterwards holds the last three raw
+// rows of the sequence. y and edge as in gemm_bf16_kernel<true>, state [B, C, 3] oldest first.
+__global__ void conv_edge_kernel(const float* __restrict__ edge, const uint16_t* __restrict__ w,
+                                 float* __restrict__ y, long long ldy, float* __restrict__ state, int T, int C) {
+    const int b = blockIdx.y, c = blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= C) return;
+    const uint2 wp = *(const uint2*)(w + (size_t)c * 4);
+    const float w0 = bf_lo(wp.x), w1 = bf_hi(wp.x), w2 = bf_lo(wp.y), w3 = bf_hi(wp.y);
+    float* st = state + ((size_t)b * C + c) * 3;
+    float h0 = st[0], h1 = st[1], h2 = st[2];
+    const int nt = T / GBM;
+    for (int t = 0; t < nt; t++) {
+        const float* e = edge + (size_t)(b * nt + t) * 6 * C + c;
+        const float x0 = e[0], x1 = e[C], x2 = e[2 * (size_t)C];
+        const float xs[3] = {x0, x1, x2};
+        float* yr = y + ((size_t)b * T + (size_t)t * GBM) * ldy + c;
+#pragma unroll
+        for (int r = 0; r < 3; r++) {
+            yr[(size_t)r * ldy] = conv4_silu(w0, w1, w2, w3, h0, h1, h2, xs[r]);
+            h0 = h1;
+            h1 = h2;
+            h2 = xs[r];
+        }
+        h0 = e[3 * (size_t)C];
+        h1 = e[4 * (size_t)C];
+        h2 = e[5 * (size_t)C];
+    }
+    st[0] = h0;
+    st[1] = h1;
+    st[2] = h2;
 }
 
 
@@ -342,22 +490,92 @@ int launch_gemm_i8f32(const float* X, long long ldx, const int8_t* W, long long 
     return after_launch("gemm_i8");
 }
 
-// Y[M, N] (+)= X[M, K] W[N, K]^T, bf16 X (row stride ldx) and W (row stride ldw), fp32 Y (row
-// stride ldy). Needs K % 64 == 0, 16-byte aligned rows of X and W, and buffer offsets below 2^31
-// (rows x stride x 2 bytes of each operand).
+// Y_s[M, N_s] (+)= X[M, K] W_s[N_s, K]^T for nseg (<= 3) weights sharing X, in one launch: the
+// weights are stacked along N (each segment but the last with N_s % 8 == 0), bf16 X (row stride
+// ldx) and W_s (row stride ldw_s), fp32 Y_s (row stride ldy_s). Needs K % 64 == 0, 16-byte
+// aligned rows of X and W_s, and buffer offsets below 2^31 (rows x stride x 2 bytes).
+int launch_gemm_bf16_multi(const uint16_t* X, long long ldx, int nseg, const uint16_t* const* W, const long long* ldw,
+                           float* const* Y, const long long* ldy, const int* N, int M, int K, int accumulate,
+                           hipStream_t st) {
+    if (nseg < 1 || nseg > kMaxGemmSeg) return fail(AEGIST_ERR_SHAPE, "gemm_bf16: 1 to 3 weights per launch");
+    if (K % GBK || K <= 0) return fail(AEGIST_ERR_SHAPE, "gemm_bf16: K must be a positive multiple of 64");
+    if (ldx < K || ldx % 8 || (uintptr_t)X % 16 || (long long)M * ldx * 2 >= 0x7fffffffLL)
+        return fail(AEGIST_ERR_SHAPE, "gemm_bf16: X needs ldx >= K, 16-byte aligned rows, < 2 GiB");
+    GemmArgs ga{};
+    ga.X = X;
+    int nt = 0;
+    for (int i = 0; i < nseg; i++) {
+        if (N[i] <= 0) continue;
+        if (ldw[i] < K || ldy[i] < N[i] || ldw[i] % 8 || (uintptr_t)W[i] % 16 ||
+            (long long)N[i] * ldw[i] * 2 >= 0x7fffffffLL)
+            return fail(AEGIST_ERR_SHAPE, "gemm_bf16: need ldw >= K, ldy >= N, 16-byte aligned W rows, W < 2 GiB");
+        if (ga.nseg > 0 && ga.seg[ga.nseg - 1].N % 8)
+            return fail(AEGIST_ERR_SHAPE, "gemm_bf16: every weight but the last needs N % 8 == 0");
+        ga.seg[ga.nseg++] = GemmSeg{W[i], Y[i], ldy[i], nt, N[i], (int)ldw[i]};
+        nt += N[i];
+    }
+    if (M <= 0 || ga.nseg == 0) return 0;
+    ga.ldx = (int)ldx;
+    ga.M = M;
+    ga.N = nt;
+    ga.K = K;
+    ga.accumulate = accumulate;
+    const int tiles_m = (M + GBM - 1) / GBM;
+    ga.tiles_n = (nt + GBN - 1) / GBN;
+    ga.ntiles = tiles_m * ga.tiles_n;
+    ga.per_xcd = (ga.ntiles + 7) / 8;
+    gemm_bf16_kernel<false><<<8 * ga.per_xcd, 512, 0, st>>>(ga);
+    return after_launch("gemm_bf16");
+}
+
+// Y[M, N] (+)= X[M, K] W[N, K]^T, one weight (as above).
 int launch_gemm_bf16(const uint16_t* X, long long ldx, const uint16_t* W, long long ldw, float* Y, long long ldy, int M,
                      int N, int K, int accumulate, hipStream_t st) {
     if (M <= 0 || N <= 0) return 0;
-    if (K % GBK || K <= 0) return fail(AEGIST_ERR_SHAPE, "gemm_bf16: K must be a positive multiple of 64");
-    if (ldx < K || ldw < K || ldy < N || ldx % 8 || ldw % 8 || (uintptr_t)X % 16 || (uintptr_t)W % 16)
-        return fail(AEGIST_ERR_SHAPE, "gemm_bf16: need ld >= K, 16-byte aligned rows");
-    if ((long long)M * ldx * 2 >= 0x7fffffffLL || (long long)N * ldw * 2 >= 0x7fffffffLL)
-        return fail(AEGIST_ERR_SHAPE, "gemm_bf16: an operand passes 2 GiB");
-    const int tiles_m = (M + GBM - 1) / GBM, tiles_n = (N + GBN - 1) / GBN, ntiles = tiles_m * tiles_n;
-    const int per_xcd = (ntiles + 7) / 8;
-    gemm_bf16_kernel<<<8 * per_xcd, 512, 0, st>>>(X, (int)ldx, W, (int)ldw, Y, (int)ldy, M, N, K, accumulate, tiles_n,
-                                                  ntiles, per_xcd);
-    return after_launch("gemm_bf16");
+    return launch_gemm_bf16_multi(X, ldx, 1, &W, &ldw, &Y, &ldy, &N, M, K, accumulate, st);
+}
+
+// Bytes of the edge buffer launch_gemm_bf16_conv needs for M rows of N channels.
+size_t gemm_conv_edge_bytes(int M, int N) { return (size_t)(M / GBM) * 6 * N * 4; }
+
+// Whether launch_gemm_bf16_conv takes these operands: B sequences of T tokens (M = B T), T a
+// multiple of the 256-row tile, N a multiple of 4, aligned rows, operands below 2 GiB.
+bool gemm_conv_fits(const void* X, long long ldx, const void* W, long long ldw, const void* conv_w, int B, int T, int N,
+                    int K) {
+    return B > 0 && T > 0 && T % GBM == 0 && N % 4 == 0 && (uintptr_t)conv_w % 16 == 0 &&
+           gemm_bf16_fits(X, ldx, W, ldw, B * T, N, K);
+}
+
+// y[B T, N] = silu(conv4_t(X W^T)) per sequence with the causal depthwise conv over tokens (taps
+// conv_w [N][4], the inputs before token 0 from state [B, N, 3], which then holds the last three
+// raw rows): the projection and the DeltaNet short convolution in one GEMM launch plus a small
+// edge launch, so the raw projection never reaches HBM. edge: gemm_conv_edge_bytes(B T, N).
+int launch_gemm_bf16_conv(const uint16_t* X, long long ldx, const uint16_t* W, long long ldw, const uint16_t* conv_w,
+                          float* state, float* y, long long ldy, float* edge, int B, int T, int N, int K,
+                          hipStream_t st) {
+    if (!gemm_conv_fits(X, ldx, W, ldw, conv_w, B, T, N, K) || ldy < N || ldy % 4 || (uintptr_t)y % 16 ||
+        (uintptr_t)edge % 16)
+        return fail(AEGIST_ERR_SHAPE, "gemm_bf16_conv: need T % 256 == 0, N % 4 == 0, aligned rows");
+    const int M = B * T;
+    GemmArgs ga{};
+    ga.X = X;
+    ga.seg[0] = GemmSeg{W, y, ldy, 0, N, (int)ldw};
+    ga.nseg = 1;
+    ga.conv_w = conv_w;
+    ga.edge = edge;
+    ga.ldx = (int)ldx;
+    ga.M = M;
+    ga.N = N;
+    ga.K = K;
+    ga.accumulate = 0;
+    ga.tiles_n = (N + GBN - 1) / GBN;
+    ga.ntiles = (M / GBM) * ga.tiles_n;
+    ga.per_xcd = (ga.ntiles + 7) / 8;
+    gemm_bf16_kernel<true><<<8 * ga.per_xcd, 512, 0, st>>>(ga);
+    int rc = after_launch("gemm_bf16_conv");
+    if (rc) return rc;
+    conv_edge_kernel<<<dim3((N + 255) / 256, B), 256, 0, st>>>(edge, conv_w, y, ldy, state, T, N);
+    return after_launch("conv_edge");
 }
 
 }  // namespace aegist

@@ -299,7 +299,7 @@ __global__ void __launch_bounds__(256) conv_silu_kernel(const float* __restrict_
             float xm2 = t >= 2 ? x[(size_t)(t - 2) * C + c] : (t == 0 ? s1 : s2);
             float xm1 = t >= 1 ? x[(size_t)(t - 1) * C + c] : s2;
             float x0 = x[(size_t)t * C + c];
-            y[(size_t)t * C + c] = silu_f(w0 * xm3 + w1 * xm2 + w2 * xm1 + w3 * x0);
+            y[(size_t)t * C + c] = conv4_silu(w0, w1, w2, w3, xm3, xm2, xm1, x0);
         }
     }
     __syncthreads();
@@ -570,7 +570,7 @@ __global__ void __launch_bounds__(256) conv_silu_batched_kernel(const float* __r
             const float xm3 = t >= 3 ? x[(size_t)(t - 3) * C + c] : (t == 0 ? s0 : (t == 1 ? s1 : s2));
             const float xm2 = t >= 2 ? x[(size_t)(t - 2) * C + c] : (t == 0 ? s1 : s2);
             const float xm1 = t >= 1 ? x[(size_t)(t - 1) * C + c] : s2;
-            y[(size_t)t * C + c] = silu_f(w0 * xm3 + w1 * xm2 + w2 * xm1 + w3 * x[(size_t)t * C + c]);
+            y[(size_t)t * C + c] = conv4_silu(w0, w1, w2, w3, xm3, xm2, xm1, x[(size_t)t * C + c]);
         }
     }
     __syncthreads();
@@ -629,7 +629,7 @@ __global__ void __launch_bounds__(256) conv_silu_chunk_kernel(const float* __res
             f32x4 o;
 #pragma unroll
             for (int e = 0; e < 4; e++)
-                o[e] = silu_f(wt[e][0] * h0[e] + wt[e][1] * h1[e] + wt[e][2] * h2[e] + wt[e][3] * xin[i][e]);
+                o[e] = conv4_silu(wt[e][0], wt[e][1], wt[e][2], wt[e][3], h0[e], h1[e], h2[e], xin[i][e]);
             *(f32x4*)(y + (size_t)(t0 + i) * C + c) = o;
         }
         h0 = h1;

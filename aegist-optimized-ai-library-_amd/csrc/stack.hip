@@ -48,6 +48,14 @@ size_t prefill_f16_bytes(int B, int KV, int rows);
 bool gemm_bf16_fits(const void* X, long long ldx, const void* W, long long ldw, int M, int N, int K);
 int launch_gemm_bf16(const uint16_t* X, long long ldx, const uint16_t* W, long long ldw, float* Y, long long ldy, int M,
                      int N, int K, int accumulate, hipStream_t st);
+int launch_gemm_bf16_multi(const uint16_t* X, long long ldx, int nseg, const uint16_t* const* W, const long long* ldw,
+                           float* const* Y, const long long* ldy, const int* N, int M, int K, int accumulate,
+                           hipStream_t st);
+bool gemm_conv_fits(const void* X, long long ldx, const void* W, long long ldw, const void* conv_w, int B, int T, int N,
+                    int K);
+int launch_gemm_bf16_conv(const uint16_t* X, long long ldx, const uint16_t* W, long long ldw, const uint16_t* conv_w,
+                          float* state, float* y, long long ldy, float* edge, int B, int T, int N, int K,
+                          hipStream_t st);
 size_t decode_workspace_bytes(int B, int H, int KV, int L, bool with_q);
 int launch_proj(const void* X, int x_dtype, long long ldx, const void* W, int w_dtype, const uint16_t* scale, float* Y,
                 long long ldy, int M, int N, int K, int accumulate, hipStream_t st);
@@ -144,6 +152,15 @@ int gemm_group(Stack* s, const uint16_t* A, int n, const uint16_t* const* W, flo
     if (M <= 64 && K % 16 == 0)
         return launch_proj_multi(A, AEGIST_BF16, K, AEGIST_BF16, n, (const void* const*)W, nullptr, Y, ldy, N, M, K, 0,
                                  stream);
+    // up to three weights in one tiled-GEMM launch (stacked along N): the narrow ones (the
+    // DeltaNet b / a rows, 32 each) then ride in the last column tile of a wide one instead of
+    // taking a whole launch of mostly idle 256-column tiles each
+    bool one = n <= 3;
+    for (int i = 0; i < n && one; i++) one = gemm_bf16_fits(A, K, W[i], K, M, N[i], K) && (i == n - 1 || N[i] % 8 == 0);
+    if (one) {
+        const long long ldw[3] = {K, K, K};
+        return launch_gemm_bf16_multi(A, K, n, W, ldw, Y, ldy, N, M, K, 0, stream);
+    }
     for (int i = 0; i < n; i++) {
         int rc = gemm(s, A, W[i], Y[i], M, N[i], K, (int)ldy[i], 0.f, stream);
         if (rc) return rc;
@@ -157,18 +174,40 @@ int gemm_group(Stack* s, const uint16_t* A, int n, const uint16_t* const* W, flo
         if (_r) return _r;     \
     } while (0)
 
+// AEGIST_GEMM_CONV=0 keeps the short convolution in its own launch (A/B runs, parity tests).
+bool conv_gemm_enabled() {
+    const char* e = getenv("AEGIST_GEMM_CONV");
+    return !(e && e[0] == '0');
+}
+
 int delta_layer(Stack* s, const AegistLayerWeights& w, int sl, float* x, int B, int T, hipStream_t st) {
     const AegistStackConfig& c = s->cfg;
     const int rows = B * T, C = s->C(), HV = c.hv, HK = c.hk, dm = c.d_model;
     const size_t mb = (size_t)c.max_batch;
     float* conv = s->conv + (size_t)sl * mb * C * 3;
     float* rec = s->rec + (size_t)sl * mb * HV * D * D;
-    {
+    // prefill in whole 256-token tiles: the qkv projection's GEMM applies the short convolution
+    // and SiLU in its epilogue (the raw projection never reaches HBM; s->proj holds the tiles'
+    // edge rows instead)
+    const bool conv_fused = T > 1 && conv_gemm_enabled() && gemm_conv_fits(s->hb, dm, w.w_qkv, dm, w.conv_w, B, T, C, dm);
+    if (conv_fused) {
+        RC(launch_gemm_bf16_conv(s->hb, dm, w.w_qkv, dm, w.conv_w, conv, s->y, C, s->proj, B, T, C, dm, st));
+        const uint16_t* W[3] = {w.w_z, w.w_b, w.w_a};
+        float* Y[3] = {s->z, s->ba, s->ba + HV};
+        const int N[3] = {HV * D, HV, HV};
+        const long long ldy[3] = {HV * D, 2 * HV, 2 * HV};
+        RC(gemm_group(s, s->hb, 3, W, Y, N, ldy, rows, dm, st));
+    } else {
         const uint16_t* W[4] = {w.w_qkv, w.w_z, w.w_b, w.w_a};
         float* Y[4] = {s->proj, s->z, s->ba, s->ba + HV};
         const int N[4] = {C, HV * D, HV, HV};
         const long long ldy[4] = {C, HV * D, 2 * HV, 2 * HV};
-        RC(gemm_group(s, s->hb, 4, W, Y, N, ldy, rows, dm, st));
+        if (rows <= 64) {
+            RC(gemm_group(s, s->hb, 4, W, Y, N, ldy, rows, dm, st));
+        } else {
+            RC(gemm_group(s, s->hb, 1, W, Y, N, ldy, rows, dm, st));
+            RC(gemm_group(s, s->hb, 3, W + 1, Y + 1, N + 1, ldy + 1, rows, dm, st));
+        }
     }
     const float qscale = 1.f / sqrtf((float)D);
     if (T == 1) {
@@ -182,7 +221,7 @@ int delta_layer(Stack* s, const AegistLayerWeights& w, int sl, float* x, int B, 
     {
         // prefill: conv over the chunk, then the fp32 token-by-token scan below 64 tokens (the
         // engine scans every length, hybrid.rs:845-852), the chunked WY form from 64 tokens up
-        RC(launch_conv_silu_batched(s->proj, s->y, w.conv_w, conv, B, T, C, st));
+        if (!conv_fused) RC(launch_conv_silu_batched(s->proj, s->y, w.conv_w, conv, B, T, C, st));
         const long long sb = (long long)T * C, so_b = (long long)T * HV * D;
         if (T < 64)
             RC(aegist_delta_recurrent(s->y, s->y + (size_t)HK * D, s->y + (size_t)2 * HK * D, AEGIST_F32, sb, C, D, sb,

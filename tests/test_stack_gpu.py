@@ -133,3 +133,51 @@ def test_stack_head_ratios(dev, hk, hv):
         stack.close()
     finally:
         CFG = saved
+
+
+def test_stack_conv_fused_prefill(dev):
+    """Prefill in whole 256-token tiles runs the qkv projection with the short convolution in the
+    GEMM epilogue (the edge rows of every tile through a second launch, the conv state carried
+    across feeds). It must match the unfused path (AEGIST_GEMM_CONV=0: GEMM, then the conv launch)
+    bit for bit over a 512-token prefill, a 256-token continuation and two decode steps, and the
+    oracle to the stack bar."""
+    import os
+    B, cap = 2, 1024
+    layers, dl = make_layers(3, dev)
+    c = CFG
+    C = 2 * c["hk"] * 128 + c["hv"] * 128
+    nd, na = KINDS.count("delta"), KINDS.count("attn")
+    cache = {"length": 0,
+             "conv": [torch.zeros(B, C, 3) for _ in range(nd)],
+             "state": [torch.zeros(B, c["hv"], 128, 128) for _ in range(nd)],
+             "k": [torch.zeros(B, c["n_kv"], cap, 256, dtype=torch.bfloat16) for _ in range(na)],
+             "v": [torch.zeros(B, c["n_kv"], cap, 256, dtype=torch.bfloat16) for _ in range(na)]}
+    cache_p = {k: ([t.clone() for t in v] if isinstance(v, list) else v) for k, v in cache.items()}
+    fused = ops.HybridStack(c, KINDS, dl, max_batch=B, max_tokens=B * 512, max_context=cap)
+    plain = ops.HybridStack(c, KINDS, dl, max_batch=B, max_tokens=B * 512, max_context=cap)
+    g_ = torch.Generator().manual_seed(4)
+    feeds = [torch.randn(B, 512, c["d_model"], generator=g_), torch.randn(B, 256, c["d_model"], generator=g_),
+             torch.randn(B, 1, c["d_model"], generator=g_), torch.randn(B, 1, c["d_model"], generator=g_)]
+    old = os.environ.pop("AEGIST_GEMM_CONV", None)
+    try:
+        for i, x in enumerate(feeds):
+            print(f"feed {i}: {x.shape[1]} tokens", flush=True)
+            xa, xb = x.to(dev), x.to(dev)
+            fused.forward(xa)
+            os.environ["AEGIST_GEMM_CONV"] = "0"
+            plain.forward(xb)
+            del os.environ["AEGIST_GEMM_CONV"]
+            torch.cuda.synchronize()
+            assert torch.equal(xa, xb), (i, (xa - xb).abs().max().item())
+            if i < 3:
+                ref = R.hybrid_stack_forward(x.clone(), layers, KINDS, cache, c)
+                xp = perturb(x, 200 + i)
+                ref_p = R.hybrid_stack_forward(xp.clone(), layers, KINDS, cache_p, c)
+                check_stack_feed(xa.cpu() - x, ref - x, ref_p - xp, f"feed {i} ({x.shape[1]} tokens)")
+    finally:
+        if old is not None:
+            os.environ["AEGIST_GEMM_CONV"] = old
+        else:
+            os.environ.pop("AEGIST_GEMM_CONV", None)
+    fused.close()
+    plain.close()
