@@ -189,6 +189,16 @@ __global__ void __launch_bounds__(512, 1) gemm_bf16_kernel(const GemmArgs ga) {
     } else {
         // one segment, M a multiple of 256, no accumulation (the launcher checks). The previous
         // wave along M (wave - 2) publishes its last 16-row tile through LDS.
+        // the taps of the lane's 4 columns per 16-column group, requested before the exchange so
+        // their latency hides behind it (columns past N read column 0)
+        uint4 wq[8][2];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const int n = n0 + 128 * wn + 16 * i + 4 * g;
+            const uint16_t* wp = ga.conv_w + (size_t)(n < N ? n : 0) * 4;
+            wq[i][0] = *(const uint4*)wp;        // columns n, n + 1
+            wq[i][1] = *(const uint4*)(wp + 8);  // columns n + 2, n + 3
+        }
         __syncthreads();  // every wave is past its last LDS operand read
         // [8 i][64 lanes] per wave, waves 0..3 in A0 and 4..7 in B0 (32 KB each)
         auto xch = [&](int w, int i) { return (f32x4*)(w < 4 ? A0 : B0) + ((w % 4) * 8 + i) * WAVE; };
@@ -210,9 +220,7 @@ __global__ void __launch_bounds__(512, 1) gemm_bf16_kernel(const GemmArgs ga) {
         for (int i = 0; i < 8; i++) {
             const int n = n0 + 128 * wn + 16 * i + 4 * g;
             const bool nok = n < N;  // N is a multiple of 4
-            const int nc = nok ? n : 0;
-            const uint4 w01 = *(const uint4*)(ga.conv_w + (size_t)nc * 4);      // columns n, n + 1
-            const uint4 w23 = *(const uint4*)(ga.conv_w + (size_t)nc * 4 + 8);  // columns n + 2, n + 3
+            const uint4 w01 = wq[i][0], w23 = wq[i][1];
             float wt[4][4];
             {
                 const uint32_t wv[8] = {w01.x, w01.y, w01.z, w01.w, w23.x, w23.y, w23.z, w23.w};
