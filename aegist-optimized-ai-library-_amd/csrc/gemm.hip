@@ -159,30 +159,48 @@ __global__ void __launch_bounds__(512, 1) gemm_bf16_kernel(const GemmArgs ga) {
     // lane (c = r16, g) of tile (i, j) holds Y[m][n .. n + 3], m = m0 + 64 wm + 16 j + c,
     // n = n0 + 128 wn + 16 i + 4 g
     if constexpr (!kConv) {
+        // each lane's segment is picked by selects over the (uniform) segment fields: indexing
+        // the argument array by a lane value would read it from memory, one wait per access
+        const GemmSeg s0 = ga.seg[0], s1 = ga.seg[1], s2 = ga.seg[2];
+        const int b1 = ga.nseg > 1 ? s1.n0 : 0x7fffffff, b2 = ga.nseg > 2 ? s2.n0 : 0x7fffffff;
 #pragma unroll
         for (int i = 0; i < 8; i++) {
             const int n = n0 + 128 * wn + 16 * i + 4 * g;
             if (n >= N) continue;
-            int si = 0;
+            const bool in2 = n >= b2, in1 = !in2 && n >= b1;
+            float* const Yb = in2 ? s2.Y : in1 ? s1.Y : s0.Y;
+            const long long ldy = in2 ? s2.ldy : in1 ? s1.ldy : s0.ldy;
+            const int nl = n - (in2 ? b2 : in1 ? b1 : 0);  // 4-aligned; boundaries are multiples of 8
+            const int sN = in2 ? s2.N : in1 ? s1.N : s0.N;
+            const bool vec = (ldy % 4) == 0 && ((uintptr_t)Yb % 16) == 0 && nl + 3 < sN;
+            if (vec) {
+                // stores take their data straight from the accumulators, which nothing writes
+                // afterwards (a temporary would be reused by the next group and have to wait for
+                // the store to finish); the old values of the 4 rows are all requested first
+                if (ga.accumulate) {
+                    f32x4 old[4];
 #pragma unroll
-            for (int q = 1; q < kMaxGemmSeg; q++)
-                if (q < ga.nseg && n >= ga.seg[q].n0) si = q;
-            const GemmSeg& sg = ga.seg[si];
-            const int nl = n - sg.n0;  // 4-aligned; segment boundaries are multiples of 8
-            const bool vec = (sg.ldy % 4) == 0 && ((uintptr_t)sg.Y % 16) == 0 && nl + 3 < sg.N;
+                    for (int j = 0; j < 4; j++) {
+                        const int m = m0 + 64 * wm + 16 * j + r16;
+                        old[j] = m < M ? *(const f32x4*)(Yb + (size_t)m * ldy + nl) : f32x4{0.f, 0.f, 0.f, 0.f};
+                    }
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const int m = m0 + 64 * wm + 16 * j + r16;
-                if (m >= M) continue;
-                float* y = sg.Y + (size_t)m * sg.ldy + nl;
-                if (vec) {
-                    f32x4 v = acc[i][j];
-                    if (ga.accumulate) v += *(const f32x4*)y;
-                    *(f32x4*)y = v;
-                } else {
+                    for (int j = 0; j < 4; j++) acc[i][j] += old[j];
+                }
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const int m = m0 + 64 * wm + 16 * j + r16;
+                    if (m < M) *(f32x4*)(Yb + (size_t)m * ldy + nl) = acc[i][j];
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const int m = m0 + 64 * wm + 16 * j + r16;
+                    if (m >= M) continue;
+                    float* y = Yb + (size_t)m * ldy + nl;
 #pragma unroll
                     for (int e = 0; e < 4; e++)
-                        if (nl + e < sg.N) y[e] = (ga.accumulate ? y[e] : 0.f) + acc[i][j][e];
+                        if (nl + e < sN) y[e] = (ga.accumulate ? y[e] : 0.f) + acc[i][j][e];
                 }
             }
         }
