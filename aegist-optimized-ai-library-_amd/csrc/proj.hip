@@ -329,9 +329,9 @@ __global__ __launch_bounds__(64 * NWAVE) void proj_skinny_kernel(const TX* __res
 // each lane is permuted, the 1 KB it covers is not), so the 16 rows a fragment read touches
 // hit 16 different bank groups.
 constexpr int SKC = 256;  // k per chunk
-template <typename TX, int NW, int NS>
+template <typename TX, int NW, int NS, int MT = 1>
 struct StreamSmem {
-    static constexpr int XB = 16 * SKC * sizeof(TX);  // X bytes per stage (16 rows)
+    static constexpr int XB = 16 * MT * SKC * sizeof(TX);  // X bytes per stage (16 MT rows)
     __attribute__((aligned(16))) unsigned char w[NS][16 * NW][SKC * 2];
     __attribute__((aligned(16))) unsigned char x[NS][XB];
 };
@@ -356,15 +356,16 @@ __device__ __forceinline__ void wait_vm(int n) {
     }
 }
 
-template <typename TX, int NW, int NS>
+template <typename TX, int NW, int NS, int MT = 1>
 __global__ __launch_bounds__(64 * NW) void proj_stream_kernel(const TX* __restrict__ X, long long ldx,
                                                                const ProjSegs segs, int M, int K, int accumulate,
                                                                float* __restrict__ part) {
-    __shared__ StreamSmem<TX, NW, NS> sm;
+    static_assert(MT == 1 || sizeof(TX) == 2, "several m tiles take bf16 X only");
+    __shared__ StreamSmem<TX, NW, NS, MT> sm;
     constexpr int RW = 16 * NW;                       // W rows per workgroup
     constexpr int WI = RW / 2 / NW;                   // W load instructions per wave per stage (= 8)
-    constexpr int XI = StreamSmem<TX, NW, NS>::XB / 1024 / NW;  // X load instructions per wave per stage
-    static_assert(XI * NW * 1024 == StreamSmem<TX, NW, NS>::XB, "X stage must split evenly over the waves");
+    constexpr int XI = StreamSmem<TX, NW, NS, MT>::XB / 1024 / NW;  // X load instructions per wave per stage
+    static_assert(XI * NW * 1024 == StreamSmem<TX, NW, NS, MT>::XB, "X stage must split evenly over the waves");
     constexpr int PER = WI + XI;                      // loads per wave per stage
     const int lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
     const int r16 = lane % 16, g = lane / 16;
@@ -404,7 +405,9 @@ __global__ __launch_bounds__(64 * NW) void proj_stream_kernel(const TX* __restri
         }
     };
 
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    f32x4 acc[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int c = 0; c < NS - 1; c++)
         if (c < nch) issue(c);
@@ -421,8 +424,11 @@ __global__ __launch_bounds__(64 * NW) void proj_stream_kernel(const TX* __restri
             // k block i of the chunk: lane (row, g) takes slot 4 i + g of its row (swizzled)
             const bf16x8 a = *(const bf16x8*)&sm.w[st][row][((4 * i + g) ^ (row & 15)) * 16];
             if constexpr (sizeof(TX) == 2) {
-                const bf16x8 b = *(const bf16x8*)&sm.x[st][(r16 * SKC + 32 * i + 8 * g) * 2];
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0, 0);
+#pragma unroll
+                for (int mt = 0; mt < MT; mt++) {
+                    const bf16x8 b = *(const bf16x8*)&sm.x[st][((16 * mt + r16) * SKC + 32 * i + 8 * g) * 2];
+                    acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc[mt], 0, 0, 0);
+                }
             } else {
                 const float* xp = (const float*)&sm.x[st][(r16 * SKC + 32 * i + 8 * g) * 4];
                 const f32x4 x0 = *(const f32x4*)xp, x1 = *(const f32x4*)(xp + 4);
@@ -437,41 +443,63 @@ __global__ __launch_bounds__(64 * NW) void proj_stream_kernel(const TX* __restri
                                    v1 - __uint_as_float(__float_as_uint(v1) & 0xffff0000u)};
                     l[e] = __builtin_bit_cast(uint32_t, __builtin_convertvector(lo, b2));
                 }
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, __builtin_bit_cast(bf16x8, h), acc, 0, 0, 0);
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, __builtin_bit_cast(bf16x8, l), acc, 0, 0, 0);
+                acc[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, __builtin_bit_cast(bf16x8, h), acc[0], 0, 0, 0);
+                acc[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, __builtin_bit_cast(bf16x8, l), acc[0], 0, 0, 0);
             }
         }
     }
-    // lane (m = r16, g) holds Y[m][n0 + 16 wave + 4 g .. +3]
-    const int m = r16, nb = n0 + 16 * wave + 4 * g;
-    if (part) {
-        if (m < M && nb < N) {
+    // lane (m = 16 mt + r16, g) of tile mt holds Y[m][n0 + 16 wave + 4 g .. +3]
+    const int nb = n0 + 16 * wave + 4 * g;
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++) {
+        const int m = 16 * mt + r16;
+        if (m >= M || nb >= N) continue;
+        if (part) {
             float* pp = part + ((size_t)ks * M + m) * N + nb;
             if (nb + 3 < N && (N % 4) == 0) {
-                *(f32x4*)pp = acc;
+                *(f32x4*)pp = acc[mt];
             } else {
 #pragma unroll
                 for (int j = 0; j < 4; j++)
-                    if (nb + j < N) pp[j] = acc[j];
+                    if (nb + j < N) pp[j] = acc[mt][j];
             }
+            continue;
         }
-        return;
-    }
-    if (m < M && nb < N) {
         float* yp = Y + (size_t)m * ldy + nb;
         if (nb + 3 < N && ((uintptr_t)yp % 16) == 0) {
-            f32x4 v = acc;
+            f32x4 v = acc[mt];
             if (accumulate) v += *(const f32x4*)yp;
             *(f32x4*)yp = v;
         } else {
 #pragma unroll
             for (int j = 0; j < 4; j++)
-                if (nb + j < N) yp[j] = (accumulate ? yp[j] : 0.f) + acc[j];
+                if (nb + j < N) yp[j] = (accumulate ? yp[j] : 0.f) + acc[mt][j];
         }
     }
 }
 
-template <typename TX, int NW, int NS>
+// Y[m][n] (+)= sum over ks = 0 .. nks - 1, in that order, of part[ks][m][n] (the split-K slices
+// of proj_stream_kernel); 4 columns per thread, N % 4 == 0.
+__global__ void proj_splitk_reduce_kernel(const float* __restrict__ part, int nks, int M, int N, float* __restrict__ Y,
+                                          long long ldy, int accumulate) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x, n4 = N / 4;
+    if (i >= M * n4) return;
+    const int m = i / n4, n = 4 * (i % n4);
+    const size_t slice = (size_t)M * N;
+    const float* p = part + (size_t)m * N + n;
+    f32x4 v = *(const f32x4*)p;
+    for (int k = 1; k < nks; k++) v += *(const f32x4*)(p + k * slice);
+    float* y = Y + (size_t)m * ldy + n;
+    if (((uintptr_t)y % 16) == 0) {
+        if (accumulate) v = *(const f32x4*)y + v;
+        *(f32x4*)y = v;
+    } else {
+#pragma unroll
+        for (int j = 0; j < 4; j++) y[j] = (accumulate ? y[j] : 0.f) + v[j];
+    }
+}
+
+template <typename TX, int NW, int NS, int MT = 1>
 int launch_stream(const TX* X, long long ldx, ProjSegs segs, int M, int K, int accumulate, hipStream_t st,
                   float* part = nullptr, int nks = 1) {
     int t = 0;
@@ -480,7 +508,7 @@ int launch_stream(const TX* X, long long ldx, ProjSegs segs, int M, int K, int a
         t += (segs.s[i].N + 16 * NW - 1) / (16 * NW);
     }
     segs.tile0[segs.n] = t;
-    proj_stream_kernel<TX, NW, NS><<<dim3(t, nks), 64 * NW, 0, st>>>(X, ldx, segs, M, K, accumulate, part);
+    proj_stream_kernel<TX, NW, NS, MT><<<dim3(t, nks), 64 * NW, 0, st>>>(X, ldx, segs, M, K, accumulate, part);
     return 0;
 }
 
@@ -566,6 +594,33 @@ int run_proj(const TX* X, long long ldx, const ProjSegs& segs, int M, int K, int
         if (M <= 16 && K % SKC == 0 && !scaled && tiles > 256 && stream_enabled()) {
             launch_stream<TX, 2, 2>(X, ldx, segs, M, K, accumulate, st);
             return after_launch("proj_stream");
+        }
+        // 17..64 rows of bf16 X and one weight whose rows give too few workgroups (2048 x 4096:
+        // 64 workgroups of 32 rows): the same stream with all the rows' X staged once per chunk,
+        // split over K into ~256 workgroups when the calling thread has bound a workspace for
+        // the fp32 partials, which a second launch adds in slice order (deterministic). Measured
+        // at M = 64: 2048 x 4096 21.2 -> 13.7 us; with enough rows (8192 x 2048 and the stack's
+        // grouped input projections) the row-tile kernel below is as fast, so it keeps them.
+        if constexpr (std::is_same<TX, uint16_t>::value) {
+            const long long t = (segs.s[0].N + 31) / 32;
+            if (M > 16 && M <= 64 && K % SKC == 0 && !scaled && segs.n == 1 && t < 192 && segs.s[0].N % 4 == 0 &&
+                stream_enabled()) {
+                const int nks = (int)std::min<long long>(K / SKC, (256 + t - 1) / t);
+                size_t bound = 0;
+                void* ws = bound_workspace(&bound);
+                if (nks > 1 && ws && bound >= (size_t)nks * M * segs.s[0].N * 4) {
+                    float* part = (float*)ws;
+                    if (M <= 32) launch_stream<TX, 2, 2, 2>(X, ldx, segs, M, K, accumulate, st, part, nks);
+                    else launch_stream<TX, 2, 2, 4>(X, ldx, segs, M, K, accumulate, st, part, nks);
+                    int rc = after_launch("proj_stream64");
+                    if (rc) return rc;
+                    const ProjSeg& sg = segs.s[0];
+                    const int nthr = M * (sg.N / 4);
+                    proj_splitk_reduce_kernel<<<(nthr + 255) / 256, 256, 0, st>>>(part, nks, M, sg.N, sg.Y, sg.ldy,
+                                                                                 accumulate);
+                    return after_launch("proj_splitk_reduce");
+                }
+            }
         }
     }
     // m tiles per workgroup: the whole batch up to 64 rows of bf16 X (32 of fp32 X, whose hi/lo

@@ -493,9 +493,12 @@ def bench_proj(torch, ops, dev, reps=3):
     ships them; bf16 weights with bf16 activations, as config 4 runs them). The timed loop walks
     a ring of distinct weight matrices totalling > 1 GB so that every launch streams its weights
     from HBM, as a 40-layer decode step does (a single 17-67 MB matrix would sit in the MALL).
-    Bytes per launch = W + X + Y."""
+    Bytes per launch = W + X + Y. A workspace is bound on the calling thread (as the engine binds
+    its scratch), which lets 17..64 rows against a weight of few rows split K."""
     from aegist_mixer._lib import BF16, F32, I8, call
     stream = torch.cuda.current_stream().cuda_stream
+    ws = torch.empty(16 << 20, device=dev, dtype=torch.uint8)
+    call("aegist_bind_workspace", ws.data_ptr(), ws.numel())
     out = []
     for wdt, xdt, N, K in [(I8, F32, 8192, 2048), (BF16, BF16, 8192, 2048), (BF16, BF16, 2048, 4096)]:
         wbytes = N * K * (1 if wdt == I8 else 2)
@@ -531,8 +534,10 @@ def bench_proj(torch, ops, dev, reps=3):
                         "K": K, "us": round(us, 2), "GB_s": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)})
         del Ws
         torch.cuda.empty_cache()
-    return {"workload": "decode projections Y[M,N] = X[M,K] W[N,K]^T (x scale), weights streamed from HBM",
-            "points": out}
+    call("aegist_bind_workspace", None, 0)
+    del ws
+    return {"workload": "decode projections Y[M,N] = X[M,K] W[N,K]^T (x scale), weights streamed from HBM "
+                        "(16 MB workspace bound)", "points": out}
 
 
 def bench_moe(torch, ops, dev, reps=3):

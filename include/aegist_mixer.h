@@ -358,7 +358,12 @@ int aegist_gemv_bf16(const float* x, const uint16_t* W, float* y, int N, int K, 
 int aegist_gemm_i8(const float* X, const int8_t* W, const uint16_t* scale, float* Y, int M, int N, int K,
                    int accumulate, void* stream);
 /* Strided form of the three above: X dtype AEGIST_F32 | AEGIST_BF16 (row stride ldx elements),
- * W dtype AEGIST_I8 | AEGIST_BF16, scale NULL = 1, Y fp32 with row stride ldy. */
+ * W dtype AEGIST_I8 | AEGIST_BF16, scale NULL = 1, Y fp32 with row stride ldy. 17..64 rows of
+ * bf16 X against one bf16 weight of under 6144 rows (K % 256 == 0, N % 4 == 0, no scale) split
+ * K when the calling thread has bound a workspace (aegist_bind_workspace) of at least
+ * splits * M * N * 4 bytes (splits <= 256 * 32 / N, at most K / 256): fp32 partials, added in
+ * slice order by a second launch (deterministic; the same result to fp32 rounding as the
+ * unsplit kernel, which runs otherwise). */
 int aegist_linear(const void* X, int x_dtype, long long ldx, const void* W, int w_dtype, const uint16_t* scale,
                   float* Y, long long ldy, int M, int N, int K, int accumulate, void* stream);
 /* Grouped form: n (1..4) weight matrices W[i] [N[i], K] of one dtype that share the input X

@@ -152,3 +152,35 @@ def test_linear_multi_streamed_layer_group(dev):
     torch.cuda.synchronize()
     for w, o in zip(wb, outs):
         assert rel_err(o, R.qlinear_engine(xb.float(), w.float(), None)) < TOL_BF16X
+
+
+@pytest.mark.parametrize("M,N,K,acc", [(64, 2048, 4096, False), (64, 2048, 4096, True), (33, 1000, 2048, True),
+                                       (17, 2048, 512, False), (40, 4096, 768, False)])
+def test_linear_bf16_splitk_bound_workspace(dev, M, N, K, acc):
+    """17..64 rows of bf16 X against one bf16 weight of few rows split K over the calling thread's
+    bound workspace (fp32 partials added in slice order by a second launch): same bar against the
+    oracle, deterministic from call to call, and the same as the unbound path to fp32 rounding."""
+    from aegist_mixer._lib import call
+    print(f"linear bf16 split-K M={M} N={N} K={K} acc={acc}", flush=True)
+    g = torch.Generator().manual_seed(M * 13 + N + K)
+    w = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16)
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    y0 = torch.randn(M, N, generator=g)
+    ref = R.qlinear_engine(x.float(), w.float(), None) + (y0 if acc else 0)
+    xd, wd = x.to(dev), w.to(dev)
+    plain = y0.to(dev)
+    ops.linear(xd, wd, out=plain, accumulate=acc)
+    ws = torch.empty(16 << 20, device=dev, dtype=torch.uint8)
+    call("aegist_bind_workspace", ws.data_ptr(), ws.numel())
+    try:
+        outs = []
+        for _ in range(2):
+            out = y0.to(dev)
+            ops.linear(xd, wd, out=out, accumulate=acc)
+            outs.append(out)
+        torch.cuda.synchronize()
+    finally:
+        call("aegist_bind_workspace", None, 0)
+    assert torch.equal(outs[0], outs[1])
+    assert rel_err(outs[0], ref) < TOL_BF16X
+    assert rel_err(outs[0], plain) < 1e-6
