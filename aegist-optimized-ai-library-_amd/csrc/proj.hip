@@ -31,6 +31,9 @@ int launch_gemm_i8f32(const float* X, long long ldx, const int8_t* W, long long 
                       long long ldy, int M, int N, int K, int accumulate, hipStream_t st);
 int launch_gemm_bf16(const uint16_t* X, long long ldx, const uint16_t* W, long long ldw, float* Y, long long ldy, int M,
                      int N, int K, int accumulate, hipStream_t st);
+int launch_gemm_bf16_multi(const uint16_t* X, long long ldx, int nseg, const uint16_t* const* W, const long long* ldw,
+                           float* const* Y, const long long* ldy, const int* N, int M, int K, int accumulate,
+                           hipStream_t st);
 }  // namespace aegist
 
 namespace {
@@ -566,11 +569,28 @@ int run_proj(const TX* X, long long ldx, const ProjSegs& segs, int M, int K, int
             return 0;
         }
     }
-    // bf16 weights and activations past 64 rows: the tiled MFMA GEMM, one launch per weight
+    // bf16 weights and activations past 64 rows: the tiled MFMA GEMM, all weights in one launch
+    // (stacked along N) when each but the last has a multiple of 8 rows, else one launch each
     if constexpr (std::is_same<TW, uint16_t>::value && std::is_same<TX, uint16_t>::value) {
-        bool ok = M > 64;
-        for (int i = 0; i < segs.n && ok; i++)
+        bool ok = M > 64, stack8 = segs.n <= 3;
+        for (int i = 0; i < segs.n && ok; i++) {
             ok = segs.s[i].scale == nullptr && gemm_bf16_fits(X, ldx, segs.s[i].W, K, M, segs.s[i].N, K);
+            if (i + 1 < segs.n && segs.s[i].N % 8) stack8 = false;
+        }
+        if (ok && stack8) {
+            const uint16_t* W[MAX_SEG];
+            float* Y[MAX_SEG];
+            long long ldw[MAX_SEG], ldy[MAX_SEG];
+            int N[MAX_SEG];
+            for (int i = 0; i < segs.n; i++) {
+                W[i] = (const uint16_t*)segs.s[i].W;
+                Y[i] = segs.s[i].Y;
+                ldw[i] = K;
+                ldy[i] = segs.s[i].ldy;
+                N[i] = segs.s[i].N;
+            }
+            return launch_gemm_bf16_multi(X, ldx, segs.n, W, ldw, Y, ldy, N, M, K, accumulate, st);
+        }
         if (ok) {
             for (int i = 0; i < segs.n; i++) {
                 int rc = launch_gemm_bf16(X, ldx, (const uint16_t*)segs.s[i].W, K, segs.s[i].Y, segs.s[i].ldy, M,

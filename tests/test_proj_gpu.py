@@ -138,6 +138,23 @@ def test_linear_multi_matches_separate(dev, M):
         assert rel_err(o, R.qlinear_engine(xb.float(), w.float(), None)) < TOL_BF16X
 
 
+@pytest.mark.parametrize("Ns", [[264, 40, 302], [100, 64], [8, 8, 1000]])
+def test_linear_multi_stacked_gemm(dev, Ns):
+    """Past 64 rows, bf16 weights sharing X run as one tiled-GEMM launch stacked along N when every
+    weight but the last has a multiple of 8 rows (segment boundaries inside a 256-column tile, a
+    ragged last segment, three segments in one tile), else one launch per weight: each output
+    equal to the oracle per weight."""
+    print(f"linear_multi stacked GEMM Ns={Ns}", flush=True)
+    g = torch.Generator().manual_seed(sum(Ns))
+    K, M = 512, 300
+    wb = [(torch.randn(n, K, generator=g) * 0.02).to(torch.bfloat16) for n in Ns]
+    xb = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    outs = ops.linear_multi(xb.to(dev), [w.to(dev) for w in wb])
+    torch.cuda.synchronize()
+    for w, o in zip(wb, outs):
+        assert rel_err(o, R.qlinear_engine(xb.float(), w.float(), None)) < TOL_BF16X
+
+
 def test_linear_multi_streamed_layer_group(dev):
     """A DeltaNet layer's input group at config-4 width (in_qkv 8192, in_z 4096, in_b 32,
     in_a 32 rows over K 2048, bf16 weights and activations, M = 16): one stream-kernel launch,
