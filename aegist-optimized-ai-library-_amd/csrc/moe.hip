@@ -37,6 +37,7 @@ using namespace aegist;
 namespace {
 
 constexpr int PB = 32;            // picks per expert tile (two 16-column MFMA tiles)
+constexpr int PBB = 64;           // picks per big (prefill) tile: four 16-column MFMA tiles
 constexpr int RB = 64;            // output rows per workgroup (4 waves x 16)
 constexpr int MAX_E = 1024;       // experts per layer the grouping kernel handles
 
@@ -135,10 +136,11 @@ __global__ void __launch_bounds__(256) router_topk_kernel(const float* __restric
 // ---------------------------------------------------------------------------------------------
 // Grouping (one workgroup of 1024 threads): picks i = t K + k with expert idx[i]; out of range
 // experts are dropped and counted. eoff[E + 1]: exclusive prefix of the counts; ptok / psrc:
-// token and pick index of each grouped position. An expert's positions are cut into blocks of
-// PB; blocks of <= 16 positions go to tiles1 (meta[0] of them), larger ones to tiles2
-// (meta[2]), as (expert, p0, p1). meta[1] = dropped picks. The order of positions inside an
-// expert is unspecified (atomics); no result depends on it.
+// token and pick index of each grouped position. An expert's positions are cut into blocks
+// (moe_group_kernel): blocks of <= 16 positions go to tiles1 (meta[0] of them), of 17..32 to
+// tiles2 (meta[2]), of up to 64 to tiles3 (meta[3]), as (expert, p0, p1). meta[1] = dropped
+// picks. The order of positions inside an expert is unspecified (atomics); no result depends on
+// it (every pick's sums run in the same order whatever tile it lands in with whom).
 __device__ __forceinline__ int block_excl_scan(int v, int* wsum, int* total) {
     const int lane = threadIdx.x % WAVE, w = threadIdx.x / WAVE, nw = blockDim.x / WAVE;
     int x = v;
@@ -159,11 +161,15 @@ __device__ __forceinline__ int block_excl_scan(int v, int* wsum, int* total) {
     return off + x - v;
 }
 
+// Tiles: with `big3` set, an expert with more than 32 picks has them all in ceil(c / 64) blocks
+// of balanced size (tiles3, 33..64 picks each but for c = 65..95: 32..48); otherwise blocks of
+// PB = 32 (tiles2) and a last one of <= 16 (tiles1).
 __global__ void __launch_bounds__(1024) moe_group_kernel(const int* __restrict__ idx, int N, int K, int E,
                                                          const unsigned long long* __restrict__ eptr,
                                                          int* __restrict__ eoff, int* __restrict__ ptok,
                                                          int* __restrict__ psrc, MoeTile* __restrict__ tiles1,
-                                                         MoeTile* __restrict__ tiles2, int* __restrict__ meta) {
+                                                         MoeTile* __restrict__ tiles2, MoeTile* __restrict__ tiles3,
+                                                         int big3, int* __restrict__ meta) {
     __shared__ int cnt[MAX_E], cur[MAX_E], wsum[16], bad;
     const int tid = threadIdx.x;
     for (int e = tid; e < MAX_E; e += blockDim.x) cnt[e] = 0;
@@ -175,18 +181,23 @@ __global__ void __launch_bounds__(1024) moe_group_kernel(const int* __restrict__
         else atomicAdd(&bad, 1);
     }
     __syncthreads();
-    const int c = tid < E ? cnt[tid] : 0, rem = c % PB;
+    const int c = tid < E ? cnt[tid] : 0;
+    const int n3 = big3 && c > 32 ? (c + PBB - 1) / PBB : 0;
+    const int c3 = n3 > 0 ? c : 0, cr = c - c3, rem = cr % PB;
     const int small = rem > 0 && rem <= 16 ? 1 : 0;      // the last block, if it is small
-    const int big = c / PB + (rem > 16 ? 1 : 0);         // full blocks and a large last block
-    int tot_c, tot_1, tot_2;
+    const int big = cr / PB + (rem > 16 ? 1 : 0);        // full blocks and a large last block
+    int tot_c, tot_1, tot_2, tot_3;
     const int off = block_excl_scan(c, wsum, &tot_c);
     const int off1 = block_excl_scan(small, wsum, &tot_1);
     const int off2 = block_excl_scan(big, wsum, &tot_2);
+    const int off3 = block_excl_scan(n3, wsum, &tot_3);
     if (tid < E) {
         eoff[tid] = off;
         cur[tid] = off;
         const unsigned long long base = c > 0 ? eptr[tid] : 0ull;
-        for (int j = 0; j < big; j++) tiles2[off2 + j] = MoeTile{base, off + j * PB, off + min(c, (j + 1) * PB)};
+        for (int j = 0; j < n3; j++) tiles3[off3 + j] = MoeTile{base, off + c3 * j / n3, off + c3 * (j + 1) / n3};
+        for (int j = 0; j < big; j++)
+            tiles2[off2 + j] = MoeTile{base, off + c3 + j * PB, off + c3 + min(cr, (j + 1) * PB)};
         if (small) tiles1[off1] = MoeTile{base, off + c - rem, off + c};
     }
     if (tid == 0) {
@@ -194,6 +205,7 @@ __global__ void __launch_bounds__(1024) moe_group_kernel(const int* __restrict__
         meta[0] = tot_1;
         meta[1] = bad;
         meta[2] = tot_2;
+        meta[3] = tot_3;
     }
     __syncthreads();
     for (int i = tid; i < N; i += blockDim.x) {
@@ -555,6 +567,268 @@ __global__ void __launch_bounds__(256, 2) moe_down_kernel(const MoeTile* __restr
     }
 }
 
+// ---------------------------------------------------------------------------------------------
+// Prefill-sized tiles (up to 64 picks of an expert with more than 32): a workgroup of 8 waves covers UB = 256 rows
+// of the output (gate / up: 256 units, i.e. 256 gate and 256 up rows; down: 256 output rows) for
+// all the tile's picks. Each wave owns 32 rows of every matrix (RT 16-row tiles in all) and walks
+// the 64-groups in order; the picks' activations of one group (hi and lo, 64 picks x 64 values)
+// are staged once per workgroup in LDS by direct global -> LDS loads (double-buffered, 16-byte
+// slots XOR-swizzled by the pick row), so each activation byte is fetched once per workgroup and
+// each code byte once per tile, against once per 32 picks and once per 16 rows in the kernels
+// above. Per group and row tile the 4 x 2 x 2 products on the group's codes give P, and the lane
+// adds s P + (m - 128 s) X into its accumulators, the same fp32 formula as expert_block.
+constexpr int UB = 256;  // rows per matrix per big workgroup (8 waves x 32)
+
+// Rows of sc and gs are padded by one word so that the rows one read touches (4 apart in sc, 1
+// apart in gs) fall in different banks.
+struct BigSmem {
+    uint32_t sc[2 * UB * 33];                // (s | m << 16) fp16 pairs, [matrix row][group], G <= 32
+    float gs[PBB * 65];                      // activation group sums [pick][group], G <= 64
+};
+constexpr int kActBytes = 2 * PBB * 128;     // one group's activations: hi, lo x 64 picks x 128 B
+
+// Stage (s, m) pairs of nrow rows (row0 .. row0 + nrow) x G groups as packed fp16 pairs, rows
+// G + 1 words apart.
+__device__ __forceinline__ void stage_sc_packed(uint32_t* sc, const uint16_t* __restrict__ s,
+                                                const uint16_t* __restrict__ mn, long long row0, int nrow, int G) {
+    const uint16_t* s0 = s + (size_t)row0 * G;
+    const uint16_t* m0 = mn + (size_t)row0 * G;
+    const int n8 = nrow * G / 8;
+    typedef uint32_t u4v __attribute__((ext_vector_type(4)));
+    for (int i = threadIdx.x; i < n8; i += blockDim.x) {
+        const u4v sv = ld_global<u4v>(s0 + 8 * i), mv = ld_global<u4v>(m0 + 8 * i);
+        const uint32_t sw[4] = {sv.x, sv.y, sv.z, sv.w}, mw[4] = {mv.x, mv.y, mv.z, mv.w};
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const int k = 8 * i + e;  // row k / G, group k % G
+            sc[k + k / G] = ((sw[e / 2] >> (16 * (e & 1))) & 0xffffu) | (((mw[e / 2] >> (16 * (e & 1))) & 0xffffu) << 16);
+        }
+    }
+}
+
+// The big-tile block: RT row tiles per wave (codes of row tile rt at code row qrow[rt] + lane n,
+// scales at LDS row srow[rt] + .. of sc), activations of pick rows xrow(p) (element offset of the
+// pick's row in xh / xl), groups [0, G). acc[rt][t]: lane (n, g) holds rows 4 g + j, pick 16 t + n.
+template <int RT>
+__device__ __forceinline__ void big_block(const unsigned char* __restrict__ qbase, const long long (&qrow)[RT],
+                                          const int (&srow)[RT], int Kdim, const uint16_t* __restrict__ xh,
+                                          const uint16_t* __restrict__ xl, const long long* __restrict__ xrow8,
+                                          const uint32_t* sc, const float* gs, int G, unsigned char* act0,
+                                          unsigned char* act1, f32x4 (&acc)[RT][4]) {
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid / WAVE), lane = tid % WAVE;
+    const int n = lane % 16, g = lane / 16;
+#pragma unroll
+    for (int rt = 0; rt < RT; rt++)
+#pragma unroll
+        for (int t = 0; t < 4; t++) acc[rt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const size_t rowbytes = Kdim / 2;
+    const unsigned char* arow[RT];
+#pragma unroll
+    for (int rt = 0; rt < RT; rt++) arow[rt] = qbase + (size_t)(qrow[rt] + n) * rowbytes + 8 * g;
+    typedef uint32_t u2v __attribute__((ext_vector_type(2)));
+    // activation pieces: 16 per group (8 per array, 8 picks x 128 B each), 2 per wave; lane L of
+    // piece q (pick 8 (q % 8) + L / 8) fetches the global 16-byte slot (L % 8) ^ sw(pick) so that
+    // LDS slot L % 8 of the pick's row holds it
+    const int q0 = 2 * wave, pk0 = 8 * (q0 % 8) + lane / 8, pk1 = 8 * ((q0 + 1) % 8) + lane / 8;
+    const int sl0 = ((lane % 8) ^ ((pk0 >> 1) & 7)) * 8, sl1 = ((lane % 8) ^ ((pk1 >> 1) & 7)) * 8;
+    const uint16_t* src0 = (q0 < 8 ? xh : xl) + xrow8[pk0] + sl0;
+    const uint16_t* src1 = (q0 + 1 < 8 ? xh : xl) + xrow8[pk1] + sl1;
+    typedef __attribute__((address_space(3))) void lds_void;
+    auto stage = [&](unsigned char* buf, int grp) {
+        __builtin_amdgcn_global_load_lds(src0 + 64 * grp, (lds_void*)(buf + q0 * 1024), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(src1 + 64 * grp, (lds_void*)(buf + (q0 + 1) * 1024), 16, 0, 0);
+    };
+    // codes of group grp for every row tile (ring of 2 groups)
+    u2v ar[2][RT];
+#pragma unroll
+    for (int u = 0; u < 2; u++)
+#pragma unroll
+        for (int rt = 0; rt < RT; rt++) ar[u][rt] = ld_global<u2v>(arow[rt] + 32 * min(u, G - 1));
+    stage(act0, 0);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    auto group = [&](const unsigned char* cur, unsigned char* nxt, int grp, int slot) {
+        if (grp + 1 < G) stage(nxt, grp + 1);
+        // this group's activation fragments: pick tile t, k step ks: LDS slot (2 g + ks) ^ sw(row)
+        bf16x8 bh[4][2], bl[4][2];
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const int row = 16 * t + n;
+#pragma unroll
+            for (int ks = 0; ks < 2; ks++) {
+                const int off = row * 128 + (((2 * g + ks) ^ ((row >> 1) & 7)) * 16);
+                bh[t][ks] = *(const bf16x8*)(cur + off);
+                bl[t][ks] = *(const bf16x8*)(cur + PBB * 128 + off);
+            }
+        }
+        float X[4];
+#pragma unroll
+        for (int t = 0; t < 4; t++) X[t] = gs[(16 * t + n) * (G + 1) + grp];
+#pragma unroll
+        for (int rt = 0; rt < RT; rt++) {
+            const u2v a2 = ar[slot][rt];
+            f32x4 P[4];
+#pragma unroll
+            for (int t = 0; t < 4; t++) P[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < 2; ks++) {
+                const bf16x8 a = codes_bf16(ks ? a2.y : a2.x);
+#pragma unroll
+                for (int t = 0; t < 4; t++) {
+                    P[t] = mfma_bf(a, bh[t][ks], P[t]);
+                    P[t] = mfma_bf(a, bl[t][ks], P[t]);
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const uint32_t pr = sc[(srow[rt] + 4 * g + j) * (G + 1) + grp];
+                const float sv = h2f((uint16_t)(pr & 0xffffu)), mv = h2f((uint16_t)(pr >> 16));
+                const float mp = mv - 128.f * sv;
+#pragma unroll
+                for (int t = 0; t < 4; t++) acc[rt][t][j] = fmaf(sv, P[t][j], fmaf(mp, X[t], acc[rt][t][j]));
+            }
+        }
+        // refill this ring slot with the codes two groups ahead (clamped: static wait counts)
+#pragma unroll
+        for (int rt = 0; rt < RT; rt++) ar[slot][rt] = ld_global<u2v>(arow[rt] + 32 * min(grp + 2, G - 1));
+        // the next group's direct loads are older than the RT code loads just issued
+        __builtin_amdgcn_s_waitcnt((RT & 15) | (7 << 4) | (15 << 8));
+        __syncthreads();
+    };
+    int grp = 0;
+    for (; grp + 2 <= G; grp += 2) {
+        group(act0, act1, grp, 0);
+        group(act1, act0, grp + 1, 1);
+    }
+    if (grp < G) group(act0, act1, grp, 0);
+}
+
+// Gate / up for big tiles: units [256 ub, 256 ub + 256) x one tile of <= 64 picks. act as in
+// moe_gate_up_kernel (bf16 hi / lo in chunk order, group sums over 64 units).
+__global__ void __launch_bounds__(512, 1) moe_gate_up_big_kernel(const MoeTile* __restrict__ tiles,
+                                                              const int* __restrict__ ntiles,
+                                                              const int* __restrict__ ptok,
+                                                              const uint16_t* __restrict__ xh,
+                                                              const uint16_t* __restrict__ xl,
+                                                              const float* __restrict__ xs, int D, int I,
+                                                              ExpertOffsets off, uint16_t* __restrict__ ah,
+                                                              uint16_t* __restrict__ al, float* __restrict__ as) {
+    __shared__ BigSmem sm;
+    __shared__ __attribute__((aligned(1024))) unsigned char act0[kActBytes];
+    __shared__ __attribute__((aligned(1024))) unsigned char act1[kActBytes];
+    __shared__ float red[8][PBB];
+    __shared__ long long xrow8[PBB];
+    const int ub = blockIdx.x, tile = blockIdx.y;
+    const MoeTile tl = tiles[tile];
+    if (tile >= *ntiles) return;
+    const int G = D / 64, u0 = ub * UB;
+    const int p0 = tl.p0, np = tl.p1 - tl.p0;
+    const unsigned char* base = (const unsigned char*)tl.base;
+    const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE, n = lane % 16, g = lane / 16;
+    // picks past the tile repeat its last one (their results are not stored)
+    if (tid < PBB) xrow8[tid] = (long long)ptok[p0 + min(tid, np - 1)] * D;
+    stage_sc_packed(sm.sc, (const uint16_t*)(base + off.gu_s), (const uint16_t*)(base + off.gu_m), u0, UB, G);
+    stage_sc_packed(sm.sc + UB * (G + 1), (const uint16_t*)(base + off.gu_s), (const uint16_t*)(base + off.gu_m),
+                    I + u0, UB, G);
+    for (int i = tid; i < PBB * G; i += blockDim.x) {
+        const int pr = i / G, c = i % G;
+        sm.gs[pr * (G + 1) + c] = xs[(size_t)ptok[p0 + min(pr, np - 1)] * G + c];
+    }
+    __syncthreads();
+    // wave w: units u0 + 32 w .. + 32: gate row tiles 0, 1 and up row tiles 2, 3
+    const int wu = u0 + 32 * wave;
+    const long long qrow[4] = {wu, wu + 16, I + wu, I + wu + 16};
+    const int srow[4] = {32 * wave, 32 * wave + 16, UB + 32 * wave, UB + 32 * wave + 16};
+    f32x4 acc[4][4];
+    big_block<4>(base, qrow, srow, D, xh, xl, xrow8, sm.sc, sm.gs, G, act0, act1, acc);
+    // act = silu(gate) * up; lane (n, g) of tile (rt, t) holds units wu + 16 rt + 4 g + j of pick
+    // 16 t + n. A chunk of 8 units lies in lanes g = 2c and 2c + 1: the even lane takes the odd
+    // lane's 4 values and writes the chunk (hi, lo in chunk order) and its sum.
+    float wsum[4] = {0.f, 0.f, 0.f, 0.f};  // per pick tile: this lane's chunk sums
+#pragma unroll
+    for (int rt = 0; rt < 2; rt++)
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            float a[4], o[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) a[j] = silu_f(acc[rt][t][j]) * acc[rt + 2][t][j];
+#pragma unroll
+            for (int j = 0; j < 4; j++) o[j] = __shfl_xor(a[j], 16, WAVE);
+            if ((g & 1) == 0) {
+                const float v[8] = {a[0], a[1], a[2], a[3], o[0], o[1], o[2], o[3]};
+                uint4 hi, lo;
+                float sum;
+                split8(v, hi, lo, sum);
+                wsum[t] += sum;
+                const int pr = 16 * t + n;
+                if (pr < np) {
+                    const size_t p = p0 + pr;
+                    const int u = wu + 16 * rt + 4 * g;  // the chunk's first unit
+                    *(uint4*)(ah + p * I + u) = hi;
+                    *(uint4*)(al + p * I + u) = lo;
+                }
+            }
+        }
+    // group sums: a 64-unit group is waves 2 k and 2 k + 1; per wave, the even lanes g = 0, 2 of
+    // pick n hold its chunk sums
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        const float s2 = wsum[t] + __shfl_xor(wsum[t], 32, WAVE);
+        if (g == 0) red[wave][16 * t + n] = s2;
+    }
+    __syncthreads();
+    if (tid < 4 * PBB) {
+        const int k = tid / PBB, pr = tid % PBB;
+        if (pr < np) as[(size_t)(p0 + pr) * (I / 64) + (u0 / 64) + k] = red[2 * k][pr] + red[2 * k + 1][pr];
+    }
+}
+
+// Down for big tiles: output rows [256 ob, 256 ob + 256) x one tile of <= 64 picks; ypick[src][o] =
+// wts[src] * (dn_o . act), as moe_down_kernel.
+__global__ void __launch_bounds__(512, 1) moe_down_big_kernel(const MoeTile* __restrict__ tiles,
+                                                           const int* __restrict__ ntiles, const int* __restrict__ psrc,
+                                                           const float* __restrict__ wts,
+                                                           const uint16_t* __restrict__ ah,
+                                                           const uint16_t* __restrict__ al,
+                                                           const float* __restrict__ as, int D, int I,
+                                                           ExpertOffsets off, float* __restrict__ ypick) {
+    __shared__ BigSmem sm;
+    __shared__ __attribute__((aligned(1024))) unsigned char act0[kActBytes];
+    __shared__ __attribute__((aligned(1024))) unsigned char act1[kActBytes];
+    __shared__ long long xrow8[PBB];
+    const int ob = blockIdx.x, tile = blockIdx.y;
+    const MoeTile tl = tiles[tile];
+    if (tile >= *ntiles) return;
+    const int G = I / 64, o0 = ob * UB;
+    const int p0 = tl.p0, np = tl.p1 - tl.p0;
+    const unsigned char* base = (const unsigned char*)tl.base;
+    const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE, n = lane % 16, g = lane / 16;
+    if (tid < PBB) xrow8[tid] = (long long)(p0 + min(tid, np - 1)) * I;
+    stage_sc_packed(sm.sc, (const uint16_t*)(base + off.dn_s), (const uint16_t*)(base + off.dn_m), o0, UB, G);
+    for (int i = tid; i < PBB * G; i += blockDim.x) {
+        const int pr = i / G, c = i % G;
+        sm.gs[pr * (G + 1) + c] = as[(size_t)(p0 + min(pr, np - 1)) * G + c];
+    }
+    __syncthreads();
+    const int wo = o0 + 32 * wave;
+    const long long qrow[2] = {wo, wo + 16};
+    const int srow[2] = {32 * wave, 32 * wave + 16};
+    f32x4 acc[2][4];
+    big_block<2>(base + off.dn_q, qrow, srow, I, ah, al, xrow8, sm.sc, sm.gs, G, act0, act1, acc);
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        const int pr = 16 * t + n;
+        if (pr >= np) continue;
+        const int src = psrc[p0 + pr];
+        const float w = wts[src];
+#pragma unroll
+        for (int rt = 0; rt < 2; rt++) {
+            const f32x4 v = acc[rt][t];
+            *(float4*)(ypick + (size_t)src * D + wo + 16 * rt + 4 * g) = float4{w * v[0], w * v[1], w * v[2], w * v[3]};
+        }
+    }
+}
+
 // x[t] += sum_k ypick[t K + k] (k in order) and, with a shared expert, + sigmoid(h_t . wg) ysh[t].
 // Grid (T, D / 256): one thread per column; the K pick rows are loaded together.
 __global__ void __launch_bounds__(256) moe_combine_kernel(float* __restrict__ x, const float* __restrict__ ypick,
@@ -605,10 +879,16 @@ __global__ void silu_mul_kernel(const float* __restrict__ g, const float* __rest
     if (i < n) out[i] = silu_f(g[i]) * u[i];
 }
 
+// AEGIST_MOE_BIG=0 keeps every tile at <= 32 picks (A/B runs).
+static bool big_tiles_enabled() {
+    const char* e = getenv("AEGIST_MOE_BIG");
+    return !(e && e[0] == '0');
+}
+
 // Workspace plan of aegist_moe_experts.
 struct MoePlan {
-    size_t xh, xl, xs, ah, al, as, yp, eoff, ptok, psrc, tiles1, tiles2, meta, total;
-    int max1, max2;  // tile-list capacities: <= 16 picks (one per expert), larger
+    size_t xh, xl, xs, ah, al, as, yp, eoff, ptok, psrc, tiles1, tiles2, tiles3, meta, total;
+    int max1, max2, max3;  // tile-list capacities: <= 16 picks (one per expert), 17..32, 33..64
 };
 static size_t al256(size_t x) { return (x + 255) / 256 * 256; }
 static MoePlan moe_plan(int T, int K, int D, int I, int E) {
@@ -617,6 +897,7 @@ static MoePlan moe_plan(int T, int K, int D, int I, int E) {
     p.max1 = (int)std::min<size_t>(N, (size_t)E);
     // an expert with c picks has floor(c / PB) + [c % PB > 16] <= c / 17 large blocks
     p.max2 = (int)(N / 17);
+    p.max3 = (int)(N / 16);  // ceil(c / 64) <= c / 16 for every c > 32
     size_t o = 0;
     auto take = [&](size_t bytes) {
         const size_t at = o;
@@ -635,6 +916,7 @@ static MoePlan moe_plan(int T, int K, int D, int I, int E) {
     p.psrc = take(N * 4);
     p.tiles1 = take((size_t)p.max1 * sizeof(MoeTile));
     p.tiles2 = take((size_t)std::max(p.max2, 1) * sizeof(MoeTile));
+    p.tiles3 = take((size_t)std::max(p.max3, 1) * sizeof(MoeTile));
     p.meta = take(16);
     p.total = o;
     return p;
@@ -704,6 +986,7 @@ int aegist_moe_experts(const float* h, const unsigned long long* eptr, const int
     int* psrc = (int*)(w + p.psrc);
     MoeTile* tiles1 = (MoeTile*)(w + p.tiles1);
     MoeTile* tiles2 = (MoeTile*)(w + p.tiles2);
+    MoeTile* tiles3 = (MoeTile*)(w + p.tiles3);
     int* meta = (int*)(w + p.meta);
     uint16_t* xh = (uint16_t*)(w + p.xh);
     uint16_t* xl = (uint16_t*)(w + p.xl);
@@ -713,7 +996,11 @@ int aegist_moe_experts(const float* h, const unsigned long long* eptr, const int
     float* as = (float*)(w + p.as);
     float* yp = (float*)(w + p.yp);
 
-    moe_group_kernel<<<1, 1024, 0, st>>>(idx, N, K, E, eptr, eoff, ptok, psrc, tiles1, tiles2, meta);
+    // experts with more than 32 picks take the big-tile kernels where the shapes allow, once the
+    // batch is large enough for such experts to be common (16 picks per expert on average)
+    const bool big = (long long)N >= 16LL * E && D % UB == 0 && I % UB == 0 && D / 64 <= 32 && big_tiles_enabled();
+    moe_group_kernel<<<1, 1024, 0, st>>>(idx, N, K, E, eptr, eoff, ptok, psrc, tiles1, tiles2, tiles3, big ? 1 : 0,
+                                         meta);
     int rc = after_launch("moe_group");
     if (rc) return rc;
     const long long nq = (long long)T * (D / 8);
@@ -732,12 +1019,22 @@ int aegist_moe_experts(const float* h, const unsigned long long* eptr, const int
                                                                          ah, al, as);
         if ((rc = after_launch("moe_gate_up"))) return rc;
     }
+    if (big) {
+        moe_gate_up_big_kernel<<<dim3(I / UB, p.max3), 512, 0, st>>>(tiles3, meta + 3, ptok, xh, xl, xs, D, I, off, ah,
+                                                                   al, as);
+        if ((rc = after_launch("moe_gate_up_big"))) return rc;
+    }
     moe_down_kernel<1><<<dim3(D / RB, p.max1), 256, lds_dn, st>>>(tiles1, meta, psrc, wts, ah, al, as, D, I, off, yp);
     if ((rc = after_launch("moe_down"))) return rc;
     if (p.max2 > 0) {
         moe_down_kernel<2><<<dim3(D / RB, p.max2), 256, lds_dn, st>>>(tiles2, meta + 2, psrc, wts, ah, al, as, D, I,
                                                                       off, yp);
         if ((rc = after_launch("moe_down"))) return rc;
+    }
+    if (big) {
+        moe_down_big_kernel<<<dim3(D / UB, p.max3), 512, 0, st>>>(tiles3, meta + 3, psrc, wts, ah, al, as, D, I, off,
+                                                                yp);
+        if ((rc = after_launch("moe_down_big"))) return rc;
     }
     moe_combine_kernel<<<dim3(T, (D + 255) / 256), 256, 0, st>>>(x, yp, idx, E, ysh, h, wg, D, K);
     return after_launch("moe_combine");

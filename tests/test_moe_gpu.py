@@ -104,8 +104,13 @@ def _run_experts(dev, T, D, I, E, K, seed, x0=None, shared=False, eptr_perm=None
     return xd.cpu().double() - x.double(), ref
 
 
-@pytest.mark.parametrize("T,E,K", [(1, 256, 8), (16, 256, 8), (4, 8, 8), (300, 16, 8)])
+@pytest.mark.parametrize("T,E,K", [(1, 256, 8), (16, 256, 8), (4, 8, 8), (300, 16, 8), (200, 16, 8), (130, 8, 4),
+                                   (512, 64, 8), (100, 24, 8)])
 def test_moe_experts(dev, T, E, K):
+    """Decode and prefill batches: in batches of 16 or more picks per expert on average, experts
+    with more than 32 picks take balanced tiles of up to 64 (300 x 8 / 16: 150 each = 3 x 50;
+    200 x 8 / 16: 2 x 50; 130 x 4 / 8: 65 = 33 + 32; 512 x 8 / 64: ~64 each, one or two tiles;
+    100 x 8 / 24: ~33 each, so some experts stay on the <= 32-pick tiles)."""
     print(f"moe experts T={T} E={E} K={K}", flush=True)
     got, ref = _run_experts(dev, T, 2048, 512, E, K, seed=T * 7 + E)
     err = rel_err(got, ref)
@@ -179,3 +184,23 @@ def test_moe_rejects_bad_shapes(dev):
     with pytest.raises(AegistError):
         ops.moe_experts(torch.zeros(2, 128, device=dev), rows, torch.zeros(2, 2, dtype=torch.int32, device=dev),
                         torch.zeros(2, 2, device=dev), torch.zeros(2, 128, device=dev), 96)  # I % 64
+
+
+def test_moe_experts_big_tiles_match_small(dev):
+    """The 64-pick big-tile kernels against the <= 32-pick kernels (AEGIST_MOE_BIG=0) on the
+    same prefill batch: both within the oracle bar, and within fp32 rounding of each other."""
+    import os
+    T, E, K, D, I = 256, 16, 8, 2048, 512
+    got_big, ref = _run_experts(dev, T, D, I, E, K, seed=21)
+    old = os.environ.get("AEGIST_MOE_BIG")
+    os.environ["AEGIST_MOE_BIG"] = "0"
+    try:
+        got_small, _ = _run_experts(dev, T, D, I, E, K, seed=21)
+    finally:
+        if old is None:
+            del os.environ["AEGIST_MOE_BIG"]
+        else:
+            os.environ["AEGIST_MOE_BIG"] = old
+    assert rel_err(got_big, ref) < TOL_MOE
+    assert rel_err(got_small, ref) < TOL_MOE
+    assert rel_err(got_big, got_small) < 1e-5
