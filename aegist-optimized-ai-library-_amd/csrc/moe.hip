@@ -568,8 +568,8 @@ __global__ void __launch_bounds__(256, 2) moe_down_kernel(const MoeTile* __restr
 }
 
 // ---------------------------------------------------------------------------------------------
-// Prefill-sized tiles (up to 64 picks of an expert with more than 32): a workgroup of 8 waves covers UB = 256 rows
-// of the output (gate / up: 256 units, i.e. 256 gate and 256 up rows; down: 256 output rows) for
+// Prefill-sized tiles (up to 64 picks of an expert with more than 32): a workgroup of 4 waves covers UB = 128 rows
+// of the output (gate / up: 128 units, i.e. 128 gate and 128 up rows; down: 128 output rows) for
 // all the tile's picks. Each wave owns 32 rows of every matrix (RT 16-row tiles in all) and walks
 // the 64-groups in order; the picks' activations of one group (hi and lo, 64 picks x 64 values)
 // are staged once per workgroup in LDS by direct global -> LDS loads (double-buffered, 16-byte
@@ -577,13 +577,14 @@ __global__ void __launch_bounds__(256, 2) moe_down_kernel(const MoeTile* __restr
 // each code byte once per tile, against once per 32 picks and once per 16 rows in the kernels
 // above. Per group and row tile the 4 x 2 x 2 products on the group's codes give P, and the lane
 // adds s P + (m - 128 s) X into its accumulators, the same fp32 formula as expert_block.
-constexpr int UB = 256;  // rows per matrix per big workgroup (8 waves x 32)
+constexpr int NWB = 4;         // waves per big workgroup (two workgroups per CU)
+constexpr int UB = 32 * NWB;   // rows per matrix per big workgroup
 
 // Rows of sc and gs are padded by one word so that the rows one read touches (4 apart in sc, 1
 // apart in gs) fall in different banks.
 struct BigSmem {
     uint32_t sc[2 * UB * 33];                // (s | m << 16) fp16 pairs, [matrix row][group], G <= 32
-    float gs[PBB * 65];                      // activation group sums [pick][group], G <= 64
+    float gs[PBB * 33];                      // activation group sums [pick][group], G <= 32
 };
 constexpr int kActBytes = 2 * PBB * 128;     // one group's activations: hi, lo x 64 picks x 128 B
 
@@ -626,17 +627,21 @@ __device__ __forceinline__ void big_block(const unsigned char* __restrict__ qbas
 #pragma unroll
     for (int rt = 0; rt < RT; rt++) arow[rt] = qbase + (size_t)(qrow[rt] + n) * rowbytes + 8 * g;
     typedef uint32_t u2v __attribute__((ext_vector_type(2)));
-    // activation pieces: 16 per group (8 per array, 8 picks x 128 B each), 2 per wave; lane L of
-    // piece q (pick 8 (q % 8) + L / 8) fetches the global 16-byte slot (L % 8) ^ sw(pick) so that
-    // LDS slot L % 8 of the pick's row holds it
-    const int q0 = 2 * wave, pk0 = 8 * (q0 % 8) + lane / 8, pk1 = 8 * ((q0 + 1) % 8) + lane / 8;
-    const int sl0 = ((lane % 8) ^ ((pk0 >> 1) & 7)) * 8, sl1 = ((lane % 8) ^ ((pk1 >> 1) & 7)) * 8;
-    const uint16_t* src0 = (q0 < 8 ? xh : xl) + xrow8[pk0] + sl0;
-    const uint16_t* src1 = (q0 + 1 < 8 ? xh : xl) + xrow8[pk1] + sl1;
+    // activation pieces: 16 per group (8 per array, 8 picks x 128 B each), 16 / NWB per wave;
+    // lane L of piece q (pick 8 (q % 8) + L / 8) fetches the global 16-byte slot (L % 8) ^ sw(pick)
+    // so that LDS slot L % 8 of the pick's row holds it
+    constexpr int PPW = 16 / NWB;
+    const uint16_t* src[PPW];
+#pragma unroll
+    for (int u = 0; u < PPW; u++) {
+        const int q = PPW * wave + u, pk = 8 * (q % 8) + lane / 8;
+        src[u] = (q < 8 ? xh : xl) + xrow8[pk] + ((lane % 8) ^ ((pk >> 1) & 7)) * 8;
+    }
     typedef __attribute__((address_space(3))) void lds_void;
     auto stage = [&](unsigned char* buf, int grp) {
-        __builtin_amdgcn_global_load_lds(src0 + 64 * grp, (lds_void*)(buf + q0 * 1024), 16, 0, 0);
-        __builtin_amdgcn_global_load_lds(src1 + 64 * grp, (lds_void*)(buf + (q0 + 1) * 1024), 16, 0, 0);
+#pragma unroll
+        for (int u = 0; u < PPW; u++)
+            __builtin_amdgcn_global_load_lds(src[u] + 64 * grp, (lds_void*)(buf + (PPW * wave + u) * 1024), 16, 0, 0);
     };
     // codes of group grp for every row tile (ring of 2 groups)
     u2v ar[2][RT];
@@ -705,7 +710,7 @@ __device__ __forceinline__ void big_block(const unsigned char* __restrict__ qbas
 
 // Gate / up for big tiles: units [256 ub, 256 ub + 256) x one tile of <= 64 picks. act as in
 // moe_gate_up_kernel (bf16 hi / lo in chunk order, group sums over 64 units).
-__global__ void __launch_bounds__(512, 1) moe_gate_up_big_kernel(const MoeTile* __restrict__ tiles,
+__global__ void __launch_bounds__(64 * NWB, 2) moe_gate_up_big_kernel(const MoeTile* __restrict__ tiles,
                                                               const int* __restrict__ ntiles,
                                                               const int* __restrict__ ptok,
                                                               const uint16_t* __restrict__ xh,
@@ -716,7 +721,7 @@ __global__ void __launch_bounds__(512, 1) moe_gate_up_big_kernel(const MoeTile* 
     __shared__ BigSmem sm;
     __shared__ __attribute__((aligned(1024))) unsigned char act0[kActBytes];
     __shared__ __attribute__((aligned(1024))) unsigned char act1[kActBytes];
-    __shared__ float red[8][PBB];
+    __shared__ float red[NWB][PBB];
     __shared__ long long xrow8[PBB];
     const int ub = blockIdx.x, tile = blockIdx.y;
     const MoeTile tl = tiles[tile];
@@ -777,7 +782,7 @@ __global__ void __launch_bounds__(512, 1) moe_gate_up_big_kernel(const MoeTile* 
         if (g == 0) red[wave][16 * t + n] = s2;
     }
     __syncthreads();
-    if (tid < 4 * PBB) {
+    if (tid < (UB / 64) * PBB) {
         const int k = tid / PBB, pr = tid % PBB;
         if (pr < np) as[(size_t)(p0 + pr) * (I / 64) + (u0 / 64) + k] = red[2 * k][pr] + red[2 * k + 1][pr];
     }
@@ -785,7 +790,7 @@ __global__ void __launch_bounds__(512, 1) moe_gate_up_big_kernel(const MoeTile* 
 
 // Down for big tiles: output rows [256 ob, 256 ob + 256) x one tile of <= 64 picks; ypick[src][o] =
 // wts[src] * (dn_o . act), as moe_down_kernel.
-__global__ void __launch_bounds__(512, 1) moe_down_big_kernel(const MoeTile* __restrict__ tiles,
+__global__ void __launch_bounds__(64 * NWB, 2) moe_down_big_kernel(const MoeTile* __restrict__ tiles,
                                                            const int* __restrict__ ntiles, const int* __restrict__ psrc,
                                                            const float* __restrict__ wts,
                                                            const uint16_t* __restrict__ ah,
@@ -998,7 +1003,8 @@ int aegist_moe_experts(const float* h, const unsigned long long* eptr, const int
 
     // experts with more than 32 picks take the big-tile kernels where the shapes allow, once the
     // batch is large enough for such experts to be common (16 picks per expert on average)
-    const bool big = (long long)N >= 16LL * E && D % UB == 0 && I % UB == 0 && D / 64 <= 32 && big_tiles_enabled();
+    const bool big = (long long)N >= 16LL * E && D % UB == 0 && I % UB == 0 && D / 64 <= 32 && I / 64 <= 32 &&
+                     big_tiles_enabled();
     moe_group_kernel<<<1, 1024, 0, st>>>(idx, N, K, E, eptr, eoff, ptok, psrc, tiles1, tiles2, tiles3, big ? 1 : 0,
                                          meta);
     int rc = after_launch("moe_group");
@@ -1020,7 +1026,7 @@ int aegist_moe_experts(const float* h, const unsigned long long* eptr, const int
         if ((rc = after_launch("moe_gate_up"))) return rc;
     }
     if (big) {
-        moe_gate_up_big_kernel<<<dim3(I / UB, p.max3), 512, 0, st>>>(tiles3, meta + 3, ptok, xh, xl, xs, D, I, off, ah,
+        moe_gate_up_big_kernel<<<dim3(I / UB, p.max3), 64 * NWB, 0, st>>>(tiles3, meta + 3, ptok, xh, xl, xs, D, I, off, ah,
                                                                    al, as);
         if ((rc = after_launch("moe_gate_up_big"))) return rc;
     }
@@ -1032,7 +1038,7 @@ int aegist_moe_experts(const float* h, const unsigned long long* eptr, const int
         if ((rc = after_launch("moe_down"))) return rc;
     }
     if (big) {
-        moe_down_big_kernel<<<dim3(D / UB, p.max3), 512, 0, st>>>(tiles3, meta + 3, psrc, wts, ah, al, as, D, I, off,
+        moe_down_big_kernel<<<dim3(D / UB, p.max3), 64 * NWB, 0, st>>>(tiles3, meta + 3, psrc, wts, ah, al, as, D, I, off,
                                                                 yp);
         if ((rc = after_launch("moe_down_big"))) return rc;
     }
