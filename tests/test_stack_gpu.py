@@ -139,8 +139,8 @@ def test_stack_conv_fused_prefill(dev):
     """Prefill in whole 256-token tiles runs the qkv projection with the short convolution in the
     GEMM epilogue (the edge rows of every tile through a second launch, the conv state carried
     across feeds). It must match the unfused path (AEGIST_GEMM_CONV=0: GEMM, then the conv launch)
-    bit for bit over a 512-token prefill, a 256-token continuation and two decode steps, and the
-    oracle to the stack bar."""
+    bit for bit over a 512-token prefill, a decode step, a 256-token continuation (its conv state
+    left by the decode step) and another decode step, and the oracle to the stack bar."""
     import os
     B, cap = 2, 1024
     layers, dl = make_layers(3, dev)
@@ -156,8 +156,8 @@ def test_stack_conv_fused_prefill(dev):
     fused = ops.HybridStack(c, KINDS, dl, max_batch=B, max_tokens=B * 512, max_context=cap)
     plain = ops.HybridStack(c, KINDS, dl, max_batch=B, max_tokens=B * 512, max_context=cap)
     g_ = torch.Generator().manual_seed(4)
-    feeds = [torch.randn(B, 512, c["d_model"], generator=g_), torch.randn(B, 256, c["d_model"], generator=g_),
-             torch.randn(B, 1, c["d_model"], generator=g_), torch.randn(B, 1, c["d_model"], generator=g_)]
+    feeds = [torch.randn(B, 512, c["d_model"], generator=g_), torch.randn(B, 1, c["d_model"], generator=g_),
+             torch.randn(B, 256, c["d_model"], generator=g_), torch.randn(B, 1, c["d_model"], generator=g_)]
     old = os.environ.pop("AEGIST_GEMM_CONV", None)
     try:
         for i, x in enumerate(feeds):
