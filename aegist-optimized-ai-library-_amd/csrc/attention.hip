@@ -179,7 +179,7 @@ template <> __device__ __forceinline__ void unpack8<float>(const uint4* raw, int
 
 // TQ: float = the queries come normed and rotated in q; uint16_t / float with kFused = the prep
 // is done here from fp.qg (bf16 / fp32 inputs).
-template <bool kList, bool kFused = false, typename Tin = float>
+template <bool kList, bool kFused = false, typename Tin = float, bool kNT = false>
 __global__ void __launch_bounds__(256) attn_decode_split_kernel(const float* __restrict__ q,
                                                                 const uint16_t* __restrict__ kc,
                                                                 const uint16_t* __restrict__ vc,
@@ -274,8 +274,16 @@ __global__ void __launch_bounds__(256) attn_decode_split_kernel(const float* __r
         for (int it = 0; it < NST; it++) {
             const int idx = it * WAVE + lane, row = idx / (HD * 2 / 16), cc = idx % (HD * 2 / 16);
             const int key = listed ? __shfl(kp, row, WAVE) : min(t0 + row, k1 - 1);
-            kreg[it] = *(const uint4*)(kbase + (size_t)key * HD + cc * 8);
-            vreg[it] = *(const uint4*)(vbase + (size_t)key * HD + cc * 8);
+            if constexpr (kNT) {
+                typedef unsigned u32x4nt __attribute__((ext_vector_type(4)));
+                const u32x4nt kq = __builtin_nontemporal_load((const u32x4nt*)(kbase + (size_t)key * HD + cc * 8));
+                const u32x4nt vq = __builtin_nontemporal_load((const u32x4nt*)(vbase + (size_t)key * HD + cc * 8));
+                kreg[it] = uint4{kq.x, kq.y, kq.z, kq.w};
+                vreg[it] = uint4{vq.x, vq.y, vq.z, vq.w};
+            } else {
+                kreg[it] = *(const uint4*)(kbase + (size_t)key * HD + cc * 8);
+                vreg[it] = *(const uint4*)(vbase + (size_t)key * HD + cc * 8);
+            }
         }
     };
     // fused prep: the raw query rows and norm weights are requested before the first tile, and
@@ -1641,18 +1649,29 @@ int launch_decode_core(const float* q, const uint16_t* kc, const uint16_t* vc, c
     size_t part_bytes = ((size_t)B * KV * sp.nsplit * G * HD * 4 + 255) / 256 * 256;
     float* ml = (float*)((char*)ws + part_bytes);
     const dim3 grid(sp.nsplit, KV, B);
+    // Batched calls read the caches with nontemporal loads: each K / V byte is used once, and
+    // kept out of L2 / MALL the stream runs faster (B = 64, L = 4096: 108 -> 94 us; B = 8,
+    // L = 32768: 103 -> 93 us). A batch-1 call (two (sequence, KV head) units) measured 3-5%
+    // slower that way at L = 131072, so it keeps ordinary loads.
+    const bool nt = (long long)B * KV >= 8;
+#define AEG_SPLIT(LIST, FUSED, TIN, F)                                                                          \
+    do {                                                                                                         \
+        if (nt)                                                                                                  \
+            attn_decode_split_kernel<LIST, FUSED, TIN, true><<<grid, 256, 0, st>>>(q, kc, vc, part, ml, H, KV, L, \
+                                                                                  cap, sp.per_split, scale, kl, F); \
+        else                                                                                                     \
+            attn_decode_split_kernel<LIST, FUSED, TIN, false><<<grid, 256, 0, st>>>(q, kc, vc, part, ml, H, KV, L, \
+                                                                                   cap, sp.per_split, scale, kl, F); \
+    } while (0)
     if (fused && fused_dtype == AEGIST_BF16)
-        attn_decode_split_kernel<false, true, uint16_t><<<grid, 256, 0, st>>>(q, kc, vc, part, ml, H, KV, L, cap,
-                                                                             sp.per_split, scale, kl, *fused);
+        AEG_SPLIT(false, true, uint16_t, *fused);
     else if (fused)
-        attn_decode_split_kernel<false, true, float><<<grid, 256, 0, st>>>(q, kc, vc, part, ml, H, KV, L, cap,
-                                                                          sp.per_split, scale, kl, *fused);
+        AEG_SPLIT(false, true, float, *fused);
     else if (kl.blist)
-        attn_decode_split_kernel<true><<<grid, 256, 0, st>>>(q, kc, vc, part, ml, H, KV, L, cap, sp.per_split, scale,
-                                                             kl, FusedPrep{});
+        AEG_SPLIT(true, false, float, FusedPrep{});
     else
-        attn_decode_split_kernel<false><<<grid, 256, 0, st>>>(q, kc, vc, part, ml, H, KV, L, cap, sp.per_split, scale,
-                                                              kl, FusedPrep{});
+        AEG_SPLIT(false, false, float, FusedPrep{});
+#undef AEG_SPLIT
     int rc = after_launch("attention_decode_split");
     if (rc) return rc;
     attn_decode_merge_wide_kernel<TG, Tout><<<B * KV * G, 256, 0, st>>>(part, ml, gate, gate_stride, out, out_stride,
