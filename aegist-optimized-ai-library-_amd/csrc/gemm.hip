@@ -187,10 +187,12 @@ __global__ void __launch_bounds__(512, 1) gemm_bf16_kernel(const GemmArgs ga) {
 #pragma unroll
                     for (int j = 0; j < 4; j++) acc[i][j] += old[j];
                 }
+                // nontemporal: Y is written once and read by the next launch, and the stores kept
+                // out of L2 leave it to the operand tiles (qkv 8192 x 2048 at M = 32768: 1190 -> 1100 us)
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
                     const int m = m0 + 64 * wm + 16 * j + r16;
-                    if (m < M) *(f32x4*)(Yb + (size_t)m * ldy + nl) = acc[i][j];
+                    if (m < M) __builtin_nontemporal_store(acc[i][j], (f32x4*)(Yb + (size_t)m * ldy + nl));
                 }
             } else {
 #pragma unroll
@@ -275,7 +277,7 @@ __global__ void __launch_bounds__(512, 1) gemm_bf16_kernel(const GemmArgs ga) {
 #pragma unroll
                     for (int e = 0; e < 4; e++)
                         o[e] = conv4_silu(wt[e][0], wt[e][1], wt[e][2], wt[e][3], h0[e], h1[e], h2[e], x[e]);
-                    *(f32x4*)(sg.Y + (size_t)m * sg.ldy + n) = o;
+                    __builtin_nontemporal_store(o, (f32x4*)(sg.Y + (size_t)m * sg.ldy + n));
                 }
                 if (lr < 3 || lr >= GBM - 3)
                     *(f32x4*)(ga.edge + ((size_t)tile_m * 6 + (lr < 3 ? lr : lr - (GBM - 6))) * N + n) = x;
@@ -477,7 +479,7 @@ __global__ void __launch_bounds__(512, 1) gemm_i8f32_kernel(const float* __restr
 #pragma unroll
                 for (int e = 0; e < 4; e++) v[e] *= sc[e];
                 if (accumulate) v += *(const f32x4*)(yrow + n);
-                *(f32x4*)(yrow + n) = v;
+                __builtin_nontemporal_store(v, (f32x4*)(yrow + n));
             } else {
 #pragma unroll
                 for (int e = 0; e < 4; e++)
